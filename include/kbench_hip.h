@@ -1,0 +1,120 @@
+/*
+ * libkbench_hip -- C ABI of the MI355X (gfx950) log-space solver path.
+ *
+ * The reference (SisyphusMountain/kernel-bench) has no native FFI: its hot
+ * path is Triton kernels launched from Python wrappers in
+ * kbench/core/kernels/*.py.  Each entry point below replaces a group of those
+ * launches; the comment on each names the reference interface (file:line,
+ * paths relative to the reference root, "pristine" =
+ * experiments/pristine_kernels/).
+ *
+ * Conventions: plain pointers and sizes only.  Pointers named in *_io structs
+ * are device pointers (HIP global memory) unless noted; `stream` is a
+ * hipStream_t passed as void*.  Every function returns 0 on success or a
+ * negative KB_ERR_* code; kb_last_error() describes the failure of the last
+ * call on the calling thread.  Nothing here synchronises the stream unless
+ * its comment says so.
+ */
+#ifndef KBENCH_HIP_H
+#define KBENCH_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KB_ABI_VERSION 1
+
+#define KB_ERR_ARG (-1)    /* invalid argument / layout (reference raises ValueError) */
+#define KB_ERR_HIP (-2)    /* HIP runtime error (reference: RuntimeError) */
+#define KB_ERR_SOLVE (-3)  /* iterative solve failed (reference: RuntimeError, _implicit_grad.py:94) */
+
+/* Message of the last failing call on this thread. */
+const char* kb_last_error(void);
+int kb_abi_version(void);
+
+/*
+ * Static problem layout, host pointers (read once by kb_plan_create).
+ * Field meanings follow the reference's `static` namespace
+ * (kbench/runtime.py:47-60): state_helpers (node_parent, node_child1/2 with a
+ * >= S "no child" sentinel, node_subtree_start/end, unnorm_row_max) and
+ * wave_layout (leaf_state_index, root_row_ids, wave_metas[start, W, sl, sr,
+ * reduce_idx, log_split_probs]) plus rate_item_idx.  Splits are given with
+ * their global parent row (wave start + reduce_idx).
+ */
+typedef struct kb_layout {
+  int32_t S, C, n_fam, n_waves;
+  const int64_t* node_parent;        /* [S], -1 at the root */
+  const int64_t* node_child1;        /* [S], >= S: none */
+  const int64_t* node_child2;        /* [S] */
+  const int64_t* node_subtree_start; /* [S] preorder index */
+  const int64_t* node_subtree_end;   /* [S] preorder index + subtree size */
+  const float* unnorm_row_max;       /* [S] */
+  const int64_t* leaf_state_index;   /* [C], -1 for non-leaf rows */
+  const int64_t* rate_item_idx;      /* [C] */
+  const int64_t* root_row_ids;       /* [n_fam] */
+  const int64_t* wave_start;         /* [n_waves] */
+  const int64_t* wave_size;          /* [n_waves] */
+  const int32_t* wave_has_splits;    /* [n_waves] */
+  int64_t n_splits;
+  const int64_t* split_parent;       /* [n_splits] global parent row */
+  const int64_t* split_left;         /* [n_splits] global child rows */
+  const int64_t* split_right;
+  const double* split_log_prob;      /* [n_splits] log2 split probability */
+} kb_layout;
+
+typedef struct kb_plan kb_plan;
+
+/* Build the device-resident layout tables (allocates device memory). */
+int kb_plan_create(const kb_layout* layout, kb_plan** out);
+void kb_plan_destroy(kb_plan* plan);
+/* out[0..n): S, C, n_fam, n_waves, pointer-jump rounds, bottom-up levels. */
+int kb_plan_info(const kb_plan* plan, int32_t* out, int n);
+
+/*
+ * Whole forward pass: theta -> loss and the forward intermediates.
+ * Replaces reference kbench/runtime.py:63-75 run_forward, i.e.
+ * solver.py:16-96 solve_e_pi (extract_parameters_* + e_fixed_point_triton,
+ * pristine e_step.py:438-501) -> forward.py:8-117 pi_wave_forward
+ * (compute_dts_forward dts_fused.py:171-231, compute_leaf_initial_wave_step
+ * wave_step.py:313-361, compute_wave_step wave_step.py:363-410) ->
+ * solver.py:141-142 nll_from_root_rows.
+ * One fused kernel per wave runs the split reduction and all pi_iters-1
+ * sweeps with the row on chip.  Output pointers are device buffers of the
+ * reference's saved-tensor shapes (runtime.py:29-32).
+ */
+typedef struct kb_forward_io {
+  const float* theta;        /* [S,3] if statewise else [3] */
+  int32_t statewise;
+  const float* col_weights;  /* [S] */
+  int32_t use_col_weights;   /* 0 when all col_weights are equal (solver.py:11-13) */
+  double e_init;
+  int32_t e_max_iter;
+  double e_tol;
+  int32_t pi_iters;
+  float* E;                  /* [S] (item rows = 1) */
+  float* E_s1;
+  float* E_s2;
+  float* Ebar;
+  float* log_pS;             /* [S] statewise, [1] global */
+  float* log_pD;
+  float* log_pL;
+  float* max_coupling;       /* [S] */
+  float* col_log_probs;      /* [S] */
+  float* pi;                 /* [C,S] pi_wave */
+  float* pibar;              /* [C,S] pibar_wave */
+  float* pibar_row_max;      /* [C] */
+  float* loss;               /* [1] */
+} kb_forward_io;
+
+int kb_forward(kb_plan* plan, const kb_forward_io* io, void* stream);
+
+/* Synchronises `stream`; returns the E-step iteration count and the float64 loss. */
+int kb_forward_stats(kb_plan* plan, int32_t* n_e_iter, double* loss64, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KBENCH_HIP_H */

@@ -1,0 +1,383 @@
+// C-ABI of libkbench_hip: plan creation (device-resident layout tables built
+// once per static problem) and the whole-pass drivers.  Declarations and the
+// reference interface each entry point replaces are in include/kbench_hip.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/kbench_hip.h"
+#include "kb_kernels.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int set_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+#define KB_HIP(expr)                                                                       \
+  do {                                                                                     \
+    hipError_t _e = (expr);                                                                \
+    if (_e != hipSuccess)                                                                  \
+      return set_error(KB_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(_e));         \
+  } while (0)
+
+template <typename T>
+int upload(T** dst, const std::vector<T>& src) {
+  *dst = nullptr;
+  if (src.empty()) return 0;
+  KB_HIP(hipMalloc((void**)dst, src.size() * sizeof(T)));
+  KB_HIP(hipMemcpy(*dst, src.data(), src.size() * sizeof(T), hipMemcpyHostToDevice));
+  return 0;
+}
+
+template <typename T>
+int alloc(T** dst, size_t n) {
+  *dst = nullptr;
+  if (n == 0) return 0;
+  KB_HIP(hipMalloc((void**)dst, n * sizeof(T)));
+  return 0;
+}
+
+}  // namespace
+
+struct kb_plan {
+  int S = 0, C = 0, n_fam = 0, n_waves = 0;
+  int n_jump = 0, n_tlevels = 0, n_blevels = 0;
+  std::vector<int> wave_start, wave_size, wave_split;
+  // device tables
+  int* d_parent = nullptr; int* d_c1 = nullptr; int* d_c2 = nullptr; int* d_jump = nullptr;
+  int* d_blevel_ptr = nullptr; int* d_blevel_node = nullptr;
+  int* d_tlevel_ptr = nullptr; int* d_tlevel_node = nullptr;
+  int* d_sub_start = nullptr; int* d_sub_end = nullptr;
+  int* d_item = nullptr; int* d_leaf = nullptr; int* d_roots = nullptr;
+  int* d_split_ptr = nullptr; int* d_split_l = nullptr; int* d_split_r = nullptr; float* d_split_lsp = nullptr;
+  int* d_split_parent = nullptr;
+  int* d_child_ptr = nullptr; int* d_child_in = nullptr;
+  float* d_unnorm = nullptr;
+  // per-solve constants [S]
+  float* c_DL = nullptr; float* c_SL1 = nullptr; float* c_SL2 = nullptr; float* c_pS = nullptr;
+  float* c_pD = nullptr; float* c_colw = nullptr;
+  float* lin_a = nullptr; float* lin_emc = nullptr; float* lin_k1 = nullptr; float* lin_k2 = nullptr;
+  double* E64 = nullptr; int* n_e_iter = nullptr; double* loss_terms = nullptr; double* loss64 = nullptr;
+  std::vector<void*> owned;
+
+  kb::TreeDev tree() const {
+    kb::TreeDev t;
+    t.S = S;
+    t.n_jump = n_jump;
+    t.n_blevels = n_blevels;
+    t.parent = d_parent;
+    t.c1 = d_c1;
+    t.c2 = d_c2;
+    t.jump = d_jump;
+    t.blevel_ptr = d_blevel_ptr;
+    t.blevel_node = d_blevel_node;
+    t.sub_start = d_sub_start;
+    t.sub_end = d_sub_end;
+    return t;
+  }
+};
+
+extern "C" {
+
+const char* kb_last_error(void) { return g_last_error.c_str(); }
+
+int kb_abi_version(void) { return KB_ABI_VERSION; }
+
+void kb_plan_destroy(kb_plan* p) {
+  if (!p) return;
+  for (void* ptr : p->owned)
+    if (ptr) (void)hipFree(ptr);
+  delete p;
+}
+
+int kb_plan_create(const kb_layout* L, kb_plan** out) {
+  if (!L || !out) return set_error(KB_ERR_ARG, "null argument");
+  *out = nullptr;
+  const int S = L->S, C = L->C;
+  if (S < 1 || C < 0) return set_error(KB_ERR_ARG, "bad sizes S=%d C=%d", S, C);
+  if (S > 8192) return set_error(KB_ERR_ARG, "S=%d exceeds the supported maximum 8192", S);
+  kb_plan* p = new kb_plan();
+  p->S = S;
+  p->C = C;
+  p->n_fam = L->n_fam;
+  p->n_waves = L->n_waves;
+
+  // ---- species tree
+  std::vector<int> parent(S), c1(S), c2(S), depth(S, -1), ss(S), se(S);
+  for (int s = 0; s < S; ++s) {
+    int64_t pa = L->node_parent[s];
+    parent[s] = (pa >= 0 && pa < S) ? (int)pa : -1;
+    int64_t a = L->node_child1[s], b = L->node_child2[s];
+    c1[s] = (a >= 0 && a < S) ? (int)a : -1;
+    c2[s] = (b >= 0 && b < S) ? (int)b : -1;
+    ss[s] = (int)L->node_subtree_start[s];
+    se[s] = (int)L->node_subtree_end[s];
+  }
+  // depth by walking to the root (bounded: a cycle is a layout error)
+  int max_chain = 1;
+  for (int s = 0; s < S; ++s) {
+    int d = 0, cur = s;
+    while (parent[cur] >= 0) {
+      cur = parent[cur];
+      if (++d > S) {
+        kb_plan_destroy(p);
+        return set_error(KB_ERR_ARG, "node_parent has a cycle");
+      }
+    }
+    depth[s] = d;
+    max_chain = std::max(max_chain, d + 1);
+  }
+  int n_jump = 0;
+  while ((1 << n_jump) < max_chain) ++n_jump;
+  std::vector<int> jump((size_t)std::max(n_jump, 1) * S, -1);
+  for (int s = 0; s < S; ++s) jump[s] = parent[s];
+  for (int t = 1; t < n_jump; ++t)
+    for (int s = 0; s < S; ++s) {
+      int a = jump[(size_t)(t - 1) * S + s];
+      jump[(size_t)t * S + s] = a >= 0 ? jump[(size_t)(t - 1) * S + a] : -1;
+    }
+  int maxd = 0;
+  for (int s = 0; s < S; ++s) maxd = std::max(maxd, depth[s]);
+  std::vector<int> tptr(maxd + 2, 0), tnode;
+  for (int d = 0; d <= maxd; ++d) {
+    for (int s = 0; s < S; ++s)
+      if (depth[s] == d) tnode.push_back(s);
+    tptr[d + 1] = (int)tnode.size();
+  }
+  std::vector<int> bptr(1, 0), bnode;
+  for (int d = maxd; d >= 0; --d) {
+    bool any = false;
+    for (int s = 0; s < S; ++s)
+      if (depth[s] == d && (c1[s] >= 0 || c2[s] >= 0)) {
+        bnode.push_back(s);
+        any = true;
+      }
+    if (any) bptr.push_back((int)bnode.size());
+  }
+  p->n_jump = n_jump;
+  p->n_tlevels = maxd + 1;
+  p->n_blevels = (int)bptr.size() - 1;
+
+  // ---- rows, splits, waves
+  std::vector<int> item(C), leaf(C), roots(L->n_fam);
+  for (int r = 0; r < C; ++r) {
+    item[r] = (int)L->rate_item_idx[r];
+    leaf[r] = (int)L->leaf_state_index[r];
+  }
+  for (int f = 0; f < L->n_fam; ++f) roots[f] = (int)L->root_row_ids[f];
+  const int64_t NS = L->n_splits;
+  std::vector<int> cnt(C + 1, 0);
+  for (int64_t i = 0; i < NS; ++i) {
+    int64_t pr = L->split_parent[i];
+    if (pr < 0 || pr >= C) {
+      kb_plan_destroy(p);
+      return set_error(KB_ERR_ARG, "split %lld has parent row %lld outside [0,%d)", (long long)i, (long long)pr, C);
+    }
+    int64_t a = L->split_left[i], b = L->split_right[i];
+    if (a < 0 || a >= pr || b < 0 || b >= pr) {
+      kb_plan_destroy(p);
+      return set_error(KB_ERR_ARG, "split %lld children (%lld,%lld) must precede parent row %lld",
+                       (long long)i, (long long)a, (long long)b, (long long)pr);
+    }
+    cnt[pr + 1]++;
+  }
+  for (int r = 0; r < C; ++r) cnt[r + 1] += cnt[r];
+  std::vector<int> sptr(cnt), fill(cnt.begin(), cnt.end() - 1);
+  std::vector<int> sl(NS), sr(NS), spar(NS);
+  std::vector<float> slsp(NS);
+  for (int64_t i = 0; i < NS; ++i) {  // stable: keeps the layout's split order per parent
+    int pr = (int)L->split_parent[i];
+    int pos = fill[pr]++;
+    sl[pos] = (int)L->split_left[i];
+    sr[pos] = (int)L->split_right[i];
+    slsp[pos] = (float)L->split_log_prob[i];
+    spar[pos] = pr;
+  }
+  // child -> incoming (split, side) CSR in increasing split order: fixed gather order
+  std::vector<int> ccnt(C + 1, 0);
+  for (int64_t i = 0; i < NS; ++i) {
+    ccnt[sl[i] + 1]++;
+    ccnt[sr[i] + 1]++;
+  }
+  for (int r = 0; r < C; ++r) ccnt[r + 1] += ccnt[r];
+  std::vector<int> cfill(ccnt.begin(), ccnt.end() - 1), cin(2 * NS);
+  for (int64_t i = 0; i < NS; ++i) {
+    cin[cfill[sl[i]]++] = (int)(2 * i);
+    cin[cfill[sr[i]]++] = (int)(2 * i + 1);
+  }
+  for (int w = 0; w < L->n_waves; ++w) {
+    p->wave_start.push_back((int)L->wave_start[w]);
+    p->wave_size.push_back((int)L->wave_size[w]);
+    p->wave_split.push_back(L->wave_has_splits[w] ? 1 : 0);
+  }
+  std::vector<float> unnorm(L->unnorm_row_max, L->unnorm_row_max + S);
+
+  int rc = 0;
+  rc |= upload(&p->d_parent, parent);
+  rc |= upload(&p->d_c1, c1);
+  rc |= upload(&p->d_c2, c2);
+  rc |= upload(&p->d_jump, jump);
+  rc |= upload(&p->d_blevel_ptr, bptr);
+  rc |= upload(&p->d_blevel_node, bnode);
+  rc |= upload(&p->d_tlevel_ptr, tptr);
+  rc |= upload(&p->d_tlevel_node, tnode);
+  rc |= upload(&p->d_sub_start, ss);
+  rc |= upload(&p->d_sub_end, se);
+  rc |= upload(&p->d_item, item);
+  rc |= upload(&p->d_leaf, leaf);
+  rc |= upload(&p->d_roots, roots);
+  rc |= upload(&p->d_split_ptr, sptr);
+  rc |= upload(&p->d_split_l, sl);
+  rc |= upload(&p->d_split_r, sr);
+  rc |= upload(&p->d_split_lsp, slsp);
+  rc |= upload(&p->d_split_parent, spar);
+  rc |= upload(&p->d_child_ptr, ccnt);
+  rc |= upload(&p->d_child_in, cin);
+  rc |= upload(&p->d_unnorm, unnorm);
+  rc |= alloc(&p->c_DL, S);
+  rc |= alloc(&p->c_SL1, S);
+  rc |= alloc(&p->c_SL2, S);
+  rc |= alloc(&p->c_pS, S);
+  rc |= alloc(&p->c_pD, S);
+  rc |= alloc(&p->c_colw, S);
+  rc |= alloc(&p->lin_a, S);
+  rc |= alloc(&p->lin_emc, S);
+  rc |= alloc(&p->lin_k1, S);
+  rc |= alloc(&p->lin_k2, S);
+  rc |= alloc(&p->E64, S);
+  rc |= alloc(&p->n_e_iter, 1);
+  rc |= alloc(&p->loss_terms, std::max(1, L->n_fam));
+  rc |= alloc(&p->loss64, 1);
+  for (void* ptr : {(void*)p->d_parent, (void*)p->d_c1, (void*)p->d_c2, (void*)p->d_jump, (void*)p->d_blevel_ptr,
+                    (void*)p->d_blevel_node, (void*)p->d_tlevel_ptr, (void*)p->d_tlevel_node, (void*)p->d_sub_start,
+                    (void*)p->d_sub_end, (void*)p->d_item, (void*)p->d_leaf, (void*)p->d_roots, (void*)p->d_split_ptr,
+                    (void*)p->d_split_l, (void*)p->d_split_r, (void*)p->d_split_lsp, (void*)p->d_split_parent,
+                    (void*)p->d_child_ptr, (void*)p->d_child_in, (void*)p->d_unnorm, (void*)p->c_DL, (void*)p->c_SL1,
+                    (void*)p->c_SL2, (void*)p->c_pS, (void*)p->c_pD, (void*)p->c_colw, (void*)p->lin_a,
+                    (void*)p->lin_emc, (void*)p->lin_k1, (void*)p->lin_k2, (void*)p->E64, (void*)p->n_e_iter,
+                    (void*)p->loss_terms, (void*)p->loss64})
+    p->owned.push_back(ptr);
+  if (rc) {
+    kb_plan_destroy(p);
+    return KB_ERR_HIP;
+  }
+  *out = p;
+  return 0;
+}
+
+int kb_plan_info(const kb_plan* p, int32_t* out, int n) {
+  if (!p || !out) return set_error(KB_ERR_ARG, "null argument");
+  int32_t v[6] = {p->S, p->C, p->n_fam, p->n_waves, p->n_jump, p->n_blevels};
+  for (int i = 0; i < n && i < 6; ++i) out[i] = v[i];
+  return 0;
+}
+
+int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
+  if (!p || !io) return set_error(KB_ERR_ARG, "null argument");
+  if (io->pi_iters < 2 || io->pi_iters % 2 != 0)
+    return set_error(KB_ERR_ARG, "pi_iters must be an even integer at least 2");
+  if (io->e_max_iter < 1) return set_error(KB_ERR_ARG, "e_max_iter must be at least 1");
+  if (!(io->e_tol > 0.0)) return set_error(KB_ERR_ARG, "e_tol must be positive");
+  hipStream_t st = (hipStream_t)stream;
+  const int S = p->S;
+
+  kb::EStepParams E{};
+  E.tr = p->tree();
+  E.S = S;
+  E.n_tlevels = p->n_tlevels;
+  E.tlevel_ptr = p->d_tlevel_ptr;
+  E.tlevel_node = p->d_tlevel_node;
+  E.theta = io->theta;
+  E.statewise = io->statewise;
+  E.col_weights = io->col_weights;
+  E.use_col = io->use_col_weights;
+  E.unnorm_row_max = p->d_unnorm;
+  E.e_init = io->e_init;
+  E.max_iter = io->e_max_iter;
+  E.tol = io->e_tol;
+  E.E = io->E;
+  E.E_s1 = io->E_s1;
+  E.E_s2 = io->E_s2;
+  E.Ebar = io->Ebar;
+  E.log_pS = io->log_pS;
+  E.log_pD = io->log_pD;
+  E.log_pL = io->log_pL;
+  E.mt = io->max_coupling;
+  E.col_log_probs = io->col_log_probs;
+  E.E64 = p->E64;
+  E.n_iter_out = p->n_e_iter;
+  E.c_DL = p->c_DL;
+  E.c_SL1 = p->c_SL1;
+  E.c_SL2 = p->c_SL2;
+  E.c_pS = p->c_pS;
+  E.c_pD = p->c_pD;
+  E.c_colw = p->c_colw;
+  E.lin_a = p->lin_a;
+  E.lin_emc = p->lin_emc;
+  E.lin_k1 = p->lin_k1;
+  E.lin_k2 = p->lin_k2;
+  kb::launch_estep(E, st);
+  KB_HIP(hipGetLastError());
+
+  kb::FwdParams F{};
+  F.tr = p->tree();
+  F.S = S;
+  F.n_sweeps = io->pi_iters - 1;
+  F.use_col = io->use_col_weights;
+  F.const_stride = 0;
+  F.lin_a = p->lin_a;
+  F.lin_emc = p->lin_emc;
+  F.lin_k1 = p->lin_k1;
+  F.lin_k2 = p->lin_k2;
+  F.colw = p->c_colw;
+  F.col = io->col_log_probs;
+  F.mt = io->max_coupling;
+  F.DL = p->c_DL;
+  F.Ebar = io->Ebar;
+  F.E = io->E;
+  F.SL1 = p->c_SL1;
+  F.SL2 = p->c_SL2;
+  F.leaf_logp = p->c_pS;
+  F.pD = kb::RateDev{p->c_pD, 0, 1};
+  F.pS = kb::RateDev{p->c_pS, 0, 1};
+  F.item = p->d_item;
+  F.leaf_state = p->d_leaf;
+  F.split_ptr = p->d_split_ptr;
+  F.split_l = p->d_split_l;
+  F.split_r = p->d_split_r;
+  F.split_lsp = p->d_split_lsp;
+  F.pi = io->pi;
+  F.pibar = io->pibar;
+  F.rowmax = io->pibar_row_max;
+  for (int w = 0; w < p->n_waves; ++w) {
+    kb::launch_fwd_wave(F, p->wave_start[w], p->wave_size[w], p->wave_split[w] ? 0 : 1, st);
+  }
+  KB_HIP(hipGetLastError());
+  kb::launch_loss(io->pi, p->d_roots, io->E, S, p->n_fam, p->loss_terms, p->loss64, io->loss, st);
+  KB_HIP(hipGetLastError());
+  return 0;
+}
+
+int kb_forward_stats(kb_plan* p, int32_t* n_e_iter, double* loss64, void* stream) {
+  if (!p) return set_error(KB_ERR_ARG, "null argument");
+  KB_HIP(hipStreamSynchronize((hipStream_t)stream));
+  if (n_e_iter) KB_HIP(hipMemcpy(n_e_iter, p->n_e_iter, sizeof(int), hipMemcpyDeviceToHost));
+  if (loss64) KB_HIP(hipMemcpy(loss64, p->loss64, sizeof(double), hipMemcpyDeviceToHost));
+  return 0;
+}
+
+}  // extern "C"

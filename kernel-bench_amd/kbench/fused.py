@@ -1,0 +1,296 @@
+"""Whole-pass native driver: the MI355X fast path for ``run_forward`` / ``run_backward``.
+
+``FusedSolver`` builds the device-resident layout tables once per static
+problem (``kb_plan_create``) and then runs a whole forward or backward pass
+with a handful of launches on the current stream:
+
+* forward: one single-workgroup kernel for the parameters and the E-step fixed
+  point, one fused kernel per wave (split reduction + all ``pi_iters-1`` sweeps
+  + final Pibar), and a two-kernel deterministic loss reduction;
+* backward: one fused kernel per wave in reverse order (child-owned gather of
+  the adjoint, active mask, split recomputation, self-loop Neumann series,
+  parameter buckets, split-side staging) and a final O(S) epilogue for the
+  E adjoint and the theta / column VJP.
+
+It computes what the reference's frozen glue computes
+(reference kbench/runtime.py:63-115) and returns the same tensors; the glue
+path in ``kbench.runtime`` drives the per-call wrappers instead.
+"""
+
+from __future__ import annotations
+
+import ctypes as ct
+from types import SimpleNamespace
+
+import numpy as np
+import torch
+
+from . import _native as N
+
+FORWARD_SAVED_NAMES = (
+    "E", "E_s1", "E_s2", "Ebar", "root_rows", "pi_wave", "pibar_wave",
+    "pibar_row_max", "log_pS", "log_pD", "log_pL", "max_coupling", "col_log_probs",
+)
+
+_SOLVER_DEFAULTS = {
+    "e_init": -1.0, "e_max_iter": 2000, "e_tol": 1e-8, "pi_iters": 6, "neumann_terms": 3,
+    "self_loop_solver": "neumann", "bicgstab_max_iter": 500, "bicgstab_tol": 1e-7,
+    "bicgstab_breakdown_tol": 1e-30, "adjoint_pruning_threshold": 1e-6,
+    "use_adjoint_pruning": True, "pibar_side_threshold": 0.0,
+}
+
+
+def _np(x, dtype=None):
+    if torch.is_tensor(x):
+        x = x.detach().cpu().numpy()
+    a = np.asarray(x)
+    return a.astype(dtype) if dtype is not None else a
+
+
+def _get(static, key):
+    return static[key] if isinstance(static, dict) else getattr(static, key)
+
+
+def solver_options_dict(so) -> dict:
+    d = dict(_SOLVER_DEFAULTS)
+    if so is None:
+        return d
+    if isinstance(so, dict):
+        d.update(so)
+    else:
+        for k in d:
+            if hasattr(so, k):
+                d[k] = getattr(so, k)
+    return d
+
+
+class FusedSolver:
+    """Native whole-pass solver bound to one static layout and one device."""
+
+    def __init__(self, static, solver_options=None, device=None):
+        wl = _get(static, "wave_layout")
+        sh = _get(static, "state_helpers")
+        self.statewise = bool(_get(static, "statewise"))
+        self.itemwise = bool(_get(static, "itemwise"))
+        if self.itemwise:
+            raise NotImplementedError("the fused driver covers item_rows == 1 (itemwise=False)")
+        so = solver_options if solver_options is not None else (
+            static.get("solver_options") if isinstance(static, dict) else getattr(static, "solver_options", None))
+        self.so = solver_options_dict(so)
+        self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        S = int(sh["S"])
+        item = _np(_get(static, "rate_item_idx"), np.int64)
+        if np.any(item != 0):
+            raise NotImplementedError("the fused driver needs rate_item_idx == 0 (itemwise=False)")
+        leaf = _np(wl["leaf_state_index"], np.int64)
+        C = int(leaf.shape[0])
+        roots = _np(wl["root_row_ids"], np.int64)
+        ws, wsz, whs = [], [], []
+        sp, sl, sr, lsp = [], [], [], []
+        for m in wl["wave_metas"]:
+            start, W = int(m["start"]), int(m["W"])
+            ws.append(start)
+            wsz.append(W)
+            has = "sl" in m
+            whs.append(1 if has else 0)
+            if has:
+                a = _np(m["sl"], np.int64)
+                b = _np(m["sr"], np.int64)
+                red = _np(m["reduce_idx"], np.int64)
+                lp = m.get("log_split_probs")
+                lp = np.zeros(a.shape[0]) if lp is None else _np(lp, np.float64).reshape(-1)
+                sp.append(red + start)
+                sl.append(a)
+                sr.append(b)
+                lsp.append(lp)
+        cat = lambda xs, dt: (np.concatenate(xs).astype(dt) if xs else np.zeros(0, dtype=dt))
+        self._arrays = arrays = {
+            "node_parent": _np(sh["node_parent"], np.int64),
+            "node_child1": _np(sh["node_child1"], np.int64),
+            "node_child2": _np(sh["node_child2"], np.int64),
+            "node_subtree_start": _np(sh["node_subtree_start"], np.int64),
+            "node_subtree_end": _np(sh["node_subtree_end"], np.int64),
+            "unnorm_row_max": _np(sh["unnorm_row_max"], np.float32),
+            "leaf_state_index": leaf,
+            "rate_item_idx": item,
+            "root_row_ids": roots,
+            "wave_start": np.asarray(ws, np.int64),
+            "wave_size": np.asarray(wsz, np.int64),
+            "wave_has_splits": np.asarray(whs, np.int32),
+            "split_parent": cat(sp, np.int64),
+            "split_left": cat(sl, np.int64),
+            "split_right": cat(sr, np.int64),
+            "split_log_prob": cat(lsp, np.float64),
+        }
+        arrays = {k: np.ascontiguousarray(v) for k, v in arrays.items()}
+        self._arrays = arrays
+        L = N.KbLayout()
+        L.S, L.C, L.n_fam, L.n_waves = S, C, int(roots.shape[0]), len(ws)
+        for k, v in arrays.items():
+            if v.dtype == np.int64:
+                setattr(L, k, v.ctypes.data_as(N.P_i64))
+            elif v.dtype == np.int32:
+                setattr(L, k, v.ctypes.data_as(N.P_i32))
+            elif v.dtype == np.float32:
+                setattr(L, k, v.ctypes.data_as(N.P_f32))
+            else:
+                setattr(L, k, v.ctypes.data_as(N.P_f64))
+        L.n_splits = int(arrays["split_left"].shape[0])
+        lib = N.lib()
+        handle = ct.c_void_p()
+        with torch.cuda.device(self.device):
+            N.check(lib.kb_plan_create(ct.byref(L), ct.byref(handle)))
+        self._plan = handle
+        self.S, self.C, self.n_fam = S, C, int(roots.shape[0])
+        self.root_row_ids = torch.as_tensor(roots, device=self.device)
+        self.n_waves = len(ws)
+        self.n_splits = L.n_splits
+        self.last_n_e_iter = None
+        self.last_n_bicgstab = None
+
+    def close(self):
+        if getattr(self, "_plan", None):
+            N.lib().kb_plan_destroy(self._plan)
+            self._plan = None
+
+    def __del__(self):  # pragma: no cover - interpreter shutdown order
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ------------------------------------------------------------------
+    def _use_col(self, col_weights) -> bool:
+        flat = col_weights.detach().reshape(-1)
+        return not bool(torch.all(flat == flat[0]).item())
+
+    def run_forward(self, theta, col_weights, *, use_col_weights=None):
+        """theta -> (loss, saved), the reference ``run_forward`` contract."""
+        so = self.so
+        dev = self.device
+        S, C = self.S, self.C
+        theta = theta.detach().to(device=dev, dtype=torch.float32).contiguous()
+        col_weights = col_weights.detach().to(device=dev, dtype=torch.float32).contiguous()
+        if self.statewise and tuple(theta.shape) != (S, 3):
+            raise ValueError(f"statewise theta must have shape ({S}, 3), got {tuple(theta.shape)}")
+        if not self.statewise and tuple(theta.shape) != (3,):
+            raise ValueError(f"theta must have shape (3,), got {tuple(theta.shape)}")
+        use_col = self._use_col(col_weights) if use_col_weights is None else bool(use_col_weights)
+        f32 = dict(device=dev, dtype=torch.float32)
+        E, E_s1, E_s2, Ebar = (torch.empty((1, S), **f32) for _ in range(4))
+        npar = S if self.statewise else 1
+        pS, pD, pL = (torch.empty((npar,), **f32) for _ in range(3))
+        mt = torch.empty((S,), **f32)
+        col = torch.empty((S,), **f32)
+        pi = torch.empty((C, S), **f32)
+        pibar = torch.empty((C, S), **f32)
+        rowmax = torch.empty((C,), **f32)
+        loss = torch.empty((), **f32)
+        io = N.KbForwardIO(
+            theta=N.ptr(theta), statewise=int(self.statewise), col_weights=N.ptr(col_weights),
+            use_col_weights=int(use_col), e_init=float(so["e_init"]), e_max_iter=int(so["e_max_iter"]),
+            e_tol=float(so["e_tol"]), pi_iters=int(so["pi_iters"]),
+            E=N.ptr(E), E_s1=N.ptr(E_s1), E_s2=N.ptr(E_s2), Ebar=N.ptr(Ebar),
+            log_pS=N.ptr(pS), log_pD=N.ptr(pD), log_pL=N.ptr(pL), max_coupling=N.ptr(mt),
+            col_log_probs=N.ptr(col), pi=N.ptr(pi), pibar=N.ptr(pibar), pibar_row_max=N.ptr(rowmax),
+            loss=N.ptr(loss),
+        )
+        with torch.cuda.device(dev):
+            N.check(N.lib().kb_forward(self._plan, ct.byref(io), N.stream_handle(dev)))
+        if not self.statewise:
+            pS, pD, pL = (t.reshape(()) for t in (pS, pD, pL))
+        saved = dict(zip(FORWARD_SAVED_NAMES, (
+            E, E_s1, E_s2, Ebar, pi.index_select(0, self.root_row_ids), pi, pibar, rowmax,
+            pS, pD, pL, mt, col,
+        )))
+        saved["_use_col_weights"] = use_col
+        return loss, saved
+
+    def forward_stats(self):
+        n = ct.c_int32()
+        l64 = ct.c_double()
+        with torch.cuda.device(self.device):
+            N.check(N.lib().kb_forward_stats(self._plan, ct.byref(n), ct.byref(l64), N.stream_handle(self.device)))
+        self.last_n_e_iter = int(n.value)
+        return {"n_e_iter": int(n.value), "loss64": float(l64.value)}
+
+    def run_backward(self, theta, col_weights, saved, *, return_info=False):
+        """(forward intermediates) -> (grad_theta, grad_col), the reference ``run_backward`` contract."""
+        lib = N.lib()
+        if not hasattr(lib, "kb_backward"):
+            raise N.NativeLibraryMissing("libkbench_hip was built without kb_backward")
+        so = self.so
+        if str(so["self_loop_solver"]).strip().lower() != "neumann":
+            raise NotImplementedError("the fused backward implements the neumann self-loop solver")
+        dev = self.device
+        S, C = self.S, self.C
+        theta_d = theta.detach().to(device=dev, dtype=torch.float32).contiguous()
+        cw = col_weights.detach().to(device=dev, dtype=torch.float32).contiguous()
+        use_col = self._use_col(cw)
+        f32 = dict(device=dev, dtype=torch.float32)
+        grad_theta = torch.empty(tuple(theta_d.shape), **f32)
+        grad_col = torch.empty((S,), **f32)
+        mask = torch.empty((C,), device=dev, dtype=torch.uint8)
+        acc = torch.empty((8, S), device=dev, dtype=torch.float64) if return_info else None
+        c = lambda name: saved[name].detach().to(device=dev, dtype=torch.float32).contiguous()
+        tens = {k: c(k) for k in ("E", "E_s1", "E_s2", "Ebar", "log_pS", "log_pD", "log_pL", "max_coupling",
+                                  "col_log_probs", "pi_wave", "pibar_wave", "pibar_row_max")}
+        io = N.KbBackwardIO(
+            theta=N.ptr(theta_d), statewise=int(self.statewise), col_weights=N.ptr(cw), use_col_weights=int(use_col),
+            neumann_terms=int(so["neumann_terms"]), pruning_threshold=float(so["adjoint_pruning_threshold"]),
+            use_pruning=int(bool(so["use_adjoint_pruning"])), bicgstab_max_iter=int(so["bicgstab_max_iter"]),
+            bicgstab_tol=float(so["bicgstab_tol"]), bicgstab_breakdown_tol=float(so["bicgstab_breakdown_tol"]),
+            E=N.ptr(tens["E"]), E_s1=N.ptr(tens["E_s1"]), E_s2=N.ptr(tens["E_s2"]), Ebar=N.ptr(tens["Ebar"]),
+            log_pS=N.ptr(tens["log_pS"]), log_pD=N.ptr(tens["log_pD"]), log_pL=N.ptr(tens["log_pL"]),
+            max_coupling=N.ptr(tens["max_coupling"]), col_log_probs=N.ptr(tens["col_log_probs"]),
+            pi=N.ptr(tens["pi_wave"]), pibar=N.ptr(tens["pibar_wave"]), pibar_row_max=N.ptr(tens["pibar_row_max"]),
+            grad_theta=N.ptr(grad_theta), grad_col=N.ptr(grad_col), active_mask=N.ptr(mask), acc_out=N.ptr(acc),
+        )
+        self._keep = (tens, theta_d, cw)
+        with torch.cuda.device(dev):
+            N.check(lib.kb_backward(self._plan, ct.byref(io), N.stream_handle(dev)))
+        if return_info:
+            return grad_theta, grad_col, {"active_mask": mask, "acc": acc}
+        return grad_theta, grad_col
+
+    def backward_stats(self):
+        n = ct.c_int32()
+        with torch.cuda.device(self.device):
+            N.check(N.lib().kb_backward_stats(self._plan, ct.byref(n), N.stream_handle(self.device)))
+        self.last_n_bicgstab = int(n.value)
+        return {"n_bicgstab": int(n.value)}
+
+
+def static_from_problem(problem: dict, device) -> SimpleNamespace:
+    """Torch ``static`` namespace (the reference ``make_static`` result) from a generated problem."""
+    from .runtime import make_static
+
+    return make_static(problem_to_captured(problem), device)
+
+
+def problem_to_captured(problem: dict) -> dict:
+    """Generated numpy problem -> the reference's captured-dict format with torch tensors."""
+
+    def conv(x):
+        if isinstance(x, np.ndarray):
+            if x.dtype == np.float64:
+                return torch.from_numpy(x.astype(np.float32))
+            return torch.from_numpy(x)
+        if isinstance(x, dict):
+            return {k: conv(v) for k, v in x.items()}
+        if isinstance(x, list):
+            return [conv(v) for v in x]
+        return x
+
+    st = problem["static"]
+    return {
+        "meta": dict(problem["meta"]),
+        "static": {
+            "wave_layout": conv(st["wave_layout"]),
+            "state_helpers": conv(st["state_helpers"]),
+            "rate_item_idx": conv(st["rate_item_idx"]),
+            "itemwise": st["itemwise"],
+            "statewise": st["statewise"],
+        },
+        "inputs": {k: conv(v) for k, v in problem["inputs"].items()},
+    }

@@ -113,6 +113,55 @@ int kb_forward(kb_plan* plan, const kb_forward_io* io, void* stream);
 /* Synchronises `stream`; returns the E-step iteration count and the float64 loss. */
 int kb_forward_stats(kb_plan* plan, int32_t* n_e_iter, double* loss64, void* stream);
 
+/*
+ * Whole backward pass: forward intermediates -> (grad_theta, grad_col).
+ * Replaces reference kbench/runtime.py:77-115 run_backward, i.e.
+ * _implicit_grad.py:97-370 (per wave in reverse:
+ * active_mask_from_rhs_absmax_fused wave_backward.py:168-201,
+ * compute_dts_forward with active parents, wave_backward_uniform_fused
+ * wave_backward.py:1398-1522, the _scatter_accum bucket sums,
+ * dts_cross_backward_accum_fused wave_backward.py:1980-2190,
+ * uniform_cross_pibar_vjp_tree_from_ud_fused wave_backward.py:2330-2446)
+ * and _e_adjoint_and_theta_vjp _implicit_grad.py:373-475 (BiCGSTAB + VJP).
+ * One fused kernel per wave; child adjoints are gathered from per-split
+ * staging rows in a fixed order (no atomics), so the result is bitwise
+ * reproducible.  A BiCGSTAB failure is reported by kb_backward_stats.
+ */
+typedef struct kb_backward_io {
+  const float* theta;
+  int32_t statewise;
+  const float* col_weights;
+  int32_t use_col_weights;
+  int32_t neumann_terms;
+  double pruning_threshold;
+  int32_t use_pruning;
+  int32_t bicgstab_max_iter;
+  double bicgstab_tol;
+  double bicgstab_breakdown_tol;
+  const float* E;            /* saved forward tensors (kb_forward_io shapes) */
+  const float* E_s1;
+  const float* E_s2;
+  const float* Ebar;
+  const float* log_pS;
+  const float* log_pD;
+  const float* log_pL;
+  const float* max_coupling;
+  const float* col_log_probs;
+  const float* pi;
+  const float* pibar;
+  const float* pibar_row_max;
+  float* grad_theta;         /* theta's shape */
+  float* grad_col;           /* [S] */
+  uint8_t* active_mask;      /* optional [C] out: 1 = row active */
+  double* acc_out;           /* optional [8,S] out: gradient accumulators
+                                (pD, pS, E, Ebar, E_s1, E_s2, max_coupling, col) */
+} kb_backward_io;
+
+int kb_backward(kb_plan* plan, const kb_backward_io* io, void* stream);
+
+/* Synchronises `stream`; BiCGSTAB iteration count; KB_ERR_SOLVE if it failed. */
+int kb_backward_stats(kb_plan* plan, int32_t* n_iter, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -72,6 +72,13 @@ struct kb_plan {
   float* c_pD = nullptr; float* c_colw = nullptr;
   float* lin_a = nullptr; float* lin_emc = nullptr; float* lin_k1 = nullptr; float* lin_k2 = nullptr;
   double* E64 = nullptr; int* n_e_iter = nullptr; double* loss_terms = nullptr; double* loss64 = nullptr;
+  int* d_root_index = nullptr;
+  int64_t n_splits = 0;
+  // backward work (allocated on first use)
+  float* b_staging = nullptr; unsigned char* b_split_on = nullptr; unsigned char* b_mask = nullptr;
+  float* b_contrib = nullptr; double* b_partial = nullptr; double* b_acc = nullptr; double* b_work = nullptr;
+  int* b_status = nullptr;
+  float* b_DL = nullptr; float* b_SL1 = nullptr; float* b_SL2 = nullptr; float* b_pS = nullptr; float* b_pD = nullptr;
   std::vector<void*> owned;
 
   kb::TreeDev tree() const {
@@ -180,6 +187,16 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
   }
   for (int f = 0; f < L->n_fam; ++f) roots[f] = (int)L->root_row_ids[f];
   const int64_t NS = L->n_splits;
+  // rows -> wave; every wave a contiguous row range, in order
+  std::vector<int> wave_of(C, -1);
+  for (int w = 0; w < L->n_waves; ++w) {
+    const int64_t b = L->wave_start[w], e = b + L->wave_size[w];
+    if (b < 0 || e > C || L->wave_size[w] < 0) {
+      kb_plan_destroy(p);
+      return set_error(KB_ERR_ARG, "wave %d covers rows [%lld,%lld) outside [0,%d)", w, (long long)b, (long long)e, C);
+    }
+    for (int64_t r = b; r < e; ++r) wave_of[r] = w;
+  }
   std::vector<int> cnt(C + 1, 0);
   for (int64_t i = 0; i < NS; ++i) {
     int64_t pr = L->split_parent[i];
@@ -188,9 +205,10 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
       return set_error(KB_ERR_ARG, "split %lld has parent row %lld outside [0,%d)", (long long)i, (long long)pr, C);
     }
     int64_t a = L->split_left[i], b = L->split_right[i];
-    if (a < 0 || a >= pr || b < 0 || b >= pr) {
+    if (a < 0 || a >= C || b < 0 || b >= C || wave_of[pr] < 0 || wave_of[a] < 0 || wave_of[b] < 0 ||
+        wave_of[a] >= wave_of[pr] || wave_of[b] >= wave_of[pr]) {
       kb_plan_destroy(p);
-      return set_error(KB_ERR_ARG, "split %lld children (%lld,%lld) must precede parent row %lld",
+      return set_error(KB_ERR_ARG, "split %lld children (%lld,%lld) must lie in waves before parent row %lld",
                        (long long)i, (long long)a, (long long)b, (long long)pr);
     }
     cnt[pr + 1]++;
@@ -225,6 +243,15 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
     p->wave_split.push_back(L->wave_has_splits[w] ? 1 : 0);
   }
   std::vector<float> unnorm(L->unnorm_row_max, L->unnorm_row_max + S);
+  std::vector<int> root_index(C, -1);
+  for (int f = 0; f < L->n_fam; ++f) {
+    if (roots[f] < 0 || roots[f] >= C) {
+      kb_plan_destroy(p);
+      return set_error(KB_ERR_ARG, "root_row_ids[%d]=%d outside [0,%d)", f, roots[f], C);
+    }
+    root_index[roots[f]] = f;
+  }
+  p->n_splits = NS;
 
   int rc = 0;
   rc |= upload(&p->d_parent, parent);
@@ -248,6 +275,7 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
   rc |= upload(&p->d_child_ptr, ccnt);
   rc |= upload(&p->d_child_in, cin);
   rc |= upload(&p->d_unnorm, unnorm);
+  rc |= upload(&p->d_root_index, root_index);
   rc |= alloc(&p->c_DL, S);
   rc |= alloc(&p->c_SL1, S);
   rc |= alloc(&p->c_SL2, S);
@@ -269,7 +297,7 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
                     (void*)p->d_child_ptr, (void*)p->d_child_in, (void*)p->d_unnorm, (void*)p->c_DL, (void*)p->c_SL1,
                     (void*)p->c_SL2, (void*)p->c_pS, (void*)p->c_pD, (void*)p->c_colw, (void*)p->lin_a,
                     (void*)p->lin_emc, (void*)p->lin_k1, (void*)p->lin_k2, (void*)p->E64, (void*)p->n_e_iter,
-                    (void*)p->loss_terms, (void*)p->loss64})
+                    (void*)p->loss_terms, (void*)p->loss64, (void*)p->d_root_index})
     p->owned.push_back(ptr);
   if (rc) {
     kb_plan_destroy(p);
@@ -369,6 +397,143 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
   KB_HIP(hipGetLastError());
   kb::launch_loss(io->pi, p->d_roots, io->E, S, p->n_fam, p->loss_terms, p->loss64, io->loss, st);
   KB_HIP(hipGetLastError());
+  return 0;
+}
+
+static int ensure_backward_work(kb_plan* p) {
+  if (p->b_contrib) return 0;
+  const int S = p->S, C = p->C;
+  const int64_t NS = p->n_splits;
+  int rc = 0;
+  rc |= alloc(&p->b_staging, (size_t)std::max<int64_t>(1, 2 * NS) * S);
+  rc |= alloc(&p->b_split_on, (size_t)std::max<int64_t>(1, NS));
+  rc |= alloc(&p->b_mask, (size_t)std::max(1, C));
+  rc |= alloc(&p->b_contrib, (size_t)std::max(1, C) * 8 * S);
+  rc |= alloc(&p->b_partial, (size_t)kb::reduce_chunks(std::max(1, C)) * 8 * S);
+  rc |= alloc(&p->b_acc, (size_t)8 * S);
+  rc |= alloc(&p->b_work, (size_t)kb::epilogue_work_vectors() * S);
+  rc |= alloc(&p->b_status, 2);
+  rc |= alloc(&p->b_DL, S);
+  rc |= alloc(&p->b_SL1, S);
+  rc |= alloc(&p->b_SL2, S);
+  rc |= alloc(&p->b_pS, S);
+  rc |= alloc(&p->b_pD, S);
+  for (void* ptr : {(void*)p->b_staging, (void*)p->b_split_on, (void*)p->b_mask, (void*)p->b_contrib,
+                    (void*)p->b_partial, (void*)p->b_acc, (void*)p->b_work, (void*)p->b_status, (void*)p->b_DL,
+                    (void*)p->b_SL1, (void*)p->b_SL2, (void*)p->b_pS, (void*)p->b_pD})
+    p->owned.push_back(ptr);
+  return rc ? KB_ERR_HIP : 0;
+}
+
+int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
+  if (!p || !io) return set_error(KB_ERR_ARG, "null argument");
+  if (io->neumann_terms < 0) return set_error(KB_ERR_ARG, "neumann_terms must be non-negative");
+  if (io->bicgstab_max_iter < 1) return set_error(KB_ERR_ARG, "max_iter must be at least 1");
+  if (!(io->bicgstab_tol > 0.0)) return set_error(KB_ERR_ARG, "tol must be positive");
+  if (!(io->bicgstab_breakdown_tol > 0.0)) return set_error(KB_ERR_ARG, "breakdown_tol must be positive");
+  if (io->pruning_threshold < 0.0) return set_error(KB_ERR_ARG, "adjoint_pruning_threshold must be non-negative");
+  int rc = ensure_backward_work(p);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  const int S = p->S, C = p->C;
+
+  kb::BwdConstArgs K{};
+  K.S = S;
+  K.statewise = io->statewise;
+  K.log_pS = io->log_pS;
+  K.log_pD = io->log_pD;
+  K.E = io->E;
+  K.E_s1 = io->E_s1;
+  K.E_s2 = io->E_s2;
+  K.DL = p->b_DL;
+  K.SL1 = p->b_SL1;
+  K.SL2 = p->b_SL2;
+  K.pS_state = p->b_pS;
+  K.pD_state = p->b_pD;
+  kb::launch_bwd_consts(K, st);
+
+  kb::BwdParams B{};
+  B.tr = p->tree();
+  B.S = S;
+  B.n_terms = io->neumann_terms;
+  B.thr = (float)io->pruning_threshold;
+  B.use_pruning = io->use_pruning;
+  B.use_col = io->use_col_weights;
+  B.const_stride = 0;
+  B.DL = p->b_DL;
+  B.Ebar = io->Ebar;
+  B.E = io->E;
+  B.SL1 = p->b_SL1;
+  B.SL2 = p->b_SL2;
+  B.mt = io->max_coupling;
+  B.col = io->col_log_probs;
+  B.leaf_logp = p->b_pS;
+  B.pD = kb::RateDev{p->b_pD, 0, 1};
+  B.pS = kb::RateDev{p->b_pS, 0, 1};
+  B.pi = io->pi;
+  B.pibar = io->pibar;
+  B.rowmax = io->pibar_row_max;
+  B.item = p->d_item;
+  B.leaf_state = p->d_leaf;
+  B.root_index = p->d_root_index;
+  B.split_ptr = p->d_split_ptr;
+  B.split_l = p->d_split_l;
+  B.split_r = p->d_split_r;
+  B.split_lsp = p->d_split_lsp;
+  B.child_ptr = p->d_child_ptr;
+  B.child_in = p->d_child_in;
+  B.staging = p->b_staging;
+  B.split_on = p->b_split_on;
+  B.mask = io->active_mask ? (unsigned char*)io->active_mask : p->b_mask;
+  B.contrib = p->b_contrib;
+  for (int w = p->n_waves - 1; w >= 0; --w)
+    kb::launch_bwd_wave(B, p->wave_start[w], p->wave_size[w], p->wave_split[w] ? 0 : 1, st);
+  KB_HIP(hipGetLastError());
+  kb::launch_bwd_reduce(p->b_contrib, B.mask, C, S, p->b_partial, p->b_acc, st);
+  KB_HIP(hipGetLastError());
+  if (io->acc_out)
+    KB_HIP(hipMemcpyAsync(io->acc_out, p->b_acc, (size_t)8 * S * sizeof(double), hipMemcpyDeviceToDevice, st));
+
+  kb::EpiParams X{};
+  X.tr = p->tree();
+  X.S = S;
+  X.n_tlevels = p->n_tlevels;
+  X.tlevel_ptr = p->d_tlevel_ptr;
+  X.tlevel_node = p->d_tlevel_node;
+  X.E = io->E;
+  X.log_pS = io->log_pS;
+  X.log_pD = io->log_pD;
+  X.log_pL = io->log_pL;
+  X.mt = io->max_coupling;
+  X.col = io->col_log_probs;
+  X.statewise = io->statewise;
+  X.use_col = io->use_col_weights;
+  X.theta = io->theta;
+  X.col_weights = io->col_weights;
+  X.acc = p->b_acc;
+  X.n_fam = p->n_fam;
+  X.n_items_rows = 1;
+  X.max_iter = io->bicgstab_max_iter;
+  X.tol = io->bicgstab_tol;
+  X.breakdown = io->bicgstab_breakdown_tol;
+  X.grad_theta = io->grad_theta;
+  X.grad_col = io->grad_col;
+  X.work = p->b_work;
+  X.status = p->b_status;
+  kb::launch_epilogue(X, st);
+  KB_HIP(hipGetLastError());
+  return 0;
+}
+
+int kb_backward_stats(kb_plan* p, int32_t* n_iter, void* stream) {
+  if (!p) return set_error(KB_ERR_ARG, "null argument");
+  if (!p->b_status) return set_error(KB_ERR_ARG, "no backward has run on this plan");
+  KB_HIP(hipStreamSynchronize((hipStream_t)stream));
+  int st[2];
+  KB_HIP(hipMemcpy(st, p->b_status, sizeof(st), hipMemcpyDeviceToHost));
+  if (n_iter) *n_iter = st[0];
+  if (st[1])
+    return set_error(KB_ERR_SOLVE, "E-adjoint BiCGSTAB solve failed after %d iterations", st[0]);
   return 0;
 }
 

@@ -65,4 +65,68 @@ struct FwdParams {
 
 void launch_fwd_wave(const FwdParams& P, int ws, int W, int leaf_wave, hipStream_t st);
 
+// ----------------------------------------------------------------------------
+// backward (kb_bwd.hip, kb_epi.hip)
+// ----------------------------------------------------------------------------
+struct BwdConstArgs {
+  int S;
+  int statewise;
+  const float* log_pS; const float* log_pD; const float* E; const float* E_s1; const float* E_s2;
+  float* DL; float* SL1; float* SL2; float* pS_state; float* pD_state;
+};
+
+struct BwdParams {
+  TreeDev tr;
+  int S;
+  int n_terms;                // neumann_terms
+  float thr;                  // adjoint_pruning_threshold
+  int use_pruning;
+  int use_col;
+  int const_stride;
+  const float* DL; const float* Ebar; const float* E; const float* SL1; const float* SL2;
+  const float* mt; const float* col;
+  const float* leaf_logp;     // [G,S] log pS
+  RateDev pD, pS;
+  const float* pi; const float* pibar; const float* rowmax;
+  const int* item; const int* leaf_state; const int* root_index;
+  const int* split_ptr; const int* split_l; const int* split_r; const float* split_lsp;
+  const int* child_ptr; const int* child_in;
+  float* staging;             // [2 * n_splits, S]
+  unsigned char* split_on;    // [n_splits]
+  unsigned char* mask;        // [C]
+  float* contrib;             // [C, 8, S]
+};
+
+struct EpiParams {
+  TreeDev tr;
+  int S;
+  int n_tlevels;
+  const int* tlevel_ptr;
+  const int* tlevel_node;
+  const float* E; const float* log_pS; const float* log_pD; const float* log_pL; const float* mt;
+  const float* col;
+  int statewise;
+  int use_col;
+  const float* theta;
+  const float* col_weights;
+  const double* acc;          // [8, S]
+  int n_fam;
+  int n_items_rows;           // rows of E (1 unless itemwise)
+  int max_iter;
+  double tol;
+  double breakdown;
+  float* grad_theta;
+  float* grad_col;
+  double* work;               // [N_WORK, S]
+  int* status;                // [0] iterations, [1] failure flag
+};
+
+void launch_bwd_consts(const BwdConstArgs& A, hipStream_t st);
+void launch_bwd_wave(const BwdParams& P, int ws, int W, int leaf_wave, hipStream_t st);
+void launch_bwd_reduce(const float* contrib, const unsigned char* mask, int C, int S, double* partial,
+                       double* out, hipStream_t st);
+int reduce_chunks(int C);
+void launch_epilogue(const EpiParams& P, hipStream_t st);
+int epilogue_work_vectors();
+
 }  // namespace kb

@@ -41,3 +41,32 @@ def test_fused_forward_matches_oracle(name, statewise):
         ok, ma, mr = kbtest.compare_inf_safe(saved[k].cpu().numpy(), ref[k])
         print(f"  {k}: ok={ok} max_abs={ma:.3e} max_rel={mr:.3e}")
         assert ok and (ma <= 2e-4 or mr <= 1e-5)
+
+
+@pytest.mark.parametrize("name,statewise", [("tiny", None), ("1", None), ("1", True), ("2", None)])
+def test_fused_backward_matches_oracle(name, statewise):
+    print(f"[fused-backward] config={name} statewise={statewise}", flush=True)
+    solver, static, theta, cw, loss, saved = _run_fused_forward(name, statewise)
+    gt, gc, info = solver.run_backward(theta, cw, saved, return_info=True)
+    stats = solver.backward_stats()
+    torch.cuda.synchronize()
+    # oracle backward on the oracle's own forward (independent chain)
+    ref_gt, ref_gc, ref_info = kbtest.oracle_backward(name, statewise)
+    rt = kbtest.norm_rel(gt.cpu().numpy(), ref_gt)
+    rc = kbtest.norm_rel(gc.cpu().numpy(), ref_gc)
+    print(f"  grad_theta normrel={rt:.3e}  grad_col normrel={rc:.3e}  bicgstab={stats['n_bicgstab']}/{ref_info['n_bicgstab']}")
+    mask = info["active_mask"].cpu().numpy().astype(bool)
+    ref_mask = np.zeros_like(mask)
+    for ws, act in ref_info["masks"]:
+        ref_mask[ws:ws + act.shape[0]] = act
+    print(f"  active rows got={mask.sum()} ref={ref_mask.sum()} mismatches={(mask != ref_mask).sum()}")
+    acc = info["acc"].cpu().numpy()
+    names = ["g_pD", "g_pS", "g_E", "g_Ebar", "g_Es1", "g_Es2", "g_mt", "g_col"]
+    for j, nm in enumerate(names):
+        ref = np.asarray(ref_info["acc"][nm], dtype=np.float64).reshape(-1)
+        got = acc[j]
+        if ref.size == 1:
+            got = np.array([got.sum()])
+        print(f"  acc {nm}: normrel={kbtest.norm_rel(got, ref):.3e}")
+    assert (mask == ref_mask).all()
+    assert rt <= 1e-4 and rc <= 1e-4

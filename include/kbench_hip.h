@@ -162,6 +162,16 @@ int kb_backward(kb_plan* plan, const kb_backward_io* io, void* stream);
 /* Synchronises `stream`; BiCGSTAB iteration count; KB_ERR_SOLVE if it failed. */
 int kb_backward_stats(kb_plan* plan, int32_t* n_iter, void* stream);
 
+/*
+ * Measurement hooks (no reference counterpart: the reference is timed with
+ * CUDA events around whole passes, bench/_common.py:49-77).  When enabled,
+ * kb_forward / kb_backward record a HIP event pair around every wave-kernel
+ * launch on the launch stream; kb_profile_read returns the per-wave launch
+ * durations (ms) of the last pass (which = 0 forward, 1 backward).
+ */
+int kb_profile_enable(kb_plan* plan, int enable);
+int kb_profile_read(kb_plan* plan, int which, float* ms, int n);
+
 #ifdef __cplusplus
 }
 #endif

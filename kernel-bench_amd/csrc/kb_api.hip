@@ -57,6 +57,12 @@ struct kb_plan {
   int S = 0, C = 0, n_fam = 0, n_waves = 0;
   int n_jump = 0, n_tlevels = 0, n_blevels = 0;
   std::vector<int> wave_start, wave_size, wave_split;
+  // dependency levels: rows grouped by clade-DAG depth (0 = no splits); a row
+  // only reads its own children, so level order is a valid schedule
+  int n_levels = 0;
+  std::vector<int> level_ptr;
+  int* d_sched_rows = nullptr;
+  int* d_row_kind = nullptr;  // 1: row of a leaf wave (leaf initialisation), 0: split row
   // device tables
   int* d_parent = nullptr; int* d_c1 = nullptr; int* d_c2 = nullptr; int* d_jump = nullptr;
   int* d_blevel_ptr = nullptr; int* d_blevel_node = nullptr;
@@ -79,6 +85,9 @@ struct kb_plan {
   float* b_contrib = nullptr; double* b_partial = nullptr; double* b_acc = nullptr; double* b_work = nullptr;
   int* b_status = nullptr;
   float* b_DL = nullptr; float* b_SL1 = nullptr; float* b_SL2 = nullptr; float* b_pS = nullptr; float* b_pD = nullptr;
+  // optional per-launch timing of the wave kernels (HIP events on the launch stream)
+  int prof = 0;
+  std::vector<hipEvent_t> ev_fwd, ev_bwd;
   std::vector<void*> owned;
 
   kb::TreeDev tree() const {
@@ -106,6 +115,8 @@ int kb_abi_version(void) { return KB_ABI_VERSION; }
 
 void kb_plan_destroy(kb_plan* p) {
   if (!p) return;
+  for (hipEvent_t e : p->ev_fwd) (void)hipEventDestroy(e);
+  for (hipEvent_t e : p->ev_bwd) (void)hipEventDestroy(e);
   for (void* ptr : p->owned)
     if (ptr) (void)hipFree(ptr);
   delete p;
@@ -252,6 +263,21 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
     root_index[roots[f]] = f;
   }
   p->n_splits = NS;
+  // DAG depth of every row (children precede parents: checked above)
+  std::vector<int> row_kind(C, 0), dagd(C, 0);
+  for (int w = 0; w < L->n_waves; ++w)
+    for (int64_t r = L->wave_start[w]; r < L->wave_start[w] + L->wave_size[w]; ++r)
+      row_kind[r] = L->wave_has_splits[w] ? 0 : 1;
+  for (int r = 0; r < C; ++r)
+    for (int i = sptr[r]; i < sptr[r + 1]; ++i) dagd[r] = std::max(dagd[r], 1 + std::max(dagd[sl[i]], dagd[sr[i]]));
+  int maxdag = 0;
+  for (int r = 0; r < C; ++r) maxdag = std::max(maxdag, dagd[r]);
+  p->n_levels = C > 0 ? maxdag + 1 : 0;
+  p->level_ptr.assign(p->n_levels + 1, 0);
+  for (int r = 0; r < C; ++r) p->level_ptr[dagd[r] + 1]++;
+  for (int d = 0; d < p->n_levels; ++d) p->level_ptr[d + 1] += p->level_ptr[d];
+  std::vector<int> sched(C), lfill(p->level_ptr.begin(), p->level_ptr.end() - 1);
+  for (int r = 0; r < C; ++r) sched[lfill[dagd[r]]++] = r;
 
   int rc = 0;
   rc |= upload(&p->d_parent, parent);
@@ -276,6 +302,8 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
   rc |= upload(&p->d_child_in, cin);
   rc |= upload(&p->d_unnorm, unnorm);
   rc |= upload(&p->d_root_index, root_index);
+  rc |= upload(&p->d_sched_rows, sched);
+  rc |= upload(&p->d_row_kind, row_kind);
   rc |= alloc(&p->c_DL, S);
   rc |= alloc(&p->c_SL1, S);
   rc |= alloc(&p->c_SL2, S);
@@ -297,7 +325,8 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
                     (void*)p->d_child_ptr, (void*)p->d_child_in, (void*)p->d_unnorm, (void*)p->c_DL, (void*)p->c_SL1,
                     (void*)p->c_SL2, (void*)p->c_pS, (void*)p->c_pD, (void*)p->c_colw, (void*)p->lin_a,
                     (void*)p->lin_emc, (void*)p->lin_k1, (void*)p->lin_k2, (void*)p->E64, (void*)p->n_e_iter,
-                    (void*)p->loss_terms, (void*)p->loss64, (void*)p->d_root_index})
+                    (void*)p->loss_terms, (void*)p->loss64, (void*)p->d_root_index,
+                    (void*)p->d_sched_rows, (void*)p->d_row_kind})
     p->owned.push_back(ptr);
   if (rc) {
     kb_plan_destroy(p);
@@ -309,8 +338,8 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
 
 int kb_plan_info(const kb_plan* p, int32_t* out, int n) {
   if (!p || !out) return set_error(KB_ERR_ARG, "null argument");
-  int32_t v[6] = {p->S, p->C, p->n_fam, p->n_waves, p->n_jump, p->n_blevels};
-  for (int i = 0; i < n && i < 6; ++i) out[i] = v[i];
+  int32_t v[7] = {p->S, p->C, p->n_fam, p->n_waves, p->n_jump, p->n_blevels, p->n_levels};
+  for (int i = 0; i < n && i < 7; ++i) out[i] = v[i];
   return 0;
 }
 
@@ -391,8 +420,12 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
   F.pi = io->pi;
   F.pibar = io->pibar;
   F.rowmax = io->pibar_row_max;
-  for (int w = 0; w < p->n_waves; ++w) {
-    kb::launch_fwd_wave(F, p->wave_start[w], p->wave_size[w], p->wave_split[w] ? 0 : 1, st);
+  F.sched_rows = p->d_sched_rows;
+  F.row_kind = p->d_row_kind;
+  for (int d = 0; d < p->n_levels; ++d) {
+    if (p->prof) KB_HIP(hipEventRecord(p->ev_fwd[2 * d], st));
+    kb::launch_fwd_wave(F, p->level_ptr[d], p->level_ptr[d + 1] - p->level_ptr[d], st);
+    if (p->prof) KB_HIP(hipEventRecord(p->ev_fwd[2 * d + 1], st));
   }
   KB_HIP(hipGetLastError());
   kb::launch_loss(io->pi, p->d_roots, io->E, S, p->n_fam, p->loss_terms, p->loss64, io->loss, st);
@@ -486,8 +519,13 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   B.split_on = p->b_split_on;
   B.mask = io->active_mask ? (unsigned char*)io->active_mask : p->b_mask;
   B.contrib = p->b_contrib;
-  for (int w = p->n_waves - 1; w >= 0; --w)
-    kb::launch_bwd_wave(B, p->wave_start[w], p->wave_size[w], p->wave_split[w] ? 0 : 1, st);
+  B.sched_rows = p->d_sched_rows;
+  B.row_kind = p->d_row_kind;
+  for (int d = p->n_levels - 1; d >= 0; --d) {
+    if (p->prof) KB_HIP(hipEventRecord(p->ev_bwd[2 * d], st));
+    kb::launch_bwd_wave(B, p->level_ptr[d], p->level_ptr[d + 1] - p->level_ptr[d], st);
+    if (p->prof) KB_HIP(hipEventRecord(p->ev_bwd[2 * d + 1], st));
+  }
   KB_HIP(hipGetLastError());
   kb::launch_bwd_reduce(p->b_contrib, B.mask, C, S, p->b_partial, p->b_acc, st);
   KB_HIP(hipGetLastError());
@@ -534,6 +572,29 @@ int kb_backward_stats(kb_plan* p, int32_t* n_iter, void* stream) {
   if (n_iter) *n_iter = st[0];
   if (st[1])
     return set_error(KB_ERR_SOLVE, "E-adjoint BiCGSTAB solve failed after %d iterations", st[0]);
+  return 0;
+}
+
+int kb_profile_enable(kb_plan* p, int enable) {
+  if (!p) return set_error(KB_ERR_ARG, "null argument");
+  if (enable && p->ev_fwd.empty()) {
+    p->ev_fwd.resize(2 * (size_t)std::max(1, p->n_levels));
+    p->ev_bwd.resize(2 * (size_t)std::max(1, p->n_levels));
+    for (auto& e : p->ev_fwd) KB_HIP(hipEventCreate(&e));
+    for (auto& e : p->ev_bwd) KB_HIP(hipEventCreate(&e));
+  }
+  p->prof = enable ? 1 : 0;
+  return 0;
+}
+
+int kb_profile_read(kb_plan* p, int which, float* ms, int n) {
+  if (!p || !ms) return set_error(KB_ERR_ARG, "null argument");
+  if (p->ev_fwd.empty()) return set_error(KB_ERR_ARG, "profiling was never enabled on this plan");
+  std::vector<hipEvent_t>& ev = which == 0 ? p->ev_fwd : p->ev_bwd;
+  for (int w = 0; w < n && w < p->n_levels; ++w) {
+    KB_HIP(hipEventSynchronize(ev[2 * w + 1]));
+    KB_HIP(hipEventElapsedTime(&ms[w], ev[2 * w], ev[2 * w + 1]));
+  }
   return 0;
 }
 

@@ -61,7 +61,7 @@ __device__ __forceinline__ void block_sum2(float& a, float& b, float* red) {
 }
 
 template <int NT, int CPT>
-__global__ __launch_bounds__(NT) void bwd_wave_kernel(BwdParams P, int ws, int leaf_wave) {
+__global__ __launch_bounds__(NT) void bwd_wave_kernel(BwdParams P, int first) {
   constexpr int MAXS = NT * CPT;
   __shared__ float B0[MAXS];
   __shared__ float B1[MAXS];
@@ -71,7 +71,8 @@ __global__ __launch_bounds__(NT) void bwd_wave_kernel(BwdParams P, int ws, int l
 
   const int S = P.S;
   const int tid = threadIdx.x;
-  const int row = ws + blockIdx.x;
+  const int row = P.sched_rows[first + blockIdx.x];
+  const int leaf_wave = P.row_kind[row];
   const int item = P.item[row];
   const size_t cb = (size_t)item * P.const_stride;
   const size_t rb = (size_t)row * S;
@@ -412,11 +413,11 @@ __global__ __launch_bounds__(NT) void bwd_wave_kernel(BwdParams P, int ws, int l
 
 #define KB_BWD_CASE(NT_, CPT_)                                                                   \
   if (S <= NT_ * CPT_) {                                                                         \
-    hipLaunchKernelGGL((bwd_wave_kernel<NT_, CPT_>), dim3(W), dim3(NT_), 0, st, P, ws, leaf_wave); \
+    hipLaunchKernelGGL((bwd_wave_kernel<NT_, CPT_>), dim3(W), dim3(NT_), 0, st, P, first);        \
     return;                                                                                      \
   }
 
-void launch_bwd_wave(const BwdParams& P, int ws, int W, int leaf_wave, hipStream_t st) {
+void launch_bwd_wave(const BwdParams& P, int first, int W, hipStream_t st) {
   if (W <= 0) return;
   const int S = P.S;
   KB_BWD_CASE(64, 1)

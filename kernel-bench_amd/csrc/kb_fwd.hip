@@ -23,7 +23,7 @@
 namespace kb {
 
 template <int NT, int CPT>
-__global__ __launch_bounds__(NT) void fwd_wave_kernel(FwdParams P, int ws, int leaf_wave) {
+__global__ __launch_bounds__(NT) void fwd_wave_kernel(FwdParams P, int first) {
   constexpr int MAXS = NT * CPT;
   __shared__ float X[MAXS];
   __shared__ float B0[MAXS];
@@ -32,7 +32,8 @@ __global__ __launch_bounds__(NT) void fwd_wave_kernel(FwdParams P, int ws, int l
 
   const int S = P.S;
   const int tid = threadIdx.x;
-  const int row = ws + blockIdx.x;
+  const int row = P.sched_rows[first + blockIdx.x];
+  const int leaf_wave = P.row_kind[row];
   const int item = P.item[row];
   const size_t cb = (size_t)item * P.const_stride;
 
@@ -215,11 +216,11 @@ __global__ __launch_bounds__(NT) void fwd_wave_kernel(FwdParams P, int ws, int l
 
 #define KB_FWD_CASE(NT_, CPT_)                                                                   \
   if (S <= NT_ * CPT_) {                                                                         \
-    hipLaunchKernelGGL((fwd_wave_kernel<NT_, CPT_>), dim3(W), dim3(NT_), 0, st, P, ws, leaf_wave); \
+    hipLaunchKernelGGL((fwd_wave_kernel<NT_, CPT_>), dim3(W), dim3(NT_), 0, st, P, first);        \
     return;                                                                                      \
   }
 
-void launch_fwd_wave(const FwdParams& P, int ws, int W, int leaf_wave, hipStream_t st) {
+void launch_fwd_wave(const FwdParams& P, int first, int W, hipStream_t st) {
   if (W <= 0) return;
   const int S = P.S;
   KB_FWD_CASE(64, 1)

@@ -59,11 +59,14 @@ struct FwdParams {
   const int* leaf_state;      // [C]
   const int* split_ptr;       // [C+1] splits of each parent row
   const int* split_l; const int* split_r; const float* split_lsp;
+  const int* sched_rows;      // rows in dependency-level order
+  const int* row_kind;        // 1: leaf row, 0: split row
   // outputs
   float* pi; float* pibar; float* rowmax;
 };
 
-void launch_fwd_wave(const FwdParams& P, int ws, int W, int leaf_wave, hipStream_t st);
+// Launch the rows sched_rows[first .. first + n).
+void launch_fwd_wave(const FwdParams& P, int first, int n, hipStream_t st);
 
 // ----------------------------------------------------------------------------
 // backward (kb_bwd.hip, kb_epi.hip)
@@ -95,6 +98,8 @@ struct BwdParams {
   unsigned char* split_on;    // [n_splits]
   unsigned char* mask;        // [C]
   float* contrib;             // [C, 8, S]
+  const int* sched_rows;
+  const int* row_kind;
 };
 
 struct EpiParams {
@@ -122,7 +127,7 @@ struct EpiParams {
 };
 
 void launch_bwd_consts(const BwdConstArgs& A, hipStream_t st);
-void launch_bwd_wave(const BwdParams& P, int ws, int W, int leaf_wave, hipStream_t st);
+void launch_bwd_wave(const BwdParams& P, int first, int n, hipStream_t st);
 void launch_bwd_reduce(const float* contrib, const unsigned char* mask, int C, int S, double* partial,
                        double* out, hipStream_t st);
 int reduce_chunks(int C);

@@ -90,6 +90,10 @@ def _declare(lib):
     if hasattr(lib, "kb_backward"):
         lib.kb_backward.argtypes = [vp, ct.POINTER(KbBackwardIO), vp]
         lib.kb_backward.restype = ct.c_int
+    lib.kb_profile_enable.argtypes = [vp, ct.c_int]
+    lib.kb_profile_enable.restype = ct.c_int
+    lib.kb_profile_read.argtypes = [vp, ct.c_int, P_f32, ct.c_int]
+    lib.kb_profile_read.restype = ct.c_int
     if hasattr(lib, "kb_backward_stats"):
         lib.kb_backward_stats.argtypes = [vp, P_i32, vp]
         lib.kb_backward_stats.restype = ct.c_int

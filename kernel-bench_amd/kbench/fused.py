@@ -145,6 +145,9 @@ class FusedSolver:
         self.root_row_ids = torch.as_tensor(roots, device=self.device)
         self.n_waves = len(ws)
         self.n_splits = L.n_splits
+        info = (ct.c_int32 * 7)()
+        N.check(lib.kb_plan_info(handle, info, 7))
+        self.n_levels = int(info[6])
         self.last_n_e_iter = None
         self.last_n_bicgstab = None
 
@@ -205,6 +208,39 @@ class FusedSolver:
         )))
         saved["_use_col_weights"] = use_col
         return loss, saved
+
+    def profile(self, enable: bool = True) -> None:
+        """Record HIP events around every wave-kernel launch of later passes."""
+        N.check(N.lib().kb_profile_enable(self._plan, int(bool(enable))))
+
+    def level_launch_ms(self, which: str):
+        """Per-level launch durations (ms) of the last forward / backward pass (``profile`` on).
+
+        Index d is dependency level d (the backward runs the levels in reverse).
+        """
+        out = (ct.c_float * self.n_levels)()
+        N.check(N.lib().kb_profile_read(self._plan, 0 if which == "forward" else 1, out, self.n_levels))
+        return np.asarray(out[:], dtype=np.float64)
+
+    def level_of_rows(self):
+        """Clade-DAG depth of every row: 0 without splits, else 1 + max over its children."""
+        a = self._arrays
+        depth = np.zeros(self.C, dtype=np.int64)
+        par, l, r = a["split_parent"], a["split_left"], a["split_right"]
+        order = np.argsort(par, kind="stable")
+        for i in order:  # parents in increasing row order; children precede parents
+            d = 1 + max(depth[l[i]], depth[r[i]])
+            if d > depth[par[i]]:
+                depth[par[i]] = d
+        return depth
+
+    def level_shapes(self):
+        """(rows, splits) of every dependency level."""
+        depth = self.level_of_rows()
+        rows = np.bincount(depth, minlength=self.n_levels)
+        par = self._arrays["split_parent"]
+        splits = np.bincount(depth[par], minlength=self.n_levels) if par.size else np.zeros_like(rows)
+        return rows.astype(np.int64), splits.astype(np.int64)
 
     def forward_stats(self):
         n = ct.c_int32()

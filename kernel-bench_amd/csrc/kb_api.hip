@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -77,6 +78,10 @@ struct kb_plan {
   float* c_DL = nullptr; float* c_SL1 = nullptr; float* c_SL2 = nullptr; float* c_pS = nullptr;
   float* c_pD = nullptr; float* c_colw = nullptr;
   float* lin_a = nullptr; float* lin_emc = nullptr; float* lin_k1 = nullptr; float* lin_k2 = nullptr;
+  float* c_Ebar = nullptr; float* c_E = nullptr; float* c_mt = nullptr; float* c_col = nullptr;
+  // preorder tables (see kb_rowops.hpp)
+  int* d_pre = nullptr; int* d_pcol = nullptr; int* d_c1pos = nullptr; int* d_c2pos = nullptr; int* d_ppos = nullptr;
+  int* d_pflag = nullptr; int* d_endpos = nullptr; int* d_tin = nullptr; int* d_euler = nullptr;
   double* E64 = nullptr; int* n_e_iter = nullptr; double* loss_terms = nullptr; double* loss64 = nullptr;
   int* d_root_index = nullptr;
   int64_t n_splits = 0;
@@ -89,6 +94,21 @@ struct kb_plan {
   int prof = 0;
   std::vector<hipEvent_t> ev_fwd, ev_bwd;
   std::vector<void*> owned;
+
+  kb::PreDev predev() const {
+    kb::PreDev t;
+    t.S = S;
+    t.pre = d_pre;
+    t.col = d_pcol;
+    t.c1pos = d_c1pos;
+    t.c2pos = d_c2pos;
+    t.ppos = d_ppos;
+    t.pflag = d_pflag;
+    t.endpos = d_endpos;
+    t.tin = d_tin;
+    t.euler = d_euler;
+    return t;
+  }
 
   kb::TreeDev tree() const {
     kb::TreeDev t;
@@ -185,6 +205,66 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
         any = true;
       }
     if (any) bptr.push_back((int)bnode.size());
+  }
+  // preorder (child1 first) and its Euler tour
+  std::vector<int> pre(S, -1), pcol(S), c1pos(S), c2pos(S), ppos(S), pflag(S, 0), endpos(S), tin(S), euler;
+  {
+    int root = -1;
+    for (int s = 0; s < S; ++s)
+      if (parent[s] < 0) {
+        if (root >= 0) {
+          kb_plan_destroy(p);
+          return set_error(KB_ERR_ARG, "node_parent has more than one root");
+        }
+        root = s;
+      }
+    if (root < 0) {
+      kb_plan_destroy(p);
+      return set_error(KB_ERR_ARG, "node_parent has no root");
+    }
+    std::vector<int> stack{root};
+    int order = 0;
+    while (!stack.empty()) {
+      int v = stack.back();
+      stack.pop_back();
+      pre[v] = order;
+      pcol[order] = v;
+      ++order;
+      if (c2[v] >= 0) stack.push_back(c2[v]);
+      if (c1[v] >= 0) stack.push_back(c1[v]);
+    }
+    if (order != S) {
+      kb_plan_destroy(p);
+      return set_error(KB_ERR_ARG, "species tree is not connected (%d of %d nodes reachable)", order, S);
+    }
+    std::vector<int> size(S, 1);
+    for (int i = S - 1; i >= 0; --i) {
+      int v = pcol[i];
+      if (c1[v] >= 0) size[v] += size[c1[v]];
+      if (c2[v] >= 0) size[v] += size[c2[v]];
+    }
+    for (int i = 0; i < S; ++i) {
+      int v = pcol[i];
+      c1pos[i] = c1[v] >= 0 ? pre[c1[v]] : -1;
+      c2pos[i] = c2[v] >= 0 ? pre[c2[v]] : -1;
+      ppos[i] = parent[v] >= 0 ? pre[parent[v]] : -1;
+      pflag[i] = (parent[v] >= 0 && c1[parent[v]] == v) ? 1 : 0;
+      endpos[i] = i + size[v];
+    }
+    std::vector<int> open;
+    for (int i = 0; i < S; ++i) {
+      while (!open.empty() && endpos[open.back()] <= i) {
+        euler.push_back((open.back() << 1) | 1);
+        open.pop_back();
+      }
+      tin[i] = (int)euler.size();
+      euler.push_back(i << 1);
+      open.push_back(i);
+    }
+    while (!open.empty()) {
+      euler.push_back((open.back() << 1) | 1);
+      open.pop_back();
+    }
   }
   p->n_jump = n_jump;
   p->n_tlevels = maxd + 1;
@@ -303,6 +383,19 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
   rc |= upload(&p->d_unnorm, unnorm);
   rc |= upload(&p->d_root_index, root_index);
   rc |= upload(&p->d_sched_rows, sched);
+  rc |= upload(&p->d_pre, pre);
+  rc |= upload(&p->d_pcol, pcol);
+  rc |= upload(&p->d_c1pos, c1pos);
+  rc |= upload(&p->d_c2pos, c2pos);
+  rc |= upload(&p->d_ppos, ppos);
+  rc |= upload(&p->d_pflag, pflag);
+  rc |= upload(&p->d_endpos, endpos);
+  rc |= upload(&p->d_tin, tin);
+  rc |= upload(&p->d_euler, euler);
+  rc |= alloc(&p->c_Ebar, S);
+  rc |= alloc(&p->c_E, S);
+  rc |= alloc(&p->c_mt, S);
+  rc |= alloc(&p->c_col, S);
   rc |= upload(&p->d_row_kind, row_kind);
   rc |= alloc(&p->c_DL, S);
   rc |= alloc(&p->c_SL1, S);
@@ -326,7 +419,10 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
                     (void*)p->c_SL2, (void*)p->c_pS, (void*)p->c_pD, (void*)p->c_colw, (void*)p->lin_a,
                     (void*)p->lin_emc, (void*)p->lin_k1, (void*)p->lin_k2, (void*)p->E64, (void*)p->n_e_iter,
                     (void*)p->loss_terms, (void*)p->loss64, (void*)p->d_root_index,
-                    (void*)p->d_sched_rows, (void*)p->d_row_kind})
+                    (void*)p->d_sched_rows, (void*)p->d_row_kind, (void*)p->d_pre, (void*)p->d_pcol,
+                    (void*)p->d_c1pos, (void*)p->d_c2pos, (void*)p->d_ppos, (void*)p->d_pflag, (void*)p->d_endpos,
+                    (void*)p->d_tin, (void*)p->d_euler, (void*)p->c_Ebar, (void*)p->c_E, (void*)p->c_mt,
+                    (void*)p->c_col})
     p->owned.push_back(ptr);
   if (rc) {
     kb_plan_destroy(p);
@@ -383,6 +479,11 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
   E.c_pS = p->c_pS;
   E.c_pD = p->c_pD;
   E.c_colw = p->c_colw;
+  E.c_Ebar = p->c_Ebar;
+  E.c_E = p->c_E;
+  E.c_mt = p->c_mt;
+  E.c_col = p->c_col;
+  E.pre = p->d_pre;
   E.lin_a = p->lin_a;
   E.lin_emc = p->lin_emc;
   E.lin_k1 = p->lin_k1;
@@ -400,12 +501,17 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
   F.lin_emc = p->lin_emc;
   F.lin_k1 = p->lin_k1;
   F.lin_k2 = p->lin_k2;
+  F.pre = p->predev();
+  {
+    const char* w = getenv("KB_FWD_WIDE");
+    F.wide = (w && w[0] == '1') ? 1 : 0;
+  }
   F.colw = p->c_colw;
-  F.col = io->col_log_probs;
-  F.mt = io->max_coupling;
+  F.col = p->c_col;
+  F.mt = p->c_mt;
   F.DL = p->c_DL;
-  F.Ebar = io->Ebar;
-  F.E = io->E;
+  F.Ebar = p->c_Ebar;
+  F.E = p->c_E;
   F.SL1 = p->c_SL1;
   F.SL2 = p->c_SL2;
   F.leaf_logp = p->c_pS;

@@ -216,17 +216,22 @@ __global__ __launch_bounds__(ENT) void estep_fixed_point_kernel(EStepParams P) {
         P.log_pD[0] = (float)pD[k];
         P.log_pL[0] = (float)pL[k];
       }
-      // forward / backward constants
-      P.c_DL[s] = (float)(1.0 + pD[k] + E);
-      P.c_SL1[s] = (float)(pS[k] + Es2);
-      P.c_SL2[s] = (float)(pS[k] + Es1);
-      P.c_pS[s] = (float)pS[k];
-      P.c_pD[s] = (float)pD[k];
-      P.c_colw[s] = (float)w[k];
-      P.lin_a[s] = (float)(exp2(1.0 + pD[k] + E) + exp2(Ebar));
-      P.lin_emc[s] = (float)exp2(E + mt[k]);
-      P.lin_k1[s] = (float)exp2(pS[k] + Es2);
-      P.lin_k2[s] = (float)exp2(pS[k] + Es1);
+      // row-kernel constants at preorder positions
+      const int i = P.pre[s];
+      P.c_DL[i] = (float)(1.0 + pD[k] + E);
+      P.c_SL1[i] = (float)(pS[k] + Es2);
+      P.c_SL2[i] = (float)(pS[k] + Es1);
+      P.c_pS[i] = (float)pS[k];
+      P.c_pD[i] = (float)pD[k];
+      P.c_colw[i] = (float)w[k];
+      P.c_Ebar[i] = (float)Ebar;
+      P.c_E[i] = (float)E;
+      P.c_mt[i] = (float)mt[k];
+      P.c_col[i] = (float)cl[k];
+      P.lin_a[i] = (float)(exp2(1.0 + pD[k] + E) + exp2(Ebar));
+      P.lin_emc[i] = (float)exp2(E + mt[k]);
+      P.lin_k1[i] = (float)exp2(pS[k] + Es2);
+      P.lin_k2[i] = (float)exp2(pS[k] + Es1);
     }
   }
 }

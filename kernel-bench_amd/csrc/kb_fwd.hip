@@ -1,4 +1,4 @@
-// Fused forward wave kernel: one workgroup per clade row does the split
+// Fused forward row kernel: one workgroup per clade row does the split
 // reduction (dts) or the leaf initialisation, all pi_iters-1 self-loop sweeps,
 // and the final Pibar / row max, with the row resident on chip throughout.
 //
@@ -12,96 +12,117 @@
 //    (forward.py:80-115);
 //  * final Pibar and row max from the last Pi (wave_step.py:205-220).
 //
-// The sweeps run in linear space: x = 2^(Pi - M) with a per-row exponent M that
-// is renormalised by an exact power of two after every sweep, so a sweep is
+// The sweeps run in linear space: x = 2^(Pi - M) with a per-row exponent M
+// renormalised by an exact power of two after every sweep (the row sum is
+// brought into [1/2, 1)), so a sweep is
 //   y = a x + emc NA(x) + k1 x[c1] + k2 x[c2] + (leaf | dts) 2^-M
-// with per-column constants a = 2^DL + 2^Ebar, emc = 2^(E+mt), k1 = 2^SL1,
-// k2 = 2^SL2 prepared once per solve.
+// with per-position constants a = 2^DL + 2^Ebar, emc = 2^(E+mt), k1 = 2^SL1,
+// k2 = 2^SL2 prepared once per solve.  NA(x)[s] = rowsum - pathsum(s) as in
+// the reference; the path sums come from an Euler-tour prefix scan.
+// Threads own contiguous preorder positions (see kb_rowops.hpp): three
+// barriers per sweep.
 #include "kb_device.hpp"
 #include "kb_kernels.hpp"
+#include "kb_rowops.hpp"
 
 namespace kb {
 
-template <int NT, int CPT>
-__global__ __launch_bounds__(NT) void fwd_wave_kernel(FwdParams P, int first) {
+template <int NT, int CPT, bool WEIGHTED>
+__global__ __launch_bounds__(NT) void fwd_row_kernel(FwdParams P, int first) {
   constexpr int MAXS = NT * CPT;
-  __shared__ float X[MAXS];
-  __shared__ float B0[MAXS];
-  __shared__ float B1[MAXS];
-  __shared__ float red[NT / 64];
+  constexpr int NW = NT / 64;
+  __shared__ float Xs[2][MAXS + 64];   // unnormalised y of the sweep (double buffer); [MAXS] == 0
+  __shared__ float Sc[2 * MAXS];       // Euler scan / staging
+  __shared__ float wtA[NW], wtB[NW];
 
+  const PreDev& T = P.pre;
   const int S = P.S;
   const int tid = threadIdx.x;
   const int row = P.sched_rows[first + blockIdx.x];
-  const int leaf_wave = P.row_kind[row];
+  const int leaf_row = P.row_kind[row];
   const int item = P.item[row];
-  const size_t cb = (size_t)item * P.const_stride;
+  const size_t cb = (size_t)item * P.const_stride;   // constants are [G, S] in preorder
 
+  OwnTables<NT, CPT> O;
+  O.load(T);
+  if (tid < 64) {
+    Xs[0][MAXS + tid] = 0.0f;
+    Xs[1][MAXS + tid] = 0.0f;
+  }
+  const int(&colv)[CPT] = O.col;
+  const int(&c1p)[CPT] = O.c1p;
+  const int(&c2p)[CPT] = O.c2p;
+
+  // ---- initial row (log2), own positions
   float v[CPT];
-  int leaf = -1;
+  int lpos = -1;
   float leaf_obs = 0.0f;
-  if (leaf_wave) {
-    leaf = P.leaf_state[row];
-    const int ls = P.tr.sub_start[leaf], le = P.tr.sub_end[leaf];
-    leaf_obs = P.leaf_logp[cb + leaf];
-    const float leaf_col = P.use_col ? P.col[leaf] : 0.0f;
+  if (leaf_row) {
+    const int leaf = P.leaf_state[row];
+    lpos = T.pre[leaf];
+    const int lend = T.endpos[lpos];
+    leaf_obs = P.leaf_logp[cb + lpos];
+    const float leaf_col = WEIGHTED ? P.col[lpos] : 0.0f;
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const int s = tid + k * NT;
+      const int i = own_pos<NT, CPT>(k);
       v[k] = KB_NEG_INF;
-      if (s < S) {
-        const bool hit = s == leaf;
-        const int st = P.tr.sub_start[s];
-        const bool desc = st >= ls && st < le;
+      if (i < S) {
+        const bool hit = i == lpos;
+        const bool desc = i >= lpos && i < lend;
+        const size_t ci = cb + i;
         const float pi_w = hit ? leaf_obs : KB_NEG_INF;
-        const float pibar_w = desc ? KB_NEG_INF : P.mt[cb + s] + leaf_col + leaf_obs;
-        const float pi_s1 = P.tr.c1[s] == leaf ? leaf_obs : KB_NEG_INF;
-        const float pi_s2 = P.tr.c2[s] == leaf ? leaf_obs : KB_NEG_INF;
-        const float t0 = P.DL[cb + s] + pi_w;
-        const float t1 = pi_w + P.Ebar[cb + s];
-        const float t2 = pibar_w + P.E[cb + s];
-        const float t3 = P.SL1[cb + s] + pi_s1;
-        const float t4 = P.SL2[cb + s] + pi_s2;
-        const float t5 = hit ? P.leaf_logp[cb + s] : KB_NEG_INF;
-        float m = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, t5));
-        float ms = fsafe(m);
-        float sum = exp2f(t0 - ms) + exp2f(t1 - ms) + exp2f(t2 - ms) + exp2f(t3 - ms) + exp2f(t4 - ms) +
-                    exp2f(t5 - ms);
+        const float pibar_w = desc ? KB_NEG_INF : P.mt[ci] + leaf_col + leaf_obs;
+        const float pi_s1 = c1p[k] == lpos ? leaf_obs : KB_NEG_INF;
+        const float pi_s2 = c2p[k] == lpos ? leaf_obs : KB_NEG_INF;  // padding ZERO never equals lpos
+        const float t0 = P.DL[ci] + pi_w;
+        const float t1 = pi_w + P.Ebar[ci];
+        const float t2 = pibar_w + P.E[ci];
+        const float t3 = P.SL1[ci] + pi_s1;
+        const float t4 = P.SL2[ci] + pi_s2;
+        const float t5 = hit ? P.leaf_logp[ci] : KB_NEG_INF;
+        const float m = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, t5));
+        const float ms = fsafe(m);
+        const float sum = exp2f(t0 - ms) + exp2f(t1 - ms) + exp2f(t2 - ms) + exp2f(t3 - ms) + exp2f(t4 - ms) +
+                          exp2f(t5 - ms);
         v[k] = log2f(sum) + m;
       }
     }
   } else {
     float m[CPT], acc[CPT];
+    int a1[CPT], a2[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       m[k] = KB_NEG_INF;
       acc[k] = 0.0f;
+      a1[k] = c1p[k] < MAXS ? T.col[c1p[k]] : -1;
+      a2[k] = c2p[k] < MAXS ? T.col[c2p[k]] : -1;
     }
     const int b = P.split_ptr[row], e = P.split_ptr[row + 1];
-    for (int i = b; i < e; ++i) {
-      const size_t l = (size_t)P.split_l[i] * S, r = (size_t)P.split_r[i] * S;
-      const float lsp = P.split_lsp[i];
+    for (int si = b; si < e; ++si) {
+      const size_t l = (size_t)P.split_l[si] * S, r = (size_t)P.split_r[si] * S;
+      const float lsp = P.split_lsp[si];
       const float* Pl = P.pi + l;
       const float* Pr = P.pi + r;
       const float* Bl = P.pibar + l;
       const float* Br = P.pibar + r;
 #pragma unroll
       for (int k = 0; k < CPT; ++k) {
-        const int s = tid + k * NT;
-        if (s < S) {
-          const int a1 = P.tr.c1[s], a2 = P.tr.c2[s];
+        const int i = own_pos<NT, CPT>(k);
+        if (i < S) {
+          const int s = colv[k];
           const float pl = Pl[s], pr = Pr[s];
-          const float d = P.pD.at(item, s), sp = P.pS.at(item, s);
+          const float d = P.pD.at(item, i), sp = P.pS.at(item, i);
           const float t0 = lsp + d + pl + pr;
           const float t1 = lsp + pl + Br[s];
           const float t2 = lsp + pr + Bl[s];
-          const float l1 = a1 >= 0 ? Pl[a1] : KB_NEG_INF, r1 = a1 >= 0 ? Pr[a1] : KB_NEG_INF;
-          const float l2 = a2 >= 0 ? Pl[a2] : KB_NEG_INF, r2 = a2 >= 0 ? Pr[a2] : KB_NEG_INF;
+          const float l1 = a1[k] >= 0 ? Pl[a1[k]] : KB_NEG_INF, r1 = a1[k] >= 0 ? Pr[a1[k]] : KB_NEG_INF;
+          const float l2 = a2[k] >= 0 ? Pl[a2[k]] : KB_NEG_INF, r2 = a2[k] >= 0 ? Pr[a2[k]] : KB_NEG_INF;
           const float t3 = lsp + sp + l1 + r2;
           const float t4 = lsp + sp + r1 + l2;
-          float m5 = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), t4);
-          float ms = fsafe(m5);
-          float s5 = exp2f(t0 - ms) + exp2f(t1 - ms) + exp2f(t2 - ms) + exp2f(t3 - ms) + exp2f(t4 - ms);
+          const float m5 = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), t4);
+          const float ms = fsafe(m5);
+          const float s5 = exp2f(t0 - ms) + exp2f(t1 - ms) + exp2f(t2 - ms) + exp2f(t3 - ms) + exp2f(t4 - ms);
           lse_merge(m[k], acc[k], m5, s5);
         }
       }
@@ -110,124 +131,105 @@ __global__ __launch_bounds__(NT) void fwd_wave_kernel(FwdParams P, int first) {
     for (int k = 0; k < CPT; ++k) v[k] = log2f(acc[k]) + m[k];
   }
 
-  // ---- to linear space with an exact power-of-two row scale
+  // ---- linear space relative to the row maximum
   float lm = KB_NEG_INF;
 #pragma unroll
-  for (int k = 0; k < CPT; ++k)
-    if (tid + k * NT < S) lm = fmaxf(lm, v[k]);
-  const float M0 = block_max<NT>(lm, red);
-  const float Ms = fsafe(M0);
-  float x[CPT], dl[CPT], ca[CPT], ce[CPT], ck1[CPT], ck2[CPT], cw[CPT];
-  int c1[CPT], c2[CPT];
+  for (int k = 0; k < CPT; ++k) lm = fmaxf(lm, v[k]);
+  const float Ms = fsafe(block_max1<NT>(lm, wtB));  // wtA is written next without a barrier
+  float y[CPT], dl[CPT], ca[CPT], ce[CPT], ck1[CPT], ck2[CPT], cw[CPT];
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
-    const int s = tid + k * NT;
-    const bool ok = s < S;
-    x[k] = ok ? exp2f(v[k] - Ms) : 0.0f;
-    dl[k] = leaf_wave ? 0.0f : x[k];
-    ca[k] = ok ? P.lin_a[cb + s] : 0.0f;
-    ce[k] = ok ? P.lin_emc[cb + s] : 0.0f;
-    ck1[k] = ok ? P.lin_k1[cb + s] : 0.0f;
-    ck2[k] = ok ? P.lin_k2[cb + s] : 0.0f;
-    cw[k] = ok ? (P.use_col ? P.colw[s] : 1.0f) : 0.0f;
-    c1[k] = ok ? P.tr.c1[s] : -1;
-    c2[k] = ok ? P.tr.c2[s] : -1;
+    const int i = own_pos<NT, CPT>(k);
+    const bool ok = i < S;
+    y[k] = ok ? exp2f(v[k] - Ms) : 0.0f;
+    dl[k] = leaf_row ? 0.0f : y[k];
+    ca[k] = ok ? P.lin_a[cb + i] : 0.0f;
+    ce[k] = ok ? P.lin_emc[cb + i] : 0.0f;
+    ck1[k] = ok ? P.lin_k1[cb + i] : 0.0f;
+    ck2[k] = ok ? P.lin_k2[cb + i] : 0.0f;
+    cw[k] = WEIGHTED ? (ok ? P.colw[i] : 0.0f) : 1.0f;
   }
-  const float leaf_lin = leaf_wave ? exp2f(P.leaf_logp[cb + leaf] - Ms) : 0.0f;
+  const float leaf_lin = leaf_row ? exp2f(leaf_obs - Ms) : 0.0f;  // lpos = -1 for split rows
   int kexp = 0;
+  float x[CPT], ps[CPT], rowsum = 0.0f, f = 1.0f;
 
-  for (int sweep = 0; sweep < P.n_sweeps; ++sweep) {
+  for (int sweep = 0;; ++sweep) {
+    float* X = Xs[sweep & 1];
+    // phase A: publish y (padding slot stays 0), reduce the (weighted) row sum,
+    // renormalise by an exact power of two
     float ls = 0.0f;
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const int s = tid + k * NT;
-      if (s < S) {
-        X[s] = x[k];
-        B0[s] = cw[k] * x[k];
-        ls += cw[k] * x[k];
-      }
+      X[own_pos<NT, CPT>(k)] = y[k];
+      ls += cw[k] * y[k];
     }
-    const float rowsum = block_sum<NT>(ls, red);
-    const float* ps = path_sum_lds<NT, CPT>(P.tr, B0, B1);
-    const float scale = ldexpf(1.0f, -kexp);
-    float y[CPT];
-    float ymax = 0.0f;
+    const float tsum = block_sum1<NT>(ls, wtA);
+    const int e = tsum > 0.0f ? __builtin_amdgcn_frexp_expf(tsum) : 0;
+    f = __builtin_amdgcn_ldexpf(1.0f, -e);
+    kexp += e;
+    rowsum = tsum * f;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) x[k] = y[k] * f;
+    // ancestors-or-self path sums (of the unnormalised values)
+    path_sum_euler<NT, CPT>(O, X, Sc, wtB, ps, WEIGHTED ? P.colw : nullptr);
+    if (sweep == P.n_sweeps) break;
+    const float scale = __builtin_amdgcn_ldexpf(1.0f, -kexp);
+    const float lterm = leaf_lin * scale;
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const int s = tid + k * NT;
-      float yy = 0.0f;
-      if (s < S) {
-        float na = rowsum - ps[s];
-        na = na > 0.0f ? na : 0.0f;
-        yy = ca[k] * x[k] + ce[k] * na;
-        if (c1[k] >= 0) yy += ck1[k] * X[c1[k]];
-        if (c2[k] >= 0) yy += ck2[k] * X[c2[k]];
-        if (leaf_wave) {
-          if (s == leaf) yy += leaf_lin * scale;
-        } else {
-          yy += dl[k] * scale;
-        }
-      }
+      const float na = fmaxf(rowsum - ps[k] * f, 0.0f);
+      float yy = ca[k] * x[k] + ce[k] * na;
+      yy += ck1[k] * (X[c1p[k]] * f);
+      yy += ck2[k] * (X[c2p[k]] * f);
+      yy += dl[k] * scale;
+      yy += own_pos<NT, CPT>(k) == lpos ? lterm : 0.0f;
       y[k] = yy;
-      ymax = fmaxf(ymax, yy);
-    }
-    const float gmax = block_max<NT>(ymax, red);  // barrier: LDS reads above are complete
-    if (gmax > 0.0f) {
-      int e;
-      frexpf(gmax, &e);
-#pragma unroll
-      for (int k = 0; k < CPT; ++k) x[k] = ldexpf(y[k], -e);
-      kexp += e;
-    } else {
-#pragma unroll
-      for (int k = 0; k < CPT; ++k) x[k] = y[k];
     }
   }
 
   // ---- outputs: Pi, Pibar from the final Pi, and the (weighted) row max
   const float M = Ms + (float)kexp;
-  const size_t rb = (size_t)row * S;
-  float ls = 0.0f, lmax = KB_NEG_INF;
-  float piv[CPT];
+  float piv[CPT], pbv[CPT];
+  float lmax = KB_NEG_INF;
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
-    const int s = tid + k * NT;
-    if (s < S) {
+    const int i = own_pos<NT, CPT>(k);
+    piv[k] = KB_NEG_INF;
+    pbv[k] = KB_NEG_INF;
+    if (i < S) {
       piv[k] = x[k] > 0.0f ? log2f(x[k]) + M : KB_NEG_INF;
-      P.pi[rb + s] = piv[k];
-      lmax = fmaxf(lmax, P.use_col ? P.col[s] + piv[k] : piv[k]);
-      B0[s] = cw[k] * x[k];
-      ls += cw[k] * x[k];
+      const float na = rowsum - ps[k] * f;
+      pbv[k] = na > 0.0f ? log2f(na) + M + P.mt[cb + i] : KB_NEG_INF;
+      lmax = fmaxf(lmax, WEIGHTED ? P.col[i] + piv[k] : piv[k]);
     }
   }
-  const float rowsum = block_sum<NT>(ls, red);
-  const float* ps = path_sum_lds<NT, CPT>(P.tr, B0, B1);
-#pragma unroll
-  for (int k = 0; k < CPT; ++k) {
-    const int s = tid + k * NT;
-    if (s < S) {
-      float na = rowsum - ps[s];
-      P.pibar[rb + s] = na > 0.0f ? log2f(na) + M + P.mt[cb + s] : KB_NEG_INF;
-    }
-  }
-  const float rmax = block_max<NT>(lmax, red);
+  // Sc (last read inside path_sum_euler) is reused as staging after this barrier.
+  const float rmax = block_max1<NT>(lmax, wtA);
+  const size_t rb = (size_t)row * S;
+  store_row_pre<NT, CPT>(T, piv, Sc, P.pi + rb);
+  store_row_pre<NT, CPT>(T, pbv, Sc + MAXS, P.pibar + rb);
   if (tid == 0) P.rowmax[row] = rmax;
 }
 
-#define KB_FWD_CASE(NT_, CPT_)                                                                   \
-  if (S <= NT_ * CPT_) {                                                                         \
-    hipLaunchKernelGGL((fwd_wave_kernel<NT_, CPT_>), dim3(W), dim3(NT_), 0, st, P, first);        \
-    return;                                                                                      \
+#define KB_FWD_CASE(NT_, CPT_)                                                                            \
+  if (S <= NT_ * CPT_) {                                                                                  \
+    if (P.use_col)                                                                                        \
+      hipLaunchKernelGGL((fwd_row_kernel<NT_, CPT_, true>), dim3(W), dim3(NT_), 0, st, P, first);         \
+    else                                                                                                  \
+      hipLaunchKernelGGL((fwd_row_kernel<NT_, CPT_, false>), dim3(W), dim3(NT_), 0, st, P, first);        \
+    return;                                                                                               \
   }
 
 void launch_fwd_wave(const FwdParams& P, int first, int W, hipStream_t st) {
   if (W <= 0) return;
   const int S = P.S;
-  KB_FWD_CASE(64, 1)
-  KB_FWD_CASE(128, 1)
-  KB_FWD_CASE(256, 1)
+  if (P.wide > 0) {  // fewer, wider threads per row (tuning knob)
+    KB_FWD_CASE(256, 8)
+  }
+  KB_FWD_CASE(64, 2)
+  KB_FWD_CASE(128, 2)
   KB_FWD_CASE(256, 2)
-  KB_FWD_CASE(512, 2)
+  KB_FWD_CASE(256, 4)
   KB_FWD_CASE(512, 4)
   KB_FWD_CASE(1024, 4)
   KB_FWD_CASE(1024, 8)

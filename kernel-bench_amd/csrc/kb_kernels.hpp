@@ -3,6 +3,7 @@
 #pragma once
 
 #include "kb_device.hpp"
+#include "kb_rowops.hpp"
 
 namespace kb {
 
@@ -15,6 +16,7 @@ struct EStepParams {
   int n_tlevels;              // depth levels, root first
   const int* tlevel_ptr;      // [n_tlevels + 1]
   const int* tlevel_node;     // [S]
+  const int* pre;             // [S] column -> preorder position (layout of the c_* / lin_* constants)
   const float* theta;         // [S,3] (statewise) or [3]
   int statewise;
   const float* col_weights;   // [S]
@@ -29,8 +31,9 @@ struct EStepParams {
   float* mt; float* col_log_probs;               // [S]
   double* E64;                                    // optional float64 E
   int* n_iter_out;
-  // per-column constants of the wave kernels (float32, [S])
+  // constants of the row kernels (float32, [S], preorder positions)
   float* c_DL; float* c_SL1; float* c_SL2; float* c_pS; float* c_pD; float* c_colw;
+  float* c_Ebar; float* c_E; float* c_mt; float* c_col;
   float* lin_a; float* lin_emc; float* lin_k1; float* lin_k2;
 };
 
@@ -43,11 +46,13 @@ void launch_loss(const float* pi, const int* root_rows, const float* E, int S, i
 // ----------------------------------------------------------------------------
 struct FwdParams {
   TreeDev tr;
+  PreDev pre;
   int S;
+  int wide;                   // >0: prefer 256 threads x 8 positions per row
   int n_sweeps;               // pi_iters - 1
   int use_col;
   int const_stride;           // 0: one constant row; S: item-indexed rows
-  // per-column constants, row = item * const_stride
+  // per-position constants (preorder), row = item * const_stride
   const float* lin_a; const float* lin_emc; const float* lin_k1; const float* lin_k2;
   const float* colw;          // [S] 2^col_log_probs (weighted) -- may be null when !use_col
   const float* col;           // [S]

@@ -1,0 +1,271 @@
+// Row operations in preorder, wavefront-segment ownership.
+//
+// Inside a row kernel with NT threads (NW = NT/64 wavefronts), wavefront w owns
+// the preorder segment [w*SEG, (w+1)*SEG), SEG = 64*CPT, and lane l of it owns
+// positions w*SEG + k*64 + l for k < CPT ("slot k").  For a fixed slot the 64
+// lanes touch 64 consecutive positions, so LDS reads/writes of own positions
+// are bank-conflict free, and the position order is (wave, slot, lane).
+//
+// In preorder every subtree is a contiguous range [i, end(i)), so
+//   * the sum over the complement of a subtree (the transpose of the
+//     "all non-ancestors" sum) is  scan[i-1] + (total - scan[end(i)-1])  for an
+//     inclusive prefix scan over positions;
+//   * the ancestors-or-self path sum of node i is the prefix, up to i's entry,
+//     of its Euler tour (+x on entry, -x on exit).
+// Both are one block scan: DPP row shifts / row broadcasts inside a wavefront,
+// a running carry across slots, and one LDS exchange of wavefront totals.
+#pragma once
+
+#include "kb_device.hpp"
+
+namespace kb {
+
+// ---- wavefront primitives (DPP) ---------------------------------------------
+
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ float dpp_shift0(float x) {
+  // lanes without a source read 0 (the identity of +)
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, BANK_MASK, false));
+}
+
+// Inclusive scan (+) across the 64 lanes of a wavefront.
+__device__ __forceinline__ float wave_scan_incl(float x) {
+  x += dpp_shift0<0x111>(x);       // row_shr:1
+  x += dpp_shift0<0x112>(x);       // row_shr:2
+  x += dpp_shift0<0x114>(x);       // row_shr:4
+  x += dpp_shift0<0x118>(x);       // row_shr:8
+  x += dpp_shift0<0x142, 0xa>(x);  // row_bcast:15 -> rows 1, 3
+  x += dpp_shift0<0x143, 0xc>(x);  // row_bcast:31 -> rows 2, 3
+  return x;
+}
+
+__device__ __forceinline__ float lane_value(float x, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
+__device__ __forceinline__ float wave_reduce_sum(float x) { return lane_value(wave_scan_incl(x), 63); }
+
+__device__ __forceinline__ float wave_reduce_max(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+  return x;
+}
+
+// ---- block reductions / scans (one barrier each) -----------------------------
+// `wtot` is LDS scratch of NW floats (2*NW for the paired scan).  It is read
+// by every thread after the barrier, so the next writer must be separated from
+// these reads by another barrier: callers alternate scratch arrays.
+
+template <int NT>
+__device__ __forceinline__ float block_sum1(float x, float* wtot) {
+  constexpr int NW = NT / 64;
+  const float ws = wave_reduce_sum(x);
+  if ((threadIdx.x & 63) == 0) wtot[threadIdx.x >> 6] = ws;
+  __syncthreads();
+  float t = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) t += wtot[i];
+  return t;
+}
+
+template <int NT>
+__device__ __forceinline__ float block_max1(float x, float* wtot) {
+  constexpr int NW = NT / 64;
+  const float wm = wave_reduce_max(x);
+  if ((threadIdx.x & 63) == 0) wtot[threadIdx.x >> 6] = wm;
+  __syncthreads();
+  float t = KB_NEG_INF;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) t = fmaxf(t, wtot[i]);
+  return t;
+}
+
+// In-place inclusive scan over positions of v[k] (slot k of this lane).
+// Returns the block total.
+template <int NT, int N>
+__device__ __forceinline__ float block_scan_incl(float (&v)[N], float* wtot) {
+  constexpr int NW = NT / 64;
+  float carry = 0.0f;
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    const float s = wave_scan_incl(v[k]);
+    v[k] = s + carry;
+    carry += lane_value(s, 63);
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) wtot[w] = carry;
+  __syncthreads();
+  float off = 0.0f, total = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const float t = wtot[i];
+    if (i < w) off += t;
+    total += t;
+  }
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] += off;
+  return total;
+}
+
+// Two scans sharing one barrier (wtot holds 2*NW floats).
+template <int NT, int N>
+__device__ __forceinline__ void block_scan_incl2(float (&a)[N], float (&b)[N], float* wtot, float& ta, float& tb) {
+  constexpr int NW = NT / 64;
+  float ca = 0.0f, cb = 0.0f;
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    const float sa = wave_scan_incl(a[k]);
+    const float sb = wave_scan_incl(b[k]);
+    a[k] = sa + ca;
+    b[k] = sb + cb;
+    ca += lane_value(sa, 63);
+    cb += lane_value(sb, 63);
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    wtot[w] = ca;
+    wtot[NW + w] = cb;
+  }
+  __syncthreads();
+  float oa = 0.0f, ob = 0.0f;
+  ta = 0.0f;
+  tb = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const float x = wtot[i], y = wtot[NW + i];
+    if (i < w) {
+      oa += x;
+      ob += y;
+    }
+    ta += x;
+    tb += y;
+  }
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    a[k] += oa;
+    b[k] += ob;
+  }
+}
+
+// ---- preorder tables ---------------------------------------------------------
+
+struct PreDev {
+  int S;
+  const int* pre;     // [S]   column -> preorder position
+  const int* col;     // [S]   position -> column
+  const int* c1pos;   // [S]   position of node_child1 (-1: leaf)
+  const int* c2pos;   // [S]   position of node_child2 (-1: leaf)
+  const int* ppos;    // [S]   position of the parent (-1: root)
+  const int* pflag;   // [S]   1 if this position is node_child1 of its parent
+  const int* endpos;  // [S]   exclusive end of the subtree
+  const int* tin;     // [S]   Euler entry event of the position
+  const int* euler;   // [2S]  event -> (position << 1) | is_exit
+};
+
+// Position of slot k of this thread.
+template <int NT, int CPT>
+__device__ __forceinline__ int own_pos(int k) {
+  return (threadIdx.x >> 6) * (64 * CPT) + k * 64 + (threadIdx.x & 63);
+}
+
+// Euler event of slot j (< 2*CPT) of this thread.
+template <int NT, int CPT>
+__device__ __forceinline__ int own_event(int j) {
+  return (threadIdx.x >> 6) * (128 * CPT) + j * 64 + (threadIdx.x & 63);
+}
+
+// Per-thread copy of the preorder tables of its own positions and events.
+// Invalid entries point at the padding slot ZERO (= NT*CPT) of the LDS row
+// buffers, which always holds 0, so the sweep loops need no bounds branches.
+// Euler events are owned contiguously: thread t holds events
+// [t*2*CPT, (t+1)*2*CPT), so their scan is a sequential local scan plus one
+// wavefront scan.
+template <int NT, int CPT>
+struct OwnTables {
+  static constexpr int ZERO = NT * CPT;
+  int col[CPT], c1p[CPT], c2p[CPT], tin[CPT];
+  int ev[2 * CPT];  // (position << 1) | is_exit; padding: ZERO << 1
+  __device__ __forceinline__ void load(const PreDev& T) {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int i = own_pos<NT, CPT>(k);
+      const bool ok = i < T.S;
+      col[k] = ok ? T.col[i] : -1;
+      const int a = ok ? T.c1pos[i] : -1, b = ok ? T.c2pos[i] : -1;
+      c1p[k] = a >= 0 ? a : ZERO;
+      c2p[k] = b >= 0 ? b : ZERO;
+      tin[k] = ok ? T.tin[i] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < 2 * CPT; ++j) {
+      const int q = threadIdx.x * (2 * CPT) + j;
+      ev[j] = q < 2 * T.S ? T.euler[q] : (ZERO << 1);
+    }
+  }
+};
+
+// Coalesced load of a global row (column order) into LDS at preorder
+// positions, then into v[] (own positions).  One barrier; the caller separates
+// reuse of `lds` with a barrier.  Positions >= S read `fill`.
+template <int NT, int CPT>
+__device__ __forceinline__ void load_row_pre(const PreDev& T, const float* grow, float* lds, float (&v)[CPT],
+                                             float fill) {
+  for (int s = threadIdx.x; s < T.S; s += NT) lds[T.pre[s]] = grow[s];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int i = own_pos<NT, CPT>(k);
+    v[k] = i < T.S ? lds[i] : fill;
+  }
+}
+
+// Own positions -> LDS -> coalesced global row in column order.  One barrier.
+template <int NT, int CPT>
+__device__ __forceinline__ void store_row_pre(const PreDev& T, const float (&v)[CPT], float* lds, float* grow) {
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int i = own_pos<NT, CPT>(k);
+    if (i < T.S) lds[i] = v[k];
+  }
+  __syncthreads();
+  for (int s = threadIdx.x; s < T.S; s += NT) grow[s] = lds[T.pre[s]];
+}
+
+// Ancestors-or-self path sums of the LDS vector x[] (preorder positions,
+// x[ZERO] == 0), optionally weighted per position by wgt[] (global, padded
+// with a 0 at ZERO is not required: the padding slot's x is 0): Euler-tour
+// prefix scan.  Returns ps[] for own positions.  Reads x[] after the caller's
+// barrier; writes `scan` (2*NT*CPT floats).  Two barriers.
+template <int NT, int CPT>
+__device__ __forceinline__ void path_sum_euler(const OwnTables<NT, CPT>& O, const float* x, float* scan, float* wtot,
+                                               float (&ps)[CPT], const float* wgt = nullptr) {
+  constexpr int E = 2 * CPT;
+  constexpr int NW = NT / 64;
+  float ev[E];
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    const int p = O.ev[j] >> 1;
+    const float xv = wgt ? x[p] * (p < O.ZERO ? wgt[p] : 0.0f) : x[p];
+    ev[j] = (O.ev[j] & 1) ? -xv : xv;
+  }
+#pragma unroll
+  for (int j = 1; j < E; ++j) ev[j] += ev[j - 1];
+  const float tsum = ev[E - 1];
+  const float ws = wave_scan_incl(tsum);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 63) wtot[w] = ws;
+  __syncthreads();
+  float off = ws - tsum;
+#pragma unroll
+  for (int i = 0; i < NW; ++i)
+    if (i < w) off += wtot[i];
+  float4* dst = reinterpret_cast<float4*>(scan + threadIdx.x * E);
+#pragma unroll
+  for (int j = 0; j < E; j += 4)
+    dst[j / 4] = make_float4(ev[j] + off, ev[j + 1] + off, ev[j + 2] + off, ev[j + 3] + off);
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) ps[k] = scan[O.tin[k]];
+}
+
+}  // namespace kb

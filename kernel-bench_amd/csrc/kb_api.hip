@@ -90,6 +90,7 @@ struct kb_plan {
   float* b_contrib = nullptr; double* b_partial = nullptr; double* b_acc = nullptr; double* b_work = nullptr;
   int* b_status = nullptr;
   float* b_DL = nullptr; float* b_SL1 = nullptr; float* b_SL2 = nullptr; float* b_pS = nullptr; float* b_pD = nullptr;
+  float* b_Ebar = nullptr; float* b_E = nullptr; float* b_mt = nullptr; float* b_col = nullptr; double* b_acc_pre = nullptr;
   // optional per-launch timing of the wave kernels (HIP events on the launch stream)
   int prof = 0;
   std::vector<hipEvent_t> ev_fwd, ev_bwd;
@@ -557,7 +558,13 @@ static int ensure_backward_work(kb_plan* p) {
   rc |= alloc(&p->b_SL2, S);
   rc |= alloc(&p->b_pS, S);
   rc |= alloc(&p->b_pD, S);
-  for (void* ptr : {(void*)p->b_staging, (void*)p->b_split_on, (void*)p->b_mask, (void*)p->b_contrib,
+  rc |= alloc(&p->b_Ebar, S);
+  rc |= alloc(&p->b_E, S);
+  rc |= alloc(&p->b_mt, S);
+  rc |= alloc(&p->b_col, S);
+  rc |= alloc(&p->b_acc_pre, (size_t)8 * S);
+  for (void* ptr : {(void*)p->b_Ebar, (void*)p->b_E, (void*)p->b_mt, (void*)p->b_col, (void*)p->b_acc_pre,
+                    (void*)p->b_staging, (void*)p->b_split_on, (void*)p->b_mask, (void*)p->b_contrib,
                     (void*)p->b_partial, (void*)p->b_acc, (void*)p->b_work, (void*)p->b_status, (void*)p->b_DL,
                     (void*)p->b_SL1, (void*)p->b_SL2, (void*)p->b_pS, (void*)p->b_pD})
     p->owned.push_back(ptr);
@@ -584,6 +591,14 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   K.E = io->E;
   K.E_s1 = io->E_s1;
   K.E_s2 = io->E_s2;
+  K.pre = p->d_pre;
+  K.Ebar = io->Ebar;
+  K.mt = io->max_coupling;
+  K.col = io->col_log_probs;
+  K.Ebar_pre = p->b_Ebar;
+  K.E_pre = p->b_E;
+  K.mt_pre = p->b_mt;
+  K.col_pre = p->b_col;
   K.DL = p->b_DL;
   K.SL1 = p->b_SL1;
   K.SL2 = p->b_SL2;
@@ -599,13 +614,14 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   B.use_pruning = io->use_pruning;
   B.use_col = io->use_col_weights;
   B.const_stride = 0;
+  B.pre = p->predev();
   B.DL = p->b_DL;
-  B.Ebar = io->Ebar;
-  B.E = io->E;
+  B.Ebar = p->b_Ebar;
+  B.E = p->b_E;
   B.SL1 = p->b_SL1;
   B.SL2 = p->b_SL2;
-  B.mt = io->max_coupling;
-  B.col = io->col_log_probs;
+  B.mt = p->b_mt;
+  B.col = p->b_col;
   B.leaf_logp = p->b_pS;
   B.pD = kb::RateDev{p->b_pD, 0, 1};
   B.pS = kb::RateDev{p->b_pS, 0, 1};
@@ -633,7 +649,8 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
     if (p->prof) KB_HIP(hipEventRecord(p->ev_bwd[2 * d + 1], st));
   }
   KB_HIP(hipGetLastError());
-  kb::launch_bwd_reduce(p->b_contrib, B.mask, C, S, p->b_partial, p->b_acc, st);
+  kb::launch_bwd_reduce(p->b_contrib, B.mask, C, S, p->b_partial, p->b_acc_pre, st);
+  kb::launch_bwd_unpermute(p->b_acc_pre, p->d_pre, S, p->b_acc, st);
   KB_HIP(hipGetLastError());
   if (io->acc_out)
     KB_HIP(hipMemcpyAsync(io->acc_out, p->b_acc, (size_t)8 * S * sizeof(double), hipMemcpyDeviceToDevice, st));

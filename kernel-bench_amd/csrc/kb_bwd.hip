@@ -13,78 +13,61 @@
 //     buckets aw_k = v w_L e_k / sum e                              (wave_backward.py:747-966)
 //     split adjoints into the child rows, incl. the Pibar VJP      (wave_backward.py:1529-1945, 2229-2327)
 //
+// One workgroup per clade row, rows scheduled by clade-DAG level in reverse.
+// Threads own preorder positions (kb_rowops.hpp), where every subtree is a
+// contiguous range: A - subtree(u)[i] = P[i-1] + (A - P[end(i)-1]) for the
+// inclusive scan P of u over positions, one block scan per Neumann term.
+//
 // Determinism: the reference scatters child adjoints and gradient sums with
-// float atomics.  Here every split side writes a staging row; a child row
-// gathers its staging rows in increasing split order when its own wave runs,
-// and every per-row gradient bucket is stored and reduced over rows in a
-// fixed order, so results are bitwise reproducible.
+// float atomics.  Here every split side writes a staging row (preorder
+// layout); a child row gathers its staging rows in increasing split order,
+// and every per-row gradient bucket is stored and reduced over rows in a fixed
+// order, so results are bitwise reproducible.
 #include "kb_device.hpp"
 #include "kb_kernels.hpp"
+#include "kb_rowops.hpp"
 
 namespace kb {
 
-// Two subtree sums at once (same level schedule, half the barriers).
-template <int NT>
-__device__ __forceinline__ void subtree_sum2_lds(const TreeDev& tr, float* u, float* w) {
-  for (int lv = 0; lv < tr.n_blevels; ++lv) {
-    const int b = tr.blevel_ptr[lv], e = tr.blevel_ptr[lv + 1];
-    for (int i = b + threadIdx.x; i < e; i += NT) {
-      const int p = tr.blevel_node[i];
-      const int x = tr.c1[p], y = tr.c2[p];
-      u[p] += (x >= 0 ? u[x] : 0.0f) + (y >= 0 ? u[y] : 0.0f);
-      w[p] += (x >= 0 ? w[x] : 0.0f) + (y >= 0 ? w[y] : 0.0f);
-    }
-    __syncthreads();
-  }
-}
-
-template <int NT>
-__device__ __forceinline__ void block_sum2(float& a, float& b, float* red) {
-  constexpr int NW = NT / 64;
-  a = wave_sum(a);
-  b = wave_sum(b);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  if (lane == 0) {
-    red[w] = a;
-    red[NW + w] = b;
-  }
-  __syncthreads();
-  float ra = red[0], rb = red[NW];
-#pragma unroll
-  for (int i = 1; i < NW; ++i) {
-    ra += red[i];
-    rb += red[NW + i];
-  }
-  __syncthreads();
-  a = ra;
-  b = rb;
-}
-
-template <int NT, int CPT>
-__global__ __launch_bounds__(NT) void bwd_wave_kernel(BwdParams P, int first) {
+template <int NT, int CPT, bool WEIGHTED>
+__global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first) {
   constexpr int MAXS = NT * CPT;
-  __shared__ float B0[MAXS];
-  __shared__ float B1[MAXS];
-  __shared__ float B2[MAXS];
-  __shared__ float B3[MAXS];
-  __shared__ float red[2 * (NT / 64)];
+  constexpr int LD = MAXS + 64;  // [MAXS] is the padding slot, kept at 0
+  constexpr int NW = NT / 64;
+  __shared__ float L[4 * LD];
+  __shared__ float wA[2 * NW], wB[2 * NW];
+  float* R0 = L;
+  float* R1 = L + LD;
+  float* R2 = L + 2 * LD;
+  float* R3 = L + 3 * LD;
+  float* Sc = R2;  // one-time Euler scan (2*MAXS floats) overlays R2..R3; their padding is re-zeroed after
 
+  const PreDev& T = P.pre;
   const int S = P.S;
   const int tid = threadIdx.x;
   const int row = P.sched_rows[first + blockIdx.x];
-  const int leaf_wave = P.row_kind[row];
+  const int leaf_row = P.row_kind[row];
   const int item = P.item[row];
   const size_t cb = (size_t)item * P.const_stride;
   const size_t rb = (size_t)row * S;
   const int sb = P.split_ptr[row], se = P.split_ptr[row + 1];
+  constexpr int ZERO = MAXS;
 
-  // ---- 1. adjoint of this row: root seed or fixed-order gather of staging rows
-  float piv[CPT];
-#pragma unroll
-  for (int k = 0; k < CPT; ++k) {
-    const int s = tid + k * NT;
-    piv[k] = s < S ? P.pi[rb + s] : KB_NEG_INF;
+  OwnTables<NT, CPT> O;
+  O.load(T);
+  if (tid < 64) {
+    R0[MAXS + tid] = 0.0f;
+    R1[MAXS + tid] = 0.0f;
+    R2[MAXS + tid] = 0.0f;
+    R3[MAXS + tid] = 0.0f;
   }
+  bool okp[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) okp[k] = own_pos<NT, CPT>(k) < S;
+
+  // ---- 1. Pi* of this row and its adjoint: root seed or fixed-order gather
+  float piv[CPT];
+  load_row_pre<NT, CPT>(T, P.pi + rb, R0, piv, KB_NEG_INF);
   float rhs[CPT];
   const int fam = P.root_index[row];
   if (fam >= 0) {
@@ -92,17 +75,16 @@ __global__ __launch_bounds__(NT) void bwd_wave_kernel(BwdParams P, int first) {
     float lm = KB_NEG_INF;
 #pragma unroll
     for (int k = 0; k < CPT; ++k) lm = fmaxf(lm, piv[k]);
-    const float rmax = block_max<NT>(lm, red);
+    const float rmax = block_max1<NT>(lm, wA);
     const float rms = fsafe(rmax);
     float ls = 0.0f;
 #pragma unroll
-    for (int k = 0; k < CPT; ++k)
-      if (tid + k * NT < S) ls += exp2f(piv[k] - rms);
-    const float tot = block_sum<NT>(ls, red);
+    for (int k = 0; k < CPT; ++k) ls += okp[k] ? exp2f(piv[k] - rms) : 0.0f;
+    const float tot = block_sum1<NT>(ls, wB);
     const float lse = (tot > 0.0f ? log2f(tot) : KB_NEG_INF) + rmax;
+    const float lses = fsafe(lse);
 #pragma unroll
-    for (int k = 0; k < CPT; ++k)
-      rhs[k] = (piv[k] == KB_NEG_INF) ? 0.0f : -exp2f(piv[k] - (lse == KB_NEG_INF ? 0.0f : lse));
+    for (int k = 0; k < CPT; ++k) rhs[k] = (piv[k] == KB_NEG_INF) ? 0.0f : -exp2f(piv[k] - lses);
   } else {
 #pragma unroll
     for (int k = 0; k < CPT; ++k) rhs[k] = 0.0f;
@@ -112,109 +94,119 @@ __global__ __launch_bounds__(NT) void bwd_wave_kernel(BwdParams P, int first) {
       if (!P.split_on[side >> 1]) continue;
       const float* st = P.staging + (size_t)side * S;
 #pragma unroll
-      for (int k = 0; k < CPT; ++k) {
-        const int s = tid + k * NT;
-        if (s < S) rhs[k] += st[s];
-      }
+      for (int k = 0; k < CPT; ++k)
+        if (okp[k]) rhs[k] += st[own_pos<NT, CPT>(k)];
     }
   }
 
-  // ---- 2. active mask (bit-exact rule of the reference)
+  // ---- 2. active mask (the reference's rule, wave_backward.py:150-163)
   float am = 0.0f;
 #pragma unroll
   for (int k = 0; k < CPT; ++k) am = fmaxf(am, fabsf(rhs[k]));
-  const float amax = block_max<NT>(am, red);
+  const float amax = block_max1<NT>(am, fam >= 0 ? wA : wB);
   const bool active = P.use_pruning ? (amax >= P.thr) : (amax > P.thr);
   if (tid == 0) P.mask[row] = active ? 1 : 0;
   if (!active) {
     for (int i = sb + tid; i < se; i += NT) P.split_on[i] = 0;
     return;
   }
+  __syncthreads();  // R0 (Pi*) and the scratch above are reused below
 
-  // ---- 3. split term at Pi* (split rows)
+  // ---- 3. split term at Pi* (split rows), children staged through LDS
   float dts[CPT];
-  if (!leaf_wave) {
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) dts[k] = KB_NEG_INF;
+  if (!leaf_row) {
     float m[CPT], acc[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       m[k] = KB_NEG_INF;
       acc[k] = 0.0f;
     }
-    for (int i = sb; i < se; ++i) {
-      const size_t l = (size_t)P.split_l[i] * S, r = (size_t)P.split_r[i] * S;
-      const float lsp = P.split_lsp[i];
-      const float* Pl = P.pi + l;
-      const float* Pr = P.pi + r;
-      const float* Bl = P.pibar + l;
-      const float* Br = P.pibar + r;
+    for (int si = sb; si < se; ++si) {
+      const size_t l = (size_t)P.split_l[si] * S, r = (size_t)P.split_r[si] * S;
+      const float lsp = P.split_lsp[si];
+      for (int s = tid; s < S; s += NT) {
+        const int i = T.pre[s];
+        R0[i] = P.pi[l + s];
+        R1[i] = P.pi[r + s];
+        R2[i] = P.pibar[l + s];
+        R3[i] = P.pibar[r + s];
+      }
+      __syncthreads();
 #pragma unroll
       for (int k = 0; k < CPT; ++k) {
-        const int s = tid + k * NT;
-        if (s < S) {
-          const int a1 = P.tr.c1[s], a2 = P.tr.c2[s];
-          const float pl = Pl[s], pr = Pr[s];
-          const float d = P.pD.at(item, s), sp = P.pS.at(item, s);
+        const int i = own_pos<NT, CPT>(k);
+        if (okp[k]) {
+          const bool h1 = O.c1p[k] != ZERO, h2 = O.c2p[k] != ZERO;
+          const float pl = R0[i], pr = R1[i];
+          const float d = P.pD.at(item, i), sp = P.pS.at(item, i);
+          const float l1 = h1 ? R0[O.c1p[k]] : KB_NEG_INF, r1 = h1 ? R1[O.c1p[k]] : KB_NEG_INF;
+          const float l2 = h2 ? R0[O.c2p[k]] : KB_NEG_INF, r2 = h2 ? R1[O.c2p[k]] : KB_NEG_INF;
           const float t0 = lsp + d + pl + pr;
-          const float t1 = lsp + pl + Br[s];
-          const float t2 = lsp + pr + Bl[s];
-          const float l1 = a1 >= 0 ? Pl[a1] : KB_NEG_INF, r1 = a1 >= 0 ? Pr[a1] : KB_NEG_INF;
-          const float l2 = a2 >= 0 ? Pl[a2] : KB_NEG_INF, r2 = a2 >= 0 ? Pr[a2] : KB_NEG_INF;
+          const float t1 = lsp + pl + R3[i];
+          const float t2 = lsp + pr + R2[i];
           const float t3 = lsp + sp + l1 + r2;
           const float t4 = lsp + sp + r1 + l2;
-          float m5 = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), t4);
-          float ms = fsafe(m5);
-          float s5 = exp2f(t0 - ms) + exp2f(t1 - ms) + exp2f(t2 - ms) + exp2f(t3 - ms) + exp2f(t4 - ms);
+          const float m5 = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), t4);
+          const float ms = fsafe(m5);
+          const float s5 = exp2f(t0 - ms) + exp2f(t1 - ms) + exp2f(t2 - ms) + exp2f(t3 - ms) + exp2f(t4 - ms);
           lse_merge(m[k], acc[k], m5, s5);
         }
       }
+      __syncthreads();
     }
 #pragma unroll
     for (int k = 0; k < CPT; ++k) dts[k] = log2f(acc[k]) + m[k];
   }
 
-  // ---- 4. J^T coefficients at Pi* (precompute kernel)
+  // ---- 4. J^T coefficients at Pi* (precompute kernel, wave_backward.py:264-416)
   const float rms = fsafe(P.rowmax[row]);
-  float pp[CPT];
+  float pbv[CPT], pp[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int i = own_pos<NT, CPT>(k);
+    R0[i] = piv[k];  // Pi* at own positions for the child gathers (padding position i >= S: -inf)
+  }
+  load_row_pre<NT, CPT>(T, P.pibar + rb, R1, pbv, KB_NEG_INF);  // barrier also publishes R0
   float ls = 0.0f;
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
-    const int s = tid + k * NT;
-    pp[k] = 0.0f;
-    if (s < S) {
-      pp[k] = exp2f((P.use_col ? P.col[s] + piv[k] : piv[k]) - rms);
-      B0[s] = pp[k];
-      B2[s] = piv[k];
-      ls += pp[k];
-    }
+    const int i = own_pos<NT, CPT>(k);
+    pp[k] = okp[k] ? exp2f((WEIGHTED ? P.col[i] : 0.0f) + piv[k] - rms) : 0.0f;
+    R2[i] = pp[k];
+    ls += pp[k];
   }
-  const float rowsum = block_sum<NT>(ls, red);
-  const float* ps = path_sum_lds<NT, CPT>(P.tr, B0, B1);
-  const int leaf = leaf_wave ? P.leaf_state[row] : -1;
-  float q[6][CPT], inv_denom[CPT];
+  const float rowsum = block_sum1<NT>(ls, wA);
+  float ps[CPT];
+  path_sum_euler<NT, CPT>(O, R2, Sc, wB, ps);
+  const int lpos = leaf_row ? T.pre[P.leaf_state[row]] : -1;
+  float q[6][CPT], pcoef[CPT];
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
-    const int s = tid + k * NT;
+    const int i = own_pos<NT, CPT>(k);
 #pragma unroll
     for (int j = 0; j < 6; ++j) q[j][k] = 0.0f;
-    inv_denom[k] = 0.0f;
-    if (s < S) {
-      const float denom = rowsum - ps[s];
-      inv_denom[k] = denom > 0.0f ? 1.0f / denom : 0.0f;
-      const int a1 = P.tr.c1[s], a2 = P.tr.c2[s];
-      const float t0 = P.DL[cb + s] + piv[k];
-      const float t1 = piv[k] + P.Ebar[cb + s];
-      const float t2 = P.pibar[rb + s] + P.E[cb + s];
-      const float t3 = P.SL1[cb + s] + (a1 >= 0 ? B2[a1] : KB_NEG_INF);
-      const float t4 = P.SL2[cb + s] + (a2 >= 0 ? B2[a2] : KB_NEG_INF);
-      const float t5 = (leaf_wave && s == leaf) ? P.leaf_logp[cb + s] : KB_NEG_INF;
-      float m = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, t5));
+    pcoef[k] = 0.0f;
+    if (okp[k]) {
+      const float denom = rowsum - ps[k];
+      const float inv_denom = denom > 0.0f ? 1.0f / denom : 0.0f;
+      const bool h1 = O.c1p[k] != ZERO, h2 = O.c2p[k] != ZERO;
+      const size_t ci = cb + i;
+      const float t0 = P.DL[ci] + piv[k];
+      const float t1 = piv[k] + P.Ebar[ci];
+      const float t2 = pbv[k] + P.E[ci];
+      const float t3 = P.SL1[ci] + (h1 ? R0[O.c1p[k]] : KB_NEG_INF);
+      const float t4 = P.SL2[ci] + (h2 ? R0[O.c2p[k]] : KB_NEG_INF);
+      const float t5 = i == lpos ? P.leaf_logp[ci] : KB_NEG_INF;
+      const float m = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, t5));
       const float msf = fsafe(m);
       float e[6] = {exp2f(t0 - msf), exp2f(t1 - msf), exp2f(t2 - msf), exp2f(t3 - msf), exp2f(t4 - msf),
                     exp2f(t5 - msf)};
       const float sum = e[0] + e[1] + e[2] + e[3] + e[4] + e[5];
       const float inv_sum = sum > 0.0f ? 1.0f / sum : 0.0f;
       float wL = 1.0f;
-      if (!leaf_wave) {
+      if (!leaf_row) {
         const float dl = log2f(sum) + m;
         const float pm = fmaxf(dl, dts[k]);
         const float pms = fsafe(pm);
@@ -223,35 +215,39 @@ __global__ __launch_bounds__(NT) void bwd_wave_kernel(BwdParams P, int first) {
       }
 #pragma unroll
       for (int j = 0; j < 6; ++j) q[j][k] = wL * e[j] * inv_sum;
+      pcoef[k] = q[2][k] * inv_denom;
     }
   }
-  __syncthreads();  // B2 / path-sum buffers are reused below
-  // child-edge weights: into column s from its parent p, q3[p] if s == c1[p] else q4[p]
+  // child-edge weights into position i from its parent: q3 if i is child1, else q4.
+  // Sc (= R2..R3) is still being read above: barrier, then restore the padding.
+  __syncthreads();
+  if (tid < 64) {
+    R2[MAXS + tid] = 0.0f;
+    R3[MAXS + tid] = 0.0f;
+  }
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
-    const int s = tid + k * NT;
-    if (s < S) {
-      B0[s] = q[3][k];
-      B1[s] = q[4][k];
-    }
+    const int i = own_pos<NT, CPT>(k);
+    R2[i] = q[3][k];
+    R3[i] = q[4][k];
   }
   __syncthreads();
-  float edge[CPT];
-  int par[CPT];
+  float edge[CPT], diag[CPT];
+  int ppos[CPT], endm1[CPT], prev[CPT], pfl[CPT];
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
-    const int s = tid + k * NT;
-    edge[k] = 0.0f;
-    par[k] = -1;
-    if (s < S) {
-      const int p = P.tr.parent[s];
-      par[k] = p;
-      if (p >= 0) edge[k] = (P.tr.c1[p] == s) ? B0[p] : B1[p];
-    }
+    const int i = own_pos<NT, CPT>(k);
+    const int pa = okp[k] ? T.ppos[i] : -1;
+    ppos[k] = pa >= 0 ? pa : ZERO;
+    pfl[k] = pa >= 0 ? T.pflag[i] : 0;
+    edge[k] = pa >= 0 ? (T.pflag[i] ? R2[pa] : R3[pa]) : 0.0f;
+    endm1[k] = okp[k] ? T.endpos[i] - 1 : ZERO;
+    prev[k] = i > 0 ? i - 1 : ZERO;
+    diag[k] = q[0][k] + q[1][k];
   }
-  __syncthreads();
+  __syncthreads();  // R2 / R3 become scan buffers
 
-  // ---- 5. Neumann series v = sum_{n<=N} (J^T)^n rhs, row on chip
+  // ---- 5. Neumann series v = sum_{n<=N} (J^T)^n rhs with the row on chip
   float v[CPT], term[CPT];
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
@@ -259,50 +255,43 @@ __global__ __launch_bounds__(NT) void bwd_wave_kernel(BwdParams P, int first) {
     term[k] = rhs[k];
   }
   for (int n = 0; n < P.n_terms; ++n) {
-    float lu = 0.0f;
+    float* Tb = (n & 1) ? R1 : R0;
+    float* Pb = (n & 1) ? R3 : R2;
+    float* wt = (n & 1) ? wB : wA;
+    float u[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const int s = tid + k * NT;
-      if (s < S) {
-        const float u = term[k] * (q[2][k] * inv_denom[k]);
-        B0[s] = term[k];
-        B1[s] = u;
-        lu += u;
-      }
+      Tb[own_pos<NT, CPT>(k)] = term[k];
+      u[k] = term[k] * pcoef[k];
     }
-    const float A = block_sum<NT>(lu, red);
-    subtree_sum_lds<NT>(P.tr, B1);
+    const float A = block_scan_incl<NT, CPT>(u, wt);  // barrier: publishes Tb
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-      const int s = tid + k * NT;
-      if (s < S) {
-        float nt = term[k] * (q[0][k] + q[1][k]) + pp[k] * (A - B1[s]);
-        if (par[k] >= 0) nt += B0[par[k]] * edge[k];
-        term[k] = nt;
-        v[k] += nt;
-      }
-    }
+    for (int k = 0; k < CPT; ++k) Pb[own_pos<NT, CPT>(k)] = u[k];
     __syncthreads();
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const float comp = Pb[prev[k]] + (A - Pb[endm1[k]]);
+      const float nt = term[k] * diag[k] + pp[k] * comp + Tb[ppos[k]] * edge[k];
+      term[k] = nt;
+      v[k] += nt;
+    }
   }
 
-  // ---- 6. column gradient of the self loop and the parameter buckets
+  // ---- 6. self-loop column gradient and parameter buckets
   float c[8][CPT];
   {
-    float lu = 0.0f;
+    const int n = P.n_terms;
+    float* Pb = (n & 1) ? R3 : R2;
+    float* wt = (n & 1) ? wB : wA;
+    float u[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) u[k] = v[k] * pcoef[k];
+    const float A = block_scan_incl<NT, CPT>(u, wt);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) Pb[own_pos<NT, CPT>(k)] = u[k];
+    __syncthreads();
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const int s = tid + k * NT;
-      if (s < S) {
-        const float u = v[k] * (q[2][k] * inv_denom[k]);
-        B1[s] = u;
-        lu += u;
-      }
-    }
-    const float A = block_sum<NT>(lu, red);
-    subtree_sum_lds<NT>(P.tr, B1);
-#pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-      const int s = tid + k * NT;
       const float aw0 = v[k] * q[0][k], aw1 = v[k] * q[1][k], aw2 = v[k] * q[2][k];
       const float aw3 = v[k] * q[3][k], aw4 = v[k] * q[4][k], aw5 = v[k] * q[5][k];
       c[0][k] = aw0;
@@ -312,136 +301,142 @@ __global__ __launch_bounds__(NT) void bwd_wave_kernel(BwdParams P, int first) {
       c[4][k] = aw4;
       c[5][k] = aw3;
       c[6][k] = aw2;
-      c[7][k] = s < S ? pp[k] * (A - B1[s]) : 0.0f;
+      c[7][k] = okp[k] ? pp[k] * (Pb[prev[k]] + (A - Pb[endm1[k]])) : 0.0f;
     }
-    __syncthreads();
   }
 
-  // ---- 7. split adjoints into the child rows (staging) incl. the Pibar VJP
-  for (int i = sb; i < se; ++i) {
-    const int lrow = P.split_l[i], rrow = P.split_r[i];
+  // ---- 7. split adjoints into the child rows (staging, preorder layout)
+  for (int si = sb; si < se; ++si) {
+    const int lrow = P.split_l[si], rrow = P.split_r[si];
     const size_t l = (size_t)lrow * S, r = (size_t)rrow * S;
-    const float lsp = P.split_lsp[i];
-    const float* Pl = P.pi + l;
-    const float* Pr = P.pi + r;
-    const float* Bl = P.pibar + l;
-    const float* Br = P.pibar + r;
+    const float lsp = P.split_lsp[si];
     const float rml = P.rowmax[lrow], rmr = P.rowmax[rrow];
-    float vd0[CPT], vd1[CPT], vd2[CPT];
-    float al = 0.0f, ar = 0.0f;
+    const float rmsl = fsafe(rml), rmsr = fsafe(rmr);
+    __syncthreads();  // previous readers of R0..R3 are done
+    for (int s = tid; s < S; s += NT) {
+      const int i = T.pre[s];
+      R0[i] = P.pi[l + s];
+      R1[i] = P.pi[r + s];
+      R2[i] = P.pibar[l + s];
+      R3[i] = P.pibar[r + s];
+    }
+    __syncthreads();
+    float vd0[CPT], vd1[CPT], vd2[CPT], vd3[CPT], vd4[CPT], udl[CPT], udr[CPT], ppl[CPT], ppr[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const int s = tid + k * NT;
-      vd0[k] = vd1[k] = vd2[k] = 0.0f;
-      if (s < S) {
-        const int a1 = P.tr.c1[s], a2 = P.tr.c2[s];
-        const float pl = Pl[s], pr = Pr[s], bl = Bl[s], br = Br[s];
-        const float d = P.pD.at(item, s), sp = P.pS.at(item, s);
-        const float l1 = a1 >= 0 ? Pl[a1] : KB_NEG_INF, r1 = a1 >= 0 ? Pr[a1] : KB_NEG_INF;
-        const float l2 = a2 >= 0 ? Pl[a2] : KB_NEG_INF, r2 = a2 >= 0 ? Pr[a2] : KB_NEG_INF;
-        const float pp_ = piv[k];
-        const bool pv = pp_ != KB_NEG_INF;
-        const float base = pv ? lsp - pp_ : 0.0f;
-        const float w0 = pv ? exp2f(base + (d + pl + pr)) : 0.0f;
-        const float w1 = pv ? exp2f(base + (pl + br)) : 0.0f;
-        const float w2 = pv ? exp2f(base + (pr + bl)) : 0.0f;
-        const float w3 = pv ? exp2f(base + (sp + l1 + r2)) : 0.0f;
-        const float w4 = pv ? exp2f(base + (sp + r1 + l2)) : 0.0f;
-        vd0[k] = v[k] * w0;
-        vd1[k] = v[k] * w1;
-        vd2[k] = v[k] * w2;
-        const float vd3 = v[k] * w3, vd4 = v[k] * w4;
-        B2[s] = vd3;
-        B3[s] = vd4;
-        const float mts = P.mt[cb + s];
+      const int i = own_pos<NT, CPT>(k);
+      vd0[k] = vd1[k] = vd2[k] = vd3[k] = vd4[k] = udl[k] = udr[k] = ppl[k] = ppr[k] = 0.0f;
+      if (okp[k]) {
+        const bool h1 = O.c1p[k] != ZERO, h2 = O.c2p[k] != ZERO;
+        const float pl = R0[i], pr = R1[i], bl = R2[i], br = R3[i];
+        const float l1 = h1 ? R0[O.c1p[k]] : KB_NEG_INF, r1 = h1 ? R1[O.c1p[k]] : KB_NEG_INF;
+        const float l2 = h2 ? R0[O.c2p[k]] : KB_NEG_INF, r2 = h2 ? R1[O.c2p[k]] : KB_NEG_INF;
+        const float d = P.pD.at(item, i), sp = P.pS.at(item, i);
+        const bool pv = piv[k] != KB_NEG_INF;
+        const float base = pv ? lsp - piv[k] : 0.0f;
+        vd0[k] = pv ? v[k] * exp2f(base + (d + pl + pr)) : 0.0f;
+        vd1[k] = pv ? v[k] * exp2f(base + (pl + br)) : 0.0f;
+        vd2[k] = pv ? v[k] * exp2f(base + (pr + bl)) : 0.0f;
+        vd3[k] = pv ? v[k] * exp2f(base + (sp + l1 + r2)) : 0.0f;
+        vd4[k] = pv ? v[k] * exp2f(base + (sp + r1 + l2)) : 0.0f;
+        const float mts = P.mt[cb + i];
         const float inv_l = bl != KB_NEG_INF ? exp2f(rml + mts - bl) : 0.0f;
         const float inv_r = br != KB_NEG_INF ? exp2f(rmr + mts - br) : 0.0f;
-        const float udl = vd2[k] * inv_l, udr = vd1[k] * inv_r;
-        B0[s] = udl;
-        B1[s] = udr;
-        al += udl;
-        ar += udr;
-        c[0][k] += vd0[k];
-        c[1][k] += vd3 + vd4;
-        c[6][k] += vd1[k] + vd2[k];
+        udl[k] = vd2[k] * inv_l;
+        udr[k] = vd1[k] * inv_r;
+        const float cw = WEIGHTED ? P.col[i] : 0.0f;
+        ppl[k] = exp2f(cw + pl - rmsl);
+        ppr[k] = exp2f(cw + pr - rmsr);
       }
     }
-    block_sum2<NT>(al, ar, red);
-    subtree_sum2_lds<NT>(P.tr, B0, B1);
-    float* stl = P.staging + (size_t)(2 * i) * S;
-    float* str = P.staging + (size_t)(2 * i + 1) * S;
-    const float rmsl = fsafe(rml), rmsr = fsafe(rmr);
+    __syncthreads();  // staged children fully read
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const int s = tid + k * NT;
-      if (s < S) {
-        const float cw = P.use_col ? P.col[s] : 0.0f;
-        const float ppl = exp2f(cw + Pl[s] - rmsl);
-        const float ppr = exp2f(cw + Pr[s] - rmsr);
-        const float tl = ppl * (al - B0[s]);
-        const float tr = ppr * (ar - B1[s]);
-        float shl = 0.0f, shr = 0.0f;
-        const int p = par[k];
-        if (p >= 0) {
-          if (P.tr.c1[p] == s) {
-            shl = B2[p];
-            shr = B3[p];
-          } else {
-            shl = B3[p];
-            shr = B2[p];
-          }
-        }
-        stl[s] = vd0[k] + vd1[k] + shl + tl;
-        str[s] = vd0[k] + vd2[k] + shr + tr;
+      const int i = own_pos<NT, CPT>(k);
+      R0[i] = vd3[k];
+      R1[i] = vd4[k];
+    }
+    float Al, Ar;
+    block_scan_incl2<NT, CPT>(udl, udr, wA, Al, Ar);  // barrier: publishes R0 / R1
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int i = own_pos<NT, CPT>(k);
+      R2[i] = udl[k];
+      R3[i] = udr[k];
+    }
+    __syncthreads();
+    float* stl = P.staging + (size_t)(2 * si) * S;
+    float* str = P.staging + (size_t)(2 * si + 1) * S;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int i = own_pos<NT, CPT>(k);
+      if (okp[k]) {
+        const float tl = ppl[k] * (R2[prev[k]] + (Al - R2[endm1[k]]));
+        const float tr = ppr[k] * (R3[prev[k]] + (Ar - R3[endm1[k]]));
+        const int pa = ppos[k];
+        const bool first = pfl[k] != 0;
+        const float sh3 = R0[pa], sh4 = R1[pa];  // padding slot holds 0
+        const float shl = first ? sh3 : sh4;
+        const float shr = first ? sh4 : sh3;
+        stl[i] = vd0[k] + vd1[k] + shl + tl;
+        str[i] = vd0[k] + vd2[k] + shr + tr;
+        c[0][k] += vd0[k];
+        c[1][k] += vd3[k] + vd4[k];
+        c[6][k] += vd1[k] + vd2[k];
         c[7][k] += tl + tr;
       }
     }
-    if (tid == 0) P.split_on[i] = 1;
-    __syncthreads();
+    if (tid == 0) P.split_on[si] = 1;
   }
 
-  // ---- 8. per-row gradient buckets (reduced over rows in a fixed order later)
+  // ---- 8. per-row gradient buckets (preorder layout; reduced over rows later)
   float* cr = P.contrib + (size_t)row * 8 * S;
 #pragma unroll
   for (int j = 0; j < 8; ++j)
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-      const int s = tid + k * NT;
-      if (s < S) cr[(size_t)j * S + s] = c[j][k];
-    }
+    for (int k = 0; k < CPT; ++k)
+      if (okp[k]) cr[(size_t)j * S + own_pos<NT, CPT>(k)] = c[j][k];
 }
 
-#define KB_BWD_CASE(NT_, CPT_)                                                                   \
-  if (S <= NT_ * CPT_) {                                                                         \
-    hipLaunchKernelGGL((bwd_wave_kernel<NT_, CPT_>), dim3(W), dim3(NT_), 0, st, P, first);        \
-    return;                                                                                      \
+#define KB_BWD_CASE(NT_, CPT_)                                                                      \
+  if (S <= NT_ * CPT_) {                                                                            \
+    if (P.use_col)                                                                                  \
+      hipLaunchKernelGGL((bwd_row_kernel<NT_, CPT_, true>), dim3(W), dim3(NT_), 0, st, P, first);   \
+    else                                                                                            \
+      hipLaunchKernelGGL((bwd_row_kernel<NT_, CPT_, false>), dim3(W), dim3(NT_), 0, st, P, first);  \
+    return;                                                                                         \
   }
 
 void launch_bwd_wave(const BwdParams& P, int first, int W, hipStream_t st) {
   if (W <= 0) return;
   const int S = P.S;
-  KB_BWD_CASE(64, 1)
-  KB_BWD_CASE(128, 1)
-  KB_BWD_CASE(256, 1)
+  KB_BWD_CASE(64, 2)
+  KB_BWD_CASE(128, 2)
   KB_BWD_CASE(256, 2)
-  KB_BWD_CASE(512, 2)
+  KB_BWD_CASE(256, 4)
   KB_BWD_CASE(512, 4)
   KB_BWD_CASE(1024, 4)
   KB_BWD_CASE(1024, 8)
 }
 
 // ---- backward constants from the saved tensors, in the glue's float32 order
-// (_implicit_grad.py:136-143: DL = 1 + pD + E, SL1 = pS + E_s2, SL2 = pS + E_s1)
+// (_implicit_grad.py:136-143: DL = 1 + pD + E, SL1 = pS + E_s2, SL2 = pS + E_s1),
+// written at preorder positions for the row kernel.
 __global__ void bwd_consts_kernel(BwdConstArgs A) {
   const int s = blockIdx.x * blockDim.x + threadIdx.x;
   if (s >= A.S) return;
+  const int i = A.pre[s];
   const float pS = A.log_pS[A.statewise ? s : 0];
   const float pD = A.log_pD[A.statewise ? s : 0];
-  A.DL[s] = (1.0f + pD) + A.E[s];
-  A.SL1[s] = pS + A.E_s2[s];
-  A.SL2[s] = pS + A.E_s1[s];
-  A.pS_state[s] = pS;
-  A.pD_state[s] = pD;
+  A.DL[i] = (1.0f + pD) + A.E[s];
+  A.SL1[i] = pS + A.E_s2[s];
+  A.SL2[i] = pS + A.E_s1[s];
+  A.pS_state[i] = pS;
+  A.pD_state[i] = pD;
+  A.Ebar_pre[i] = A.Ebar[s];
+  A.E_pre[i] = A.E[s];
+  A.mt_pre[i] = A.mt[s];
+  A.col_pre[i] = A.col[s];
 }
 
 void launch_bwd_consts(const BwdConstArgs& A, hipStream_t st) {
@@ -450,6 +445,7 @@ void launch_bwd_consts(const BwdConstArgs& A, hipStream_t st) {
 
 // ---- column sums of the per-row buckets over active rows, fixed order.
 // Stage 1: chunk c of rows -> partial[c][8*S]; stage 2: sum of chunks.
+// The result is in preorder-position order: out[j*S + pre(s)].
 constexpr int RED_CHUNK = 256;
 
 __global__ void bwd_reduce_stage1(const float* contrib, const unsigned char* mask, int C, int S, double* partial) {
@@ -471,12 +467,23 @@ __global__ void bwd_reduce_stage2(const double* partial, int n_chunks, int S, do
   out[j] = acc;
 }
 
+__global__ void bwd_unpermute(const double* in, const int* pre, int S, double* out) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= 8 * S) return;
+  const int a = j / S, s = j - a * S;
+  out[j] = in[(size_t)a * S + pre[s]];
+}
+
 void launch_bwd_reduce(const float* contrib, const unsigned char* mask, int C, int S, double* partial,
                        double* out, hipStream_t st) {
   const int n_chunks = (C + RED_CHUNK - 1) / RED_CHUNK;
   dim3 g1((8 * S + 255) / 256, n_chunks);
   hipLaunchKernelGGL(bwd_reduce_stage1, g1, dim3(256), 0, st, contrib, mask, C, S, partial);
   hipLaunchKernelGGL(bwd_reduce_stage2, dim3((8 * S + 255) / 256), dim3(256), 0, st, partial, n_chunks, S, out);
+}
+
+void launch_bwd_unpermute(const double* in, const int* pre, int S, double* out, hipStream_t st) {
+  hipLaunchKernelGGL(bwd_unpermute, dim3((8 * S + 255) / 256), dim3(256), 0, st, in, pre, S, out);
 }
 
 int reduce_chunks(int C) { return (C + RED_CHUNK - 1) / RED_CHUNK; }

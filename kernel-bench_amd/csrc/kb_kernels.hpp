@@ -79,12 +79,17 @@ void launch_fwd_wave(const FwdParams& P, int first, int n, hipStream_t st);
 struct BwdConstArgs {
   int S;
   int statewise;
+  const int* pre;
   const float* log_pS; const float* log_pD; const float* E; const float* E_s1; const float* E_s2;
+  const float* Ebar; const float* mt; const float* col;
+  // outputs at preorder positions
   float* DL; float* SL1; float* SL2; float* pS_state; float* pD_state;
+  float* Ebar_pre; float* E_pre; float* mt_pre; float* col_pre;
 };
 
 struct BwdParams {
   TreeDev tr;
+  PreDev pre;
   int S;
   int n_terms;                // neumann_terms
   float thr;                  // adjoint_pruning_threshold
@@ -135,6 +140,7 @@ void launch_bwd_consts(const BwdConstArgs& A, hipStream_t st);
 void launch_bwd_wave(const BwdParams& P, int first, int n, hipStream_t st);
 void launch_bwd_reduce(const float* contrib, const unsigned char* mask, int C, int S, double* partial,
                        double* out, hipStream_t st);
+void launch_bwd_unpermute(const double* in, const int* pre, int S, double* out, hipStream_t st);
 int reduce_chunks(int C);
 void launch_epilogue(const EpiParams& P, hipStream_t st);
 int epilogue_work_vectors();

@@ -91,6 +91,8 @@ struct kb_plan {
   int* b_status = nullptr;
   float* b_DL = nullptr; float* b_SL1 = nullptr; float* b_SL2 = nullptr; float* b_pS = nullptr; float* b_pD = nullptr;
   float* b_Ebar = nullptr; float* b_E = nullptr; float* b_mt = nullptr; float* b_col = nullptr; double* b_acc_pre = nullptr;
+  int b_nb_max = 0, b_n_partials = 0;
+  std::vector<int> b_poff;
   // optional per-launch timing of the wave kernels (HIP events on the launch stream)
   int prof = 0;
   std::vector<hipEvent_t> ev_fwd, ev_bwd;
@@ -540,16 +542,40 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
   return 0;
 }
 
-static int ensure_backward_work(kb_plan* p) {
-  if (p->b_contrib) return 0;
+static int ensure_backward_work(kb_plan* p, int use_col) {
   const int S = p->S, C = p->C;
+  // resident workgroups of the backward row kernel: its per-level grid
+  int dev = 0, n_cu = 0;
+  KB_HIP(hipGetDevice(&dev));
+  KB_HIP(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
+  const int nb_max = std::max(1, n_cu * kb::bwd_blocks_per_cu(S, use_col));
+  if (p->b_contrib && p->b_nb_max == nb_max) return 0;
+  p->b_nb_max = nb_max;
+  p->b_poff.assign(p->n_levels + 1, 0);
+  for (int d = 0; d < p->n_levels; ++d)
+    p->b_poff[d + 1] = p->b_poff[d] + std::min(nb_max, p->level_ptr[d + 1] - p->level_ptr[d]);
+  p->b_n_partials = p->b_poff[p->n_levels];
+  if (p->b_contrib) {
+    (void)hipFree(p->b_contrib);
+    (void)hipFree(p->b_partial);
+    for (auto& ptr : p->owned)
+      if (ptr == (void*)p->b_contrib || ptr == (void*)p->b_partial) ptr = nullptr;
+    p->b_contrib = nullptr;
+    p->b_partial = nullptr;
+    int rc = 0;
+    rc |= alloc(&p->b_contrib, (size_t)std::max(1, p->b_n_partials) * 8 * S);
+    rc |= alloc(&p->b_partial, (size_t)kb::reduce_chunks(std::max(1, p->b_n_partials)) * 8 * S);
+    p->owned.push_back(p->b_contrib);
+    p->owned.push_back(p->b_partial);
+    return rc ? KB_ERR_HIP : 0;
+  }
   const int64_t NS = p->n_splits;
   int rc = 0;
   rc |= alloc(&p->b_staging, (size_t)std::max<int64_t>(1, 2 * NS) * S);
   rc |= alloc(&p->b_split_on, (size_t)std::max<int64_t>(1, NS));
   rc |= alloc(&p->b_mask, (size_t)std::max(1, C));
-  rc |= alloc(&p->b_contrib, (size_t)std::max(1, C) * 8 * S);
-  rc |= alloc(&p->b_partial, (size_t)kb::reduce_chunks(std::max(1, C)) * 8 * S);
+  rc |= alloc(&p->b_contrib, (size_t)std::max(1, p->b_n_partials) * 8 * S);
+  rc |= alloc(&p->b_partial, (size_t)kb::reduce_chunks(std::max(1, p->b_n_partials)) * 8 * S);
   rc |= alloc(&p->b_acc, (size_t)8 * S);
   rc |= alloc(&p->b_work, (size_t)kb::epilogue_work_vectors() * S);
   rc |= alloc(&p->b_status, 2);
@@ -578,7 +604,7 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   if (!(io->bicgstab_tol > 0.0)) return set_error(KB_ERR_ARG, "tol must be positive");
   if (!(io->bicgstab_breakdown_tol > 0.0)) return set_error(KB_ERR_ARG, "breakdown_tol must be positive");
   if (io->pruning_threshold < 0.0) return set_error(KB_ERR_ARG, "adjoint_pruning_threshold must be non-negative");
-  int rc = ensure_backward_work(p);
+  int rc = ensure_backward_work(p, io->use_col_weights);
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
   const int S = p->S, C = p->C;
@@ -645,11 +671,12 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   B.row_kind = p->d_row_kind;
   for (int d = p->n_levels - 1; d >= 0; --d) {
     if (p->prof) KB_HIP(hipEventRecord(p->ev_bwd[2 * d], st));
-    kb::launch_bwd_wave(B, p->level_ptr[d], p->level_ptr[d + 1] - p->level_ptr[d], st);
+    const int n = p->level_ptr[d + 1] - p->level_ptr[d];
+    kb::launch_bwd_wave(B, p->level_ptr[d], n, std::min(n, p->b_nb_max), p->b_poff[d], st);
     if (p->prof) KB_HIP(hipEventRecord(p->ev_bwd[2 * d + 1], st));
   }
   KB_HIP(hipGetLastError());
-  kb::launch_bwd_reduce(p->b_contrib, B.mask, C, S, p->b_partial, p->b_acc_pre, st);
+  kb::launch_bwd_reduce(p->b_contrib, p->b_n_partials, S, p->b_partial, p->b_acc_pre, st);
   kb::launch_bwd_unpermute(p->b_acc_pre, p->d_pre, S, p->b_acc, st);
   KB_HIP(hipGetLastError());
   if (io->acc_out)

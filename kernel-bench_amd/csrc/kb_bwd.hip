@@ -30,7 +30,7 @@
 namespace kb {
 
 template <int NT, int CPT, bool WEIGHTED>
-__global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first) {
+__global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int n_rows, int poff) {
   constexpr int MAXS = NT * CPT;
   constexpr int LD = MAXS + 64;  // [MAXS] is the padding slot, kept at 0
   constexpr int NW = NT / 64;
@@ -45,12 +45,6 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first) {
   const PreDev& T = P.pre;
   const int S = P.S;
   const int tid = threadIdx.x;
-  const int row = P.sched_rows[first + blockIdx.x];
-  const int leaf_row = P.row_kind[row];
-  const int item = P.item[row];
-  const size_t cb = (size_t)item * P.const_stride;
-  const size_t rb = (size_t)row * S;
-  const int sb = P.split_ptr[row], se = P.split_ptr[row + 1];
   constexpr int ZERO = MAXS;
 
   OwnTables<NT, CPT> O;
@@ -64,6 +58,22 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first) {
   bool okp[CPT];
 #pragma unroll
   for (int k = 0; k < CPT; ++k) okp[k] = own_pos<NT, CPT>(k) < S;
+  // gradient buckets of every row this workgroup processes (static round-robin
+  // assignment, so the summation order is fixed)
+  float cacc[8][CPT];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) cacc[j][k] = 0.0f;
+
+  for (int rr = blockIdx.x; rr < n_rows; rr += gridDim.x) {
+  __syncthreads();  // LDS of the previous row is no longer read
+  const int row = P.sched_rows[first + rr];
+  const int leaf_row = P.row_kind[row];
+  const int item = P.item[row];
+  const size_t cb = (size_t)item * P.const_stride;
+  const size_t rb = (size_t)row * S;
+  const int sb = P.split_ptr[row], se = P.split_ptr[row + 1];
 
   // ---- 1. Pi* of this row and its adjoint: root seed or fixed-order gather
   float piv[CPT];
@@ -108,7 +118,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first) {
   if (tid == 0) P.mask[row] = active ? 1 : 0;
   if (!active) {
     for (int i = sb + tid; i < se; i += NT) P.split_on[i] = 0;
-    return;
+    continue;
   }
   __syncthreads();  // R0 (Pi*) and the scratch above are reused below
 
@@ -278,7 +288,6 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first) {
   }
 
   // ---- 6. self-loop column gradient and parameter buckets
-  float c[8][CPT];
   {
     const int n = P.n_terms;
     float* Pb = (n & 1) ? R3 : R2;
@@ -294,14 +303,14 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first) {
     for (int k = 0; k < CPT; ++k) {
       const float aw0 = v[k] * q[0][k], aw1 = v[k] * q[1][k], aw2 = v[k] * q[2][k];
       const float aw3 = v[k] * q[3][k], aw4 = v[k] * q[4][k], aw5 = v[k] * q[5][k];
-      c[0][k] = aw0;
-      c[1][k] = aw3 + aw4 + aw5;
-      c[2][k] = aw0 + aw2;
-      c[3][k] = aw1;
-      c[4][k] = aw4;
-      c[5][k] = aw3;
-      c[6][k] = aw2;
-      c[7][k] = okp[k] ? pp[k] * (Pb[prev[k]] + (A - Pb[endm1[k]])) : 0.0f;
+      cacc[0][k] += aw0;
+      cacc[1][k] += aw3 + aw4 + aw5;
+      cacc[2][k] += aw0 + aw2;
+      cacc[3][k] += aw1;
+      cacc[4][k] += aw4;
+      cacc[5][k] += aw3;
+      cacc[6][k] += aw2;
+      cacc[7][k] += okp[k] ? pp[k] * (Pb[prev[k]] + (A - Pb[endm1[k]])) : 0.0f;
     }
   }
 
@@ -380,35 +389,37 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first) {
         const float shr = first ? sh4 : sh3;
         stl[i] = vd0[k] + vd1[k] + shl + tl;
         str[i] = vd0[k] + vd2[k] + shr + tr;
-        c[0][k] += vd0[k];
-        c[1][k] += vd3[k] + vd4[k];
-        c[6][k] += vd1[k] + vd2[k];
-        c[7][k] += tl + tr;
+        cacc[0][k] += vd0[k];
+        cacc[1][k] += vd3[k] + vd4[k];
+        cacc[6][k] += vd1[k] + vd2[k];
+        cacc[7][k] += tl + tr;
       }
     }
     if (tid == 0) P.split_on[si] = 1;
   }
 
-  // ---- 8. per-row gradient buckets (preorder layout; reduced over rows later)
-  float* cr = P.contrib + (size_t)row * 8 * S;
+  }  // rows
+
+  // one partial per workgroup (preorder layout; reduced over partials later)
+  float* cr = P.contrib + (size_t)(poff + blockIdx.x) * 8 * S;
 #pragma unroll
   for (int j = 0; j < 8; ++j)
 #pragma unroll
     for (int k = 0; k < CPT; ++k)
-      if (okp[k]) cr[(size_t)j * S + own_pos<NT, CPT>(k)] = c[j][k];
+      if (okp[k]) cr[(size_t)j * S + own_pos<NT, CPT>(k)] = cacc[j][k];
 }
 
 #define KB_BWD_CASE(NT_, CPT_)                                                                      \
   if (S <= NT_ * CPT_) {                                                                            \
     if (P.use_col)                                                                                  \
-      hipLaunchKernelGGL((bwd_row_kernel<NT_, CPT_, true>), dim3(W), dim3(NT_), 0, st, P, first);   \
+      hipLaunchKernelGGL((bwd_row_kernel<NT_, CPT_, true>), dim3(nb), dim3(NT_), 0, st, P, first, W, poff);  \
     else                                                                                            \
-      hipLaunchKernelGGL((bwd_row_kernel<NT_, CPT_, false>), dim3(W), dim3(NT_), 0, st, P, first);  \
+      hipLaunchKernelGGL((bwd_row_kernel<NT_, CPT_, false>), dim3(nb), dim3(NT_), 0, st, P, first, W, poff); \
     return;                                                                                         \
   }
 
-void launch_bwd_wave(const BwdParams& P, int first, int W, hipStream_t st) {
-  if (W <= 0) return;
+void launch_bwd_wave(const BwdParams& P, int first, int W, int nb, int poff, hipStream_t st) {
+  if (W <= 0 || nb <= 0) return;
   const int S = P.S;
   KB_BWD_CASE(64, 2)
   KB_BWD_CASE(128, 2)
@@ -417,6 +428,27 @@ void launch_bwd_wave(const BwdParams& P, int first, int W, hipStream_t st) {
   KB_BWD_CASE(512, 4)
   KB_BWD_CASE(1024, 4)
   KB_BWD_CASE(1024, 8)
+}
+
+#define KB_BWD_OCC(NT_, CPT_)                                                                          \
+  if (S <= NT_ * CPT_) {                                                                               \
+    int n = 0;                                                                                         \
+    if (use_col)                                                                                       \
+      (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, bwd_row_kernel<NT_, CPT_, true>, NT_, 0);  \
+    else                                                                                               \
+      (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, bwd_row_kernel<NT_, CPT_, false>, NT_, 0); \
+    return n > 0 ? n : 1;                                                                              \
+  }
+
+int bwd_blocks_per_cu(int S, int use_col) {
+  KB_BWD_OCC(64, 2)
+  KB_BWD_OCC(128, 2)
+  KB_BWD_OCC(256, 2)
+  KB_BWD_OCC(256, 4)
+  KB_BWD_OCC(512, 4)
+  KB_BWD_OCC(1024, 4)
+  KB_BWD_OCC(1024, 8)
+  return 1;
 }
 
 // ---- backward constants from the saved tensors, in the glue's float32 order
@@ -448,14 +480,13 @@ void launch_bwd_consts(const BwdConstArgs& A, hipStream_t st) {
 // The result is in preorder-position order: out[j*S + pre(s)].
 constexpr int RED_CHUNK = 256;
 
-__global__ void bwd_reduce_stage1(const float* contrib, const unsigned char* mask, int C, int S, double* partial) {
+__global__ void bwd_reduce_stage1(const float* contrib, int C, int S, double* partial) {
   const int j = blockIdx.x * blockDim.x + threadIdx.x;  // index in [0, 8S)
   const int chunk = blockIdx.y;
   if (j >= 8 * S) return;
   const int r0 = chunk * RED_CHUNK, r1 = min(C, r0 + RED_CHUNK);
   double acc = 0.0;
-  for (int r = r0; r < r1; ++r)
-    if (mask[r]) acc += (double)contrib[(size_t)r * 8 * S + j];
+  for (int r = r0; r < r1; ++r) acc += (double)contrib[(size_t)r * 8 * S + j];
   partial[(size_t)chunk * 8 * S + j] = acc;
 }
 
@@ -474,11 +505,10 @@ __global__ void bwd_unpermute(const double* in, const int* pre, int S, double* o
   out[j] = in[(size_t)a * S + pre[s]];
 }
 
-void launch_bwd_reduce(const float* contrib, const unsigned char* mask, int C, int S, double* partial,
-                       double* out, hipStream_t st) {
+void launch_bwd_reduce(const float* contrib, int C, int S, double* partial, double* out, hipStream_t st) {
   const int n_chunks = (C + RED_CHUNK - 1) / RED_CHUNK;
   dim3 g1((8 * S + 255) / 256, n_chunks);
-  hipLaunchKernelGGL(bwd_reduce_stage1, g1, dim3(256), 0, st, contrib, mask, C, S, partial);
+  hipLaunchKernelGGL(bwd_reduce_stage1, g1, dim3(256), 0, st, contrib, C, S, partial);
   hipLaunchKernelGGL(bwd_reduce_stage2, dim3((8 * S + 255) / 256), dim3(256), 0, st, partial, n_chunks, S, out);
 }
 

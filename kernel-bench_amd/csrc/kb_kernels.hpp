@@ -107,7 +107,7 @@ struct BwdParams {
   float* staging;             // [2 * n_splits, S]
   unsigned char* split_on;    // [n_splits]
   unsigned char* mask;        // [C]
-  float* contrib;             // [C, 8, S]
+  float* contrib;             // [n_partials, 8, S] gradient buckets, one row per workgroup and level
   const int* sched_rows;
   const int* row_kind;
 };
@@ -137,9 +137,11 @@ struct EpiParams {
 };
 
 void launch_bwd_consts(const BwdConstArgs& A, hipStream_t st);
-void launch_bwd_wave(const BwdParams& P, int first, int n, hipStream_t st);
-void launch_bwd_reduce(const float* contrib, const unsigned char* mask, int C, int S, double* partial,
-                       double* out, hipStream_t st);
+// Rows sched_rows[first .. first + n) on nb workgroups (round-robin); partial
+// bucket rows poff .. poff + nb.
+void launch_bwd_wave(const BwdParams& P, int first, int n, int nb, int poff, hipStream_t st);
+int bwd_blocks_per_cu(int S, int use_col);
+void launch_bwd_reduce(const float* contrib, int C, int S, double* partial, double* out, hipStream_t st);
 void launch_bwd_unpermute(const double* in, const int* pre, int S, double* out, hipStream_t st);
 int reduce_chunks(int C);
 void launch_epilogue(const EpiParams& P, hipStream_t st);

@@ -150,6 +150,7 @@ class FusedSolver:
         self.n_levels = int(info[6])
         self.last_n_e_iter = None
         self.last_n_bicgstab = None
+        self._use_col_cache = None
 
     def close(self):
         if getattr(self, "_plan", None):
@@ -164,8 +165,19 @@ class FusedSolver:
 
     # ------------------------------------------------------------------
     def _use_col(self, col_weights) -> bool:
+        """True unless every column weight is equal (then the uniform fast path applies).
+
+        The answer is cached per (storage, version) so repeated solves with the
+        same weights do not synchronise the host with the device.
+        """
+        key = (col_weights.data_ptr(), col_weights._version, tuple(col_weights.shape), col_weights.device)
+        hit = self._use_col_cache
+        if hit is not None and hit[0] == key:
+            return hit[1]
         flat = col_weights.detach().reshape(-1)
-        return not bool(torch.all(flat == flat[0]).item())
+        val = not bool(torch.all(flat == flat[0]).item())
+        self._use_col_cache = (key, val)
+        return val
 
     def run_forward(self, theta, col_weights, *, use_col_weights=None):
         """theta -> (loss, saved), the reference ``run_forward`` contract."""
@@ -262,7 +274,8 @@ class FusedSolver:
         S, C = self.S, self.C
         theta_d = theta.detach().to(device=dev, dtype=torch.float32).contiguous()
         cw = col_weights.detach().to(device=dev, dtype=torch.float32).contiguous()
-        use_col = self._use_col(cw)
+        use_col = saved.get("_use_col_weights")
+        use_col = self._use_col(cw) if use_col is None else bool(use_col)
         f32 = dict(device=dev, dtype=torch.float32)
         grad_theta = torch.empty(tuple(theta_d.shape), **f32)
         grad_col = torch.empty((S,), **f32)

@@ -45,7 +45,24 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-families", type=int, default=20)
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run 5 plain copy kernels of MIB MiB (read + write), the reference point "
+                         "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters to HBM bytes")
     return ap.parse_args()
+
+
+def calibrate_copy(mib: int) -> None:
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, device="cuda", dtype=torch.float32)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        torch.mul(src, 1.0, out=dst)  # one elementwise kernel: reads and writes n * 4 bytes
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "kernel": "elementwise mul by 1", "launches": 5,
+                      "bytes_read_per_launch": n * 4, "bytes_written_per_launch": n * 4}))
 
 
 def log(args, msg):
@@ -92,6 +109,9 @@ def main():
               "multi-GPU path: families would shard across GPUs with one all-reduce of O(S) gradient "
               "accumulators, which is not implemented here.", file=sys.stderr)
         sys.exit(2)
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
+        return
     import numpy as np
     import torch
 
@@ -167,17 +187,19 @@ def main():
         "fwd_wave_kernel": (fw, fwd_bytes),
         "bwd_wave_kernel": (bw, bwd_bytes),
     }
+    symbol = {"fwd_wave_kernel": "fwd_row_kernel", "bwd_wave_kernel": "bwd_row_kernel"}
     dom = max(kernels, key=lambda k: kernels[k][0].sum())
     dur, byt = kernels[dom]
     avg_ms = float(dur.mean())
     avg_bytes = float(byt.mean())
     achieved = avg_bytes / (avg_ms * 1e-3) / 1e9
     traffic = None
-    if TRAFFIC_FILE.exists():
-        try:
-            traffic = json.loads(TRAFFIC_FILE.read_text()).get(dom)
-        except Exception:
-            traffic = None
+    if TRAFFIC_FILE.exists() and args.config == "3":
+        # HBM bytes per dispatch from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this
+        # command, scaled by a copy kernel of known size (kbench.rocprof_summary)
+        rec = json.loads(TRAFFIC_FILE.read_text()).get("kernels", {})
+        hits = [v for k, v in rec.items() if symbol[dom] in k]
+        traffic = round(float(hits[0]["traffic"]), 1) if hits else None
     roofline = {
         "bound": "hbm",
         "kernel": dom,

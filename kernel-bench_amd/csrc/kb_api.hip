@@ -15,9 +15,10 @@
 #include "kb_kernels.hpp"
 
 namespace {
-
 thread_local std::string g_last_error;
+}  // namespace
 
+namespace kb {
 int set_error(int code, const char* fmt, ...) {
   char buf[512];
   va_list ap;
@@ -27,6 +28,11 @@ int set_error(int code, const char* fmt, ...) {
   g_last_error = buf;
   return code;
 }
+}  // namespace kb
+
+namespace {
+
+using kb::set_error;
 
 #define KB_HIP(expr)                                                                       \
   do {                                                                                     \

@@ -7,6 +7,10 @@
 
 namespace kb {
 
+// Records the message returned by kb_last_error(); returns `code`.
+int set_error(int code, const char* fmt, ...);
+
+
 // ----------------------------------------------------------------------------
 // parameters + E-step (kb_estep.hip)
 // ----------------------------------------------------------------------------

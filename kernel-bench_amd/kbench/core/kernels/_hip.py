@@ -1,0 +1,170 @@
+"""Plumbing shared by the HIP-backed wrappers of ``kbench.core.kernels``.
+
+* dtype codes and argument checks (the reference raises RuntimeError for an
+  unsupported dtype or device and ValueError for layouts);
+* species-tree handles (``kb_tree``), built once per set of topology tensors
+  and cached with a strong reference to those tensors, so a cached handle can
+  never be matched by a different tensor reusing the same memory;
+* fixed-order row accumulation (``kb_rows_scatter_add``, ``kb_rows_sum_into``),
+  which replaces the reference's atomic adds.
+
+There is no CPU path: every launcher raises if the HIP library is missing.
+"""
+
+from __future__ import annotations
+
+import ctypes as ct
+from collections import OrderedDict
+
+import torch
+
+from ... import _native as N
+from ..._native_ops import (KB_BF16, KB_F32, KB_F64, KbDtsCrossIO, KbDtsIO, KbEStepIO, KbEStepVjpIO,
+                            KbLeafInitIO, KbPibarVjpIO, KbWaveBwdIO, KbWaveStepIO)
+
+__all__ = [
+    "KB_BF16", "KB_F32", "KB_F64", "KbDtsCrossIO", "KbDtsIO", "KbEStepIO", "KbEStepVjpIO", "KbLeafInitIO",
+    "KbPibarVjpIO", "KbWaveBwdIO", "KbWaveStepIO",
+    "lib", "check", "ptr", "stream", "dtype_code", "require_device", "f", "i64", "tree_from_parent",
+    "tree_from_levels", "scatter_add_rows", "sum_rows_into",
+]
+
+lib = N.lib
+check = N.check
+ptr = N.ptr
+
+
+def stream(device) -> int:
+    return N.stream_handle(device)
+
+
+def dtype_code(dtype) -> int:
+    if dtype == torch.float32:
+        return KB_F32
+    if dtype == torch.float64:
+        return KB_F64
+    raise RuntimeError(f"the HIP kernels support float32 and float64 tensors only, got {dtype}")
+
+
+def require_device(t: torch.Tensor, what: str) -> None:
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{what} requires a HIP device tensor, got {t.device}")
+
+
+def f(t, dtype, device):
+    """t as a contiguous ``dtype`` tensor on ``device`` (None stays None)."""
+    if t is None:
+        return None
+    if not torch.is_tensor(t):
+        t = torch.as_tensor(t)
+    return t.to(device=device, dtype=dtype).contiguous()
+
+
+def i64(t, device):
+    return None if t is None else t.to(device=device, dtype=torch.long).contiguous()
+
+
+# ---------------------------------------------------------------- tree handles
+_TREES: "OrderedDict[tuple, tuple]" = OrderedDict()
+_TREE_CACHE_SIZE = 32
+
+
+class _Tree:
+    def __init__(self, handle: ct.c_void_p, S: int):
+        self.handle = handle
+        self.S = S
+
+    def __del__(self):  # pragma: no cover - interpreter shutdown order
+        try:
+            if self.handle:
+                N.lib().kb_tree_destroy(self.handle)
+        except Exception:
+            pass
+
+
+def _key(*ts):
+    return tuple((int(t.data_ptr()), tuple(t.shape), str(t.device), int(t._version)) for t in ts)
+
+
+def _create(S: int, parent, c1, c2) -> _Tree:
+    par = torch.as_tensor(parent, dtype=torch.long).contiguous()
+    a = torch.as_tensor(c1, dtype=torch.long).contiguous()
+    b = torch.as_tensor(c2, dtype=torch.long).contiguous()
+    h = ct.c_void_p()
+    P = ct.POINTER(ct.c_int64)
+    check(lib().kb_tree_create(int(S), ct.cast(par.data_ptr(), P), ct.cast(a.data_ptr(), P),
+                               ct.cast(b.data_ptr(), P), ct.byref(h)))
+    return _Tree(h, int(S))
+
+
+def _cached(key, keep, build):
+    hit = _TREES.get(key)
+    if hit is not None:
+        _TREES.move_to_end(key)
+        return hit[0]
+    tree = build()
+    _TREES[key] = (tree, keep)
+    while len(_TREES) > _TREE_CACHE_SIZE:
+        _TREES.popitem(last=False)
+    return tree
+
+
+def tree_from_parent(node_parent, node_child1, node_child2) -> _Tree:
+    """Tree handle from state_helpers node_parent / node_child1 / node_child2."""
+    S = int(node_parent.numel())
+    key = ("parent", S) + _key(node_parent, node_child1, node_child2)
+    return _cached(key, (node_parent, node_child1, node_child2),
+                   lambda: _create(S, node_parent.detach().cpu(), node_child1.detach().cpu(),
+                                   node_child2.detach().cpu()))
+
+
+def tree_from_levels(S, level_ptr, level_parents, level_child1, level_child2) -> _Tree:
+    """Tree handle from the compact_level_* tables (parent with its two children per entry)."""
+    S = int(S)
+    key = ("levels", S) + _key(level_ptr, level_parents, level_child1, level_child2)
+
+    def build():
+        p = level_parents.detach().cpu().long()
+        a = level_child1.detach().cpu().long()
+        b = level_child2.detach().cpu().long()
+        parent = torch.full((S,), -1, dtype=torch.long)
+        c1 = torch.full((S,), S, dtype=torch.long)
+        c2 = torch.full((S,), S, dtype=torch.long)
+        ok_a = (a >= 0) & (a < S) & (p >= 0) & (p < S)
+        ok_b = (b >= 0) & (b < S) & (p >= 0) & (p < S)
+        parent[a[ok_a]] = p[ok_a]
+        parent[b[ok_b]] = p[ok_b]
+        c1[p[ok_a]] = a[ok_a]
+        c2[p[ok_b]] = b[ok_b]
+        return _create(S, parent, c1, c2)
+
+    return _cached(key, (level_ptr, level_parents, level_child1, level_child2), build)
+
+
+# ------------------------------------------------------ fixed-order accumulation
+def scatter_add_rows(dst: torch.Tensor, src: torch.Tensor, keys: torch.Tensor, *, row_stride=None) -> None:
+    """dst[keys[r]] += src[r] for every row r, summed per key in increasing r.
+
+    ``dst`` rows are ``row_stride`` elements apart (default: dst.shape[-1]);
+    row_stride 0 adds every row into the single row ``dst`` (all keys must be 0).
+    Negative keys are skipped.
+    """
+    n = int(src.shape[0])
+    if n == 0:
+        return
+    S = int(src.shape[1])
+    keys_sorted, order = torch.sort(keys.to(device=src.device, dtype=torch.long).reshape(-1), stable=True)
+    order32 = order.to(torch.int32)
+    stride = int(dst.shape[-1]) if row_stride is None else int(row_stride)
+    check(lib().kb_rows_scatter_add(dtype_code(src.dtype), S, n, ptr(src), ptr(order32), ptr(keys_sorted),
+                                    ptr(dst), stride, stream(src.device)))
+
+
+def sum_rows_into(dst: torch.Tensor, src: torch.Tensor) -> None:
+    """dst += src.sum(0), in row order with float64 partial sums."""
+    n = int(src.shape[0])
+    if n == 0:
+        return
+    S = int(src.shape[1])
+    work = torch.empty(((n + 255) // 256) * S, device=src.device, dtype=torch.float64)
+    check(lib().kb_rows_sum_into(dtype_code(src.dtype), S, n, ptr(src), ptr(dst), ptr(work), stream(src.device)))

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
+#include <map>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -69,6 +71,20 @@ struct kb_plan {
   int n_levels = 0;
   std::vector<int> level_ptr;
   int* d_sched_rows = nullptr;
+  // row classes: rows with identical inputs (same leaf, or same splits over
+  // identical child classes) have identical forward outputs; the forward
+  // computes one representative per class and copies it to the others, the
+  // backward merges the adjoints of identical leaf rows (level 0)
+  std::vector<int> f_level_ptr;        // representatives per level
+  int* d_fsched = nullptr;             // representatives in level order
+  int* d_fsplit_l = nullptr;           // split children remapped to representatives
+  int* d_fsplit_r = nullptr;
+  int n_copy = 0;
+  int* d_copy_dst = nullptr;
+  int* d_copy_src = nullptr;
+  int n_cls0 = 0;                      // classes of level-0 rows
+  int* d_cls_ptr = nullptr;
+  int* d_cls_rows = nullptr;
   int* d_row_kind = nullptr;  // 1: row of a leaf wave (leaf initialisation), 0: split row
   // device tables
   int* d_parent = nullptr; int* d_c1 = nullptr; int* d_c2 = nullptr; int* d_jump = nullptr;
@@ -368,6 +384,71 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
   std::vector<int> sched(C), lfill(p->level_ptr.begin(), p->level_ptr.end() - 1);
   for (int r = 0; r < C; ++r) sched[lfill[dagd[r]]++] = r;
 
+  // ---- row classes (hash-consing in dependency order; KB_DEDUP=0 disables)
+  std::vector<int> cls(C, -1), rep;
+  {
+    const char* env = getenv("KB_DEDUP");
+    const bool dedup = !(env && env[0] == '0');
+    std::map<std::vector<int64_t>, int> ids;
+    std::vector<std::array<int64_t, 3>> trip;
+    for (int r : sched) {  // children precede parents
+      std::vector<int64_t> key;
+      if (!dedup) {
+        key = {2, r};
+      } else if (row_kind[r] || sptr[r] == sptr[r + 1]) {
+        key = {row_kind[r] ? 0 : 3, leaf[r], item[r], row_kind[r] ? 0 : r};
+      } else {
+        trip.clear();
+        for (int i = sptr[r]; i < sptr[r + 1]; ++i) {
+          int64_t a = cls[sl[i]], b = cls[sr[i]];
+          int64_t bits;
+          std::memcpy(&bits, &slsp[i], sizeof(bits));
+          trip.push_back({std::min(a, b), std::max(a, b), bits});
+        }
+        std::sort(trip.begin(), trip.end());
+        key = {1, item[r]};
+        for (auto& t3 : trip) key.insert(key.end(), t3.begin(), t3.end());
+      }
+      auto it = ids.find(key);
+      if (it == ids.end()) {
+        it = ids.emplace(std::move(key), (int)rep.size()).first;
+        rep.push_back(r);
+      }
+      cls[r] = it->second;
+    }
+  }
+  std::vector<int> fsched, fsl(NS), fsr(NS), copy_dst, copy_src;
+  p->f_level_ptr.assign(p->n_levels + 1, 0);
+  for (int r : sched)
+    if (rep[cls[r]] == r) {
+      fsched.push_back(r);
+      p->f_level_ptr[dagd[r] + 1]++;
+    } else {
+      copy_dst.push_back(r);
+      copy_src.push_back(rep[cls[r]]);
+    }
+  for (int d = 0; d < p->n_levels; ++d) p->f_level_ptr[d + 1] += p->f_level_ptr[d];
+  for (int64_t i = 0; i < NS; ++i) {
+    fsl[i] = rep[cls[sl[i]]];
+    fsr[i] = rep[cls[sr[i]]];
+  }
+  p->n_copy = (int)copy_dst.size();
+  // level-0 classes for the backward (members in increasing row order, representative first)
+  std::vector<int> cls_ptr{0}, cls_rows;
+  {
+    std::map<int, std::vector<int>> members;
+    for (int k = 0; k < (C > 0 ? p->level_ptr[1] : 0); ++k) members[cls[sched[k]]].push_back(sched[k]);
+    std::vector<std::vector<int>*> order;
+    for (auto& kv : members) order.push_back(&kv.second);
+    std::sort(order.begin(), order.end(), [](auto* x, auto* y) { return (*x)[0] < (*y)[0]; });
+    for (auto* m : order) {
+      std::sort(m->begin(), m->end());
+      cls_rows.insert(cls_rows.end(), m->begin(), m->end());
+      cls_ptr.push_back((int)cls_rows.size());
+    }
+  }
+  p->n_cls0 = (int)cls_ptr.size() - 1;
+
   int rc = 0;
   rc |= upload(&p->d_parent, parent);
   rc |= upload(&p->d_c1, c1);
@@ -392,6 +473,13 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
   rc |= upload(&p->d_unnorm, unnorm);
   rc |= upload(&p->d_root_index, root_index);
   rc |= upload(&p->d_sched_rows, sched);
+  rc |= upload(&p->d_fsched, fsched);
+  rc |= upload(&p->d_fsplit_l, fsl);
+  rc |= upload(&p->d_fsplit_r, fsr);
+  rc |= upload(&p->d_copy_dst, copy_dst);
+  rc |= upload(&p->d_copy_src, copy_src);
+  rc |= upload(&p->d_cls_ptr, cls_ptr);
+  rc |= upload(&p->d_cls_rows, cls_rows);
   rc |= upload(&p->d_pre, pre);
   rc |= upload(&p->d_pcol, pcol);
   rc |= upload(&p->d_c1pos, c1pos);
@@ -429,6 +517,8 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
                     (void*)p->lin_emc, (void*)p->lin_k1, (void*)p->lin_k2, (void*)p->E64, (void*)p->n_e_iter,
                     (void*)p->loss_terms, (void*)p->loss64, (void*)p->d_root_index,
                     (void*)p->d_sched_rows, (void*)p->d_row_kind, (void*)p->d_pre, (void*)p->d_pcol,
+                    (void*)p->d_fsched, (void*)p->d_fsplit_l, (void*)p->d_fsplit_r, (void*)p->d_copy_dst,
+                    (void*)p->d_copy_src, (void*)p->d_cls_ptr, (void*)p->d_cls_rows,
                     (void*)p->d_c1pos, (void*)p->d_c2pos, (void*)p->d_ppos, (void*)p->d_pflag, (void*)p->d_endpos,
                     (void*)p->d_tin, (void*)p->d_euler, (void*)p->c_Ebar, (void*)p->c_E, (void*)p->c_mt,
                     (void*)p->c_col})
@@ -529,19 +619,20 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
   F.item = p->d_item;
   F.leaf_state = p->d_leaf;
   F.split_ptr = p->d_split_ptr;
-  F.split_l = p->d_split_l;
-  F.split_r = p->d_split_r;
+  F.split_l = p->d_fsplit_l;
+  F.split_r = p->d_fsplit_r;
   F.split_lsp = p->d_split_lsp;
   F.pi = io->pi;
   F.pibar = io->pibar;
   F.rowmax = io->pibar_row_max;
-  F.sched_rows = p->d_sched_rows;
+  F.sched_rows = p->d_fsched;
   F.row_kind = p->d_row_kind;
   for (int d = 0; d < p->n_levels; ++d) {
     if (p->prof) KB_HIP(hipEventRecord(p->ev_fwd[2 * d], st));
-    kb::launch_fwd_wave(F, p->level_ptr[d], p->level_ptr[d + 1] - p->level_ptr[d], st);
+    kb::launch_fwd_wave(F, p->f_level_ptr[d], p->f_level_ptr[d + 1] - p->f_level_ptr[d], st);
     if (p->prof) KB_HIP(hipEventRecord(p->ev_fwd[2 * d + 1], st));
   }
+  kb::launch_copy_rows(io->pi, io->pibar, io->pibar_row_max, p->d_copy_dst, p->d_copy_src, p->n_copy, S, st);
   KB_HIP(hipGetLastError());
   kb::launch_loss(io->pi, p->d_roots, io->E, S, p->n_fam, p->loss_terms, p->loss64, io->loss, st);
   KB_HIP(hipGetLastError());
@@ -559,7 +650,7 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   p->b_nb_max = nb_max;
   p->b_poff.assign(p->n_levels + 1, 0);
   for (int d = 0; d < p->n_levels; ++d)
-    p->b_poff[d + 1] = p->b_poff[d] + std::min(nb_max, p->level_ptr[d + 1] - p->level_ptr[d]);
+    p->b_poff[d + 1] = p->b_poff[d] + std::min(nb_max, d == 0 ? p->n_cls0 : p->level_ptr[d + 1] - p->level_ptr[d]);
   p->b_n_partials = p->b_poff[p->n_levels];
   if (p->b_contrib) {
     (void)hipFree(p->b_contrib);
@@ -675,9 +766,13 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   B.contrib = p->b_contrib;
   B.sched_rows = p->d_sched_rows;
   B.row_kind = p->d_row_kind;
+  B.cls_ptr = p->d_cls_ptr;
+  B.cls_rows = p->d_cls_rows;
   for (int d = p->n_levels - 1; d >= 0; --d) {
     if (p->prof) KB_HIP(hipEventRecord(p->ev_bwd[2 * d], st));
-    const int n = p->level_ptr[d + 1] - p->level_ptr[d];
+    // level 0 (rows without splits) runs by class: one adjoint solve per class of identical rows
+    const int n = d == 0 ? p->n_cls0 : p->level_ptr[d + 1] - p->level_ptr[d];
+    B.class_mode = d == 0 ? 1 : 0;
     kb::launch_bwd_wave(B, p->level_ptr[d], n, std::min(n, p->b_nb_max), p->b_poff[d], st);
     if (p->prof) KB_HIP(hipEventRecord(p->ev_bwd[2 * d + 1], st));
   }

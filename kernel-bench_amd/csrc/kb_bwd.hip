@@ -68,55 +68,75 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
 
   for (int rr = blockIdx.x; rr < n_rows; rr += gridDim.x) {
   __syncthreads();  // LDS of the previous row is no longer read
-  const int row = P.sched_rows[first + rr];
+  const int mb = P.class_mode ? P.cls_ptr[rr] : 0;
+  const int me = P.class_mode ? P.cls_ptr[rr + 1] : 1;
+  const int row = P.class_mode ? P.cls_rows[mb] : P.sched_rows[first + rr];
   const int leaf_row = P.row_kind[row];
   const int item = P.item[row];
   const size_t cb = (size_t)item * P.const_stride;
   const size_t rb = (size_t)row * S;
   const int sb = P.split_ptr[row], se = P.split_ptr[row + 1];
 
-  // ---- 1. Pi* of this row and its adjoint: root seed or fixed-order gather
+  // ---- 1. Pi* of this row; adjoint = root seed or fixed-order gather of the
+  // staging rows.  In class mode (identical rows without splits) each member's
+  // adjoint gets its own active-mask decision and the active members' adjoints
+  // are summed: everything below is linear in the adjoint.
   float piv[CPT];
   load_row_pre<NT, CPT>(T, P.pi + rb, R0, piv, KB_NEG_INF);
   float rhs[CPT];
-  const int fam = P.root_index[row];
-  if (fam >= 0) {
-    // logsumexp2 (logspace.py:11-16) and _safe_exp2_ratio (_implicit_grad.py:21-25)
-    float lm = KB_NEG_INF;
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) lm = fmaxf(lm, piv[k]);
-    const float rmax = block_max1<NT>(lm, wA);
-    const float rms = fsafe(rmax);
-    float ls = 0.0f;
+  for (int k = 0; k < CPT; ++k) rhs[k] = 0.0f;
+  bool any_active = false;
+  float* wt = wA;  // block reductions alternate wA / wB
+  for (int mi = mb; mi < me; ++mi) {
+    const int mrow = P.class_mode ? P.cls_rows[mi] : row;
+    float mr[CPT];
+    const int fam = P.root_index[mrow];
+    if (fam >= 0) {
+      // logsumexp2 (logspace.py:11-16) and _safe_exp2_ratio (_implicit_grad.py:21-25)
+      float lm = KB_NEG_INF;
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) ls += okp[k] ? exp2f(piv[k] - rms) : 0.0f;
-    const float tot = block_sum1<NT>(ls, wB);
-    const float lse = (tot > 0.0f ? log2f(tot) : KB_NEG_INF) + rmax;
-    const float lses = fsafe(lse);
+      for (int k = 0; k < CPT; ++k) lm = fmaxf(lm, piv[k]);
+      const float rmax = block_max1<NT>(lm, wt);
+      wt = wt == wA ? wB : wA;
+      const float rms = fsafe(rmax);
+      float ls = 0.0f;
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) rhs[k] = (piv[k] == KB_NEG_INF) ? 0.0f : -exp2f(piv[k] - lses);
-  } else {
+      for (int k = 0; k < CPT; ++k) ls += okp[k] ? exp2f(piv[k] - rms) : 0.0f;
+      const float tot = block_sum1<NT>(ls, wt);
+      wt = wt == wA ? wB : wA;
+      const float lse = (tot > 0.0f ? log2f(tot) : KB_NEG_INF) + rmax;
+      const float lses = fsafe(lse);
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) rhs[k] = 0.0f;
-    const int gb = P.child_ptr[row], ge = P.child_ptr[row + 1];
-    for (int i = gb; i < ge; ++i) {
-      const int side = P.child_in[i];
-      if (!P.split_on[side >> 1]) continue;
-      const float* st = P.staging + (size_t)side * S;
+      for (int k = 0; k < CPT; ++k) mr[k] = (piv[k] == KB_NEG_INF) ? 0.0f : -exp2f(piv[k] - lses);
+    } else {
 #pragma unroll
-      for (int k = 0; k < CPT; ++k)
-        if (okp[k]) rhs[k] += st[own_pos<NT, CPT>(k)];
+      for (int k = 0; k < CPT; ++k) mr[k] = 0.0f;
+      const int gb = P.child_ptr[mrow], ge = P.child_ptr[mrow + 1];
+      for (int i = gb; i < ge; ++i) {
+        const int side = P.child_in[i];
+        if (!P.split_on[side >> 1]) continue;
+        const float* st = P.staging + (size_t)side * S;
+#pragma unroll
+        for (int k = 0; k < CPT; ++k)
+          if (okp[k]) mr[k] += st[own_pos<NT, CPT>(k)];
+      }
+    }
+    // ---- 2. active mask (the reference's rule, wave_backward.py:150-163)
+    float am = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) am = fmaxf(am, fabsf(mr[k]));
+    const float amax = block_max1<NT>(am, wt);
+    wt = wt == wA ? wB : wA;
+    const bool act_m = P.use_pruning ? (amax >= P.thr) : (amax > P.thr);
+    if (tid == 0) P.mask[mrow] = act_m ? 1 : 0;
+    if (act_m) {
+      any_active = true;
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) rhs[k] += mr[k];
     }
   }
-
-  // ---- 2. active mask (the reference's rule, wave_backward.py:150-163)
-  float am = 0.0f;
-#pragma unroll
-  for (int k = 0; k < CPT; ++k) am = fmaxf(am, fabsf(rhs[k]));
-  const float amax = block_max1<NT>(am, fam >= 0 ? wA : wB);
-  const bool active = P.use_pruning ? (amax >= P.thr) : (amax > P.thr);
-  if (tid == 0) P.mask[row] = active ? 1 : 0;
-  if (!active) {
+  if (!any_active) {
     for (int i = sb + tid; i < se; i += NT) P.split_on[i] = 0;
     continue;
   }

@@ -220,6 +220,23 @@ __global__ __launch_bounds__(NT) void fwd_row_kernel(FwdParams P, int first) {
     return;                                                                                               \
   }
 
+// One workgroup per copied row (rows of a class are identical).
+__global__ __launch_bounds__(256) void copy_rows_kernel(float* pi, float* pibar, float* rowmax, const int* dst,
+                                                        const int* src, int S) {
+  const size_t d = (size_t)dst[blockIdx.x] * S, s = (size_t)src[blockIdx.x] * S;
+  for (int j = threadIdx.x; j < S; j += 256) {
+    pi[d + j] = pi[s + j];
+    pibar[d + j] = pibar[s + j];
+  }
+  if (threadIdx.x == 0) rowmax[dst[blockIdx.x]] = rowmax[src[blockIdx.x]];
+}
+
+void launch_copy_rows(float* pi, float* pibar, float* rowmax, const int* dst, const int* src, int n, int S,
+                      hipStream_t st) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(copy_rows_kernel, dim3(n), dim3(256), 0, st, pi, pibar, rowmax, dst, src, S);
+}
+
 void launch_fwd_wave(const FwdParams& P, int first, int W, hipStream_t st) {
   if (W <= 0) return;
   const int S = P.S;

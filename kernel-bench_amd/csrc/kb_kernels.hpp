@@ -74,6 +74,9 @@ struct FwdParams {
   float* pi; float* pibar; float* rowmax;
 };
 
+// Pi / Pibar / row-max rows src[i] -> dst[i], i < n.
+void launch_copy_rows(float* pi, float* pibar, float* rowmax, const int* dst, const int* src, int n, int S,
+                      hipStream_t st);
 // Launch the rows sched_rows[first .. first + n).
 void launch_fwd_wave(const FwdParams& P, int first, int n, hipStream_t st);
 
@@ -114,6 +117,9 @@ struct BwdParams {
   float* contrib;             // [n_partials, 8, S] gradient buckets, one row per workgroup and level
   const int* sched_rows;
   const int* row_kind;
+  int class_mode;             // 1: entries are classes of identical rows (cls_ptr / cls_rows)
+  const int* cls_ptr;         // [n_classes + 1]
+  const int* cls_rows;        // member rows, representative first
 };
 
 struct EpiParams {

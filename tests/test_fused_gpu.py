@@ -70,3 +70,34 @@ def test_fused_backward_matches_oracle(name, statewise):
         print(f"  acc {nm}: normrel={kbtest.norm_rel(got, ref):.3e}")
     assert (mask == ref_mask).all()
     assert rt <= 1e-4 and rc <= 1e-4
+
+
+@pytest.mark.parametrize("name,statewise", [("1", True), ("2", None)])
+def test_row_classes_match_per_row_solve(name, statewise, monkeypatch):
+    """Computing each class of identical rows once (default) equals solving every row (KB_DEDUP=0)."""
+    from kbench.fused import FusedSolver, problem_to_captured
+    from kbench.runtime import make_static
+
+    p = kbtest.problem(name, statewise)
+    cap = problem_to_captured(p)
+    static = make_static(cap, "cuda")
+    theta = cap["inputs"]["theta"].cuda()
+    cw = cap["inputs"]["col_weights"].cuda()
+    out = []
+    for flag in ("1", "0"):
+        monkeypatch.setenv("KB_DEDUP", flag)
+        solver = FusedSolver(static, static.solver_options)
+        loss, saved = solver.run_forward(theta, cw)
+        gt, gc, info = solver.run_backward(theta, cw, saved, return_info=True)
+        torch.cuda.synchronize()
+        out.append((float(loss), saved["pi_wave"].cpu().numpy(), gt.cpu().numpy(), gc.cpu().numpy(),
+                    info["active_mask"].cpu().numpy()))
+    (l1, pi1, gt1, gc1, m1), (l0, pi0, gt0, gc0, m0) = out
+    # forward rows are bitwise equal when a class's splits come in the same order; allow rounding otherwise
+    ok, ma, mr = kbtest.compare_inf_safe(pi1, pi0)
+    print(f"  loss {l1:.9g} vs {l0:.9g}; pi max_abs={ma:.3e}; grads {kbtest.norm_rel(gt1, gt0):.3e} "
+          f"{kbtest.norm_rel(gc1, gc0):.3e}")
+    assert ok and (ma <= 1e-4 or mr <= 1e-6)
+    assert abs(l1 - l0) <= 1e-6 * abs(l0)
+    assert (m1 == m0).all()
+    assert kbtest.norm_rel(gt1, gt0) <= 1e-5 and kbtest.norm_rel(gc1, gc0) <= 1e-5

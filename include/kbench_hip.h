@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define KB_ABI_VERSION 1
+#define KB_ABI_VERSION 2
 
 #define KB_ERR_ARG (-1)    /* invalid argument / layout (reference raises ValueError) */
 #define KB_ERR_HIP (-2)    /* HIP runtime error (reference: RuntimeError) */
@@ -155,9 +155,16 @@ typedef struct kb_backward_io {
   uint8_t* active_mask;      /* optional [C] out: 1 = row active */
   double* acc_out;           /* optional [8,S] out: gradient accumulators
                                 (pD, pS, E, Ebar, E_s1, E_s2, max_coupling, col) */
+  int64_t forward_token;     /* kb_forward_token() of the forward that produced pi /
+                                pibar, or 0: with a token that is still current the
+                                split terms stored by that forward are reused instead
+                                of recomputed from pi / pibar */
 } kb_backward_io;
 
 int kb_backward(kb_plan* plan, const kb_backward_io* io, void* stream);
+
+/* Token of the last kb_forward on this plan (a counter; 0 before the first). */
+int64_t kb_forward_token(const kb_plan* plan);
 
 /* Synchronises `stream`; BiCGSTAB iteration count; KB_ERR_SOLVE if it failed. */
 int kb_backward_stats(kb_plan* plan, int32_t* n_iter, void* stream);

@@ -83,6 +83,14 @@ struct kb_plan {
   int* d_copy_dst = nullptr;
   int* d_copy_src = nullptr;
   int n_cls0 = 0;                      // classes of level-0 rows
+  int* d_rep_of = nullptr;             // [C] representative of each row
+  int* d_m_side_ptr = nullptr;         // level-0 members (cls_rows order): staging sides
+  int* d_m_side = nullptr;
+  int* d_m_root = nullptr;
+  float* d_dts = nullptr;              // [C, S] split terms stored by the forward (preorder rows)
+  int64_t fwd_token = 0;               // counter of forwards on this plan
+  const float* fwd_pi = nullptr;       // outputs of the forward with token fwd_token
+  const float* fwd_pibar = nullptr;
   int* d_cls_ptr = nullptr;
   int* d_cls_rows = nullptr;
   int* d_row_kind = nullptr;  // 1: row of a leaf wave (leaf initialisation), 0: split row
@@ -109,11 +117,15 @@ struct kb_plan {
   int64_t n_splits = 0;
   // backward work (allocated on first use)
   float* b_staging = nullptr; unsigned char* b_split_on = nullptr; unsigned char* b_mask = nullptr;
+  float* b_rhs0 = nullptr;
+  float* b_rhsc = nullptr;
+  unsigned char* b_m_mask = nullptr;
+  unsigned char* b_cls_active = nullptr;
   float* b_contrib = nullptr; double* b_partial = nullptr; double* b_acc = nullptr; double* b_work = nullptr;
   int* b_status = nullptr;
   float* b_DL = nullptr; float* b_SL1 = nullptr; float* b_SL2 = nullptr; float* b_pS = nullptr; float* b_pD = nullptr;
   float* b_Ebar = nullptr; float* b_E = nullptr; float* b_mt = nullptr; float* b_col = nullptr; double* b_acc_pre = nullptr;
-  int b_nb_max = 0, b_n_partials = 0;
+  int b_nb_max = 0, b_n_partials = 0, b_variant = 0;
   std::vector<int> b_poff;
   // optional per-launch timing of the wave kernels (HIP events on the launch stream)
   int prof = 0;
@@ -480,6 +492,21 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
   rc |= upload(&p->d_copy_src, copy_src);
   rc |= upload(&p->d_cls_ptr, cls_ptr);
   rc |= upload(&p->d_cls_rows, cls_rows);
+  {
+    std::vector<int> rep_of(C);
+    for (int r = 0; r < C; ++r) rep_of[r] = rep[cls[r]];
+    rc |= upload(&p->d_rep_of, rep_of);
+    std::vector<int> msp{0}, ms, mroot;
+    for (int r : cls_rows) {
+      for (int j = ccnt[r]; j < ccnt[r + 1]; ++j) ms.push_back(cin[j]);
+      msp.push_back((int)ms.size());
+      mroot.push_back(root_index[r]);
+    }
+    rc |= upload(&p->d_m_side_ptr, msp);
+    rc |= upload(&p->d_m_side, ms);
+    rc |= upload(&p->d_m_root, mroot);
+  }
+  rc |= alloc(&p->d_dts, (size_t)std::max(1, C) * S);
   rc |= upload(&p->d_pre, pre);
   rc |= upload(&p->d_pcol, pcol);
   rc |= upload(&p->d_c1pos, c1pos);
@@ -518,7 +545,8 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
                     (void*)p->loss_terms, (void*)p->loss64, (void*)p->d_root_index,
                     (void*)p->d_sched_rows, (void*)p->d_row_kind, (void*)p->d_pre, (void*)p->d_pcol,
                     (void*)p->d_fsched, (void*)p->d_fsplit_l, (void*)p->d_fsplit_r, (void*)p->d_copy_dst,
-                    (void*)p->d_copy_src, (void*)p->d_cls_ptr, (void*)p->d_cls_rows,
+                    (void*)p->d_copy_src, (void*)p->d_cls_ptr, (void*)p->d_cls_rows, (void*)p->d_rep_of, (void*)p->d_m_side_ptr, (void*)p->d_m_side, (void*)p->d_m_root,
+                    (void*)p->d_dts,
                     (void*)p->d_c1pos, (void*)p->d_c2pos, (void*)p->d_ppos, (void*)p->d_pflag, (void*)p->d_endpos,
                     (void*)p->d_tin, (void*)p->d_euler, (void*)p->c_Ebar, (void*)p->c_E, (void*)p->c_mt,
                     (void*)p->c_col})
@@ -603,7 +631,7 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
   F.pre = p->predev();
   {
     const char* w = getenv("KB_FWD_WIDE");
-    F.wide = (w && w[0] == '1') ? 1 : 0;
+    F.wide = (w && (w[0] == '1' || w[0] == '2')) ? w[0] - '0' : 0;
   }
   F.colw = p->c_colw;
   F.col = p->c_col;
@@ -627,6 +655,10 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
   F.rowmax = io->pibar_row_max;
   F.sched_rows = p->d_fsched;
   F.row_kind = p->d_row_kind;
+  F.dts_out = p->d_dts;
+  p->fwd_token += 1;
+  p->fwd_pi = io->pi;
+  p->fwd_pibar = io->pibar;
   for (int d = 0; d < p->n_levels; ++d) {
     if (p->prof) KB_HIP(hipEventRecord(p->ev_fwd[2 * d], st));
     kb::launch_fwd_wave(F, p->f_level_ptr[d], p->f_level_ptr[d + 1] - p->f_level_ptr[d], st);
@@ -645,13 +677,13 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   int dev = 0, n_cu = 0;
   KB_HIP(hipGetDevice(&dev));
   KB_HIP(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
-  const int nb_max = std::max(1, n_cu * kb::bwd_blocks_per_cu(S, use_col));
+  const char* vv = getenv("KB_BWD_VARIANT");
+  const int variant = (vv && vv[0] == '2') ? 2 : 0;
+  const int nb_max = std::max(1, n_cu * kb::bwd_blocks_per_cu(S, use_col, variant));
+  p->b_variant = variant;
   if (p->b_contrib && p->b_nb_max == nb_max) return 0;
   p->b_nb_max = nb_max;
-  p->b_poff.assign(p->n_levels + 1, 0);
-  for (int d = 0; d < p->n_levels; ++d)
-    p->b_poff[d + 1] = p->b_poff[d] + std::min(nb_max, d == 0 ? p->n_cls0 : p->level_ptr[d + 1] - p->level_ptr[d]);
-  p->b_n_partials = p->b_poff[p->n_levels];
+  p->b_n_partials = nb_max;  // one persistent bucket slot per workgroup of the per-level grids
   if (p->b_contrib) {
     (void)hipFree(p->b_contrib);
     (void)hipFree(p->b_partial);
@@ -671,6 +703,10 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   rc |= alloc(&p->b_staging, (size_t)std::max<int64_t>(1, 2 * NS) * S);
   rc |= alloc(&p->b_split_on, (size_t)std::max<int64_t>(1, NS));
   rc |= alloc(&p->b_mask, (size_t)std::max(1, C));
+  rc |= alloc(&p->b_rhs0, (size_t)std::max(1, C > 0 ? p->level_ptr[1] : 1) * S);
+  rc |= alloc(&p->b_rhsc, (size_t)std::max(1, p->n_cls0) * S);
+  rc |= alloc(&p->b_m_mask, (size_t)std::max(1, C > 0 ? p->level_ptr[1] : 1));
+  rc |= alloc(&p->b_cls_active, (size_t)std::max(1, p->n_cls0));
   rc |= alloc(&p->b_contrib, (size_t)std::max(1, p->b_n_partials) * 8 * S);
   rc |= alloc(&p->b_partial, (size_t)kb::reduce_chunks(std::max(1, p->b_n_partials)) * 8 * S);
   rc |= alloc(&p->b_acc, (size_t)8 * S);
@@ -688,6 +724,7 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   rc |= alloc(&p->b_acc_pre, (size_t)8 * S);
   for (void* ptr : {(void*)p->b_Ebar, (void*)p->b_E, (void*)p->b_mt, (void*)p->b_col, (void*)p->b_acc_pre,
                     (void*)p->b_staging, (void*)p->b_split_on, (void*)p->b_mask, (void*)p->b_contrib,
+                    (void*)p->b_rhs0, (void*)p->b_rhsc, (void*)p->b_cls_active, (void*)p->b_m_mask,
                     (void*)p->b_partial, (void*)p->b_acc, (void*)p->b_work, (void*)p->b_status, (void*)p->b_DL,
                     (void*)p->b_SL1, (void*)p->b_SL2, (void*)p->b_pS, (void*)p->b_pD})
     p->owned.push_back(ptr);
@@ -766,14 +803,29 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   B.contrib = p->b_contrib;
   B.sched_rows = p->d_sched_rows;
   B.row_kind = p->d_row_kind;
+  B.variant = p->b_variant;
+  B.rhs0 = p->b_rhs0;
+  B.rhsc = p->b_rhsc;
+  B.m_side_ptr = p->d_m_side_ptr;
+  B.m_side = p->d_m_side;
+  B.m_root = p->d_m_root;
+  B.m_mask = p->b_m_mask;
+  B.cls_active = p->b_cls_active;
+  // reuse the forward's split terms only for the outputs of the current forward
+  const bool reuse = io->forward_token != 0 && io->forward_token == p->fwd_token && io->pi == p->fwd_pi &&
+                     io->pibar == p->fwd_pibar;
+  B.dts_in = reuse ? p->d_dts : nullptr;
+  B.rep_of = p->d_rep_of;
   B.cls_ptr = p->d_cls_ptr;
   B.cls_rows = p->d_cls_rows;
+  kb::launch_fill_zero(p->b_contrib, (size_t)p->b_n_partials * 8 * S, st);
   for (int d = p->n_levels - 1; d >= 0; --d) {
     if (p->prof) KB_HIP(hipEventRecord(p->ev_bwd[2 * d], st));
     // level 0 (rows without splits) runs by class: one adjoint solve per class of identical rows
     const int n = d == 0 ? p->n_cls0 : p->level_ptr[d + 1] - p->level_ptr[d];
     B.class_mode = d == 0 ? 1 : 0;
-    kb::launch_bwd_wave(B, p->level_ptr[d], n, std::min(n, p->b_nb_max), p->b_poff[d], st);
+    if (d == 0) kb::launch_bwd_level0_prep(B, p->level_ptr[1], p->n_cls0, st);
+    kb::launch_bwd_wave(B, p->level_ptr[d], n, std::min(n, p->b_nb_max), 0, st);
     if (p->prof) KB_HIP(hipEventRecord(p->ev_bwd[2 * d + 1], st));
   }
   KB_HIP(hipGetLastError());
@@ -813,6 +865,8 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   KB_HIP(hipGetLastError());
   return 0;
 }
+
+int64_t kb_forward_token(const kb_plan* p) { return p ? p->fwd_token : 0; }
 
 int kb_backward_stats(kb_plan* p, int32_t* n_iter, void* stream) {
   if (!p) return set_error(KB_ERR_ARG, "null argument");

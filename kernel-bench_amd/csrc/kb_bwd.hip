@@ -23,6 +23,8 @@
 // layout); a child row gathers its staging rows in increasing split order,
 // and every per-row gradient bucket is stored and reduced over rows in a fixed
 // order, so results are bitwise reproducible.
+#include <algorithm>
+
 #include "kb_device.hpp"
 #include "kb_kernels.hpp"
 #include "kb_rowops.hpp"
@@ -87,54 +89,48 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
 #pragma unroll
   for (int k = 0; k < CPT; ++k) rhs[k] = 0.0f;
   bool any_active = false;
-  float* wt = wA;  // block reductions alternate wA / wB
-  for (int mi = mb; mi < me; ++mi) {
-    const int mrow = P.class_mode ? P.cls_rows[mi] : row;
-    float mr[CPT];
-    const int fam = P.root_index[mrow];
+  if (P.class_mode) {
+    // the summed adjoint of the class's active members (bwd_gather0 / bwd_classsum0)
+    any_active = P.cls_active[rr] != 0;
+    const float* src = P.rhsc + (size_t)rr * S;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k)
+      if (okp[k]) rhs[k] = src[own_pos<NT, CPT>(k)];
+  } else {
+    const int fam = P.root_index[row];
     if (fam >= 0) {
       // logsumexp2 (logspace.py:11-16) and _safe_exp2_ratio (_implicit_grad.py:21-25)
       float lm = KB_NEG_INF;
 #pragma unroll
       for (int k = 0; k < CPT; ++k) lm = fmaxf(lm, piv[k]);
-      const float rmax = block_max1<NT>(lm, wt);
-      wt = wt == wA ? wB : wA;
+      const float rmax = block_max1<NT>(lm, wA);
       const float rms = fsafe(rmax);
       float ls = 0.0f;
 #pragma unroll
       for (int k = 0; k < CPT; ++k) ls += okp[k] ? exp2f(piv[k] - rms) : 0.0f;
-      const float tot = block_sum1<NT>(ls, wt);
-      wt = wt == wA ? wB : wA;
+      const float tot = block_sum1<NT>(ls, wB);
       const float lse = (tot > 0.0f ? log2f(tot) : KB_NEG_INF) + rmax;
       const float lses = fsafe(lse);
 #pragma unroll
-      for (int k = 0; k < CPT; ++k) mr[k] = (piv[k] == KB_NEG_INF) ? 0.0f : -exp2f(piv[k] - lses);
+      for (int k = 0; k < CPT; ++k) rhs[k] = (piv[k] == KB_NEG_INF) ? 0.0f : -exp2f(piv[k] - lses);
     } else {
-#pragma unroll
-      for (int k = 0; k < CPT; ++k) mr[k] = 0.0f;
-      const int gb = P.child_ptr[mrow], ge = P.child_ptr[mrow + 1];
+      const int gb = P.child_ptr[row], ge = P.child_ptr[row + 1];
       for (int i = gb; i < ge; ++i) {
         const int side = P.child_in[i];
         if (!P.split_on[side >> 1]) continue;
         const float* st = P.staging + (size_t)side * S;
 #pragma unroll
         for (int k = 0; k < CPT; ++k)
-          if (okp[k]) mr[k] += st[own_pos<NT, CPT>(k)];
+          if (okp[k]) rhs[k] += st[own_pos<NT, CPT>(k)];
       }
     }
     // ---- 2. active mask (the reference's rule, wave_backward.py:150-163)
     float am = 0.0f;
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) am = fmaxf(am, fabsf(mr[k]));
-    const float amax = block_max1<NT>(am, wt);
-    wt = wt == wA ? wB : wA;
-    const bool act_m = P.use_pruning ? (amax >= P.thr) : (amax > P.thr);
-    if (tid == 0) P.mask[mrow] = act_m ? 1 : 0;
-    if (act_m) {
-      any_active = true;
-#pragma unroll
-      for (int k = 0; k < CPT; ++k) rhs[k] += mr[k];
-    }
+    for (int k = 0; k < CPT; ++k) am = fmaxf(am, fabsf(rhs[k]));
+    const float amax = block_max1<NT>(am, fam >= 0 ? wA : wB);
+    any_active = P.use_pruning ? (amax >= P.thr) : (amax > P.thr);
+    if (tid == 0) P.mask[row] = any_active ? 1 : 0;
   }
   if (!any_active) {
     for (int i = sb + tid; i < se; i += NT) P.split_on[i] = 0;
@@ -146,7 +142,12 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   float dts[CPT];
 #pragma unroll
   for (int k = 0; k < CPT; ++k) dts[k] = KB_NEG_INF;
-  if (!leaf_row) {
+  if (!leaf_row && P.dts_in) {
+    const float* src = P.dts_in + (size_t)P.rep_of[row] * S;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k)
+      if (okp[k]) dts[k] = src[own_pos<NT, CPT>(k)];
+  } else if (!leaf_row) {
     float m[CPT], acc[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
@@ -420,13 +421,14 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
 
   }  // rows
 
-  // one partial per workgroup (preorder layout; reduced over partials later)
-  float* cr = P.contrib + (size_t)(poff + blockIdx.x) * 8 * S;
+  // add into this workgroup's bucket slot (preorder layout): slot b is updated
+  // by workgroup b of every level in turn, so the summation order is fixed
+  float* cr = P.contrib + (size_t)blockIdx.x * 8 * S;
 #pragma unroll
   for (int j = 0; j < 8; ++j)
 #pragma unroll
     for (int k = 0; k < CPT; ++k)
-      if (okp[k]) cr[(size_t)j * S + own_pos<NT, CPT>(k)] = cacc[j][k];
+      if (okp[k]) cr[(size_t)j * S + own_pos<NT, CPT>(k)] += cacc[j][k];
 }
 
 #define KB_BWD_CASE(NT_, CPT_)                                                                      \
@@ -438,9 +440,120 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     return;                                                                                         \
   }
 
+// Level-0 rows, in two passes:
+//  gather0   one workgroup per member: adjoint row (root seed or fixed-order
+//            gather of its live staging rows; the side lists are static,
+//            m_side_ptr / m_side in member order) in preorder positions, and
+//            its active mask (in member order, m_mask, and per row, mask);
+//  classsum0 per (class, 256-position block): the sum in member order of the
+//            class's active members' rows.
+constexpr int G0_E = 8;  // positions per thread per pass of gather0
+
+__global__ __launch_bounds__(256) void bwd_gather0_kernel(BwdParams P) {
+  __shared__ float red[4];
+  const PreDev& T = P.pre;
+  const int S = P.S;
+  const int mi = blockIdx.x;
+  const int row = P.cls_rows[mi];
+  const int sb = P.m_side_ptr[mi], se = P.m_side_ptr[mi + 1];
+  float* out = P.rhs0 + (size_t)mi * S;
+  float am = 0.0f;
+  if (P.m_root[mi] >= 0) {
+    // root seed: -2^(Pi - logsumexp2(Pi)) (logspace.py:11-16, _implicit_grad.py:21-25)
+    const float* pr = P.pi + (size_t)row * S;
+    float lm = KB_NEG_INF;
+    for (int j = threadIdx.x; j < S; j += 256) lm = fmaxf(lm, pr[j]);
+    const float rmax = block_max<256>(lm, red);
+    const float rms = fsafe(rmax);
+    float ls = 0.0f;
+    for (int j = threadIdx.x; j < S; j += 256) ls += exp2f(pr[j] - rms);
+    const float tot = block_sum<256>(ls, red);
+    const float lses = fsafe((tot > 0.0f ? log2f(tot) : KB_NEG_INF) + rmax);
+    for (int i = threadIdx.x; i < S; i += 256) {
+      const float x = pr[T.col[i]];
+      const float r = x == KB_NEG_INF ? 0.0f : -exp2f(x - lses);
+      out[i] = r;
+      am = fmaxf(am, fabsf(r));
+    }
+  } else {
+    for (int base = 0; base < S; base += 256 * G0_E) {
+      float r[G0_E];
+#pragma unroll
+      for (int e = 0; e < G0_E; ++e) r[e] = 0.0f;
+      for (int j = sb; j < se; ++j) {
+        const int side = P.m_side[j];
+        if (!P.split_on[side >> 1]) continue;  // uniform across the workgroup
+        const float* st = P.staging + (size_t)side * S;
+#pragma unroll
+        for (int e = 0; e < G0_E; ++e) {
+          const int i = base + e * 256 + threadIdx.x;
+          if (i < S) r[e] += st[i];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < G0_E; ++e) {
+        const int i = base + e * 256 + threadIdx.x;
+        if (i < S) {
+          out[i] = r[e];
+          am = fmaxf(am, fabsf(r[e]));
+        }
+      }
+    }
+  }
+  const float amax = block_max<256>(am, red);
+  if (threadIdx.x == 0) {
+    const unsigned char on = (P.use_pruning ? (amax >= P.thr) : (amax > P.thr)) ? 1 : 0;
+    P.mask[row] = on;
+    P.m_mask[mi] = on;
+  }
+}
+
+__global__ __launch_bounds__(256) void bwd_classsum0_kernel(BwdParams P) {
+  __shared__ unsigned char on[256];
+  const int c = blockIdx.x;
+  const int S = P.S;
+  const int i = blockIdx.y * 256 + threadIdx.x;
+  const int mb = P.cls_ptr[c], me = P.cls_ptr[c + 1];
+  float acc = 0.0f;
+  int any = 0;
+  for (int m0 = mb; m0 < me; m0 += 256) {
+    const int n = min(256, me - m0);
+    __syncthreads();
+    if (threadIdx.x < n) on[threadIdx.x] = P.m_mask[m0 + threadIdx.x];
+    __syncthreads();
+    for (int j = 0; j < n; ++j) {
+      if (!on[j]) continue;
+      any = 1;
+      if (i < S) acc += P.rhs0[(size_t)(m0 + j) * S + i];
+    }
+  }
+  if (i < S) P.rhsc[(size_t)c * S + i] = acc;
+  if (blockIdx.y == 0 && threadIdx.x == 0) P.cls_active[c] = any ? 1 : 0;
+}
+
+void launch_bwd_level0_prep(const BwdParams& P, int n_members, int n_cls, hipStream_t st) {
+  if (n_members <= 0) return;
+  const int nblk = (P.S + 255) / 256;
+  hipLaunchKernelGGL(bwd_gather0_kernel, dim3(n_members), dim3(256), 0, st, P);
+  hipLaunchKernelGGL(bwd_classsum0_kernel, dim3(n_cls, nblk), dim3(256), 0, st, P);
+}
+
+__global__ __launch_bounds__(256) void fill_zero_kernel(float* p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = 0.0f;
+}
+
+void launch_fill_zero(float* p, size_t n, hipStream_t st) {
+  if (n == 0) return;
+  const int blocks = (int)std::min<size_t>(4096, (n + 255) / 256);
+  hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks), dim3(256), 0, st, p, n);
+}
+
 void launch_bwd_wave(const BwdParams& P, int first, int W, int nb, int poff, hipStream_t st) {
   if (W <= 0 || nb <= 0) return;
   const int S = P.S;
+  if (P.variant == 2) {
+    KB_BWD_CASE(1024, 2)
+  }
   KB_BWD_CASE(64, 2)
   KB_BWD_CASE(128, 2)
   KB_BWD_CASE(256, 2)
@@ -460,7 +573,10 @@ void launch_bwd_wave(const BwdParams& P, int first, int W, int nb, int poff, hip
     return n > 0 ? n : 1;                                                                              \
   }
 
-int bwd_blocks_per_cu(int S, int use_col) {
+int bwd_blocks_per_cu(int S, int use_col, int variant) {
+  if (variant == 2) {
+    KB_BWD_OCC(1024, 2)
+  }
   KB_BWD_OCC(64, 2)
   KB_BWD_OCC(128, 2)
   KB_BWD_OCC(256, 2)
@@ -498,7 +614,7 @@ void launch_bwd_consts(const BwdConstArgs& A, hipStream_t st) {
 // ---- column sums of the per-row buckets over active rows, fixed order.
 // Stage 1: chunk c of rows -> partial[c][8*S]; stage 2: sum of chunks.
 // The result is in preorder-position order: out[j*S + pre(s)].
-constexpr int RED_CHUNK = 256;
+constexpr int RED_CHUNK = 16;
 
 __global__ void bwd_reduce_stage1(const float* contrib, int C, int S, double* partial) {
   const int j = blockIdx.x * blockDim.x + threadIdx.x;  // index in [0, 8S)

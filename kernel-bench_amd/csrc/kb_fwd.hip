@@ -28,7 +28,7 @@
 namespace kb {
 
 template <int NT, int CPT, bool WEIGHTED>
-__global__ __launch_bounds__(NT) void fwd_row_kernel(FwdParams P, int first) {
+__global__ __launch_bounds__(NT, (NT == 1024 && CPT == 2) ? 8 : 1) void fwd_row_kernel(FwdParams P, int first) {
   constexpr int MAXS = NT * CPT;
   constexpr int NW = NT / 64;
   __shared__ float Xs[2][MAXS + 64];   // unnormalised y of the sweep (double buffer); [MAXS] == 0
@@ -129,6 +129,12 @@ __global__ __launch_bounds__(NT) void fwd_row_kernel(FwdParams P, int first) {
     }
 #pragma unroll
     for (int k = 0; k < CPT; ++k) v[k] = log2f(acc[k]) + m[k];
+    if (P.dts_out) {  // the backward reuses the split term at Pi*
+      float* dst = P.dts_out + (size_t)row * S;
+#pragma unroll
+      for (int k = 0; k < CPT; ++k)
+        if (own_pos<NT, CPT>(k) < S) dst[own_pos<NT, CPT>(k)] = v[k];
+    }
   }
 
   // ---- linear space relative to the row maximum
@@ -224,9 +230,22 @@ __global__ __launch_bounds__(NT) void fwd_row_kernel(FwdParams P, int first) {
 __global__ __launch_bounds__(256) void copy_rows_kernel(float* pi, float* pibar, float* rowmax, const int* dst,
                                                         const int* src, int S) {
   const size_t d = (size_t)dst[blockIdx.x] * S, s = (size_t)src[blockIdx.x] * S;
-  for (int j = threadIdx.x; j < S; j += 256) {
-    pi[d + j] = pi[s + j];
-    pibar[d + j] = pibar[s + j];
+  for (int j0 = threadIdx.x; j0 < S; j0 += 4 * 256) {  // 8 independent loads in flight per thread
+    float a[4], b[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j = j0 + u * 256;
+      a[u] = j < S ? pi[s + j] : 0.0f;
+      b[u] = j < S ? pibar[s + j] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j = j0 + u * 256;
+      if (j < S) {
+        pi[d + j] = a[u];
+        pibar[d + j] = b[u];
+      }
+    }
   }
   if (threadIdx.x == 0) rowmax[dst[blockIdx.x]] = rowmax[src[blockIdx.x]];
 }
@@ -240,8 +259,11 @@ void launch_copy_rows(float* pi, float* pibar, float* rowmax, const int* dst, co
 void launch_fwd_wave(const FwdParams& P, int first, int W, hipStream_t st) {
   if (W <= 0) return;
   const int S = P.S;
-  if (P.wide > 0) {  // fewer, wider threads per row (tuning knob)
+  if (P.wide == 1) {  // fewer, wider threads per row (tuning knob)
     KB_FWD_CASE(256, 8)
+  }
+  if (P.wide == 2) {  // more, narrower threads per row (tuning knob)
+    KB_FWD_CASE(1024, 2)
   }
   KB_FWD_CASE(64, 2)
   KB_FWD_CASE(128, 2)

@@ -72,6 +72,7 @@ struct FwdParams {
   const int* row_kind;        // 1: leaf row, 0: split row
   // outputs
   float* pi; float* pibar; float* rowmax;
+  float* dts_out;             // [C, S] preorder split term of every computed split row
 };
 
 // Pi / Pibar / row-max rows src[i] -> dst[i], i < n.
@@ -118,6 +119,16 @@ struct BwdParams {
   const int* sched_rows;
   const int* row_kind;
   int class_mode;             // 1: entries are classes of identical rows (cls_ptr / cls_rows)
+  int variant;                // launch shape: 0 default, 2 narrow (1024 threads x 2 states)
+  float* rhs0;                // [rows of level 0, S] preorder adjoint rows, in cls_rows order
+  float* rhsc;                // [classes of level 0, S] summed adjoint of each class
+  const int* m_side_ptr;      // [members + 1] staging sides of each level-0 member (cls_rows order)
+  const int* m_side;
+  const int* m_root;          // [members] family of a member that is a root row, else -1
+  unsigned char* m_mask;      // [members] active mask in member order
+  unsigned char* cls_active;  // [classes of level 0] any member active
+  const float* dts_in;        // [C, S] preorder split terms stored by the forward, or null: recompute
+  const int* rep_of;          // [C] row -> row whose stored split term it shares
   const int* cls_ptr;         // [n_classes + 1]
   const int* cls_rows;        // member rows, representative first
 };
@@ -150,7 +161,10 @@ void launch_bwd_consts(const BwdConstArgs& A, hipStream_t st);
 // Rows sched_rows[first .. first + n) on nb workgroups (round-robin); partial
 // bucket rows poff .. poff + nb.
 void launch_bwd_wave(const BwdParams& P, int first, int n, int nb, int poff, hipStream_t st);
-int bwd_blocks_per_cu(int S, int use_col);
+int bwd_blocks_per_cu(int S, int use_col, int variant);
+// Level-0 adjoint rows, masks and class sums.
+void launch_bwd_level0_prep(const BwdParams& P, int n_members, int n_cls, hipStream_t st);
+void launch_fill_zero(float* p, size_t n, hipStream_t st);
 void launch_bwd_reduce(const float* contrib, int C, int S, double* partial, double* out, hipStream_t st);
 void launch_bwd_unpermute(const double* in, const int* pre, int S, double* out, hipStream_t st);
 int reduce_chunks(int C);

@@ -12,7 +12,7 @@ import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libkbench_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib = None
 _load_error: str | None = None
@@ -70,7 +70,7 @@ class KbBackwardIO(ct.Structure):
         ("log_pS", vp), ("log_pD", vp), ("log_pL", vp), ("max_coupling", vp), ("col_log_probs", vp),
         ("pi", vp), ("pibar", vp), ("pibar_row_max", vp),
         ("grad_theta", vp), ("grad_col", vp),
-        ("active_mask", vp), ("acc_out", vp),
+        ("active_mask", vp), ("acc_out", vp), ("forward_token", i64),
     ]
 
 
@@ -94,6 +94,8 @@ def _declare(lib):
     lib.kb_profile_enable.restype = ct.c_int
     lib.kb_profile_read.argtypes = [vp, ct.c_int, P_f32, ct.c_int]
     lib.kb_profile_read.restype = ct.c_int
+    lib.kb_forward_token.argtypes = [vp]
+    lib.kb_forward_token.restype = ct.c_int64
     if hasattr(lib, "kb_backward_stats"):
         lib.kb_backward_stats.argtypes = [vp, P_i32, vp]
         lib.kb_backward_stats.restype = ct.c_int

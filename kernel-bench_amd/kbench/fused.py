@@ -40,6 +40,11 @@ _SOLVER_DEFAULTS = {
 }
 
 
+def _ident(t):
+    """(address, shape, version) of a tensor: equal while it is the same unmodified storage."""
+    return (int(t.data_ptr()), tuple(t.shape), int(t._version))
+
+
 def _np(x, dtype=None):
     if torch.is_tensor(x):
         x = x.detach().cpu().numpy()
@@ -212,6 +217,8 @@ class FusedSolver:
         )
         with torch.cuda.device(dev):
             N.check(N.lib().kb_forward(self._plan, ct.byref(io), N.stream_handle(dev)))
+        # the backward may reuse this forward's stored split terms while pi / pibar are unchanged
+        self._last_forward = (int(N.lib().kb_forward_token(self._plan)), _ident(pi), _ident(pibar))
         if not self.statewise:
             pS, pD, pL = (t.reshape(()) for t in (pS, pD, pL))
         saved = dict(zip(FORWARD_SAVED_NAMES, (
@@ -295,6 +302,11 @@ class FusedSolver:
             pi=N.ptr(tens["pi_wave"]), pibar=N.ptr(tens["pibar_wave"]), pibar_row_max=N.ptr(tens["pibar_row_max"]),
             grad_theta=N.ptr(grad_theta), grad_col=N.ptr(grad_col), active_mask=N.ptr(mask), acc_out=N.ptr(acc),
         )
+        token = 0
+        last = getattr(self, "_last_forward", None)
+        if last is not None and last[1] == _ident(tens["pi_wave"]) and last[2] == _ident(tens["pibar_wave"]):
+            token = last[0]
+        io.forward_token = token
         self._keep = (tens, theta_d, cw)
         with torch.cuda.device(dev):
             N.check(lib.kb_backward(self._plan, ct.byref(io), N.stream_handle(dev)))

@@ -101,3 +101,20 @@ def test_row_classes_match_per_row_solve(name, statewise, monkeypatch):
     assert abs(l1 - l0) <= 1e-6 * abs(l0)
     assert (m1 == m0).all()
     assert kbtest.norm_rel(gt1, gt0) <= 1e-5 and kbtest.norm_rel(gc1, gc0) <= 1e-5
+
+
+def test_backward_reuses_forward_split_terms_only_when_valid():
+    """The backward reuses the forward's stored split terms for that forward's own outputs, and
+    recomputes them from pi / pibar otherwise (copies, or outputs of an older forward)."""
+    solver, static, theta, cw, loss, saved = _run_fused_forward("1", True)
+    g_reuse = solver.run_backward(theta, cw, saved)
+    other = dict(saved)
+    other["pi_wave"] = saved["pi_wave"].clone()
+    other["pibar_wave"] = saved["pibar_wave"].clone()
+    g_recompute = solver.run_backward(theta, cw, other)
+    _, saved2 = solver.run_forward(theta * 1.01, cw)      # a newer forward on the same plan
+    g_old = solver.run_backward(theta, cw, saved)         # must not use the newer split terms
+    torch.cuda.synchronize()
+    for a, b, c in zip(g_reuse, g_recompute, g_old):
+        assert kbtest.norm_rel(a.cpu().numpy(), b.cpu().numpy()) <= 1e-6
+        assert kbtest.norm_rel(a.cpu().numpy(), c.cpu().numpy()) <= 1e-6

@@ -112,6 +112,8 @@ struct kb_plan {
   // preorder tables (see kb_rowops.hpp)
   int* d_pre = nullptr; int* d_pcol = nullptr; int* d_c1pos = nullptr; int* d_c2pos = nullptr; int* d_ppos = nullptr;
   int* d_pflag = nullptr; int* d_endpos = nullptr; int* d_tin = nullptr; int* d_euler = nullptr;
+  int* d_euler_col = nullptr; int* d_tin_col = nullptr;  // the Euler tour in column terms
+  kb::TreeScanDev tscan() const { return kb::TreeScanDev{S, d_pre, d_endpos, d_euler_col, d_tin_col}; }
   double* E64 = nullptr; int* n_e_iter = nullptr; double* loss_terms = nullptr; double* loss64 = nullptr;
   int* d_root_index = nullptr;
   int64_t n_splits = 0;
@@ -516,6 +518,13 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
   rc |= upload(&p->d_endpos, endpos);
   rc |= upload(&p->d_tin, tin);
   rc |= upload(&p->d_euler, euler);
+  {
+    std::vector<int> ecol(euler.size()), tcol(S);
+    for (size_t q = 0; q < euler.size(); ++q) ecol[q] = (pcol[euler[q] >> 1] << 1) | (euler[q] & 1);
+    for (int s = 0; s < S; ++s) tcol[s] = tin[pre[s]];
+    rc |= upload(&p->d_euler_col, ecol);
+    rc |= upload(&p->d_tin_col, tcol);
+  }
   rc |= alloc(&p->c_Ebar, S);
   rc |= alloc(&p->c_E, S);
   rc |= alloc(&p->c_mt, S);
@@ -548,7 +557,7 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
                     (void*)p->d_copy_src, (void*)p->d_cls_ptr, (void*)p->d_cls_rows, (void*)p->d_rep_of, (void*)p->d_m_side_ptr, (void*)p->d_m_side, (void*)p->d_m_root,
                     (void*)p->d_dts,
                     (void*)p->d_c1pos, (void*)p->d_c2pos, (void*)p->d_ppos, (void*)p->d_pflag, (void*)p->d_endpos,
-                    (void*)p->d_tin, (void*)p->d_euler, (void*)p->c_Ebar, (void*)p->c_E, (void*)p->c_mt,
+                    (void*)p->d_tin, (void*)p->d_euler, (void*)p->d_euler_col, (void*)p->d_tin_col, (void*)p->c_Ebar, (void*)p->c_E, (void*)p->c_mt,
                     (void*)p->c_col})
     p->owned.push_back(ptr);
   if (rc) {
@@ -577,6 +586,7 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
 
   kb::EStepParams E{};
   E.tr = p->tree();
+  E.ts = p->tscan();
   E.S = S;
   E.n_tlevels = p->n_tlevels;
   E.tlevel_ptr = p->d_tlevel_ptr;
@@ -837,6 +847,7 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
 
   kb::EpiParams X{};
   X.tr = p->tree();
+  X.ts = p->tscan();
   X.S = S;
   X.n_tlevels = p->n_tlevels;
   X.tlevel_ptr = p->d_tlevel_ptr;

@@ -83,6 +83,74 @@ __device__ __forceinline__ T block_max(T v, T* red) {
   return r;
 }
 
+// ---- float64 tree sums by prefix scans (depth-independent) -------------------
+// Preorder and Euler-tour tables in column terms: every subtree is the
+// preorder range [pre(s), endpos[pre(s)]); the Euler tour lists (column << 1)
+// on entry and (column << 1) | 1 on exit, tin_col[s] is the entry event.
+struct TreeScanDev {
+  int S;
+  const int* pre;        // [S] column -> preorder position
+  const int* endpos;     // [S] position -> exclusive end of its subtree
+  const int* euler_col;  // [2S]
+  const int* tin_col;    // [S]
+};
+
+// In-place inclusive scan of a[0, n) (LDS); contiguous chunk per thread.
+// The writers of a[] must have passed a barrier; ends with a barrier.
+template <int NT>
+__device__ void scan_incl_f64(double* a, int n, double* red) {
+  const int c = (n + NT - 1) / NT;
+  const int b = min(n, (int)threadIdx.x * c), e = min(n, b + c);
+  double s = 0.0;
+  for (int i = b; i < e; ++i) s += a[i];
+  double inc = s;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const double y = __shfl_up(inc, o, 64);
+    if ((int)(threadIdx.x & 63) >= o) inc += y;
+  }
+  if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = inc;
+  __syncthreads();
+  double run = inc - s;
+  for (int w = 0; w < (int)(threadIdx.x >> 6); ++w) run += red[w];
+  for (int i = b; i < e; ++i) {
+    run += a[i];
+    a[i] = run;
+  }
+  __syncthreads();
+}
+
+// Ancestors-or-self path sums of x[] in place (column order, LDS, published);
+// scan2: LDS scratch of 2S doubles.
+template <int NT>
+__device__ void euler_path_sums_f64(const TreeScanDev& t, double* x, double* scan2, double* red) {
+  const int S = t.S;
+  for (int q = threadIdx.x; q < 2 * S; q += NT) {
+    const int e = t.euler_col[q];
+    const double v = x[e >> 1];
+    scan2[q] = (e & 1) ? -v : v;
+  }
+  __syncthreads();
+  scan_incl_f64<NT>(scan2, 2 * S, red);
+  for (int s = threadIdx.x; s < S; s += NT) x[s] = scan2[t.tin_col[s]];
+  __syncthreads();
+}
+
+// Descendants-or-self (subtree) sums of u[] in place (column order, LDS,
+// published); tmp: LDS scratch of S doubles.
+template <int NT>
+__device__ void preorder_subtree_sums_f64(const TreeScanDev& t, double* u, double* tmp, double* red) {
+  const int S = t.S;
+  for (int s = threadIdx.x; s < S; s += NT) tmp[t.pre[s]] = u[s];
+  __syncthreads();
+  scan_incl_f64<NT>(tmp, S, red);
+  for (int s = threadIdx.x; s < S; s += NT) {
+    const int p = t.pre[s], e = t.endpos[p];
+    u[s] = tmp[e - 1] - (p > 0 ? tmp[p - 1] : 0.0);
+  }
+  __syncthreads();
+}
+
 // Ancestors-or-self path sums of `val` (already in LDS buffer a[]).
 // Uses a[] and b[] as ping-pong buffers; returns the buffer holding the result.
 // Caller must __syncthreads() after writing a[] and before calling.

@@ -18,8 +18,9 @@ constexpr int XNT = 1024;
 struct EpiCtx {
   const EpiParams* P;
   double* red;
-  double* X;  // LDS [S]
-  double* U;  // LDS [S]
+  double* X;      // LDS [S]
+  double* U;      // LDS [S]
+  double* scan2;  // LDS [2S] (Euler / preorder scans), null: sums by levels
 };
 
 __device__ __forceinline__ void levels_path_inplace(const EpiParams& P, double* v) {
@@ -43,6 +44,20 @@ __device__ __forceinline__ void levels_subtree_inplace(const EpiParams& P, doubl
     }
     __syncthreads();
   }
+}
+
+__device__ __forceinline__ void path_inplace(const EpiCtx& c, double* v) {
+  if (c.scan2)
+    euler_path_sums_f64<1024>(c.P->ts, v, c.scan2, c.red);
+  else
+    levels_path_inplace(*c.P, v);
+}
+
+__device__ __forceinline__ void subtree_inplace(const EpiCtx& c, double* u) {
+  if (c.scan2)
+    preorder_subtree_sums_f64<1024>(c.P->ts, u, c.scan2, c.red);
+  else
+    levels_subtree_inplace(*c.P, u);
 }
 
 // work-vector slots ([S] float64 each)
@@ -96,7 +111,7 @@ __device__ void estep_vjp(const EpiCtx& c, const double* gnew, const double* gs1
     c.U[s] = (g * W2[s] + (gebar ? gebar[s] : 0.0)) * ID[s];
   }
   __syncthreads();
-  levels_subtree_inplace(P, c.U);
+  subtree_inplace(c, c.U);
   for (int s = threadIdx.x; s < S; s += XNT) {
     const double pv = R[s] * (tot - c.U[s]);
     gE[s] += pv;
@@ -123,7 +138,8 @@ __global__ __launch_bounds__(XNT) void epilogue_kernel(EpiParams P) {
   __shared__ double X[MAXS];
   __shared__ double U[MAXS];
   __shared__ double red[XNT / 64];
-  EpiCtx c{&P, red, X, U};
+  __shared__ double scan2[MAXS <= 4096 ? 2 * MAXS : 1];
+  EpiCtx c{&P, red, X, U, MAXS <= 4096 ? scan2 : nullptr};
   const int S = P.S;
   const int tid = threadIdx.x;
   const double NINF = -__builtin_inf();
@@ -158,7 +174,7 @@ __global__ __launch_bounds__(XNT) void epilogue_kernel(EpiParams P) {
     ls += r;
   }
   const double rowsum = block_sum<XNT>(ls, red);
-  levels_path_inplace(P, U);
+  path_inplace(c, U);
   for (int s = tid; s < S; s += XNT) {
     const int a1 = P.tr.c1[s], a2 = P.tr.c2[s];
     const double E = X[s];
@@ -334,13 +350,13 @@ __global__ __launch_bounds__(XNT) void epilogue_kernel(EpiParams P) {
   const double logz = wmax + log(zsum);
   for (int s = tid; s < S; s += XNT) U[s] = exp2(((double)P.col_weights[s] - logz) / LN2);
   __syncthreads();
-  levels_path_inplace(P, U);
+  path_inplace(c, U);
   for (int s = tid; s < S; s += XNT) {
     const double valid = 1.0 - U[s];
     X[s] = (valid > 0.0 && valid >= TINY) ? G_mt[s] / valid : 0.0;
   }
   __syncthreads();
-  levels_subtree_inplace(P, X);
+  subtree_inplace(c, X);
   double lg = 0.0;
   for (int s = tid; s < S; s += XNT) {
     const double pc = exp2(((double)P.col_weights[s] - logz) / LN2);

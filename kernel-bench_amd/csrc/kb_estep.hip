@@ -32,11 +32,21 @@ __device__ __forceinline__ void path_sum_levels_inplace(const EStepParams& P, do
 
 constexpr int ENT = 1024;
 
+// Path sums in place: one Euler-tour scan when its scratch fits in LDS, else by levels.
+template <int EMAXS>
+__device__ __forceinline__ void path_sums(const EStepParams& P, double* v, double* scan2, double* red) {
+  if constexpr (EMAXS <= 4096)
+    euler_path_sums_f64<ENT>(P.ts, v, scan2, red);
+  else
+    path_sum_levels_inplace<ENT>(P, v);
+}
+
 template <int EMAXS>
 __global__ __launch_bounds__(ENT) void estep_fixed_point_kernel(EStepParams P) {
   constexpr int ECPT = EMAXS / ENT;
   __shared__ double ev[EMAXS];
   __shared__ double pv[EMAXS];
+  __shared__ double scan2[EMAXS <= 4096 ? 2 * EMAXS : 1];  // Euler-tour scan (small trees)
   __shared__ double red[ENT / 64];
   __shared__ int ired[ENT / 64];
   const int S = P.S;
@@ -93,7 +103,7 @@ __global__ __launch_bounds__(ENT) void estep_fixed_point_kernel(EStepParams P) {
       }
     }
     __syncthreads();
-    path_sum_levels_inplace<ENT>(P, pv);
+    path_sums<EMAXS>(P, pv, scan2, red);
     // col_valid_log_normalizer (extract_parameters.py:41-65), then mt = pT + norm
 #pragma unroll
     for (int k = 0; k < ECPT; ++k) {
@@ -128,6 +138,7 @@ __global__ __launch_bounds__(ENT) void estep_fixed_point_kernel(EStepParams P) {
     lin_mt[k] = exp2(mt[k]);
     e[k] = exp2(P.e_init);
   }
+  const double ratio_hi = exp2(P.tol), ratio_lo = exp2(-P.tol);
   int it = 0;
   for (;;) {
 #pragma unroll
@@ -143,7 +154,7 @@ __global__ __launch_bounds__(ENT) void estep_fixed_point_kernel(EStepParams P) {
     for (int k = 0; k < ECPT; ++k)
       if (tid + k * ENT < S) ls += w[k] * e[k];
     double rowsum = block_sum<ENT>(ls, red);  // also publishes ev/pv
-    path_sum_levels_inplace<ENT>(P, pv);
+    path_sums<EMAXS>(P, pv, scan2, red);
     int ok = 1;
 #pragma unroll
     for (int k = 0; k < ECPT; ++k) {
@@ -154,8 +165,9 @@ __global__ __launch_bounds__(ENT) void estep_fixed_point_kernel(EStepParams P) {
         double na = rowsum - pv[s];
         double eb = na > 0.0 ? lin_mt[k] * na : 0.0;
         double en = lin_pS[k] * e1 * e2 + lin_pD[k] * e[k] * e[k] + e[k] * eb + lin_pL[k];
-        double diff = fabs(log2(en / e[k]));
-        if (!(diff < P.tol)) ok = 0;
+        // |log2(en / e)| < tol without a log: en / e inside (2^-tol, 2^tol)
+        const double ratio = en / e[k];
+        if (!(ratio < ratio_hi && ratio > ratio_lo)) ok = 0;
         e[k] = en;
       }
     }
@@ -189,7 +201,7 @@ __global__ __launch_bounds__(ENT) void estep_fixed_point_kernel(EStepParams P) {
   for (int k = 0; k < ECPT; ++k)
     if (tid + k * ENT < S) ls += w[k] * e[k];
   double rowsum = block_sum<ENT>(ls, red);
-  path_sum_levels_inplace<ENT>(P, pv);
+  path_sums<EMAXS>(P, pv, scan2, red);
   const double NINF = -__builtin_inf();
 #pragma unroll
   for (int k = 0; k < ECPT; ++k) {

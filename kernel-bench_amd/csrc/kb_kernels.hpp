@@ -16,6 +16,7 @@ int set_error(int code, const char* fmt, ...);
 // ----------------------------------------------------------------------------
 struct EStepParams {
   TreeDev tr;
+  TreeScanDev ts;
   int S;
   int n_tlevels;              // depth levels, root first
   const int* tlevel_ptr;      // [n_tlevels + 1]
@@ -135,6 +136,7 @@ struct BwdParams {
 
 struct EpiParams {
   TreeDev tr;
+  TreeScanDev ts;
   int S;
   int n_tlevels;
   const int* tlevel_ptr;

@@ -301,6 +301,79 @@ int kb_rows_scatter_add(int32_t dtype, int32_t S, int64_t n, const void* src, co
  */
 int kb_rows_sum_into(int32_t dtype, int32_t S, int64_t n, const void* src, void* dst, double* work, void* stream);
 
+/* ---- forward tangents (JVP) of the forward maps, for the Newton HVP path ---- */
+
+/*
+ * e_tangent_fixed_point (kbench/core/kernels/e_step_tangent.py:174-208,
+ * kernel _e_step_tangent_2d_kernel 27-125): Richardson solve of
+ * (I - J_E^EE) dE = J_E^Ep dp at the frozen fixed point E of G item rows,
+ * from dE0 (nullable: 0), until max|dE_new - dE| <= tol * max(1, max|dE_new|)
+ * or max_iter steps, then dE_s1 / dE_s2 / dEbar of the final dE.  All
+ * parameter tensors are [G, S] item-state matrices.  The stopping test is
+ * applied per item row (the reference applies it to the max over rows; the
+ * two agree for G = 1).  n_iter [G] (nullable) gets the step count.
+ */
+typedef struct kb_etan_io {
+  int32_t dtype, G, use_col_weights, max_iter;
+  double tol;
+  const void* E;                                             /* [G, S] */
+  const void *log_pS, *log_pD, *log_pL, *max_coupling;       /* [G, S] */
+  const void* col_log_probs;                                 /* [S] */
+  const void *dlog_pS, *dlog_pD, *dlog_pL, *dmax_coupling;   /* [G, S] */
+  const void* dE0;                                           /* [G, S] or NULL */
+  void *dE, *dE_s1, *dE_s2, *dEbar;                          /* [G, S] */
+  int32_t* n_iter;                                           /* [G] or NULL */
+} kb_etan_io;
+int kb_e_tangent_fixed_point(const kb_tree* tree, const kb_etan_io* io, void* stream);
+
+/*
+ * compute_dts_tangent (kbench/core/kernels/dts_tangent.py:96-122, kernel
+ * _dts_tangent_kernel 25-93): out[w, s] = sum over the splits of row w of
+ * sum_k 2^(t_k - dts_r[w, s]) dt_k for the five DTL split terms, 0 where
+ * dts_r is -inf.  Same split grouping and parameter indexing as
+ * kb_dts_forward; the reference's atomic scatter is a fixed-order sum here.
+ */
+typedef struct kb_dts_tan_io {
+  int32_t dtype, S, W, param_by_state;
+  int64_t N, item_offset, param_row_stride;
+  const int64_t *node_child1, *node_child2;                  /* [S] */
+  const void *Pi, *Pibar, *dPi, *dPibar;                     /* [C, S] */
+  const int64_t *sl, *sr;                                    /* [N] */
+  const void* log_split_probs;                               /* [N] */
+  const int32_t *split_ptr, *split_order;                    /* [W + 1], [N] */
+  const void *log_pD, *log_pS, *dlog_pD, *dlog_pS;
+  const void* dts_r;                                         /* [W, S] */
+  const int64_t* item_idx;                                   /* [C] */
+  void* out;                                                 /* [W, S] */
+} kb_dts_tan_io;
+int kb_dts_tangent(const kb_dts_tan_io* io, void* stream);
+
+/*
+ * compute_wave_step_tangent (kbench/core/kernels/wave_tangent.py:346-431,
+ * kernel 35-177) with n_iters = 1, and compute_wave_step_tangent_selfloop
+ * (wave_tangent.py:346-389, kernel 181-343) with n_iters >= 1 and
+ * dPi_in == dPi_out, pi_ws == ws: n_iters tangent sweeps of rows
+ * [ws, ws + W) at the frozen primal rows Pi_in[pi_ws + w].  The tangent row
+ * starts from dPi_in row pi_ws + w; the result goes to dPi_out row ws + w and
+ * the dPibar of the last sweep to dPibar_out row ws + w (nullable).  dts and
+ * d_dts ([W, S]) are both given for rows with splits, both NULL otherwise.
+ * Constant rows as in kb_wave_step; leaf_logp / dleaf_logp rows item * S.
+ */
+typedef struct kb_wave_tan_io {
+  int32_t dtype, S, W, use_col_weights, use_leaf_index, n_iters;
+  int64_t ws, pi_ws, const_stride;
+  const void *Pi_in, *dPi_in;                                /* [*, S] */
+  void* dPi_out;                                             /* [C, S] */
+  void* dPibar_out;                                          /* [C, S] or NULL */
+  const void *dts, *d_dts;                                   /* [W, S] or NULL */
+  const void *max_coupling, *dMC, *DL, *dDL, *Ebar, *dEbar, *E, *dE, *SL1, *dSL1, *SL2, *dSL2;
+  const void* col_log_probs;                                 /* [S] */
+  const int64_t* item_idx;                                   /* [C] */
+  const int64_t* leaf_state;                                 /* [C] */
+  const void *leaf_logp, *dleaf_logp;                        /* [G, S] */
+} kb_wave_tan_io;
+int kb_wave_step_tangent(const kb_tree* tree, const kb_wave_tan_io* io, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,536 @@
+// Forward tangents (JVP) of the solver's forward maps: the launchers beneath
+// the drop-in replacements of the reference's kbench/core/kernels/
+// e_step_tangent.py, dts_tangent.py and wave_tangent.py (declarations and
+// the reference function each replaces: include/kbench_ops.h).
+//
+// Every map here is linear in the tangent at a frozen primal point, so each
+// kernel splits into a primal set-up (softmax weights of the LSE terms, the
+// linear row r = 2^(x - rowmax), the Pibar denominators), done once, and a
+// tangent update that is an affine map of the tangent row:
+//
+//   dX_new[s] = K[s] + a[s] dX[s] + b[s] (dRS - dAS[s]) + c[s] dX[c1(s)] + d[s] dX[c2(s)]
+//
+// with dRS = sum_s r[s] dX[s] and dAS[s] = sum over the path root..s of
+// r dX (one prefix scan over the Euler tour in LDS).  Fixed points and fixed
+// iteration counts run inside one launch with the primal coefficients kept in
+// registers and the tangent row in LDS, in float64 whatever the tensor dtype.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "kb_ops_common.hpp"
+
+namespace kbo {
+
+// Ancestors-or-self path sums of per-state register values x[k] (state
+// threadIdx.x + k * NT): written as +x at the entry event and -x at the exit
+// event of each column, scanned, read back at the entry event.  Enters with
+// ev2 free; ends with a barrier after which ev2 may be reused.
+template <int CPT>
+__device__ void reg_path_sums(const OpsTree& t, const double (&x)[CPT], double (&ps)[CPT], double* ev2,
+                              double* red) {
+  const int S = t.S;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    if (s < S) {
+      const int tin = t.tin[s];
+      const int tout = tin + 2 * (t.pend[s] - t.ppos[s]) - 1;
+      ev2[tin] = x[k];
+      ev2[tout] = -x[k];
+    }
+  }
+  __syncthreads();
+  block_scan(ev2, 2 * S, red);
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    ps[k] = s < S ? ev2[t.tin[s]] : 0.0;
+  }
+  __syncthreads();
+}
+
+// ---- E-step tangent fixed point ------------------------------------------------------
+
+template <typename T>
+struct EtArgs {
+  int G, S, use_col, max_iter;
+  double tol;
+  const T *E, *pS, *pD, *pL, *mt, *col, *dpS, *dpD, *dpL, *dmt, *dE0;
+  T *dE, *dEs1, *dEs2, *dEbar;
+  int* n_iter;
+};
+
+// One workgroup per item row g.  Primal at the frozen E*: r, denominators,
+// the four E-step term weights w_k = 2^(t_k - E_new).  Tangent update:
+//   dEbar = (dRS - dAS) / denom + dmt            (denom > 0, else 0)
+//   dE_new = w0 (dpS + dE[c1] + dE[c2]) + w1 (dpD + 2 dE) + w2 (dE + dEbar) + w3 dpL
+// (0 where E_new = -inf), iterated from dE0 (or 0) until
+// max|dE_new - dE| <= tol * max(1, max|dE_new|) or max_iter steps.
+template <typename T, int CPT>
+__global__ __launch_bounds__(NT) void etan_kernel(OpsTree t, EtArgs<T> a) {
+  extern __shared__ double smd[];
+  const int S = t.S;
+  double* D = smd;       // E row, then the tangent row
+  double* EV = smd + S;  // 2S Euler scan
+  __shared__ double red[NW];
+  const double NI = -__builtin_inf();
+  const size_t base = (size_t)blockIdx.x * S;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    if (s < S) D[s] = (double)a.E[base + s];
+  }
+  __syncthreads();
+  double r[CPT], K[CPT], w0[CPT], lin[CPT], wb[CPT], den[CPT], dm[CPT];
+  bool pos[CPT];
+  {
+    double wE[CPT];
+    double lm = NI;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int s = threadIdx.x + k * NT;
+      wE[k] = NI;
+      if (s < S) {
+        wE[k] = D[s] + (a.use_col ? (double)a.col[s] : 0.0);
+        lm = fmax(lm, wE[k]);
+      }
+    }
+    const double M = block_max(lm, red);
+    const double Ms = M == NI ? 0.0 : M;
+    double ls = 0.0;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int s = threadIdx.x + k * NT;
+      r[k] = s < S ? exp2(wE[k] - Ms) : 0.0;
+      ls += r[k];
+    }
+    const double rowsum = block_sum(ls, red);
+    double anc[CPT];
+    reg_path_sums<CPT>(t, r, anc, EV, red);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int s = threadIdx.x + k * NT;
+      K[k] = w0[k] = lin[k] = wb[k] = dm[k] = 0.0;
+      den[k] = 1.0;
+      pos[k] = false;
+      if (s < S) {
+        const size_t i = base + s;
+        const double E = D[s];
+        const int c1 = t.c1[s], c2 = t.c2[s];
+        const double Es1 = c1 >= 0 ? D[c1] : NI, Es2 = c2 >= 0 ? D[c2] : NI;
+        const double denom = rowsum - anc[k];
+        pos[k] = denom > 0.0;
+        den[k] = pos[k] ? denom : 1.0;
+        const double Eb = pos[k] ? log2(den[k]) + M + (double)a.mt[i] : NI;
+        const double t0 = (double)a.pS[i] + Es1 + Es2;
+        const double t1 = (double)a.pD[i] + 2.0 * E;
+        const double t2 = E + Eb;
+        const double t3 = (double)a.pL[i];
+        const double m = fmax(fmax(t0, t1), fmax(t2, t3));
+        const double ms = m == NI ? 0.0 : m;
+        const double e0 = exp2(t0 - ms), e1 = exp2(t1 - ms), e2 = exp2(t2 - ms), e3 = exp2(t3 - ms);
+        const double total = e0 + e1 + e2 + e3;
+        const double En = log2(total) + m;
+        dm[k] = pos[k] ? (double)a.dmt[i] : 0.0;
+        if (En != NI && total > 0.0) {
+          const double inv = 1.0 / total;
+          w0[k] = e0 * inv;
+          const double w1 = e1 * inv, w2 = e2 * inv, w3 = e3 * inv;
+          K[k] = w0[k] * (double)a.dpS[i] + w1 * (double)a.dpD[i] + w3 * (double)a.dpL[i] + w2 * dm[k];
+          lin[k] = 2.0 * w1 + w2;
+          wb[k] = pos[k] ? w2 : 0.0;
+        }
+      }
+    }
+    __syncthreads();  // every read of the E row is done
+  }
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    if (s < S) D[s] = a.dE0 ? (double)a.dE0[base + s] : 0.0;
+  }
+  __syncthreads();
+
+  // q[k] = dRS - dAS[s]; reads D, leaves it untouched.
+  auto tangent_q = [&](double (&q)[CPT]) {
+    double x[CPT];
+    double lsum = 0.0;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int s = threadIdx.x + k * NT;
+      x[k] = s < S ? r[k] * D[s] : 0.0;
+      lsum += x[k];
+    }
+    const double dRS = block_sum(lsum, red);
+    double dAS[CPT];
+    reg_path_sums<CPT>(t, x, dAS, EV, red);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) q[k] = dRS - dAS[k];
+  };
+
+  int it = 0;
+  for (;;) {
+    double q[CPT], nx[CPT];
+    tangent_q(q);
+    double ld = 0.0, lsc = 0.0;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int s = threadIdx.x + k * NT;
+      nx[k] = 0.0;
+      if (s < S) {
+        const int c1 = t.c1[s], c2 = t.c2[s];
+        const double ch = (c1 >= 0 ? D[c1] : 0.0) + (c2 >= 0 ? D[c2] : 0.0);
+        nx[k] = K[k] + w0[k] * ch + lin[k] * D[s] + wb[k] * (q[k] / den[k]);
+        ld = fmax(ld, fabs(nx[k] - D[s]));
+        lsc = fmax(lsc, fabs(nx[k]));
+      }
+    }
+    __syncthreads();  // every read of D is done
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int s = threadIdx.x + k * NT;
+      if (s < S) D[s] = nx[k];
+    }
+    ++it;
+    const double md = block_max(ld, red);  // its barriers also publish D
+    const double sc = block_max(lsc, red);
+    if (md <= a.tol * fmax(1.0, sc) || it >= a.max_iter) break;
+  }
+  // children and Ebar tangents at the final dE
+  double q[CPT];
+  tangent_q(q);
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    if (s < S) {
+      const size_t i = base + s;
+      const int c1 = t.c1[s], c2 = t.c2[s];
+      a.dE[i] = (T)D[s];
+      a.dEs1[i] = (T)(c1 >= 0 ? D[c1] : 0.0);
+      a.dEs2[i] = (T)(c2 >= 0 ? D[c2] : 0.0);
+      a.dEbar[i] = (T)(pos[k] ? q[k] / den[k] + dm[k] : 0.0);
+    }
+  }
+  if (a.n_iter && threadIdx.x == 0) a.n_iter[blockIdx.x] = it;
+}
+
+// ---- split-term tangent ---------------------------------------------------------------
+
+template <typename T>
+struct DtArgs {
+  int S, W, by_state;
+  long long item_offset, prow;
+  const T *Pi, *Pibar, *dPi, *dPibar, *lsp, *pD, *pS, *dpD, *dpS, *dts;
+  const int64_t *sl, *sr, *item, *c1, *c2;
+  const int *ptr, *order;
+  T* out;
+};
+
+// One workgroup per wave row w: out[w, s] = sum over the row's splits (in
+// increasing split order) of sum_k 2^(t_k - dts[w, s]) dt_k, 0 where
+// dts[w, s] = -inf.
+template <typename T, int CPT>
+__global__ __launch_bounds__(NT) void dts_tan_kernel(DtArgs<T> a) {
+  const int S = a.S;
+  const int w = blockIdx.x;
+  const T NI = ninf<T>();
+  const int b = a.ptr[w], e = a.ptr[w + 1];
+  const long long item = a.item[a.item_offset + w];
+  const size_t pb = (size_t)(item * a.prow);
+  double acc[CPT];
+  T base[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    acc[k] = 0.0;
+    base[k] = s < S ? a.dts[(size_t)w * S + s] : NI;
+  }
+  for (int j = b; j < e; ++j) {
+    const int si = a.order[j];
+    const size_t ol = (size_t)a.sl[si] * S, orr = (size_t)a.sr[si] * S;
+    const T lsp = a.lsp[si];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int s = threadIdx.x + k * NT;
+      if (s < S && base[k] != NI) {
+        const T d = a.by_state ? a.pD[pb + s] : a.pD[pb];
+        const T sp = a.by_state ? a.pS[pb + s] : a.pS[pb];
+        const T dd = a.by_state ? a.dpD[pb + s] : a.dpD[pb];
+        const T dsp = a.by_state ? a.dpS[pb + s] : a.dpS[pb];
+        const int c1 = child_at(a.c1, s, S), c2 = child_at(a.c2, s, S);
+        const T pl = a.Pi[ol + s], pr = a.Pi[orr + s];
+        const T l1 = c1 >= 0 ? a.Pi[ol + c1] : NI, r1 = c1 >= 0 ? a.Pi[orr + c1] : NI;
+        const T l2 = c2 >= 0 ? a.Pi[ol + c2] : NI, r2 = c2 >= 0 ? a.Pi[orr + c2] : NI;
+        const T dpl = a.dPi[ol + s], dpr = a.dPi[orr + s];
+        const T dl1 = c1 >= 0 ? a.dPi[ol + c1] : T(0), dr1 = c1 >= 0 ? a.dPi[orr + c1] : T(0);
+        const T dl2 = c2 >= 0 ? a.dPi[ol + c2] : T(0), dr2 = c2 >= 0 ? a.dPi[orr + c2] : T(0);
+        const T bs = base[k];
+        const double v0 = (double)xexp2(lsp + d + pl + pr - bs) * (double)(dd + dpl + dpr);
+        const double v1 = (double)xexp2(lsp + pl + a.Pibar[orr + s] - bs) * (double)(dpl + a.dPibar[orr + s]);
+        const double v2 = (double)xexp2(lsp + pr + a.Pibar[ol + s] - bs) * (double)(dpr + a.dPibar[ol + s]);
+        const double v3 = (double)xexp2(lsp + sp + l1 + r2 - bs) * (double)(dsp + dl1 + dr2);
+        const double v4 = (double)xexp2(lsp + sp + r1 + l2 - bs) * (double)(dsp + dr1 + dl2);
+        acc[k] += v0 + v1 + v2 + v3 + v4;
+      }
+    }
+  }
+  T* out = a.out + (size_t)w * S;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    if (s < S) out[s] = base[k] != NI ? (T)acc[k] : T(0);
+  }
+}
+
+// ---- wave-step tangent (one step, or the fixed-count self-loop) ---------------------------
+
+template <typename T>
+struct WtArgs {
+  int S, W, use_col, use_leaf, n_iters;
+  long long ws, pi_ws, cstride;
+  const T *Pi, *dPi_in;
+  T *dPi_out, *dPibar;
+  const T *dts, *ddts;
+  const T *mt, *dmt, *DL, *dDL, *Ebar, *dEbar, *E, *dE, *SL1, *dSL1, *SL2, *dSL2, *col;
+  const int64_t *item, *leaf_state;
+  const T *leaf_logp, *dleaf_logp;
+};
+
+// One workgroup per wave row w.  Primal at Pi row pi_ws + w: the weights
+// w_k = 2^(t_k - Pi_new) of the six sweep terms (and the split term), r and
+// the Pibar denominators.  n_iters tangent updates of the row:
+//   dpibar = (dRS - dAS) / denom + dmt                     (denom > 0, else 0)
+//   dPi_new = sum_k w_k dt_k,  dt = (dDL + dPi, dPi + dEbar, dpibar + dE,
+//             dSL1 + dPi[c1], dSL2 + dPi[c2], dleaf at the leaf state, d_dts)
+// (0 where Pi_new = -inf); the final row goes to dPi_out row ws + w and the
+// dpibar of the last update to dPibar row ws + w.
+template <typename T, int CPT>
+__global__ __launch_bounds__(NT) void wave_tan_kernel(OpsTree t, WtArgs<T> a) {
+  extern __shared__ double smd[];
+  const int S = t.S;
+  double* D = smd;       // Pi row, then the tangent row
+  double* EV = smd + S;  // 2S Euler scan
+  __shared__ double red[NW];
+  const double NI = -__builtin_inf();
+  const int w = blockIdx.x;
+  const long long grow = a.ws + w;
+  const long long item = a.item[grow];
+  const size_t cb = (size_t)(item * a.cstride);
+  const size_t lb = (size_t)item * S;
+  const size_t ib = (size_t)(a.pi_ws + w) * S;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    if (s < S) D[s] = (double)a.Pi[ib + s];
+  }
+  __syncthreads();
+  double r[CPT], K[CPT], lin[CPT], wb[CPT], w3[CPT], w4[CPT], den[CPT], dm[CPT];
+  bool pos[CPT];
+  {
+    double wv[CPT];
+    double lm = NI;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int s = threadIdx.x + k * NT;
+      wv[k] = NI;
+      if (s < S) {
+        wv[k] = D[s] + (a.use_col ? (double)a.col[s] : 0.0);
+        lm = fmax(lm, wv[k]);
+      }
+    }
+    const double M = block_max(lm, red);
+    const double Ms = M == NI ? 0.0 : M;
+    double ls = 0.0;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int s = threadIdx.x + k * NT;
+      r[k] = s < S ? exp2(wv[k] - Ms) : 0.0;
+      ls += r[k];
+    }
+    const double rowsum = block_sum(ls, red);
+    double anc[CPT];
+    reg_path_sums<CPT>(t, r, anc, EV, red);
+    const long long lstate = a.use_leaf ? a.leaf_state[grow] : -1;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int s = threadIdx.x + k * NT;
+      K[k] = lin[k] = wb[k] = w3[k] = w4[k] = dm[k] = 0.0;
+      den[k] = 1.0;
+      pos[k] = false;
+      if (s < S) {
+        const size_t ci = cb + s;
+        const double pi = D[s];
+        const int c1 = t.c1[s], c2 = t.c2[s];
+        const double ps1 = c1 >= 0 ? D[c1] : NI, ps2 = c2 >= 0 ? D[c2] : NI;
+        const double denom = rowsum - anc[k];
+        pos[k] = denom > 0.0;
+        den[k] = pos[k] ? denom : 1.0;
+        const double pibar = pos[k] ? log2(den[k]) + M + (double)a.mt[ci] : NI;
+        dm[k] = pos[k] ? (double)a.dmt[ci] : 0.0;
+        const bool hit = lstate == s;
+        const double t0 = (double)a.DL[ci] + pi;
+        const double t1 = pi + (double)a.Ebar[ci];
+        const double t2 = pibar + (double)a.E[ci];
+        const double t3 = (double)a.SL1[ci] + ps1;
+        const double t4 = (double)a.SL2[ci] + ps2;
+        const double t5 = hit ? (double)a.leaf_logp[lb + s] : NI;
+        double m = fmax(fmax(fmax(t0, t1), fmax(t2, t3)), fmax(t4, t5));
+        double td = NI;
+        if (a.dts) {
+          td = (double)a.dts[(size_t)w * S + s];
+          m = fmax(m, td);
+        }
+        const double ms = m == NI ? 0.0 : m;
+        const double e0 = exp2(t0 - ms), e1 = exp2(t1 - ms), e2 = exp2(t2 - ms), e3 = exp2(t3 - ms);
+        const double e4 = exp2(t4 - ms), e5 = exp2(t5 - ms), ed = a.dts ? exp2(td - ms) : 0.0;
+        const double total = e0 + e1 + e2 + e3 + e4 + e5 + ed;
+        const double res = log2(total) + m;
+        if (res != NI && total > 0.0) {
+          const double inv = 1.0 / total;
+          double k0 = e0 * (double)a.dDL[ci] + e1 * (double)a.dEbar[ci] + e2 * ((double)a.dE[ci] + dm[k]) +
+                      e3 * (double)a.dSL1[ci] + e4 * (double)a.dSL2[ci];
+          if (hit) k0 += e5 * (double)a.dleaf_logp[lb + s];
+          if (a.dts) k0 += ed * (double)a.ddts[(size_t)w * S + s];
+          K[k] = k0 * inv;
+          lin[k] = (e0 + e1) * inv;
+          wb[k] = pos[k] ? e2 * inv : 0.0;
+          w3[k] = e3 * inv;
+          w4[k] = e4 * inv;
+        }
+      }
+    }
+    __syncthreads();  // every read of the Pi row is done
+  }
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    if (s < S) D[s] = (double)a.dPi_in[ib + s];
+  }
+  __syncthreads();
+  double dpb[CPT];
+  const int n_it = a.n_iters < 1 ? 1 : a.n_iters;
+  for (int it = 0; it < n_it; ++it) {
+    double x[CPT];
+    double lsum = 0.0;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int s = threadIdx.x + k * NT;
+      x[k] = s < S ? r[k] * D[s] : 0.0;
+      lsum += x[k];
+    }
+    const double dRS = block_sum(lsum, red);
+    double dAS[CPT];
+    reg_path_sums<CPT>(t, x, dAS, EV, red);
+    double nx[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int s = threadIdx.x + k * NT;
+      nx[k] = 0.0;
+      dpb[k] = 0.0;
+      if (s < S) {
+        const double qd = (dRS - dAS[k]) / den[k];
+        dpb[k] = pos[k] ? qd + dm[k] : 0.0;
+        const int c1 = t.c1[s], c2 = t.c2[s];
+        nx[k] = K[k] + lin[k] * D[s] + wb[k] * qd + w3[k] * (c1 >= 0 ? D[c1] : 0.0) +
+                w4[k] * (c2 >= 0 ? D[c2] : 0.0);
+      }
+    }
+    __syncthreads();  // every read of D is done
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int s = threadIdx.x + k * NT;
+      if (s < S) D[s] = nx[k];
+    }
+    __syncthreads();
+  }
+  T* out = a.dPi_out + (size_t)grow * S;
+  T* pb = a.dPibar ? a.dPibar + (size_t)grow * S : nullptr;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    if (s < S) {
+      out[s] = (T)D[s];
+      if (pb) pb[s] = (T)dpb[k];
+    }
+  }
+}
+
+}  // namespace kbo
+
+using namespace kbo_host;
+
+extern "C" {
+
+int kb_e_tangent_fixed_point(const kb_tree* tr, const kb_etan_io* io, void* stream) {
+  if (!tr || !io) return kb::set_error(KB_ERR_ARG, "null argument");
+  if (int rc = dtype_ok(io->dtype)) return rc;
+  if (io->G < 0) return kb::set_error(KB_ERR_ARG, "G must be non-negative");
+  if (io->max_iter < 1 || !(io->tol >= 0.0)) return kb::set_error(KB_ERR_ARG, "max_iter must be >= 1 and tol >= 0");
+  if (io->G == 0) return 0;
+  const int S = tr->S;
+  const size_t lds = (size_t)3 * S * sizeof(double);
+  if (int rc = check_lds(lds, S, KB_F64)) return rc;
+  const kbo::OpsTree t = tr->dev();
+  KBO_DISPATCH(io->dtype, S, {
+    kbo::EtArgs<T> a{io->G, S, io->use_col_weights, io->max_iter, io->tol,
+                     (const T*)io->E, (const T*)io->log_pS, (const T*)io->log_pD, (const T*)io->log_pL,
+                     (const T*)io->max_coupling, (const T*)io->col_log_probs, (const T*)io->dlog_pS,
+                     (const T*)io->dlog_pD, (const T*)io->dlog_pL, (const T*)io->dmax_coupling, (const T*)io->dE0,
+                     (T*)io->dE, (T*)io->dE_s1, (T*)io->dE_s2, (T*)io->dEbar, io->n_iter};
+    if (int rc = set_lds(kbo::etan_kernel<T, CPT>, lds)) return rc;
+    hipLaunchKernelGGL((kbo::etan_kernel<T, CPT>), dim3(io->G), dim3(kbo::NT), lds, st_of(stream), t, a);
+  });
+  KBO_HIP(hipGetLastError());
+  return 0;
+}
+
+int kb_dts_tangent(const kb_dts_tan_io* io, void* stream) {
+  if (!io) return kb::set_error(KB_ERR_ARG, "null argument");
+  if (int rc = dtype_ok(io->dtype)) return rc;
+  if (io->W < 0 || io->N < 0 || io->S < 1) return kb::set_error(KB_ERR_ARG, "bad sizes W=%d N=%lld S=%d", io->W,
+                                                                (long long)io->N, io->S);
+  if (io->W == 0) return 0;
+  const int S = io->S;
+  KBO_DISPATCH(io->dtype, S, {
+    kbo::DtArgs<T> a{S, io->W, io->param_by_state, io->item_offset, io->param_row_stride,
+                     (const T*)io->Pi, (const T*)io->Pibar, (const T*)io->dPi, (const T*)io->dPibar,
+                     (const T*)io->log_split_probs, (const T*)io->log_pD, (const T*)io->log_pS,
+                     (const T*)io->dlog_pD, (const T*)io->dlog_pS, (const T*)io->dts_r,
+                     io->sl, io->sr, io->item_idx, io->node_child1, io->node_child2,
+                     io->split_ptr, io->split_order, (T*)io->out};
+    hipLaunchKernelGGL((kbo::dts_tan_kernel<T, CPT>), dim3(io->W), dim3(kbo::NT), 0, st_of(stream), a);
+  });
+  KBO_HIP(hipGetLastError());
+  return 0;
+}
+
+int kb_wave_step_tangent(const kb_tree* tr, const kb_wave_tan_io* io, void* stream) {
+  if (!tr || !io) return kb::set_error(KB_ERR_ARG, "null argument");
+  if (int rc = dtype_ok(io->dtype)) return rc;
+  if (io->S != tr->S) return kb::set_error(KB_ERR_ARG, "S=%d does not match the tree (%d)", io->S, tr->S);
+  if (io->W < 0) return kb::set_error(KB_ERR_ARG, "W must be non-negative");
+  if ((io->dts == nullptr) != (io->d_dts == nullptr))
+    return kb::set_error(KB_ERR_ARG, "dts and d_dts must be given together");
+  if (io->W == 0) return 0;
+  const int S = tr->S;
+  const size_t lds = (size_t)3 * S * sizeof(double);
+  if (int rc = check_lds(lds, S, KB_F64)) return rc;
+  const kbo::OpsTree t = tr->dev();
+  KBO_DISPATCH(io->dtype, S, {
+    kbo::WtArgs<T> a{S, io->W, io->use_col_weights, io->use_leaf_index, io->n_iters, io->ws, io->pi_ws,
+                     io->const_stride, (const T*)io->Pi_in, (const T*)io->dPi_in, (T*)io->dPi_out,
+                     (T*)io->dPibar_out, (const T*)io->dts, (const T*)io->d_dts,
+                     (const T*)io->max_coupling, (const T*)io->dMC, (const T*)io->DL, (const T*)io->dDL,
+                     (const T*)io->Ebar, (const T*)io->dEbar, (const T*)io->E, (const T*)io->dE,
+                     (const T*)io->SL1, (const T*)io->dSL1, (const T*)io->SL2, (const T*)io->dSL2,
+                     (const T*)io->col_log_probs, io->item_idx, io->leaf_state, (const T*)io->leaf_logp,
+                     (const T*)io->dleaf_logp};
+    if (int rc = set_lds(kbo::wave_tan_kernel<T, CPT>, lds)) return rc;
+    hipLaunchKernelGGL((kbo::wave_tan_kernel<T, CPT>), dim3(io->W), dim3(kbo::NT), lds, st_of(stream), t, a);
+  });
+  KBO_HIP(hipGetLastError());
+  return 0;
+}
+
+}  // extern "C"

@@ -77,6 +77,27 @@ class KbPibarVjpIO(ct.Structure):
         "contrib")
 
 
+class KbETanIO(ct.Structure):
+    _fields_ = [("dtype", i32), ("G", i32), ("use_col_weights", i32), ("max_iter", i32), ("tol", f64)] + _ptrs(
+        "E", "log_pS", "log_pD", "log_pL", "max_coupling", "col_log_probs", "dlog_pS", "dlog_pD", "dlog_pL",
+        "dmax_coupling", "dE0", "dE", "dE_s1", "dE_s2", "dEbar", "n_iter")
+
+
+class KbDtsTanIO(ct.Structure):
+    _fields_ = [("dtype", i32), ("S", i32), ("W", i32), ("param_by_state", i32), ("N", i64),
+                ("item_offset", i64), ("param_row_stride", i64)] + _ptrs(
+        "node_child1", "node_child2", "Pi", "Pibar", "dPi", "dPibar", "sl", "sr", "log_split_probs", "split_ptr",
+        "split_order", "log_pD", "log_pS", "dlog_pD", "dlog_pS", "dts_r", "item_idx", "out")
+
+
+class KbWaveTanIO(ct.Structure):
+    _fields_ = [("dtype", i32), ("S", i32), ("W", i32), ("use_col_weights", i32), ("use_leaf_index", i32),
+                ("n_iters", i32), ("ws", i64), ("pi_ws", i64), ("const_stride", i64)] + _ptrs(
+        "Pi_in", "dPi_in", "dPi_out", "dPibar_out", "dts", "d_dts", "max_coupling", "dMC", "DL", "dDL", "Ebar",
+        "dEbar", "E", "dE", "SL1", "dSL1", "SL2", "dSL2", "col_log_probs", "item_idx", "leaf_state", "leaf_logp",
+        "dleaf_logp")
+
+
 def declare(lib) -> None:
     def fn(name, argtypes, restype=ct.c_int):
         f = getattr(lib, name)
@@ -97,3 +118,6 @@ def declare(lib) -> None:
     fn("kb_pibar_vjp", [vp, ct.POINTER(KbPibarVjpIO), vp])
     fn("kb_rows_scatter_add", [i32, i32, i64, vp, vp, vp, vp, i64, vp])
     fn("kb_rows_sum_into", [i32, i32, i64, vp, vp, vp, vp])
+    fn("kb_e_tangent_fixed_point", [vp, ct.POINTER(KbETanIO), vp])
+    fn("kb_dts_tangent", [ct.POINTER(KbDtsTanIO), vp])
+    fn("kb_wave_step_tangent", [vp, ct.POINTER(KbWaveTanIO), vp])

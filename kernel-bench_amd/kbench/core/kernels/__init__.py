@@ -9,6 +9,10 @@ signatures):
 * ``wave_backward`` -- wave_backward.py (``active_mask_from_rhs_absmax_fused``,
   ``wave_backward_uniform_fused``, ``dts_cross_backward_accum_fused``,
   ``uniform_cross_pibar_vjp_tree_from_ud_fused``)
+* ``e_step_tangent`` -- e_step_tangent.py (``e_tangent_fixed_point``)
+* ``dts_tangent`` -- dts_tangent.py (``compute_dts_tangent``)
+* ``wave_tangent`` -- wave_tangent.py (``compute_wave_step_tangent``,
+  ``compute_wave_step_tangent_selfloop``)
 * ``_dts_layout_contract`` -- _dts_layout_contract.py (host-side layout codes)
 
 The native launchers are declared in include/kbench_ops.h.

@@ -951,3 +951,235 @@ def e_adjoint_and_theta_vjp(prob: Problem, theta, cw, use_col, saved, g_E, g_Eba
     G_col = g_col + gcol_e
     grad_theta, grad_col = theta_col_vjp(prob, theta, cw, use_col, G_pS, G_pD, G_pL, G_mt, G_col)
     return grad_theta, grad_col, {"n_bicgstab": n_bicg, "wE": wE, "q_E": q_E}
+
+
+# ----------------------------------------------------------------------------
+# forward tangents (row a11, first half): reference
+# kbench/core/kernels/{e_step_tangent,dts_tangent,wave_tangent}.py and the glue
+# newton/forward_tangent.py
+# ----------------------------------------------------------------------------
+
+def _child_tangent(tree: Tree, X, which):
+    """``X[..., c[s]]`` with 0 where the child is the ``>= S`` sentinel (tangent gathers)."""
+    c = tree.c1 if which == 1 else tree.c2
+    valid = (c >= 0) & (c < tree.S)
+    return np.where(valid, X[..., np.where(valid, c, 0)], 0.0)
+
+
+def param_jvp_uniform(theta, v, unnorm_row_max, statewise=False, itemwise=False):
+    """Tangent of :func:`extract_parameters_uniform` along ``v`` (newton/forward_tangent.py:29-41).
+
+    The rates are a base-2 log-softmax of [0, theta], so d log2 p_k = dl_k - sum_j p_j dl_j
+    with dl = [0, v]; max_coupling = log2 p_T + unnorm_row_max has the tangent of log2 p_T.
+    """
+    th = np.asarray(theta, dtype=np.float64)
+    dv = np.asarray(v, dtype=np.float64)
+    logits = np.concatenate([np.zeros(th.shape[:-1] + (1,)), th], axis=-1)
+    dlog = np.concatenate([np.zeros(dv.shape[:-1] + (1,)), dv], axis=-1)
+    p = np.exp2(log2_softmax(logits))
+    d = dlog - (p * dlog).sum(axis=-1, keepdims=True)
+    urm = np.asarray(unnorm_row_max, dtype=np.float64)
+    if statewise and not itemwise:
+        dmt = d[..., 3] + 0.0 * urm
+    else:
+        dmt = d[..., 3][..., None] + 0.0 * urm
+    return d[..., 0], d[..., 1], d[..., 2], dmt
+
+
+def e_step_tangent(E, dE, pS, pD, pL, mt, col, dpS, dpD, dpL, dmt, tree: Tree, use_col_weights: bool):
+    """Tangent of one E-step at E along (dE, dparams) (e_step_tangent.py:27-125).
+
+    Returns (dE_new, dE_s1, dE_s2, dEbar); dE_new = sum_k w_k dt_k with the softmax weights of the
+    four E-step terms, dEbar = (dRS - dAS) / denom + dmt.
+    """
+    wE = E + col if use_col_weights else E
+    row_max = wE.max(axis=1, keepdims=True)
+    rms = _safe(row_max)
+    r = np.exp2(wE - rms)
+    row_sum = r.sum(axis=1, keepdims=True)
+    dRS = (r * dE).sum(axis=1, keepdims=True)
+    anc = tree.ancestor_sum(r)
+    dAS = tree.ancestor_sum(r * dE)
+    E_s1, E_s2 = tree.child_gather(E, 1), tree.child_gather(E, 2)
+    dE_s1, dE_s2 = _child_tangent(tree, dE, 1), _child_tangent(tree, dE, 2)
+    denom = row_sum - anc
+    pos = denom > 0.0
+    sd = np.where(pos, denom, 1.0)
+    Ebar = np.where(pos, np.log2(sd) + row_max + mt, NEG_INF)
+    dEbar = np.where(pos, (dRS - dAS) / sd + dmt, 0.0)
+    t = [pS + E_s1 + E_s2, pD + 2.0 * E, E + Ebar, pL]
+    dt = [dpS + dE_s1 + dE_s2, dpD + 2.0 * dE, dE + dEbar, dpL]
+    m = np.maximum.reduce(t)
+    ms = _safe(m)
+    e = [np.exp2(tk - ms) for tk in t]
+    total = e[0] + e[1] + e[2] + e[3]
+    E_new = np.log2(np.where(total > 0, total, 1.0)) + m
+    inv = np.where(total > 0.0, 1.0 / np.where(total > 0, total, 1.0), 0.0)
+    dE_new = sum(ek * inv * dtk for ek, dtk in zip(e, dt))
+    dE_new = np.where(np.isneginf(E_new) | (total <= 0), 0.0, dE_new)
+    return dE_new, dE_s1, dE_s2, dEbar
+
+
+def e_tangent_fixed_point(E_star, dpS, dpD, dpL, dmt, pS, pD, pL, mt, col, tree: Tree, *, max_iter=2000,
+                          tol=1e-9, use_col_weights=True, dE0=None):
+    """Richardson solve of (I - J_E^EE) dE* = J_E^Ep dp at frozen E* (e_step_tangent.py:174-208).
+
+    Stops when max|dE_new - dE| <= tol * max(1, max|dE_new|).
+    """
+    G, S = E_star.shape
+    st = lambda x: np.broadcast_to(as_item_state(np.asarray(x, dtype=np.float64), S, G), (G, S))
+    args = tuple(st(x) for x in (pS, pD, pL, mt))
+    dargs = tuple(st(x) for x in (dpS, dpD, dpL, dmt))
+    dE = np.zeros_like(E_star) if dE0 is None else np.array(dE0, dtype=np.float64)
+    for _ in range(int(max_iter)):
+        nxt = e_step_tangent(E_star, dE, *args, col, *dargs, tree, use_col_weights)[0]
+        diff = float(np.abs(nxt - dE).max())
+        dE = nxt
+        if diff <= tol * max(1.0, float(np.abs(dE).max())):
+            break
+    _, dE_s1, dE_s2, dEbar = e_step_tangent(E_star, dE, *args, col, *dargs, tree, use_col_weights)
+    return dE, dE_s1, dE_s2, dEbar
+
+
+def dts_tangent(Pi, Pibar, dPi, dPibar, meta, W, pD_param, pS_param, dpD_param, dpS_param, dts_r, item_idx, ws,
+                tree: Tree):
+    """Tangent of :func:`dts_forward` (dts_tangent.py:25-122): sum over a row's splits of
+    sum_k 2^(t_k - dts_r) dt_k; 0 where dts_r is -inf."""
+    S = tree.S
+    out = np.zeros((W, S))
+    sl = np.asarray(meta["sl"])
+    N = sl.shape[0]
+    if N == 0:
+        return out
+    sr = np.asarray(meta["sr"])
+    red = np.asarray(meta["reduce_idx"])
+    lsp = np.asarray(meta.get("log_split_probs", np.zeros(N)), dtype=np.float64).reshape(N)
+    items = np.asarray(item_idx)[ws + red]
+    pD, pS = _rate_rows(pD_param, items, S), _rate_rows(pS_param, items, S)
+    dpD, dpS = _rate_rows(dpD_param, items, S), _rate_rows(dpS_param, items, S)
+    t = dts_split_terms(Pi, Pibar, sl, sr, pD, pS, lsp, tree)
+    dPl, dPr = dPi[sl], dPi[sr]
+    dt = [dpD + dPl + dPr, dPl + dPibar[sr], dPr + dPibar[sl],
+          dpS + _child_tangent(tree, dPl, 1) + _child_tangent(tree, dPr, 2),
+          dpS + _child_tangent(tree, dPr, 1) + _child_tangent(tree, dPl, 2)]
+    base = dts_r[red]
+    live = ~np.isneginf(base)
+    with np.errstate(invalid="ignore", over="ignore"):
+        contrib = sum(np.exp2(tk - np.where(live, base, 0.0)) * dtk for tk, dtk in zip(t, dt))
+    contrib = np.where(live, np.nan_to_num(contrib, nan=0.0, posinf=0.0, neginf=0.0), 0.0)
+    np.add.at(out, red, contrib)
+    return out
+
+
+@dataclass
+class WaveTangentConsts:
+    """Tangents of the wave constants (newton/forward_tangent.py:58-91), [G, S] each."""
+
+    dDL: np.ndarray
+    dEbar: np.ndarray
+    dE: np.ndarray
+    dSL1: np.ndarray
+    dSL2: np.ndarray
+    dMC: np.ndarray
+    dleaf: np.ndarray
+
+
+def wave_step_tangent(Pi_in, dPi_in, rows_item, consts: WaveConsts, dc: WaveTangentConsts, tree: Tree, *,
+                      leaf_state=None, dts_r=None, d_dts=None, n_iters=1):
+    """``n_iters`` tangent applications of the sweep at the frozen rows ``Pi_in``
+    (wave_tangent.py:38-171 one step; 174-343 the fused self-loop).
+
+    Returns (dPi after n_iters, dPibar of the last iteration's input tangent).
+    """
+    S = tree.S
+    wPi = Pi_in + consts.col if consts.use_col_weights else Pi_in
+    row_max = wPi.max(axis=1, keepdims=True)
+    rms = _safe(row_max)
+    r = np.exp2(wPi - rms)
+    row_sum = r.sum(axis=1, keepdims=True)
+    anc = tree.ancestor_sum(r)
+    mt = consts.mt[rows_item]
+    denom = row_sum - anc
+    pos = denom > 0.0
+    sd = np.where(pos, denom, 1.0)
+    pibar = np.where(pos, np.log2(sd) + row_max + mt, NEG_INF)
+    t = [consts.DL[rows_item] + Pi_in, Pi_in + consts.Ebar[rows_item], pibar + consts.E[rows_item],
+         consts.SL1[rows_item] + tree.child_gather(Pi_in, 1), consts.SL2[rows_item] + tree.child_gather(Pi_in, 2)]
+    if leaf_state is not None:
+        hit = np.arange(S)[None, :] == np.asarray(leaf_state)[:, None]
+        t5 = np.where(hit, consts.leaf_logp[rows_item], NEG_INF)
+        dt5 = np.where(hit, dc.dleaf[rows_item], 0.0)
+    else:
+        t5 = np.full_like(Pi_in, NEG_INF)
+        dt5 = np.zeros_like(Pi_in)
+    terms = t + [t5]
+    if dts_r is not None:
+        terms.append(dts_r)
+    m = np.maximum.reduce(terms)
+    ms = _safe(m)
+    e = [np.exp2(tk - ms) for tk in terms]
+    total = sum(e)
+    result = np.log2(np.where(total > 0, total, 1.0)) + m
+    inv = np.where(total > 0.0, 1.0 / np.where(total > 0, total, 1.0), 0.0)
+    valid = ~np.isneginf(result) & (total > 0)
+    dpi = np.array(dPi_in, dtype=np.float64)
+    dpibar = np.zeros_like(dpi)
+    for _ in range(max(int(n_iters), 1)):
+        dRS = (r * dpi).sum(axis=1, keepdims=True)
+        dAS = tree.ancestor_sum(r * dpi)
+        dpibar = np.where(pos, (dRS - dAS) / sd + dc.dMC[rows_item], 0.0)
+        dt = [dc.dDL[rows_item] + dpi, dpi + dc.dEbar[rows_item], dpibar + dc.dE[rows_item],
+              dc.dSL1[rows_item] + _child_tangent(tree, dpi, 1), dc.dSL2[rows_item] + _child_tangent(tree, dpi, 2),
+              dt5]
+        num = sum(ek * dtk for ek, dtk in zip(e[:6], dt))
+        if dts_r is not None:
+            num = num + e[6] * d_dts
+        dpi = np.where(valid, num * inv, 0.0)
+    return dpi, dpibar
+
+
+def jvp_root_scores(prob: Problem, theta, v, saved, *, self_iters=None, e_tol=1e-12):
+    """d(root rows of Pi)/dtheta . v (newton/forward_tangent.py:102-209), uniform column weights.
+
+    Runs the E tangent fixed point, then per wave the split-term tangent and ``self_iters``
+    tangent sweeps at the saved Pi* (default: pi_iters).  Returns (roots [n_fam, S], dPi, dPibar).
+    """
+    S, C, tree = prob.S, prob.C, prob.tree
+    G = int(prob.root_ids.shape[0]) if prob.itemwise else 1
+    n_it = int(prob.so["pi_iters"]) if self_iters is None else int(self_iters)
+    dpS, dpD, dpL, dmt = param_jvp_uniform(theta, v, prob.unnorm_row_max, prob.statewise, prob.itemwise)
+    st = lambda x: np.broadcast_to(as_item_state(np.asarray(x, dtype=np.float64), S, G), (G, S)).copy()
+    E = np.asarray(saved["E"], dtype=np.float64)
+    pS, pD, pL, mt = (st(saved[k]) for k in ("log_pS", "log_pD", "log_pL", "max_coupling"))
+    col = np.asarray(saved["col_log_probs"], dtype=np.float64)
+    dE, dE_s1, dE_s2, dEbar = e_tangent_fixed_point(E, dpS, dpD, dpL, dmt, pS, pD, pL, mt, col, tree,
+                                                    max_iter=int(prob.so["e_max_iter"]), tol=e_tol,
+                                                    use_col_weights=False)
+    consts = WaveConsts(mt=mt, DL=1.0 + pD + E, Ebar=np.asarray(saved["Ebar"], dtype=np.float64), E=E,
+                        SL1=pS + np.asarray(saved["E_s2"], dtype=np.float64),
+                        SL2=pS + np.asarray(saved["E_s1"], dtype=np.float64), leaf_logp=pS, col=col,
+                        use_col_weights=False)
+    dps_i, dpd_i = st(dpS), st(dpD)
+    dc = WaveTangentConsts(dDL=dpd_i + dE, dEbar=dEbar, dE=dE, dSL1=dps_i + dE_s2, dSL2=dps_i + dE_s1, dMC=st(dmt),
+                           dleaf=dps_i)
+    pD_param, pS_param = as_item_param(np.asarray(saved["log_pD"]), G, S), as_item_param(np.asarray(saved["log_pS"]), G, S)
+    dpD_param, dpS_param = as_item_param(dpD, G, S), as_item_param(dpS, G, S)
+    Pi = np.asarray(saved["pi_wave"], dtype=np.float64)
+    Pb = np.asarray(saved["pibar_wave"], dtype=np.float64)
+    dPi = np.zeros((C, S))
+    dPb = np.zeros((C, S))
+    for meta in prob.wave_metas:
+        ws, W = int(meta["start"]), int(meta["W"])
+        rows = np.arange(ws, ws + W)
+        items = prob.item_idx[rows]
+        if "sl" in meta:
+            dts_r = dts_forward(Pi, Pb, meta, W, pD_param, pS_param, prob.item_idx, ws, tree)
+            d_dts = dts_tangent(Pi, Pb, dPi, dPb, meta, W, pD_param, pS_param, dpD_param, dpS_param, dts_r,
+                                prob.item_idx, ws, tree)
+            leaf = None
+        else:
+            dts_r = d_dts = None
+            leaf = prob.leaf_state[rows]
+        dPi[rows], dPb[rows] = wave_step_tangent(Pi[rows], dPi[rows], items, consts, dc, tree, leaf_state=leaf,
+                                                 dts_r=dts_r, d_dts=d_dts, n_iters=n_it)
+    return dPi[prob.root_ids], dPi, dPb

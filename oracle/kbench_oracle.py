@@ -774,8 +774,13 @@ def bicgstab(Av, b, max_iter=500, tol=1e-7, breakdown_tol=1e-30):
     raise RuntimeError(f"E-adjoint BiCGSTAB solve failed after {k} iterations (relative residual {rel_res:.3e})")
 
 
-def backward(prob: Problem, theta, col_weights, saved, *, collect=False):
-    """``run_backward``: reference kbench/runtime.py:77-115 -> _implicit_grad.py:97-475."""
+def backward(prob: Problem, theta, col_weights, saved, *, collect=False, cache=None):
+    """``run_backward``: reference kbench/runtime.py:77-115 -> _implicit_grad.py:97-475.
+
+    With ``cache`` (a dict) the per-wave adjoints, split terms and masks, the accumulated
+    cotangents and the E adjoint are stored for the exact HVP (newton/ggn.py:41-210 with
+    ``cache``, newton/hvp_exact.py:37-44).
+    """
     so = prob.so
     tree = prob.tree
     S, C = prob.S, prob.C
@@ -838,6 +843,9 @@ def backward(prob: Problem, theta, col_weights, saved, *, collect=False):
             Pi_s[rows], Pibar_s[rows], row_max[rows], rhs, items, consts, tree, N_terms,
             active=act, leaf_state=leaf, dts_r=dts_r)
         g_col += cg
+        if cache is not None:
+            cache.setdefault("waves", []).append(dict(
+                ws=ws, W=W, v=np.where(act[:, None], v, 0.0), dts_r=dts_r, active=act, leaf=leaf, meta=meta))
         scatter(g_pD, aw0)
         scatter(g_pS, aw345)
         scatter(g_E, aw0 + aw2)
@@ -856,6 +864,10 @@ def backward(prob: Problem, theta, col_weights, saved, *, collect=False):
             g_col += out["col_grad"]
     grads = e_adjoint_and_theta_vjp(prob, theta, cw, use_col, saved, g_E, g_Ebar, g_Es1, g_Es2, g_pD, g_pS,
                                     g_mt, g_col)
+    if cache is not None:
+        cache["accum"] = {"g_E": g_E, "g_Ebar": g_Ebar, "g_Es1": g_Es1, "g_Es2": g_Es2, "g_pD": g_pD,
+                          "g_pS": g_pS, "g_mt": g_mt, "g_col": g_col}
+        cache["wE"] = grads[2]["wE"]
     if collect:
         grads = grads + ({"masks": masks, "acc": {"g_E": g_E, "g_Ebar": g_Ebar, "g_Es1": g_Es1, "g_Es2": g_Es2,
                                                   "g_pD": g_pD, "g_pS": g_pS, "g_mt": g_mt, "g_col": g_col}},)
@@ -926,31 +938,41 @@ def e_adjoint_and_theta_vjp(prob: Problem, theta, cw, use_col, saved, g_E, g_Eba
     wE = w_flat.reshape(E.shape)
     # param cotangents: param_loss + E-step(E*, params) with grads (wE on E_new, g_Ebar on Ebar)
     _, q0, q1, q3, wbar, gcol_e = e_step_vjp(E, pS_i, pD_i, pL_i, mt_i, col, tree, use_col, wE, zero, zero, g_Ebar)
-    pS_raw = np.asarray(saved["log_pS"])
-
-    def fold(gstate, raw):
-        # gradient w.r.t. the un-expanded parameter (as_item_state is a broadcast)
-        raw = np.asarray(raw)
-        if raw.ndim == 0:
-            return gstate.sum()
-        if raw.ndim == 1 and raw.size == S and G == 1:
-            return gstate.reshape(S)
-        return gstate.reshape(raw.shape) if gstate.size == raw.size else gstate.sum(axis=-1).reshape(raw.shape)
-
-    def fold_param(gparam, raw):
-        raw = np.asarray(raw)
-        if raw.ndim == 0:
-            return gparam.sum()
-        return gparam.reshape(raw.shape) if gparam.size == raw.size else gparam.sum(axis=-1).reshape(raw.shape)
-
-    G_pS = fold(q0, pS_raw) + fold_param(g_pS, pS_raw)
-    G_pD = fold(q1, saved["log_pD"]) + fold_param(g_pD, saved["log_pD"])
-    G_pL = fold(q3, saved["log_pL"])
-    mt_raw = np.asarray(saved["max_coupling"])
-    G_mt = fold(wbar, mt_raw) + fold(g_mt, mt_raw)
-    G_col = g_col + gcol_e
-    grad_theta, grad_col = theta_col_vjp(prob, theta, cw, use_col, G_pS, G_pD, G_pL, G_mt, G_col)
+    G_all = _fold_cotangents(saved, S, G, q0, q1, q3, wbar, gcol_e, g_pD, g_pS, g_mt, g_col)
+    grad_theta, grad_col = theta_col_vjp(prob, theta, cw, use_col, *G_all)
     return grad_theta, grad_col, {"n_bicgstab": n_bicg, "wE": wE, "q_E": q_E}
+
+
+def _fold_state(gstate, raw, S, G):
+    """Gradient w.r.t. an un-expanded parameter from its [G, S] item-state gradient (as_item_state
+    is a broadcast)."""
+    raw = np.asarray(raw)
+    if raw.ndim == 0:
+        return gstate.sum()
+    if raw.ndim == 1 and raw.size == S and G == 1:
+        return gstate.reshape(S)
+    return gstate.reshape(raw.shape) if gstate.size == raw.size else gstate.sum(axis=-1).reshape(raw.shape)
+
+
+def _fold_param(gparam, raw):
+    """Gradient w.r.t. an un-expanded parameter from its as_item_param-shaped gradient."""
+    raw = np.asarray(raw)
+    if raw.ndim == 0:
+        return gparam.sum()
+    return gparam.reshape(raw.shape) if gparam.size == raw.size else gparam.sum(axis=-1).reshape(raw.shape)
+
+
+def _fold_cotangents(saved, S, G, e_pS, e_pD, e_pL, e_mt, e_col, g_pD, g_pS, g_mt, g_col):
+    """Cotangents of (log_pS, log_pD, log_pL, max_coupling, col_log_probs) in the shapes the
+    parameter extraction returns: E-step head terms (item-state) plus the sweep accumulators
+    (reference _implicit_grad.py:440-469; newton/hvp_exact.py:163-168, 354-358)."""
+    G_pS = _fold_state(e_pS, saved["log_pS"], S, G) + _fold_param(g_pS, saved["log_pS"])
+    G_pD = _fold_state(e_pD, saved["log_pD"], S, G) + _fold_param(g_pD, saved["log_pD"])
+    G_pL = _fold_state(e_pL, saved["log_pL"], S, G)
+    mt_raw = np.asarray(saved["max_coupling"])
+    G_mt = _fold_state(e_mt, mt_raw, S, G) + _fold_state(g_mt, mt_raw, S, G)
+    G_col = g_col + e_col
+    return G_pS, G_pD, G_pL, G_mt, G_col
 
 
 # ----------------------------------------------------------------------------
@@ -1138,11 +1160,13 @@ def wave_step_tangent(Pi_in, dPi_in, rows_item, consts: WaveConsts, dc: WaveTang
     return dpi, dpibar
 
 
-def jvp_root_scores(prob: Problem, theta, v, saved, *, self_iters=None, e_tol=1e-12):
+def jvp_root_scores(prob: Problem, theta, v, saved, *, self_iters=None, e_tol=1e-12, return_full=False):
     """d(root rows of Pi)/dtheta . v (newton/forward_tangent.py:102-209), uniform column weights.
 
     Runs the E tangent fixed point, then per wave the split-term tangent and ``self_iters``
-    tangent sweeps at the saved Pi* (default: pi_iters).  Returns (roots [n_fam, S], dPi, dPibar).
+    tangent sweeps at the saved Pi* (default: pi_iters).  Returns (roots [n_fam, S], dPi, dPibar),
+    plus a dict of the parameter / E tangents and the sweep's tangent constants with
+    ``return_full``.
     """
     S, C, tree = prob.S, prob.C, prob.tree
     G = int(prob.root_ids.shape[0]) if prob.itemwise else 1
@@ -1182,4 +1206,315 @@ def jvp_root_scores(prob: Problem, theta, v, saved, *, self_iters=None, e_tol=1e
             leaf = prob.leaf_state[rows]
         dPi[rows], dPb[rows] = wave_step_tangent(Pi[rows], dPi[rows], items, consts, dc, tree, leaf_state=leaf,
                                                  dts_r=dts_r, d_dts=d_dts, n_iters=n_it)
+    if return_full:
+        full = dict(dpS=dpS, dpD=dpD, dpL=dpL, dmt=dmt, dE=dE, dE_s1=dE_s1, dE_s2=dE_s2, dEbar=dEbar, dc=dc,
+                    consts=consts, dpD_param=dpD_param, dpS_param=dpS_param, pD_param=pD_param, pS_param=pS_param)
+        return dPi[prob.root_ids], dPi, dPb, full
     return dPi[prob.root_ids], dPi, dPb
+
+
+# ----------------------------------------------------------------------------
+# second-order contractions and the exact HVP (row a11, second half): reference
+# kbench/core/kernels/{e_step_so,wave_so,dts_so}.py and newton/{ggn,hvp_exact}.py
+# ----------------------------------------------------------------------------
+
+def e_step_backward_so(E, E_new, E_s1, E_s2, Ebar, pS, pD, pL, col, tree: Tree, g_new, g_ebar, dE, dE_new, dE_s1,
+                       dE_s2, dEbar, dpS, dpD, dpL, dcol=None, use_col_weights=False):
+    """Tangent of the E-step VJP at fixed cotangents (e_step_so.py:30-220).
+
+    Returns (d_grad_E, d_grad_pS, d_grad_pD, d_grad_pL, d_grad_mc, d_grad_col).  With the term
+    weights q_k = g_new 2^(t_k - E_new):  dq_k = ln2 q_k (dt_k - dE_new); the Pibar part
+    r (tot - excl) with u = (q2 + g_ebar) / denom differentiates with the row max frozen.
+    The g_s1 / g_s2 cotangents enter the VJP linearly and drop out.
+    """
+    t = [pS + E_s1 + E_s2, pD + 2.0 * E, E + Ebar, pL]
+    dt = [dpS + dE_s1 + dE_s2, dpD + 2.0 * dE, dE + dEbar, dpL]
+    with np.errstate(invalid="ignore", over="ignore"):
+        q = [np.nan_to_num(g_new * np.exp2(tk - E_new), nan=0.0) for tk in t]
+    dq = [np.where(qk != 0.0, LN2 * qk * (dtk - dE_new), 0.0) for qk, dtk in zip(q, dt)]
+    d_gE = 2.0 * dq[1] + dq[2]
+    S = tree.S
+    for c in (tree.c1, tree.c2):
+        valid = (c >= 0) & (c < S)
+        idx = np.nonzero(valid)[0]
+        np.add.at(d_gE, (slice(None), c[idx]), dq[0][:, idx])
+    wE = E + col if use_col_weights else E
+    dcol_ = np.zeros_like(col) if dcol is None else dcol
+    dwE = dE + dcol_ if use_col_weights else dE
+    rms = _safe(wE.max(axis=1, keepdims=True))
+    r = np.exp2(wE - rms)
+    dr = LN2 * r * dwE
+    denom = r.sum(axis=1, keepdims=True) - tree.ancestor_sum(r)
+    ddenom = dr.sum(axis=1, keepdims=True) - tree.ancestor_sum(dr)
+    pos = denom > 0.0
+    sd = np.where(pos, denom, 1.0)
+    u = np.where(pos, (q[2] + g_ebar) / sd, 0.0)
+    du = np.where(pos, (dq[2] - u * ddenom) / sd, 0.0)
+    d_pv = (dr * (u.sum(axis=1, keepdims=True) - tree.subtree_sum(u))
+            + r * (du.sum(axis=1, keepdims=True) - tree.subtree_sum(du)))
+    return d_gE + d_pv, dq[0], dq[1], dq[3], dq[2], d_pv.sum(axis=0)
+
+
+def wave_backward_so(Pi, dPi, Pibar, dPibar, v, row_max, items, consts: WaveConsts, dc: WaveTangentConsts,
+                     tree: Tree, *, leaf_state=None, dts_r=None, d_dts=None, rhs_rows=None):
+    """Tangent of one self-loop J^T application and of the parameter buckets at fixed adjoint v
+    (wave_so.py:37-293), the saved row max frozen.
+
+    Returns (d_Av (+ rhs_rows when given), d_aw0, d_aw1, d_aw2, d_aw345, d_aw3, d_aw4).
+    """
+    S = tree.S
+    rms = _safe(row_max)[:, None]
+    wPi = Pi + consts.col if consts.use_col_weights else Pi
+    pp = np.exp2(wPi - rms)
+    dpp = LN2 * pp * dPi
+    denom = pp.sum(axis=1, keepdims=True) - tree.ancestor_sum(pp)
+    ddenom = dpp.sum(axis=1, keepdims=True) - tree.ancestor_sum(dpp)
+    pos = denom > 0.0
+    inv_den = np.where(pos, 1.0 / np.where(pos, denom, 1.0), 0.0)
+    t = [consts.DL[items] + Pi, Pi + consts.Ebar[items], Pibar + consts.E[items],
+         consts.SL1[items] + tree.child_gather(Pi, 1), consts.SL2[items] + tree.child_gather(Pi, 2)]
+    dt = [dc.dDL[items] + dPi, dPi + dc.dEbar[items], dPibar + dc.dE[items],
+          dc.dSL1[items] + _child_tangent(tree, dPi, 1), dc.dSL2[items] + _child_tangent(tree, dPi, 2)]
+    if leaf_state is not None:
+        hit = np.arange(S)[None, :] == np.asarray(leaf_state)[:, None]
+        t.append(np.where(hit, consts.leaf_logp[items], NEG_INF))
+        dt.append(np.where(hit, dc.dleaf[items], 0.0))
+    else:
+        t.append(np.full_like(Pi, NEG_INF))
+        dt.append(np.zeros_like(Pi))
+    m = np.maximum.reduce(t)
+    ms = _safe(m)
+    e = [np.exp2(tk - ms) for tk in t]
+    tot = sum(e)
+    inv = np.where(tot > 0.0, 1.0 / np.where(tot > 0, tot, 1.0), 0.0)
+    w = [ek * inv for ek in e]
+    dlse = sum(wk * np.where(wk != 0.0, dtk, 0.0) for wk, dtk in zip(w, dt))
+    dw = [np.where(wk != 0.0, LN2 * wk * (dtk - dlse), 0.0) for wk, dtk in zip(w, dt)]
+    if dts_r is not None:
+        with np.errstate(divide="ignore"):
+            dts_l = np.where(tot > 0.0, np.log2(np.where(tot > 0, tot, 1.0)) + m, NEG_INF)
+        pm = np.maximum(dts_l, dts_r)
+        pms = _safe(pm)
+        pi_new = np.log2(np.exp2(dts_l - pms) + np.exp2(dts_r - pms)) + pm
+        wL = np.where(np.isneginf(dts_l), 0.0, np.exp2(dts_l - np.where(np.isneginf(dts_l), 0.0, pi_new)))
+        both = ~np.isneginf(dts_r) & ~np.isneginf(dts_l)
+        dwL = np.where(both, LN2 * wL * (1.0 - wL) * (dlse - np.where(both, d_dts, 0.0)), 0.0)
+    else:
+        wL = np.ones_like(Pi)
+        dwL = np.zeros_like(Pi)
+    da = [v * (dwL * wk + wL * dwk) for wk, dwk in zip(w, dw)]
+    pc = wL * w[2] * inv_den
+    dpc = (dwL * w[2] + wL * dw[2]) * inv_den - pc * inv_den * ddenom
+    u, du = v * pc, v * dpc
+    A, dA = u.sum(axis=1, keepdims=True), du.sum(axis=1, keepdims=True)
+    out = (v * (dwL * (w[0] + w[1]) + wL * (dw[0] + dw[1])) + dpp * (A - tree.subtree_sum(u))
+           + pp * (dA - tree.subtree_sum(du)))
+    if rhs_rows is not None:
+        out = out + rhs_rows
+    for c, k in ((tree.c1, 3), (tree.c2, 4)):
+        valid = (c >= 0) & (c < S)
+        idx = np.nonzero(valid)[0]
+        np.add.at(out, (slice(None), c[idx]), (v * (dwL * w[k] + wL * dw[k]))[:, idx])
+    return out, da[0], da[1], da[2], da[3] + da[4] + da[5], da[3], da[4]
+
+
+def dts_backward_so(Pi, dPi, Pibar, dPibar, v, ws, meta, pD_param, pS_param, dpD_param, dpS_param, mt_item,
+                    dmt_item, col, row_max, item_idx, tree: Tree, use_col_weights=False):
+    """Tangent of the split-term backward and its Pibar tree VJP at fixed adjoint v (dts_so.py:29-303),
+    the saved row maxes frozen (the parent Pi normaliser is not).
+
+    Returns a dict: d_rhs_l / d_rhs_r [N, S] (into the child rows sl / sr), d_pD / d_pS / d_mt
+    [N, S] (per split, in the parent's item row) and d_col [S].
+    """
+    S = tree.S
+    sl, sr = np.asarray(meta["sl"]), np.asarray(meta["sr"])
+    red = np.asarray(meta["reduce_idx"])
+    N = sl.shape[0]
+    lsp = np.asarray(meta.get("log_split_probs", np.zeros(N)), dtype=np.float64).reshape(N)
+    items = np.asarray(item_idx)[int(meta["start"]) + red]
+    pD, pS = _rate_rows(pD_param, items, S), _rate_rows(pS_param, items, S)
+    dpD, dpS = _rate_rows(dpD_param, items, S), _rate_rows(dpS_param, items, S)
+    d = dts_split_terms(Pi, Pibar, sl, sr, pD, pS, np.zeros(N), tree)
+    dPl, dPr = dPi[sl], dPi[sr]
+    dd = [dpD + dPl + dPr, dPl + dPibar[sr], dPr + dPibar[sl],
+          dpS + _child_tangent(tree, dPl, 1) + _child_tangent(tree, dPr, 2),
+          dpS + _child_tangent(tree, dPr, 1) + _child_tangent(tree, dPl, 2)]
+    prow = int(ws) + red
+    Pp, dPp = Pi[prow], dPi[prow]
+    fin = ~np.isneginf(Pp)
+    w = [np.where(fin, np.exp2(lsp[:, None] + dk - np.where(fin, Pp, 0.0)), 0.0) for dk in d]
+    vk = v[red]
+    vd = [vk * wk for wk in w]
+    dvd = [np.where(wk != 0.0, vk * LN2 * wk * (ddk - dPp), 0.0) for wk, ddk in zip(w, dd)]
+    rl = dvd[0] + dvd[1]
+    rr = dvd[0] + dvd[2]
+    for c, (a_l, a_r) in ((tree.c1, (dvd[3], dvd[4])), (tree.c2, (dvd[4], dvd[3]))):
+        valid = (c >= 0) & (c < S)
+        idx = np.nonzero(valid)[0]
+        np.add.at(rl, (slice(None), c[idx]), a_l[:, idx])
+        np.add.at(rr, (slice(None), c[idx]), a_r[:, idx])
+    mt, dmt = mt_item[items], dmt_item[items]
+    d_col = np.zeros(S)
+    for child, vdk, dvdk, acc in ((sl, vd[2], dvd[2], rl), (sr, vd[1], dvd[1], rr)):
+        pb, dpb = Pibar[child], dPibar[child]
+        ok = ~np.isneginf(pb)
+        f = np.where(ok, np.exp2(row_max[child][:, None] + mt - np.where(ok, pb, 0.0)), 0.0)
+        ud = vdk * f
+        dud = dvdk * f + np.where(f != 0.0, vdk * LN2 * f * (dmt - dpb), 0.0)
+        A, dA = ud.sum(axis=1, keepdims=True), dud.sum(axis=1, keepdims=True)
+        pc = Pi[child]
+        wpc = pc + col if use_col_weights else pc
+        okc = ~np.isneginf(pc)
+        pp = np.where(okc, np.exp2(np.where(okc, wpc, 0.0) - _safe(row_max[child])[:, None]), 0.0)
+        contrib = LN2 * pp * dPi[child] * (A - tree.subtree_sum(ud)) + pp * (dA - tree.subtree_sum(dud))
+        acc += contrib
+        d_col += contrib.sum(axis=0)
+    return {"d_rhs_l": rl, "d_rhs_r": rr, "d_pD": dvd[0], "d_pS": dvd[3] + dvd[4], "d_mt": dvd[1] + dvd[2],
+            "d_col": d_col}
+
+
+def theta_head_hvp(prob: Problem, theta, u, G_pS, G_pD, G_pL, G_mt):
+    """Second derivative of the parameter extraction contracted with fixed cotangents, along u:
+    d/dtheta [theta_col_vjp(theta; G)] . u (newton/hvp_exact.py:153-185, the head term).
+
+    The rates are a base-2 log-softmax of [0, theta]: the VJP is G_k - p_k sum(G); its tangent
+    is -dp_k sum(G) with dp = ln2 p (dl - sum p dl), dl = [0, u].  The column normaliser of
+    max_coupling does not depend on theta.
+    """
+    th = np.asarray(theta, dtype=np.float64)
+    uu = np.asarray(u, dtype=np.float64).reshape(th.shape)
+    logits = np.concatenate([np.zeros(th.shape[:-1] + (1,)), th], axis=-1)
+    dl = np.concatenate([np.zeros(uu.shape[:-1] + (1,)), uu], axis=-1)
+    p = np.exp2(log2_softmax(logits))
+    dp = LN2 * p * (dl - (p * dl).sum(axis=-1, keepdims=True))
+    G_pT = G_mt if (prob.statewise and not prob.itemwise) else G_mt.sum(axis=-1)
+    tot = (np.stack([G_pS, G_pD, G_pL, G_pT], axis=-1)).sum(axis=-1, keepdims=True)
+    return (-dp * tot)[..., 1:]
+
+
+def build_point_cache(prob: Problem, theta, col_weights, saved):
+    """Backward once with the per-wave adjoints cached (newton/hvp_exact.py:37-44)."""
+    cache = {}
+    gt, gc, _ = backward(prob, theta, col_weights, saved, cache=cache)
+    return gt, gc, cache
+
+
+def hvp_exact(prob: Problem, theta, saved, u, cache, *, tangent_self_iters=None, e_tol=1e-12):
+    """Exact Hessian-vector product of the loss at theta (newton/hvp_exact.py:54-383),
+    forward-over-reverse at the cached point, uniform column weights, item_rows == 1.
+
+    One tangent forward sweep (``jvp_root_scores``), then in reversed wave order: the
+    second-order contraction at the cached adjoint, the tangent adjoint solve with the same
+    operator and mask, the split-term backward of the tangent adjoint and its own second-order
+    contraction; then the E side (contractions, tangent E-adjoint by BiCGSTAB) and the
+    parameter head (linear in the tangent cotangents, plus the head's Hessian term).
+    """
+    so = prob.so
+    tree = prob.tree
+    S, C = prob.S, prob.C
+    G = saved["E"].shape[0]
+    if G != 1:
+        raise NotImplementedError("oracle HVP covers item_rows == 1")
+    n_it = int(so["pi_iters"]) if tangent_self_iters is None else int(tangent_self_iters)
+    uu = np.asarray(u, dtype=np.float64).reshape(np.shape(theta))
+    roots_t, dPi, dPb, full = jvp_root_scores(prob, theta, uu, saved, self_iters=n_it, e_tol=e_tol,
+                                              return_full=True)
+    dc, consts = full["dc"], full["consts"]
+    Pi, Pb, rmax = saved["pi_wave"], saved["pibar_wave"], saved["pibar_row_max"]
+    acc = cache["accum"]
+    wE = cache["wE"]
+    st = lambda x: np.broadcast_to(as_item_state(np.asarray(x, dtype=np.float64), S, G), (G, S)).copy()
+    pD_param, pS_param = full["pD_param"], full["pS_param"]
+    # root seed tangent: -q is the loss seed, d(-q) = -ln2 q (t - <q, t>)
+    R = Pi[prob.root_ids]
+    fin = ~np.isneginf(R)
+    q = np.where(fin, np.exp2(np.where(fin, R, 0.0) - logsumexp2(R, axis=-1, keepdims=True)), 0.0)
+    d_rhs = np.zeros((C, S))
+    d_rhs[prob.root_ids] = -LN2 * q * (roots_t - (q * roots_t).sum(axis=-1, keepdims=True))
+    d_gpD, d_gpS = np.zeros_like(acc["g_pD"]), np.zeros_like(acc["g_pS"])
+    d_gE, d_gEbar, d_gEs1, d_gEs2 = (np.zeros((G, S)) for _ in range(4))
+    d_gmt, d_gcol = np.zeros_like(acc["g_mt"]), np.zeros(S)
+
+    def scatter(a, contrib):
+        if a.shape[1] == 1:
+            a[0, 0] += contrib.sum()
+        else:
+            a[0] += contrib.sum(axis=0)
+
+    N_terms = int(so["neumann_terms"])
+    for wave in cache["waves"]:
+        ws, W, meta = wave["ws"], wave["W"], wave["meta"]
+        rows = np.arange(ws, ws + W)
+        items = prob.item_idx[rows]
+        dts_r, act, leaf, v_k = wave["dts_r"], wave["active"], wave["leaf"], wave["v"]
+        d_dts = None
+        if dts_r is not None:
+            d_dts = dts_tangent(Pi, Pb, dPi, dPb, meta, W, pD_param, pS_param, full["dpD_param"],
+                                full["dpS_param"], dts_r, prob.item_idx, ws, tree)
+        c_out = wave_backward_so(Pi[rows], dPi[rows], Pb[rows], dPb[rows], v_k, rmax[rows], items, consts, dc, tree,
+                                 leaf_state=leaf, dts_r=dts_r, d_dts=d_dts, rhs_rows=d_rhs[rows])
+        dv, *l_aw, cg = wave_backward_uniform(Pi[rows], Pb[rows], rmax[rows], c_out[0], items, consts, tree, N_terms,
+                                              active=act, leaf_state=leaf, dts_r=dts_r)
+        d_gcol += cg
+        aw0, aw1, aw2, aw345, aw3, aw4 = (c + l for c, l in zip(c_out[1:], l_aw))
+        scatter(d_gpD, aw0)
+        scatter(d_gpS, aw345)
+        scatter(d_gE, aw0 + aw2)
+        scatter(d_gEbar, aw1)
+        scatter(d_gEs1, aw4)
+        scatter(d_gEs2, aw3)
+        scatter(d_gmt, aw2)
+        if dts_r is not None:
+            out = dts_cross_backward(Pi, Pb, rmax, dv, ws, meta, pD_param, pS_param, consts.mt, prob.item_idx, tree,
+                                     act, consts.col, False)
+            np.add.at(d_rhs, np.asarray(meta["sl"]), out["rhs_l"])
+            np.add.at(d_rhs, np.asarray(meta["sr"]), out["rhs_r"])
+            scatter(d_gpD, out["g_pD"])
+            scatter(d_gpS, out["g_pS"])
+            d_gmt[0] += out["g_mt_l"].sum(axis=0) + out["g_mt_r"].sum(axis=0)
+            d_gcol += out["col_grad"]
+            so2 = dts_backward_so(Pi, dPi, Pb, dPb, v_k, ws, meta, pD_param, pS_param, full["dpD_param"],
+                                  full["dpS_param"], consts.mt, dc.dMC, consts.col, rmax, prob.item_idx, tree)
+            np.add.at(d_rhs, np.asarray(meta["sl"]), so2["d_rhs_l"])
+            np.add.at(d_rhs, np.asarray(meta["sr"]), so2["d_rhs_r"])
+            scatter(d_gpD, so2["d_pD"])
+            scatter(d_gpS, so2["d_pS"])
+            d_gmt[0] += so2["d_mt"].sum(axis=0)
+            d_gcol += so2["d_col"]
+    # ---- E side
+    E = saved["E"]
+    pS_i, pD_i, pL_i, mt_i = (st(saved[k]) for k in ("log_pS", "log_pD", "log_pL", "max_coupling"))
+    col = np.asarray(saved["col_log_probs"], dtype=np.float64)
+    zero = np.zeros_like(E)
+    dE, dEs1, dEs2, dEbar = full["dE"], full["dE_s1"], full["dE_s2"], full["dEbar"]
+    dx = (dE, dE, dEs1, dEs2, dEbar, st(full["dpS"]), st(full["dpD"]), st(full["dpL"]))
+    x = (E, E, saved["E_s1"], saved["E_s2"], saved["Ebar"], pS_i, pD_i, pL_i, col, tree)
+    aux_lin = e_step_vjp(E, pS_i, pD_i, pL_i, mt_i, col, tree, False, zero, d_gEs1, d_gEs2, d_gEbar)[0]
+    so_aux = e_step_backward_so(*x, zero, acc["g_Ebar"], *dx)
+    n_fam = int(prob.root_ids.shape[0])
+    fam = 1.0 if G == n_fam else float(n_fam)
+    e2E = np.exp2(E)
+    norm = np.maximum(1.0 - e2E.mean(axis=-1, keepdims=True), np.finfo(np.float64).tiny)
+    dnorm = -LN2 * (e2E * dE).mean(axis=-1, keepdims=True)
+    dg_norm = fam * (-LN2 * e2E * dE / (S * norm) + e2E * dnorm / (S * norm * norm))
+    dq_E = d_gE + aux_lin + so_aux[0] + dg_norm
+    so_w = e_step_backward_so(*x, wE, zero, *dx)
+    rhs_E = dq_E + so_w[0]
+
+    def AG(w_flat):
+        w = w_flat.reshape(E.shape)
+        return (w - e_step_vjp(E, pS_i, pD_i, pL_i, mt_i, col, tree, False, w, zero, zero, zero)[0]).reshape(-1)
+
+    dwE_flat, _ = bicgstab(AG, rhs_E.reshape(-1), so["bicgstab_max_iter"], so["bicgstab_tol"],
+                           so["bicgstab_breakdown_tol"])
+    dwE = dwE_flat.reshape(E.shape)
+    lin = e_step_vjp(E, pS_i, pD_i, pL_i, mt_i, col, tree, False, dwE, zero, zero, d_gEbar)
+    so_p = e_step_backward_so(*x, wE, acc["g_Ebar"], *dx)
+    d_cot = _fold_cotangents(saved, S, G, lin[1] + so_p[1], lin[2] + so_p[2], lin[3] + so_p[3], lin[4] + so_p[4],
+                             lin[5] + so_p[5], d_gpD, d_gpS, d_gmt, d_gcol)
+    base = e_step_vjp(E, pS_i, pD_i, pL_i, mt_i, col, tree, False, wE, zero, zero, acc["g_Ebar"])
+    cot = _fold_cotangents(saved, S, G, base[1], base[2], base[3], base[4], base[5], acc["g_pD"], acc["g_pS"],
+                           acc["g_mt"], acc["g_col"])
+    cw = np.zeros(S)
+    lin_theta, _ = theta_col_vjp(prob, theta, cw, False, *d_cot)
+    return lin_theta + theta_head_hvp(prob, theta, uu, *cot[:4])

@@ -374,6 +374,81 @@ typedef struct kb_wave_tan_io {
 } kb_wave_tan_io;
 int kb_wave_step_tangent(const kb_tree* tree, const kb_wave_tan_io* io, void* stream);
 
+/* ---- second-order contractions of the backward maps (exact HVP) ---- */
+
+/*
+ * e_step_backward_so (kbench/core/kernels/e_step_so.py:182-220, kernels
+ * _e_step_so_prepare_kernel 30-158 and _e_step_so_finalize_kernel 161-179):
+ * tangent of the E-step VJP at fixed cotangents (g_new, g_ebar) along
+ * (dE, dE_new, dE_s1, dE_s2, dEbar, dlog_pS, dlog_pD, dlog_pL, dcol), the row
+ * max frozen.  Writes d_grad_E / pS / pD / pL / mc [G, S] and, per item row,
+ * the d_grad_col contribution col_rows [G, S] (the caller sums the rows: the
+ * reference's atomic column accumulation).  dcol is NULL for a zero tangent.
+ */
+typedef struct kb_estep_so_io {
+  int32_t dtype, G, use_col_weights;
+  const void *E, *E_new, *E_s1, *E_s2, *Ebar, *log_pS, *log_pD, *log_pL;   /* [G, S] */
+  const void* col_log_probs;                                             /* [S] */
+  const void *g_new, *g_ebar;                                            /* [G, S] */
+  const void *dE, *dE_new, *dE_s1, *dE_s2, *dEbar, *dlog_pS, *dlog_pD, *dlog_pL;  /* [G, S] */
+  const void* dcol;                                                      /* [S] or NULL */
+  void *d_grad_E, *d_grad_pS, *d_grad_pD, *d_grad_pL, *d_grad_mc;        /* [G, S] */
+  void* col_rows;                                                        /* [G, S] */
+} kb_estep_so_io;
+int kb_estep_backward_so(const kb_tree* tree, const kb_estep_so_io* io, void* stream);
+
+/*
+ * wave_backward_so (kbench/core/kernels/wave_so.py:246-293, kernel 37-243):
+ * tangent of one self-loop J^T application and of the parameter buckets
+ * (aw0..aw4, aw345) of wave rows [ws, ws + W) at the fixed adjoint v [W, S],
+ * along (dPi, dPibar, the constant tangents, d_dts), the saved
+ * pibar_row_max frozen.  d_out[w] = d(A^T v)[w] (+ d_rhs[ws + w] when d_rhs
+ * is given: the reference's FOLD_RHS).  Constant rows as in kb_wave_step.
+ */
+typedef struct kb_wave_so_io {
+  int32_t dtype, S, W, use_col_weights, use_leaf_index;
+  int64_t ws, const_stride;
+  const void *Pi, *dPi, *Pibar, *dPibar;                                 /* [C, S] */
+  const void* v;                                                         /* [W, S] */
+  const void* pibar_row_max;                                             /* [C] */
+  const void *DL, *dDL, *Ebar, *dEbar, *E, *dE, *SL1, *dSL1, *SL2, *dSL2;
+  const void* col_log_probs;                                             /* [S] */
+  const int64_t *item_idx, *leaf_state;                                  /* [C] */
+  const void *leaf_logp, *dleaf_logp;                                    /* [G, S] */
+  const void *dts, *d_dts;                                               /* [W, S] or NULL */
+  const void* d_rhs;                                                     /* [C, S] or NULL */
+  void *d_out, *d_aw0, *d_aw1, *d_aw2, *d_aw345, *d_aw3, *d_aw4;         /* [W, S] */
+} kb_wave_so_io;
+int kb_wave_backward_so(const kb_tree* tree, const kb_wave_so_io* io, void* stream);
+
+/*
+ * dts_backward_so (kbench/core/kernels/dts_so.py:233-303, kernels
+ * _dts_split_so_kernel 29-141 and _dts_tree_so_kernel 145-230): tangent of
+ * the split-term backward and of its Pibar tree VJP at the fixed adjoint v
+ * [W, S] of a wave's N splits, along (dPi, dPibar, dlog_pD, dlog_pS, dmt).
+ * Instead of the reference's atomic scatters it writes rows the caller adds
+ * in a fixed order: side_rows [2N, S] (rows 0..N-1 into Pi rows sl, N..2N-1
+ * into sr), col_rows [2N, S] (d_grad_col), pD_rows / pS_rows / mt_rows
+ * [N, S] (in the parent row's item).  ud / dud [2N, S] are staging buffers.
+ * Rates as in kb_dts_forward; mt / dmt rows item * mt_row_stride.
+ */
+typedef struct kb_dts_so_io {
+  int32_t dtype, S, param_by_state, use_col_weights;
+  int64_t N, ws, item_offset, param_row_stride, mt_row_stride;
+  const void *Pi, *dPi, *Pibar, *dPibar;                                 /* [C, S] */
+  const void* v;                                                         /* [W, S] */
+  const int64_t *sl, *sr, *reduce_idx;                                   /* [N] */
+  const void* log_split_probs;                                           /* [N] */
+  const void *log_pD, *log_pS, *dlog_pD, *dlog_pS, *mt, *dmt;
+  const int64_t* item_idx;                                               /* [C] */
+  const void* pibar_row_max;                                             /* [C] */
+  const void* col_log_probs;                                             /* [S] */
+  const int64_t *node_child1, *node_child2;                              /* [S] */
+  void *ud, *dud, *side_rows, *col_rows;                                 /* [2N, S] */
+  void *pD_rows, *pS_rows, *mt_rows;                                     /* [N, S] */
+} kb_dts_so_io;
+int kb_dts_backward_so(const kb_tree* tree, const kb_dts_so_io* io, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,538 @@
+// Second-order contractions of the backward maps for the exact Hessian-vector
+// product: the launchers beneath the drop-in replacements of the reference's
+// kbench/core/kernels/e_step_so.py, wave_so.py and dts_so.py (declarations and
+// the reference function each replaces: include/kbench_ops.h).
+//
+// Each backward map is linear in its cotangent and nonlinear in its primal
+// point; these kernels return its directional derivative along a primal
+// tangent at a fixed cotangent.  The structure mirrors the first-order
+// kernels: one 1024-thread workgroup per row, ancestor path sums by an
+// Euler-tour prefix scan and subtree sums by a preorder prefix scan in LDS,
+// scatters onto child columns written as gathers from the parent column
+// (every column has one parent), cross-row accumulations emitted as rows and
+// summed in a fixed order by the caller, float64 arithmetic inside.  The
+// saved row maxima are frozen (every output is invariant to the row
+// normaliser).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "kb_ops_common.hpp"
+
+namespace kbo {
+
+constexpr double LN2D = 0.6931471805599453;
+
+template <typename T>
+__device__ __forceinline__ double ld(const T* p, size_t i) {
+  return (double)p[i];
+}
+
+// ---- E-step ------------------------------------------------------------------------
+
+template <typename T>
+struct EsoArgs {
+  int G, S, use_col;
+  const T *E, *En, *Es1, *Es2, *Eb, *pS, *pD, *pL, *col, *gN, *gB;
+  const T *dE, *dEn, *dEs1, *dEs2, *dEb, *dpS, *dpD, *dpL, *dcol;
+  T *oE, *opS, *opD, *opL, *omc, *ocol;
+};
+
+// One workgroup per item row.  q_k = g_new 2^(t_k - E_new), dq_k = ln2 q_k (dt_k - dE_new);
+// d_grad_E = 2 dq1 + dq2 + dq0[parent] + dr (tot - excl) + r (dtot - dexcl) with
+// u = (q2 + g_ebar) / denom, du = (dq2 - u ddenom) / denom, excl = subtree sums of u.
+template <typename T, int CPT>
+__global__ __launch_bounds__(NT) void eso_kernel(OpsTree t, EsoArgs<T> a) {
+  extern __shared__ double smd[];
+  const int S = t.S;
+  double* X = smd;       // dq0 by column
+  double* EV = smd + S;  // 2S scan buffer
+  __shared__ double red[NW];
+  const double NI = -__builtin_inf();
+  const size_t base = (size_t)blockIdx.x * S;
+  double gE[CPT], wE[CPT], dwE[CPT], dq2[CPT], q2g[CPT];
+  double lm = NI;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    gE[k] = dq2[k] = q2g[k] = dwE[k] = 0.0;
+    wE[k] = NI;
+    if (s < S) {
+      const size_t i = base + s;
+      const double E = ld(a.E, i), En = ld(a.En, i), dE = ld(a.dE, i), dEn = ld(a.dEn, i), g = ld(a.gN, i);
+      const double t0 = ld(a.pS, i) + ld(a.Es1, i) + ld(a.Es2, i);
+      const double t1 = ld(a.pD, i) + 2.0 * E;
+      const double t2 = E + ld(a.Eb, i);
+      const double t3 = ld(a.pL, i);
+      const double dt0 = ld(a.dpS, i) + ld(a.dEs1, i) + ld(a.dEs2, i);
+      const double dt1 = ld(a.dpD, i) + 2.0 * dE;
+      const double dt2 = dE + ld(a.dEb, i);
+      const double dt3 = ld(a.dpL, i);
+      double q[4] = {g * exp2(t0 - En), g * exp2(t1 - En), g * exp2(t2 - En), g * exp2(t3 - En)};
+      const double dt[4] = {dt0, dt1, dt2, dt3};
+      double dq[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (q[j] != q[j]) q[j] = 0.0;  // 0 * inf
+        dq[j] = q[j] != 0.0 ? LN2D * q[j] * (dt[j] - dEn) : 0.0;
+      }
+      a.opS[i] = (T)dq[0];
+      a.opD[i] = (T)dq[1];
+      a.opL[i] = (T)dq[3];
+      a.omc[i] = (T)dq[2];
+      X[s] = dq[0];
+      gE[k] = 2.0 * dq[1] + dq[2];
+      dq2[k] = dq[2];
+      q2g[k] = q[2] + ld(a.gB, i);
+      wE[k] = E + (a.use_col ? ld(a.col, s) : 0.0);
+      dwE[k] = dE + ((a.use_col && a.dcol) ? ld(a.dcol, s) : 0.0);
+      lm = fmax(lm, wE[k]);
+    }
+  }
+  const double M = block_max(lm, red);  // its barriers publish X
+  const double Ms = M == NI ? 0.0 : M;
+  double r[CPT], dr[CPT];
+  double ls = 0.0, lds = 0.0;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    r[k] = dr[k] = 0.0;
+    if (s < S) {
+      const int p = t.par[s];
+      if (p >= 0) gE[k] += X[p];
+      r[k] = exp2(wE[k] - Ms);
+      dr[k] = LN2D * r[k] * dwE[k];
+    }
+    ls += r[k];
+    lds += dr[k];
+  }
+  const double rowsum = block_sum(ls, red);
+  const double drowsum = block_sum(lds, red);
+  double anc[CPT], danc[CPT];
+  reg_path_sums<CPT>(t, r, anc, EV, red);
+  reg_path_sums<CPT>(t, dr, danc, EV, red);
+  double u[CPT], du[CPT];
+  double lu = 0.0, ldu = 0.0;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const double denom = rowsum - anc[k];
+    const double dden = drowsum - danc[k];
+    const bool pos = denom > 0.0;
+    u[k] = pos ? q2g[k] / denom : 0.0;
+    du[k] = pos ? (dq2[k] - u[k] * dden) / denom : 0.0;
+    lu += u[k];
+    ldu += du[k];
+  }
+  const double tot = block_sum(lu, red);
+  const double dtot = block_sum(ldu, red);
+  double ex[CPT], dex[CPT];
+  reg_subtree_sums<CPT>(t, u, ex, EV, red);
+  reg_subtree_sums<CPT>(t, du, dex, EV, red);
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    if (s < S) {
+      const double pv = dr[k] * (tot - ex[k]) + r[k] * (dtot - dex[k]);
+      a.oE[base + s] = (T)(gE[k] + pv);
+      a.ocol[base + s] = (T)pv;
+    }
+  }
+}
+
+// ---- self-loop J^T and parameter buckets -------------------------------------------------
+
+template <typename T>
+struct WsoArgs {
+  int S, W, use_col, use_leaf;
+  long long ws, cstride;
+  const T *Pi, *dPi, *Pb, *dPb, *v, *rowmax;
+  const T *DL, *dDL, *Ebar, *dEbar, *E, *dE, *SL1, *dSL1, *SL2, *dSL2, *col;
+  const int64_t *item, *leaf_state;
+  const T *leaf_logp, *dleaf_logp, *dts, *ddts, *rhs;
+  T *out, *aw0, *aw1, *aw2, *aw345, *aw3, *aw4;
+};
+
+// One workgroup per wave row w (global row ws + w).  With the sweep's term
+// weights w~_k = 2^(t_k - lse), dlse = sum w~_k dt_k, dw~_k = ln2 w~_k (dt_k - dlse),
+// the split mixing weight w_L = 2^(lse - Pi_new) and
+// dw_L = ln2 w_L (1 - w_L) (dlse - d_dts):
+//   d_aw_k = v (dw_L w~_k + w_L dw~_k)
+//   d_out  = v d(diag) + dp' (A - sub) + p' (dA - dsub) + [v d(sl_wt)] at the parent,
+// u = v w_L w~_2 / denom, A = sum u, sub = subtree sums of u, p' = 2^((col +) Pi - rowmax).
+template <typename T, int CPT>
+__global__ __launch_bounds__(NT) void wso_kernel(OpsTree t, WsoArgs<T> a) {
+  extern __shared__ double smd[];
+  const int S = t.S;
+  double* Z = smd;       // child-edge contributions by column
+  double* EV = smd + S;  // 2S scan buffer
+  __shared__ double red[NW];
+  const double NI = -__builtin_inf();
+  const int w = blockIdx.x;
+  const long long grow = a.ws + w;
+  const long long item = a.item[grow];
+  const size_t cb = (size_t)(item * a.cstride);
+  const size_t lb = (size_t)item * S;
+  const size_t rb = (size_t)grow * S;
+  const size_t wb = (size_t)w * S;
+  const double rm = ld(a.rowmax, grow);
+  const double rms = rm == NI ? 0.0 : rm;
+  const long long lstate = a.use_leaf ? a.leaf_state[grow] : -1;
+  double pp[CPT], dpp[CPT], vv[CPT];
+  double lsum = 0.0, ldsum = 0.0;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    pp[k] = dpp[k] = vv[k] = 0.0;
+    if (s < S) {
+      const double pi = ld(a.Pi, rb + s);
+      pp[k] = exp2(pi + (a.use_col ? ld(a.col, s) : 0.0) - rms);
+      dpp[k] = LN2D * pp[k] * ld(a.dPi, rb + s);
+      vv[k] = ld(a.v, wb + s);
+      Z[s] = 0.0;
+    }
+    lsum += pp[k];
+    ldsum += dpp[k];
+  }
+  const double rowsum = block_sum(lsum, red);
+  const double drowsum = block_sum(ldsum, red);
+  double anc[CPT], danc[CPT];
+  reg_path_sums<CPT>(t, pp, anc, EV, red);
+  reg_path_sums<CPT>(t, dpp, danc, EV, red);
+  double dself[CPT], u[CPT], du[CPT];
+  double lu = 0.0, ldu = 0.0;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    dself[k] = u[k] = du[k] = 0.0;
+    if (s < S) {
+      const size_t ci = cb + s;
+      const double denom = rowsum - anc[k];
+      const double ddenom = drowsum - danc[k];
+      const double invd = denom > 0.0 ? 1.0 / denom : 0.0;
+      const double pi = ld(a.Pi, rb + s), dpi = ld(a.dPi, rb + s);
+      const int c1 = t.c1[s], c2 = t.c2[s];
+      const double p1 = c1 >= 0 ? ld(a.Pi, rb + c1) : NI, p2 = c2 >= 0 ? ld(a.Pi, rb + c2) : NI;
+      const double dp1 = c1 >= 0 ? ld(a.dPi, rb + c1) : 0.0, dp2 = c2 >= 0 ? ld(a.dPi, rb + c2) : 0.0;
+      const bool hit = lstate == s;
+      double tk[6], dtk[6];
+      tk[0] = ld(a.DL, ci) + pi;
+      dtk[0] = ld(a.dDL, ci) + dpi;
+      tk[1] = pi + ld(a.Ebar, ci);
+      dtk[1] = dpi + ld(a.dEbar, ci);
+      tk[2] = ld(a.Pb, rb + s) + ld(a.E, ci);
+      dtk[2] = ld(a.dPb, rb + s) + ld(a.dE, ci);
+      tk[3] = ld(a.SL1, ci) + p1;
+      dtk[3] = ld(a.dSL1, ci) + dp1;
+      tk[4] = ld(a.SL2, ci) + p2;
+      dtk[4] = ld(a.dSL2, ci) + dp2;
+      tk[5] = hit ? ld(a.leaf_logp, lb + s) : NI;
+      dtk[5] = hit ? ld(a.dleaf_logp, lb + s) : 0.0;
+      double m = tk[0];
+#pragma unroll
+      for (int j = 1; j < 6; ++j) m = fmax(m, tk[j]);
+      const double ms = m == NI ? 0.0 : m;
+      double wk[6], tot = 0.0;
+#pragma unroll
+      for (int j = 0; j < 6; ++j) {
+        wk[j] = exp2(tk[j] - ms);
+        tot += wk[j];
+      }
+      const double inv = tot > 0.0 ? 1.0 / tot : 0.0;
+      double dlse = 0.0;
+#pragma unroll
+      for (int j = 0; j < 6; ++j) {
+        wk[j] *= inv;
+        if (wk[j] != 0.0) dlse += wk[j] * dtk[j];
+      }
+      double dw[6];
+#pragma unroll
+      for (int j = 0; j < 6; ++j) dw[j] = wk[j] != 0.0 ? LN2D * wk[j] * (dtk[j] - dlse) : 0.0;
+      double wL = 1.0, dwL = 0.0;
+      if (a.dts) {
+        const double dr = ld(a.dts, wb + s);
+        const double dl = tot > 0.0 ? log2(tot) + m : NI;
+        const double pm = fmax(dl, dr);
+        const double pms = pm == NI ? 0.0 : pm;
+        const double pnew = log2(exp2(dl - pms) + exp2(dr - pms)) + pm;
+        wL = dl != NI ? exp2(dl - pnew) : 0.0;
+        dwL = (dr != NI && dl != NI) ? LN2D * wL * (1.0 - wL) * (dlse - ld(a.ddts, wb + s)) : 0.0;
+      }
+      double da[6];
+#pragma unroll
+      for (int j = 0; j < 6; ++j) da[j] = vv[k] * (dwL * wk[j] + wL * dw[j]);
+      a.aw0[wb + s] = (T)da[0];
+      a.aw1[wb + s] = (T)da[1];
+      a.aw2[wb + s] = (T)da[2];
+      a.aw345[wb + s] = (T)(da[3] + da[4] + da[5]);
+      a.aw3[wb + s] = (T)da[3];
+      a.aw4[wb + s] = (T)da[4];
+      if (c1 >= 0) Z[c1] = da[3];
+      if (c2 >= 0) Z[c2] = da[4];
+      const double pc = wL * wk[2] * invd;
+      const double dpc = (dwL * wk[2] + wL * dw[2]) * invd - pc * invd * ddenom;
+      u[k] = vv[k] * pc;
+      du[k] = vv[k] * dpc;
+      dself[k] = da[0] + da[1];
+    }
+    lu += u[k];
+    ldu += du[k];
+  }
+  const double A = block_sum(lu, red);  // its barriers publish Z
+  const double dA = block_sum(ldu, red);
+  double sub[CPT], dsub[CPT];
+  reg_subtree_sums<CPT>(t, u, sub, EV, red);
+  reg_subtree_sums<CPT>(t, du, dsub, EV, red);
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    if (s < S) {
+      double o = dself[k] + dpp[k] * (A - sub[k]) + pp[k] * (dA - dsub[k]) + Z[s];
+      if (a.rhs) o += ld(a.rhs, rb + s);
+      a.out[wb + s] = (T)o;
+    }
+  }
+}
+
+// ---- split-term backward and its Pibar tree VJP --------------------------------------------
+
+template <typename T>
+struct DsoArgs {
+  int S, by_state, use_col;
+  long long N, ws, item_offset, prow, mrow;
+  const T *Pi, *dPi, *Pb, *dPb, *v, *lsp, *pD, *pS, *dpD, *dpS, *mt, *dmt, *rowmax, *col;
+  const int64_t *sl, *sr, *red, *item, *c1, *c2;
+  T *ud, *dud, *side, *colrows, *pDrows, *pSrows, *mtrows;
+};
+
+// One workgroup per split n.  w_k = 2^(lsp + d_k - Pi_parent) (0 where Pi_parent = -inf),
+// dvd_k = v ln2 w_k (dd_k - dPi_parent); the child rows receive dvd0 + dvd1 (left),
+// dvd0 + dvd2 (right) and the speciation terms at the child columns; the Pibar
+// cotangents are staged as ud = vd f, dud = dvd f + vd ln2 f (dmt - dPibar) with
+// f = 2^(rowmax_child + mt - Pibar).
+template <typename T, int CPT>
+__global__ __launch_bounds__(NT) void dso_split_kernel(DsoArgs<T> a) {
+  extern __shared__ double smd[];
+  const int S = a.S;
+  double* L = smd;
+  double* R = smd + S;
+  const double NI = -__builtin_inf();
+  const long long n = blockIdx.x, N = a.N;
+  const long long pw = a.red[n];
+  const long long item = a.item[a.item_offset + pw];
+  const size_t pb = (size_t)(item * a.prow);
+  const size_t mb = (size_t)(item * a.mrow);
+  const long long l = a.sl[n], r = a.sr[n];
+  const size_t bl = (size_t)l * S, br = (size_t)r * S, bp = (size_t)(a.ws + pw) * S, bv = (size_t)pw * S;
+  const double lsp = ld(a.lsp, n);
+  const double rml = ld(a.rowmax, l), rmr = ld(a.rowmax, r);
+  double d3[CPT], d4[CPT];
+  int c1v[CPT], c2v[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    d3[k] = d4[k] = 0.0;
+    c1v[k] = c2v[k] = -1;
+    if (s < S) {
+      const double d = a.by_state ? ld(a.pD, pb + s) : ld(a.pD, pb);
+      const double sp = a.by_state ? ld(a.pS, pb + s) : ld(a.pS, pb);
+      const double dd = a.by_state ? ld(a.dpD, pb + s) : ld(a.dpD, pb);
+      const double dsp = a.by_state ? ld(a.dpS, pb + s) : ld(a.dpS, pb);
+      const int c1 = child_at(a.c1, s, S), c2 = child_at(a.c2, s, S);
+      c1v[k] = c1;
+      c2v[k] = c2;
+      const double pl = ld(a.Pi, bl + s), pr = ld(a.Pi, br + s);
+      const double dpl = ld(a.dPi, bl + s), dpr = ld(a.dPi, br + s);
+      const double l1 = c1 >= 0 ? ld(a.Pi, bl + c1) : NI, r1 = c1 >= 0 ? ld(a.Pi, br + c1) : NI;
+      const double l2 = c2 >= 0 ? ld(a.Pi, bl + c2) : NI, r2 = c2 >= 0 ? ld(a.Pi, br + c2) : NI;
+      const double dl1 = c1 >= 0 ? ld(a.dPi, bl + c1) : 0.0, dr1 = c1 >= 0 ? ld(a.dPi, br + c1) : 0.0;
+      const double dl2 = c2 >= 0 ? ld(a.dPi, bl + c2) : 0.0, dr2 = c2 >= 0 ? ld(a.dPi, br + c2) : 0.0;
+      const double pbl = ld(a.Pb, bl + s), pbr = ld(a.Pb, br + s);
+      const double dpbl = ld(a.dPb, bl + s), dpbr = ld(a.dPb, br + s);
+      const double dk[5] = {d + pl + pr, pl + pbr, pr + pbl, sp + l1 + r2, sp + r1 + l2};
+      const double ddk[5] = {dd + dpl + dpr, dpl + dpbr, dpr + dpbl, dsp + dl1 + dr2, dsp + dr1 + dl2};
+      const double pp = ld(a.Pi, bp + s), dpp = ld(a.dPi, bp + s);
+      const double vv = ld(a.v, bv + s);
+      double wk[5], dv[5];
+#pragma unroll
+      for (int j = 0; j < 5; ++j) {
+        wk[j] = pp != NI ? exp2(lsp + dk[j] - pp) : 0.0;
+        dv[j] = wk[j] != 0.0 ? vv * LN2D * wk[j] * (ddk[j] - dpp) : 0.0;
+      }
+      L[s] = dv[0] + dv[1];
+      R[s] = dv[0] + dv[2];
+      d3[k] = dv[3];
+      d4[k] = dv[4];
+      const double mt = ld(a.mt, mb + s), dmt = ld(a.dmt, mb + s);
+      const double fl = pbl != NI ? exp2(rml + mt - pbl) : 0.0;
+      const double fr = pbr != NI ? exp2(rmr + mt - pbr) : 0.0;
+      const double vd1 = vv * wk[1], vd2 = vv * wk[2];
+      const size_t ol = (size_t)n * S + s, orr = (size_t)(N + n) * S + s;
+      a.ud[ol] = (T)(vd2 * fl);
+      a.ud[orr] = (T)(vd1 * fr);
+      a.dud[ol] = (T)(dv[2] * fl + (fl != 0.0 ? vd2 * LN2D * fl * (dmt - dpbl) : 0.0));
+      a.dud[orr] = (T)(dv[1] * fr + (fr != 0.0 ? vd1 * LN2D * fr * (dmt - dpbr) : 0.0));
+      a.pDrows[(size_t)n * S + s] = (T)dv[0];
+      a.pSrows[(size_t)n * S + s] = (T)(dv[3] + dv[4]);
+      a.mtrows[(size_t)n * S + s] = (T)(dv[1] + dv[2]);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    if (c1v[k] >= 0) {
+      L[c1v[k]] += d3[k];
+      R[c1v[k]] += d4[k];
+    }
+    if (c2v[k] >= 0) {
+      R[c2v[k]] += d3[k];
+      L[c2v[k]] += d4[k];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    if (s < S) {
+      a.side[(size_t)n * S + s] = (T)L[s];
+      a.side[(size_t)(N + n) * S + s] = (T)R[s];
+    }
+  }
+}
+
+// One workgroup per split side i (i < N: left child sl[i], else right child
+// sr[i - N]): contrib = dp' (A - sub) + p' (dA - dsub) over the staged ud / dud,
+// p' = 2^((col +) Pi_child - rowmax_child), dp' = ln2 p' dPi_child; added to
+// the side row and written as the side's column-gradient row.
+template <typename T, int CPT>
+__global__ __launch_bounds__(NT) void dso_tree_kernel(OpsTree t, DsoArgs<T> a) {
+  extern __shared__ double smd[];
+  double* buf = smd;
+  __shared__ double red[NW];
+  const int S = a.S;
+  const double NI = -__builtin_inf();
+  const long long i = blockIdx.x, N = a.N;
+  const long long child = i < N ? a.sl[i] : a.sr[i - N];
+  const size_t rb = (size_t)i * S, cbase = (size_t)child * S;
+  const double rm = ld(a.rowmax, child);
+  const double rms = rm == NI ? 0.0 : rm;
+  double x[CPT], dx[CPT];
+  double lA = 0.0, ldA = 0.0;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    x[k] = s < S ? ld(a.ud, rb + s) : 0.0;
+    dx[k] = s < S ? ld(a.dud, rb + s) : 0.0;
+    lA += x[k];
+    ldA += dx[k];
+  }
+  const double A = block_sum(lA, red);
+  const double dA = block_sum(ldA, red);
+  double sub[CPT], dsub[CPT];
+  reg_subtree_sums<CPT>(t, x, sub, buf, red);
+  reg_subtree_sums<CPT>(t, dx, dsub, buf, red);
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    if (s < S) {
+      const double pi = ld(a.Pi, cbase + s);
+      const double pp = pi != NI ? exp2(pi + (a.use_col ? ld(a.col, s) : 0.0) - rms) : 0.0;
+      const double c = LN2D * pp * ld(a.dPi, cbase + s) * (A - sub[k]) + pp * (dA - dsub[k]);
+      a.side[rb + s] = (T)(ld(a.side, rb + s) + c);
+      a.colrows[rb + s] = (T)c;
+    }
+  }
+}
+
+}  // namespace kbo
+
+using namespace kbo_host;
+
+extern "C" {
+
+int kb_estep_backward_so(const kb_tree* tr, const kb_estep_so_io* io, void* stream) {
+  if (!tr || !io) return kb::set_error(KB_ERR_ARG, "null argument");
+  if (int rc = dtype_ok(io->dtype)) return rc;
+  if (io->G < 0) return kb::set_error(KB_ERR_ARG, "G must be non-negative");
+  if (io->G == 0) return 0;
+  const int S = tr->S;
+  const size_t lds = (size_t)3 * S * sizeof(double);
+  if (int rc = check_lds(lds, S, KB_F64)) return rc;
+  const kbo::OpsTree t = tr->dev();
+  KBO_DISPATCH(io->dtype, S, {
+    kbo::EsoArgs<T> a{io->G, S, io->use_col_weights,
+                      (const T*)io->E, (const T*)io->E_new, (const T*)io->E_s1, (const T*)io->E_s2,
+                      (const T*)io->Ebar, (const T*)io->log_pS, (const T*)io->log_pD, (const T*)io->log_pL,
+                      (const T*)io->col_log_probs, (const T*)io->g_new, (const T*)io->g_ebar,
+                      (const T*)io->dE, (const T*)io->dE_new, (const T*)io->dE_s1, (const T*)io->dE_s2,
+                      (const T*)io->dEbar, (const T*)io->dlog_pS, (const T*)io->dlog_pD, (const T*)io->dlog_pL,
+                      (const T*)io->dcol, (T*)io->d_grad_E, (T*)io->d_grad_pS, (T*)io->d_grad_pD,
+                      (T*)io->d_grad_pL, (T*)io->d_grad_mc, (T*)io->col_rows};
+    if (int rc = set_lds(kbo::eso_kernel<T, CPT>, lds)) return rc;
+    hipLaunchKernelGGL((kbo::eso_kernel<T, CPT>), dim3(io->G), dim3(kbo::NT), lds, st_of(stream), t, a);
+  });
+  KBO_HIP(hipGetLastError());
+  return 0;
+}
+
+int kb_wave_backward_so(const kb_tree* tr, const kb_wave_so_io* io, void* stream) {
+  if (!tr || !io) return kb::set_error(KB_ERR_ARG, "null argument");
+  if (int rc = dtype_ok(io->dtype)) return rc;
+  if (io->S != tr->S) return kb::set_error(KB_ERR_ARG, "S=%d does not match the tree (%d)", io->S, tr->S);
+  if (io->W < 0) return kb::set_error(KB_ERR_ARG, "W must be non-negative");
+  if ((io->dts == nullptr) != (io->d_dts == nullptr))
+    return kb::set_error(KB_ERR_ARG, "dts and d_dts must be given together");
+  if (io->W == 0) return 0;
+  const int S = tr->S;
+  const size_t lds = (size_t)3 * S * sizeof(double);
+  if (int rc = check_lds(lds, S, KB_F64)) return rc;
+  const kbo::OpsTree t = tr->dev();
+  KBO_DISPATCH(io->dtype, S, {
+    kbo::WsoArgs<T> a{S, io->W, io->use_col_weights, io->use_leaf_index, io->ws, io->const_stride,
+                      (const T*)io->Pi, (const T*)io->dPi, (const T*)io->Pibar, (const T*)io->dPibar,
+                      (const T*)io->v, (const T*)io->pibar_row_max, (const T*)io->DL, (const T*)io->dDL,
+                      (const T*)io->Ebar, (const T*)io->dEbar, (const T*)io->E, (const T*)io->dE,
+                      (const T*)io->SL1, (const T*)io->dSL1, (const T*)io->SL2, (const T*)io->dSL2,
+                      (const T*)io->col_log_probs, io->item_idx, io->leaf_state, (const T*)io->leaf_logp,
+                      (const T*)io->dleaf_logp, (const T*)io->dts, (const T*)io->d_dts, (const T*)io->d_rhs,
+                      (T*)io->d_out, (T*)io->d_aw0, (T*)io->d_aw1, (T*)io->d_aw2, (T*)io->d_aw345,
+                      (T*)io->d_aw3, (T*)io->d_aw4};
+    if (int rc = set_lds(kbo::wso_kernel<T, CPT>, lds)) return rc;
+    hipLaunchKernelGGL((kbo::wso_kernel<T, CPT>), dim3(io->W), dim3(kbo::NT), lds, st_of(stream), t, a);
+  });
+  KBO_HIP(hipGetLastError());
+  return 0;
+}
+
+int kb_dts_backward_so(const kb_tree* tr, const kb_dts_so_io* io, void* stream) {
+  if (!tr || !io) return kb::set_error(KB_ERR_ARG, "null argument");
+  if (int rc = dtype_ok(io->dtype)) return rc;
+  if (io->S != tr->S) return kb::set_error(KB_ERR_ARG, "S=%d does not match the tree (%d)", io->S, tr->S);
+  if (io->N < 0) return kb::set_error(KB_ERR_ARG, "N must be non-negative");
+  if (io->N == 0) return 0;
+  if (io->N > (1LL << 30)) return kb::set_error(KB_ERR_ARG, "N=%lld too large", (long long)io->N);
+  const int S = tr->S;
+  const size_t lds2 = (size_t)2 * S * sizeof(double), lds1 = (size_t)S * sizeof(double);
+  if (int rc = check_lds(lds2, S, KB_F64)) return rc;
+  const kbo::OpsTree t = tr->dev();
+  KBO_DISPATCH(io->dtype, S, {
+    kbo::DsoArgs<T> a{S, io->param_by_state, io->use_col_weights, io->N, io->ws, io->item_offset,
+                      io->param_row_stride, io->mt_row_stride,
+                      (const T*)io->Pi, (const T*)io->dPi, (const T*)io->Pibar, (const T*)io->dPibar,
+                      (const T*)io->v, (const T*)io->log_split_probs, (const T*)io->log_pD, (const T*)io->log_pS,
+                      (const T*)io->dlog_pD, (const T*)io->dlog_pS, (const T*)io->mt, (const T*)io->dmt,
+                      (const T*)io->pibar_row_max, (const T*)io->col_log_probs,
+                      io->sl, io->sr, io->reduce_idx, io->item_idx, io->node_child1, io->node_child2,
+                      (T*)io->ud, (T*)io->dud, (T*)io->side_rows, (T*)io->col_rows, (T*)io->pD_rows,
+                      (T*)io->pS_rows, (T*)io->mt_rows};
+    if (int rc = set_lds(kbo::dso_split_kernel<T, CPT>, lds2)) return rc;
+    hipLaunchKernelGGL((kbo::dso_split_kernel<T, CPT>), dim3((unsigned)io->N), dim3(kbo::NT), lds2,
+                       st_of(stream), a);
+    if (int rc = set_lds(kbo::dso_tree_kernel<T, CPT>, lds1)) return rc;
+    hipLaunchKernelGGL((kbo::dso_tree_kernel<T, CPT>), dim3((unsigned)(2 * io->N)), dim3(kbo::NT), lds1,
+                       st_of(stream), t, a);
+  });
+  KBO_HIP(hipGetLastError());
+  return 0;
+}
+
+}  // extern "C"

@@ -22,34 +22,6 @@
 
 namespace kbo {
 
-// Ancestors-or-self path sums of per-state register values x[k] (state
-// threadIdx.x + k * NT): written as +x at the entry event and -x at the exit
-// event of each column, scanned, read back at the entry event.  Enters with
-// ev2 free; ends with a barrier after which ev2 may be reused.
-template <int CPT>
-__device__ void reg_path_sums(const OpsTree& t, const double (&x)[CPT], double (&ps)[CPT], double* ev2,
-                              double* red) {
-  const int S = t.S;
-#pragma unroll
-  for (int k = 0; k < CPT; ++k) {
-    const int s = threadIdx.x + k * NT;
-    if (s < S) {
-      const int tin = t.tin[s];
-      const int tout = tin + 2 * (t.pend[s] - t.ppos[s]) - 1;
-      ev2[tin] = x[k];
-      ev2[tout] = -x[k];
-    }
-  }
-  __syncthreads();
-  block_scan(ev2, 2 * S, red);
-#pragma unroll
-  for (int k = 0; k < CPT; ++k) {
-    const int s = threadIdx.x + k * NT;
-    ps[k] = s < S ? ev2[t.tin[s]] : 0.0;
-  }
-  __syncthreads();
-}
-
 // ---- E-step tangent fixed point ------------------------------------------------------
 
 template <typename T>

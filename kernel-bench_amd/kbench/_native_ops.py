@@ -98,6 +98,29 @@ class KbWaveTanIO(ct.Structure):
         "dleaf_logp")
 
 
+class KbEStepSoIO(ct.Structure):
+    _fields_ = [("dtype", i32), ("G", i32), ("use_col_weights", i32)] + _ptrs(
+        "E", "E_new", "E_s1", "E_s2", "Ebar", "log_pS", "log_pD", "log_pL", "col_log_probs", "g_new", "g_ebar",
+        "dE", "dE_new", "dE_s1", "dE_s2", "dEbar", "dlog_pS", "dlog_pD", "dlog_pL", "dcol",
+        "d_grad_E", "d_grad_pS", "d_grad_pD", "d_grad_pL", "d_grad_mc", "col_rows")
+
+
+class KbWaveSoIO(ct.Structure):
+    _fields_ = [("dtype", i32), ("S", i32), ("W", i32), ("use_col_weights", i32), ("use_leaf_index", i32),
+                ("ws", i64), ("const_stride", i64)] + _ptrs(
+        "Pi", "dPi", "Pibar", "dPibar", "v", "pibar_row_max", "DL", "dDL", "Ebar", "dEbar", "E", "dE", "SL1", "dSL1",
+        "SL2", "dSL2", "col_log_probs", "item_idx", "leaf_state", "leaf_logp", "dleaf_logp", "dts", "d_dts", "d_rhs",
+        "d_out", "d_aw0", "d_aw1", "d_aw2", "d_aw345", "d_aw3", "d_aw4")
+
+
+class KbDtsSoIO(ct.Structure):
+    _fields_ = [("dtype", i32), ("S", i32), ("param_by_state", i32), ("use_col_weights", i32), ("N", i64),
+                ("ws", i64), ("item_offset", i64), ("param_row_stride", i64), ("mt_row_stride", i64)] + _ptrs(
+        "Pi", "dPi", "Pibar", "dPibar", "v", "sl", "sr", "reduce_idx", "log_split_probs", "log_pD", "log_pS",
+        "dlog_pD", "dlog_pS", "mt", "dmt", "item_idx", "pibar_row_max", "col_log_probs", "node_child1",
+        "node_child2", "ud", "dud", "side_rows", "col_rows", "pD_rows", "pS_rows", "mt_rows")
+
+
 def declare(lib) -> None:
     def fn(name, argtypes, restype=ct.c_int):
         f = getattr(lib, name)
@@ -121,3 +144,6 @@ def declare(lib) -> None:
     fn("kb_e_tangent_fixed_point", [vp, ct.POINTER(KbETanIO), vp])
     fn("kb_dts_tangent", [ct.POINTER(KbDtsTanIO), vp])
     fn("kb_wave_step_tangent", [vp, ct.POINTER(KbWaveTanIO), vp])
+    fn("kb_estep_backward_so", [vp, ct.POINTER(KbEStepSoIO), vp])
+    fn("kb_wave_backward_so", [vp, ct.POINTER(KbWaveSoIO), vp])
+    fn("kb_dts_backward_so", [vp, ct.POINTER(KbDtsSoIO), vp])

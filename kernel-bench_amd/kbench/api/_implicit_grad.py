@@ -114,6 +114,39 @@ def implicit_grad_loglik_vjp_wave(wave_layout, state_helpers, *, Pi_star_wave, P
     if side_thr < 0.0:
         raise ValueError("pibar_side_threshold must be non-negative")
 
+    roots = wave_layout["root_row_ids"]
+    root_pi = Pi_star_wave.index_select(0, roots)
+    seed = -_safe_exp2_ratio(root_pi, _logsumexp2(root_pi, dim=-1, keepdim=True))
+    acc = _reverse_wave_sweep(
+        wave_layout, state_helpers, Pi_star_wave=Pi_star_wave, Pibar_star_wave=Pibar_star_wave, E_star=E_star,
+        E_s1=E_s1, E_s2=E_s2, Ebar=Ebar, log_pS=log_pS, log_pD=log_pD, max_coupling_mat=max_coupling_mat,
+        col_log_probs=col_log_probs, use_col_weights=use_col_weights, uniform_pibar_row_max=uniform_pibar_row_max,
+        item_idx=item_idx, seed_root=seed, neumann_terms=neumann_terms, self_loop_solver=self_loop_solver,
+        adjoint_pruning_threshold=thr, use_adjoint_pruning=use_adjoint_pruning, pibar_side_threshold=side_thr,
+        collect_backward_relres=collect_backward_relres)
+    if collect_backward_relres:
+        return acc
+    return _e_adjoint_and_theta_vjp(
+        E_star, log_pS, log_pD, log_pL, max_coupling_mat, col_log_probs, use_col_weights, acc["grad_E"],
+        acc["grad_Ebar"], acc["grad_E_s1"], acc["grad_E_s2"], acc["grad_log_pD"], acc["grad_log_pS"], acc["grad_mc"],
+        acc["grad_col"], int(roots.numel()), theta, col_weights, state_helpers, statewise=statewise,
+        itemwise=itemwise, bicgstab_max_iter=bicgstab_max_iter, bicgstab_tol=bicgstab_tol,
+        bicgstab_breakdown_tol=bicgstab_breakdown_tol)
+
+
+@torch.no_grad()
+def _reverse_wave_sweep(wave_layout, state_helpers, *, Pi_star_wave, Pibar_star_wave, E_star, E_s1, E_s2, Ebar,
+                        log_pS, log_pD, max_coupling_mat, col_log_probs, use_col_weights, uniform_pibar_row_max,
+                        item_idx, seed_root, neumann_terms, self_loop_solver, adjoint_pruning_threshold,
+                        use_adjoint_pruning, pibar_side_threshold, collect_backward_relres=False, cache=None):
+    """Reverse wave sweep of the adjoint from a root-row seed (reference _implicit_grad.py:199-353).
+
+    Returns the accumulated cotangents (grad_E, grad_Ebar, grad_E_s1, grad_E_s2, grad_log_pD,
+    grad_log_pS, grad_mc, grad_col).  With ``cache`` (a dict) every wave's adjoint (inactive
+    rows zeroed), split term and active mask are appended to ``cache["waves"]`` in sweep order
+    (the point cache of newton/ggn.py:41-210).
+    """
+    thr, side_thr = float(adjoint_pruning_threshold), float(pibar_side_threshold)
     C, S = Pi_star_wave.shape
     dev, dt = Pi_star_wave.device, Pi_star_wave.dtype
     G = int(E_star.shape[0])
@@ -130,8 +163,7 @@ def implicit_grad_loglik_vjp_wave(wave_layout, state_helpers, *, Pi_star_wave, P
     g_E, g_Ebar, g_Es1, g_Es2 = (torch.zeros_like(x) for x in (E_star, Ebar, E_star, E_star))
 
     roots = wave_layout["root_row_ids"]
-    root_pi = Pi_star_wave.index_select(0, roots)
-    rhs_all.index_copy_(0, roots, -_safe_exp2_ratio(root_pi, _logsumexp2(root_pi, dim=-1, keepdim=True)))
+    rhs_all.index_copy_(0, roots, seed_root.to(dt))
 
     def add_rows(acc, items, contrib):
         contrib = contrib.to(acc.dtype)
@@ -195,6 +227,11 @@ def implicit_grad_loglik_vjp_wave(wave_layout, state_helpers, *, Pi_star_wave, P
                 relres_fam.scatter_reduce_(0, items_w, last.float(), reduce="amax", include_self=True)
         else:
             v_k, aw0, aw1, aw2, aw345, aw3, aw4 = out
+        if cache is not None:
+            on = active.reshape(W, -1).ne(0).any(dim=1)
+            cache.setdefault("waves", []).append(dict(
+                ws=ws, W=W, v=torch.where(on.unsqueeze(1), v_k, torch.zeros_like(v_k)), dts_r=dts_r,
+                active_mask=active, has_splits=has_splits, has_leaf_term=has_leaf, meta=meta))
         items = item_idx[ws: ws + W]
         add_rows(g_pD, items, aw0)
         add_rows(g_pS, items, aw345)
@@ -222,32 +259,36 @@ def implicit_grad_loglik_vjp_wave(wave_layout, state_helpers, *, Pi_star_wave, P
                 use_col_weights=use_col_weights, side_active_threshold=side_thr)
     if collect_backward_relres:
         return relres_fam, vk_fam
-    return _e_adjoint_and_theta_vjp(
-        E_star, log_pS, log_pD, log_pL, max_coupling_mat, col_log_probs, use_col_weights, g_E, g_Ebar, g_Es1,
-        g_Es2, g_pD, g_pS, g_mt, g_col, int(roots.numel()), theta, col_weights, state_helpers,
-        statewise=statewise, itemwise=itemwise, bicgstab_max_iter=bicgstab_max_iter, bicgstab_tol=bicgstab_tol,
-        bicgstab_breakdown_tol=bicgstab_breakdown_tol)
+    return dict(grad_E=g_E, grad_Ebar=g_Ebar, grad_E_s1=g_Es1, grad_E_s2=g_Es2, grad_log_pD=g_pD, grad_log_pS=g_pS,
+                grad_mc=g_mt, grad_col=g_col)
 
 
 def _e_adjoint_and_theta_vjp(E_star, log_pS, log_pD, log_pL, max_coupling_mat, col_log_probs, use_col_weights,
                              grad_E, grad_Ebar, grad_E_s1, grad_E_s2, grad_log_pD, grad_log_pS,
                              grad_max_coupling_mat, grad_col_log_probs, n_fam, theta, col_weights, state_helpers, *,
                              statewise, itemwise, bicgstab_max_iter=500, bicgstab_tol=1e-7,
-                             bicgstab_breakdown_tol=1e-30):
-    """E adjoint by BiCGSTAB on (I - J_E^T) w = q_E, then the theta / column VJP (reference _implicit_grad.py:372-475)."""
+                             bicgstab_breakdown_tol=1e-30, drop_norm=False, cache=None):
+    """E adjoint by BiCGSTAB on (I - J_E^T) w = q_E, then the theta / column VJP (reference _implicit_grad.py:372-475).
+
+    ``drop_norm`` leaves out the loss's explicit log2(1 - mean 2^E) term (a root-score
+    cotangent instead of the loss, newton/ggn.py:213-244); ``cache`` receives the E-side
+    adjoint (``cache["e_side"]``: q_E, wE, aux_to_e).
+    """
     topo = (state_helpers["node_parent"], state_helpers["node_child1"], state_helpers["node_child2"],
             int(state_helpers["max_ancestor_depth"]))
     E_req = E_star.detach().requires_grad_(True)
     with torch.enable_grad():
         E_new, Es1_new, Es2_new, Ebar_new = e_step_triton_autograd(
             E_req, log_pS, log_pD, log_pL, max_coupling_mat, col_log_probs, *topo, use_col_weights=use_col_weights)
-        norm = (1 - torch.exp2(E_req).mean(dim=-1)).clamp_min(torch.finfo(E_req.dtype).tiny)
-        denom = torch.log2(norm)
-        direct = denom.sum() if E_req.shape[0] == n_fam else (n_fam * denom).sum()
-        (aux,) = torch.autograd.grad((direct, Es1_new, Es2_new, Ebar_new), E_req,
-                                     grad_outputs=(torch.ones_like(direct), grad_E_s1, grad_E_s2, grad_Ebar),
-                                     retain_graph=True)
-    q = (grad_E + aux).reshape(-1)
+        outs, gouts = (Es1_new, Es2_new, Ebar_new), (grad_E_s1, grad_E_s2, grad_Ebar)
+        if not drop_norm:
+            norm = (1 - torch.exp2(E_req).mean(dim=-1)).clamp_min(torch.finfo(E_req.dtype).tiny)
+            denom = torch.log2(norm)
+            direct = denom.sum() if E_req.shape[0] == n_fam else (n_fam * denom).sum()
+            outs, gouts = (direct, *outs), (torch.ones_like(direct), *gouts)
+        (aux,) = torch.autograd.grad(outs, E_req, grad_outputs=gouts, retain_graph=True)
+    q_E = grad_E + aux
+    q = q_E.reshape(-1)
     shape = E_star.shape
 
     def apply(w_flat):
@@ -258,6 +299,8 @@ def _e_adjoint_and_theta_vjp(E_star, log_pS, log_pD, log_pL, max_coupling_mat, c
 
     wE = _bicgstab(apply, q, max_iter=bicgstab_max_iter, tol=bicgstab_tol,
                    breakdown_tol=bicgstab_breakdown_tol).view(shape)
+    if cache is not None:
+        cache["e_side"] = dict(q_E=q_E, wE=wE, aux_to_e=aux)
 
     theta_req = theta.detach().requires_grad_(True)
     col_req = col_weights.detach().requires_grad_(True)

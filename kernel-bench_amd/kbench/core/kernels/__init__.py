@@ -13,6 +13,9 @@ signatures):
 * ``dts_tangent`` -- dts_tangent.py (``compute_dts_tangent``)
 * ``wave_tangent`` -- wave_tangent.py (``compute_wave_step_tangent``,
   ``compute_wave_step_tangent_selfloop``)
+* ``e_step_so`` -- e_step_so.py (``e_step_backward_so``)
+* ``wave_so`` -- wave_so.py (``wave_backward_so``)
+* ``dts_so`` -- dts_so.py (``dts_backward_so``)
 * ``_dts_layout_contract`` -- _dts_layout_contract.py (host-side layout codes)
 
 The native launchers are declared in include/kbench_ops.h.

@@ -19,12 +19,14 @@ from collections import OrderedDict
 import torch
 
 from ... import _native as N
-from ..._native_ops import (KB_BF16, KB_F32, KB_F64, KbDtsCrossIO, KbDtsIO, KbDtsTanIO, KbEStepIO, KbEStepVjpIO,
-                            KbETanIO, KbLeafInitIO, KbPibarVjpIO, KbWaveBwdIO, KbWaveStepIO, KbWaveTanIO)
+from ..._native_ops import (KB_BF16, KB_F32, KB_F64, KbDtsCrossIO, KbDtsIO, KbDtsSoIO, KbDtsTanIO, KbEStepIO,
+                            KbEStepSoIO, KbEStepVjpIO, KbETanIO, KbLeafInitIO, KbPibarVjpIO, KbWaveBwdIO, KbWaveSoIO,
+                            KbWaveStepIO, KbWaveTanIO)
 
 __all__ = [
     "KB_BF16", "KB_F32", "KB_F64", "KbDtsCrossIO", "KbDtsIO", "KbEStepIO", "KbEStepVjpIO", "KbLeafInitIO",
-    "KbPibarVjpIO", "KbWaveBwdIO", "KbWaveStepIO", "KbETanIO", "KbDtsTanIO", "KbWaveTanIO",
+    "KbPibarVjpIO", "KbWaveBwdIO", "KbWaveStepIO", "KbETanIO", "KbDtsTanIO", "KbWaveTanIO", "KbEStepSoIO",
+    "KbWaveSoIO", "KbDtsSoIO",
     "lib", "check", "ptr", "stream", "dtype_code", "require_device", "f", "i64", "tree_from_parent",
     "tree_from_levels", "scatter_add_rows", "sum_rows_into",
 ]

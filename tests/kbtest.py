@@ -72,3 +72,15 @@ def norm_rel(got, ref):
     ref = np.asarray(ref, dtype=np.float64)
     den = max(float(np.abs(ref).max()), 1e-300)
     return float(np.abs(got - ref).max()) / den
+
+
+@functools.lru_cache(maxsize=None)
+def oracle_point_cache(name: str, statewise: bool | None = None):
+    """Oracle backward at the generated theta with the per-wave adjoint cache of the exact HVP."""
+    import kbench_oracle as O
+
+    p = problem(name, statewise)
+    prob, loss, saved = oracle_forward(name, statewise)
+    theta = np.asarray(p["inputs"]["theta"], dtype=np.float32).astype(np.float64)
+    cw = np.asarray(p["inputs"]["col_weights"], dtype=np.float64)
+    return O.build_point_cache(prob, theta, cw, saved)

@@ -1,0 +1,262 @@
+"""GPU parity of the second-order wrappers (kbench.core.kernels.{e_step,wave,dts}_so) and of the
+exact / Gauss-Newton HVP glue (newton.hvp_exact, newton.ggn) against the float64 CPU oracle.
+
+Kernel tests feed the oracle's primal point and random tangents / cotangents
+to the HIP wrappers in float64 (tight tolerance) and float32 (rel 1e-4).  The
+exact HVP runs the glue on the GPU's own fp32 forward and is compared with
+the oracle's HVP at the oracle's forward; at config 3 (the S = 2047 per-species
+setup of the Newton-CG benchmark) by symmetry, linearity and determinism.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import kbench_oracle as O
+import kbtest
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float64: 1e-9, torch.float32: 1e-4}
+
+
+def _static(name, statewise=None):
+    from kbench.fused import problem_to_captured
+    from kbench.runtime import make_static
+
+    p = kbtest.problem(name, statewise)
+    cap = problem_to_captured(p)
+    static = make_static(cap, "cuda")
+    return static, cap["inputs"]["theta"].cuda(), cap["inputs"]["col_weights"].cuda()
+
+
+def _t(x, dt):
+    return torch.as_tensor(np.ascontiguousarray(x), dtype=dt, device="cuda")
+
+
+def _rel(got, ref):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert got.shape == ref.shape, (got.shape, ref.shape)
+    assert np.isfinite(got).all()
+    return float(np.abs(got - ref).max()) / max(1.0, float(np.abs(ref).max()))
+
+
+@pytest.mark.parametrize("dt", [torch.float64, torch.float32])
+@pytest.mark.parametrize("use_col", [False, True])
+def test_e_step_backward_so_matches_oracle(dt, use_col):
+    from kbench.core.kernels.e_step_so import e_step_backward_so
+
+    print(f"[e-so] dtype={dt} use_col={use_col}", flush=True)
+    static, _, _ = _static("1")
+    prob, _, _ = kbtest.oracle_forward("1")
+    rng = np.random.default_rng(31)
+    S, G, tree = prob.S, 3, prob.tree
+    E = np.log2(rng.uniform(0.05, 0.6, (G, S)))
+    pS, pD, pL, mt = (rng.uniform(-4, -0.5, (G, S)) for _ in range(4))
+    col = rng.uniform(-1, 1, S)
+    En, Es1, Es2, Eb = O.e_step(E, pS, pD, pL, mt, col, tree, use_col)
+    gN, gB = rng.normal(size=(G, S)), rng.normal(size=(G, S))
+    dE, dEn, dEs1, dEs2, dEb, dpS, dpD, dpL = (rng.normal(size=(G, S)) for _ in range(8))
+    dEs1 = np.where(np.isfinite(Es1), dEs1, 0.0)
+    dEs2 = np.where(np.isfinite(Es2), dEs2, 0.0)
+    dEb = np.where(np.isfinite(Eb), dEb, 0.0)
+    dcol = rng.normal(size=S)
+    ref = O.e_step_backward_so(E, En, Es1, Es2, Eb, pS, pD, pL, col, tree, gN, gB, dE, dEn, dEs1, dEs2, dEb, dpS, dpD,
+                               dpL, dcol, use_col)
+    h = static.state_helpers
+    got = e_step_backward_so(*(_t(x, dt) for x in (E, En, Es1, Es2, Eb, pS, pD, pL, col)), h["node_parent"],
+                             h["node_child1"], h["node_child2"], int(h["max_ancestor_depth"]), _t(gN, dt), None, None,
+                             _t(gB, dt), *(_t(x, dt) for x in (dE, dEn, dEs1, dEs2, dEb, dpS, dpD, dpL, dcol)),
+                             use_col_weights=use_col)
+    torch.cuda.synchronize()
+    for name, g, r in zip(("dE", "dpS", "dpD", "dpL", "dmc", "dcol"), got, ref):
+        e = _rel(g.cpu().numpy(), r)
+        print(f"  {name}: rel={e:.3e}")
+        assert e <= TOL[dt]
+
+
+def _wave_consts(prob, saved, rng):
+    S, G = prob.S, 1
+    E = np.asarray(saved["E"])
+    st = lambda x: np.broadcast_to(O.as_item_state(np.asarray(x, dtype=np.float64), S, G), (G, S)).copy()
+    pS, pD, mt = st(saved["log_pS"]), st(saved["log_pD"]), st(saved["max_coupling"])
+    consts = O.WaveConsts(mt=mt, DL=1.0 + pD + E, Ebar=np.asarray(saved["Ebar"]), E=E, SL1=pS + saved["E_s2"],
+                          SL2=pS + saved["E_s1"], leaf_logp=pS, col=np.zeros(S), use_col_weights=False)
+    dc = O.WaveTangentConsts(*(0.3 * rng.normal(size=(G, S)) for _ in range(7)))
+    return consts, dc
+
+
+@pytest.mark.parametrize("dt", [torch.float64, torch.float32])
+def test_wave_backward_so_matches_oracle(dt):
+    from kbench.core.kernels.wave_so import wave_backward_so
+
+    print(f"[wave-so] config=1 dtype={dt}", flush=True)
+    static, _, _ = _static("1")
+    prob, _, saved = kbtest.oracle_forward("1")
+    rng = np.random.default_rng(32)
+    S, G, C = prob.S, 1, prob.C
+    consts, dc = _wave_consts(prob, saved, rng)
+    Pi, Pb, rmax = saved["pi_wave"], saved["pibar_wave"], saved["pibar_row_max"]
+    fd_dir = lambda X: np.where(np.isfinite(X), rng.normal(size=X.shape), 0.0)
+    dPi, dPb = fd_dir(Pi), fd_dir(Pb)
+    d_rhs = rng.normal(size=(C, S))
+    h = static.state_helpers
+    cargs = [_t(x, dt) for x in (consts.mt, consts.DL, dc.dDL, consts.Ebar, dc.dEbar, consts.E, dc.dE, consts.SL1,
+                                  dc.dSL1, consts.SL2, dc.dSL2)]
+    pDp = O.as_item_param(np.asarray(saved["log_pD"]), G, S)
+    pSp = O.as_item_param(np.asarray(saved["log_pS"]), G, S)
+    worst = 0.0
+    n_w = len(prob.wave_metas)
+    for i in (0, 1, n_w // 2, n_w - 1):
+        mo = prob.wave_metas[i]
+        ws, W = int(mo["start"]), int(mo["W"])
+        rows = np.arange(ws, ws + W)
+        split = "sl" in mo
+        leaf = None if split else prob.leaf_state[rows]
+        dts = d_dts = None
+        if split:
+            dts = O.dts_forward(Pi, Pb, mo, W, pDp, pSp, prob.item_idx, ws, prob.tree)
+            d_dts = fd_dir(dts)
+        v = rng.normal(size=(W, S))
+        ref = O.wave_backward_so(Pi[rows], dPi[rows], Pb[rows], dPb[rows], v, rmax[rows], prob.item_idx[rows], consts,
+                                 dc, prob.tree, leaf_state=leaf, dts_r=dts, d_dts=d_dts, rhs_rows=d_rhs[rows])
+        got = wave_backward_so(_t(Pi, dt), _t(dPi, dt), _t(Pb, dt), _t(dPb, dt), _t(v, dt), ws, W, S, _t(rmax, dt),
+                               *cargs, None, h["node_child1"], h["node_child2"], h["node_parent"],
+                               int(h["max_ancestor_depth"]), None if dts is None else _t(dts, dt),
+                               None if d_dts is None else _t(d_dts, dt),
+                               leaf_state_idx=static.wave_layout["leaf_state_index"], leaf_logp=_t(consts.leaf_logp, dt),
+                               dleaf_logp=_t(dc.dleaf, dt), item_idx=static.rate_item_idx, has_leaf_term=not split,
+                               use_col_weights=False, d_rhs=_t(d_rhs, dt))
+        torch.cuda.synchronize()
+        for g, r in zip(got, ref):
+            worst = max(worst, _rel(g.cpu().numpy(), r))
+    print(f"  worst rel={worst:.3e}")
+    assert worst <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", [torch.float64, torch.float32])
+@pytest.mark.parametrize("statewise", [False, True])
+def test_dts_backward_so_matches_oracle(dt, statewise):
+    from kbench.core.kernels.dts_so import dts_backward_so
+
+    print(f"[dts-so] config=1 statewise={statewise} dtype={dt}", flush=True)
+    static, _, _ = _static("1", statewise)
+    prob, _, saved = kbtest.oracle_forward("1", statewise)
+    rng = np.random.default_rng(33)
+    S, G, C = prob.S, 1, prob.C
+    consts, dc = _wave_consts(prob, saved, rng)
+    Pi, Pb, rmax = saved["pi_wave"], saved["pibar_wave"], saved["pibar_row_max"]
+    fd_dir = lambda X: np.where(np.isfinite(X), rng.normal(size=X.shape), 0.0)
+    dPi, dPb = fd_dir(Pi), fd_dir(Pb)
+    pDp = O.as_item_param(np.asarray(saved["log_pD"]), G, S)
+    pSp = O.as_item_param(np.asarray(saved["log_pS"]), G, S)
+    dpD, dpS = rng.normal(size=pDp.shape), rng.normal(size=pSp.shape)
+    h = static.state_helpers
+    metas_t = static.wave_layout["wave_metas"]
+    worst = 0.0
+    picks = [i for i, m in enumerate(prob.wave_metas) if "sl" in m]
+    for i in picks[:: max(1, len(picks) // 5)]:
+        mo, mt_ = prob.wave_metas[i], metas_t[i]
+        ws, W = int(mo["start"]), int(mo["W"])
+        v = rng.normal(size=(W, S))
+        ref = O.dts_backward_so(Pi, dPi, Pb, dPb, v, ws, mo, pDp, pSp, dpD, dpS, consts.mt, dc.dMC, consts.col, rmax,
+                                prob.item_idx, prob.tree)
+        r_rhs = np.zeros((C, S))
+        np.add.at(r_rhs, np.asarray(mo["sl"]), ref["d_rhs_l"])
+        np.add.at(r_rhs, np.asarray(mo["sr"]), ref["d_rhs_r"])
+        d_rhs = torch.zeros((C, S), dtype=dt, device="cuda")
+        g_pD, g_pS = torch.zeros(pDp.shape, dtype=dt, device="cuda"), torch.zeros(pSp.shape, dtype=dt, device="cuda")
+        g_mt, g_col = torch.zeros((G, S), dtype=dt, device="cuda"), torch.zeros(S, dtype=dt, device="cuda")
+        meta = dict(mt_)
+        if mo.get("log_split_probs") is not None:
+            meta["log_split_probs"] = _t(np.asarray(mo["log_split_probs"]), dt)
+        dts_backward_so(_t(Pi, dt), _t(dPi, dt), _t(Pb, dt), _t(dPb, dt), _t(v, dt), ws, meta, S, _t(pDp, dt),
+                        _t(pSp, dt), _t(dpD, dt), _t(dpS, dt), _t(consts.mt, dt), _t(dc.dMC, dt),
+                        torch.zeros(S, dtype=dt, device="cuda"), h["node_child1"], h["node_child2"],
+                        h["node_parent"], int(h["max_ancestor_depth"]), _t(rmax, dt), static.rate_item_idx, d_rhs,
+                        g_pD, g_pS, g_mt, g_col)
+        torch.cuda.synchronize()
+        red = lambda x, shape: x.sum(axis=0).reshape(shape) if shape[-1] != 1 else np.array(x.sum()).reshape(shape)
+        pairs = [(d_rhs, r_rhs), (g_pD, red(ref["d_pD"], pDp.shape)), (g_pS, red(ref["d_pS"], pSp.shape)),
+                 (g_mt, ref["d_mt"].sum(axis=0).reshape(1, S)), (g_col, ref["d_col"])]
+        for g, r in pairs:
+            worst = max(worst, _rel(g.cpu().numpy(), r))
+    print(f"  worst rel={worst:.3e}")
+    assert worst <= TOL[dt]
+
+
+@pytest.mark.parametrize("name,statewise", [("tiny", None), ("tiny", True), ("1", True)])
+def test_exact_hvp_matches_oracle(name, statewise):
+    from kbench.runtime import run_forward
+    from newton.hvp_exact import make_exact_hvp
+
+    print(f"[hvp] config={name} statewise={statewise}", flush=True)
+    static, theta, cw = _static(name, statewise)
+    _, sv = run_forward(static, theta, cw)
+    hvp = make_exact_hvp(static, theta, cw, sv)
+    u = np.random.default_rng(34).normal(size=tuple(theta.shape))
+    Hu = hvp(torch.as_tensor(u, dtype=theta.dtype).cuda().reshape(-1))
+    torch.cuda.synchronize()
+    prob, _, saved = kbtest.oracle_forward(name, statewise)
+    _, _, cache = kbtest.oracle_point_cache(name, statewise)
+    th = np.asarray(kbtest.problem(name, statewise)["inputs"]["theta"], dtype=np.float32).astype(np.float64)
+    ref = O.hvp_exact(prob, th, saved, u, cache)
+    e = _rel(Hu.cpu().numpy(), ref.reshape(-1))
+    print(f"  |H u| = {np.abs(ref).max():.4e} rel={e:.3e}")
+    assert e <= 1e-3
+
+
+def test_exact_hvp_config3_symmetric_linear_deterministic():
+    """Full size (config 3 with per-species theta, the Newton-CG setup): symmetry, linearity, determinism."""
+    import time
+
+    from kbench.runtime import run_forward
+    from newton.hvp_exact import make_exact_hvp
+
+    print("[hvp] config=3 statewise=True", flush=True)
+    static, theta, cw = _static("3", True)
+    _, sv = run_forward(static, theta, cw)
+    t0 = time.perf_counter()
+    hvp = make_exact_hvp(static, theta, cw, sv)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    g = np.random.default_rng(35)
+    u1 = torch.as_tensor(g.normal(size=tuple(theta.shape)), dtype=theta.dtype).cuda().reshape(-1)
+    u2 = torch.as_tensor(g.normal(size=tuple(theta.shape)), dtype=theta.dtype).cuda().reshape(-1)
+    H1 = hvp(u1)
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    H1b = hvp(u1)
+    H2 = hvp(u2)
+    H12 = hvp(u1 + 2.0 * u2)
+    torch.cuda.synchronize()
+    print(f"  point cache {1e3 * (t1 - t0):.1f} ms, one HVP {1e3 * (t2 - t1):.1f} ms")
+    assert torch.equal(H1, H1b)
+    assert torch.isfinite(H1).all() and torch.isfinite(H2).all()
+    a, b = float((u2.double() * H1.double()).sum()), float((u1.double() * H2.double()).sum())
+    scale = max(abs(a), abs(b), 1e-30)
+    print(f"  u2.H u1={a:.6e} u1.H u2={b:.6e} asym={abs(a - b) / scale:.3e}")
+    assert abs(a - b) <= 5e-3 * scale
+    lin = _rel(H12.cpu().numpy(), (H1 + 2.0 * H2).cpu().numpy())
+    print(f"  linearity rel={lin:.3e}")
+    assert lin <= 1e-4
+
+
+def test_ggn_hvp_is_symmetric_and_psd():
+    from kbench.runtime import run_forward
+    from newton.ggn import make_ggn_hvp
+
+    static, theta, cw = _static("1", True)
+    _, sv = run_forward(static, theta, cw)
+    hvp = make_ggn_hvp(static, theta, cw, sv)
+    g = np.random.default_rng(36)
+    u1 = torch.as_tensor(g.normal(size=tuple(theta.shape)), dtype=theta.dtype).cuda().reshape(-1)
+    u2 = torch.as_tensor(g.normal(size=tuple(theta.shape)), dtype=theta.dtype).cuda().reshape(-1)
+    M1, M2 = hvp(u1), hvp(u2)
+    torch.cuda.synchronize()
+    a, b = float((u2.double() * M1.double()).sum()), float((u1.double() * M2.double()).sum())
+    q1 = float((u1.double() * M1.double()).sum())
+    print(f"  u2.M u1={a:.6e} u1.M u2={b:.6e} u1.M u1={q1:.6e}")
+    assert abs(a - b) <= 1e-3 * max(abs(a), abs(b), 1e-30)
+    assert q1 >= -1e-6 * abs(q1)

@@ -45,6 +45,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-families", type=int, default=20)
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--workload", choices=("solve", "glue", "hvp"), default="solve",
+                    help="solve: whole-pass driver (the metric); glue: the same solve through the per-wrapper "
+                         "drop-in path; hvp: exact Hessian-vector products of the config-5 Newton-CG setup")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 5 plain copy kernels of MIB MiB (read + write), the reference point "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters to HBM bytes")
@@ -102,6 +105,62 @@ def cpu_baseline(args, full_rows: int) -> dict:
     }
 
 
+def bench_other(args, static, theta, cw, summ) -> None:
+    """Secondary workloads (not the metric): the per-wrapper solve and the exact HVP."""
+    import numpy as np
+    import torch
+
+    from kbench.runtime import run_backward, run_forward
+
+    cfg = {"S_columns": summ["S"], "C": summ["C"], "n_waves": summ["n_waves"], "n_splits": summ["n_splits"]}
+    if args.workload == "glue":
+        def step():
+            loss, sv = run_forward(static, theta, cw)
+            run_backward(static, theta, cw, sv)
+            return loss
+
+        metric = "fwd+bwd ms per solve through the per-wrapper drop-in path (reference glue call sequence)"
+    else:
+        from newton.hvp_exact import make_exact_hvp
+
+        loss, sv = run_forward(static, theta, cw)
+        t0 = time.perf_counter()
+        hvp = make_exact_hvp(static, theta, cw, sv)
+        torch.cuda.synchronize()
+        cfg["point_cache_ms"] = round((time.perf_counter() - t0) * 1e3, 3)
+        g = np.random.default_rng(0)
+        us = [torch.as_tensor(g.normal(size=tuple(theta.shape)), dtype=theta.dtype, device=theta.device).reshape(-1)
+              for _ in range(4)]
+        k = [0]
+
+        def step():
+            k[0] += 1
+            return hvp(us[k[0] % len(us)])
+
+        metric = "exact Hessian-vector product ms (config 5: per-species theta, forward tangent + tangent adjoint)"
+    for i in range(args.warmup):
+        step()
+        torch.cuda.synchronize()
+        log(args, f"[bench] warmup {i + 1}/{args.warmup}")
+    times = []
+    for i in range(args.steps):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t) * 1e3)
+        log(args, f"[bench] step {i + 1}/{args.steps}: {times[-1]:.3f} ms")
+    ms = statistics.mean(times)
+    out = {"metric": metric, "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
+           "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+           "config": dict(workload=f"config{args.config} {args.workload}", **cfg),
+           "median_ms": round(statistics.median(times), 4), "min_ms": round(min(times), 4)}
+    if args.workload == "hvp":
+        out["ms_per_newton_cg_step_50_hvps"] = round(50 * ms, 2)
+    print(json.dumps(out))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -133,6 +192,8 @@ def main():
     theta = cap["inputs"]["theta"].to(dev)
     cw = cap["inputs"]["col_weights"].to(dev)
     log(args, f"[bench] setup {time.time() - t0:.1f}s {summ}")
+    if args.workload != "solve":
+        return bench_other(args, static, theta, cw, summ)
 
     def step():
         loss, saved = solver.run_forward(theta, cw)

@@ -296,7 +296,7 @@ int kb_rows_scatter_add(int32_t dtype, int32_t S, int64_t n, const void* src, co
 
 /*
  * dst[s] += sum over r < n of src[r * S + s] (fixed order, float64 partial
- * sums; work: ceil(n / 256) * S doubles).  Replaces atomic column reductions
+ * sums; work: ceil(n / 64) * S doubles).  Replaces atomic column reductions
  * into grad_col_log_probs (pristine wave_backward.py:700-733, 2320-2327).
  */
 int kb_rows_sum_into(int32_t dtype, int32_t S, int64_t n, const void* src, void* dst, double* work, void* stream);

@@ -1069,7 +1069,7 @@ __global__ __launch_bounds__(256) void scatter_add_kernel(int S, long long n, co
   dst[(size_t)(key * dst_stride) + s] += acc;
 }
 
-constexpr int SUM_CHUNK = 256;
+constexpr int SUM_CHUNK = 64;
 
 template <typename T>
 __global__ __launch_bounds__(256) void rows_sum_stage1(int S, long long n, const T* src, double* work) {

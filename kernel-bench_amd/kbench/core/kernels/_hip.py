@@ -28,7 +28,7 @@ __all__ = [
     "KbPibarVjpIO", "KbWaveBwdIO", "KbWaveStepIO", "KbETanIO", "KbDtsTanIO", "KbWaveTanIO", "KbEStepSoIO",
     "KbWaveSoIO", "KbDtsSoIO",
     "lib", "check", "ptr", "stream", "dtype_code", "require_device", "f", "i64", "tree_from_parent",
-    "tree_from_levels", "scatter_add_rows", "sum_rows_into",
+    "tree_from_levels", "scatter_add_rows", "sum_rows_into", "static_cached",
 ]
 
 lib = N.lib
@@ -143,20 +143,51 @@ def tree_from_levels(S, level_ptr, level_parents, level_child1, level_child2) ->
     return _cached(key, (level_ptr, level_parents, level_child1, level_child2), build)
 
 
+# ------------------------------------------------------ static-layout cache
+_STATIC: "OrderedDict[tuple, tuple]" = OrderedDict()
+_STATIC_CACHE_SIZE = 8192
+
+
+def static_cached(tag, tensors, build):
+    """``build()`` memoised on the identity of layout tensors that do not change between calls
+    (wave metadata, topology) and on any plain values among ``tensors``.  The entry keeps strong
+    references to the tensors, so their memory cannot be reused by another tensor while the entry
+    lives; an in-place change bumps their version and misses."""
+    key = (tag,) + tuple(_key(t)[0] if torch.is_tensor(t) else t for t in tensors)
+    hit = _STATIC.get(key)
+    if hit is not None:
+        _STATIC.move_to_end(key)
+        return hit[0]
+    val = build()
+    _STATIC[key] = (val, tuple(t for t in tensors if torch.is_tensor(t)))
+    while len(_STATIC) > _STATIC_CACHE_SIZE:
+        _STATIC.popitem(last=False)
+    return val
+
+
 # ------------------------------------------------------ fixed-order accumulation
-def scatter_add_rows(dst: torch.Tensor, src: torch.Tensor, keys: torch.Tensor, *, row_stride=None) -> None:
+def _sorted_keys(keys, device):
+    keys_sorted, order = torch.sort(keys.to(device=device, dtype=torch.long).reshape(-1), stable=True)
+    return keys_sorted, order.to(torch.int32)
+
+
+def scatter_add_rows(dst: torch.Tensor, src: torch.Tensor, keys, *, row_stride=None, static=None) -> None:
     """dst[keys[r]] += src[r] for every row r, summed per key in increasing r.
 
     ``dst`` rows are ``row_stride`` elements apart (default: dst.shape[-1]);
     row_stride 0 adds every row into the single row ``dst`` (all keys must be 0).
-    Negative keys are skipped.
+    Negative keys are skipped.  With ``static`` (a tuple of layout tensors that determine
+    ``keys``), ``keys`` may be a callable and its sort is cached on their identity.
     """
     n = int(src.shape[0])
     if n == 0:
         return
     S = int(src.shape[1])
-    keys_sorted, order = torch.sort(keys.to(device=src.device, dtype=torch.long).reshape(-1), stable=True)
-    order32 = order.to(torch.int32)
+    if static is not None:
+        keys_sorted, order32 = static_cached(("scatter_keys", str(src.device)), static,
+                                             lambda: _sorted_keys(keys() if callable(keys) else keys, src.device))
+    else:
+        keys_sorted, order32 = _sorted_keys(keys, src.device)
     stride = int(dst.shape[-1]) if row_stride is None else int(row_stride)
     check(lib().kb_rows_scatter_add(dtype_code(src.dtype), S, n, ptr(src), ptr(order32), ptr(keys_sorted),
                                     ptr(dst), stride, stream(src.device)))
@@ -168,5 +199,5 @@ def sum_rows_into(dst: torch.Tensor, src: torch.Tensor) -> None:
     if n == 0:
         return
     S = int(src.shape[1])
-    work = torch.empty(((n + 255) // 256) * S, device=src.device, dtype=torch.float64)
+    work = torch.empty(((n + 63) // 64) * S, device=src.device, dtype=torch.float64)
     check(lib().kb_rows_sum_into(dtype_code(src.dtype), S, n, ptr(src), ptr(dst), ptr(work), stream(src.device)))

@@ -19,7 +19,14 @@ __all__ = ["compute_dts_forward"]
 
 
 def split_groups(reduce_idx: torch.Tensor, W: int):
-    """(ptr [W+1], order [N]) int32: the splits of row w are order[ptr[w]:ptr[w+1]], increasing."""
+    """(ptr [W+1], order [N]) int32: the splits of row w are order[ptr[w]:ptr[w+1]], increasing.
+
+    Cached on the identity of ``reduce_idx`` (static wave metadata)."""
+    return H.static_cached(("split_groups", int(W), str(reduce_idx.device)), (reduce_idx,),
+                           lambda: _split_groups(reduce_idx, W))
+
+
+def _split_groups(reduce_idx: torch.Tensor, W: int):
     red = reduce_idx.to(dtype=torch.long).reshape(-1)
     counts = torch.bincount(red, minlength=int(W))[: int(W)]
     ptr = torch.zeros(int(W) + 1, device=red.device, dtype=torch.int32)

@@ -93,7 +93,7 @@ def dts_backward_so(Pi, dPi, Pibar, dPibar, v, ws, meta, S, log_pD_param, log_pS
         col_rows=H.ptr(colrows), pD_rows=H.ptr(pDr), pS_rows=H.ptr(pSr), mt_rows=H.ptr(mtr),
     )
     H.check(H.lib().kb_dts_backward_so(tree.handle, io, H.stream(dev)))
-    H.scatter_add_rows(d_rhs, side, torch.cat((sl64, sr64)))
+    H.scatter_add_rows(d_rhs, side, lambda: torch.cat((sl64, sr64)), static=(sl64, sr64))
     H.sum_rows_into(d_grad_col, colrows)
     parent_items = item[start + red]
     _accum_param(d_grad_pD, pDr, parent_items)

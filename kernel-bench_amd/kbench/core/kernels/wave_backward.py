@@ -342,24 +342,37 @@ def dts_cross_backward_accum_fused(Pi_star, Pibar_star, v_k, ws, sl, sr, reduce_
     H.check(H.lib().kb_dts_cross_backward(io, H.stream(dev)))
 
     # children's adjoint rows: side r of split i goes to row sl[i] (r < n) or sr[i]
-    H.scatter_add_rows(accumulated_rhs, side_rows, torch.cat((sl64, sr64)))
+    H.scatter_add_rows(accumulated_rhs, side_rows, lambda: torch.cat((sl64, sr64)), static=(sl64, sr64))
     if accum_param_reductions:
-        zeros = torch.zeros((n,), device=dev, dtype=torch.long)
-        pkey = item.index_select(0, red + int(ws)) if (item is not None and glayout in (2, 3)) else zeros
-        if glayout in (1, 3):
-            stride = 0 if glayout == 1 else S
-            H.scatter_add_rows(grad_log_pD.reshape(-1), param_rows[:n], pkey, row_stride=stride)
-            H.scatter_add_rows(grad_log_pS.reshape(-1), param_rows[n:], pkey, row_stride=stride)
+        if glayout == 1 or (glayout == 3 and int(grad_log_pD.shape[0]) == 1):
+            # one parameter row: every split adds into it (parallel fixed-order row sum)
+            H.sum_rows_into(grad_log_pD.reshape(-1), param_rows[:n])
+            H.sum_rows_into(grad_log_pS.reshape(-1), param_rows[n:])
+        elif glayout == 0:
+            H.sum_rows_into(grad_log_pD.reshape(-1), param_sums[:n].reshape(n, 1))
+            H.sum_rows_into(grad_log_pS.reshape(-1), param_sums[n:].reshape(n, 1))
         else:
-            stride = 0 if glayout == 0 else 1
-            H.scatter_add_rows(grad_log_pD.reshape(-1), param_sums[:n].reshape(n, 1), pkey, row_stride=stride)
-            H.scatter_add_rows(grad_log_pS.reshape(-1), param_sums[n:].reshape(n, 1), pkey, row_stride=stride)
+            if item is None:
+                raise ValueError("per-item parameter gradients need item_idx")
+            st = (item, red, int(ws))
+            pkey = lambda: item.index_select(0, red + int(ws))
+            if glayout == 3:
+                H.scatter_add_rows(grad_log_pD.reshape(-1), param_rows[:n], pkey, row_stride=S, static=st)
+                H.scatter_add_rows(grad_log_pS.reshape(-1), param_rows[n:], pkey, row_stride=S, static=st)
+            else:
+                H.scatter_add_rows(grad_log_pD.reshape(-1), param_sums[:n].reshape(n, 1), pkey, row_stride=1,
+                                   static=st)
+                H.scatter_add_rows(grad_log_pS.reshape(-1), param_sums[n:].reshape(n, 1), pkey, row_stride=1,
+                                   static=st)
     else:
         param_pD, param_pS = param_sums[:n].clone(), param_sums[n:].clone()
     if accum_mt_reduction:
-        if gmt_layout == 1:
-            keys = torch.cat((item.index_select(0, sl64), item.index_select(0, sr64)))
-            H.scatter_add_rows(grad_mt.reshape(-1), mt_rows, keys, row_stride=S)
+        if gmt_layout == 1 and int(grad_mt.shape[0]) == 1:
+            H.sum_rows_into(grad_mt.reshape(-1), mt_rows)
+        elif gmt_layout == 1:
+            H.scatter_add_rows(grad_mt.reshape(-1), mt_rows,
+                               lambda: torch.cat((item.index_select(0, sl64), item.index_select(0, sr64))),
+                               row_stride=S, static=(item, sl64, sr64))
         elif grad_mt.numel() == 1:
             tmp = torch.zeros((S,), device=dev, dtype=dt)
             H.sum_rows_into(tmp, mt_rows)
@@ -438,7 +451,7 @@ def uniform_cross_pibar_vjp_tree_from_ud_fused(Pi_star, col_log_probs, pibar_ud,
         contrib=H.ptr(contrib),
     )
     H.check(H.lib().kb_pibar_vjp(tree.handle, io, H.stream(dev)))
-    H.scatter_add_rows(accumulated_rhs, contrib, torch.cat((sl64, sr64)))
+    H.scatter_add_rows(accumulated_rhs, contrib, lambda: torch.cat((sl64, sr64)), static=(sl64, sr64))
     if grad_col_log_probs is not None:
         H.sum_rows_into(grad_col_log_probs, contrib)
     return side_active

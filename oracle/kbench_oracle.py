@@ -976,7 +976,7 @@ def _fold_cotangents(saved, S, G, e_pS, e_pD, e_pL, e_mt, e_col, g_pD, g_pS, g_m
 
 
 # ----------------------------------------------------------------------------
-# forward tangents (row a11, first half): reference
+# forward tangents (JVP) of the forward maps: reference
 # kbench/core/kernels/{e_step_tangent,dts_tangent,wave_tangent}.py and the glue
 # newton/forward_tangent.py
 # ----------------------------------------------------------------------------
@@ -1214,7 +1214,7 @@ def jvp_root_scores(prob: Problem, theta, v, saved, *, self_iters=None, e_tol=1e
 
 
 # ----------------------------------------------------------------------------
-# second-order contractions and the exact HVP (row a11, second half): reference
+# second-order contractions and the exact HVP: reference
 # kbench/core/kernels/{e_step_so,wave_so,dts_so}.py and newton/{ggn,hvp_exact}.py
 # ----------------------------------------------------------------------------
 

@@ -83,12 +83,13 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   // staging rows.  In class mode (identical rows without splits) each member's
   // adjoint gets its own active-mask decision and the active members' adjoints
   // are summed: everything below is linear in the adjoint.
-  float piv[CPT];
-  load_row_pre<NT, CPT>(T, P.pi + rb, R0, piv, KB_NEG_INF);
+  // The adjoint gathers are issued first, then Pi* and Pibar* go through LDS to
+  // preorder positions under one barrier, so the three loads overlap.
   float rhs[CPT];
 #pragma unroll
   for (int k = 0; k < CPT; ++k) rhs[k] = 0.0f;
   bool any_active = false;
+  const int fam = P.class_mode ? -1 : P.root_index[row];
   if (P.class_mode) {
     // the summed adjoint of the class's active members (bwd_gather0 / bwd_classsum0)
     any_active = P.cls_active[rr] != 0;
@@ -96,8 +97,31 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
 #pragma unroll
     for (int k = 0; k < CPT; ++k)
       if (okp[k]) rhs[k] = src[own_pos<NT, CPT>(k)];
-  } else {
-    const int fam = P.root_index[row];
+  } else if (fam < 0) {
+    const int gb = P.child_ptr[row], ge = P.child_ptr[row + 1];
+    for (int i = gb; i < ge; ++i) {
+      const int side = P.child_in[i];
+      if (!P.split_on[side >> 1]) continue;
+      const float* st = P.staging + (size_t)side * S;
+#pragma unroll
+      for (int k = 0; k < CPT; ++k)
+        if (okp[k]) rhs[k] += st[own_pos<NT, CPT>(k)];
+    }
+  }
+  float piv[CPT], pbv[CPT];
+  for (int s = tid; s < S; s += NT) {
+    const int i = T.pre[s];
+    R0[i] = P.pi[rb + s];
+    R1[i] = P.pibar[rb + s];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int i = own_pos<NT, CPT>(k);
+    piv[k] = okp[k] ? R0[i] : KB_NEG_INF;
+    pbv[k] = okp[k] ? R1[i] : KB_NEG_INF;
+  }
+  if (!P.class_mode) {
     if (fam >= 0) {
       // logsumexp2 (logspace.py:11-16) and _safe_exp2_ratio (_implicit_grad.py:21-25)
       float lm = KB_NEG_INF;
@@ -113,16 +137,6 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       const float lses = fsafe(lse);
 #pragma unroll
       for (int k = 0; k < CPT; ++k) rhs[k] = (piv[k] == KB_NEG_INF) ? 0.0f : -exp2f(piv[k] - lses);
-    } else {
-      const int gb = P.child_ptr[row], ge = P.child_ptr[row + 1];
-      for (int i = gb; i < ge; ++i) {
-        const int side = P.child_in[i];
-        if (!P.split_on[side >> 1]) continue;
-        const float* st = P.staging + (size_t)side * S;
-#pragma unroll
-        for (int k = 0; k < CPT; ++k)
-          if (okp[k]) rhs[k] += st[own_pos<NT, CPT>(k)];
-      }
     }
     // ---- 2. active mask (the reference's rule, wave_backward.py:150-163)
     float am = 0.0f;
@@ -193,13 +207,13 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
 
   // ---- 4. J^T coefficients at Pi* (precompute kernel, wave_backward.py:264-416)
   const float rms = fsafe(P.rowmax[row]);
-  float pbv[CPT], pp[CPT];
+  float pp[CPT];
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int i = own_pos<NT, CPT>(k);
     R0[i] = piv[k];  // Pi* at own positions for the child gathers (padding position i >= S: -inf)
   }
-  load_row_pre<NT, CPT>(T, P.pibar + rb, R1, pbv, KB_NEG_INF);  // barrier also publishes R0
+  __syncthreads();  // publishes R0
   float ls = 0.0f;
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {

@@ -49,7 +49,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   const int tid = threadIdx.x;
   constexpr int ZERO = MAXS;
 
-  OwnTables<NT, CPT> O;
+  OwnTablesC<NT, CPT> O;
   O.load(T);
   if (tid < 64) {
     R0[MAXS + tid] = 0.0f;
@@ -59,20 +59,83 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   }
   bool okp[CPT];
 #pragma unroll
-  for (int k = 0; k < CPT; ++k) okp[k] = own_pos<NT, CPT>(k) < S;
+  for (int k = 0; k < CPT; ++k) okp[k] = own_pos_c<NT, CPT>(k) < S;
+  // static per position: parent position (ZERO at the root), child-1 flag,
+  // subtree end - 1 and the previous position (ZERO at position 0)
+  int ppos[CPT], endm1[CPT], prev[CPT], pfl[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int i = own_pos_c<NT, CPT>(k);
+    const int pa = okp[k] ? T.ppos[i] : -1;
+    ppos[k] = pa >= 0 ? pa : ZERO;
+    pfl[k] = pa >= 0 ? T.pflag[i] : 0;
+    endm1[k] = okp[k] ? T.endpos[i] - 1 : ZERO;
+    prev[k] = i > 0 ? i - 1 : ZERO;
+  }
   // gradient buckets of every row this workgroup processes (static round-robin
   // assignment, so the summation order is fixed)
-  float cacc[8][CPT];
+  // (in LDS for rows of up to 2048 states, own positions only: each thread
+  // reads and writes just its own entries, so the accumulation needs no
+  // barrier; in registers for longer rows, whose LDS rows leave no room)
+  constexpr bool BK_LDS = MAXS <= 2048;
+  __shared__ float Bk[BK_LDS ? 8 * MAXS : 1];
+  float cacc[BK_LDS ? 1 : 8][CPT];
 #pragma unroll
   for (int j = 0; j < 8; ++j)
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) cacc[j][k] = 0.0f;
+    for (int k = 0; k < CPT; ++k) {
+      if constexpr (BK_LDS)
+        Bk[j * MAXS + own_pos_c<NT, CPT>(k)] = 0.0f;
+      else
+        cacc[j][k] = 0.0f;
+    }
+  auto bucket = [&](int j, int k) -> float& {
+    if constexpr (BK_LDS)
+      return Bk[j * MAXS + own_pos_c<NT, CPT>(k)];
+    else
+      return cacc[j][k];
+  };
+  // bucket j += x at the own positions (vector LDS read-modify-write)
+  auto bucket_add = [&](int j, const float (&x)[CPT]) {
+    if constexpr (BK_LDS) {
+      float cur[CPT];
+      lds_load_own<CPT>(Bk + j * MAXS, cur);
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) cur[k] += x[k];
+      lds_store_own<CPT>(Bk + j * MAXS, cur);
+    } else {
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) cacc[j][k] += x[k];
+    }
+  };
+
+  // Pi* / Pibar* rows are fetched one row ahead: column s = tid + j*NT of the
+  // next row this workgroup processes goes to registers while the current row
+  // is solved, then to its preorder position spre[j] in LDS.
+  auto row_of = [&](int r2) { return P.class_mode ? P.cls_rows[P.cls_ptr[r2]] : P.sched_rows[first + r2]; };
+  int spre[CPT];
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int s = tid + j * NT;
+    spre[j] = s < S ? T.pre[s] : -1;
+  }
+  float nPi[CPT], nPb[CPT];
+  auto fetch_rows = [&](int r2) {
+    const size_t b2 = (size_t)row_of(r2) * S;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int s = tid + j * NT;
+      nPi[j] = spre[j] >= 0 ? P.pi[b2 + s] : 0.0f;
+      nPb[j] = spre[j] >= 0 ? P.pibar[b2 + s] : 0.0f;
+    }
+  };
+  if ((int)blockIdx.x < n_rows) fetch_rows(blockIdx.x);
 
   for (int rr = blockIdx.x; rr < n_rows; rr += gridDim.x) {
   __syncthreads();  // LDS of the previous row is no longer read
   const int mb = P.class_mode ? P.cls_ptr[rr] : 0;
   const int me = P.class_mode ? P.cls_ptr[rr + 1] : 1;
-  const int row = P.class_mode ? P.cls_rows[mb] : P.sched_rows[first + rr];
+  const int row = row_of(rr);
   const int leaf_row = P.row_kind[row];
   const int item = P.item[row];
   const size_t cb = (size_t)item * P.const_stride;
@@ -96,7 +159,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     const float* src = P.rhsc + (size_t)rr * S;
 #pragma unroll
     for (int k = 0; k < CPT; ++k)
-      if (okp[k]) rhs[k] = src[own_pos<NT, CPT>(k)];
+      if (okp[k]) rhs[k] = src[own_pos_c<NT, CPT>(k)];
   } else if (fam < 0) {
     const int gb = P.child_ptr[row], ge = P.child_ptr[row + 1];
     for (int i = gb; i < ge; ++i) {
@@ -105,21 +168,23 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       const float* st = P.staging + (size_t)side * S;
 #pragma unroll
       for (int k = 0; k < CPT; ++k)
-        if (okp[k]) rhs[k] += st[own_pos<NT, CPT>(k)];
+        if (okp[k]) rhs[k] += st[own_pos_c<NT, CPT>(k)];
     }
   }
   float piv[CPT], pbv[CPT];
-  for (int s = tid; s < S; s += NT) {
-    const int i = T.pre[s];
-    R0[i] = P.pi[rb + s];
-    R1[i] = P.pibar[rb + s];
-  }
+#pragma unroll
+  for (int j = 0; j < CPT; ++j)
+    if (spre[j] >= 0) {
+      R0[spre[j]] = nPi[j];
+      R1[spre[j]] = nPb[j];
+    }
+  if (rr + (int)gridDim.x < n_rows) fetch_rows(rr + gridDim.x);
   __syncthreads();
+  lds_load_own<CPT>(R0, piv);
+  lds_load_own<CPT>(R1, pbv);
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
-    const int i = own_pos<NT, CPT>(k);
-    piv[k] = okp[k] ? R0[i] : KB_NEG_INF;
-    pbv[k] = okp[k] ? R1[i] : KB_NEG_INF;
+    if (!okp[k]) piv[k] = pbv[k] = KB_NEG_INF;
   }
   if (!P.class_mode) {
     if (fam >= 0) {
@@ -160,7 +225,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     const float* src = P.dts_in + (size_t)P.rep_of[row] * S;
 #pragma unroll
     for (int k = 0; k < CPT; ++k)
-      if (okp[k]) dts[k] = src[own_pos<NT, CPT>(k)];
+      if (okp[k]) dts[k] = src[own_pos_c<NT, CPT>(k)];
   } else if (!leaf_row) {
     float m[CPT], acc[CPT];
 #pragma unroll
@@ -181,7 +246,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       __syncthreads();
 #pragma unroll
       for (int k = 0; k < CPT; ++k) {
-        const int i = own_pos<NT, CPT>(k);
+        const int i = own_pos_c<NT, CPT>(k);
         if (okp[k]) {
           const bool h1 = O.c1p[k] != ZERO, h2 = O.c2p[k] != ZERO;
           const float pl = R0[i], pr = R1[i];
@@ -208,20 +273,16 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   // ---- 4. J^T coefficients at Pi* (precompute kernel, wave_backward.py:264-416)
   const float rms = fsafe(P.rowmax[row]);
   float pp[CPT];
-#pragma unroll
-  for (int k = 0; k < CPT; ++k) {
-    const int i = own_pos<NT, CPT>(k);
-    R0[i] = piv[k];  // Pi* at own positions for the child gathers (padding position i >= S: -inf)
-  }
-  __syncthreads();  // publishes R0
+  lds_store_own<CPT>(R0, piv);  // Pi* at own positions for the child gathers (padding positions: -inf)
+  __syncthreads();               // publishes R0
   float ls = 0.0f;
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
-    const int i = own_pos<NT, CPT>(k);
+    const int i = own_pos_c<NT, CPT>(k);
     pp[k] = okp[k] ? exp2f((WEIGHTED ? P.col[i] : 0.0f) + piv[k] - rms) : 0.0f;
-    R2[i] = pp[k];
     ls += pp[k];
   }
+  lds_store_own<CPT>(R2, pp);
   const float rowsum = block_sum1<NT>(ls, wA);
   float ps[CPT];
   path_sum_euler<NT, CPT>(O, R2, Sc, wB, ps);
@@ -229,7 +290,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   float q[6][CPT], pcoef[CPT];
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
-    const int i = own_pos<NT, CPT>(k);
+    const int i = own_pos_c<NT, CPT>(k);
 #pragma unroll
     for (int j = 0; j < 6; ++j) q[j][k] = 0.0f;
     pcoef[k] = 0.0f;
@@ -270,27 +331,32 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     R2[MAXS + tid] = 0.0f;
     R3[MAXS + tid] = 0.0f;
   }
-#pragma unroll
-  for (int k = 0; k < CPT; ++k) {
-    const int i = own_pos<NT, CPT>(k);
-    R2[i] = q[3][k];
-    R3[i] = q[4][k];
-  }
+  lds_store_own<CPT>(R2, q[3]);
+  lds_store_own<CPT>(R3, q[4]);
   __syncthreads();
   float edge[CPT], diag[CPT];
-  int ppos[CPT], endm1[CPT], prev[CPT], pfl[CPT];
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
-    const int i = own_pos<NT, CPT>(k);
-    const int pa = okp[k] ? T.ppos[i] : -1;
-    ppos[k] = pa >= 0 ? pa : ZERO;
-    pfl[k] = pa >= 0 ? T.pflag[i] : 0;
-    edge[k] = pa >= 0 ? (T.pflag[i] ? R2[pa] : R3[pa]) : 0.0f;
-    endm1[k] = okp[k] ? T.endpos[i] - 1 : ZERO;
-    prev[k] = i > 0 ? i - 1 : ZERO;
+    edge[k] = ppos[k] != ZERO ? (pfl[k] ? R2[ppos[k]] : R3[ppos[k]]) : 0.0f;
     diag[k] = q[0][k] + q[1][k];
   }
   __syncthreads();  // R2 / R3 become scan buffers
+
+  // The first split's four child rows (Pi, Pibar of both children) are loaded
+  // into registers here, so their latency overlaps the Neumann loop.
+  float pf[4][CPT];
+  if (se > sb) {
+    const size_t l = (size_t)P.split_l[sb] * S, r = (size_t)P.split_r[sb] * S;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int s = tid + j * NT;
+      const bool ok = s < S;
+      pf[0][j] = ok ? P.pi[l + s] : 0.0f;
+      pf[1][j] = ok ? P.pi[r + s] : 0.0f;
+      pf[2][j] = ok ? P.pibar[l + s] : 0.0f;
+      pf[3][j] = ok ? P.pibar[r + s] : 0.0f;
+    }
+  }
 
   // ---- 5. Neumann series v = sum_{n<=N} (J^T)^n rhs with the row on chip
   float v[CPT], term[CPT];
@@ -299,24 +365,41 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     v[k] = rhs[k];
     term[k] = rhs[k];
   }
+  // Per term: the scan of u = term * pcoef is a per-thread running sum plus one
+  // wavefront scan of the thread totals; the scan value at position i - 1 comes
+  // from the thread itself, the previous lane (shuffle) or, for a wavefront's
+  // first position, the wavefront offset, so only P[end(i) - 1] and the
+  // parent's term are read back from LDS.
   for (int n = 0; n < P.n_terms; ++n) {
     float* Tb = (n & 1) ? R1 : R0;
     float* Pb = (n & 1) ? R3 : R2;
     float* wt = (n & 1) ? wB : wA;
-    float u[CPT];
+    float sc[CPT];
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-      Tb[own_pos<NT, CPT>(k)] = term[k];
-      u[k] = term[k] * pcoef[k];
+    for (int k = 0; k < CPT; ++k) sc[k] = term[k] * pcoef[k] + (k > 0 ? sc[k - 1] : 0.0f);
+    const float tsum = sc[CPT - 1];
+    const float ws = wave_scan_incl(tsum);
+    if ((tid & 63) == 63) wt[tid >> 6] = ws;
+    lds_store_own<CPT>(Tb, term);
+    __syncthreads();
+    float woff = 0.0f, A = 0.0f;
+#pragma unroll
+    for (int x = 0; x < NW; ++x) {
+      const float t = wt[x];
+      if (x < (tid >> 6)) woff += t;
+      A += t;
     }
-    const float A = block_scan_incl<NT, CPT>(u, wt);  // barrier: publishes Tb
+    const float base = woff + (ws - tsum);
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) Pb[own_pos<NT, CPT>(k)] = u[k];
+    for (int k = 0; k < CPT; ++k) sc[k] += base;
+    lds_store_own<CPT>(Pb, sc);
+    const float up = __shfl_up(sc[CPT - 1], 1, 64);
+    const float p0 = (tid & 63) == 0 ? woff : up;  // P[i - 1] of slot 0
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const float comp = Pb[prev[k]] + (A - Pb[endm1[k]]);
-      const float nt = term[k] * diag[k] + pp[k] * comp + Tb[ppos[k]] * edge[k];
+      const float pm1 = k == 0 ? p0 : sc[k - 1];
+      const float nt = term[k] * diag[k] + pp[k] * (pm1 + (A - Pb[endm1[k]])) + Tb[ppos[k]] * edge[k];
       term[k] = nt;
       v[k] += nt;
     }
@@ -330,23 +413,25 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     float u[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) u[k] = v[k] * pcoef[k];
-    const float A = block_scan_incl<NT, CPT>(u, wt);
-#pragma unroll
-    for (int k = 0; k < CPT; ++k) Pb[own_pos<NT, CPT>(k)] = u[k];
+    const float A = block_scan_incl_c<NT, CPT>(u, wt);
+    lds_store_own<CPT>(Pb, u);
     __syncthreads();
+    float x[8][CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const float aw0 = v[k] * q[0][k], aw1 = v[k] * q[1][k], aw2 = v[k] * q[2][k];
       const float aw3 = v[k] * q[3][k], aw4 = v[k] * q[4][k], aw5 = v[k] * q[5][k];
-      cacc[0][k] += aw0;
-      cacc[1][k] += aw3 + aw4 + aw5;
-      cacc[2][k] += aw0 + aw2;
-      cacc[3][k] += aw1;
-      cacc[4][k] += aw4;
-      cacc[5][k] += aw3;
-      cacc[6][k] += aw2;
-      cacc[7][k] += okp[k] ? pp[k] * (Pb[prev[k]] + (A - Pb[endm1[k]])) : 0.0f;
+      x[0][k] = aw0;
+      x[1][k] = aw3 + aw4 + aw5;
+      x[2][k] = aw0 + aw2;
+      x[3][k] = aw1;
+      x[4][k] = aw4;
+      x[5][k] = aw3;
+      x[6][k] = aw2;
+      x[7][k] = okp[k] ? pp[k] * (Pb[prev[k]] + (A - Pb[endm1[k]])) : 0.0f;
     }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) bucket_add(j, x[j]);
   }
 
   // ---- 7. split adjoints into the child rows (staging, preorder layout)
@@ -357,22 +442,41 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     const float rml = P.rowmax[lrow], rmr = P.rowmax[rrow];
     const float rmsl = fsafe(rml), rmsr = fsafe(rmr);
     __syncthreads();  // previous readers of R0..R3 are done
-    for (int s = tid; s < S; s += NT) {
-      const int i = T.pre[s];
-      R0[i] = P.pi[l + s];
-      R1[i] = P.pi[r + s];
-      R2[i] = P.pibar[l + s];
-      R3[i] = P.pibar[r + s];
+    if (si == sb) {
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) {
+        const int s = tid + j * NT;
+        if (s < S) {
+          const int i = T.pre[s];
+          R0[i] = pf[0][j];
+          R1[i] = pf[1][j];
+          R2[i] = pf[2][j];
+          R3[i] = pf[3][j];
+        }
+      }
+    } else {
+      for (int s = tid; s < S; s += NT) {
+        const int i = T.pre[s];
+        R0[i] = P.pi[l + s];
+        R1[i] = P.pi[r + s];
+        R2[i] = P.pibar[l + s];
+        R3[i] = P.pibar[r + s];
+      }
     }
     __syncthreads();
     float vd0[CPT], vd1[CPT], vd2[CPT], vd3[CPT], vd4[CPT], udl[CPT], udr[CPT], ppl[CPT], ppr[CPT];
+    float cPl[CPT], cPr[CPT], cBl[CPT], cBr[CPT];
+    lds_load_own<CPT>(R0, cPl);
+    lds_load_own<CPT>(R1, cPr);
+    lds_load_own<CPT>(R2, cBl);
+    lds_load_own<CPT>(R3, cBr);
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const int i = own_pos<NT, CPT>(k);
+      const int i = own_pos_c<NT, CPT>(k);
       vd0[k] = vd1[k] = vd2[k] = vd3[k] = vd4[k] = udl[k] = udr[k] = ppl[k] = ppr[k] = 0.0f;
       if (okp[k]) {
         const bool h1 = O.c1p[k] != ZERO, h2 = O.c2p[k] != ZERO;
-        const float pl = R0[i], pr = R1[i], bl = R2[i], br = R3[i];
+        const float pl = cPl[k], pr = cPr[k], bl = cBl[k], br = cBr[k];
         const float l1 = h1 ? R0[O.c1p[k]] : KB_NEG_INF, r1 = h1 ? R1[O.c1p[k]] : KB_NEG_INF;
         const float l2 = h2 ? R0[O.c2p[k]] : KB_NEG_INF, r2 = h2 ? R1[O.c2p[k]] : KB_NEG_INF;
         const float d = P.pD.at(item, i), sp = P.pS.at(item, i);
@@ -394,26 +498,20 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       }
     }
     __syncthreads();  // staged children fully read
-#pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-      const int i = own_pos<NT, CPT>(k);
-      R0[i] = vd3[k];
-      R1[i] = vd4[k];
-    }
+    lds_store_own<CPT>(R0, vd3);
+    lds_store_own<CPT>(R1, vd4);
     float Al, Ar;
-    block_scan_incl2<NT, CPT>(udl, udr, wA, Al, Ar);  // barrier: publishes R0 / R1
-#pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-      const int i = own_pos<NT, CPT>(k);
-      R2[i] = udl[k];
-      R3[i] = udr[k];
-    }
+    block_scan_incl2_c<NT, CPT>(udl, udr, wA, Al, Ar);  // barrier: publishes R0 / R1
+    lds_store_own<CPT>(R2, udl);
+    lds_store_own<CPT>(R3, udr);
     __syncthreads();
     float* stl = P.staging + (size_t)(2 * si) * S;
     float* str = P.staging + (size_t)(2 * si + 1) * S;
+    float y[4][CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const int i = own_pos<NT, CPT>(k);
+      const int i = own_pos_c<NT, CPT>(k);
+      y[0][k] = y[1][k] = y[2][k] = y[3][k] = 0.0f;
       if (okp[k]) {
         const float tl = ppl[k] * (R2[prev[k]] + (Al - R2[endm1[k]]));
         const float tr = ppr[k] * (R3[prev[k]] + (Ar - R3[endm1[k]]));
@@ -424,12 +522,16 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
         const float shr = first ? sh4 : sh3;
         stl[i] = vd0[k] + vd1[k] + shl + tl;
         str[i] = vd0[k] + vd2[k] + shr + tr;
-        cacc[0][k] += vd0[k];
-        cacc[1][k] += vd3[k] + vd4[k];
-        cacc[6][k] += vd1[k] + vd2[k];
-        cacc[7][k] += tl + tr;
+        y[0][k] = vd0[k];
+        y[1][k] = vd3[k] + vd4[k];
+        y[2][k] = vd1[k] + vd2[k];
+        y[3][k] = tl + tr;
       }
     }
+    bucket_add(0, y[0]);
+    bucket_add(1, y[1]);
+    bucket_add(6, y[2]);
+    bucket_add(7, y[3]);
     if (tid == 0) P.split_on[si] = 1;
   }
 
@@ -442,7 +544,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   for (int j = 0; j < 8; ++j)
 #pragma unroll
     for (int k = 0; k < CPT; ++k)
-      if (okp[k]) cr[(size_t)j * S + own_pos<NT, CPT>(k)] += cacc[j][k];
+      if (okp[k]) cr[(size_t)j * S + own_pos_c<NT, CPT>(k)] += bucket(j, k);
 }
 
 #define KB_BWD_CASE(NT_, CPT_)                                                                      \

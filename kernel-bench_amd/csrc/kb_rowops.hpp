@@ -204,6 +204,146 @@ struct OwnTables {
   }
 };
 
+// ---- contiguous ownership ------------------------------------------------------
+// Alternative layout for kernels whose inner loop is a block scan: thread t owns
+// positions t*CPT + k, so a scan is a per-thread running sum plus ONE wavefront
+// scan of the thread totals (instead of one per slot), and the scan value at
+// position i-1 of slot 0 is the previous lane's last value.  Own positions are
+// moved to and from LDS with vector accesses (conflict-free).
+
+template <int NT, int CPT>
+__device__ __forceinline__ int own_pos_c(int k) {
+  return threadIdx.x * CPT + k;
+}
+
+template <int CPT>
+__device__ __forceinline__ void lds_store_own(float* lds, const float (&v)[CPT]) {
+  float* p = lds + threadIdx.x * CPT;
+  if constexpr (CPT % 4 == 0) {
+#pragma unroll
+    for (int k = 0; k < CPT; k += 4) *reinterpret_cast<float4*>(p + k) = make_float4(v[k], v[k + 1], v[k + 2], v[k + 3]);
+  } else if constexpr (CPT % 2 == 0) {
+#pragma unroll
+    for (int k = 0; k < CPT; k += 2) *reinterpret_cast<float2*>(p + k) = make_float2(v[k], v[k + 1]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) p[k] = v[k];
+  }
+}
+
+template <int CPT>
+__device__ __forceinline__ void lds_load_own(const float* lds, float (&v)[CPT]) {
+  const float* p = lds + threadIdx.x * CPT;
+  if constexpr (CPT % 4 == 0) {
+#pragma unroll
+    for (int k = 0; k < CPT; k += 4) {
+      const float4 q = *reinterpret_cast<const float4*>(p + k);
+      v[k] = q.x;
+      v[k + 1] = q.y;
+      v[k + 2] = q.z;
+      v[k + 3] = q.w;
+    }
+  } else if constexpr (CPT % 2 == 0) {
+#pragma unroll
+    for (int k = 0; k < CPT; k += 2) {
+      const float2 q = *reinterpret_cast<const float2*>(p + k);
+      v[k] = q.x;
+      v[k + 1] = q.y;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) v[k] = p[k];
+  }
+}
+
+// In-place inclusive scan over positions of contiguously owned v[]; returns the
+// block total.  One barrier; callers alternate `wtot` arrays.
+template <int NT, int CPT>
+__device__ __forceinline__ float block_scan_incl_c(float (&v)[CPT], float* wtot) {
+  constexpr int NW = NT / 64;
+#pragma unroll
+  for (int k = 1; k < CPT; ++k) v[k] += v[k - 1];
+  const float tsum = v[CPT - 1];
+  const float ws = wave_scan_incl(tsum);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 63) wtot[w] = ws;
+  __syncthreads();
+  float off = ws - tsum, total = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const float t = wtot[i];
+    if (i < w) off += t;
+    total += t;
+  }
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) v[k] += off;
+  return total;
+}
+
+// Two contiguous-ownership scans sharing one barrier (wtot holds 2*NW floats).
+template <int NT, int CPT>
+__device__ __forceinline__ void block_scan_incl2_c(float (&a)[CPT], float (&b)[CPT], float* wtot, float& ta,
+                                                   float& tb) {
+  constexpr int NW = NT / 64;
+#pragma unroll
+  for (int k = 1; k < CPT; ++k) {
+    a[k] += a[k - 1];
+    b[k] += b[k - 1];
+  }
+  const float sa = a[CPT - 1], sb = b[CPT - 1];
+  const float wa = wave_scan_incl(sa), wb = wave_scan_incl(sb);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 63) {
+    wtot[w] = wa;
+    wtot[NW + w] = wb;
+  }
+  __syncthreads();
+  float oa = wa - sa, ob = wb - sb;
+  ta = 0.0f;
+  tb = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const float x = wtot[i], y = wtot[NW + i];
+    if (i < w) {
+      oa += x;
+      ob += y;
+    }
+    ta += x;
+    tb += y;
+  }
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    a[k] += oa;
+    b[k] += ob;
+  }
+}
+
+// Preorder tables of the contiguously owned positions (same fields as
+// OwnTables; the Euler events are owned contiguously in both layouts).
+template <int NT, int CPT>
+struct OwnTablesC {
+  static constexpr int ZERO = NT * CPT;
+  int col[CPT], c1p[CPT], c2p[CPT], tin[CPT];
+  int ev[2 * CPT];
+  __device__ __forceinline__ void load(const PreDev& T) {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int i = own_pos_c<NT, CPT>(k);
+      const bool ok = i < T.S;
+      col[k] = ok ? T.col[i] : -1;
+      const int a = ok ? T.c1pos[i] : -1, b = ok ? T.c2pos[i] : -1;
+      c1p[k] = a >= 0 ? a : ZERO;
+      c2p[k] = b >= 0 ? b : ZERO;
+      tin[k] = ok ? T.tin[i] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < 2 * CPT; ++j) {
+      const int q = threadIdx.x * (2 * CPT) + j;
+      ev[j] = q < 2 * T.S ? T.euler[q] : (ZERO << 1);
+    }
+  }
+};
+
 // Coalesced load of a global row (column order) into LDS at preorder
 // positions, then into v[] (own positions).  One barrier; the caller separates
 // reuse of `lds` with a barrier.  Positions >= S read `fill`.
@@ -236,8 +376,8 @@ __device__ __forceinline__ void store_row_pre(const PreDev& T, const float (&v)[
 // with a 0 at ZERO is not required: the padding slot's x is 0): Euler-tour
 // prefix scan.  Returns ps[] for own positions.  Reads x[] after the caller's
 // barrier; writes `scan` (2*NT*CPT floats).  Two barriers.
-template <int NT, int CPT>
-__device__ __forceinline__ void path_sum_euler(const OwnTables<NT, CPT>& O, const float* x, float* scan, float* wtot,
+template <int NT, int CPT, class Tables>
+__device__ __forceinline__ void path_sum_euler(const Tables& O, const float* x, float* scan, float* wtot,
                                                float (&ps)[CPT], const float* wgt = nullptr) {
   constexpr int E = 2 * CPT;
   constexpr int NW = NT / 64;

@@ -310,17 +310,12 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       float e[6] = {exp2f(t0 - msf), exp2f(t1 - msf), exp2f(t2 - msf), exp2f(t3 - msf), exp2f(t4 - msf),
                     exp2f(t5 - msf)};
       const float sum = e[0] + e[1] + e[2] + e[3] + e[4] + e[5];
-      const float inv_sum = sum > 0.0f ? 1.0f / sum : 0.0f;
-      float wL = 1.0f;
-      if (!leaf_row) {
-        const float dl = log2f(sum) + m;
-        const float pm = fmaxf(dl, dts[k]);
-        const float pms = fsafe(pm);
-        const float pnew = log2f(exp2f(dl - pms) + exp2f(dts[k] - pms)) + pm;
-        wL = dl == KB_NEG_INF ? 0.0f : exp2f(dl - pnew);
-      }
+      // q_j = w_L e_j / sum with the split mixing weight
+      // w_L = 2^dl / (2^dl + 2^dts), 2^dl = sum 2^m:  q_j = e_j / (sum + 2^(dts - m))
+      const float den = sum + (leaf_row ? 0.0f : exp2f(dts[k] - msf));
+      const float inv = sum > 0.0f ? 1.0f / den : 0.0f;
 #pragma unroll
-      for (int j = 0; j < 6; ++j) q[j][k] = wL * e[j] * inv_sum;
+      for (int j = 0; j < 6; ++j) q[j][k] = e[j] * inv;
       pcoef[k] = q[2][k] * inv_denom;
     }
   }
@@ -365,41 +360,45 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     v[k] = rhs[k];
     term[k] = rhs[k];
   }
-  // Per term: the scan of u = term * pcoef is a per-thread running sum plus one
-  // wavefront scan of the thread totals; the scan value at position i - 1 comes
-  // from the thread itself, the previous lane (shuffle) or, for a wavefront's
-  // first position, the wavefront offset, so only P[end(i) - 1] and the
-  // parent's term are read back from LDS.
+  // One barrier per term.  The scan of u = term * pcoef is published
+  // wavefront-local (a per-thread running sum plus one wavefront scan of the
+  // thread totals); after the barrier each wavefront offset comes from the
+  // published totals (lanes 0..NW-1, one more wavefront scan), so
+  // P[j] = L[j] + off(wavefront of j).  P[i - 1] comes from the thread itself,
+  // the previous lane, or the offset; P[end(i) - 1] and the parent's term are
+  // read back.  Buffers alternate by parity, so the next term's writes never
+  // race this term's reads.
+  int wend[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) wend[k] = endm1[k] < ZERO ? endm1[k] / (64 * CPT) : 0;
+  const int wv = tid >> 6, lane = tid & 63;
   for (int n = 0; n < P.n_terms; ++n) {
     float* Tb = (n & 1) ? R1 : R0;
-    float* Pb = (n & 1) ? R3 : R2;
+    float* Lb = (n & 1) ? R3 : R2;
     float* wt = (n & 1) ? wB : wA;
     float sc[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) sc[k] = term[k] * pcoef[k] + (k > 0 ? sc[k - 1] : 0.0f);
     const float tsum = sc[CPT - 1];
     const float ws = wave_scan_incl(tsum);
-    if ((tid & 63) == 63) wt[tid >> 6] = ws;
+    if (lane == 63) wt[wv] = ws;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) sc[k] += ws - tsum;  // wavefront-local inclusive scan
+    lds_store_own<CPT>(Lb, sc);
     lds_store_own<CPT>(Tb, term);
     __syncthreads();
-    float woff = 0.0f, A = 0.0f;
-#pragma unroll
-    for (int x = 0; x < NW; ++x) {
-      const float t = wt[x];
-      if (x < (tid >> 6)) woff += t;
-      A += t;
-    }
-    const float base = woff + (ws - tsum);
-#pragma unroll
-    for (int k = 0; k < CPT; ++k) sc[k] += base;
-    lds_store_own<CPT>(Pb, sc);
+    const float wtot = lane < NW ? wt[lane] : 0.0f;
+    const float wincl = wave_scan_incl(wtot);
+    const float wexcl = wincl - wtot;                 // lane x: offset of wavefront x
+    const float A = lane_value(wincl, NW - 1);
+    const float woff = lane_value(wexcl, wv);         // this wavefront's offset
     const float up = __shfl_up(sc[CPT - 1], 1, 64);
-    const float p0 = (tid & 63) == 0 ? woff : up;  // P[i - 1] of slot 0
-    __syncthreads();
+    const float p0 = (lane == 0 ? 0.0f : up) + woff;  // P[i - 1] of slot 0
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const float pm1 = k == 0 ? p0 : sc[k - 1];
-      const float nt = term[k] * diag[k] + pp[k] * (pm1 + (A - Pb[endm1[k]])) + Tb[ppos[k]] * edge[k];
+      const float oe = __shfl(wexcl, wend[k], 64);
+      const float pm1 = k == 0 ? p0 : sc[k - 1] + woff;
+      const float nt = term[k] * diag[k] + pp[k] * (pm1 + (A - (Lb[endm1[k]] + oe))) + Tb[ppos[k]] * edge[k];
       term[k] = nt;
       v[k] += nt;
     }

@@ -49,7 +49,6 @@ __global__ __launch_bounds__(NT, (NT == 1024 && CPT == 2) ? 8 : 1) void fwd_row_
     Xs[0][MAXS + tid] = 0.0f;
     Xs[1][MAXS + tid] = 0.0f;
   }
-  const int(&colv)[CPT] = O.col;
   const int(&c1p)[CPT] = O.c1p;
   const int(&c2p)[CPT] = O.c2p;
 
@@ -89,35 +88,47 @@ __global__ __launch_bounds__(NT, (NT == 1024 && CPT == 2) ? 8 : 1) void fwd_row_
       }
     }
   } else {
+    // child rows staged through LDS at preorder positions (coalesced global
+    // loads of column s = tid + j*NT; positions of the padding slot stay 0)
+    float* L0 = Xs[0];
+    float* L1 = Xs[1];
+    float* L2 = Sc;
+    float* L3 = Sc + MAXS;
     float m[CPT], acc[CPT];
-    int a1[CPT], a2[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       m[k] = KB_NEG_INF;
       acc[k] = 0.0f;
-      a1[k] = c1p[k] < MAXS ? T.col[c1p[k]] : -1;
-      a2[k] = c2p[k] < MAXS ? T.col[c2p[k]] : -1;
     }
     const int b = P.split_ptr[row], e = P.split_ptr[row + 1];
     for (int si = b; si < e; ++si) {
       const size_t l = (size_t)P.split_l[si] * S, r = (size_t)P.split_r[si] * S;
       const float lsp = P.split_lsp[si];
-      const float* Pl = P.pi + l;
-      const float* Pr = P.pi + r;
-      const float* Bl = P.pibar + l;
-      const float* Br = P.pibar + r;
+      if (si > b) __syncthreads();  // the previous split's readers are done
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) {
+        const int sj = tid + j * NT;
+        if (sj < S) {
+          const int i = T.pre[sj];
+          L0[i] = P.pi[l + sj];
+          L1[i] = P.pi[r + sj];
+          L2[i] = P.pibar[l + sj];
+          L3[i] = P.pibar[r + sj];
+        }
+      }
+      __syncthreads();
 #pragma unroll
       for (int k = 0; k < CPT; ++k) {
         const int i = own_pos<NT, CPT>(k);
         if (i < S) {
-          const int s = colv[k];
-          const float pl = Pl[s], pr = Pr[s];
+          const bool h1 = c1p[k] != MAXS, h2 = c2p[k] != MAXS;
+          const float pl = L0[i], pr = L1[i];
           const float d = P.pD.at(item, i), sp = P.pS.at(item, i);
           const float t0 = lsp + d + pl + pr;
-          const float t1 = lsp + pl + Br[s];
-          const float t2 = lsp + pr + Bl[s];
-          const float l1 = a1[k] >= 0 ? Pl[a1[k]] : KB_NEG_INF, r1 = a1[k] >= 0 ? Pr[a1[k]] : KB_NEG_INF;
-          const float l2 = a2[k] >= 0 ? Pl[a2[k]] : KB_NEG_INF, r2 = a2[k] >= 0 ? Pr[a2[k]] : KB_NEG_INF;
+          const float t1 = lsp + pl + L3[i];
+          const float t2 = lsp + pr + L2[i];
+          const float l1 = h1 ? L0[c1p[k]] : KB_NEG_INF, r1 = h1 ? L1[c1p[k]] : KB_NEG_INF;
+          const float l2 = h2 ? L0[c2p[k]] : KB_NEG_INF, r2 = h2 ? L1[c2p[k]] : KB_NEG_INF;
           const float t3 = lsp + sp + l1 + r2;
           const float t4 = lsp + sp + r1 + l2;
           const float m5 = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), t4);
@@ -127,6 +138,7 @@ __global__ __launch_bounds__(NT, (NT == 1024 && CPT == 2) ? 8 : 1) void fwd_row_
         }
       }
     }
+    __syncthreads();  // the staging buffers become the sweep buffers
 #pragma unroll
     for (int k = 0; k < CPT; ++k) v[k] = log2f(acc[k]) + m[k];
     if (P.dts_out) {  // the backward reuses the split term at Pi*

@@ -112,6 +112,7 @@ struct kb_plan {
   // preorder tables (see kb_rowops.hpp)
   int* d_pre = nullptr; int* d_pcol = nullptr; int* d_c1pos = nullptr; int* d_c2pos = nullptr; int* d_ppos = nullptr;
   int* d_pflag = nullptr; int* d_endpos = nullptr; int* d_tin = nullptr; int* d_euler = nullptr;
+  int* d_post = nullptr;
   int* d_euler_col = nullptr; int* d_tin_col = nullptr;  // the Euler tour in column terms
   kb::TreeScanDev tscan() const { return kb::TreeScanDev{S, d_pre, d_endpos, d_euler_col, d_tin_col}; }
   double* E64 = nullptr; int* n_e_iter = nullptr; double* loss_terms = nullptr; double* loss64 = nullptr;
@@ -146,6 +147,7 @@ struct kb_plan {
     t.endpos = d_endpos;
     t.tin = d_tin;
     t.euler = d_euler;
+    t.post = d_post;
     return t;
   }
 
@@ -519,6 +521,13 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
   rc |= upload(&p->d_tin, tin);
   rc |= upload(&p->d_euler, euler);
   {
+    std::vector<int> post;
+    post.reserve(S);
+    for (int e : euler)
+      if (e & 1) post.push_back(e >> 1);
+    rc |= upload(&p->d_post, post);
+  }
+  {
     std::vector<int> ecol(euler.size()), tcol(S);
     for (size_t q = 0; q < euler.size(); ++q) ecol[q] = (pcol[euler[q] >> 1] << 1) | (euler[q] & 1);
     for (int s = 0; s < S; ++s) tcol[s] = tin[pre[s]];
@@ -557,7 +566,7 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
                     (void*)p->d_copy_src, (void*)p->d_cls_ptr, (void*)p->d_cls_rows, (void*)p->d_rep_of, (void*)p->d_m_side_ptr, (void*)p->d_m_side, (void*)p->d_m_root,
                     (void*)p->d_dts,
                     (void*)p->d_c1pos, (void*)p->d_c2pos, (void*)p->d_ppos, (void*)p->d_pflag, (void*)p->d_endpos,
-                    (void*)p->d_tin, (void*)p->d_euler, (void*)p->d_euler_col, (void*)p->d_tin_col, (void*)p->c_Ebar, (void*)p->c_E, (void*)p->c_mt,
+                    (void*)p->d_tin, (void*)p->d_euler, (void*)p->d_post, (void*)p->d_euler_col, (void*)p->d_tin_col, (void*)p->c_Ebar, (void*)p->c_E, (void*)p->c_mt,
                     (void*)p->c_col})
     p->owned.push_back(ptr);
   if (rc) {

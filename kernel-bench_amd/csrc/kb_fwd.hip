@@ -19,8 +19,20 @@
 // with per-position constants a = 2^DL + 2^Ebar, emc = 2^(E+mt), k1 = 2^SL1,
 // k2 = 2^SL2 prepared once per solve.  NA(x)[s] = rowsum - pathsum(s) as in
 // the reference; the path sums come from an Euler-tour prefix scan.
-// Threads own contiguous preorder positions (see kb_rowops.hpp): three
-// barriers per sweep.
+// Two layouts of the sweep loop:
+//  * fwd_row_kernel (rows of up to 4096 positions): ONE barrier per sweep.
+//    Thread t owns preorder positions t*CPT+k and postorder slots t*CPT+k.  The
+//    path sum is  ps(i) = Pre(i) - PostEx(tin(i) - i),  Pre the inclusive
+//    preorder prefix sum and PostEx the exclusive postorder prefix sum (the
+//    nodes left before entering i, tin(i) - i of them, are the first ones in
+//    postorder).  Each thread updates its preorder positions AND the nodes of
+//    its postorder slots (same arithmetic on the same published values, so both
+//    copies are identical), scans both in registers, and publishes y, the two
+//    wavefront-local scans and the wavefront totals under one barrier; the
+//    wavefront offsets are applied by the readers.  Three double-buffered LDS
+//    rows.
+//  * fwd_row_kernel_euler (larger rows): wavefront-segment ownership and an
+//    Euler-tour scan, three barriers per sweep, half the LDS.
 #include "kb_device.hpp"
 #include "kb_kernels.hpp"
 #include "kb_rowops.hpp"
@@ -28,7 +40,7 @@
 namespace kb {
 
 template <int NT, int CPT, bool WEIGHTED>
-__global__ __launch_bounds__(NT, (NT == 1024 && CPT == 2) ? 8 : 1) void fwd_row_kernel(FwdParams P, int first) {
+__global__ __launch_bounds__(NT, (NT == 1024 && CPT == 2) ? 8 : 1) void fwd_row_kernel_euler(FwdParams P, int first) {
   constexpr int MAXS = NT * CPT;
   constexpr int NW = NT / 64;
   __shared__ float Xs[2][MAXS + 64];   // unnormalised y of the sweep (double buffer); [MAXS] == 0
@@ -229,12 +241,282 @@ __global__ __launch_bounds__(NT, (NT == 1024 && CPT == 2) ? 8 : 1) void fwd_row_
   if (tid == 0) P.rowmax[row] = rmax;
 }
 
-#define KB_FWD_CASE(NT_, CPT_)                                                                            \
+template <int NT, int CPT, bool WEIGHTED>
+__global__ __launch_bounds__(NT, 1) void fwd_row_kernel(FwdParams P, int first) {
+  constexpr int MAXS = NT * CPT;
+  constexpr int NW = NT / 64;
+  constexpr int ZERO = MAXS;      // padding slot: 0 in the sweep buffers
+  constexpr int SEG = 64 * CPT;   // postorder slots per wavefront
+  __shared__ __align__(16) float Lb[4][MAXS + 64];  // split staging; then X (y of the sweep), Q (postorder scan)
+  __shared__ float wP[NW], wQ[NW], wM[NW];
+  float* X = Lb[0];
+  float* Q = Lb[1];
+
+  const PreDev& T = P.pre;
+  const int S = P.S;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int row = P.sched_rows[first + blockIdx.x];
+  const int leaf_row = P.row_kind[row];
+  const int item = P.item[row];
+  const size_t cb = (size_t)item * P.const_stride;   // constants are [G, S] in preorder
+
+  // Tables of the own positions i = tid*CPT + k and of the own postorder slots.
+  // In preorder (child1 first) child1 of i is i + 1: from registers, except
+  // for the last own position, whose child1 is read from X.
+  int c2p[CPT], nex[CPT], qp[CPT], pre_s[CPT];
+  bool h1[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int i = own_pos_c<NT, CPT>(k);
+    const bool ok = i < S;
+    const int a = ok ? T.c1pos[i] : -1, b = ok ? T.c2pos[i] : -1;
+    h1[k] = a >= 0;
+    c2p[k] = b >= 0 ? b : ZERO;
+    nex[k] = ok ? T.tin[i] - i : 0;
+    qp[k] = ok ? T.post[i] : ZERO;
+    const int sj = tid + k * NT;
+    pre_s[k] = sj < S ? T.pre[sj] : 0;
+  }
+  const int c1last = h1[CPT - 1] ? own_pos_c<NT, CPT>(CPT - 1) + 1 : ZERO;
+
+  // ---- initial row (log2), own positions
+  float v[CPT];
+  int lpos = -1;
+  float leaf_obs = 0.0f;
+  if (leaf_row) {
+    const int leaf = P.leaf_state[row];
+    lpos = T.pre[leaf];
+    const int lend = T.endpos[lpos];
+    leaf_obs = P.leaf_logp[cb + lpos];
+    const float leaf_col = WEIGHTED ? P.col[lpos] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int i = own_pos_c<NT, CPT>(k);
+      v[k] = KB_NEG_INF;
+      if (i < S) {
+        const bool hit = i == lpos;
+        const bool desc = i >= lpos && i < lend;
+        const size_t ci = cb + i;
+        const float pi_w = hit ? leaf_obs : KB_NEG_INF;
+        const float pibar_w = desc ? KB_NEG_INF : P.mt[ci] + leaf_col + leaf_obs;
+        const float pi_s1 = (h1[k] && i + 1 == lpos) ? leaf_obs : KB_NEG_INF;
+        const float pi_s2 = c2p[k] == lpos ? leaf_obs : KB_NEG_INF;  // padding ZERO never equals lpos
+        const float t0 = P.DL[ci] + pi_w;
+        const float t1 = pi_w + P.Ebar[ci];
+        const float t2 = pibar_w + P.E[ci];
+        const float t3 = P.SL1[ci] + pi_s1;
+        const float t4 = P.SL2[ci] + pi_s2;
+        const float t5 = hit ? P.leaf_logp[ci] : KB_NEG_INF;
+        const float m = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, t5));
+        const float ms = fsafe(m);
+        const float sum = exp2f(t0 - ms) + exp2f(t1 - ms) + exp2f(t2 - ms) + exp2f(t3 - ms) + exp2f(t4 - ms) +
+                          exp2f(t5 - ms);
+        v[k] = log2f(sum) + m;
+      }
+    }
+  } else {
+    // child rows staged through LDS at preorder positions (coalesced global
+    // loads of column s = tid + j*NT)
+    float m[CPT], acc[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      m[k] = KB_NEG_INF;
+      acc[k] = 0.0f;
+    }
+    const int b = P.split_ptr[row], e = P.split_ptr[row + 1];
+    for (int si = b; si < e; ++si) {
+      const size_t l = (size_t)P.split_l[si] * S, r = (size_t)P.split_r[si] * S;
+      const float lsp = P.split_lsp[si];
+      if (si > b) __syncthreads();  // the previous split's readers are done
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) {
+        const int sj = tid + j * NT;
+        if (sj < S) {
+          const int i = pre_s[j];
+          Lb[0][i] = P.pi[l + sj];
+          Lb[1][i] = P.pi[r + sj];
+          Lb[2][i] = P.pibar[l + sj];
+          Lb[3][i] = P.pibar[r + sj];
+        }
+      }
+      __syncthreads();
+      float pl[CPT], pr[CPT], bl[CPT], br[CPT];
+      lds_load_own<CPT>(Lb[0], pl);
+      lds_load_own<CPT>(Lb[1], pr);
+      lds_load_own<CPT>(Lb[2], bl);
+      lds_load_own<CPT>(Lb[3], br);
+      const bool hl = h1[CPT - 1];
+      const float pl_last = hl ? Lb[0][c1last] : KB_NEG_INF, pr_last = hl ? Lb[1][c1last] : KB_NEG_INF;
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        const int i = own_pos_c<NT, CPT>(k);
+        if (i < S) {
+          const bool h2 = c2p[k] != ZERO;
+          const float d = P.pD.at(item, i), sp = P.pS.at(item, i);
+          const float t0 = lsp + d + pl[k] + pr[k];
+          const float t1 = lsp + pl[k] + br[k];
+          const float t2 = lsp + pr[k] + bl[k];
+          float l1, r1;
+          if (k + 1 < CPT) {
+            l1 = h1[k] ? pl[k + 1] : KB_NEG_INF;
+            r1 = h1[k] ? pr[k + 1] : KB_NEG_INF;
+          } else {
+            l1 = pl_last;
+            r1 = pr_last;
+          }
+          const float l2 = h2 ? Lb[0][c2p[k]] : KB_NEG_INF, r2 = h2 ? Lb[1][c2p[k]] : KB_NEG_INF;
+          const float t3 = lsp + sp + l1 + r2;
+          const float t4 = lsp + sp + r1 + l2;
+          const float m5 = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), t4);
+          const float ms = fsafe(m5);
+          const float s5 = exp2f(t0 - ms) + exp2f(t1 - ms) + exp2f(t2 - ms) + exp2f(t3 - ms) + exp2f(t4 - ms);
+          lse_merge(m[k], acc[k], m5, s5);
+        }
+      }
+    }
+    __syncthreads();  // the staging buffers become the sweep buffers
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) v[k] = log2f(acc[k]) + m[k];
+    if (P.dts_out) {  // the backward reuses the split term at Pi*
+      float* dst = P.dts_out + (size_t)row * S;
+#pragma unroll
+      for (int k = 0; k < CPT; ++k)
+        if (own_pos_c<NT, CPT>(k) < S) dst[own_pos_c<NT, CPT>(k)] = v[k];
+    }
+  }
+  if (tid < 64) {  // padding slots read by the child gathers (after the staging)
+    X[MAXS + tid] = 0.0f;
+    Q[MAXS + tid] = 0.0f;
+  }
+
+  // ---- linear space relative to the row maximum
+  float lm = KB_NEG_INF;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) lm = fmaxf(lm, v[k]);
+  const float Ms = fsafe(block_max1<NT>(lm, wM));
+  const float leaf_lin = leaf_row ? exp2f(leaf_obs - Ms) : 0.0f;  // lpos = -1 for split rows
+  float y[CPT], dl[CPT], ca[CPT], ce[CPT], ck1[CPT], ck2[CPT], cw[CPT], cwq[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int i = own_pos_c<NT, CPT>(k);
+    const bool ok = i < S;
+    y[k] = ok ? exp2f(v[k] - Ms) : 0.0f;
+    dl[k] = leaf_row ? (i == lpos ? leaf_lin : 0.0f) : y[k];
+    ca[k] = ok ? P.lin_a[cb + i] : 0.0f;
+    ce[k] = ok ? P.lin_emc[cb + i] : 0.0f;
+    ck1[k] = h1[k] ? P.lin_k1[cb + i] : 0.0f;  // 0 without child1: the x1 operand is then unused
+    ck2[k] = ok ? P.lin_k2[cb + i] : 0.0f;
+    cw[k] = WEIGHTED ? (ok ? P.colw[i] : 0.0f) : 1.0f;
+    cwq[k] = WEIGHTED ? (qp[k] < S ? P.colw[qp[k]] : 0.0f) : 1.0f;
+  }
+  int kexp = 0;
+  float ps[CPT], rowsum = 0.0f, f = 1.0f;
+
+  for (int sweep = 0;; ++sweep) {
+    // phase A: publish y; inclusive preorder scan (wavefront-local) in registers
+    float sp[CPT], ta = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      ta += cw[k] * y[k];
+      sp[k] = ta;
+    }
+    const float wa = wave_scan_incl(ta);
+    lds_store_own<CPT>(X, y);
+    if (lane == 63) wP[wv] = wa;
+    __syncthreads();
+    // phase B: preorder offsets and row sum; the postorder values and the
+    // child2 values (read before the next barrier); exclusive postorder scan
+    const float tp = lane < NW ? wP[lane] : 0.0f;
+    float yq[CPT], x2[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      yq[k] = X[qp[k]];
+      x2[k] = X[c2p[k]];
+    }
+    const float x1last = X[c1last];
+    const float ip = wave_scan_first<NW>(tp);
+    const float tsum = lane_value(ip, NW - 1);
+    const float offp = lane_value(ip - tp, wv) + (wa - ta);
+    float sq[CPT], tb = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      sq[k] = tb;
+      tb += cwq[k] * yq[k];
+    }
+    const float wb = wave_scan_incl(tb);
+    const float ob = wb - tb;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) sq[k] += ob;
+    lds_store_own<CPT>(Q, sq);
+    if (lane == 63) wQ[wv] = wb;
+    const int e = tsum > 0.0f ? __builtin_amdgcn_frexp_expf(tsum) : 0;
+    f = __builtin_amdgcn_ldexpf(1.0f, -e);
+    kexp += e;
+    rowsum = tsum * f;
+    __syncthreads();
+    // phase C: path sums ps(i) = Pre(i) - PostEx(tin(i) - i)
+    const float tq = lane < NW ? wQ[lane] : 0.0f;
+    const float iq = wave_scan_first<NW>(tq);
+    const float eq = iq - tq;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int n = nex[k];
+      ps[k] = (sp[k] + offp) - (Q[n] + __shfl(eq, n / SEG, 64));
+    }
+    if (sweep == P.n_sweeps) break;
+    // y' = f (a y + k1 y[c1] + k2 y[c2] + emc (tsum - ps)) + dl 2^-kexp: f is a
+    // power of two, so scaling the sum instead of each operand rounds the same
+    const float scale = __builtin_amdgcn_ldexpf(1.0f, -kexp);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const float x1 = k + 1 < CPT ? y[k + 1] : x1last;
+      float z = ca[k] * y[k];
+      z += ck1[k] * x1;
+      z += ck2[k] * x2[k];
+      z += ce[k] * fmaxf(tsum - ps[k], 0.0f);
+      y[k] = z * f + dl[k] * scale;
+    }
+  }
+
+  // ---- outputs: Pi, Pibar from the final Pi, and the (weighted) row max
+  const float M = Ms + (float)kexp;
+  float piv[CPT], pbv[CPT];
+  float lmax = KB_NEG_INF;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int i = own_pos_c<NT, CPT>(k);
+    piv[k] = KB_NEG_INF;
+    pbv[k] = KB_NEG_INF;
+    if (i < S) {
+      const float x = y[k] * f;
+      piv[k] = x > 0.0f ? log2f(x) + M : KB_NEG_INF;
+      const float na = rowsum - ps[k] * f;
+      pbv[k] = na > 0.0f ? log2f(na) + M + P.mt[cb + i] : KB_NEG_INF;
+      lmax = fmaxf(lmax, WEIGHTED ? P.col[i] + piv[k] : piv[k]);
+    }
+  }
+  // Lb[2], Lb[3] are unused since the staging
+  lds_store_own<CPT>(Lb[2], piv);
+  lds_store_own<CPT>(Lb[3], pbv);
+  const float rmax = block_max1<NT>(lmax, wM);  // also publishes the staging
+  const size_t rb = (size_t)row * S;
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int sj = tid + j * NT;
+    if (sj < S) {
+      P.pi[rb + sj] = Lb[2][pre_s[j]];
+      P.pibar[rb + sj] = Lb[3][pre_s[j]];
+    }
+  }
+  if (tid == 0) P.rowmax[row] = rmax;
+}
+
+#define KB_FWD_CASE(NT_, CPT_, KERNEL_)                                                                   \
   if (S <= NT_ * CPT_) {                                                                                  \
     if (P.use_col)                                                                                        \
-      hipLaunchKernelGGL((fwd_row_kernel<NT_, CPT_, true>), dim3(W), dim3(NT_), 0, st, P, first);         \
+      hipLaunchKernelGGL((KERNEL_<NT_, CPT_, true>), dim3(W), dim3(NT_), 0, st, P, first);                \
     else                                                                                                  \
-      hipLaunchKernelGGL((fwd_row_kernel<NT_, CPT_, false>), dim3(W), dim3(NT_), 0, st, P, first);        \
+      hipLaunchKernelGGL((KERNEL_<NT_, CPT_, false>), dim3(W), dim3(NT_), 0, st, P, first);               \
     return;                                                                                               \
   }
 
@@ -272,18 +554,18 @@ void launch_fwd_wave(const FwdParams& P, int first, int W, hipStream_t st) {
   if (W <= 0) return;
   const int S = P.S;
   if (P.wide == 1) {  // fewer, wider threads per row (tuning knob)
-    KB_FWD_CASE(256, 8)
+    KB_FWD_CASE(256, 8, fwd_row_kernel)
   }
   if (P.wide == 2) {  // more, narrower threads per row (tuning knob)
-    KB_FWD_CASE(1024, 2)
+    KB_FWD_CASE(1024, 2, fwd_row_kernel)
   }
-  KB_FWD_CASE(64, 2)
-  KB_FWD_CASE(128, 2)
-  KB_FWD_CASE(256, 2)
-  KB_FWD_CASE(256, 4)
-  KB_FWD_CASE(512, 4)
-  KB_FWD_CASE(1024, 4)
-  KB_FWD_CASE(1024, 8)
+  KB_FWD_CASE(64, 2, fwd_row_kernel)
+  KB_FWD_CASE(128, 2, fwd_row_kernel)
+  KB_FWD_CASE(256, 2, fwd_row_kernel)
+  KB_FWD_CASE(256, 4, fwd_row_kernel)
+  KB_FWD_CASE(512, 4, fwd_row_kernel)
+  KB_FWD_CASE(1024, 4, fwd_row_kernel)
+  KB_FWD_CASE(1024, 8, fwd_row_kernel_euler)
 }
 
 }  // namespace kb

@@ -39,6 +39,18 @@ __device__ __forceinline__ float wave_scan_incl(float x) {
   return x;
 }
 
+// Inclusive scan (+) over lanes [0, N) of a wavefront, N <= 16 (row 0 only;
+// the other lanes hold partial sums).
+template <int N>
+__device__ __forceinline__ float wave_scan_first(float x) {
+  static_assert(N >= 1 && N <= 16, "row-0 scan");
+  if constexpr (N > 1) x += dpp_shift0<0x111>(x);
+  if constexpr (N > 2) x += dpp_shift0<0x112>(x);
+  if constexpr (N > 4) x += dpp_shift0<0x114>(x);
+  if constexpr (N > 8) x += dpp_shift0<0x118>(x);
+  return x;
+}
+
 __device__ __forceinline__ float lane_value(float x, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
 }
@@ -160,6 +172,7 @@ struct PreDev {
   const int* endpos;  // [S]   exclusive end of the subtree
   const int* tin;     // [S]   Euler entry event of the position
   const int* euler;   // [2S]  event -> (position << 1) | is_exit
+  const int* post;    // [S]   postorder slot -> position (the order of the Euler exit events)
 };
 
 // Position of slot k of this thread.

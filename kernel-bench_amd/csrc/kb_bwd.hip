@@ -387,18 +387,26 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     lds_store_own<CPT>(Lb, sc);
     lds_store_own<CPT>(Tb, term);
     __syncthreads();
-    const float wtot = lane < NW ? wt[lane] : 0.0f;
-    const float wincl = wave_scan_incl(wtot);
-    const float wexcl = wincl - wtot;                 // lane x: offset of wavefront x
-    const float A = lane_value(wincl, NW - 1);
-    const float woff = lane_value(wexcl, wv);         // this wavefront's offset
-    const float up = __shfl_up(sc[CPT - 1], 1, 64);
-    const float p0 = (lane == 0 ? 0.0f : up) + woff;  // P[i - 1] of slot 0
+    float le[CPT], tpar[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const float oe = __shfl(wexcl, wend[k], 64);
+      le[k] = Lb[endm1[k]];
+      tpar[k] = Tb[ppos[k]];
+    }
+    const float wtot = lane < NW ? wt[lane] : 0.0f;
+    const float wincl = wave_scan_first<NW>(wtot);
+    const float wexcl = wincl - wtot;                 // lane x < NW: offset of wavefront x
+    const float A = lane_value(wincl, NW - 1);
+    const float woff = lane_value(wexcl, wv);         // this wavefront's offset
+    const float p0 = wave_prev_lane(sc[CPT - 1]) + woff;  // P[i - 1] of slot 0
+    float oe[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) oe[k] = __shfl(wexcl, wend[k], 64);
+    __builtin_amdgcn_sched_barrier(0);  // all permutes in flight before the first use
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
       const float pm1 = k == 0 ? p0 : sc[k - 1] + woff;
-      const float nt = term[k] * diag[k] + pp[k] * (pm1 + (A - (Lb[endm1[k]] + oe))) + Tb[ppos[k]] * edge[k];
+      const float nt = term[k] * diag[k] + pp[k] * (pm1 + (A - (le[k] + oe[k]))) + tpar[k] * edge[k];
       term[k] = nt;
       v[k] += nt;
     }

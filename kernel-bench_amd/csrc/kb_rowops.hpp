@@ -39,6 +39,11 @@ __device__ __forceinline__ float wave_scan_incl(float x) {
   return x;
 }
 
+// Value of the previous lane (lane 0 reads 0): DPP wavefront shift.
+__device__ __forceinline__ float wave_prev_lane(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x138, 0xf, 0xf, false));  // wave_shr:1
+}
+
 // Inclusive scan (+) over lanes [0, N) of a wavefront, N <= 16 (row 0 only;
 // the other lanes hold partial sums).
 template <int N>

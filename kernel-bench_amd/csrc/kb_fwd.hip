@@ -241,8 +241,13 @@ __global__ __launch_bounds__(NT, (NT == 1024 && CPT == 2) ? 8 : 1) void fwd_row_
   if (tid == 0) P.rowmax[row] = rmax;
 }
 
+// Minimum waves per SIMD (the second launch-bounds argument): 6 keeps three
+// 512 x 4 workgroups resident per CU (at most 80 VGPRs; the weighted variant
+// would spill).
+#define FWD_MIN_WAVES(NT, CPT, W) (((NT) == 512 && (CPT) == 4 && !(W)) ? 6 : 1)
+
 template <int NT, int CPT, bool WEIGHTED>
-__global__ __launch_bounds__(NT, 1) void fwd_row_kernel(FwdParams P, int first) {
+__global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_kernel(FwdParams P, int first) {
   constexpr int MAXS = NT * CPT;
   constexpr int NW = NT / 64;
   constexpr int ZERO = MAXS;      // padding slot: 0 in the sweep buffers
@@ -504,8 +509,9 @@ __global__ __launch_bounds__(NT, 1) void fwd_row_kernel(FwdParams P, int first) 
   for (int j = 0; j < CPT; ++j) {
     const int sj = tid + j * NT;
     if (sj < S) {
-      P.pi[rb + sj] = Lb[2][pre_s[j]];
-      P.pibar[rb + sj] = Lb[3][pre_s[j]];
+      const int i = T.pre[sj];  // reloaded: keeps the table out of registers during the sweeps
+      P.pi[rb + sj] = Lb[2][i];
+      P.pibar[rb + sj] = Lb[3][i];
     }
   }
   if (tid == 0) P.rowmax[row] = rmax;

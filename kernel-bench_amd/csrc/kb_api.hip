@@ -596,6 +596,7 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
   kb::EStepParams E{};
   E.tr = p->tree();
   E.ts = p->tscan();
+  E.pd = p->predev();
   E.S = S;
   E.n_tlevels = p->n_tlevels;
   E.tlevel_ptr = p->d_tlevel_ptr;

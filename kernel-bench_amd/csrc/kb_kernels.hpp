@@ -17,6 +17,7 @@ int set_error(int code, const char* fmt, ...);
 struct EStepParams {
   TreeDev tr;
   TreeScanDev ts;
+  PreDev pd;                  // preorder tables (register-resident kernel)
   int S;
   int n_tlevels;              // depth levels, root first
   const int* tlevel_ptr;      // [n_tlevels + 1]

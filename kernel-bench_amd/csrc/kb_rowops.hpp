@@ -68,6 +68,52 @@ __device__ __forceinline__ float wave_reduce_max(float x) {
   return x;
 }
 
+// ---- float64 wavefront primitives (DPP on the two 32-bit halves) -------------
+
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ double dpp_shift0_f64(double x) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(x);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)b, CTRL, ROW_MASK, BANK_MASK, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), CTRL, ROW_MASK, BANK_MASK, false);
+  return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+}
+
+__device__ __forceinline__ double wave_scan_incl_f64(double x) {
+  x += dpp_shift0_f64<0x111>(x);
+  x += dpp_shift0_f64<0x112>(x);
+  x += dpp_shift0_f64<0x114>(x);
+  x += dpp_shift0_f64<0x118>(x);
+  x += dpp_shift0_f64<0x142, 0xa>(x);
+  x += dpp_shift0_f64<0x143, 0xc>(x);
+  return x;
+}
+
+template <int N>
+__device__ __forceinline__ double wave_scan_first_f64(double x) {
+  static_assert(N >= 1 && N <= 16, "row-0 scan");
+  if constexpr (N > 1) x += dpp_shift0_f64<0x111>(x);
+  if constexpr (N > 2) x += dpp_shift0_f64<0x112>(x);
+  if constexpr (N > 4) x += dpp_shift0_f64<0x114>(x);
+  if constexpr (N > 8) x += dpp_shift0_f64<0x118>(x);
+  return x;
+}
+
+__device__ __forceinline__ double lane_value_f64(double x, int lane) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(x);
+  const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, lane);
+  const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), lane);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+__device__ __forceinline__ double wave_prev_lane_f64(double x) { return dpp_shift0_f64<0x138>(x); }  // wave_shr:1
+
+__device__ __forceinline__ double shfl_f64(double x, int src) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(x);
+  const unsigned lo = (unsigned)__shfl((int)(unsigned)b, src, 64);
+  const unsigned hi = (unsigned)__shfl((int)(unsigned)(b >> 32), src, 64);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
 // ---- block reductions / scans (one barrier each) -----------------------------
 // `wtot` is LDS scratch of NW floats (2*NW for the paired scan).  It is read
 // by every thread after the barrier, so the next writer must be separated from

@@ -858,6 +858,7 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   kb::EpiParams X{};
   X.tr = p->tree();
   X.ts = p->tscan();
+  X.pd = p->predev();
   X.S = S;
   X.n_tlevels = p->n_tlevels;
   X.tlevel_ptr = p->d_tlevel_ptr;

@@ -371,8 +371,473 @@ __global__ __launch_bounds__(XNT) void epilogue_kernel(EpiParams P) {
   }
 }
 
+// ---- register-resident epilogue for trees of up to NT*CPT nodes ------------
+// The algorithm, the order of the BiCGSTAB steps and the stopping rules are
+// those of epilogue_kernel above; every [S] vector lives in registers at
+// preorder positions (thread t owns positions t*CPT + k), and the sums over
+// the tree are register scans (DPP float64) with one LDS exchange:
+//   * one E-step VJP (a parent gather and one subtree sum): one barrier;
+//   * one or two dot products: one barrier;
+//   * ancestors-or-self sums, Pre(i) - PostEx(tin(i) - i): two barriers.
+template <int NT, int CPT>
+__global__ __launch_bounds__(NT) void epilogue_pre_kernel(EpiParams P) {
+  constexpr int MAXS = NT * CPT;
+  constexpr int NW = NT / 64;
+  constexpr int ZERO = MAXS;     // padding slot: 0 in every buffer
+  constexpr int SEG = 64 * CPT;  // positions / postorder slots per wavefront
+  __shared__ __align__(16) double Xp[MAXS + 64];  // VJP: child1-side values for the parent gather
+  __shared__ __align__(16) double Up[MAXS + 64];  // VJP: child2-side values; E for the child gathers
+  __shared__ __align__(16) double Lv[MAXS + 64];  // wavefront-local inclusive preorder scan
+  __shared__ __align__(16) double Xw[MAXS + 64];  // path sums: values at positions
+  __shared__ __align__(16) double Qb[MAXS + 64];  // path sums: wavefront-local exclusive postorder scan
+  __shared__ double wV[NW], wP[NW], wQ[NW], mred[NW];
+  __shared__ double red[2][2 * NW];
+  const PreDev& T = P.pd;
+  const int S = P.S;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const double NINF = -__builtin_inf();
+  const double TINY = 2.2250738585072014e-308;
+  const double LN2 = 0.6931471805599453;
+
+  int colk[CPT], c2p[CPT], nex[CPT], qp[CPT], ppos[CPT], endm1[CPT];
+  bool okp[CPT], h1[CPT], pfl[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int i = tid * CPT + k;
+    okp[k] = i < S;
+    colk[k] = okp[k] ? T.col[i] : 0;
+    const int a = okp[k] ? T.c1pos[i] : -1, b = okp[k] ? T.c2pos[i] : -1;
+    h1[k] = a >= 0;  // child1 of i is i + 1 (preorder, child1 first)
+    c2p[k] = b >= 0 ? b : ZERO;
+    nex[k] = okp[k] ? T.tin[i] - i : 0;
+    qp[k] = okp[k] ? T.post[i] : ZERO;
+    const int pa = okp[k] ? T.ppos[i] : -1;
+    ppos[k] = pa >= 0 ? pa : ZERO;
+    pfl[k] = pa >= 0 && T.pflag[i] != 0;
+    endm1[k] = okp[k] ? T.endpos[i] - 1 : ZERO;
+  }
+  const int c1last = h1[CPT - 1] ? tid * CPT + CPT : ZERO;
+  if (tid < 64) {
+    Xp[MAXS + tid] = 0.0;
+    Up[MAXS + tid] = 0.0;
+    Lv[MAXS + tid] = 0.0;
+    Xw[MAXS + tid] = 0.0;
+    Qb[MAXS + tid] = 0.0;
+  }
+  __syncthreads();
+
+  // sums over all positions of a and b (fixed order), one barrier
+  int rbuf = 0;
+  auto sum2 = [&](double a, double b, double& ra, double& rb) {
+    const double sa = lane_value_f64(wave_scan_incl_f64(a), 63);
+    const double sb = lane_value_f64(wave_scan_incl_f64(b), 63);
+    double* R = red[rbuf];
+    rbuf ^= 1;
+    if (lane == 0) {
+      R[wv] = sa;
+      R[NW + wv] = sb;
+    }
+    __syncthreads();
+    ra = 0.0;
+    rb = 0.0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      ra += R[w];
+      rb += R[NW + w];
+    }
+  };
+  auto dot = [&](const double (&a)[CPT], const double (&b)[CPT]) {
+    double l = 0.0, r0, r1;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) l += a[k] * b[k];
+    sum2(l, 0.0, r0, r1);
+    return r0;
+  };
+
+  // ancestors-or-self sums of x and the total (two barriers)
+  auto path_sums = [&](const double (&x)[CPT], double (&ps)[CPT], double& total) {
+    double sp[CPT], ta = 0.0;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      ta += x[k];
+      sp[k] = ta;
+    }
+    const double wa = wave_scan_incl_f64(ta);
+    lds_store_own_f64<CPT>(Xw, x);
+    if (lane == 63) wP[wv] = wa;
+    __syncthreads();
+    const double tp = lane < NW ? wP[lane] : 0.0;
+    double yq[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) yq[k] = Xw[qp[k]];
+    const double ip = wave_scan_first_f64<NW>(tp);
+    total = lane_value_f64(ip, NW - 1);
+    const double offp = lane_value_f64(ip - tp, wv) + (wa - ta);
+    double sq[CPT], tb = 0.0;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      sq[k] = tb;
+      tb += yq[k];
+    }
+    const double wb = wave_scan_incl_f64(tb);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) sq[k] += wb - tb;
+    lds_store_own_f64<CPT>(Qb, sq);
+    if (lane == 63) wQ[wv] = wb;
+    __syncthreads();
+    const double tq = lane < NW ? wQ[lane] : 0.0;
+    const double iq = wave_scan_first_f64<NW>(tq);
+    const double eq = iq - tq;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int n = nex[k];
+      ps[k] = (sp[k] + offp) - (Qb[n] + shfl_f64(eq, n / SEG));
+    }
+  };
+
+  // subtree (descendants-or-self) sums of u after the caller's scan setup:
+  // sc = wavefront-local inclusive scan (published in Lv with the wavefront
+  // totals in wV before the caller's barrier); returns the total
+  auto subtree_finish = [&](const double (&sc)[CPT], double (&sub)[CPT]) {
+    double le[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) le[k] = Lv[endm1[k]];
+    const double tv = lane < NW ? wV[lane] : 0.0;
+    const double iv = wave_scan_first_f64<NW>(tv);
+    const double ev = iv - tv;
+    const double tot = lane_value_f64(iv, NW - 1);
+    const double offv = lane_value_f64(ev, wv);
+    const double pm0 = wave_prev_lane_f64(sc[CPT - 1]) + offv;  // P[i - 1] of slot 0
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const double pm1 = k == 0 ? pm0 : sc[k - 1] + offv;
+      sub[k] = (le[k] + shfl_f64(ev, endm1[k] / SEG)) - pm1;
+    }
+    return tot;
+  };
+
+  // ---- E-step linearisation at E* (fp64 recomputation of pristine e_step.py:42-91)
+  double Ev[CPT], R[CPT], ID[CPT], W0[CPT], W1[CPT], W2[CPT], W3[CPT];
+  double lm = NINF;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    Ev[k] = okp[k] ? (double)P.E[colk[k]] : 0.0;
+    if (okp[k]) lm = fmax(lm, P.use_col ? (double)P.col[colk[k]] + Ev[k] : Ev[k]);
+  }
+  lds_store_own_f64<CPT>(Up, Ev);  // for the child gathers (published by the barriers below)
+  const double rmax = block_max<NT>(lm, mred);
+  const double rms = rmax == NINF ? 0.0 : rmax;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k)
+    R[k] = okp[k] ? exp2((P.use_col ? (double)P.col[colk[k]] + Ev[k] : Ev[k]) - rms) : 0.0;
+  double Upath[CPT], rowsum;
+  path_sums(R, Upath, rowsum);
+  {
+    const double e1last = Up[c1last];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      W0[k] = W1[k] = W2[k] = W3[k] = ID[k] = 0.0;
+      if (!okp[k]) continue;
+      const int s = colk[k];
+      const double E = Ev[k];
+      const double Es1 = h1[k] ? (k + 1 < CPT ? Ev[k + 1] : e1last) : NINF;
+      const double Es2 = c2p[k] != ZERO ? Up[c2p[k]] : NINF;
+      const double denom = rowsum - Upath[k];
+      const double Ebar = denom > 0.0 ? log2(denom) + rmax + (double)P.mt[s] : NINF;
+      ID[k] = denom > 0.0 ? 1.0 / denom : 0.0;
+      const double pS = P.log_pS[P.statewise ? s : 0], pD = P.log_pD[P.statewise ? s : 0];
+      const double pL = P.log_pL[P.statewise ? s : 0];
+      const double t0 = pS + Es1 + Es2, t1 = pD + 2.0 * E, t2 = E + Ebar, t3 = pL;
+      const double m = fmax(fmax(t0, t1), fmax(t2, t3));
+      const double ms = m == NINF ? 0.0 : m;
+      const double En = log2(exp2(t0 - ms) + exp2(t1 - ms) + exp2(t2 - ms) + exp2(t3 - ms)) + m;
+      auto wgt = [&](double t) {
+        double w = exp2(t - En);
+        return (w == w) ? w : 0.0;  // NaN (both -inf) -> 0
+      };
+      W0[k] = wgt(t0);
+      W1[k] = wgt(t1);
+      W2[k] = wgt(t2);
+      W3[k] = wgt(t3);
+    }
+  }
+
+  // E-step VJP (pristine e_step.py:164-241) at the own positions, one barrier:
+  //   q_j = g W_j, wbar = q2 + gebar, tot = sum wbar ID,
+  //   gE = 2 q1 + q2 + (parent's q0 + gs1 if child1, else q0 + gs2) + R (tot - subtree(wbar ID)).
+  // gs1 / gs2 / gebar are column-indexed (may be null); pv = R (tot - subtree).
+  auto vjp = [&](const double (&g)[CPT], const double* gs1, const double* gs2, const double* gebar,
+                 double (&gE)[CPT], double (&wbar)[CPT], double (&pv)[CPT]) {
+    double xo[CPT], uo[CPT], sc[CPT], ta = 0.0;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int s = colk[k];
+      const double q0 = g[k] * W0[k];
+      xo[k] = q0 + ((gs1 && okp[k]) ? gs1[s] : 0.0);
+      uo[k] = q0 + ((gs2 && okp[k]) ? gs2[s] : 0.0);
+      wbar[k] = g[k] * W2[k] + ((gebar && okp[k]) ? gebar[s] : 0.0);
+      ta += wbar[k] * ID[k];
+      sc[k] = ta;
+    }
+    const double wa = wave_scan_incl_f64(ta);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) sc[k] += wa - ta;
+    lds_store_own_f64<CPT>(Xp, xo);
+    lds_store_own_f64<CPT>(Up, uo);
+    lds_store_own_f64<CPT>(Lv, sc);
+    if (lane == 63) wV[wv] = wa;
+    __syncthreads();
+    double par[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) par[k] = pfl[k] ? Xp[ppos[k]] : Up[ppos[k]];  // root: padding 0
+    double sub[CPT];
+    const double tot = subtree_finish(sc, sub);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const double q1 = g[k] * W1[k], q2 = g[k] * W2[k];
+      double acc = 2.0 * q1 + q2;
+      acc += par[k];
+      const double p = R[k] * (tot - sub[k]);
+      gE[k] = acc + p;
+      pv[k] = p;
+    }
+  };
+  // y = x - J^T x
+  auto ag = [&](const double (&xv)[CPT], double (&y)[CPT]) {
+    double gE[CPT], wb[CPT], pv[CPT];
+    vjp(xv, nullptr, nullptr, nullptr, gE, wb, pv);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) y[k] = xv[k] - gE[k];
+  };
+
+  const double* acc = P.acc;
+  const double* a_pD = acc + 0 * (size_t)S;
+  const double* a_pS = acc + 1 * (size_t)S;
+  const double* a_E = acc + 2 * (size_t)S;
+  const double* a_Ebar = acc + 3 * (size_t)S;
+  const double* a_Es1 = acc + 4 * (size_t)S;
+  const double* a_Es2 = acc + 5 * (size_t)S;
+  const double* a_mt = acc + 6 * (size_t)S;
+  const double* a_col = acc + 7 * (size_t)S;
+
+  // ---- q_E = grad_E + d/dE [n_fam log2(norm) + <E_s1,gEs1> + <E_s2,gEs2> + <Ebar,gEbar>]
+  double qE[CPT];
+  {
+    double le = 0.0, r0, r1;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k)
+      if (okp[k]) le += exp2(Ev[k]);
+    sum2(le, 0.0, r0, r1);
+    const double mean = r0 / (double)S;
+    const double norm = 1.0 - mean;
+    const double scale = (P.n_items_rows == P.n_fam) ? 1.0 : (double)P.n_fam;
+    double zero[CPT], gE[CPT], wb[CPT], pv[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) zero[k] = 0.0;
+    vjp(zero, a_Es1, a_Es2, a_Ebar, gE, wb, pv);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const double dd = (norm >= TINY) ? -scale * exp2(Ev[k]) / ((double)S * norm) : 0.0;
+      qE[k] = okp[k] ? a_E[colk[k]] + gE[k] + dd : 0.0;
+    }
+  }
+
+  // ---- BiCGSTAB on (I - J^T) w = q_E (_implicit_grad.py:28-94, same stopping rules).
+  // A x with x = 0 is exactly 0, so r = q_E.
+  double x[CPT], r[CPT], xs[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    x[k] = 0.0;
+    r[k] = qE[k];
+  }
+  const double qq = dot(qE, qE);
+  const double bnorm = fmax(sqrt(qq), 1.0);
+  double rel = sqrt(qq) / bnorm;
+  int kit = 0;
+  int done = rel <= P.tol;
+  int failed = 0;
+  bool use_xs = false;
+  if (!done) {
+    double rh[CPT], vv[CPT], pp[CPT], sv[CPT], tv[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      rh[k] = r[k];
+      vv[k] = 0.0;
+      pp[k] = 0.0;
+    }
+    double rho_old = 1.0, alpha = 1.0, omega = 1.0, rho_next = 0.0;
+    for (kit = 1; kit <= P.max_iter; ++kit) {
+      const double rho = kit == 1 ? dot(rh, r) : rho_next;
+      if (fabs(rho) <= P.breakdown) break;
+      const double beta = (rho / rho_old) * (alpha / omega);
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) pp[k] = r[k] + beta * (pp[k] - omega * vv[k]);
+      ag(pp, vv);
+      const double den = dot(rh, vv);
+      if (fabs(den) <= P.breakdown) break;
+      alpha = rho / den;
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) sv[k] = r[k] - alpha * vv[k];
+      if (sqrt(dot(sv, sv)) / bnorm <= P.tol) {
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) xs[k] = x[k] + alpha * pp[k];
+        use_xs = true;
+        done = 1;
+        break;
+      }
+      ag(sv, tv);
+      double tt, ts;
+      {
+        double lt = 0.0, ls = 0.0;
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) {
+          lt += tv[k] * tv[k];
+          ls += tv[k] * sv[k];
+        }
+        sum2(lt, ls, tt, ts);
+      }
+      if (fabs(tt) <= P.breakdown) break;
+      omega = ts / tt;
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        x[k] = x[k] + alpha * pp[k] + omega * sv[k];
+        r[k] = sv[k] - omega * tv[k];
+      }
+      double rr;
+      {
+        double lr = 0.0, lh = 0.0;
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) {
+          lr += r[k] * r[k];
+          lh += rh[k] * r[k];
+        }
+        sum2(lr, lh, rr, rho_next);
+      }
+      rel = sqrt(rr) / bnorm;
+      if (rel <= P.tol) {
+        done = 1;
+        break;
+      }
+      if (fabs(omega) <= P.breakdown) break;
+      rho_old = rho;
+    }
+    if (!done) failed = 1;
+    if (kit > P.max_iter) kit = P.max_iter;
+  }
+  if (tid == 0) {
+    P.status[0] = kit;
+    P.status[1] = failed;
+  }
+
+  // ---- parameter cotangents: param_loss + E-step(E*, params) with (wE, g_Ebar)
+  double G_pS[CPT], G_pD[CPT], G_pL[CPT], G_mt[CPT], G_col[CPT];
+  {
+    double ws[CPT], gE[CPT], wb[CPT], pv[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) ws[k] = use_xs ? xs[k] : x[k];
+    vjp(ws, nullptr, nullptr, a_Ebar, gE, wb, pv);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int s = colk[k];
+      G_pS[k] = okp[k] ? ws[k] * W0[k] + a_pS[s] : 0.0;
+      G_pD[k] = okp[k] ? ws[k] * W1[k] + a_pD[s] : 0.0;
+      G_pL[k] = okp[k] ? ws[k] * W3[k] : 0.0;
+      G_mt[k] = okp[k] ? wb[k] + a_mt[s] : 0.0;
+      G_col[k] = okp[k] ? pv[k] + a_col[s] : 0.0;
+    }
+  }
+
+  // theta VJP through log2-softmax of [0, theta] (extract_parameters.py:71-74)
+  if (P.statewise) {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      if (!okp[k]) continue;
+      const int s = colk[k];
+      const float* th = P.theta + 3 * (size_t)s;
+      const double l0 = 0.0, l1 = th[0], l2 = th[1], l3 = th[2];
+      const double mx = fmax(fmax(l0, l1), fmax(l2, l3));
+      const double z = exp2(l0 - mx) + exp2(l1 - mx) + exp2(l2 - mx) + exp2(l3 - mx);
+      const double gs = G_pS[k] + G_pD[k] + G_pL[k] + G_mt[k];
+      P.grad_theta[3 * (size_t)s + 0] = (float)(G_pD[k] - exp2(l1 - mx) / z * gs);
+      P.grad_theta[3 * (size_t)s + 1] = (float)(G_pL[k] - exp2(l2 - mx) / z * gs);
+      P.grad_theta[3 * (size_t)s + 2] = (float)(G_mt[k] - exp2(l3 - mx) / z * gs);
+    }
+  } else {
+    double a = 0.0, b = 0.0, d = 0.0, e = 0.0;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      a += G_pS[k];
+      b += G_pD[k];
+      d += G_pL[k];
+      e += G_mt[k];
+    }
+    sum2(a, b, a, b);
+    sum2(d, e, d, e);
+    if (tid == 0) {
+      const double l0 = 0.0, l1 = P.theta[0], l2 = P.theta[1], l3 = P.theta[2];
+      const double mx = fmax(fmax(l0, l1), fmax(l2, l3));
+      const double z = exp2(l0 - mx) + exp2(l1 - mx) + exp2(l2 - mx) + exp2(l3 - mx);
+      const double gs = a + b + d + e;
+      P.grad_theta[0] = (float)(b - exp2(l1 - mx) / z * gs);
+      P.grad_theta[1] = (float)(d - exp2(l2 - mx) / z * gs);
+      P.grad_theta[2] = (float)(e - exp2(l3 - mx) / z * gs);
+    }
+  }
+
+  // column VJP: col_log_probs = log_softmax(w)/ln2, col_norm = -log2(1 - pathsum(2^cl))
+  double lmx = NINF;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k)
+    if (okp[k]) lmx = fmax(lmx, (double)P.col_weights[colk[k]]);
+  const double wmax = block_max<NT>(lmx, mred);
+  double lz = 0.0;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k)
+    if (okp[k]) lz += exp((double)P.col_weights[colk[k]] - wmax);
+  double zsum, unused;
+  sum2(lz, 0.0, zsum, unused);
+  const double logz = wmax + log(zsum);
+  double pc[CPT], pcs[CPT], ptot;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) pc[k] = okp[k] ? exp2(((double)P.col_weights[colk[k]] - logz) / LN2) : 0.0;
+  path_sums(pc, pcs, ptot);
+  double sc[CPT], ta = 0.0;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const double valid = 1.0 - pcs[k];
+    const double xv = (okp[k] && valid > 0.0 && valid >= TINY) ? G_mt[k] / valid : 0.0;
+    ta += xv;
+    sc[k] = ta;
+  }
+  const double wa = wave_scan_incl_f64(ta);
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) sc[k] += wa - ta;
+  lds_store_own_f64<CPT>(Lv, sc);
+  if (lane == 63) wV[wv] = wa;
+  __syncthreads();
+  double sub[CPT];
+  subtree_finish(sc, sub);
+  double g[CPT], lg = 0.0;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    g[k] = okp[k] ? G_col[k] + pc[k] * sub[k] : 0.0;
+    lg += g[k];
+  }
+  double gsum;
+  sum2(lg, 0.0, gsum, unused);
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    if (!okp[k]) continue;
+    const int s = colk[k];
+    const double qn = exp((double)P.col_weights[s] - logz);
+    P.grad_col[s] = (float)((g[k] - qn * gsum) / LN2);
+  }
+}
+
 void launch_epilogue(const EpiParams& P, hipStream_t st) {
-  if (P.S <= 2048)
+  if (P.S <= 2048 && P.pd.post)
+    hipLaunchKernelGGL((epilogue_pre_kernel<1024, 2>), dim3(1), dim3(1024), 0, st, P);
+  else if (P.S <= 2048)
     hipLaunchKernelGGL(epilogue_kernel<2048>, dim3(1), dim3(XNT), 0, st, P);
   else
     hipLaunchKernelGGL(epilogue_kernel<8192>, dim3(1), dim3(XNT), 0, st, P);

@@ -258,18 +258,6 @@ __global__ __launch_bounds__(ENT) void estep_fixed_point_kernel(EStepParams P) {
 // flags of an update are published with the next iteration's first barrier,
 // whose path sums are then also the outputs' (same rule as the kernel above).
 
-template <int CPT>
-__device__ __forceinline__ void lds_store_own_f64(double* lds, const double (&v)[CPT]) {
-  double* p = lds + threadIdx.x * CPT;
-  if constexpr (CPT % 2 == 0) {
-#pragma unroll
-    for (int k = 0; k < CPT; k += 2) *reinterpret_cast<double2*>(p + k) = make_double2(v[k], v[k + 1]);
-  } else {
-#pragma unroll
-    for (int k = 0; k < CPT; ++k) p[k] = v[k];
-  }
-}
-
 template <int NT, int CPT>
 __global__ __launch_bounds__(NT) void estep_pre_kernel(EStepParams P) {
   constexpr int MAXS = NT * CPT;

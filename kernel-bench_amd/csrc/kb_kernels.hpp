@@ -138,6 +138,7 @@ struct BwdParams {
 struct EpiParams {
   TreeDev tr;
   TreeScanDev ts;
+  PreDev pd;                  // preorder tables (register-resident kernel)
   int S;
   int n_tlevels;
   const int* tlevel_ptr;

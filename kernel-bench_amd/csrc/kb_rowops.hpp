@@ -114,6 +114,19 @@ __device__ __forceinline__ double shfl_f64(double x, int src) {
   return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
 }
 
+// Own positions (contiguous ownership) of a float64 LDS row.
+template <int CPT>
+__device__ __forceinline__ void lds_store_own_f64(double* lds, const double (&v)[CPT]) {
+  double* p = lds + threadIdx.x * CPT;
+  if constexpr (CPT % 2 == 0) {
+#pragma unroll
+    for (int k = 0; k < CPT; k += 2) *reinterpret_cast<double2*>(p + k) = make_double2(v[k], v[k + 1]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) p[k] = v[k];
+  }
+}
+
 // ---- block reductions / scans (one barrier each) -----------------------------
 // `wtot` is LDS scratch of NW floats (2*NW for the paired scan).  It is read
 // by every thread after the barrier, so the next writer must be separated from

@@ -118,3 +118,39 @@ def test_backward_reuses_forward_split_terms_only_when_valid():
     for a, b, c in zip(g_reuse, g_recompute, g_old):
         assert kbtest.norm_rel(a.cpu().numpy(), b.cpu().numpy()) <= 1e-6
         assert kbtest.norm_rel(a.cpu().numpy(), c.cpu().numpy()) <= 1e-6
+
+
+@pytest.mark.parametrize("name,statewise", [("1", True), ("2", None)])
+def test_fused_weighted_columns_match_oracle(name, statewise):
+    """Non-uniform column weights: the weighted row kernels and the column branches of the
+    E-step and the epilogue against the oracle on the same (float32-rounded) weights."""
+    import kbench_oracle as O
+    from kbench.fused import FusedSolver, problem_to_captured
+    from kbench.runtime import make_static
+
+    print(f"[fused-weighted] config={name} statewise={statewise}", flush=True)
+    p = kbtest.problem(name, statewise)
+    cap = problem_to_captured(p)
+    static = make_static(cap, "cuda")
+    solver = FusedSolver(static, static.solver_options)
+    theta = cap["inputs"]["theta"].cuda()
+    rng = np.random.default_rng(11)
+    cw32 = rng.normal(0.0, 0.5, size=int(cap["inputs"]["col_weights"].numel())).astype(np.float32)
+    cw = torch.from_numpy(cw32).cuda()
+    loss, saved = solver.run_forward(theta, cw)
+    gt, gc = solver.run_backward(theta, cw, saved)
+    torch.cuda.synchronize()
+
+    prob = O.Problem.from_dict(p)
+    th64 = np.asarray(p["inputs"]["theta"], dtype=np.float32).astype(np.float64)
+    cw64 = cw32.astype(np.float64)
+    ref_loss, ref = O.forward(prob, th64, cw64)
+    ref_gt, ref_gc, _info, _extra = O.backward(prob, th64, cw64, ref, collect=True)
+    rel = abs(float(loss) - ref_loss) / abs(ref_loss)
+    ok, ma, mr = kbtest.compare_inf_safe(saved["pi_wave"].cpu().numpy(), ref["pi_wave"])
+    rt = kbtest.norm_rel(gt.cpu().numpy(), ref_gt)
+    rc = kbtest.norm_rel(gc.cpu().numpy(), ref_gc)
+    print(f"  loss rel={rel:.3e} pi ok={ok} max_abs={ma:.3e} grad_theta={rt:.3e} grad_col={rc:.3e}")
+    assert rel <= 1e-5
+    assert ok and (ma <= 2e-4 or mr <= 1e-5)
+    assert rt <= 1e-4 and rc <= 1e-4

@@ -697,8 +697,11 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   int dev = 0, n_cu = 0;
   KB_HIP(hipGetDevice(&dev));
   KB_HIP(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
+  // launch shape: 0 = 512 x 4 on levels with at least one row per workgroup
+  // slot and 1024 x 2 (more, narrower threads: shorter per-row latency) on the
+  // smaller levels; KB_BWD_VARIANT=0 / 2 forces one shape everywhere
   const char* vv = getenv("KB_BWD_VARIANT");
-  const int variant = (vv && vv[0] == '2') ? 2 : 0;
+  const int variant = (vv && vv[0] == '2') ? 2 : (vv && vv[0] == '0') ? 0 : 1;
   const int nb_max = std::max(1, n_cu * kb::bwd_blocks_per_cu(S, use_col, variant));
   p->b_variant = variant;
   if (p->b_contrib && p->b_nb_max == nb_max) return 0;
@@ -845,6 +848,7 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
     const int n = d == 0 ? p->n_cls0 : p->level_ptr[d + 1] - p->level_ptr[d];
     B.class_mode = d == 0 ? 1 : 0;
     if (d == 0) kb::launch_bwd_level0_prep(B, p->level_ptr[1], p->n_cls0, st);
+    B.variant = p->b_variant == 1 ? (n < p->b_nb_max ? 2 : 0) : p->b_variant;
     kb::launch_bwd_wave(B, p->level_ptr[d], n, std::min(n, p->b_nb_max), 0, st);
     if (p->prof) KB_HIP(hipEventRecord(p->ev_bwd[2 * d + 1], st));
   }

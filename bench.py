@@ -259,8 +259,10 @@ def main():
         # HBM bytes per dispatch from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this
         # command, scaled by a copy kernel of known size (kbench.rocprof_summary)
         rec = json.loads(TRAFFIC_FILE.read_text()).get("kernels", {})
+        # (a kernel launched in several shapes: dispatch-weighted mean over them)
         hits = [v for k, v in rec.items() if symbol[dom] in k]
-        traffic = round(float(hits[0]["traffic"]), 1) if hits else None
+        n = sum(float(v["dispatches"]) for v in hits)
+        traffic = round(sum(float(v["traffic"]) * float(v["dispatches"]) for v in hits) / n, 1) if n else None
     roofline = {
         "bound": "hbm",
         "kernel": dom,

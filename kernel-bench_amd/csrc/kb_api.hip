@@ -652,6 +652,12 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
   {
     const char* w = getenv("KB_FWD_WIDE");
     F.wide = (w && (w[0] == '1' || w[0] == '2')) ? w[0] - '0' : 0;
+    // 512 x 4 keeps three rows per CU resident, 1024 x 2 two rows with a
+    // shorter per-row latency: the wider shape wins below ~6 rows per CU
+    int dev = 0, n_cu = 0;
+    KB_HIP(hipGetDevice(&dev));
+    KB_HIP(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
+    F.narrow_below = 6 * n_cu;
   }
   F.colw = p->c_colw;
   F.col = p->c_col;

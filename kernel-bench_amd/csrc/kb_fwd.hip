@@ -562,7 +562,7 @@ void launch_fwd_wave(const FwdParams& P, int first, int W, hipStream_t st) {
   if (P.wide == 1) {  // fewer, wider threads per row (tuning knob)
     KB_FWD_CASE(256, 8, fwd_row_kernel)
   }
-  if (P.wide == 2) {  // more, narrower threads per row (tuning knob)
+  if (P.wide == 2 || (P.wide == 0 && W < P.narrow_below)) {  // more, narrower threads per row
     KB_FWD_CASE(1024, 2, fwd_row_kernel)
   }
   KB_FWD_CASE(64, 2, fwd_row_kernel)

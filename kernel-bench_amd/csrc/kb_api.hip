@@ -703,7 +703,7 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   int dev = 0, n_cu = 0;
   KB_HIP(hipGetDevice(&dev));
   KB_HIP(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
-  // launch shape: 0 = 512 x 4 on levels with at least one row per workgroup
+  // launch shape: 0 = 512 x 4 on levels with at least two rows per workgroup
   // slot and 1024 x 2 (more, narrower threads: shorter per-row latency) on the
   // smaller levels; KB_BWD_VARIANT=0 / 2 forces one shape everywhere
   const char* vv = getenv("KB_BWD_VARIANT");
@@ -854,7 +854,7 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
     const int n = d == 0 ? p->n_cls0 : p->level_ptr[d + 1] - p->level_ptr[d];
     B.class_mode = d == 0 ? 1 : 0;
     if (d == 0) kb::launch_bwd_level0_prep(B, p->level_ptr[1], p->n_cls0, st);
-    B.variant = p->b_variant == 1 ? (n < p->b_nb_max ? 2 : 0) : p->b_variant;
+    B.variant = p->b_variant == 1 ? (n < 2 * p->b_nb_max ? 2 : 0) : p->b_variant;
     kb::launch_bwd_wave(B, p->level_ptr[d], n, std::min(n, p->b_nb_max), 0, st);
     if (p->prof) KB_HIP(hipEventRecord(p->ev_bwd[2 * d + 1], st));
   }

@@ -835,8 +835,8 @@ __global__ __launch_bounds__(NT) void epilogue_pre_kernel(EpiParams P) {
 }
 
 void launch_epilogue(const EpiParams& P, hipStream_t st) {
-  if (P.S <= 2048 && P.pd.post)
-    hipLaunchKernelGGL((epilogue_pre_kernel<1024, 2>), dim3(1), dim3(1024), 0, st, P);
+  if (P.S <= 2048 && P.pd.post)  // 512 x 4: fewer wavefronts, less per-wavefront scan overhead
+    hipLaunchKernelGGL((epilogue_pre_kernel<512, 4>), dim3(1), dim3(512), 0, st, P);
   else if (P.S <= 2048)
     hipLaunchKernelGGL(epilogue_kernel<2048>, dim3(1), dim3(XNT), 0, st, P);
   else

@@ -473,9 +473,9 @@ __global__ __launch_bounds__(NT) void estep_pre_kernel(EStepParams P) {
         const double na = rowsum - ps[k];
         const double eb = na > 0.0 ? lin_mt[k] * na : 0.0;
         const double en = lin_pS[k] * e1[k] * e2[k] + lin_pD[k] * e[k] * e[k] + e[k] * eb + lin_pL[k];
-        // |log2(en / e)| < tol without a log: en / e inside (2^-tol, 2^tol)
-        const double ratio = en / e[k];
-        if (!(ratio < ratio_hi && ratio > ratio_lo)) ok_local = false;
+        // |log2(en / e)| < tol without a log or a division (e > 0):
+        // en / e inside (2^-tol, 2^tol)
+        if (!(en < e[k] * ratio_hi && en > e[k] * ratio_lo)) ok_local = false;
         e[k] = en;
       }
     }

@@ -83,6 +83,10 @@ struct kb_plan {
   int* d_copy_dst = nullptr;
   int* d_copy_src = nullptr;
   int n_cls0 = 0;                      // classes of level-0 rows
+  int n_chunks0 = 0;                   // level-0 classes cut into chunks of <= KB_CHUNK0 members
+  int* d_ck_ptr = nullptr;
+  int* d_cls_ck_ptr = nullptr;
+  unsigned char* b_ck_any = nullptr;
   int* d_rep_of = nullptr;             // [C] representative of each row
   int* d_m_side_ptr = nullptr;         // level-0 members (cls_rows order): staging sides
   int* d_m_side = nullptr;
@@ -464,6 +468,15 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
     }
   }
   p->n_cls0 = (int)cls_ptr.size() - 1;
+  // chunks of at most KB_CHUNK0 members of a level-0 class (nearly equal sizes)
+  std::vector<int> ck_ptr{0}, cls_ck_ptr{0};
+  for (int c = 0; c < p->n_cls0; ++c) {
+    const int b = cls_ptr[c], n = cls_ptr[c + 1] - b;
+    const int pieces = (n + kb::KB_CHUNK0 - 1) / kb::KB_CHUNK0;
+    for (int k = 1; k <= pieces; ++k) ck_ptr.push_back(b + (int)((int64_t)n * k / pieces));
+    cls_ck_ptr.push_back((int)ck_ptr.size() - 1);
+  }
+  p->n_chunks0 = (int)ck_ptr.size() - 1;
 
   int rc = 0;
   rc |= upload(&p->d_parent, parent);
@@ -495,6 +508,8 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
   rc |= upload(&p->d_copy_dst, copy_dst);
   rc |= upload(&p->d_copy_src, copy_src);
   rc |= upload(&p->d_cls_ptr, cls_ptr);
+  rc |= upload(&p->d_ck_ptr, ck_ptr);
+  rc |= upload(&p->d_cls_ck_ptr, cls_ck_ptr);
   rc |= upload(&p->d_cls_rows, cls_rows);
   {
     std::vector<int> rep_of(C);
@@ -563,7 +578,7 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
                     (void*)p->loss_terms, (void*)p->loss64, (void*)p->d_root_index,
                     (void*)p->d_sched_rows, (void*)p->d_row_kind, (void*)p->d_pre, (void*)p->d_pcol,
                     (void*)p->d_fsched, (void*)p->d_fsplit_l, (void*)p->d_fsplit_r, (void*)p->d_copy_dst,
-                    (void*)p->d_copy_src, (void*)p->d_cls_ptr, (void*)p->d_cls_rows, (void*)p->d_rep_of, (void*)p->d_m_side_ptr, (void*)p->d_m_side, (void*)p->d_m_root,
+                    (void*)p->d_copy_src, (void*)p->d_cls_ptr, (void*)p->d_cls_rows, (void*)p->d_ck_ptr, (void*)p->d_cls_ck_ptr, (void*)p->d_rep_of, (void*)p->d_m_side_ptr, (void*)p->d_m_side, (void*)p->d_m_root,
                     (void*)p->d_dts,
                     (void*)p->d_c1pos, (void*)p->d_c2pos, (void*)p->d_ppos, (void*)p->d_pflag, (void*)p->d_endpos,
                     (void*)p->d_tin, (void*)p->d_euler, (void*)p->d_post, (void*)p->d_euler_col, (void*)p->d_tin_col, (void*)p->c_Ebar, (void*)p->c_E, (void*)p->c_mt,
@@ -736,6 +751,7 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   rc |= alloc(&p->b_rhsc, (size_t)std::max(1, p->n_cls0) * S);
   rc |= alloc(&p->b_m_mask, (size_t)std::max(1, C > 0 ? p->level_ptr[1] : 1));
   rc |= alloc(&p->b_cls_active, (size_t)std::max(1, p->n_cls0));
+  rc |= alloc(&p->b_ck_any, (size_t)std::max(1, p->n_chunks0));
   rc |= alloc(&p->b_contrib, (size_t)std::max(1, p->b_n_partials) * 8 * S);
   rc |= alloc(&p->b_partial, (size_t)kb::reduce_chunks(std::max(1, p->b_n_partials)) * 8 * S);
   rc |= alloc(&p->b_acc, (size_t)8 * S);
@@ -753,7 +769,7 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   rc |= alloc(&p->b_acc_pre, (size_t)8 * S);
   for (void* ptr : {(void*)p->b_Ebar, (void*)p->b_E, (void*)p->b_mt, (void*)p->b_col, (void*)p->b_acc_pre,
                     (void*)p->b_staging, (void*)p->b_split_on, (void*)p->b_mask, (void*)p->b_contrib,
-                    (void*)p->b_rhs0, (void*)p->b_rhsc, (void*)p->b_cls_active, (void*)p->b_m_mask,
+                    (void*)p->b_rhs0, (void*)p->b_rhsc, (void*)p->b_cls_active, (void*)p->b_ck_any, (void*)p->b_m_mask,
                     (void*)p->b_partial, (void*)p->b_acc, (void*)p->b_work, (void*)p->b_status, (void*)p->b_DL,
                     (void*)p->b_SL1, (void*)p->b_SL2, (void*)p->b_pS, (void*)p->b_pD})
     p->owned.push_back(ptr);
@@ -834,6 +850,10 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   B.row_kind = p->d_row_kind;
   B.variant = p->b_variant;
   B.rhs0 = p->b_rhs0;
+  B.n_chunks0 = p->n_chunks0;
+  B.ck_ptr = p->d_ck_ptr;
+  B.cls_ck_ptr = p->d_cls_ck_ptr;
+  B.ck_any = p->b_ck_any;
   B.rhsc = p->b_rhsc;
   B.m_side_ptr = p->d_m_side_ptr;
   B.m_side = p->d_m_side;

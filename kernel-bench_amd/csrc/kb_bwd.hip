@@ -654,9 +654,108 @@ __global__ __launch_bounds__(256) void bwd_classsum0_kernel(BwdParams P) {
   if (blockIdx.y == 0 && threadIdx.x == 0) P.cls_active[c] = any ? 1 : 0;
 }
 
+// Level-0 adjoints for trees of up to 256 * G0_E nodes, one workgroup per
+// chunk of a class's members (at most KB_CHUNK0): each member's adjoint row
+// stays in registers (position e*256 + tid), gets its active mask, and the
+// active members are summed in member order into the chunk's partial row
+// (kept in the rhs0 buffer).  bwd_chunksum0_kernel then adds a class's chunk
+// rows in chunk order.  Same per-member arithmetic as bwd_gather0_kernel,
+// without the [members, S] round trip through HBM.
+__global__ __launch_bounds__(256) void bwd_chunk0_kernel(BwdParams P) {
+  __shared__ float red[4];
+  const PreDev& T = P.pre;
+  const int S = P.S;
+  const int k = blockIdx.x;
+  const int mb = P.ck_ptr[k], me = P.ck_ptr[k + 1];
+  float acc[G0_E];
+#pragma unroll
+  for (int e = 0; e < G0_E; ++e) acc[e] = 0.0f;
+  int any = 0;
+  for (int mi = mb; mi < me; ++mi) {
+    const int row = P.cls_rows[mi];
+    float r[G0_E];
+#pragma unroll
+    for (int e = 0; e < G0_E; ++e) r[e] = 0.0f;
+    if (P.m_root[mi] >= 0) {
+      // root seed: -2^(Pi - logsumexp2(Pi)) (logspace.py:11-16, _implicit_grad.py:21-25)
+      const float* pr = P.pi + (size_t)row * S;
+      float lm = KB_NEG_INF;
+      for (int j = threadIdx.x; j < S; j += 256) lm = fmaxf(lm, pr[j]);
+      const float rmax = block_max<256>(lm, red);
+      const float rms = fsafe(rmax);
+      float ls = 0.0f;
+      for (int j = threadIdx.x; j < S; j += 256) ls += exp2f(pr[j] - rms);
+      const float tot = block_sum<256>(ls, red);
+      const float lses = fsafe((tot > 0.0f ? log2f(tot) : KB_NEG_INF) + rmax);
+#pragma unroll
+      for (int e = 0; e < G0_E; ++e) {
+        const int i = e * 256 + threadIdx.x;
+        if (i < S) {
+          const float x = pr[T.col[i]];
+          r[e] = x == KB_NEG_INF ? 0.0f : -exp2f(x - lses);
+        }
+      }
+    } else {
+      const int sb = P.m_side_ptr[mi], se = P.m_side_ptr[mi + 1];
+      for (int j = sb; j < se; ++j) {
+        const int side = P.m_side[j];
+        if (!P.split_on[side >> 1]) continue;  // uniform across the workgroup
+        const float* st = P.staging + (size_t)side * S;
+#pragma unroll
+        for (int e = 0; e < G0_E; ++e) {
+          const int i = e * 256 + threadIdx.x;
+          if (i < S) r[e] += st[i];
+        }
+      }
+    }
+    float am = 0.0f;
+#pragma unroll
+    for (int e = 0; e < G0_E; ++e)
+      if (e * 256 + (int)threadIdx.x < S) am = fmaxf(am, fabsf(r[e]));
+    const float amax = block_max<256>(am, red);
+    const bool on = P.use_pruning ? (amax >= P.thr) : (amax > P.thr);
+    if (threadIdx.x == 0) {
+      P.mask[row] = on ? 1 : 0;
+      P.m_mask[mi] = on ? 1 : 0;
+    }
+    if (on) {
+      any = 1;
+#pragma unroll
+      for (int e = 0; e < G0_E; ++e) acc[e] += r[e];
+    }
+  }
+  float* out = P.rhs0 + (size_t)k * S;
+#pragma unroll
+  for (int e = 0; e < G0_E; ++e) {
+    const int i = e * 256 + threadIdx.x;
+    if (i < S) out[i] = acc[e];
+  }
+  if (threadIdx.x == 0) P.ck_any[k] = any ? 1 : 0;
+}
+
+__global__ __launch_bounds__(256) void bwd_chunksum0_kernel(BwdParams P) {
+  const int c = blockIdx.x;
+  const int S = P.S;
+  const int i = blockIdx.y * 256 + threadIdx.x;
+  const int kb = P.cls_ck_ptr[c], ke = P.cls_ck_ptr[c + 1];
+  float acc = 0.0f;
+  int any = 0;
+  for (int k = kb; k < ke; ++k) {
+    any |= P.ck_any[k];
+    if (i < S) acc += P.rhs0[(size_t)k * S + i];
+  }
+  if (i < S) P.rhsc[(size_t)c * S + i] = acc;
+  if (blockIdx.y == 0 && threadIdx.x == 0) P.cls_active[c] = any ? 1 : 0;
+}
+
 void launch_bwd_level0_prep(const BwdParams& P, int n_members, int n_cls, hipStream_t st) {
   if (n_members <= 0) return;
   const int nblk = (P.S + 255) / 256;
+  if (P.S <= 256 * G0_E && P.n_chunks0 > 0) {
+    hipLaunchKernelGGL(bwd_chunk0_kernel, dim3(P.n_chunks0), dim3(256), 0, st, P);
+    hipLaunchKernelGGL(bwd_chunksum0_kernel, dim3(n_cls, nblk), dim3(256), 0, st, P);
+    return;
+  }
   hipLaunchKernelGGL(bwd_gather0_kernel, dim3(n_members), dim3(256), 0, st, P);
   hipLaunchKernelGGL(bwd_classsum0_kernel, dim3(n_cls, nblk), dim3(256), 0, st, P);
 }

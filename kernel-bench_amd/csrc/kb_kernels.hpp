@@ -134,7 +134,14 @@ struct BwdParams {
   const int* rep_of;          // [C] row -> row whose stored split term it shares
   const int* cls_ptr;         // [n_classes + 1]
   const int* cls_rows;        // member rows, representative first
+  // level-0 classes cut into chunks of at most KB_CHUNK0 members
+  int n_chunks0;
+  const int* ck_ptr;          // [chunks + 1] member (cls_rows) ranges
+  const int* cls_ck_ptr;      // [classes + 1] chunk ranges
+  unsigned char* ck_any;      // [chunks] any member of the chunk active
 };
+
+constexpr int KB_CHUNK0 = 8;
 
 struct EpiParams {
   TreeDev tr;

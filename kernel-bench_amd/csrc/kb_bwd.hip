@@ -49,6 +49,10 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   const int tid = threadIdx.x;
   constexpr int ZERO = MAXS;
 
+  // The narrow 1024 x 2 shape runs the levels with about one row per
+  // workgroup: it fetches rows when needed instead of one row ahead, and loads
+  // the Euler tables per row instead of holding them (128 VGPRs at 16 waves).
+  constexpr bool AHEAD = !(NT == 1024 && CPT == 2);
   OwnTablesC<NT, CPT> O;
   O.load(T);
   if (tid < 64) {
@@ -129,7 +133,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       nPb[j] = spre[j] >= 0 ? P.pibar[b2 + s] : 0.0f;
     }
   };
-  if ((int)blockIdx.x < n_rows) fetch_rows(blockIdx.x);
+  if (AHEAD && (int)blockIdx.x < n_rows) fetch_rows(blockIdx.x);
 
   for (int rr = blockIdx.x; rr < n_rows; rr += gridDim.x) {
   __syncthreads();  // LDS of the previous row is no longer read
@@ -172,13 +176,14 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     }
   }
   float piv[CPT], pbv[CPT];
+  if (!AHEAD) fetch_rows(rr);
 #pragma unroll
   for (int j = 0; j < CPT; ++j)
     if (spre[j] >= 0) {
       R0[spre[j]] = nPi[j];
       R1[spre[j]] = nPb[j];
     }
-  if (rr + (int)gridDim.x < n_rows) fetch_rows(rr + gridDim.x);
+  if (AHEAD && rr + (int)gridDim.x < n_rows) fetch_rows(rr + gridDim.x);
   __syncthreads();
   lds_load_own<CPT>(R0, piv);
   lds_load_own<CPT>(R1, pbv);
@@ -285,7 +290,13 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   lds_store_own<CPT>(R2, pp);
   const float rowsum = block_sum1<NT>(ls, wA);
   float ps[CPT];
-  path_sum_euler<NT, CPT>(O, R2, Sc, wB, ps);
+  if constexpr (AHEAD) {
+    path_sum_euler<NT, CPT>(O, R2, Sc, wB, ps);
+  } else {
+    OwnTablesC<NT, CPT> Oe;
+    Oe.load(T);
+    path_sum_euler<NT, CPT>(Oe, R2, Sc, wB, ps);
+  }
   const int lpos = leaf_row ? T.pre[P.leaf_state[row]] : -1;
   float q[6][CPT], pcoef[CPT];
 #pragma unroll

@@ -54,16 +54,26 @@ def require_device(t: torch.Tensor, what: str) -> None:
 
 
 def f(t, dtype, device):
-    """t as a contiguous ``dtype`` tensor on ``device`` (None stays None)."""
+    """t as a contiguous ``dtype`` tensor on ``device`` (None stays None).
+
+    Tensors that already qualify are returned as they are without a dispatch
+    (the per-sweep wrappers call this for every constant on every launch).
+    """
     if t is None:
         return None
     if not torch.is_tensor(t):
         t = torch.as_tensor(t)
+    elif t.dtype is dtype and t.device == device and t.is_contiguous():
+        return t
     return t.to(device=device, dtype=dtype).contiguous()
 
 
 def i64(t, device):
-    return None if t is None else t.to(device=device, dtype=torch.long).contiguous()
+    if t is None:
+        return None
+    if t.dtype is torch.long and t.device == device and t.is_contiguous():
+        return t
+    return t.to(device=device, dtype=torch.long).contiguous()
 
 
 # ---------------------------------------------------------------- tree handles
@@ -85,7 +95,8 @@ class _Tree:
 
 
 def _key(*ts):
-    return tuple((int(t.data_ptr()), tuple(t.shape), str(t.device), int(t._version)) for t in ts)
+    # addresses are unique across devices in one process (unified addressing)
+    return tuple((t.data_ptr(), t.shape, t._version) for t in ts)
 
 
 def _create(S: int, parent, c1, c2) -> _Tree:

@@ -665,8 +665,10 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
   F.lin_k2 = p->lin_k2;
   F.pre = p->predev();
   {
+    // KB_FWD_WIDE: 1 = 256 x 8, 2 = 1024 x 2 on every level, 3 = the size-based
+    // shapes without the narrow one (tuning / test knob); default 0
     const char* w = getenv("KB_FWD_WIDE");
-    F.wide = (w && (w[0] == '1' || w[0] == '2')) ? w[0] - '0' : 0;
+    F.wide = (w && (w[0] == '1' || w[0] == '2' || w[0] == '3')) ? w[0] - '0' : 0;
     // 512 x 4 keeps three rows per CU resident, 1024 x 2 two rows with a
     // shorter per-row latency: the wider shape wins below ~6 rows per CU
     int dev = 0, n_cu = 0;

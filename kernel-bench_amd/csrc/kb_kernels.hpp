@@ -54,7 +54,7 @@ struct FwdParams {
   TreeDev tr;
   PreDev pre;
   int S;
-  int wide;                   // 1: 256 x 8, 2: 1024 x 2 threads x positions per row on every level
+  int wide;                   // 1: 256 x 8, 2: 1024 x 2 on every level, 3: no narrow shape
   int narrow_below;           // wide == 0: 1024 x 2 on levels with fewer rows than this
   int n_sweeps;               // pi_iters - 1
   int use_col;

@@ -154,3 +154,53 @@ def test_fused_weighted_columns_match_oracle(name, statewise):
     assert rel <= 1e-5
     assert ok and (ma <= 2e-4 or mr <= 1e-5)
     assert rt <= 1e-4 and rc <= 1e-4
+
+
+def _big_tree_problem(leaves, families, statewise):
+    """Large species tree, few families: the 2048- and 8192-position row kernels at an oracle-sized C."""
+    from kbench import synth
+
+    cfg = synth.ProblemConfig(leaves, families, n_nni=1, family_leaves_median=21.0, family_leaves_sigma=0.6,
+                              family_leaves_max=80, statewise=statewise, seed=17)
+    return synth.build_problem(cfg)
+
+
+@pytest.mark.parametrize("leaves,families,statewise,weighted", [(1024, 6, True, False), (1024, 6, False, True),
+                                                                (4096, 3, False, False), (4096, 3, True, True)])
+@pytest.mark.parametrize("shapes", ["default", "wide"])
+def test_fused_large_trees_match_oracle(leaves, families, statewise, weighted, shapes, monkeypatch):
+    """S = 2047 and 8191: forward rows, loss and gradients against the oracle, with the default launch
+    shapes (narrow shapes on these small levels) and with the wide ones forced."""
+    import kbench_oracle as O
+    from kbench.fused import FusedSolver, problem_to_captured
+    from kbench.runtime import make_static
+
+    if shapes == "wide":
+        monkeypatch.setenv("KB_FWD_WIDE", "3")
+        monkeypatch.setenv("KB_BWD_VARIANT", "0")
+    print(f"[fused-large] leaves={leaves} statewise={statewise} weighted={weighted} shapes={shapes}", flush=True)
+    p = _big_tree_problem(leaves, families, statewise)
+    cap = problem_to_captured(p)
+    static = make_static(cap, "cuda")
+    solver = FusedSolver(static, static.solver_options)
+    theta = cap["inputs"]["theta"].cuda()
+    n = int(cap["inputs"]["col_weights"].numel())
+    cw32 = (np.random.default_rng(5).normal(0.0, 0.5, size=n) if weighted else np.zeros(n)).astype(np.float32)
+    cw = torch.from_numpy(cw32).cuda()
+    loss, saved = solver.run_forward(theta, cw)
+    gt, gc = solver.run_backward(theta, cw, saved)
+    torch.cuda.synchronize()
+
+    prob = O.Problem.from_dict(p)
+    th64 = np.asarray(p["inputs"]["theta"], dtype=np.float32).astype(np.float64)
+    ref_loss, ref = O.forward(prob, th64, cw32.astype(np.float64))
+    ref_gt, ref_gc, _info, _extra = O.backward(prob, th64, cw32.astype(np.float64), ref, collect=True)
+    rel = abs(float(loss) - ref_loss) / abs(ref_loss)
+    ok, ma, mr = kbtest.compare_inf_safe(saved["pi_wave"].cpu().numpy(), ref["pi_wave"])
+    rt = kbtest.norm_rel(gt.cpu().numpy(), ref_gt)
+    rc = kbtest.norm_rel(gc.cpu().numpy(), ref_gc)
+    print(f"  S={prob.S} C={prob.C} loss rel={rel:.3e} pi ok={ok} max_abs={ma:.3e} "
+          f"grad_theta={rt:.3e} grad_col={rc:.3e}")
+    assert rel <= 1e-5
+    assert ok and (ma <= 2e-4 or mr <= 1e-5)
+    assert rt <= 1e-4 and rc <= 1e-4

@@ -1082,6 +1082,16 @@ __global__ __launch_bounds__(256) void rows_sum_stage1(int S, long long n, const
   work[(size_t)blockIdx.y * S + s] = acc;
 }
 
+// One chunk or fewer rows: both stages in one launch (same sums).
+template <typename T>
+__global__ __launch_bounds__(256) void rows_sum_single(int S, long long n, const T* src, T* dst) {
+  const int s = blockIdx.x * 256 + threadIdx.x;
+  if (s >= S) return;
+  double acc = 0.0;
+  for (long long r = 0; r < n; ++r) acc += (double)src[(size_t)r * S + s];
+  dst[s] = (T)((double)dst[s] + acc);
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void rows_sum_stage2(int S, int n_chunks, const double* work, T* dst) {
   const int s = blockIdx.x * 256 + threadIdx.x;
@@ -1452,7 +1462,14 @@ int kb_rows_sum_into(int32_t dtype, int32_t S, int64_t n, const void* src, void*
   if (int rc = dtype_ok(dtype)) return rc;
   const int chunks = (int)((n + kbo::SUM_CHUNK - 1) / kbo::SUM_CHUNK);
   dim3 g1((S + 255) / 256, chunks);
-  if (dtype == KB_F64) {
+  if (chunks == 1) {  // one launch, same sum as the two stages
+    if (dtype == KB_F64)
+      hipLaunchKernelGGL(kbo::rows_sum_single<double>, dim3((S + 255) / 256), dim3(256), 0, st_of(stream), S,
+                         (long long)n, (const double*)src, (double*)dst);
+    else
+      hipLaunchKernelGGL(kbo::rows_sum_single<float>, dim3((S + 255) / 256), dim3(256), 0, st_of(stream), S,
+                         (long long)n, (const float*)src, (float*)dst);
+  } else if (dtype == KB_F64) {
     hipLaunchKernelGGL(kbo::rows_sum_stage1<double>, g1, dim3(256), 0, st_of(stream), S, (long long)n,
                        (const double*)src, work);
     hipLaunchKernelGGL(kbo::rows_sum_stage2<double>, dim3((S + 255) / 256), dim3(256), 0, st_of(stream), S, chunks,

@@ -820,7 +820,6 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   B.thr = (float)io->pruning_threshold;
   B.use_pruning = io->use_pruning;
   B.use_col = io->use_col_weights;
-  B.const_stride = 0;
   B.pre = p->predev();
   B.DL = p->b_DL;
   B.Ebar = p->b_Ebar;
@@ -829,13 +828,11 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   B.SL2 = p->b_SL2;
   B.mt = p->b_mt;
   B.col = p->b_col;
-  B.leaf_logp = p->b_pS;
-  B.pD = kb::RateDev{p->b_pD, 0, 1};
-  B.pS = kb::RateDev{p->b_pS, 0, 1};
+  B.pD = p->b_pD;
+  B.pS = p->b_pS;
   B.pi = io->pi;
   B.pibar = io->pibar;
   B.rowmax = io->pibar_row_max;
-  B.item = p->d_item;
   B.leaf_state = p->d_leaf;
   B.root_index = p->d_root_index;
   B.split_ptr = p->d_split_ptr;

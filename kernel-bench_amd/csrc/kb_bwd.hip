@@ -93,6 +93,24 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       else
         cacc[j][k] = 0.0f;
     }
+  // Per-position constants, one [S] row shared by every row: for rows of up
+  // to 2048 states, seven of them stay in LDS for the whole launch (own
+  // positions, so each thread reads back only what it wrote), and the per-row
+  // coefficient passes read LDS instead of waiting on memory.  mt (and the
+  // column weights) stay in memory: LDS has no room for an eighth row.
+  constexpr bool CK_LDS = MAXS <= 2048;
+  enum { K_DL, K_EBAR, K_E, K_SL1, K_SL2, K_PD, K_PS, K_N };
+  __shared__ float Kc[CK_LDS ? K_N * MAXS : 1];
+  const float* const kg[K_N] = {P.DL, P.Ebar, P.E, P.SL1, P.SL2, P.pD, P.pS};
+  // constant j at own position k (0 at padding positions)
+  auto kc_own = [&](int j, float (&x)[CPT]) {
+    if constexpr (CK_LDS) {
+      lds_load_own<CPT>(Kc + j * MAXS, x);
+    } else {
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) x[k] = okp[k] ? kg[j][own_pos_c<NT, CPT>(k)] : 0.0f;
+    }
+  };
   auto bucket = [&](int j, int k) -> float& {
     if constexpr (BK_LDS)
       return Bk[j * MAXS + own_pos_c<NT, CPT>(k)];
@@ -134,6 +152,15 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     }
   };
   if (AHEAD && (int)blockIdx.x < n_rows) fetch_rows(blockIdx.x);
+  if constexpr (CK_LDS) {
+#pragma unroll
+    for (int j = 0; j < K_N; ++j) {
+      float x[CPT];
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) x[k] = okp[k] ? kg[j][own_pos_c<NT, CPT>(k)] : 0.0f;
+      lds_store_own<CPT>(Kc + j * MAXS, x);
+    }
+  }
 
   for (int rr = blockIdx.x; rr < n_rows; rr += gridDim.x) {
   __syncthreads();  // LDS of the previous row is no longer read
@@ -141,8 +168,6 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   const int me = P.class_mode ? P.cls_ptr[rr + 1] : 1;
   const int row = row_of(rr);
   const int leaf_row = P.row_kind[row];
-  const int item = P.item[row];
-  const size_t cb = (size_t)item * P.const_stride;
   const size_t rb = (size_t)row * S;
   const int sb = P.split_ptr[row], se = P.split_ptr[row + 1];
 
@@ -232,12 +257,14 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     for (int k = 0; k < CPT; ++k)
       if (okp[k]) dts[k] = src[own_pos_c<NT, CPT>(k)];
   } else if (!leaf_row) {
-    float m[CPT], acc[CPT];
+    float m[CPT], acc[CPT], kd[CPT], ks[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       m[k] = KB_NEG_INF;
       acc[k] = 0.0f;
     }
+    kc_own(K_PD, kd);
+    kc_own(K_PS, ks);
     for (int si = sb; si < se; ++si) {
       const size_t l = (size_t)P.split_l[si] * S, r = (size_t)P.split_r[si] * S;
       const float lsp = P.split_lsp[si];
@@ -255,7 +282,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
         if (okp[k]) {
           const bool h1 = O.c1p[k] != ZERO, h2 = O.c2p[k] != ZERO;
           const float pl = R0[i], pr = R1[i];
-          const float d = P.pD.at(item, i), sp = P.pS.at(item, i);
+          const float d = kd[k], sp = ks[k];
           const float l1 = h1 ? R0[O.c1p[k]] : KB_NEG_INF, r1 = h1 ? R1[O.c1p[k]] : KB_NEG_INF;
           const float l2 = h2 ? R0[O.c2p[k]] : KB_NEG_INF, r2 = h2 ? R1[O.c2p[k]] : KB_NEG_INF;
           const float t0 = lsp + d + pl + pr;
@@ -299,6 +326,13 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   }
   const int lpos = leaf_row ? T.pre[P.leaf_state[row]] : -1;
   float q[6][CPT], pcoef[CPT];
+  float kDL[CPT], kEb[CPT], kE[CPT], kS1[CPT], kS2[CPT], kLf[CPT];
+  kc_own(K_DL, kDL);
+  kc_own(K_EBAR, kEb);
+  kc_own(K_E, kE);
+  kc_own(K_SL1, kS1);
+  kc_own(K_SL2, kS2);
+  kc_own(K_PS, kLf);  // the leaf term's log pS
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int i = own_pos_c<NT, CPT>(k);
@@ -309,13 +343,12 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       const float denom = rowsum - ps[k];
       const float inv_denom = denom > 0.0f ? 1.0f / denom : 0.0f;
       const bool h1 = O.c1p[k] != ZERO, h2 = O.c2p[k] != ZERO;
-      const size_t ci = cb + i;
-      const float t0 = P.DL[ci] + piv[k];
-      const float t1 = piv[k] + P.Ebar[ci];
-      const float t2 = pbv[k] + P.E[ci];
-      const float t3 = P.SL1[ci] + (h1 ? R0[O.c1p[k]] : KB_NEG_INF);
-      const float t4 = P.SL2[ci] + (h2 ? R0[O.c2p[k]] : KB_NEG_INF);
-      const float t5 = i == lpos ? P.leaf_logp[ci] : KB_NEG_INF;
+      const float t0 = kDL[k] + piv[k];
+      const float t1 = piv[k] + kEb[k];
+      const float t2 = pbv[k] + kE[k];
+      const float t3 = kS1[k] + (h1 ? R0[O.c1p[k]] : KB_NEG_INF);
+      const float t4 = kS2[k] + (h2 ? R0[O.c2p[k]] : KB_NEG_INF);
+      const float t5 = i == lpos ? kLf[k] : KB_NEG_INF;
       const float m = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, t5));
       const float msf = fsafe(m);
       float e[6] = {exp2f(t0 - msf), exp2f(t1 - msf), exp2f(t2 - msf), exp2f(t3 - msf), exp2f(t4 - msf),
@@ -483,7 +516,9 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     }
     __syncthreads();
     float vd0[CPT], vd1[CPT], vd2[CPT], vd3[CPT], vd4[CPT], udl[CPT], udr[CPT], ppl[CPT], ppr[CPT];
-    float cPl[CPT], cPr[CPT], cBl[CPT], cBr[CPT];
+    float cPl[CPT], cPr[CPT], cBl[CPT], cBr[CPT], kd[CPT], ks[CPT];
+    kc_own(K_PD, kd);
+    kc_own(K_PS, ks);
     lds_load_own<CPT>(R0, cPl);
     lds_load_own<CPT>(R1, cPr);
     lds_load_own<CPT>(R2, cBl);
@@ -497,7 +532,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
         const float pl = cPl[k], pr = cPr[k], bl = cBl[k], br = cBr[k];
         const float l1 = h1 ? R0[O.c1p[k]] : KB_NEG_INF, r1 = h1 ? R1[O.c1p[k]] : KB_NEG_INF;
         const float l2 = h2 ? R0[O.c2p[k]] : KB_NEG_INF, r2 = h2 ? R1[O.c2p[k]] : KB_NEG_INF;
-        const float d = P.pD.at(item, i), sp = P.pS.at(item, i);
+        const float d = kd[k], sp = ks[k];
         const bool pv = piv[k] != KB_NEG_INF;
         const float base = pv ? lsp - piv[k] : 0.0f;
         vd0[k] = pv ? v[k] * exp2f(base + (d + pl + pr)) : 0.0f;
@@ -505,7 +540,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
         vd2[k] = pv ? v[k] * exp2f(base + (pr + bl)) : 0.0f;
         vd3[k] = pv ? v[k] * exp2f(base + (sp + l1 + r2)) : 0.0f;
         vd4[k] = pv ? v[k] * exp2f(base + (sp + r1 + l2)) : 0.0f;
-        const float mts = P.mt[cb + i];
+        const float mts = P.mt[i];
         const float inv_l = bl != KB_NEG_INF ? exp2f(rml + mts - bl) : 0.0f;
         const float inv_r = br != KB_NEG_INF ? exp2f(rmr + mts - br) : 0.0f;
         udl[k] = vd2[k] * inv_l;

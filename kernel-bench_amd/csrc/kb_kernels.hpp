@@ -106,13 +106,12 @@ struct BwdParams {
   float thr;                  // adjoint_pruning_threshold
   int use_pruning;
   int use_col;
-  int const_stride;
+  // per-position constants: one [S] row in preorder, shared by every row
   const float* DL; const float* Ebar; const float* E; const float* SL1; const float* SL2;
   const float* mt; const float* col;
-  const float* leaf_logp;     // [G,S] log pS
-  RateDev pD, pS;
+  const float* pD; const float* pS;  // [S] split-term rates (pS is also the leaf term's log pS)
   const float* pi; const float* pibar; const float* rowmax;
-  const int* item; const int* leaf_state; const int* root_index;
+  const int* leaf_state; const int* root_index;
   const int* split_ptr; const int* split_l; const int* split_r; const float* split_lsp;
   const int* child_ptr; const int* child_in;
   float* staging;             // [2 * n_splits, S]

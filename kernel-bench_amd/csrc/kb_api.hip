@@ -658,7 +658,6 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
   F.S = S;
   F.n_sweeps = io->pi_iters - 1;
   F.use_col = io->use_col_weights;
-  F.const_stride = 0;
   F.lin_a = p->lin_a;
   F.lin_emc = p->lin_emc;
   F.lin_k1 = p->lin_k1;
@@ -684,10 +683,8 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
   F.E = p->c_E;
   F.SL1 = p->c_SL1;
   F.SL2 = p->c_SL2;
-  F.leaf_logp = p->c_pS;
-  F.pD = kb::RateDev{p->c_pD, 0, 1};
-  F.pS = kb::RateDev{p->c_pS, 0, 1};
-  F.item = p->d_item;
+  F.pD = p->c_pD;
+  F.pS = p->c_pS;
   F.leaf_state = p->d_leaf;
   F.split_ptr = p->d_split_ptr;
   F.split_l = p->d_fsplit_l;

@@ -466,7 +466,7 @@ __global__ __launch_bounds__(NT) void epilogue_pre_kernel(EpiParams P) {
     lds_store_own_f64<CPT>(Xw, x);
     if (lane == 63) wP[wv] = wa;
     __syncthreads();
-    const double tp = lane < NW ? wP[lane] : 0.0;
+    const double tp = lds_wave_values<NW>(wP, lane, 0.0);
     double yq[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) yq[k] = Xw[qp[k]];
@@ -485,7 +485,7 @@ __global__ __launch_bounds__(NT) void epilogue_pre_kernel(EpiParams P) {
     lds_store_own_f64<CPT>(Qb, sq);
     if (lane == 63) wQ[wv] = wb;
     __syncthreads();
-    const double tq = lane < NW ? wQ[lane] : 0.0;
+    const double tq = lds_wave_values<NW>(wQ, lane, 0.0);
     const double iq = wave_scan_first_f64<NW>(tq);
     const double eq = iq - tq;
 #pragma unroll
@@ -502,7 +502,7 @@ __global__ __launch_bounds__(NT) void epilogue_pre_kernel(EpiParams P) {
     double le[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) le[k] = Lv[endm1[k]];
-    const double tv = lane < NW ? wV[lane] : 0.0;
+    const double tv = lds_wave_values<NW>(wV, lane, 0.0);
     const double iv = wave_scan_first_f64<NW>(tv);
     const double ev = iv - tv;
     const double tot = lane_value_f64(iv, NW - 1);

@@ -308,7 +308,7 @@ __global__ __launch_bounds__(NT) void estep_pre_kernel(EStepParams P) {
     lds_store_own_f64<CPT>(Xw, x);
     if (lane == 63) wP[wv] = wa;
     __syncthreads();
-    const double tp = lane < NW ? wP[lane] : 0.0;
+    const double tp = lds_wave_values<NW>(wP, lane, 0.0);
     double yq[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) yq[k] = Xw[qp[k]];
@@ -327,7 +327,7 @@ __global__ __launch_bounds__(NT) void estep_pre_kernel(EStepParams P) {
     lds_store_own_f64<CPT>(Qb, sq);
     if (lane == 63) wQ[wv] = wb;
     __syncthreads();
-    const double tq = lane < NW ? wQ[lane] : 0.0;
+    const double tq = lds_wave_values<NW>(wQ, lane, 0.0);
     const double iq = wave_scan_first_f64<NW>(tq);
     const double eq = iq - tq;
 #pragma unroll
@@ -428,10 +428,10 @@ __global__ __launch_bounds__(NT) void estep_pre_kernel(EStepParams P) {
     __syncthreads();
     // phase B: stop test, row sum and preorder offsets, postorder and child
     // gathers, exclusive postorder scan
-    const int fl = lane < NW ? wok[lane] : 1;
+    const int fl = lds_wave_values<NW>(wok, lane, 1);
     const bool all_ok = __ballot(fl == 0) == 0;
     const bool stop = it > 0 && (all_ok || it >= P.max_iter);
-    const double tp = lane < NW ? wP[lane] : 0.0;
+    const double tp = lds_wave_values<NW>(wP, lane, 0.0);
     double yq[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
@@ -457,7 +457,7 @@ __global__ __launch_bounds__(NT) void estep_pre_kernel(EStepParams P) {
     if (lane == 63) wQ[wv] = wb;
     __syncthreads();
     // phase C: path sums, then the update
-    const double tq = lane < NW ? wQ[lane] : 0.0;
+    const double tq = lds_wave_values<NW>(wQ, lane, 0.0);
     const double iq = wave_scan_first_f64<NW>(tq);
     const double eq = iq - tq;
 #pragma unroll

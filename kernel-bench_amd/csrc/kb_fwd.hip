@@ -52,8 +52,6 @@ __global__ __launch_bounds__(NT, (NT == 1024 && CPT == 2) ? 8 : 1) void fwd_row_
   const int tid = threadIdx.x;
   const int row = P.sched_rows[first + blockIdx.x];
   const int leaf_row = P.row_kind[row];
-  const int item = P.item[row];
-  const size_t cb = (size_t)item * P.const_stride;   // constants are [G, S] in preorder
 
   OwnTables<NT, CPT> O;
   O.load(T);
@@ -72,7 +70,7 @@ __global__ __launch_bounds__(NT, (NT == 1024 && CPT == 2) ? 8 : 1) void fwd_row_
     const int leaf = P.leaf_state[row];
     lpos = T.pre[leaf];
     const int lend = T.endpos[lpos];
-    leaf_obs = P.leaf_logp[cb + lpos];
+    leaf_obs = P.pS[lpos];
     const float leaf_col = WEIGHTED ? P.col[lpos] : 0.0f;
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
@@ -81,7 +79,7 @@ __global__ __launch_bounds__(NT, (NT == 1024 && CPT == 2) ? 8 : 1) void fwd_row_
       if (i < S) {
         const bool hit = i == lpos;
         const bool desc = i >= lpos && i < lend;
-        const size_t ci = cb + i;
+        const int ci = i;
         const float pi_w = hit ? leaf_obs : KB_NEG_INF;
         const float pibar_w = desc ? KB_NEG_INF : P.mt[ci] + leaf_col + leaf_obs;
         const float pi_s1 = c1p[k] == lpos ? leaf_obs : KB_NEG_INF;
@@ -91,7 +89,7 @@ __global__ __launch_bounds__(NT, (NT == 1024 && CPT == 2) ? 8 : 1) void fwd_row_
         const float t2 = pibar_w + P.E[ci];
         const float t3 = P.SL1[ci] + pi_s1;
         const float t4 = P.SL2[ci] + pi_s2;
-        const float t5 = hit ? P.leaf_logp[ci] : KB_NEG_INF;
+        const float t5 = hit ? P.pS[ci] : KB_NEG_INF;
         const float m = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, t5));
         const float ms = fsafe(m);
         const float sum = exp2f(t0 - ms) + exp2f(t1 - ms) + exp2f(t2 - ms) + exp2f(t3 - ms) + exp2f(t4 - ms) +
@@ -135,7 +133,7 @@ __global__ __launch_bounds__(NT, (NT == 1024 && CPT == 2) ? 8 : 1) void fwd_row_
         if (i < S) {
           const bool h1 = c1p[k] != MAXS, h2 = c2p[k] != MAXS;
           const float pl = L0[i], pr = L1[i];
-          const float d = P.pD.at(item, i), sp = P.pS.at(item, i);
+          const float d = P.pD[i], sp = P.pS[i];
           const float t0 = lsp + d + pl + pr;
           const float t1 = lsp + pl + L3[i];
           const float t2 = lsp + pr + L2[i];
@@ -173,10 +171,10 @@ __global__ __launch_bounds__(NT, (NT == 1024 && CPT == 2) ? 8 : 1) void fwd_row_
     const bool ok = i < S;
     y[k] = ok ? exp2f(v[k] - Ms) : 0.0f;
     dl[k] = leaf_row ? 0.0f : y[k];
-    ca[k] = ok ? P.lin_a[cb + i] : 0.0f;
-    ce[k] = ok ? P.lin_emc[cb + i] : 0.0f;
-    ck1[k] = ok ? P.lin_k1[cb + i] : 0.0f;
-    ck2[k] = ok ? P.lin_k2[cb + i] : 0.0f;
+    ca[k] = ok ? P.lin_a[i] : 0.0f;
+    ce[k] = ok ? P.lin_emc[i] : 0.0f;
+    ck1[k] = ok ? P.lin_k1[i] : 0.0f;
+    ck2[k] = ok ? P.lin_k2[i] : 0.0f;
     cw[k] = WEIGHTED ? (ok ? P.colw[i] : 0.0f) : 1.0f;
   }
   const float leaf_lin = leaf_row ? exp2f(leaf_obs - Ms) : 0.0f;  // lpos = -1 for split rows
@@ -229,7 +227,7 @@ __global__ __launch_bounds__(NT, (NT == 1024 && CPT == 2) ? 8 : 1) void fwd_row_
     if (i < S) {
       piv[k] = x[k] > 0.0f ? log2f(x[k]) + M : KB_NEG_INF;
       const float na = rowsum - ps[k] * f;
-      pbv[k] = na > 0.0f ? log2f(na) + M + P.mt[cb + i] : KB_NEG_INF;
+      pbv[k] = na > 0.0f ? log2f(na) + M + P.mt[i] : KB_NEG_INF;
       lmax = fmaxf(lmax, WEIGHTED ? P.col[i] + piv[k] : piv[k]);
     }
   }
@@ -262,8 +260,6 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int row = P.sched_rows[first + blockIdx.x];
   const int leaf_row = P.row_kind[row];
-  const int item = P.item[row];
-  const size_t cb = (size_t)item * P.const_stride;   // constants are [G, S] in preorder
 
   // Tables of the own positions i = tid*CPT + k and of the own postorder slots.
   // In preorder (child1 first) child1 of i is i + 1: from registers, except
@@ -284,6 +280,33 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
   }
   const int c1last = h1[CPT - 1] ? own_pos_c<NT, CPT>(CPT - 1) + 1 : ZERO;
 
+  // Per-position row constants.  Shapes of two positions per thread have
+  // registers to spare and run the levels with few rows per CU, where a row's
+  // dependent loads are not hidden by other workgroups: they load the
+  // constants before the row's own loads, so the latencies overlap.
+  constexpr bool EARLY = CPT == 2;
+  float kd[CPT], ks[CPT], ca[CPT], ce[CPT], ck1[CPT], ck2[CPT];
+  auto load_lin = [&]() {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int i = own_pos_c<NT, CPT>(k);
+      const bool ok = i < S;
+      ca[k] = ok ? P.lin_a[i] : 0.0f;
+      ce[k] = ok ? P.lin_emc[i] : 0.0f;
+      ck1[k] = h1[k] ? P.lin_k1[i] : 0.0f;  // 0 without child1: the x1 operand is then unused
+      ck2[k] = ok ? P.lin_k2[i] : 0.0f;
+    }
+  };
+  if constexpr (EARLY) {
+    load_lin();
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int i = own_pos_c<NT, CPT>(k);
+      kd[k] = i < S ? P.pD[i] : 0.0f;
+      ks[k] = i < S ? P.pS[i] : 0.0f;
+    }
+  }
+
   // ---- initial row (log2), own positions
   float v[CPT];
   int lpos = -1;
@@ -292,7 +315,7 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
     const int leaf = P.leaf_state[row];
     lpos = T.pre[leaf];
     const int lend = T.endpos[lpos];
-    leaf_obs = P.leaf_logp[cb + lpos];
+    leaf_obs = P.pS[lpos];
     const float leaf_col = WEIGHTED ? P.col[lpos] : 0.0f;
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
@@ -301,7 +324,7 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
       if (i < S) {
         const bool hit = i == lpos;
         const bool desc = i >= lpos && i < lend;
-        const size_t ci = cb + i;
+        const int ci = i;
         const float pi_w = hit ? leaf_obs : KB_NEG_INF;
         const float pibar_w = desc ? KB_NEG_INF : P.mt[ci] + leaf_col + leaf_obs;
         const float pi_s1 = (h1[k] && i + 1 == lpos) ? leaf_obs : KB_NEG_INF;
@@ -311,7 +334,7 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
         const float t2 = pibar_w + P.E[ci];
         const float t3 = P.SL1[ci] + pi_s1;
         const float t4 = P.SL2[ci] + pi_s2;
-        const float t5 = hit ? P.leaf_logp[ci] : KB_NEG_INF;
+        const float t5 = hit ? P.pS[ci] : KB_NEG_INF;
         const float m = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, t5));
         const float ms = fsafe(m);
         const float sum = exp2f(t0 - ms) + exp2f(t1 - ms) + exp2f(t2 - ms) + exp2f(t3 - ms) + exp2f(t4 - ms) +
@@ -357,7 +380,7 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
         const int i = own_pos_c<NT, CPT>(k);
         if (i < S) {
           const bool h2 = c2p[k] != ZERO;
-          const float d = P.pD.at(item, i), sp = P.pS.at(item, i);
+          const float d = EARLY ? kd[k] : P.pD[i], sp = EARLY ? ks[k] : P.pS[i];
           const float t0 = lsp + d + pl[k] + pr[k];
           const float t1 = lsp + pl[k] + br[k];
           const float t2 = lsp + pr[k] + bl[k];
@@ -400,17 +423,14 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
   for (int k = 0; k < CPT; ++k) lm = fmaxf(lm, v[k]);
   const float Ms = fsafe(block_max1<NT>(lm, wM));
   const float leaf_lin = leaf_row ? exp2f(leaf_obs - Ms) : 0.0f;  // lpos = -1 for split rows
-  float y[CPT], dl[CPT], ca[CPT], ce[CPT], ck1[CPT], ck2[CPT], cw[CPT], cwq[CPT];
+  float y[CPT], dl[CPT], cw[CPT], cwq[CPT];
+  if constexpr (!EARLY) load_lin();
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int i = own_pos_c<NT, CPT>(k);
     const bool ok = i < S;
     y[k] = ok ? exp2f(v[k] - Ms) : 0.0f;
     dl[k] = leaf_row ? (i == lpos ? leaf_lin : 0.0f) : y[k];
-    ca[k] = ok ? P.lin_a[cb + i] : 0.0f;
-    ce[k] = ok ? P.lin_emc[cb + i] : 0.0f;
-    ck1[k] = h1[k] ? P.lin_k1[cb + i] : 0.0f;  // 0 without child1: the x1 operand is then unused
-    ck2[k] = ok ? P.lin_k2[cb + i] : 0.0f;
     cw[k] = WEIGHTED ? (ok ? P.colw[i] : 0.0f) : 1.0f;
     cwq[k] = WEIGHTED ? (qp[k] < S ? P.colw[qp[k]] : 0.0f) : 1.0f;
   }
@@ -431,7 +451,7 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
     __syncthreads();
     // phase B: preorder offsets and row sum; the postorder values and the
     // child2 values (read before the next barrier); exclusive postorder scan
-    const float tp = lane < NW ? wP[lane] : 0.0f;
+    const float tp = lds_wave_values<NW>(wP, lane, 0.0f);
     float yq[CPT], x2[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
@@ -460,7 +480,7 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
     rowsum = tsum * f;
     __syncthreads();
     // phase C: path sums ps(i) = Pre(i) - PostEx(tin(i) - i)
-    const float tq = lane < NW ? wQ[lane] : 0.0f;
+    const float tq = lds_wave_values<NW>(wQ, lane, 0.0f);
     const float iq = wave_scan_first<NW>(tq);
     const float eq = iq - tq;
 #pragma unroll
@@ -496,7 +516,7 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
       const float x = y[k] * f;
       piv[k] = x > 0.0f ? log2f(x) + M : KB_NEG_INF;
       const float na = rowsum - ps[k] * f;
-      pbv[k] = na > 0.0f ? log2f(na) + M + P.mt[cb + i] : KB_NEG_INF;
+      pbv[k] = na > 0.0f ? log2f(na) + M + P.mt[i] : KB_NEG_INF;
       lmax = fmaxf(lmax, WEIGHTED ? P.col[i] + piv[k] : piv[k]);
     }
   }

@@ -58,16 +58,13 @@ struct FwdParams {
   int narrow_below;           // wide == 0: 1024 x 2 on levels with fewer rows than this
   int n_sweeps;               // pi_iters - 1
   int use_col;
-  int const_stride;           // 0: one constant row; S: item-indexed rows
-  // per-position constants (preorder), row = item * const_stride
+  // per-position constants: one [S] row in preorder, shared by every row
   const float* lin_a; const float* lin_emc; const float* lin_k1; const float* lin_k2;
   const float* colw;          // [S] 2^col_log_probs (weighted) -- may be null when !use_col
   const float* col;           // [S]
   const float* mt; const float* DL; const float* Ebar; const float* E; const float* SL1; const float* SL2;
-  const float* leaf_logp;     // [G,S] log pS used by the leaf term
-  RateDev pD, pS;             // split-term rates
+  const float* pD; const float* pS;  // [S] split-term rates (pS is also the leaf term's log pS)
   // layout
-  const int* item;            // [C]
   const int* leaf_state;      // [C]
   const int* split_ptr;       // [C+1] splits of each parent row
   const int* split_l; const int* split_r; const float* split_lsp;

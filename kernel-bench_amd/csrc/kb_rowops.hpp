@@ -44,6 +44,16 @@ __device__ __forceinline__ float wave_prev_lane(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x138, 0xf, 0xf, false));  // wave_shr:1
 }
 
+// Per-wavefront values published in LDS (w[0..NW-1]), read by lanes 0..NW-1
+// (zero elsewhere) without a branch, so the scheduler can issue the read
+// together with the gathers around it.  NW is a power of two.
+template <int NW, typename T>
+__device__ __forceinline__ T lds_wave_values(const T* w, int lane, T zero) {
+  static_assert((NW & (NW - 1)) == 0, "power of two");
+  const T x = w[lane & (NW - 1)];
+  return lane < NW ? x : zero;
+}
+
 // Inclusive scan (+) over lanes [0, N) of a wavefront, N <= 16 (row 0 only;
 // the other lanes hold partial sums).
 template <int N>

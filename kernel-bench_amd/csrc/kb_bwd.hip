@@ -363,23 +363,28 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       pcoef[k] = q[2][k] * inv_denom;
     }
   }
-  // child-edge weights into position i from its parent: q3 if i is child1, else q4.
-  // Sc (= R2..R3) is still being read above: barrier, then restore the padding.
+  // child-edge weights into position i from its parent: q3 if i is child1,
+  // else q4.  The parent's owner scatters them into R1 (free since Pibar* was
+  // read; every position has one parent, the root none), one barrier, and
+  // each thread reads its own positions.  The barrier also ends the reads of
+  // Sc (= R2..R3), whose padding is then restored for the scan buffers.
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    if (O.c1p[k] != ZERO) R1[O.c1p[k]] = q[3][k];
+    if (O.c2p[k] != ZERO) R1[O.c2p[k]] = q[4][k];
+  }
   __syncthreads();
   if (tid < 64) {
     R2[MAXS + tid] = 0.0f;
     R3[MAXS + tid] = 0.0f;
   }
-  lds_store_own<CPT>(R2, q[3]);
-  lds_store_own<CPT>(R3, q[4]);
-  __syncthreads();
   float edge[CPT], diag[CPT];
+  lds_load_own<CPT>(R1, edge);
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
-    edge[k] = ppos[k] != ZERO ? (pfl[k] ? R2[ppos[k]] : R3[ppos[k]]) : 0.0f;
+    edge[k] = ppos[k] != ZERO ? edge[k] : 0.0f;
     diag[k] = q[0][k] + q[1][k];
   }
-  __syncthreads();  // R2 / R3 become scan buffers
 
   // The first split's four child rows (Pi, Pibar of both children) are loaded
   // into registers here, so their latency overlaps the Neumann loop.

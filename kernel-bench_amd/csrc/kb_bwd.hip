@@ -42,7 +42,6 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   float* R1 = L + LD;
   float* R2 = L + 2 * LD;
   float* R3 = L + 3 * LD;
-  float* Sc = R2;  // one-time Euler scan (2*MAXS floats) overlays R2..R3; their padding is re-zeroed after
 
   const PreDev& T = P.pre;
   const int S = P.S;
@@ -50,8 +49,8 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   constexpr int ZERO = MAXS;
 
   // The narrow 1024 x 2 shape runs the levels with about one row per
-  // workgroup: it fetches rows when needed instead of one row ahead, and loads
-  // the Euler tables per row instead of holding them (128 VGPRs at 16 waves).
+  // workgroup: it fetches rows when needed instead of one row ahead (128
+  // VGPRs at 16 waves).
   constexpr bool AHEAD = !(NT == 1024 && CPT == 2);
   OwnTablesC<NT, CPT> O;
   O.load(T);
@@ -66,10 +65,14 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   for (int k = 0; k < CPT; ++k) okp[k] = own_pos_c<NT, CPT>(k) < S;
   // static per position: parent position (ZERO at the root), child-1 flag,
   // subtree end - 1 and the previous position (ZERO at position 0)
-  int ppos[CPT], endm1[CPT], prev[CPT], pfl[CPT];
+  // and, for the root-path sums, the position at own postorder slot k (the
+  // padding slot ZERO past the row) and tin(i) - i
+  int ppos[CPT], endm1[CPT], prev[CPT], pfl[CPT], qp[CPT], nex[CPT];
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int i = own_pos_c<NT, CPT>(k);
+    qp[k] = okp[k] ? T.post[i] : ZERO;
+    nex[k] = okp[k] ? T.tin[i] - i : 0;
     const int pa = okp[k] ? T.ppos[i] : -1;
     ppos[k] = pa >= 0 ? pa : ZERO;
     pfl[k] = pa >= 0 ? T.pflag[i] : 0;
@@ -304,25 +307,56 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
 
   // ---- 4. J^T coefficients at Pi* (precompute kernel, wave_backward.py:264-416)
   const float rms = fsafe(P.rowmax[row]);
-  float pp[CPT];
-  lds_store_own<CPT>(R0, piv);  // Pi* at own positions for the child gathers (padding positions: -inf)
-  __syncthreads();               // publishes R0
-  float ls = 0.0f;
+  // p' = 2^(col + Pi* - rowmax) and its root-path sums ps(i) = Pre(i) -
+  // PostEx(tin(i) - i) (inclusive preorder scan, exclusive postorder scan;
+  // the postorder slots of position i's left context end at tin(i) - i).
+  // The preorder scan runs in registers; one barrier publishes Pi* (R0, for
+  // the child gathers), p' (R2, for the postorder gathers) and the wavefront
+  // totals, a second one the postorder scan (R3).  The row sum is the
+  // preorder total.
+  float pp[CPT], sp[CPT], ta = 0.0f;
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int i = own_pos_c<NT, CPT>(k);
     pp[k] = okp[k] ? exp2f((WEIGHTED ? P.col[i] : 0.0f) + piv[k] - rms) : 0.0f;
-    ls += pp[k];
+    ta += pp[k];
+    sp[k] = ta;
   }
+  const int wv = tid >> 6, lane = tid & 63;
+  const float wa = wave_scan_incl(ta);
+  lds_store_own<CPT>(R0, piv);  // padding positions: -inf
   lds_store_own<CPT>(R2, pp);
-  const float rowsum = block_sum1<NT>(ls, wA);
-  float ps[CPT];
-  if constexpr (AHEAD) {
-    path_sum_euler<NT, CPT>(O, R2, Sc, wB, ps);
-  } else {
-    OwnTablesC<NT, CPT> Oe;
-    Oe.load(T);
-    path_sum_euler<NT, CPT>(Oe, R2, Sc, wB, ps);
+  if (lane == 63) wA[wv] = wa;
+  __syncthreads();
+  float ps[CPT], rowsum;
+  {
+    constexpr int SEG = 64 * CPT;  // postorder slots per wavefront
+    const float tp = lds_wave_values<NW>(wA, lane, 0.0f);
+    float yq[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) yq[k] = R2[qp[k]];
+    const float ip = wave_scan_first<NW>(tp);
+    rowsum = lane_value(ip, NW - 1);
+    const float offp = lane_value(ip - tp, wv) + (wa - ta);
+    float sq[CPT], tb = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      sq[k] = tb;
+      tb += yq[k];
+    }
+    const float wb = wave_scan_incl(tb);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) sq[k] += wb - tb;
+    lds_store_own<CPT>(R3, sq);
+    if (lane == 63) wB[wv] = wb;
+    __syncthreads();
+    const float tq = lds_wave_values<NW>(wB, lane, 0.0f);
+    const float eq = wave_scan_first<NW>(tq) - tq;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int n = nex[k];
+      ps[k] = (sp[k] + offp) - (R3[n] + __shfl(eq, n / SEG, 64));
+    }
   }
   const int lpos = leaf_row ? T.pre[P.leaf_state[row]] : -1;
   float q[6][CPT], pcoef[CPT];
@@ -367,17 +401,13 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   // else q4.  The parent's owner scatters them into R1 (free since Pibar* was
   // read; every position has one parent, the root none), one barrier, and
   // each thread reads its own positions.  The barrier also ends the reads of
-  // Sc (= R2..R3), whose padding is then restored for the scan buffers.
+  // R2 / R3, which become the scan buffers.
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     if (O.c1p[k] != ZERO) R1[O.c1p[k]] = q[3][k];
     if (O.c2p[k] != ZERO) R1[O.c2p[k]] = q[4][k];
   }
   __syncthreads();
-  if (tid < 64) {
-    R2[MAXS + tid] = 0.0f;
-    R3[MAXS + tid] = 0.0f;
-  }
   float edge[CPT], diag[CPT];
   lds_load_own<CPT>(R1, edge);
 #pragma unroll
@@ -420,7 +450,6 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   int wend[CPT];
 #pragma unroll
   for (int k = 0; k < CPT; ++k) wend[k] = endm1[k] < ZERO ? endm1[k] / (64 * CPT) : 0;
-  const int wv = tid >> 6, lane = tid & 63;
   for (int n = 0; n < P.n_terms; ++n) {
     float* Tb = (n & 1) ? R1 : R0;
     float* Lb = (n & 1) ? R3 : R2;

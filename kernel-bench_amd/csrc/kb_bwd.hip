@@ -38,6 +38,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   constexpr int NW = NT / 64;
   __shared__ float L[4 * LD];
   __shared__ float wA[2 * NW], wB[2 * NW];
+  __shared__ float wMk[NW];  // wavefront maxima of |adjoint| for the active mask
   float* R0 = L;
   float* R1 = L + LD;
   float* R2 = L + 2 * LD;
@@ -64,10 +65,10 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
 #pragma unroll
   for (int k = 0; k < CPT; ++k) okp[k] = own_pos_c<NT, CPT>(k) < S;
   // static per position: parent position (ZERO at the root), child-1 flag,
-  // subtree end - 1 and the previous position (ZERO at position 0)
+  // subtree end - 1
   // and, for the root-path sums, the position at own postorder slot k (the
   // padding slot ZERO past the row) and tin(i) - i
-  int ppos[CPT], endm1[CPT], prev[CPT], pfl[CPT], qp[CPT], nex[CPT];
+  int ppos[CPT], endm1[CPT], pfl[CPT], qp[CPT], nex[CPT];
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int i = own_pos_c<NT, CPT>(k);
@@ -77,7 +78,6 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     ppos[k] = pa >= 0 ? pa : ZERO;
     pfl[k] = pa >= 0 ? T.pflag[i] : 0;
     endm1[k] = okp[k] ? T.endpos[i] - 1 : ZERO;
-    prev[k] = i > 0 ? i - 1 : ZERO;
   }
   // gradient buckets of every row this workgroup processes (static round-robin
   // assignment, so the summation order is fixed)
@@ -203,6 +203,16 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
         if (okp[k]) rhs[k] += st[own_pos_c<NT, CPT>(k)];
     }
   }
+  // rows below the roots: their adjoint is known here, so the wavefront maxima
+  // for the active mask are published under the staging barrier below
+  const bool mask_early = !P.class_mode && fam < 0;
+  if (mask_early) {
+    float am = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) am = fmaxf(am, fabsf(rhs[k]));
+    const float wm = wave_reduce_max(am);
+    if ((tid & 63) == 0) wMk[tid >> 6] = wm;
+  }
   float piv[CPT], pbv[CPT];
   if (!AHEAD) fetch_rows(rr);
 #pragma unroll
@@ -237,10 +247,17 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       for (int k = 0; k < CPT; ++k) rhs[k] = (piv[k] == KB_NEG_INF) ? 0.0f : -exp2f(piv[k] - lses);
     }
     // ---- 2. active mask (the reference's rule, wave_backward.py:150-163)
-    float am = 0.0f;
+    float amax;
+    if (mask_early) {
+      amax = 0.0f;
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) am = fmaxf(am, fabsf(rhs[k]));
-    const float amax = block_max1<NT>(am, fam >= 0 ? wA : wB);
+      for (int w = 0; w < NW; ++w) amax = fmaxf(amax, wMk[w]);
+    } else {
+      float am = 0.0f;
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) am = fmaxf(am, fabsf(rhs[k]));
+      amax = block_max1<NT>(am, wA);
+    }
     any_active = P.use_pruning ? (amax >= P.thr) : (amax > P.thr);
     if (tid == 0) P.mask[row] = any_active ? 1 : 0;
   }
@@ -248,7 +265,11 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     for (int i = sb + tid; i < se; i += NT) P.split_on[i] = 0;
     continue;
   }
-  __syncthreads();  // R0 (Pi*) and the scratch above are reused below
+  // The root rows' reductions above used the scratch that the path sums
+  // reuse, and the split term below (without stored split terms) restages
+  // R0..R3: those wait for every wavefront here.  Otherwise each thread has
+  // read only its own positions of R0 / R1 since the staging barrier.
+  if (fam >= 0 || (!leaf_row && !P.dts_in)) __syncthreads();
 
   // ---- 3. split term at Pi* (split rows), children staged through LDS
   float dts[CPT];
@@ -495,12 +516,12 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     const int n = P.n_terms;
     float* Pb = (n & 1) ? R3 : R2;
     float* wt = (n & 1) ? wB : wA;
-    float u[CPT];
+    float u[CPT], sc[CPT], pm1[CPT], rest[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) u[k] = v[k] * pcoef[k];
-    const float A = block_scan_incl_c<NT, CPT>(u, wt);
-    lds_store_own<CPT>(Pb, u);
+    local_scan_publish<NT, CPT>(sc, u, Pb, wt);
     __syncthreads();
+    subtree_terms<NT, CPT>(sc, Pb, wt, endm1, wend, pm1, rest);
     float x[8][CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
@@ -513,7 +534,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       x[4][k] = aw4;
       x[5][k] = aw3;
       x[6][k] = aw2;
-      x[7][k] = okp[k] ? pp[k] * (Pb[prev[k]] + (A - Pb[endm1[k]])) : 0.0f;
+      x[7][k] = okp[k] ? pp[k] * (pm1[k] + rest[k]) : 0.0f;
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) bucket_add(j, x[j]);
@@ -587,11 +608,12 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     __syncthreads();  // staged children fully read
     lds_store_own<CPT>(R0, vd3);
     lds_store_own<CPT>(R1, vd4);
-    float Al, Ar;
-    block_scan_incl2_c<NT, CPT>(udl, udr, wA, Al, Ar);  // barrier: publishes R0 / R1
-    lds_store_own<CPT>(R2, udl);
-    lds_store_own<CPT>(R3, udr);
+    float scl[CPT], scr[CPT], pml[CPT], rsl[CPT], pmr[CPT], rsr[CPT];
+    local_scan_publish<NT, CPT>(scl, udl, R2, wA);
+    local_scan_publish<NT, CPT>(scr, udr, R3, wA + NW);
     __syncthreads();
+    subtree_terms<NT, CPT>(scl, R2, wA, endm1, wend, pml, rsl);
+    subtree_terms<NT, CPT>(scr, R3, wA + NW, endm1, wend, pmr, rsr);
     float* stl = P.staging + (size_t)(2 * si) * S;
     float* str = P.staging + (size_t)(2 * si + 1) * S;
     float y[4][CPT];
@@ -600,8 +622,8 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       const int i = own_pos_c<NT, CPT>(k);
       y[0][k] = y[1][k] = y[2][k] = y[3][k] = 0.0f;
       if (okp[k]) {
-        const float tl = ppl[k] * (R2[prev[k]] + (Al - R2[endm1[k]]));
-        const float tr = ppr[k] * (R3[prev[k]] + (Ar - R3[endm1[k]]));
+        const float tl = ppl[k] * (pml[k] + rsl[k]);
+        const float tr = ppr[k] * (pmr[k] + rsr[k]);
         const int pa = ppos[k];
         const bool first = pfl[k] != 0;
         const float sh3 = R0[pa], sh4 = R1[pa];  // padding slot holds 0

@@ -367,6 +367,49 @@ __device__ __forceinline__ float block_scan_incl_c(float (&v)[CPT], float* wtot)
   return total;
 }
 
+// Subtree sums with one barrier.  Before it, local_scan_publish stores the
+// wavefront-local inclusive scan of u (own positions) at L and the wavefront
+// total at wt[wavefront]; after it, subtree_terms gives for every own
+// position i  P(i - 1)  and  A - P(end(i) - 1)  of the block-wide inclusive
+// scan P (A its total, P(-1) = 0), adding the wavefront offsets to what it
+// reads.  wend[k] is the wavefront that owns end(i) - 1.
+template <int NT, int CPT>
+__device__ __forceinline__ void local_scan_publish(float (&sc)[CPT], const float (&u)[CPT], float* L, float* wt) {
+  float t = 0.0f;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    t += u[k];
+    sc[k] = t;
+  }
+  const float ws = wave_scan_incl(t);
+  if ((threadIdx.x & 63) == 63) wt[threadIdx.x >> 6] = ws;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) sc[k] += ws - t;
+  lds_store_own<CPT>(L, sc);
+}
+
+template <int NT, int CPT>
+__device__ __forceinline__ void subtree_terms(const float (&sc)[CPT], const float* L, const float* wt,
+                                              const int (&endm1)[CPT], const int (&wend)[CPT], float (&pm1)[CPT],
+                                              float (&rest)[CPT]) {
+  constexpr int NW = NT / 64;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  float le[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) le[k] = L[endm1[k]];
+  const float wtot = lds_wave_values<NW>(wt, lane, 0.0f);
+  const float wincl = wave_scan_first<NW>(wtot);
+  const float wexcl = wincl - wtot;  // lane x < NW: offset of wavefront x
+  const float A = lane_value(wincl, NW - 1);
+  const float woff = lane_value(wexcl, wv);
+  const float p0 = wave_prev_lane(sc[CPT - 1]) + woff;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    pm1[k] = k == 0 ? p0 : sc[k - 1] + woff;
+    rest[k] = A - (le[k] + __shfl(wexcl, wend[k], 64));
+  }
+}
+
 // Two contiguous-ownership scans sharing one barrier (wtot holds 2*NW floats).
 template <int NT, int CPT>
 __device__ __forceinline__ void block_scan_incl2_c(float (&a)[CPT], float (&b)[CPT], float* wtot, float& ta,

@@ -107,6 +107,7 @@ struct kb_plan {
   int* d_split_ptr = nullptr; int* d_split_l = nullptr; int* d_split_r = nullptr; float* d_split_lsp = nullptr;
   int* d_split_parent = nullptr;
   int* d_child_ptr = nullptr; int* d_child_in = nullptr;
+  int* d_bslot = nullptr;  // [2C] first two child sides of the row at each schedule slot
   float* d_unnorm = nullptr;
   // per-solve constants [S]
   float* c_DL = nullptr; float* c_SL1 = nullptr; float* c_SL2 = nullptr; float* c_pS = nullptr;
@@ -323,6 +324,10 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
   }
   for (int f = 0; f < L->n_fam; ++f) roots[f] = (int)L->root_row_ids[f];
   const int64_t NS = L->n_splits;
+  if (NS < 0 || NS >= (int64_t{1} << 29)) {  // split sides are ints below 2^30
+    kb_plan_destroy(p);
+    return set_error(KB_ERR_ARG, "n_splits %lld outside [0, 2^29)", (long long)NS);
+  }
   // rows -> wave; every wave a contiguous row range, in order
   std::vector<int> wave_of(C, -1);
   for (int w = 0; w < L->n_waves; ++w) {
@@ -499,6 +504,17 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
   rc |= upload(&p->d_split_parent, spar);
   rc |= upload(&p->d_child_ptr, ccnt);
   rc |= upload(&p->d_child_in, cin);
+  {
+    // schedule slot j: the first two child sides of row sched[j] (-1: none),
+    // bit 30 of the second set when the row has more
+    std::vector<int> bslot(2 * (size_t)C);
+    for (int j = 0; j < C; ++j) {
+      const int r = sched[j], gb = ccnt[r], n = ccnt[r + 1] - gb;
+      bslot[2 * (size_t)j] = n > 0 ? cin[gb] : -1;
+      bslot[2 * (size_t)j + 1] = n > 1 ? (cin[gb + 1] | (n > 2 ? (1 << 30) : 0)) : -1;
+    }
+    rc |= upload(&p->d_bslot, bslot);
+  }
   rc |= upload(&p->d_unnorm, unnorm);
   rc |= upload(&p->d_root_index, root_index);
   rc |= upload(&p->d_sched_rows, sched);
@@ -572,7 +588,7 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
                     (void*)p->d_blevel_node, (void*)p->d_tlevel_ptr, (void*)p->d_tlevel_node, (void*)p->d_sub_start,
                     (void*)p->d_sub_end, (void*)p->d_item, (void*)p->d_leaf, (void*)p->d_roots, (void*)p->d_split_ptr,
                     (void*)p->d_split_l, (void*)p->d_split_r, (void*)p->d_split_lsp, (void*)p->d_split_parent,
-                    (void*)p->d_child_ptr, (void*)p->d_child_in, (void*)p->d_unnorm, (void*)p->c_DL, (void*)p->c_SL1,
+                    (void*)p->d_child_ptr, (void*)p->d_child_in, (void*)p->d_bslot, (void*)p->d_unnorm, (void*)p->c_DL, (void*)p->c_SL1,
                     (void*)p->c_SL2, (void*)p->c_pS, (void*)p->c_pD, (void*)p->c_colw, (void*)p->lin_a,
                     (void*)p->lin_emc, (void*)p->lin_k1, (void*)p->lin_k2, (void*)p->E64, (void*)p->n_e_iter,
                     (void*)p->loss_terms, (void*)p->loss64, (void*)p->d_root_index,
@@ -838,6 +854,7 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   B.split_lsp = p->d_split_lsp;
   B.child_ptr = p->d_child_ptr;
   B.child_in = p->d_child_in;
+  B.bslot = p->d_bslot;
   B.staging = p->b_staging;
   B.split_on = p->b_split_on;
   B.mask = io->active_mask ? (unsigned char*)io->active_mask : p->b_mask;

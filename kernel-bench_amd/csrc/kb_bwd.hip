@@ -154,7 +154,33 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       nPb[j] = spre[j] >= 0 ? P.pibar[b2 + s] : 0.0f;
     }
   };
-  if (AHEAD && (int)blockIdx.x < n_rows) fetch_rows(blockIdx.x);
+  // The adjoint of a row below the roots is the sum of its child sides'
+  // staging rows whose split was active, in side order.  The first two sides
+  // come from the schedule-slot table; their split_on flags and staging rows
+  // are fetched one row ahead too (vector loads: lanes 0 / 1 hold the two
+  // sides, so the LDS waits in between do not wait on them).  Further sides
+  // (rare) are gathered when the row starts.
+  float nst0[CPT], nst1[CPT];
+  int nfl = 0, nmore = 0;
+  auto rhs_rec = [&](int r2) -> int { return P.bslot[2 * (size_t)(first + r2) + (tid & 1)]; };
+  auto fetch_rhs = [&](int rec) {
+    const int s0 = __builtin_amdgcn_readlane(rec, 0), s1r = __builtin_amdgcn_readlane(rec, 1);
+    const int s1 = s1r < 0 ? -1 : (s1r & ((1 << 30) - 1));
+    nmore = s1r >= 0 && (s1r >> 30) != 0;
+    const int sl = (tid & 1) ? s1 : s0;
+    nfl = sl >= 0 ? (int)P.split_on[sl >> 1] : 0;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int i = own_pos_c<NT, CPT>(k);
+      nst0[k] = (s0 >= 0 && okp[k]) ? P.staging[(size_t)s0 * S + i] : 0.0f;
+      nst1[k] = (s1 >= 0 && okp[k]) ? P.staging[(size_t)s1 * S + i] : 0.0f;
+    }
+  };
+  if (AHEAD && (int)blockIdx.x < n_rows) {
+    fetch_rows(blockIdx.x);
+    if (!P.class_mode) fetch_rhs(rhs_rec(blockIdx.x));
+  }
+  int rec_next = -1;
   if constexpr (CK_LDS) {
 #pragma unroll
     for (int j = 0; j < K_N; ++j) {
@@ -192,15 +218,26 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
 #pragma unroll
     for (int k = 0; k < CPT; ++k)
       if (okp[k]) rhs[k] = src[own_pos_c<NT, CPT>(k)];
-  } else if (fam < 0) {
-    const int gb = P.child_ptr[row], ge = P.child_ptr[row + 1];
-    for (int i = gb; i < ge; ++i) {
-      const int side = P.child_in[i];
-      if (!P.split_on[side >> 1]) continue;
-      const float* st = P.staging + (size_t)side * S;
+  } else {
+    if (!AHEAD) fetch_rhs(rhs_rec(rr));
+    if (__builtin_amdgcn_readlane(nfl, 0)) {
 #pragma unroll
-      for (int k = 0; k < CPT; ++k)
-        if (okp[k]) rhs[k] += st[own_pos_c<NT, CPT>(k)];
+      for (int k = 0; k < CPT; ++k) rhs[k] += nst0[k];
+    }
+    if (__builtin_amdgcn_readlane(nfl, 1)) {
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) rhs[k] += nst1[k];
+    }
+    if (nmore) {
+      const int gb = P.child_ptr[row] + 2, ge = P.child_ptr[row + 1];
+      for (int i = gb; i < ge; ++i) {
+        const int side = P.child_in[i];
+        if (!P.split_on[side >> 1]) continue;
+        const float* st = P.staging + (size_t)side * S;
+#pragma unroll
+        for (int k = 0; k < CPT; ++k)
+          if (okp[k]) rhs[k] += st[own_pos_c<NT, CPT>(k)];
+      }
     }
   }
   // rows below the roots: their adjoint is known here, so the wavefront maxima
@@ -221,7 +258,10 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       R0[spre[j]] = nPi[j];
       R1[spre[j]] = nPb[j];
     }
-  if (AHEAD && rr + (int)gridDim.x < n_rows) fetch_rows(rr + gridDim.x);
+  if (AHEAD && rr + (int)gridDim.x < n_rows) {
+    fetch_rows(rr + gridDim.x);
+    if (!P.class_mode) rec_next = rhs_rec(rr + gridDim.x);
+  }
   __syncthreads();
   lds_load_own<CPT>(R0, piv);
   lds_load_own<CPT>(R1, pbv);
@@ -510,6 +550,8 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       v[k] += nt;
     }
   }
+
+  if (AHEAD && !P.class_mode && rr + (int)gridDim.x < n_rows) fetch_rhs(rec_next);
 
   // ---- 6. self-loop column gradient and parameter buckets
   {

@@ -111,6 +111,7 @@ struct BwdParams {
   const int* leaf_state; const int* root_index;
   const int* split_ptr; const int* split_l; const int* split_r; const float* split_lsp;
   const int* child_ptr; const int* child_in;
+  const int* bslot;           // [2 * C] schedule slot -> first two child sides (-1: none; bit 30: more follow)
   float* staging;             // [2 * n_splits, S]
   unsigned char* split_on;    // [n_splits]
   unsigned char* mask;        // [C]

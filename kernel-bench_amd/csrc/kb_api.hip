@@ -107,7 +107,7 @@ struct kb_plan {
   int* d_split_ptr = nullptr; int* d_split_l = nullptr; int* d_split_r = nullptr; float* d_split_lsp = nullptr;
   int* d_split_parent = nullptr;
   int* d_child_ptr = nullptr; int* d_child_in = nullptr;
-  int* d_bslot = nullptr;  // [2C] first two child sides of the row at each schedule slot
+  int* d_bslot = nullptr;  // [KB_BREC * C] the backward's record of every schedule slot
   float* d_unnorm = nullptr;
   // per-solve constants [S]
   float* c_DL = nullptr; float* c_SL1 = nullptr; float* c_SL2 = nullptr; float* c_pS = nullptr;
@@ -504,17 +504,6 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
   rc |= upload(&p->d_split_parent, spar);
   rc |= upload(&p->d_child_ptr, ccnt);
   rc |= upload(&p->d_child_in, cin);
-  {
-    // schedule slot j: the first two child sides of row sched[j] (-1: none),
-    // bit 30 of the second set when the row has more
-    std::vector<int> bslot(2 * (size_t)C);
-    for (int j = 0; j < C; ++j) {
-      const int r = sched[j], gb = ccnt[r], n = ccnt[r + 1] - gb;
-      bslot[2 * (size_t)j] = n > 0 ? cin[gb] : -1;
-      bslot[2 * (size_t)j + 1] = n > 1 ? (cin[gb + 1] | (n > 2 ? (1 << 30) : 0)) : -1;
-    }
-    rc |= upload(&p->d_bslot, bslot);
-  }
   rc |= upload(&p->d_unnorm, unnorm);
   rc |= upload(&p->d_root_index, root_index);
   rc |= upload(&p->d_sched_rows, sched);
@@ -531,6 +520,28 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
     std::vector<int> rep_of(C);
     for (int r = 0; r < C; ++r) rep_of[r] = rep[cls[r]];
     rc |= upload(&p->d_rep_of, rep_of);
+    // the backward's record of schedule slot j (row sched[j]), KB_BREC ints
+    std::vector<int> brec((size_t)kb::KB_BREC * C, -1);
+    for (int j = 0; j < C; ++j) {
+      const int r = sched[j], gb = ccnt[r], n = ccnt[r + 1] - gb;
+      int* q = brec.data() + (size_t)kb::KB_BREC * j;
+      q[kb::BR_S0] = n > 0 ? cin[gb] : -1;
+      q[kb::BR_S1] = n > 1 ? (cin[gb + 1] | (n > 2 ? (1 << 30) : 0)) : -1;
+      q[kb::BR_ROW] = r;
+      q[kb::BR_FAM] = root_index[r];
+      q[kb::BR_LEAF] = row_kind[r];
+      q[kb::BR_SB] = sptr[r];
+      q[kb::BR_SE] = sptr[r + 1];
+      q[kb::BR_REP] = rep_of[r];
+      const bool hs = sptr[r + 1] > sptr[r];
+      q[kb::BR_L0] = hs ? sl[sptr[r]] : -1;
+      q[kb::BR_R0] = hs ? sr[sptr[r]] : -1;
+      int lsp_bits = 0;
+      if (hs) std::memcpy(&lsp_bits, &slsp[sptr[r]], sizeof(lsp_bits));
+      q[kb::BR_LSP0] = lsp_bits;
+      q[kb::BR_LPOS] = row_kind[r] ? pre[leaf[r]] : -1;
+    }
+    rc |= upload(&p->d_bslot, brec);
     std::vector<int> msp{0}, ms, mroot;
     for (int r : cls_rows) {
       for (int j = ccnt[r]; j < ccnt[r + 1]; ++j) ms.push_back(cin[j]);

@@ -134,9 +134,16 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     }
   };
 
-  // Pi* / Pibar* rows are fetched one row ahead: column s = tid + j*NT of the
-  // next row this workgroup processes goes to registers while the current row
-  // is solved, then to its preorder position spre[j] in LDS.
+  // What a row needs from memory is fetched one row ahead, while the previous
+  // row is solved: Pi* / Pibar* (column s = tid + j*NT to registers, then to
+  // its preorder position spre[j] in LDS), and below the class level the
+  // row's record (BrecField, lanes 0..KB_BREC-1), the split_on flags and
+  // staging rows of its first two child sides (whose active sum, in side
+  // order, is the adjoint; further sides, rare, are gathered when the row
+  // starts), the row maxima of the row and of its first split's children, and
+  // its stored split term.  Flags and maxima are vector loads (lanes 0..2
+  // hold the different entries), so the LDS waits in between do not wait on
+  // them.  The narrow shape fetches all of it when the row starts.
   auto row_of = [&](int r2) { return P.class_mode ? P.cls_rows[P.cls_ptr[r2]] : P.sched_rows[first + r2]; };
   int spre[CPT];
 #pragma unroll
@@ -145,8 +152,8 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     spre[j] = s < S ? T.pre[s] : -1;
   }
   float nPi[CPT], nPb[CPT];
-  auto fetch_rows = [&](int r2) {
-    const size_t b2 = (size_t)row_of(r2) * S;
+  auto fetch_rows = [&](int row2) {
+    const size_t b2 = (size_t)row2 * S;
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
       const int s = tid + j * NT;
@@ -154,33 +161,52 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       nPb[j] = spre[j] >= 0 ? P.pibar[b2 + s] : 0.0f;
     }
   };
-  // The adjoint of a row below the roots is the sum of its child sides'
-  // staging rows whose split was active, in side order.  The first two sides
-  // come from the schedule-slot table; their split_on flags and staging rows
-  // are fetched one row ahead too (vector loads: lanes 0 / 1 hold the two
-  // sides, so the LDS waits in between do not wait on them).  Further sides
-  // (rare) are gathered when the row starts.
-  float nst0[CPT], nst1[CPT];
-  int nfl = 0, nmore = 0;
-  auto rhs_rec = [&](int r2) -> int { return P.bslot[2 * (size_t)(first + r2) + (tid & 1)]; };
-  auto fetch_rhs = [&](int rec) {
-    const int s0 = __builtin_amdgcn_readlane(rec, 0), s1r = __builtin_amdgcn_readlane(rec, 1);
+  auto load_rec = [&](int r2) -> int { return P.bslot[(size_t)KB_BREC * (first + r2) + (tid & (KB_BREC - 1))]; };
+  // (read fields at uniform points only: a lane read inside divergent code may
+  // see a register that was restored for the active lanes alone)
+  auto field = [](int rec, int f) { return __builtin_amdgcn_readlane(rec, f); };
+  float nst0[CPT], nst1[CPT], nds[CPT], nrm = 0.0f;
+  int nfl = 0;
+  auto fetch_row_data = [&](int rec) {
+    const int s0 = field(rec, BR_S0), s1r = field(rec, BR_S1);
     const int s1 = s1r < 0 ? -1 : (s1r & ((1 << 30) - 1));
-    nmore = s1r >= 0 && (s1r >> 30) != 0;
     const int sl = (tid & 1) ? s1 : s0;
     nfl = sl >= 0 ? (int)P.split_on[sl >> 1] : 0;
+    const int frow = field(rec, BR_ROW), fl0 = field(rec, BR_L0), fr0 = field(rec, BR_R0);
+    const int leaf = field(rec, BR_LEAF), rep = field(rec, BR_REP);
+    const int q = tid & 3;
+    const int rmr = q == 0 ? frow : q == 1 ? fl0 : fr0;
+    nrm = rmr >= 0 ? P.rowmax[rmr] : 0.0f;
+    const bool dts = !leaf && P.dts_in;
+    const size_t db = (size_t)rep * S;
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int i = own_pos_c<NT, CPT>(k);
       nst0[k] = (s0 >= 0 && okp[k]) ? P.staging[(size_t)s0 * S + i] : 0.0f;
       nst1[k] = (s1 >= 0 && okp[k]) ? P.staging[(size_t)s1 * S + i] : 0.0f;
+      nds[k] = (dts && okp[k]) ? P.dts_in[db + i] : KB_NEG_INF;
     }
   };
+  int crec = 0, nrec = 0;  // records of the next two rows (AHEAD, below the class level)
   if (AHEAD && (int)blockIdx.x < n_rows) {
-    fetch_rows(blockIdx.x);
-    if (!P.class_mode) fetch_rhs(rhs_rec(blockIdx.x));
+    if (P.class_mode) {
+      fetch_rows(row_of(blockIdx.x));
+    } else {
+      crec = load_rec(blockIdx.x);
+      fetch_rows(field(crec, BR_ROW));
+      fetch_row_data(crec);
+      if ((int)(blockIdx.x + gridDim.x) < n_rows) nrec = load_rec(blockIdx.x + gridDim.x);
+    }
   }
-  int rec_next = -1;
+  // the next row's fetches (AHEAD, below the class level)
+  auto advance = [&](int rr2) {
+    if (rr2 + (int)gridDim.x < n_rows) {
+      crec = nrec;
+      fetch_rows(field(crec, BR_ROW));
+      fetch_row_data(crec);
+      if (rr2 + 2 * (int)gridDim.x < n_rows) nrec = load_rec(rr2 + 2 * gridDim.x);
+    }
+  };
   if constexpr (CK_LDS) {
 #pragma unroll
     for (int j = 0; j < K_N; ++j) {
@@ -193,12 +219,20 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
 
   for (int rr = blockIdx.x; rr < n_rows; rr += gridDim.x) {
   __syncthreads();  // LDS of the previous row is no longer read
-  const int mb = P.class_mode ? P.cls_ptr[rr] : 0;
-  const int me = P.class_mode ? P.cls_ptr[rr + 1] : 1;
-  const int row = row_of(rr);
-  const int leaf_row = P.row_kind[row];
-  const size_t rb = (size_t)row * S;
-  const int sb = P.split_ptr[row], se = P.split_ptr[row + 1];
+  const int cm = P.class_mode;
+  const int rec = cm ? 0 : (AHEAD ? crec : load_rec(rr));
+  // every field read here, at a uniform point
+  const int f_row = field(rec, BR_ROW), f_leaf = field(rec, BR_LEAF), f_sb = field(rec, BR_SB);
+  const int f_se = field(rec, BR_SE), f_fam = field(rec, BR_FAM), f_s1 = field(rec, BR_S1);
+  const int f_lpos = field(rec, BR_LPOS), f_l0 = field(rec, BR_L0), f_r0 = field(rec, BR_R0);
+  const float f_lsp0 = __int_as_float(field(rec, BR_LSP0));
+  const int row = cm ? row_of(rr) : f_row;
+  const int leaf_row = cm ? P.row_kind[row] : f_leaf;
+  const int sb = cm ? P.split_ptr[row] : f_sb, se = cm ? P.split_ptr[row + 1] : f_se;
+  if (!AHEAD) {
+    fetch_rows(row);
+    if (!cm) fetch_row_data(rec);
+  }
 
   // ---- 1. Pi* of this row; adjoint = root seed or fixed-order gather of the
   // staging rows.  In class mode (identical rows without splits) each member's
@@ -210,7 +244,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
 #pragma unroll
   for (int k = 0; k < CPT; ++k) rhs[k] = 0.0f;
   bool any_active = false;
-  const int fam = P.class_mode ? -1 : P.root_index[row];
+  const int fam = cm ? -1 : f_fam;
   if (P.class_mode) {
     // the summed adjoint of the class's active members (bwd_gather0 / bwd_classsum0)
     any_active = P.cls_active[rr] != 0;
@@ -219,7 +253,6 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     for (int k = 0; k < CPT; ++k)
       if (okp[k]) rhs[k] = src[own_pos_c<NT, CPT>(k)];
   } else {
-    if (!AHEAD) fetch_rhs(rhs_rec(rr));
     if (__builtin_amdgcn_readlane(nfl, 0)) {
 #pragma unroll
       for (int k = 0; k < CPT; ++k) rhs[k] += nst0[k];
@@ -228,7 +261,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
 #pragma unroll
       for (int k = 0; k < CPT; ++k) rhs[k] += nst1[k];
     }
-    if (nmore) {
+    if (f_s1 >= 0 && (f_s1 >> 30) != 0) {  // more than two child sides
       const int gb = P.child_ptr[row] + 2, ge = P.child_ptr[row + 1];
       for (int i = gb; i < ge; ++i) {
         const int side = P.child_in[i];
@@ -251,17 +284,13 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     if ((tid & 63) == 0) wMk[tid >> 6] = wm;
   }
   float piv[CPT], pbv[CPT];
-  if (!AHEAD) fetch_rows(rr);
 #pragma unroll
   for (int j = 0; j < CPT; ++j)
     if (spre[j] >= 0) {
       R0[spre[j]] = nPi[j];
       R1[spre[j]] = nPb[j];
     }
-  if (AHEAD && rr + (int)gridDim.x < n_rows) {
-    fetch_rows(rr + gridDim.x);
-    if (!P.class_mode) rec_next = rhs_rec(rr + gridDim.x);
-  }
+  if (AHEAD && cm && rr + (int)gridDim.x < n_rows) fetch_rows(row_of(rr + gridDim.x));
   __syncthreads();
   lds_load_own<CPT>(R0, piv);
   lds_load_own<CPT>(R1, pbv);
@@ -301,8 +330,12 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     any_active = P.use_pruning ? (amax >= P.thr) : (amax > P.thr);
     if (tid == 0) P.mask[row] = any_active ? 1 : 0;
   }
+  // row data of this row that is read after the next row's fetches
+  const float rms = fsafe(cm ? P.rowmax[row] : lane_value(nrm, 0));
+  const float rml0 = cm ? 0.0f : lane_value(nrm, 1), rmr0 = cm ? 0.0f : lane_value(nrm, 2);
   if (!any_active) {
     for (int i = sb + tid; i < se; i += NT) P.split_on[i] = 0;
+    if (AHEAD && !cm) advance(rr);
     continue;
   }
   // The root rows' reductions above used the scratch that the path sums
@@ -316,10 +349,15 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
 #pragma unroll
   for (int k = 0; k < CPT; ++k) dts[k] = KB_NEG_INF;
   if (!leaf_row && P.dts_in) {
-    const float* src = P.dts_in + (size_t)P.rep_of[row] * S;
+    if (cm) {
+      const float* src = P.dts_in + (size_t)P.rep_of[row] * S;
 #pragma unroll
-    for (int k = 0; k < CPT; ++k)
-      if (okp[k]) dts[k] = src[own_pos_c<NT, CPT>(k)];
+      for (int k = 0; k < CPT; ++k)
+        if (okp[k]) dts[k] = src[own_pos_c<NT, CPT>(k)];
+    } else {
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) dts[k] = nds[k];
+    }
   } else if (!leaf_row) {
     float m[CPT], acc[CPT], kd[CPT], ks[CPT];
 #pragma unroll
@@ -367,7 +405,6 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   }
 
   // ---- 4. J^T coefficients at Pi* (precompute kernel, wave_backward.py:264-416)
-  const float rms = fsafe(P.rowmax[row]);
   // p' = 2^(col + Pi* - rowmax) and its root-path sums ps(i) = Pre(i) -
   // PostEx(tin(i) - i) (inclusive preorder scan, exclusive postorder scan;
   // the postorder slots of position i's left context end at tin(i) - i).
@@ -419,7 +456,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       ps[k] = (sp[k] + offp) - (R3[n] + __shfl(eq, n / SEG, 64));
     }
   }
-  const int lpos = leaf_row ? T.pre[P.leaf_state[row]] : -1;
+  const int lpos = cm ? (leaf_row ? T.pre[P.leaf_state[row]] : -1) : f_lpos;
   float q[6][CPT], pcoef[CPT];
   float kDL[CPT], kEb[CPT], kE[CPT], kS1[CPT], kS2[CPT], kLf[CPT];
   kc_own(K_DL, kDL);
@@ -481,7 +518,8 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   // into registers here, so their latency overlaps the Neumann loop.
   float pf[4][CPT];
   if (se > sb) {
-    const size_t l = (size_t)P.split_l[sb] * S, r = (size_t)P.split_r[sb] * S;
+    const size_t l = (size_t)(cm ? P.split_l[sb] : f_l0) * S;
+    const size_t r = (size_t)(cm ? P.split_r[sb] : f_r0) * S;
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
       const int s = tid + j * NT;
@@ -551,7 +589,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     }
   }
 
-  if (AHEAD && !P.class_mode && rr + (int)gridDim.x < n_rows) fetch_rhs(rec_next);
+  if (AHEAD && !cm) advance(rr);
 
   // ---- 6. self-loop column gradient and parameter buckets
   {
@@ -584,10 +622,11 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
 
   // ---- 7. split adjoints into the child rows (staging, preorder layout)
   for (int si = sb; si < se; ++si) {
-    const int lrow = P.split_l[si], rrow = P.split_r[si];
+    const bool s0 = si == sb && !cm;  // the first split's data came with the row
+    const int lrow = s0 ? f_l0 : P.split_l[si], rrow = s0 ? f_r0 : P.split_r[si];
     const size_t l = (size_t)lrow * S, r = (size_t)rrow * S;
-    const float lsp = P.split_lsp[si];
-    const float rml = P.rowmax[lrow], rmr = P.rowmax[rrow];
+    const float lsp = s0 ? f_lsp0 : P.split_lsp[si];
+    const float rml = s0 ? rml0 : P.rowmax[lrow], rmr = s0 ? rmr0 : P.rowmax[rrow];
     const float rmsl = fsafe(rml), rmsr = fsafe(rmr);
     __syncthreads();  // previous readers of R0..R3 are done
     if (si == sb) {

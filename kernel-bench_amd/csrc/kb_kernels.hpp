@@ -95,6 +95,17 @@ struct BwdConstArgs {
   float* Ebar_pre; float* E_pre; float* mt_pre; float* col_pre;
 };
 
+// The backward's record of a schedule slot (KB_BREC ints): the row's first
+// two child sides (-1: none; bit 30 of the second: more sides follow), the
+// row, its family root index (-1: not a root), leaf-row flag, split range,
+// class representative, the first split's children (-1: no split) and log
+// split probability (float bits), and the leaf's preorder position (-1: split
+// row).
+enum BrecField {
+  BR_S0, BR_S1, BR_ROW, BR_FAM, BR_LEAF, BR_SB, BR_SE, BR_REP, BR_L0, BR_R0, BR_LSP0, BR_LPOS,
+  KB_BREC = 16
+};
+
 struct BwdParams {
   TreeDev tr;
   PreDev pre;
@@ -111,7 +122,7 @@ struct BwdParams {
   const int* leaf_state; const int* root_index;
   const int* split_ptr; const int* split_l; const int* split_r; const float* split_lsp;
   const int* child_ptr; const int* child_in;
-  const int* bslot;           // [2 * C] schedule slot -> first two child sides (-1: none; bit 30: more follow)
+  const int* bslot;           // [KB_BREC * C] record of every schedule slot (BrecField)
   float* staging;             // [2 * n_splits, S]
   unsigned char* split_on;    // [n_splits]
   unsigned char* mask;        // [C]

@@ -195,17 +195,18 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       crec = load_rec(blockIdx.x);
       fetch_rows(field(crec, BR_ROW));
       fetch_row_data(crec);
-      if ((int)(blockIdx.x + gridDim.x) < n_rows) nrec = load_rec(blockIdx.x + gridDim.x);
+      nrec = load_rec(min((int)(blockIdx.x + gridDim.x), n_rows - 1));
     }
   }
-  // the next row's fetches (AHEAD, below the class level)
+  // the next row's fetches (AHEAD, below the class level).  Unconditional,
+  // with clamped slots (past the last row they fetch a row again, unused): a
+  // conditional load would join into a register copy that waits for every
+  // load just issued.
   auto advance = [&](int rr2) {
-    if (rr2 + (int)gridDim.x < n_rows) {
-      crec = nrec;
-      fetch_rows(field(crec, BR_ROW));
-      fetch_row_data(crec);
-      if (rr2 + 2 * (int)gridDim.x < n_rows) nrec = load_rec(rr2 + 2 * gridDim.x);
-    }
+    crec = nrec;
+    nrec = load_rec(min(rr2 + 2 * (int)gridDim.x, n_rows - 1));
+    fetch_rows(field(crec, BR_ROW));
+    fetch_row_data(crec);
   };
   if constexpr (CK_LDS) {
 #pragma unroll

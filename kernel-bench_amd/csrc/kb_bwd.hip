@@ -371,13 +371,15 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     for (int si = sb; si < se; ++si) {
       const size_t l = (size_t)P.split_l[si] * S, r = (size_t)P.split_r[si] * S;
       const float lsp = P.split_lsp[si];
-      for (int s = tid; s < S; s += NT) {
-        const int i = T.pre[s];
-        R0[i] = P.pi[l + s];
-        R1[i] = P.pi[r + s];
-        R2[i] = P.pibar[l + s];
-        R3[i] = P.pibar[r + s];
-      }
+#pragma unroll
+      for (int j = 0; j < CPT; ++j)
+        if (spre[j] >= 0) {
+          const int s = tid + j * NT;
+          R0[spre[j]] = P.pi[l + s];
+          R1[spre[j]] = P.pi[r + s];
+          R2[spre[j]] = P.pibar[l + s];
+          R3[spre[j]] = P.pibar[r + s];
+        }
       __syncthreads();
 #pragma unroll
       for (int k = 0; k < CPT; ++k) {
@@ -632,24 +634,23 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     __syncthreads();  // previous readers of R0..R3 are done
     if (si == sb) {
 #pragma unroll
-      for (int j = 0; j < CPT; ++j) {
-        const int s = tid + j * NT;
-        if (s < S) {
-          const int i = T.pre[s];
-          R0[i] = pf[0][j];
-          R1[i] = pf[1][j];
-          R2[i] = pf[2][j];
-          R3[i] = pf[3][j];
+      for (int j = 0; j < CPT; ++j)
+        if (spre[j] >= 0) {
+          R0[spre[j]] = pf[0][j];
+          R1[spre[j]] = pf[1][j];
+          R2[spre[j]] = pf[2][j];
+          R3[spre[j]] = pf[3][j];
         }
-      }
     } else {
-      for (int s = tid; s < S; s += NT) {
-        const int i = T.pre[s];
-        R0[i] = P.pi[l + s];
-        R1[i] = P.pi[r + s];
-        R2[i] = P.pibar[l + s];
-        R3[i] = P.pibar[r + s];
-      }
+#pragma unroll
+      for (int j = 0; j < CPT; ++j)
+        if (spre[j] >= 0) {
+          const int s = tid + j * NT;
+          R0[spre[j]] = P.pi[l + s];
+          R1[spre[j]] = P.pi[r + s];
+          R2[spre[j]] = P.pibar[l + s];
+          R3[spre[j]] = P.pibar[r + s];
+        }
     }
     __syncthreads();
     float vd0[CPT], vd1[CPT], vd2[CPT], vd3[CPT], vd4[CPT], udl[CPT], udr[CPT], ppl[CPT], ppr[CPT];

@@ -419,7 +419,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int i = own_pos_c<NT, CPT>(k);
-    pp[k] = okp[k] ? exp2f((WEIGHTED ? P.col[i] : 0.0f) + piv[k] - rms) : 0.0f;
+    pp[k] = okp[k] ? exp2_hw((WEIGHTED ? P.col[i] : 0.0f) + piv[k] - rms) : 0.0f;
     ta += pp[k];
     sp[k] = ta;
   }
@@ -476,7 +476,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     pcoef[k] = 0.0f;
     if (okp[k]) {
       const float denom = rowsum - ps[k];
-      const float inv_denom = denom > 0.0f ? 1.0f / denom : 0.0f;
+      const float inv_denom = denom > 0.0f ? rcp_hw(denom) : 0.0f;
       const bool h1 = O.c1p[k] != ZERO, h2 = O.c2p[k] != ZERO;
       const float t0 = kDL[k] + piv[k];
       const float t1 = piv[k] + kEb[k];
@@ -486,13 +486,13 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       const float t5 = i == lpos ? kLf[k] : KB_NEG_INF;
       const float m = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, t5));
       const float msf = fsafe(m);
-      float e[6] = {exp2f(t0 - msf), exp2f(t1 - msf), exp2f(t2 - msf), exp2f(t3 - msf), exp2f(t4 - msf),
-                    exp2f(t5 - msf)};
+      float e[6] = {exp2_hw(t0 - msf), exp2_hw(t1 - msf), exp2_hw(t2 - msf), exp2_hw(t3 - msf),
+                    exp2_hw(t4 - msf), exp2_hw(t5 - msf)};
       const float sum = e[0] + e[1] + e[2] + e[3] + e[4] + e[5];
       // q_j = w_L e_j / sum with the split mixing weight
       // w_L = 2^dl / (2^dl + 2^dts), 2^dl = sum 2^m:  q_j = e_j / (sum + 2^(dts - m))
-      const float den = sum + (leaf_row ? 0.0f : exp2f(dts[k] - msf));
-      const float inv = sum > 0.0f ? 1.0f / den : 0.0f;
+      const float den = sum + (leaf_row ? 0.0f : exp2_hw(dts[k] - msf));
+      const float inv = sum > 0.0f ? rcp_hw(den) : 0.0f;
 #pragma unroll
       for (int j = 0; j < 6; ++j) q[j][k] = e[j] * inv;
       pcoef[k] = q[2][k] * inv_denom;
@@ -593,6 +593,11 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   }
 
   if (AHEAD && !cm) advance(rr);
+  // mt at the own positions for the split adjoints (its load overlaps the
+  // self-loop gradient and the child staging)
+  float kmt[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) kmt[k] = okp[k] ? P.mt[own_pos_c<NT, CPT>(k)] : 0.0f;
 
   // ---- 6. self-loop column gradient and parameter buckets
   {
@@ -673,19 +678,19 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
         const float d = kd[k], sp = ks[k];
         const bool pv = piv[k] != KB_NEG_INF;
         const float base = pv ? lsp - piv[k] : 0.0f;
-        vd0[k] = pv ? v[k] * exp2f(base + (d + pl + pr)) : 0.0f;
-        vd1[k] = pv ? v[k] * exp2f(base + (pl + br)) : 0.0f;
-        vd2[k] = pv ? v[k] * exp2f(base + (pr + bl)) : 0.0f;
-        vd3[k] = pv ? v[k] * exp2f(base + (sp + l1 + r2)) : 0.0f;
-        vd4[k] = pv ? v[k] * exp2f(base + (sp + r1 + l2)) : 0.0f;
-        const float mts = P.mt[i];
-        const float inv_l = bl != KB_NEG_INF ? exp2f(rml + mts - bl) : 0.0f;
-        const float inv_r = br != KB_NEG_INF ? exp2f(rmr + mts - br) : 0.0f;
+        vd0[k] = pv ? v[k] * exp2_hw(base + (d + pl + pr)) : 0.0f;
+        vd1[k] = pv ? v[k] * exp2_hw(base + (pl + br)) : 0.0f;
+        vd2[k] = pv ? v[k] * exp2_hw(base + (pr + bl)) : 0.0f;
+        vd3[k] = pv ? v[k] * exp2_hw(base + (sp + l1 + r2)) : 0.0f;
+        vd4[k] = pv ? v[k] * exp2_hw(base + (sp + r1 + l2)) : 0.0f;
+        const float mts = kmt[k];
+        const float inv_l = bl != KB_NEG_INF ? exp2_hw(rml + mts - bl) : 0.0f;
+        const float inv_r = br != KB_NEG_INF ? exp2_hw(rmr + mts - br) : 0.0f;
         udl[k] = vd2[k] * inv_l;
         udr[k] = vd1[k] * inv_r;
         const float cw = WEIGHTED ? P.col[i] : 0.0f;
-        ppl[k] = exp2f(cw + pl - rmsl);
-        ppr[k] = exp2f(cw + pr - rmsr);
+        ppl[k] = exp2_hw(cw + pl - rmsl);
+        ppr[k] = exp2_hw(cw + pr - rmsr);
       }
     }
     __syncthreads();  // staged children fully read

@@ -34,6 +34,14 @@ struct TreeDev {
 };
 
 __device__ __forceinline__ float fsafe(float m) { return m == KB_NEG_INF ? 0.0f : m; }
+
+// 2^x by the hardware instruction: the same as exp2f for x >= -126 and 0 below
+// (where exp2f returns a denormal).  For terms whose size next to the others
+// of their sum or product makes such values negligible.
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// 1/x by the hardware reciprocal (1 ulp) instead of a correctly rounded division.
+__device__ __forceinline__ float rcp_hw(float x) { return __builtin_amdgcn_rcpf(x); }
 __device__ __forceinline__ double dsafe(double m) { return m == -__builtin_inf() ? 0.0 : m; }
 
 template <typename T>

@@ -40,6 +40,10 @@ __device__ __forceinline__ float fsafe(float m) { return m == KB_NEG_INF ? 0.0f 
 // of their sum or product makes such values negligible.
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// log2 x by the hardware instruction: the same as log2f for x >= 2^-126 and
+// for 0; for the sums of max-shifted terms, which are 0 or at least 1.
+__device__ __forceinline__ float log2_hw(float x) { return __builtin_amdgcn_logf(x); }
+
 // 1/x by the hardware reciprocal (1 ulp) instead of a correctly rounded division.
 __device__ __forceinline__ float rcp_hw(float x) { return __builtin_amdgcn_rcpf(x); }
 __device__ __forceinline__ double dsafe(double m) { return m == -__builtin_inf() ? 0.0 : m; }
@@ -212,8 +216,8 @@ __device__ __forceinline__ float lse2_5(float t0, float t1, float t2, float t3, 
 __device__ __forceinline__ void lse_merge(float& m, float& acc, float m2, float s2) {
   float nm = fmaxf(m, m2);
   float nms = fsafe(nm);
-  float a = (m == KB_NEG_INF) ? 0.0f : acc * exp2f(m - nms);
-  float b = (m2 == KB_NEG_INF) ? 0.0f : s2 * exp2f(m2 - nms);
+  float a = (m == KB_NEG_INF) ? 0.0f : acc * exp2_hw(m - nms);
+  float b = (m2 == KB_NEG_INF) ? 0.0f : s2 * exp2_hw(m2 - nms);
   acc = a + b;
   m = nm;
 }

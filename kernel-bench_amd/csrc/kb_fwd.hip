@@ -92,9 +92,9 @@ __global__ __launch_bounds__(NT, (NT == 1024 && CPT == 2) ? 8 : 1) void fwd_row_
         const float t5 = hit ? P.pS[ci] : KB_NEG_INF;
         const float m = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, t5));
         const float ms = fsafe(m);
-        const float sum = exp2f(t0 - ms) + exp2f(t1 - ms) + exp2f(t2 - ms) + exp2f(t3 - ms) + exp2f(t4 - ms) +
-                          exp2f(t5 - ms);
-        v[k] = log2f(sum) + m;
+        const float sum = exp2_hw(t0 - ms) + exp2_hw(t1 - ms) + exp2_hw(t2 - ms) + exp2_hw(t3 - ms) +
+                          exp2_hw(t4 - ms) + exp2_hw(t5 - ms);
+        v[k] = log2_hw(sum) + m;
       }
     }
   } else {
@@ -143,14 +143,15 @@ __global__ __launch_bounds__(NT, (NT == 1024 && CPT == 2) ? 8 : 1) void fwd_row_
           const float t4 = lsp + sp + r1 + l2;
           const float m5 = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), t4);
           const float ms = fsafe(m5);
-          const float s5 = exp2f(t0 - ms) + exp2f(t1 - ms) + exp2f(t2 - ms) + exp2f(t3 - ms) + exp2f(t4 - ms);
+          const float s5 =
+              exp2_hw(t0 - ms) + exp2_hw(t1 - ms) + exp2_hw(t2 - ms) + exp2_hw(t3 - ms) + exp2_hw(t4 - ms);
           lse_merge(m[k], acc[k], m5, s5);
         }
       }
     }
     __syncthreads();  // the staging buffers become the sweep buffers
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) v[k] = log2f(acc[k]) + m[k];
+    for (int k = 0; k < CPT; ++k) v[k] = log2_hw(acc[k]) + m[k];
     if (P.dts_out) {  // the backward reuses the split term at Pi*
       float* dst = P.dts_out + (size_t)row * S;
 #pragma unroll
@@ -337,9 +338,9 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
         const float t5 = hit ? P.pS[ci] : KB_NEG_INF;
         const float m = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, t5));
         const float ms = fsafe(m);
-        const float sum = exp2f(t0 - ms) + exp2f(t1 - ms) + exp2f(t2 - ms) + exp2f(t3 - ms) + exp2f(t4 - ms) +
-                          exp2f(t5 - ms);
-        v[k] = log2f(sum) + m;
+        const float sum = exp2_hw(t0 - ms) + exp2_hw(t1 - ms) + exp2_hw(t2 - ms) + exp2_hw(t3 - ms) +
+                          exp2_hw(t4 - ms) + exp2_hw(t5 - ms);
+        v[k] = log2_hw(sum) + m;
       }
     }
   } else {
@@ -397,14 +398,15 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
           const float t4 = lsp + sp + r1 + l2;
           const float m5 = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), t4);
           const float ms = fsafe(m5);
-          const float s5 = exp2f(t0 - ms) + exp2f(t1 - ms) + exp2f(t2 - ms) + exp2f(t3 - ms) + exp2f(t4 - ms);
+          const float s5 =
+              exp2_hw(t0 - ms) + exp2_hw(t1 - ms) + exp2_hw(t2 - ms) + exp2_hw(t3 - ms) + exp2_hw(t4 - ms);
           lse_merge(m[k], acc[k], m5, s5);
         }
       }
     }
     __syncthreads();  // the staging buffers become the sweep buffers
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) v[k] = log2f(acc[k]) + m[k];
+    for (int k = 0; k < CPT; ++k) v[k] = log2_hw(acc[k]) + m[k];
     if (P.dts_out) {  // the backward reuses the split term at Pi*
       float* dst = P.dts_out + (size_t)row * S;
 #pragma unroll

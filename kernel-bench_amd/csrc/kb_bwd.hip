@@ -552,10 +552,9 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   int wend[CPT];
 #pragma unroll
   for (int k = 0; k < CPT; ++k) wend[k] = endm1[k] < ZERO ? endm1[k] / (64 * CPT) : 0;
-  for (int n = 0; n < P.n_terms; ++n) {
-    float* Tb = (n & 1) ? R1 : R0;
-    float* Lb = (n & 1) ? R3 : R2;
-    float* wt = (n & 1) ? wB : wA;
+  // term n uses the buffers of its parity; the loop runs the terms in pairs
+  // so that every LDS address is a register plus a constant
+  auto neumann_term = [&](float* Tb, float* Lb, float* wt) {
     float sc[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) sc[k] = term[k] * pcoef[k] + (k > 0 ? sc[k - 1] : 0.0f);
@@ -590,6 +589,14 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       term[k] = nt;
       v[k] += nt;
     }
+  };
+  {
+    int n = 0;
+    for (; n + 2 <= P.n_terms; n += 2) {
+      neumann_term(R0, R2, wA);
+      neumann_term(R1, R3, wB);
+    }
+    if (n < P.n_terms) neumann_term(R0, R2, wA);
   }
 
   if (AHEAD && !cm) advance(rr);

@@ -79,9 +79,9 @@ struct kb_plan {
   int* d_fsched = nullptr;             // representatives in level order
   int* d_fsplit_l = nullptr;           // split children remapped to representatives
   int* d_fsplit_r = nullptr;
-  int n_copy = 0;
-  int* d_copy_dst = nullptr;
-  int* d_copy_src = nullptr;
+  int n_copy = 0;                       // rows identical to an earlier representative
+  int* d_dup_ptr = nullptr;             // [forward slots + 1] -> d_dup_rows
+  int* d_dup_rows = nullptr;
   int n_cls0 = 0;                      // classes of level-0 rows
   int n_chunks0 = 0;                   // level-0 classes cut into chunks of <= KB_CHUNK0 members
   int* d_ck_ptr = nullptr;
@@ -510,8 +510,18 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
   rc |= upload(&p->d_fsched, fsched);
   rc |= upload(&p->d_fsplit_l, fsl);
   rc |= upload(&p->d_fsplit_r, fsr);
-  rc |= upload(&p->d_copy_dst, copy_dst);
-  rc |= upload(&p->d_copy_src, copy_src);
+  {
+    // per forward slot (representative), its identical rows
+    std::vector<int> slot_of(C, -1);
+    for (size_t j = 0; j < fsched.size(); ++j) slot_of[fsched[j]] = (int)j;
+    std::vector<int> dptr(fsched.size() + 1, 0), drows(copy_dst.size());
+    for (size_t k = 0; k < copy_dst.size(); ++k) dptr[slot_of[copy_src[k]] + 1]++;
+    for (size_t j = 0; j < fsched.size(); ++j) dptr[j + 1] += dptr[j];
+    std::vector<int> dfill(dptr.begin(), dptr.end() - 1);
+    for (size_t k = 0; k < copy_dst.size(); ++k) drows[dfill[slot_of[copy_src[k]]]++] = copy_dst[k];
+    rc |= upload(&p->d_dup_ptr, dptr);
+    rc |= upload(&p->d_dup_rows, drows);
+  }
   rc |= upload(&p->d_cls_ptr, cls_ptr);
   rc |= upload(&p->d_ck_ptr, ck_ptr);
   rc |= upload(&p->d_cls_ck_ptr, cls_ck_ptr);
@@ -604,8 +614,8 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
                     (void*)p->lin_emc, (void*)p->lin_k1, (void*)p->lin_k2, (void*)p->E64, (void*)p->n_e_iter,
                     (void*)p->loss_terms, (void*)p->loss64, (void*)p->d_root_index,
                     (void*)p->d_sched_rows, (void*)p->d_row_kind, (void*)p->d_pre, (void*)p->d_pcol,
-                    (void*)p->d_fsched, (void*)p->d_fsplit_l, (void*)p->d_fsplit_r, (void*)p->d_copy_dst,
-                    (void*)p->d_copy_src, (void*)p->d_cls_ptr, (void*)p->d_cls_rows, (void*)p->d_ck_ptr, (void*)p->d_cls_ck_ptr, (void*)p->d_rep_of, (void*)p->d_m_side_ptr, (void*)p->d_m_side, (void*)p->d_m_root,
+                    (void*)p->d_fsched, (void*)p->d_fsplit_l, (void*)p->d_fsplit_r, (void*)p->d_dup_ptr,
+                    (void*)p->d_dup_rows, (void*)p->d_cls_ptr, (void*)p->d_cls_rows, (void*)p->d_ck_ptr, (void*)p->d_cls_ck_ptr, (void*)p->d_rep_of, (void*)p->d_m_side_ptr, (void*)p->d_m_side, (void*)p->d_m_root,
                     (void*)p->d_dts,
                     (void*)p->d_c1pos, (void*)p->d_c2pos, (void*)p->d_ppos, (void*)p->d_pflag, (void*)p->d_endpos,
                     (void*)p->d_tin, (void*)p->d_euler, (void*)p->d_post, (void*)p->d_euler_col, (void*)p->d_tin_col, (void*)p->c_Ebar, (void*)p->c_E, (void*)p->c_mt,
@@ -722,6 +732,8 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
   F.rowmax = io->pibar_row_max;
   F.sched_rows = p->d_fsched;
   F.row_kind = p->d_row_kind;
+  F.dup_ptr = p->d_dup_ptr;
+  F.dup_rows = p->d_dup_rows;
   F.dts_out = p->d_dts;
   p->fwd_token += 1;
   p->fwd_pi = io->pi;
@@ -731,7 +743,6 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
     kb::launch_fwd_wave(F, p->f_level_ptr[d], p->f_level_ptr[d + 1] - p->f_level_ptr[d], st);
     if (p->prof) KB_HIP(hipEventRecord(p->ev_fwd[2 * d + 1], st));
   }
-  kb::launch_copy_rows(io->pi, io->pibar, io->pibar_row_max, p->d_copy_dst, p->d_copy_src, p->n_copy, S, st);
   KB_HIP(hipGetLastError());
   kb::launch_loss(io->pi, p->d_roots, io->E, S, p->n_fam, p->loss_terms, p->loss64, io->loss, st);
   KB_HIP(hipGetLastError());

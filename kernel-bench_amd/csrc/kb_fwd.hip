@@ -238,6 +238,17 @@ __global__ __launch_bounds__(NT, (NT == 1024 && CPT == 2) ? 8 : 1) void fwd_row_
   store_row_pre<NT, CPT>(T, piv, Sc, P.pi + rb);
   store_row_pre<NT, CPT>(T, pbv, Sc + MAXS, P.pibar + rb);
   if (tid == 0) P.rowmax[row] = rmax;
+  // the rows identical to this one get the same outputs (still staged in Sc)
+  for (int d = P.dup_ptr[first + blockIdx.x]; d < P.dup_ptr[first + blockIdx.x + 1]; ++d) {
+    const int r2 = P.dup_rows[d];
+    const size_t b2 = (size_t)r2 * S;
+    for (int s = tid; s < S; s += NT) {
+      const int i = T.pre[s];
+      P.pi[b2 + s] = Sc[i];
+      P.pibar[b2 + s] = Sc[MAXS + i];
+    }
+    if (tid == 0) P.rowmax[r2] = rmax;
+  }
 }
 
 // Minimum waves per SIMD (the second launch-bounds argument): 6 keeps three
@@ -527,16 +538,34 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
   lds_store_own<CPT>(Lb[3], pbv);
   const float rmax = block_max1<NT>(lmax, wM);  // also publishes the staging
   const size_t rb = (size_t)row * S;
+  float oa[CPT], ob[CPT];
 #pragma unroll
   for (int j = 0; j < CPT; ++j) {
     const int sj = tid + j * NT;
+    oa[j] = ob[j] = 0.0f;
     if (sj < S) {
       const int i = T.pre[sj];  // reloaded: keeps the table out of registers during the sweeps
-      P.pi[rb + sj] = Lb[2][i];
-      P.pibar[rb + sj] = Lb[3][i];
+      oa[j] = Lb[2][i];
+      ob[j] = Lb[3][i];
+      P.pi[rb + sj] = oa[j];
+      P.pibar[rb + sj] = ob[j];
     }
   }
   if (tid == 0) P.rowmax[row] = rmax;
+  // the rows identical to this one get the same outputs
+  for (int d = P.dup_ptr[first + blockIdx.x]; d < P.dup_ptr[first + blockIdx.x + 1]; ++d) {
+    const int r2 = P.dup_rows[d];
+    const size_t b2 = (size_t)r2 * S;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int sj = tid + j * NT;
+      if (sj < S) {
+        P.pi[b2 + sj] = oa[j];
+        P.pibar[b2 + sj] = ob[j];
+      }
+    }
+    if (tid == 0) P.rowmax[r2] = rmax;
+  }
 }
 
 #define KB_FWD_CASE(NT_, CPT_, KERNEL_)                                                                   \
@@ -548,35 +577,6 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
     return;                                                                                               \
   }
 
-// One workgroup per copied row (rows of a class are identical).
-__global__ __launch_bounds__(256) void copy_rows_kernel(float* pi, float* pibar, float* rowmax, const int* dst,
-                                                        const int* src, int S) {
-  const size_t d = (size_t)dst[blockIdx.x] * S, s = (size_t)src[blockIdx.x] * S;
-  for (int j0 = threadIdx.x; j0 < S; j0 += 4 * 256) {  // 8 independent loads in flight per thread
-    float a[4], b[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int j = j0 + u * 256;
-      a[u] = j < S ? pi[s + j] : 0.0f;
-      b[u] = j < S ? pibar[s + j] : 0.0f;
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int j = j0 + u * 256;
-      if (j < S) {
-        pi[d + j] = a[u];
-        pibar[d + j] = b[u];
-      }
-    }
-  }
-  if (threadIdx.x == 0) rowmax[dst[blockIdx.x]] = rowmax[src[blockIdx.x]];
-}
-
-void launch_copy_rows(float* pi, float* pibar, float* rowmax, const int* dst, const int* src, int n, int S,
-                      hipStream_t st) {
-  if (n <= 0) return;
-  hipLaunchKernelGGL(copy_rows_kernel, dim3(n), dim3(256), 0, st, pi, pibar, rowmax, dst, src, S);
-}
 
 void launch_fwd_wave(const FwdParams& P, int first, int W, hipStream_t st) {
   if (W <= 0) return;

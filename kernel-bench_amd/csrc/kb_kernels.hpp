@@ -70,14 +70,14 @@ struct FwdParams {
   const int* split_l; const int* split_r; const float* split_lsp;
   const int* sched_rows;      // rows in dependency-level order
   const int* row_kind;        // 1: leaf row, 0: split row
+  const int* dup_ptr;         // [slots + 1] rows identical to the row of each slot ...
+  const int* dup_rows;        // ... which receive the same outputs
   // outputs
   float* pi; float* pibar; float* rowmax;
   float* dts_out;             // [C, S] preorder split term of every computed split row
 };
 
 // Pi / Pibar / row-max rows src[i] -> dst[i], i < n.
-void launch_copy_rows(float* pi, float* pibar, float* rowmax, const int* dst, const int* src, int n, int S,
-                      hipStream_t st);
 // Launch the rows sched_rows[first .. first + n).
 void launch_fwd_wave(const FwdParams& P, int first, int n, hipStream_t st);
 

@@ -860,74 +860,102 @@ __global__ __launch_bounds__(256) void bwd_classsum0_kernel(BwdParams P) {
 // without the [members, S] round trip through HBM.
 __global__ __launch_bounds__(256) void bwd_chunk0_kernel(BwdParams P) {
   __shared__ float red[4];
+  __shared__ float wmax[KB_CHUNK0][4];
   const PreDev& T = P.pre;
   const int S = P.S;
+  const int tid = threadIdx.x;
   const int k = blockIdx.x;
   const int mb = P.ck_ptr[k], me = P.ck_ptr[k + 1];
-  float acc[G0_E];
+  // Every member's adjoint row stays in registers: all members' staging loads
+  // are issued before the first reduction, and one barrier gives every
+  // member's mask.
+  float r[KB_CHUNK0][G0_E];
+  bool has_root = false;
 #pragma unroll
-  for (int e = 0; e < G0_E; ++e) acc[e] = 0.0f;
-  int any = 0;
-  for (int mi = mb; mi < me; ++mi) {
-    const int row = P.cls_rows[mi];
-    float r[G0_E];
+  for (int m = 0; m < KB_CHUNK0; ++m) {
 #pragma unroll
-    for (int e = 0; e < G0_E; ++e) r[e] = 0.0f;
+    for (int e = 0; e < G0_E; ++e) r[m][e] = 0.0f;
+    const int mi = mb + m;
+    if (mi >= me) continue;
     if (P.m_root[mi] >= 0) {
-      // root seed: -2^(Pi - logsumexp2(Pi)) (logspace.py:11-16, _implicit_grad.py:21-25)
-      const float* pr = P.pi + (size_t)row * S;
+      has_root = true;
+      continue;
+    }
+    for (int j = P.m_side_ptr[mi]; j < P.m_side_ptr[mi + 1]; ++j) {
+      const int side = P.m_side[j];
+      const bool on = P.split_on[side >> 1] != 0;  // uniform across the workgroup
+      const float* st = P.staging + (size_t)side * S;
+#pragma unroll
+      for (int e = 0; e < G0_E; ++e) {
+        const int i = e * 256 + tid;
+        const float x = i < S ? st[i] : 0.0f;
+        r[m][e] = on ? r[m][e] + x : r[m][e];
+      }
+    }
+  }
+  if (has_root) {
+    // root seeds -2^(Pi - logsumexp2(Pi)) (logspace.py:11-16, _implicit_grad.py:21-25)
+#pragma unroll
+    for (int m = 0; m < KB_CHUNK0; ++m) {
+      const int mi = mb + m;
+      if (mi >= me || P.m_root[mi] < 0) continue;
+      const float* pr = P.pi + (size_t)P.cls_rows[mi] * S;
       float lm = KB_NEG_INF;
-      for (int j = threadIdx.x; j < S; j += 256) lm = fmaxf(lm, pr[j]);
+      for (int j = tid; j < S; j += 256) lm = fmaxf(lm, pr[j]);
       const float rmax = block_max<256>(lm, red);
       const float rms = fsafe(rmax);
       float ls = 0.0f;
-      for (int j = threadIdx.x; j < S; j += 256) ls += exp2f(pr[j] - rms);
+      for (int j = tid; j < S; j += 256) ls += exp2f(pr[j] - rms);
       const float tot = block_sum<256>(ls, red);
       const float lses = fsafe((tot > 0.0f ? log2f(tot) : KB_NEG_INF) + rmax);
 #pragma unroll
       for (int e = 0; e < G0_E; ++e) {
-        const int i = e * 256 + threadIdx.x;
+        const int i = e * 256 + tid;
         if (i < S) {
           const float x = pr[T.col[i]];
-          r[e] = x == KB_NEG_INF ? 0.0f : -exp2f(x - lses);
-        }
-      }
-    } else {
-      const int sb = P.m_side_ptr[mi], se = P.m_side_ptr[mi + 1];
-      for (int j = sb; j < se; ++j) {
-        const int side = P.m_side[j];
-        if (!P.split_on[side >> 1]) continue;  // uniform across the workgroup
-        const float* st = P.staging + (size_t)side * S;
-#pragma unroll
-        for (int e = 0; e < G0_E; ++e) {
-          const int i = e * 256 + threadIdx.x;
-          if (i < S) r[e] += st[i];
+          r[m][e] = x == KB_NEG_INF ? 0.0f : -exp2f(x - lses);
         }
       }
     }
+  }
+  // the members' active masks (the reference's rule), one barrier
+#pragma unroll
+  for (int m = 0; m < KB_CHUNK0; ++m) {
     float am = 0.0f;
 #pragma unroll
     for (int e = 0; e < G0_E; ++e)
-      if (e * 256 + (int)threadIdx.x < S) am = fmaxf(am, fabsf(r[e]));
-    const float amax = block_max<256>(am, red);
+      if (e * 256 + tid < S) am = fmaxf(am, fabsf(r[m][e]));
+    const float wm = wave_reduce_max(am);
+    if ((tid & 63) == 0) wmax[m][tid >> 6] = wm;
+  }
+  __syncthreads();
+  float acc[G0_E];
+#pragma unroll
+  for (int e = 0; e < G0_E; ++e) acc[e] = 0.0f;
+  int any = 0;
+#pragma unroll
+  for (int m = 0; m < KB_CHUNK0; ++m) {
+    const int mi = mb + m;
+    if (mi >= me) continue;
+    const float amax = fmaxf(fmaxf(wmax[m][0], wmax[m][1]), fmaxf(wmax[m][2], wmax[m][3]));
     const bool on = P.use_pruning ? (amax >= P.thr) : (amax > P.thr);
-    if (threadIdx.x == 0) {
-      P.mask[row] = on ? 1 : 0;
+    if (tid == 0) {
+      P.mask[P.cls_rows[mi]] = on ? 1 : 0;
       P.m_mask[mi] = on ? 1 : 0;
     }
     if (on) {
       any = 1;
 #pragma unroll
-      for (int e = 0; e < G0_E; ++e) acc[e] += r[e];
+      for (int e = 0; e < G0_E; ++e) acc[e] += r[m][e];
     }
   }
   float* out = P.rhs0 + (size_t)k * S;
 #pragma unroll
   for (int e = 0; e < G0_E; ++e) {
-    const int i = e * 256 + threadIdx.x;
+    const int i = e * 256 + tid;
     if (i < S) out[i] = acc[e];
   }
-  if (threadIdx.x == 0) P.ck_any[k] = any ? 1 : 0;
+  if (tid == 0) P.ck_any[k] = any ? 1 : 0;
 }
 
 __global__ __launch_bounds__(256) void bwd_chunksum0_kernel(BwdParams P) {

@@ -349,6 +349,9 @@ class ProblemConfig:
     seed: int = 0
     max_wave_rows: int = MAX_WAVE_ROWS
     solver_options: dict = field(default_factory=dict)
+    # families of one gene leaf (their root row is a leaf row), appended after
+    # the simulated ones from a separate random stream
+    single_leaf_families: int = 0
 
 
 def build_problem(cfg: ProblemConfig) -> dict:
@@ -390,6 +393,14 @@ def build_problem(cfg: ProblemConfig) -> dict:
         for _ in range(cfg.n_nni):
             trees.append(_nni(k, kids, rng))
         families.append((species, trees))
+
+    if cfg.single_leaf_families > 0:
+        rng1 = np.random.default_rng(cfg.seed + 7919)
+        n_sp = cfg.n_species_leaves
+        leaf_species = np.nonzero(tree.n_leaves_below == 1)[0] if hasattr(tree, "n_leaves_below") else np.arange(n_sp)
+        for _ in range(cfg.single_leaf_families):
+            sp = int(leaf_species[rng1.integers(leaf_species.size)])
+            families.append((np.array([sp], dtype=np.int64), [np.zeros((0, 2), dtype=np.int64)] * (1 + cfg.n_nni)))
 
     # clades / splits per family
     fam_rows = []   # per family: list of (size, mask) sorted

@@ -204,3 +204,49 @@ def test_fused_large_trees_match_oracle(leaves, families, statewise, weighted, s
     assert rel <= 1e-5
     assert ok and (ma <= 2e-4 or mr <= 1e-5)
     assert rt <= 1e-4 and rc <= 1e-4
+
+
+@pytest.mark.parametrize("statewise", [False, True])
+def test_fused_single_leaf_families_match_oracle(statewise):
+    """Families of one gene leaf: their root row is a leaf row, so level 0 holds root members (the root
+    seed in the level-0 chunk path; two of them share a species, so one class holds two roots)."""
+    import kbench_oracle as O
+    from kbench import synth
+    from kbench.fused import FusedSolver, problem_to_captured
+    from kbench.runtime import make_static
+
+    print(f"[fused-single-leaf] statewise={statewise}", flush=True)
+    cfg = synth.ProblemConfig(32, 6, n_nni=1, family_leaves_median=4.0, family_leaves_sigma=0.5,
+                              family_leaves_max=10, statewise=statewise, seed=23, single_leaf_families=3)
+    p = synth.build_problem(cfg)
+    roots = np.asarray(p["static"]["wave_layout"]["root_row_ids"])
+    w0 = p["static"]["wave_layout"]["wave_metas"][0]
+    assert np.sum(roots < int(w0["start"]) + int(w0["W"])) == 3  # three roots among the leaf rows
+    cap = problem_to_captured(p)
+    static = make_static(cap, "cuda")
+    solver = FusedSolver(static, static.solver_options)
+    theta = cap["inputs"]["theta"].cuda()
+    cw = cap["inputs"]["col_weights"].cuda()
+    loss, saved = solver.run_forward(theta, cw)
+    gt, gc, info = solver.run_backward(theta, cw, saved, return_info=True)
+    torch.cuda.synchronize()
+
+    prob = O.Problem.from_dict(p)
+    th64 = np.asarray(p["inputs"]["theta"], dtype=np.float32).astype(np.float64)
+    cw64 = np.asarray(p["inputs"]["col_weights"], dtype=np.float32).astype(np.float64)
+    ref_loss, ref = O.forward(prob, th64, cw64)
+    ref_gt, ref_gc, _info, extra = O.backward(prob, th64, cw64, ref, collect=True)
+    rel = abs(float(loss) - ref_loss) / abs(ref_loss)
+    ok, ma, mr = kbtest.compare_inf_safe(saved["pi_wave"].cpu().numpy(), ref["pi_wave"])
+    rt = kbtest.norm_rel(gt.cpu().numpy(), ref_gt)
+    rc = kbtest.norm_rel(gc.cpu().numpy(), ref_gc)
+    print(f"  S={prob.S} C={prob.C} loss rel={rel:.3e} pi ok={ok} max_abs={ma:.3e} "
+          f"grad_theta={rt:.3e} grad_col={rc:.3e}")
+    assert rel <= 1e-5
+    assert ok and (ma <= 2e-4 or mr <= 1e-5)
+    assert rt <= 1e-4 and rc <= 1e-4
+    mask = info["active_mask"].cpu().numpy().astype(bool)
+    ref_mask = np.zeros_like(mask)
+    for ws, act in extra["masks"]:
+        ref_mask[ws:ws + len(act)] = act
+    assert np.array_equal(mask, ref_mask)

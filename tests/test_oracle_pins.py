@@ -394,3 +394,31 @@ def test_converged_gradient_matches_finite_differences(weighted):
             cm[j] -= h
             fdc[j] = (O.forward(prob, theta, cp)[0] - O.forward(prob, theta, cm)[0]) / (2 * h)
         assert np.abs(gc - fdc).max() <= 1e-6 * np.abs(fdc).max()
+
+
+def test_converged_gradient_with_single_leaf_families():
+    """Families of one gene leaf (root row = leaf row): grad_theta of the converged solve vs central
+    differences of the loss."""
+    from kbench import synth
+
+    cfg = synth.ProblemConfig(8, 3, n_nni=1, family_leaves_median=3.0, family_leaves_sigma=0.3,
+                              family_leaves_max=5, seed=11, single_leaf_families=2)
+    p = synth.build_problem(cfg)
+    roots = np.asarray(p["static"]["wave_layout"]["root_row_ids"])
+    w0 = p["static"]["wave_layout"]["wave_metas"][0]
+    assert np.sum(roots < int(w0["start"]) + int(w0["W"])) == 2
+    prob = O.Problem.from_dict(p)
+    prob.so.update(pi_iters=120, neumann_terms=200, use_adjoint_pruning=False, adjoint_pruning_threshold=0.0,
+                   bicgstab_tol=1e-13, e_tol=1e-14)
+    theta = np.asarray(p["inputs"]["theta"], dtype=np.float64)
+    cw = np.zeros(prob.S)
+    loss, saved = O.forward(prob, theta, cw)
+    gt, _gc, _ = O.backward(prob, theta, cw, saved)
+    h = 1e-5
+    fd = np.zeros_like(theta)
+    for idx in np.ndindex(theta.shape):
+        tp, tm = theta.copy(), theta.copy()
+        tp[idx] += h
+        tm[idx] -= h
+        fd[idx] = (O.forward(prob, tp, cw)[0] - O.forward(prob, tm, cw)[0]) / (2 * h)
+    assert np.abs(gt - fd).max() <= 1e-6 * np.abs(fd).max()

@@ -18,6 +18,14 @@
 // contiguous range: A - subtree(u)[i] = P[i-1] + (A - P[end(i)-1]) for the
 // inclusive scan P of u over positions, one block scan per Neumann term.
 //
+// Latency: one workgroup per CU walks the level's rows persistently.  While
+// a row is solved, the next row's data (its schedule-slot record, Pi* /
+// Pibar* rows, child staging rows and split flags, row maxima and stored
+// split term) is already in flight; seven per-position constant rows stay in
+// LDS for the launch; the scans that need every wavefront publish
+// wavefront-local values and let the readers add the wavefront offsets, so
+// most phases take one barrier.
+//
 // Determinism: the reference scatters child adjoints and gradient sums with
 // float atomics.  Here every split side writes a staging row (preorder
 // layout); a child row gathers its staging rows in increasing split order,

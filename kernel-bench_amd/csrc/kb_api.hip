@@ -399,6 +399,11 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
     for (int64_t r = L->wave_start[w]; r < L->wave_start[w] + L->wave_size[w]; ++r)
       row_kind[r] = L->wave_has_splits[w] ? 0 : 1;
   for (int r = 0; r < C; ++r)
+    if (row_kind[r] && (leaf[r] < 0 || leaf[r] >= S)) {  // the leaf term indexes the state
+      kb_plan_destroy(p);
+      return set_error(KB_ERR_ARG, "leaf row %d has leaf state %d outside [0,%d)", r, leaf[r], S);
+    }
+  for (int r = 0; r < C; ++r)
     for (int i = sptr[r]; i < sptr[r + 1]; ++i) dagd[r] = std::max(dagd[r], 1 + std::max(dagd[sl[i]], dagd[sr[i]]));
   int maxdag = 0;
   for (int r = 0; r < C; ++r) maxdag = std::max(maxdag, dagd[r]);

@@ -250,3 +250,23 @@ def test_fused_single_leaf_families_match_oracle(statewise):
     for ws, act in extra["masks"]:
         ref_mask[ws:ws + len(act)] = act
     assert np.array_equal(mask, ref_mask)
+
+
+@pytest.mark.parametrize("bad", [-1, "S"])
+def test_plan_rejects_leaf_rows_without_a_valid_state(bad):
+    """A leaf row's leaf state indexes the state axis: out of range it is refused at plan creation
+    (before any kernel could read outside the tables)."""
+    from kbench.fused import FusedSolver, problem_to_captured
+    from kbench.runtime import make_static
+
+    p = kbtest.problem("tiny", None)
+    cap = problem_to_captured(p)
+    wl = cap["static"]["wave_layout"]
+    leaf = wl["leaf_state_index"].clone()
+    w0 = wl["wave_metas"][0]
+    S = int(cap["static"]["state_helpers"]["S"])
+    leaf[int(w0["start"])] = S if bad == "S" else bad
+    wl["leaf_state_index"] = leaf
+    static = make_static(cap, "cuda")
+    with pytest.raises(ValueError, match="leaf state"):
+        FusedSolver(static, static.solver_options)

@@ -110,7 +110,8 @@ def bench_other(args, static, theta, cw, summ) -> None:
     import numpy as np
     import torch
 
-    from kbench.runtime import run_backward, run_forward
+    sys.path.insert(0, str(ROOT / "tests"))  # the call-sequence drivers of the per-call wrappers
+    from dropin.solve import plan_of, run_backward, run_forward
 
     cfg = {"S_columns": summ["S"], "C": summ["C"], "n_waves": summ["n_waves"], "n_splits": summ["n_splits"]}
     if args.workload == "glue":
@@ -121,11 +122,11 @@ def bench_other(args, static, theta, cw, summ) -> None:
 
         metric = "fwd+bwd ms per solve through the per-wrapper drop-in path (reference glue call sequence)"
     else:
-        from newton.hvp_exact import make_exact_hvp
+        from dropin.hvp import HvpPlan
 
         loss, sv = run_forward(static, theta, cw)
         t0 = time.perf_counter()
-        hvp = make_exact_hvp(static, theta, cw, sv)
+        hvp = HvpPlan(plan_of(static), theta, cw, sv)
         torch.cuda.synchronize()
         cfg["point_cache_ms"] = round((time.perf_counter() - t0) * 1e3, 3)
         g = np.random.default_rng(0)

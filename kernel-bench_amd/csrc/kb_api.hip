@@ -131,6 +131,7 @@ struct kb_plan {
   unsigned char* b_cls_active = nullptr;
   float* b_contrib = nullptr; double* b_partial = nullptr; double* b_acc = nullptr; double* b_work = nullptr;
   int* b_status = nullptr;
+  int* h_status = nullptr;  // pinned host copy of b_status (kb_backward_stats)
   float* b_DL = nullptr; float* b_SL1 = nullptr; float* b_SL2 = nullptr; float* b_pS = nullptr; float* b_pD = nullptr;
   float* b_Ebar = nullptr; float* b_E = nullptr; float* b_mt = nullptr; float* b_col = nullptr; double* b_acc_pre = nullptr;
   int b_nb_max = 0, b_n_partials = 0, b_variant = 0;
@@ -185,6 +186,7 @@ void kb_plan_destroy(kb_plan* p) {
   for (hipEvent_t e : p->ev_bwd) (void)hipEventDestroy(e);
   for (void* ptr : p->owned)
     if (ptr) (void)hipFree(ptr);
+  if (p->h_status) (void)hipHostFree(p->h_status);
   delete p;
 }
 
@@ -316,13 +318,30 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
   p->n_tlevels = maxd + 1;
   p->n_blevels = (int)bptr.size() - 1;
 
-  // ---- rows, splits, waves
+  // ---- rows, splits, waves (int64 values range-checked before narrowing)
   std::vector<int> item(C), leaf(C), roots(L->n_fam);
   for (int r = 0; r < C; ++r) {
-    item[r] = (int)L->rate_item_idx[r];
-    leaf[r] = (int)L->leaf_state_index[r];
+    const int64_t it = L->rate_item_idx[r], lf = L->leaf_state_index[r];
+    if (it != 0) {  // one parameter row: the whole-pass kernels address every constant at row 0
+      kb_plan_destroy(p);
+      return set_error(KB_ERR_ARG, "rate_item_idx[%d]=%lld: the whole-pass driver needs every row in item 0", r,
+                       (long long)it);
+    }
+    if (lf < -1 || lf >= S) {
+      kb_plan_destroy(p);
+      return set_error(KB_ERR_ARG, "leaf_state_index[%d]=%lld: leaf state outside [-1,%d)", r, (long long)lf, S);
+    }
+    item[r] = 0;
+    leaf[r] = (int)lf;
   }
-  for (int f = 0; f < L->n_fam; ++f) roots[f] = (int)L->root_row_ids[f];
+  for (int f = 0; f < L->n_fam; ++f) {
+    const int64_t rt = L->root_row_ids[f];
+    if (rt < 0 || rt >= C) {
+      kb_plan_destroy(p);
+      return set_error(KB_ERR_ARG, "root_row_ids[%d]=%lld outside [0,%d)", f, (long long)rt, C);
+    }
+    roots[f] = (int)rt;
+  }
   const int64_t NS = L->n_splits;
   if (NS < 0 || NS >= (int64_t{1} << 29)) {  // split sides are ints below 2^30
     kb_plan_destroy(p);
@@ -336,8 +355,19 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
       kb_plan_destroy(p);
       return set_error(KB_ERR_ARG, "wave %d covers rows [%lld,%lld) outside [0,%d)", w, (long long)b, (long long)e, C);
     }
-    for (int64_t r = b; r < e; ++r) wave_of[r] = w;
+    for (int64_t r = b; r < e; ++r) {
+      if (wave_of[r] >= 0) {
+        kb_plan_destroy(p);
+        return set_error(KB_ERR_ARG, "row %lld lies in waves %d and %d", (long long)r, wave_of[r], w);
+      }
+      wave_of[r] = w;
+    }
   }
+  for (int r = 0; r < C; ++r)
+    if (wave_of[r] < 0) {
+      kb_plan_destroy(p);
+      return set_error(KB_ERR_ARG, "row %d lies in no wave", r);
+    }
   std::vector<int> cnt(C + 1, 0);
   for (int64_t i = 0; i < NS; ++i) {
     int64_t pr = L->split_parent[i];
@@ -385,13 +415,7 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
   }
   std::vector<float> unnorm(L->unnorm_row_max, L->unnorm_row_max + S);
   std::vector<int> root_index(C, -1);
-  for (int f = 0; f < L->n_fam; ++f) {
-    if (roots[f] < 0 || roots[f] >= C) {
-      kb_plan_destroy(p);
-      return set_error(KB_ERR_ARG, "root_row_ids[%d]=%d outside [0,%d)", f, roots[f], C);
-    }
-    root_index[roots[f]] = f;
-  }
+  for (int f = 0; f < L->n_fam; ++f) root_index[roots[f]] = f;
   p->n_splits = NS;
   // DAG depth of every row (children precede parents: checked above)
   std::vector<int> row_kind(C, 0), dagd(C, 0);
@@ -963,9 +987,10 @@ int64_t kb_forward_token(const kb_plan* p) { return p ? p->fwd_token : 0; }
 int kb_backward_stats(kb_plan* p, int32_t* n_iter, void* stream) {
   if (!p) return set_error(KB_ERR_ARG, "null argument");
   if (!p->b_status) return set_error(KB_ERR_ARG, "no backward has run on this plan");
+  if (!p->h_status) KB_HIP(hipHostMalloc((void**)&p->h_status, 2 * sizeof(int), hipHostMallocDefault));
+  KB_HIP(hipMemcpyAsync(p->h_status, p->b_status, 2 * sizeof(int), hipMemcpyDeviceToHost, (hipStream_t)stream));
   KB_HIP(hipStreamSynchronize((hipStream_t)stream));
-  int st[2];
-  KB_HIP(hipMemcpy(st, p->b_status, sizeof(st), hipMemcpyDeviceToHost));
+  const int st[2] = {p->h_status[0], p->h_status[1]};
   if (n_iter) *n_iter = st[0];
   if (st[1])
     return set_error(KB_ERR_SOLVE, "E-adjoint BiCGSTAB solve failed after %d iterations", st[0]);

@@ -13,13 +13,14 @@ with a handful of launches on the current stream:
   E adjoint and the theta / column VJP.
 
 It computes what the reference's frozen glue computes
-(reference kbench/runtime.py:63-115) and returns the same tensors; the glue
-path in ``kbench.runtime`` drives the per-call wrappers instead.
+(reference kbench/runtime.py:63-115) and returns the same tensors;
+``kbench.runtime`` exposes it under the reference's entry-point names.
 """
 
 from __future__ import annotations
 
 import ctypes as ct
+import weakref
 from types import SimpleNamespace
 
 import numpy as np
@@ -40,9 +41,22 @@ _SOLVER_DEFAULTS = {
 }
 
 
-def _ident(t):
-    """(address, shape, version) of a tensor: equal while it is the same unmodified storage."""
-    return (int(t.data_ptr()), tuple(t.shape), int(t._version))
+class _TensorKey:
+    """Identity of a live tensor object and its in-place version counter.
+
+    Holds a weak reference, so a key never matches a different tensor that was
+    later allocated at the freed address (the object identity is checked, not
+    the address), and never keeps the tensor alive.
+    """
+
+    __slots__ = ("ref", "version")
+
+    def __init__(self, t):
+        self.ref = weakref.ref(t)
+        self.version = int(t._version)
+
+    def matches(self, t) -> bool:
+        return self.ref() is t and int(t._version) == self.version
 
 
 def _np(x, dtype=None):
@@ -69,12 +83,77 @@ def solver_options_dict(so) -> dict:
     return d
 
 
+def layout_arrays(static) -> dict:
+    """Host (numpy) arrays of the ``kb_layout`` struct from a ``static`` namespace or dict.
+
+    Splits are flattened over the waves with their global parent row
+    (wave start + reduce_idx); a wave without ``log_split_probs`` has 0.
+    """
+    wl = _get(static, "wave_layout")
+    sh = _get(static, "state_helpers")
+    ws, wsz, whs = [], [], []
+    sp, sl, sr, lsp = [], [], [], []
+    for m in wl["wave_metas"]:
+        start, W = int(m["start"]), int(m["W"])
+        ws.append(start)
+        wsz.append(W)
+        has = "sl" in m
+        whs.append(1 if has else 0)
+        if has:
+            a = _np(m["sl"], np.int64)
+            lp = m.get("log_split_probs")
+            sp.append(_np(m["reduce_idx"], np.int64) + start)
+            sl.append(a)
+            sr.append(_np(m["sr"], np.int64))
+            lsp.append(np.zeros(a.shape[0]) if lp is None else _np(lp, np.float64).reshape(-1))
+    cat = lambda xs, dt: (np.concatenate(xs).astype(dt) if xs else np.zeros(0, dtype=dt))
+    arrays = {
+        "node_parent": _np(sh["node_parent"], np.int64),
+        "node_child1": _np(sh["node_child1"], np.int64),
+        "node_child2": _np(sh["node_child2"], np.int64),
+        "node_subtree_start": _np(sh["node_subtree_start"], np.int64),
+        "node_subtree_end": _np(sh["node_subtree_end"], np.int64),
+        "unnorm_row_max": _np(sh["unnorm_row_max"], np.float32),
+        "leaf_state_index": _np(wl["leaf_state_index"], np.int64),
+        "rate_item_idx": _np(_get(static, "rate_item_idx"), np.int64),
+        "root_row_ids": _np(wl["root_row_ids"], np.int64),
+        "wave_start": np.asarray(ws, np.int64),
+        "wave_size": np.asarray(wsz, np.int64),
+        "wave_has_splits": np.asarray(whs, np.int32),
+        "split_parent": cat(sp, np.int64),
+        "split_left": cat(sl, np.int64),
+        "split_right": cat(sr, np.int64),
+        "split_log_prob": cat(lsp, np.float64),
+    }
+    arrays = {k: np.ascontiguousarray(v) for k, v in arrays.items()}
+    arrays["S"] = int(_get(static, "state_helpers")["S"])
+    return arrays
+
+
+def kb_layout(arrays: dict) -> "N.KbLayout":
+    """The ``kb_layout`` struct over ``arrays`` (the arrays must outlive the struct)."""
+    L = N.KbLayout()
+    L.S, L.C = int(arrays["S"]), int(arrays["leaf_state_index"].shape[0])
+    L.n_fam, L.n_waves = int(arrays["root_row_ids"].shape[0]), int(arrays["wave_start"].shape[0])
+    for k, v in arrays.items():
+        if k == "S":
+            continue
+        if v.dtype == np.int64:
+            setattr(L, k, v.ctypes.data_as(N.P_i64))
+        elif v.dtype == np.int32:
+            setattr(L, k, v.ctypes.data_as(N.P_i32))
+        elif v.dtype == np.float32:
+            setattr(L, k, v.ctypes.data_as(N.P_f32))
+        else:
+            setattr(L, k, v.ctypes.data_as(N.P_f64))
+    L.n_splits = int(arrays["split_left"].shape[0])
+    return L
+
+
 class FusedSolver:
     """Native whole-pass solver bound to one static layout and one device."""
 
     def __init__(self, static, solver_options=None, device=None):
-        wl = _get(static, "wave_layout")
-        sh = _get(static, "state_helpers")
         self.statewise = bool(_get(static, "statewise"))
         self.itemwise = bool(_get(static, "itemwise"))
         if self.itemwise:
@@ -83,64 +162,12 @@ class FusedSolver:
             static.get("solver_options") if isinstance(static, dict) else getattr(static, "solver_options", None))
         self.so = solver_options_dict(so)
         self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
-        S = int(sh["S"])
-        item = _np(_get(static, "rate_item_idx"), np.int64)
-        if np.any(item != 0):
+        arrays = layout_arrays(static)
+        if np.any(arrays["rate_item_idx"] != 0):
             raise NotImplementedError("the fused driver needs rate_item_idx == 0 (itemwise=False)")
-        leaf = _np(wl["leaf_state_index"], np.int64)
-        C = int(leaf.shape[0])
-        roots = _np(wl["root_row_ids"], np.int64)
-        ws, wsz, whs = [], [], []
-        sp, sl, sr, lsp = [], [], [], []
-        for m in wl["wave_metas"]:
-            start, W = int(m["start"]), int(m["W"])
-            ws.append(start)
-            wsz.append(W)
-            has = "sl" in m
-            whs.append(1 if has else 0)
-            if has:
-                a = _np(m["sl"], np.int64)
-                b = _np(m["sr"], np.int64)
-                red = _np(m["reduce_idx"], np.int64)
-                lp = m.get("log_split_probs")
-                lp = np.zeros(a.shape[0]) if lp is None else _np(lp, np.float64).reshape(-1)
-                sp.append(red + start)
-                sl.append(a)
-                sr.append(b)
-                lsp.append(lp)
-        cat = lambda xs, dt: (np.concatenate(xs).astype(dt) if xs else np.zeros(0, dtype=dt))
-        self._arrays = arrays = {
-            "node_parent": _np(sh["node_parent"], np.int64),
-            "node_child1": _np(sh["node_child1"], np.int64),
-            "node_child2": _np(sh["node_child2"], np.int64),
-            "node_subtree_start": _np(sh["node_subtree_start"], np.int64),
-            "node_subtree_end": _np(sh["node_subtree_end"], np.int64),
-            "unnorm_row_max": _np(sh["unnorm_row_max"], np.float32),
-            "leaf_state_index": leaf,
-            "rate_item_idx": item,
-            "root_row_ids": roots,
-            "wave_start": np.asarray(ws, np.int64),
-            "wave_size": np.asarray(wsz, np.int64),
-            "wave_has_splits": np.asarray(whs, np.int32),
-            "split_parent": cat(sp, np.int64),
-            "split_left": cat(sl, np.int64),
-            "split_right": cat(sr, np.int64),
-            "split_log_prob": cat(lsp, np.float64),
-        }
-        arrays = {k: np.ascontiguousarray(v) for k, v in arrays.items()}
         self._arrays = arrays
-        L = N.KbLayout()
-        L.S, L.C, L.n_fam, L.n_waves = S, C, int(roots.shape[0]), len(ws)
-        for k, v in arrays.items():
-            if v.dtype == np.int64:
-                setattr(L, k, v.ctypes.data_as(N.P_i64))
-            elif v.dtype == np.int32:
-                setattr(L, k, v.ctypes.data_as(N.P_i32))
-            elif v.dtype == np.float32:
-                setattr(L, k, v.ctypes.data_as(N.P_f32))
-            else:
-                setattr(L, k, v.ctypes.data_as(N.P_f64))
-        L.n_splits = int(arrays["split_left"].shape[0])
+        L = kb_layout(arrays)
+        S, C, roots, ws = L.S, L.C, arrays["root_row_ids"], arrays["wave_start"]
         lib = N.lib()
         handle = ct.c_void_p()
         with torch.cuda.device(self.device):
@@ -155,7 +182,8 @@ class FusedSolver:
         self.n_levels = int(info[6])
         self.last_n_e_iter = None
         self.last_n_bicgstab = None
-        self._use_col_cache = None
+        self._use_col_cache = None  # (_TensorKey of the caller's col_weights, answer)
+        self._last_forward = None   # (forward token, _TensorKey of pi, _TensorKey of pibar)
 
     def close(self):
         if getattr(self, "_plan", None):
@@ -172,16 +200,17 @@ class FusedSolver:
     def _use_col(self, col_weights) -> bool:
         """True unless every column weight is equal (then the uniform fast path applies).
 
-        The answer is cached per (storage, version) so repeated solves with the
-        same weights do not synchronise the host with the device.
+        ``col_weights`` is the caller's tensor (before any dtype / device
+        conversion).  The answer is cached for that live tensor object and its
+        version, so repeated solves with the same weights do not synchronise
+        the host with the device; any other tensor is evaluated afresh.
         """
-        key = (col_weights.data_ptr(), col_weights._version, tuple(col_weights.shape), col_weights.device)
         hit = self._use_col_cache
-        if hit is not None and hit[0] == key:
+        if hit is not None and hit[0].matches(col_weights):
             return hit[1]
         flat = col_weights.detach().reshape(-1)
         val = not bool(torch.all(flat == flat[0]).item())
-        self._use_col_cache = (key, val)
+        self._use_col_cache = (_TensorKey(col_weights), val)
         return val
 
     def run_forward(self, theta, col_weights, *, use_col_weights=None):
@@ -190,12 +219,12 @@ class FusedSolver:
         dev = self.device
         S, C = self.S, self.C
         theta = theta.detach().to(device=dev, dtype=torch.float32).contiguous()
+        use_col = self._use_col(col_weights) if use_col_weights is None else bool(use_col_weights)
         col_weights = col_weights.detach().to(device=dev, dtype=torch.float32).contiguous()
         if self.statewise and tuple(theta.shape) != (S, 3):
             raise ValueError(f"statewise theta must have shape ({S}, 3), got {tuple(theta.shape)}")
         if not self.statewise and tuple(theta.shape) != (3,):
             raise ValueError(f"theta must have shape (3,), got {tuple(theta.shape)}")
-        use_col = self._use_col(col_weights) if use_col_weights is None else bool(use_col_weights)
         f32 = dict(device=dev, dtype=torch.float32)
         E, E_s1, E_s2, Ebar = (torch.empty((1, S), **f32) for _ in range(4))
         npar = S if self.statewise else 1
@@ -217,8 +246,9 @@ class FusedSolver:
         )
         with torch.cuda.device(dev):
             N.check(N.lib().kb_forward(self._plan, ct.byref(io), N.stream_handle(dev)))
-        # the backward may reuse this forward's stored split terms while pi / pibar are unchanged
-        self._last_forward = (int(N.lib().kb_forward_token(self._plan)), _ident(pi), _ident(pibar))
+        # the backward may reuse this forward's stored split terms while pi / pibar are
+        # these same, unmodified tensor objects
+        self._last_forward = (int(N.lib().kb_forward_token(self._plan)), _TensorKey(pi), _TensorKey(pibar))
         if not self.statewise:
             pS, pD, pL = (t.reshape(()) for t in (pS, pD, pL))
         saved = dict(zip(FORWARD_SAVED_NAMES, (
@@ -269,20 +299,29 @@ class FusedSolver:
         self.last_n_e_iter = int(n.value)
         return {"n_e_iter": int(n.value), "loss64": float(l64.value)}
 
-    def run_backward(self, theta, col_weights, saved, *, return_info=False):
-        """(forward intermediates) -> (grad_theta, grad_col), the reference ``run_backward`` contract."""
+    def run_backward(self, theta, col_weights, saved, *, return_info=False, check_solve=True):
+        """(forward intermediates) -> (grad_theta, grad_col), the reference ``run_backward`` contract.
+
+        As in the reference (_implicit_grad.py:94), a failed E-adjoint BiCGSTAB
+        solve raises ``RuntimeError``; checking it reads two status words back
+        from the device once per backward (``check_solve=False`` skips the read,
+        and ``backward_stats`` reports the status later).
+        """
         lib = N.lib()
         if not hasattr(lib, "kb_backward"):
             raise N.NativeLibraryMissing("libkbench_hip was built without kb_backward")
         so = self.so
         if str(so["self_loop_solver"]).strip().lower() != "neumann":
             raise NotImplementedError("the fused backward implements the neumann self-loop solver")
+        if float(so["pibar_side_threshold"]) != 0.0:
+            # the row kernel skips only all-zero Pibar sides (the reference's rule at threshold 0)
+            raise NotImplementedError("the fused backward implements pibar_side_threshold == 0 only")
         dev = self.device
         S, C = self.S, self.C
         theta_d = theta.detach().to(device=dev, dtype=torch.float32).contiguous()
-        cw = col_weights.detach().to(device=dev, dtype=torch.float32).contiguous()
         use_col = saved.get("_use_col_weights")
-        use_col = self._use_col(cw) if use_col is None else bool(use_col)
+        use_col = self._use_col(col_weights) if use_col is None else bool(use_col)
+        cw = col_weights.detach().to(device=dev, dtype=torch.float32).contiguous()
         f32 = dict(device=dev, dtype=torch.float32)
         grad_theta = torch.empty(tuple(theta_d.shape), **f32)
         grad_col = torch.empty((S,), **f32)
@@ -303,13 +342,15 @@ class FusedSolver:
             grad_theta=N.ptr(grad_theta), grad_col=N.ptr(grad_col), active_mask=N.ptr(mask), acc_out=N.ptr(acc),
         )
         token = 0
-        last = getattr(self, "_last_forward", None)
-        if last is not None and last[1] == _ident(tens["pi_wave"]) and last[2] == _ident(tens["pibar_wave"]):
+        last = self._last_forward
+        if last is not None and last[1].matches(saved["pi_wave"]) and last[2].matches(saved["pibar_wave"]):
             token = last[0]
         io.forward_token = token
         self._keep = (tens, theta_d, cw)
         with torch.cuda.device(dev):
             N.check(lib.kb_backward(self._plan, ct.byref(io), N.stream_handle(dev)))
+            if check_solve:
+                self.backward_stats()
         if return_info:
             return grad_theta, grad_col, {"active_mask": mask, "acc": acc}
         return grad_theta, grad_col

@@ -710,9 +710,11 @@ def dts_cross_backward(Pi_s, Pibar_s, row_max, v, ws, meta, pD_param, pS_param, 
     inv_r = np.where(np.isneginf(pbr), 0.0, np.exp2(row_max[sr][:, None] + mt_r - np.where(np.isneginf(pbr), 0.0, pbr)))
     ud_l = vd[2] * inv_l
     ud_r = vd[1] * inv_r
+    direct_l, direct_r = rhs_l.copy(), rhs_r.copy()
     # tree VJP (wave_backward.py:2287-2327)
     col_grad = np.zeros(S)
-    for child, ud, acc in ((sl, ud_l, rhs_l), (sr, ud_r, rhs_r)):
+    sums = {}
+    for side, child, ud, acc in (("l", sl, ud_l, rhs_l), ("r", sr, ud_r, rhs_r)):
         A = ud.sum(axis=1, keepdims=True)
         sub = tree.subtree_sum(ud)
         wPi = Pi_s[child] + col if use_col_weights else Pi_s[child]
@@ -720,10 +722,14 @@ def dts_cross_backward(Pi_s, Pibar_s, row_max, v, ws, meta, pD_param, pS_param, 
         contrib = np.where(act[:, None], pp * (A - sub), 0.0)
         acc += contrib
         col_grad += contrib.sum(axis=0)
+        sums["A_" + side], sums["sub_" + side], sums["tree_" + side] = A[:, 0], sub, contrib
+    # the direct_* rows (before the Pibar VJP), A_*, sub_* (subtree sums of u_d) and
+    # tree_* (the Pibar VJP rows) are the intermediate outputs of the two reference
+    # kernels: dts_cross_backward_accum_fused and uniform_cross_pibar_vjp_tree_from_ud_fused
     return {
         "rhs_l": rhs_l, "rhs_r": rhs_r, "g_pD": vd[0], "g_pS": vd[3] + vd[4],
         "g_mt_l": vd[2], "g_mt_r": vd[1], "col_grad": col_grad,
-        "ud_l": ud_l, "ud_r": ud_r,
+        "ud_l": ud_l, "ud_r": ud_r, "direct_l": direct_l, "direct_r": direct_r, "active_split": act, **sums,
     }
 
 

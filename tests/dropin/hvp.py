@@ -1,0 +1,350 @@
+"""Hessian-vector products of the loss through the per-call wrappers (config 5).
+
+Forward over reverse at a fixed theta, with the wrapper calls of the
+reference's newton/forward_tangent.py:99-209 and newton/hvp_exact.py:54-383:
+
+tangent forward (``TangentForward``)
+  parameter tangents (a JVP of the rate extraction), ``e_tangent_fixed_point``,
+  then per wave in order: ``compute_dts_forward`` + ``compute_dts_tangent``
+  (split waves) and the self-loop tangent at Pi* --
+  ``compute_wave_step_tangent_selfloop`` for a fixed sweep count in one call,
+  the same count as repeated ``compute_wave_step_tangent`` calls, or sweeps
+  until max|change| <= tol * max(1, max|dPi|).
+
+tangent reverse (``HvpPlan``), per cached wave in reverse order
+  ``compute_dts_tangent`` at the cached split term, ``wave_backward_so`` at the
+  cached adjoint (seeded with the tangent adjoint rows, FOLD_RHS), the tangent
+  adjoint solve ``wave_backward_uniform_fused`` with the cached mask, the
+  bucket sums, then ``dts_cross_backward_accum_fused``,
+  ``uniform_cross_pibar_vjp_tree_from_ud_fused`` and ``dts_backward_so``
+  (split waves).
+
+E side and head
+  ``e_step_backward_so`` contractions at the cached E adjoint, a BiCGSTAB solve
+  of the tangent E adjoint, the E-step parameter VJP, and the second
+  derivative of the rate extraction by autograd.
+
+The point cache (one backward at theta keeping every wave's adjoint, split
+term and mask, the accumulated cotangents and the E adjoint) is built once per
+theta by ``SolvePlan.reverse_sweep`` / ``e_adjoint_and_vjp``.
+"""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import torch
+from torch.func import jvp
+
+from kbench.core.parameters.extract_parameters import (as_item_param, as_item_state, extract_parameters_uniform,
+                                                       extract_parameters_weighted_cols)
+
+from .krylov import bicgstab
+from .solve import LN2, SolvePlan, root_softmax2
+
+
+def _fold(acc, x, G, S):
+    """acc + x for a parameter accumulator ([G, 1] or [G, S]) and an item-state term [G, S].
+
+    With one value per item row the state axis of x is summed (the accumulator is
+    counted once, not once per state).
+    """
+    x = as_item_param(x, G, S)
+    if int(acc.shape[-1]) == 1 and int(x.shape[-1]) != 1:
+        x = x.sum(dim=-1, keepdim=True)
+    return acc + x
+
+
+class TangentForward:
+    """d(Pi)/d(theta) . u through the forward solve, at the saved point of ``plan``."""
+
+    def __init__(self, plan: SolvePlan, saved):
+        self.p = plan
+        self.sv = saved
+        S, G = plan.S, int(saved["E"].shape[0])
+        item = lambda t: as_item_state(t, S, G)
+        E, pS, pD = item(saved["E"]), item(saved["log_pS"]), item(saved["log_pD"])
+        self.base = SimpleNamespace(
+            mc=item(saved["max_coupling"].squeeze(-1)), dl=1.0 + pD + E, ebar=item(saved["Ebar"]), e=E,
+            sl1=pS + item(saved["E_s2"]), sl2=pS + item(saved["E_s1"]), leaf=pS,
+            pd_par=as_item_param(saved["log_pD"], G, S), ps_par=as_item_param(saved["log_pS"], G, S))
+
+    def param_tangent(self, theta, u):
+        """(dpS, dpD, dpL, dmt): the rate extraction's JVP along u (uniform columns)."""
+        st = self.p.static
+        urm = self.p.h["unnorm_row_max"].to(device=theta.device, dtype=theta.dtype)
+        _, tan = jvp(lambda th: extract_parameters_uniform(th, urm, statewise=st.statewise, itemwise=st.itemwise),
+                     (theta,), (u,))
+        return tan
+
+    def constants(self, theta, u, e_tol):
+        """Tangents of every constant row the sweeps read, plus the raw parameter / E tangents."""
+        p, sv = self.p, self.sv
+        S, G = p.S, int(sv["E"].shape[0])
+        dpS, dpD, dpL, dmt = self.param_tangent(theta, u)
+        dE, dEs1, dEs2, dEbar = p.k.e_tangent_fixed_point(
+            sv["E"], dpS, dpD, dpL, dmt, sv["log_pS"], sv["log_pD"], sv["log_pL"], sv["max_coupling"],
+            sv["col_log_probs"], *p.topo, max_iter=int(p.so.e_max_iter), tol=e_tol, use_col_weights=False)
+        item = lambda t: as_item_state(t, S, G)
+        de, dps = item(dE), item(dpS)
+        return SimpleNamespace(
+            dMC=item(dmt.squeeze(-1)), dDL=item(dpD) + de, dEbar=item(dEbar), dE=de, dSL1=dps + item(dEs2),
+            dSL2=dps + item(dEs1), dleaf=dps, dpd_par=as_item_param(dpD, G, S), dps_par=as_item_param(dpS, G, S),
+            raw=dict(dlog_pS=dpS, dlog_pD=dpD, dlog_pL=dpL, dmax_coupling=dmt, dE=dE, dE_s1=dEs1, dE_s2=dEs2,
+                     dEbar=dEbar))
+
+    def interleaved(self, d):
+        b = self.base
+        return (b.mc, d.dMC, b.dl, d.dDL, b.ebar, d.dEbar, b.e, d.dE, b.sl1, d.dSL1, b.sl2, d.dSL2)
+
+    def run(self, theta, u, *, sweeps=None, one_call=True, tol=None, max_sweeps=200, e_tol=None):
+        """-> (root-row tangents, namespace of dPi, dPibar, constant tangents).
+
+        ``sweeps``: a fixed count of tangent sweeps per wave, in one call (``one_call``) or
+        one call per sweep; ``None`` sweeps each wave until its largest change is at most
+        ``tol * max(1, max|dPi|)`` (``max_sweeps`` at most), then once more storing dPibar.
+        """
+        p, sv = self.p, self.sv
+        dt = sv["pi_wave"].dtype
+        tol = (1e-12 if dt == torch.float64 else 1e-6) if tol is None else tol
+        e_tol = (1e-12 if dt == torch.float64 else 1e-6) if e_tol is None else e_tol
+        d = self.constants(theta, u, e_tol)
+        pi, pibar = sv["pi_wave"], sv["pibar_wave"]
+        dpi = torch.zeros_like(pi)
+        dpibar = torch.zeros_like(pi)
+        cst = self.interleaved(d)
+        col = sv["col_log_probs"]
+        h = p.h
+        kw = dict(leaf_state_idx=p.leaf_idx, leaf_logp=self.base.leaf, dleaf_logp=d.dleaf, item_idx=p.item_idx,
+                  use_col_weights=False)
+        for w in p.waves:
+            dts = d_dts = None
+            if w.split:
+                lay = dict(log_split_probs=w.lsp, item_offset=w.ws, **w.extra)
+                dts = p.k.compute_dts_forward(pi, pibar, w.sl, w.sr, h["node_child1"], h["node_child2"], w.W,
+                                              w.reduce_idx, self.base.pd_par, self.base.ps_par, item_idx=p.item_idx,
+                                              **lay)
+                d_dts = p.k.compute_dts_tangent(pi, pibar, dpi, dpibar, w.sl, w.sr, h["node_child1"],
+                                                h["node_child2"], w.W, w.reduce_idx, self.base.pd_par,
+                                                self.base.ps_par, d.dpd_par, d.dps_par, dts, p.item_idx, **lay)
+
+            def sweep(store):
+                p.k.compute_wave_step_tangent(pi, dpi, dpi, w.ws, w.W, p.S, *cst, col, h["node_child1"],
+                                              h["node_child2"], p.topo[0], p.topo[3], dts, d_dts,
+                                              dPibar_out=dpibar if store else None, has_leaf_term=not w.split, **kw)
+
+            if sweeps is not None and one_call:
+                p.k.compute_wave_step_tangent_selfloop(pi, dpi, w.ws, w.W, p.S, max(int(sweeps), 1), *cst, col,
+                                                       h["node_child1"], h["node_child2"], p.topo[0], p.topo[3],
+                                                       dts, d_dts, dPibar_out=dpibar, has_leaf_term=not w.split,
+                                                       **kw)
+            elif sweeps is not None:
+                for k in range(max(int(sweeps), 1)):
+                    sweep(store=k == max(int(sweeps), 1) - 1)
+            else:
+                prev = dpi.narrow(0, w.ws, w.W).clone()
+                for _ in range(int(max_sweeps)):
+                    sweep(store=False)
+                    cur = dpi.narrow(0, w.ws, w.W)
+                    if float((cur - prev).abs().max()) <= tol * max(1.0, float(cur.abs().max())):
+                        break
+                    prev = cur.clone()
+                sweep(store=True)
+        return dpi.index_select(0, p.roots), SimpleNamespace(dPi=dpi, dPibar=dpibar, d=d)
+
+
+class _EGraph:
+    """One E step at (E*, parameters) kept as an autograd graph: its transposed products."""
+
+    def __init__(self, plan: SolvePlan, saved):
+        self.p = plan
+        S, G = plan.S, int(saved["E"].shape[0])
+        item = lambda t: as_item_state(t, S, G)
+        self.E = saved["E"].detach()
+        self.params = [item(saved["log_pS"]), item(saved["log_pD"]), item(saved["log_pL"]),
+                       item(saved["max_coupling"].squeeze(-1)), saved["col_log_probs"].contiguous()]
+        self.E_var = self.E.clone().requires_grad_(True)
+        with torch.enable_grad():
+            self.out = plan.k.e_step_triton_autograd(self.E_var, *self.params, *plan.topo, use_col_weights=False)
+
+    def _grad(self, outs, cots):
+        with torch.enable_grad():
+            (g,) = torch.autograd.grad(outs, self.E_var, grad_outputs=cots, retain_graph=True)
+        return g
+
+    def jt(self, w):
+        """J_E^T w (the E-step map's transpose at E*)."""
+        return self._grad(self.out[0], w.contiguous())
+
+    def aux_t(self, g_s1, g_s2, g_ebar):
+        """Transposed derivative of (E_s1, E_s2, Ebar) with respect to E."""
+        return self._grad(self.out[1:], (g_s1, g_s2, g_ebar))
+
+    def params_t(self, g_new, g_ebar):
+        """Cotangents of (pS, pD, pL, mt, col) from those of (E_new, Ebar) at fixed E*."""
+        xs = [x.detach().clone().requires_grad_(True) for x in self.params]
+        with torch.enable_grad():
+            En, _, _, Eb = self.p.k.e_step_triton_autograd(self.E, *xs, *self.p.topo, use_col_weights=False)
+            gs = torch.autograd.grad((En, Eb), xs, grad_outputs=(g_new, g_ebar), allow_unused=True)
+        return [torch.zeros_like(x) if g is None else g for g, x in zip(gs, xs)]
+
+
+class HvpPlan:
+    """H u of the summed loss at theta (uniform column weights), through the wrappers."""
+
+    def __init__(self, plan: SolvePlan, theta, col_weights, saved, *, tangent_sweeps=None):
+        self.p, self.sv = plan, saved
+        self.theta, self.cw = theta, col_weights
+        self.sweeps = int(plan.so.pi_iters if tangent_sweeps is None else tangent_sweeps)
+        S = plan.S
+        self.G = G = int(saved["E"].shape[0])
+        # point cache: one backward with every wave's adjoint kept
+        self.waves = []
+        with torch.no_grad():
+            seed = -root_softmax2(saved["pi_wave"].index_select(0, plan.roots))
+            self.acc = plan.reverse_sweep(saved, seed, use_col=False, cache=self.waves)
+        e_out = {}
+        self.grad = plan.e_adjoint_and_vjp(theta, col_weights, saved, self.acc, use_col=False, out=e_out)
+        self.wE = e_out["wE"]
+        self.tan = TangentForward(plan, saved)
+        self.eg = _EGraph(plan, saved)
+        a = self.acc
+        base = self.eg.params_t(self.wE, a.Ebar)
+        self.cot = SimpleNamespace(pS=_fold(a.pS, base[0], G, S), pD=_fold(a.pD, base[1], G, S), pL=base[2],
+                                   mt=a.mt + base[3], col=a.col + base[4])
+        # the parameter head: theta -> rates, and the first-order gradient kept differentiable
+        st = plan.static
+        self.th = theta.detach().clone().requires_grad_(True)
+        cw = col_weights.detach().clone().requires_grad_(True)
+        with torch.enable_grad():
+            pS, pD, pL, mt, col = extract_parameters_weighted_cols(self.th, cw, plan.h, statewise=st.statewise,
+                                                                   itemwise=st.itemwise, uniform_fast=True)
+            self.rates = (as_item_param(pS, G, S), as_item_param(pD, G, S), as_item_state(pL, S, G),
+                          as_item_state(mt, S, G), col)
+            (self.g1,) = torch.autograd.grad(self._pair(self.cot), self.th, create_graph=True)
+
+    def _pair(self, cot):
+        r = self.rates
+        return ((r[0] * cot.pS).sum() + (r[1] * cot.pD).sum() + (r[2] * cot.pL).sum() + (r[3] * cot.mt).sum()
+                + (r[4] * cot.col).sum())
+
+    def __call__(self, u_flat):
+        u = u_flat.reshape(self.theta.shape).to(self.theta.dtype)
+        with torch.no_grad():
+            dcot = self._tangent_cotangents(u)
+        with torch.enable_grad():
+            (hu,) = torch.autograd.grad((self.g1 * u).sum() + self._pair(dcot), self.th, retain_graph=True)
+        return hu.reshape(-1)
+
+    def _tangent_cotangents(self, u):
+        p, sv, a = self.p, self.sv, self.acc
+        S, G, C = p.S, self.G, p.C
+        t_root, tf = self.tan.run(self.theta, u, sweeps=self.sweeps)
+        d, dPi, dPibar = tf.d, tf.dPi, tf.dPibar
+        Pi, Pibar, prm, col = sv["pi_wave"], sv["pibar_wave"], sv["pibar_row_max"], sv["col_log_probs"]
+        b = self.tan.base
+        h = p.h
+        # tangent of the root seed -softmax2(root): -ln2 q (t - <q, t>)
+        q = root_softmax2(Pi.index_select(0, p.roots))
+        d_rhs = torch.zeros((C, S), dtype=Pi.dtype, device=Pi.device)
+        d_rhs.index_copy_(0, p.roots, -LN2 * q * (t_root - (q * t_root).sum(dim=-1, keepdim=True)))
+        dacc = SimpleNamespace(pD=torch.zeros_like(a.pD), pS=torch.zeros_like(a.pS), mt=torch.zeros_like(a.mt),
+                               col=torch.zeros_like(a.col), E=torch.zeros_like(a.E), Ebar=torch.zeros_like(a.E),
+                               Es1=torch.zeros_like(a.E), Es2=torch.zeros_like(a.E))
+        targets = ((dacc.pD, (0,)), (dacc.pS, (3,)), (dacc.E, (0, 2)), (dacc.Ebar, (1,)), (dacc.Es1, (5,)),
+                   (dacc.Es2, (4,)), (dacc.mt, (2,)))
+        cst_so = (b.mc,) + self.tan.interleaved(d)[2:]  # the contraction takes mt without its tangent
+        so = p.so
+        for w, v, dts, mask in self.waves:
+            d_dts = None
+            if w.split:
+                d_dts = p.k.compute_dts_tangent(Pi, Pibar, dPi, dPibar, w.sl, w.sr, h["node_child1"],
+                                                h["node_child2"], w.W, w.reduce_idx, b.pd_par, b.ps_par, d.dpd_par,
+                                                d.dps_par, dts, p.item_idx, log_split_probs=w.lsp, item_offset=w.ws)
+            seed, *so_aw = p.k.wave_backward_so(
+                Pi, dPi, Pibar, dPibar, v, w.ws, w.W, S, prm, *cst_so, col, h["node_child1"], h["node_child2"],
+                p.topo[0], p.topo[3], dts, d_dts, leaf_state_idx=p.leaf_idx, leaf_logp=b.leaf, dleaf_logp=d.dleaf,
+                item_idx=p.item_idx, has_leaf_term=w.leaf_term, use_col_weights=False, d_rhs=d_rhs)
+            dv, *lin_aw = p.k.wave_backward_uniform_fused(
+                Pi, Pibar, w.ws, w.W, S, dts, seed, b.mc, b.dl, b.ebar, b.e, b.sl1, b.sl2, col, h["node_child1"],
+                h["node_child2"], None, neumann_terms=int(so.neumann_terms), leaf_state_idx=p.leaf_idx,
+                leaf_logp=b.leaf, has_leaf_term=w.leaf_term, active_mask=mask, node_parent=p.topo[0],
+                max_ancestor_depth=p.topo[3], pibar_row_max=prm, item_idx=p.item_idx, item_indexed_consts=True,
+                grad_col_log_probs=dacc.col, use_col_weights=False, self_loop_solver=so.self_loop_solver,
+                **p.levels)
+            p._fold_buckets([x + y for x, y in zip(so_aw, lin_aw)], targets, w, G)
+            if w.split:
+                lsp = w.lsp if w.lsp is not None else w.sl.new_zeros((int(w.sl.numel()),), dtype=Pi.dtype)
+                ud, A, side_on, _, _ = p.k.dts_cross_backward_accum_fused(
+                    Pi, Pibar, dv, w.ws, w.sl, w.sr, w.reduce_idx, lsp, b.pd_par, b.ps_par, h["node_child1"],
+                    h["node_child2"], d_rhs, S, active_mask=mask, merge_s_term=True, grad_log_pD=dacc.pD,
+                    grad_log_pS=dacc.pS, grad_mt=dacc.mt, accum_param_reductions=True, accum_mt_reduction=True,
+                    output_pibar_ud=True, output_pibar_side_active=True,
+                    pibar_side_threshold=so.pibar_side_threshold, mt_squeezed=b.mc, pibar_row_max=prm,
+                    grad_mt_two_stage=bool(dacc.mt.ndim == 2 and int(dacc.mt.shape[0]) == 1),
+                    grad_mt_two_stage_tile_splits=128, skip_inactive_pibar_output_zero=True, item_idx=p.item_idx)
+                p.k.uniform_cross_pibar_vjp_tree_from_ud_fused(
+                    Pi, col, ud, A, w.sl, w.sr, d_rhs, S, active_mask=mask, reduce_idx=w.reduce_idx,
+                    pibar_row_max=prm, skip_zero_sides=True, side_active=side_on, grad_col_log_probs=dacc.col,
+                    use_col_weights=False, side_active_threshold=so.pibar_side_threshold, **p.levels)
+                p.k.dts_backward_so(
+                    Pi, dPi, Pibar, dPibar, v, w.ws, w.meta, S, b.pd_par, b.ps_par, d.dpd_par, d.dps_par, b.mc,
+                    d.dMC, col, h["node_child1"], h["node_child2"], p.topo[0], p.topo[3], prm, p.item_idx, d_rhs,
+                    dacc.pD, dacc.pS, dacc.mt, dacc.col, use_col_weights=False, **p.levels)
+        del tf, dPi, dPibar
+        return self._e_side(d, dacc)
+
+    def _e_side(self, d, dacc):
+        """Tangent E adjoint and the tangent parameter cotangents."""
+        p, sv, a, eg = self.p, self.sv, self.acc, self.eg
+        S, G = p.S, self.G
+        E = eg.E
+        raw = d.raw
+        item = lambda t: as_item_state(t, S, G)
+        point = (E, E, sv["E_s1"], sv["E_s2"], sv["Ebar"], *eg.params[:3], eg.params[4], *p.topo)
+        along = (item(raw["dE"]), item(raw["dE"]), item(raw["dE_s1"]), item(raw["dE_s2"]), item(raw["dEbar"]),
+                 item(raw["dlog_pS"]), item(raw["dlog_pD"]), item(raw["dlog_pL"]), None)
+        zero = torch.zeros_like(E)
+        so2 = lambda g_new, g_s1, g_s2, g_ebar: p.k.e_step_backward_so(*point, g_new, g_s1, g_s2, g_ebar, *along,
+                                                                       use_col_weights=False)
+        # the loss's log2(1 - mean 2^E) term: its E gradient and that gradient's tangent
+        dE = along[0]
+        e2 = torch.exp2(E)
+        survive = (1.0 - e2.mean(dim=-1, keepdim=True)).clamp_min(torch.finfo(E.dtype).tiny)
+        per_row = 1.0 if G == p.n_fam else float(p.n_fam)
+        d_survive = -LN2 * (e2 * dE).mean(dim=-1, keepdim=True)
+        d_norm_grad = per_row * (e2 * d_survive / (S * survive * survive) - LN2 * e2 * dE / (S * survive))
+        rhs = (dacc.E + eg.aux_t(dacc.Es1, dacc.Es2, dacc.Ebar) + so2(zero, a.Es1, a.Es2, a.Ebar)[0] + d_norm_grad
+               + so2(self.wE, zero, zero, zero)[0])
+        so_p = so2(self.wE, zero, zero, a.Ebar)
+        dwE = bicgstab(lambda x: x - eg.jt(x.view_as(E)).reshape(-1), rhs.reshape(-1),
+                       max_iter=int(p.so.bicgstab_max_iter), tol=float(p.so.bicgstab_tol),
+                       breakdown_tol=float(p.so.bicgstab_breakdown_tol)).view_as(E)
+        lin = eg.params_t(dwE, dacc.Ebar)
+        return SimpleNamespace(pS=_fold(dacc.pS, lin[0] + so_p[1], G, S), pD=_fold(dacc.pD, lin[1] + so_p[2], G, S),
+                               pL=lin[2] + so_p[3], mt=dacc.mt + lin[3] + so_p[4], col=dacc.col + lin[4] + so_p[5])
+
+
+def ggn_hvp(plan: SolvePlan, theta, col_weights, saved, *, tol=None, max_sweeps=200):
+    """v -> J^T B J v, the Gauss-Newton product with B_f = ln2 (diag q_f - q_f q_f^T) per family.
+
+    J = d(root rows)/d(theta) by ``TangentForward`` (sweeping each wave to convergence);
+    J^T by the backward's reverse sweep from a root-row cotangent, without the loss's
+    normaliser term.
+    """
+    tan = TangentForward(plan, saved)
+    q = root_softmax2(saved["pi_wave"].index_select(0, plan.roots))
+
+    def hvp(v_flat):
+        v = v_flat.reshape(theta.shape).to(theta.dtype)
+        with torch.no_grad():
+            t, _ = tan.run(theta, v, tol=tol, max_sweeps=max_sweeps)
+            cot = LN2 * q * (t - (q * t).sum(dim=-1, keepdim=True))
+            acc = plan.reverse_sweep(saved, cot, use_col=False)
+        g, _ = plan.e_adjoint_and_vjp(theta, col_weights, saved, acc, use_col=False, with_norm=False)
+        return g.reshape(-1)
+
+    return hvp
+
+
+__all__ = ["TangentForward", "HvpPlan", "ggn_hvp"]

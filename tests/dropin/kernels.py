@@ -1,0 +1,99 @@
+"""Wrapper namespaces a drop-in driver calls through.
+
+``real()`` resolves every wrapper from its ``kbench.core.kernels`` module at
+call time, so a tool that replaces a module attribute (as the reference's
+capture harness does, its capture/capture.py:81-127) sees every call.
+``noop()`` has the same functions with no kernel behind them: outputs are
+zero tensors cached per shape (no allocation, no launch), in-place outputs are
+left alone.  A pass over ``noop()`` costs what the driver itself costs -- its
+Python, its own torch reductions and its host syncs -- which is the floor
+under any wrapper implementation.
+"""
+
+from __future__ import annotations
+
+import importlib
+
+import torch
+
+WRAPPERS = {
+    "compute_dts_forward": "kbench.core.kernels.dts_fused",
+    "compute_leaf_initial_wave_step": "kbench.core.kernels.wave_step",
+    "compute_wave_step": "kbench.core.kernels.wave_step",
+    "e_fixed_point_triton": "kbench.core.kernels.e_step",
+    "e_step_triton_autograd": "kbench.core.kernels.e_step",
+    "active_mask_from_rhs_absmax_fused": "kbench.core.kernels.wave_backward",
+    "wave_backward_uniform_fused": "kbench.core.kernels.wave_backward",
+    "dts_cross_backward_accum_fused": "kbench.core.kernels.wave_backward",
+    "uniform_cross_pibar_vjp_tree_from_ud_fused": "kbench.core.kernels.wave_backward",
+    "e_tangent_fixed_point": "kbench.core.kernels.e_step_tangent",
+    "compute_dts_tangent": "kbench.core.kernels.dts_tangent",
+    "compute_wave_step_tangent": "kbench.core.kernels.wave_tangent",
+    "compute_wave_step_tangent_selfloop": "kbench.core.kernels.wave_tangent",
+    "e_step_backward_so": "kbench.core.kernels.e_step_so",
+    "wave_backward_so": "kbench.core.kernels.wave_so",
+    "dts_backward_so": "kbench.core.kernels.dts_so",
+}
+
+
+class _Late:
+    """Attribute access resolves ``module.name`` on every lookup."""
+
+    def __getattr__(self, name):
+        mod = WRAPPERS.get(name)
+        if mod is None:
+            raise AttributeError(name)
+        return getattr(importlib.import_module(mod), name)
+
+
+def real():
+    return _Late()
+
+
+class _Noop:
+    """Same call surface as the wrappers, without kernels (see the module docstring)."""
+
+    def __init__(self):
+        self._zeros = {}
+
+    def _z(self, shape, like, dtype=None):
+        key = (tuple(int(s) for s in shape), dtype or like.dtype, like.device)
+        t = self._zeros.get(key)
+        if t is None:
+            t = torch.zeros(key[0], dtype=key[1], device=key[2])
+            self._zeros[key] = t
+        return t
+
+    def compute_dts_forward(self, Pi, Pibar, lefts, rights, node_child1, node_child2, W, *a, **k):
+        return self._z((int(W), int(Pi.shape[1])), Pi)
+
+    def compute_leaf_initial_wave_step(self, *a, **k):
+        return None
+
+    def compute_wave_step(self, *a, **k):
+        return None
+
+    def e_fixed_point_triton(self, E0, *a, **k):
+        return E0, E0, E0, E0
+
+    def e_step_triton_autograd(self, *a, **k):
+        return real().e_step_triton_autograd(*a, **k)
+
+    def active_mask_from_rhs_absmax_fused(self, rhs, threshold, *, use_pruning=True):
+        return self._z((int(rhs.shape[0]),), rhs, torch.bool)
+
+    def wave_backward_uniform_fused(self, Pi_star, Pibar_star, ws, W, S, *a, **k):
+        z = self._z((int(W), int(S)), Pi_star)
+        return (z,) * 7
+
+    def dts_cross_backward_accum_fused(self, Pi_star, Pibar_star, v_k, ws, sl, *a, **k):
+        n, S = int(sl.shape[0]), int(Pi_star.shape[1])
+        return (self._z((2 * n, S), Pi_star), self._z((2 * n,), Pi_star), self._z((2 * n,), Pi_star, torch.bool),
+                None, None)
+
+    def uniform_cross_pibar_vjp_tree_from_ud_fused(self, *a, **k):
+        return None
+
+
+def noop():
+    return _Noop()

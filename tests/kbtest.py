@@ -84,3 +84,35 @@ def oracle_point_cache(name: str, statewise: bool | None = None):
     theta = np.asarray(p["inputs"]["theta"], dtype=np.float32).astype(np.float64)
     cw = np.asarray(p["inputs"]["col_weights"], dtype=np.float64)
     return O.build_point_cache(prob, theta, cw, saved)
+
+
+def compare_inf_safe_t(got, ref, chunk_rows: int = 2048):
+    """Device-side ``compare_inf_safe`` for large tensors, in row chunks (float64 differences).
+
+    Returns (ok_pattern, max_abs, max_rel) with the same agreement rule.
+    """
+    import torch
+
+    g_all = got.reshape(got.shape[0], -1) if got.ndim > 1 else got.reshape(-1, 1)
+    r_all = ref.reshape(ref.shape[0], -1) if ref.ndim > 1 else ref.reshape(-1, 1)
+    assert g_all.shape == r_all.shape, (tuple(got.shape), tuple(ref.shape))
+    ma = mr = 0.0
+    for i in range(0, g_all.shape[0], chunk_rows):
+        g = g_all[i:i + chunk_rows].double()
+        r = r_all[i:i + chunk_rows].double()
+        dis = ~((g == r) | (torch.isnan(g) & torch.isnan(r)))
+        if not bool(dis.any()):
+            continue
+        gd, rd = g[dis], r[dis]
+        if not (bool(torch.isfinite(gd).all()) and bool(torch.isfinite(rd).all())):
+            return False, float("inf"), float("inf")
+        d = (gd - rd).abs()
+        ma = max(ma, float(d.max()))
+        mr = max(mr, float((d / rd.abs().clamp_min(1e-12)).max()))
+    return True, ma, mr
+
+
+def norm_rel_t(got, ref) -> float:
+    """Device-side ``norm_rel``."""
+    den = max(float(ref.double().abs().max()), 1e-300)
+    return float((got.double() - ref.double()).abs().max()) / den

@@ -1,5 +1,5 @@
 """GPU parity of the second-order wrappers (kbench.core.kernels.{e_step,wave,dts}_so) and of the
-exact / Gauss-Newton HVP glue (newton.hvp_exact, newton.ggn) against the float64 CPU oracle.
+exact / Gauss-Newton HVP call sequences (tests/dropin/hvp.py) against the float64 CPU oracle.
 
 Kernel tests feed the oracle's primal point and random tangents / cotangents
 to the HIP wrappers in float64 (tight tolerance) and float32 (rel 1e-4).  The
@@ -188,13 +188,13 @@ def test_dts_backward_so_matches_oracle(dt, statewise):
 
 @pytest.mark.parametrize("name,statewise", [("tiny", None), ("tiny", True), ("1", True)])
 def test_exact_hvp_matches_oracle(name, statewise):
-    from kbench.runtime import run_forward
-    from newton.hvp_exact import make_exact_hvp
+    from dropin.hvp import HvpPlan
+    from dropin.solve import plan_of, run_forward
 
     print(f"[hvp] config={name} statewise={statewise}", flush=True)
     static, theta, cw = _static(name, statewise)
     _, sv = run_forward(static, theta, cw)
-    hvp = make_exact_hvp(static, theta, cw, sv)
+    hvp = HvpPlan(plan_of(static), theta, cw, sv)
     u = np.random.default_rng(34).normal(size=tuple(theta.shape))
     Hu = hvp(torch.as_tensor(u, dtype=theta.dtype).cuda().reshape(-1))
     torch.cuda.synchronize()
@@ -211,14 +211,14 @@ def test_exact_hvp_config3_symmetric_linear_deterministic():
     """Full size (config 3 with per-species theta, the Newton-CG setup): symmetry, linearity, determinism."""
     import time
 
-    from kbench.runtime import run_forward
-    from newton.hvp_exact import make_exact_hvp
+    from dropin.hvp import HvpPlan
+    from dropin.solve import plan_of, run_forward
 
     print("[hvp] config=3 statewise=True", flush=True)
     static, theta, cw = _static("3", True)
     _, sv = run_forward(static, theta, cw)
     t0 = time.perf_counter()
-    hvp = make_exact_hvp(static, theta, cw, sv)
+    hvp = HvpPlan(plan_of(static), theta, cw, sv)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     g = np.random.default_rng(35)
@@ -244,12 +244,12 @@ def test_exact_hvp_config3_symmetric_linear_deterministic():
 
 
 def test_ggn_hvp_is_symmetric_and_psd():
-    from kbench.runtime import run_forward
-    from newton.ggn import make_ggn_hvp
+    from dropin.hvp import ggn_hvp
+    from dropin.solve import plan_of, run_forward
 
     static, theta, cw = _static("1", True)
     _, sv = run_forward(static, theta, cw)
-    hvp = make_ggn_hvp(static, theta, cw, sv)
+    hvp = ggn_hvp(plan_of(static), theta, cw, sv)
     g = np.random.default_rng(36)
     u1 = torch.as_tensor(g.normal(size=tuple(theta.shape)), dtype=theta.dtype).cuda().reshape(-1)
     u2 = torch.as_tensor(g.normal(size=tuple(theta.shape)), dtype=theta.dtype).cuda().reshape(-1)

@@ -1,5 +1,5 @@
 """GPU parity of the forward-tangent wrappers (kbench.core.kernels.{e_step,dts,wave}_tangent) and of the
-JVP glue (newton.forward_tangent.jvp_root_scores) against the float64 CPU oracle.
+forward-tangent call sequence (tests/dropin/hvp.py ``TangentForward``) against the float64 CPU oracle.
 
 Kernel tests feed the oracle's own primal point (Pi*, E*, ...) to the HIP
 wrappers, in float64 (tight tolerance: same arithmetic up to summation order)
@@ -176,15 +176,16 @@ def test_wave_step_tangent_matches_oracle(dt, n_iters):
 
 @pytest.mark.parametrize("name,statewise", [("tiny", None), ("1", None), ("1", True)])
 def test_jvp_root_scores_matches_oracle(name, statewise):
-    from kbench.runtime import run_forward
-    from newton.forward_tangent import jvp_root_scores
+    from dropin.hvp import TangentForward
+    from dropin.solve import plan_of, run_forward
 
     print(f"[jvp] config={name} statewise={statewise}", flush=True)
     static, theta, cw = _static(name, statewise)
     _, sv = run_forward(static, theta, cw)
     v = torch.as_tensor(np.random.default_rng(14).normal(size=tuple(theta.shape)), dtype=theta.dtype).cuda()
     n_it = int(static.solver_options.pi_iters)
-    roots, full = jvp_root_scores(static, theta, v, sv, self_iters=n_it, return_full=True)
+    roots, full = TangentForward(plan_of(static), sv).run(theta, v, sweeps=n_it)
+    full = {"dPi": full.dPi, "dPibar": full.dPibar}
     torch.cuda.synchronize()
     prob, _, saved = kbtest.oracle_forward(name, statewise)
     th = np.asarray(kbtest.problem(name, statewise)["inputs"]["theta"], dtype=np.float32).astype(np.float64)
@@ -197,17 +198,18 @@ def test_jvp_root_scores_matches_oracle(name, statewise):
 
 
 def test_jvp_root_scores_adaptive_and_unfused_paths_agree():
-    """The three self-loop modes of jvp_root_scores solve the same tangent (config 1)."""
-    from kbench.runtime import run_forward
-    from newton.forward_tangent import jvp_root_scores
+    """The three self-loop modes of the tangent forward solve the same tangent (config 1)."""
+    from dropin.hvp import TangentForward
+    from dropin.solve import plan_of, run_forward
 
     static, theta, cw = _static("1", True)
     _, sv = run_forward(static, theta, cw)
     v = torch.as_tensor(np.random.default_rng(15).normal(size=tuple(theta.shape)), dtype=theta.dtype).cuda()
-    a = jvp_root_scores(static, theta, v, sv, self_iters=6)
-    b = jvp_root_scores(static, theta, v, sv, self_iters=6, fused_selfloop=False)
-    c = jvp_root_scores(static, theta, v, sv, self_iters=None, self_tol=1e-7, self_max_iter=200)
-    d = jvp_root_scores(static, theta, v, sv, self_iters=60)
+    tf = TangentForward(plan_of(static), sv)
+    a = tf.run(theta, v, sweeps=6)[0]
+    b = tf.run(theta, v, sweeps=6, one_call=False)[0]
+    c = tf.run(theta, v, sweeps=None, tol=1e-7, max_sweeps=200)[0]
+    d = tf.run(theta, v, sweeps=60)[0]
     torch.cuda.synchronize()
     assert _rel(a.cpu().numpy(), b.cpu().numpy()) <= 1e-5
     assert _rel(c.cpu().numpy(), d.cpu().numpy()) <= 1e-4
@@ -215,12 +217,14 @@ def test_jvp_root_scores_adaptive_and_unfused_paths_agree():
 
 def test_jvp_root_scores_config3_linear_and_deterministic():
     """Full size (config 3): the JVP is linear in v and bitwise reproducible."""
-    from kbench.runtime import run_forward
-    from newton.forward_tangent import jvp_root_scores
+    from dropin.hvp import TangentForward
+    from dropin.solve import plan_of, run_forward
 
     print("[jvp] config=3", flush=True)
     static, theta, cw = _static("3")
     _, sv = run_forward(static, theta, cw)
+    tf = TangentForward(plan_of(static), sv)
+    jvp_root_scores = lambda static, theta, v, sv, self_iters: tf.run(theta, v, sweeps=self_iters)[0]
     g = np.random.default_rng(16)
     v1 = torch.as_tensor(g.normal(size=tuple(theta.shape)), dtype=theta.dtype).cuda()
     v2 = torch.as_tensor(g.normal(size=tuple(theta.shape)), dtype=theta.dtype).cuda()

@@ -1,10 +1,10 @@
-"""GPU parity of the drop-in wrappers (kbench.core.kernels.*) driven by the glue.
+"""GPU parity of the drop-in wrappers (kbench.core.kernels.*) driven in the reference glue's call sequence.
 
-``kbench.runtime.run_forward`` / ``run_backward`` run the glue counterparts
-(core/inference/solver.py, forward.py, api/_implicit_grad.py), which call the
-HIP-backed wrappers with the reference's call sequence.  Checked against the
-float64 CPU oracle (loss rel 1e-5, gradients rel 1e-4, active masks exact), for
-determinism, and against the native whole-pass driver.
+``dropin.run_forward`` / ``run_backward`` (tests/dropin/solve.py) call the
+HIP-backed wrappers with the reference glue's sequence and arguments.  Checked
+against the float64 CPU oracle (loss rel 1e-5, gradients rel 1e-4, active masks
+exact), for determinism, and against the native whole-pass driver
+(``kbench.runtime``).
 """
 
 import numpy as np
@@ -28,7 +28,7 @@ def _static(name, statewise=None):
 
 @pytest.mark.parametrize("name,statewise", [("tiny", None), ("1", None), ("1", True), ("2", None)])
 def test_glue_forward_matches_oracle(name, statewise):
-    from kbench.runtime import run_forward
+    from dropin import run_forward
 
     print(f"[glue-forward] config={name} statewise={statewise}", flush=True)
     static, theta, cw = _static(name, statewise)
@@ -50,7 +50,7 @@ def test_glue_forward_matches_oracle(name, statewise):
 
 @pytest.mark.parametrize("name,statewise", [("tiny", None), ("1", None), ("1", True)])
 def test_glue_backward_matches_oracle(name, statewise):
-    from kbench.runtime import run_backward, run_forward
+    from dropin import run_backward, run_forward
 
     print(f"[glue-backward] config={name} statewise={statewise}", flush=True)
     static, theta, cw = _static(name, statewise)
@@ -65,7 +65,7 @@ def test_glue_backward_matches_oracle(name, statewise):
 
 
 def test_glue_backward_is_deterministic():
-    from kbench.runtime import run_backward, run_forward
+    from dropin import run_backward, run_forward
 
     static, theta, cw = _static("1", True)
     loss, saved = run_forward(static, theta, cw)
@@ -77,7 +77,8 @@ def test_glue_backward_is_deterministic():
 
 def test_glue_matches_fused_driver_config2():
     """The per-wrapper path and the whole-pass driver solve the same problem (forward, config 2)."""
-    from kbench.runtime import run_forward, run_forward_fused
+    from dropin import run_forward
+    from kbench.runtime import run_forward as run_forward_fused
 
     static, theta, cw = _static("2")
     l1, s1 = run_forward(static, theta, cw)
@@ -116,7 +117,7 @@ def test_active_mask_bit_exact():
 def test_wave_step_in_place_matches_out_of_place():
     """Pi_out may alias Pi_in and Pibar (the glue's even sweeps write into the Pibar buffer)."""
     from kbench.core.kernels.wave_step import compute_wave_step
-    from kbench.runtime import run_forward
+    from dropin import run_forward
 
     static, theta, cw = _static("1", True)
     loss, saved = run_forward(static, theta, cw)
@@ -151,7 +152,8 @@ def test_wave_step_in_place_matches_out_of_place():
 
 def test_glue_config3_forward_matches_fused():
     """Full-size drop-in check: config 3 forward through the wrappers equals the whole-pass driver."""
-    from kbench.runtime import run_forward, run_forward_fused
+    from dropin import run_forward
+    from kbench.runtime import run_forward as run_forward_fused
 
     print("[glue-forward] config=3", flush=True)
     static, theta, cw = _static("3")

@@ -96,6 +96,21 @@ typedef struct kb_estep_vjp_io {
 int kb_estep_vjp(const kb_tree* tree, const kb_estep_vjp_io* io, void* stream);
 
 /*
+ * kb_estep_vjp without a work buffer and without any device allocation.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight solver loops such as the
+ * E-adjoint BiCGSTAB, harnesses that forbid hipMalloc).  io->work must be NULL;
+ * the [G, S] float64 staging rows live in a device array of the library,
+ * KB_ESTEP_VJP_NOALLOC_MAX doubles (512 KiB) on each GPU for the life of the
+ * process, so G * S must not exceed KB_ESTEP_VJP_NOALLOC_MAX (else KB_ERR_ARG).
+ * Same kernels and results as kb_estep_vjp.  Every call on one GPU shares that
+ * array: calls that overlap on one GPU (concurrent streams, or host threads)
+ * race and must be serialised by the caller.
+ */
+#define KB_ESTEP_VJP_NOALLOC_MAX 65536
+int kb_estep_vjp_noalloc(const kb_tree* tree, const kb_estep_vjp_io* io, void* stream);
+
+/*
  * Self-loop constants addressing, shared by the wave kernels: constant row
  * of wave row w is  const + item_idx[ws + w] * const_stride  (const_stride 0:
  * one shared row), as the reference's CONST_ROW_STRIDE (pristine

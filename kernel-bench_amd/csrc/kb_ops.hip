@@ -18,6 +18,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <mutex>
 #include <vector>
 
 #include "kb_ops_common.hpp"
@@ -1103,6 +1104,12 @@ __global__ __launch_bounds__(256) void rows_sum_stage2(int S, int n_chunks, cons
 
 }  // namespace kbo
 
+// Device scratch of kb_estep_vjp_noalloc: the [G, S] float64 grad_col
+// contributions.  Each GPU holds its own copy for the life of the process; in
+// host code its name is only a symbol handle, so the address used in launches
+// comes from hipGetSymbolAddress (scratch_on_current_device below).
+static __device__ __align__(256) double scratch[KB_ESTEP_VJP_NOALLOC_MAX];
+
 // =====================================================================================
 // host side
 // =====================================================================================
@@ -1110,6 +1117,23 @@ __global__ __launch_bounds__(256) void rows_sum_stage2(int S, int n_chunks, cons
 namespace {
 
 using namespace kbo_host;
+
+// Address of `scratch` on the current device, looked up once per device.
+int scratch_on_current_device(double** out) {
+  static std::mutex mu;
+  static std::vector<double*> addr;  // by device ordinal; nullptr until looked up
+  int dev = -1;
+  KBO_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(mu);
+  if ((int)addr.size() <= dev) addr.resize(dev + 1, nullptr);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    KBO_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    addr[dev] = static_cast<double*>(p);
+  }
+  *out = addr[dev];
+  return 0;
+}
 
 
 int put(int** dst, const std::vector<int>& v) {
@@ -1249,10 +1273,12 @@ int kb_estep(const kb_tree* tr, const kb_estep_io* io, void* stream) {
   return 0;
 }
 
-int kb_estep_vjp(const kb_tree* tr, const kb_estep_vjp_io* io, void* stream) {
-  if (!tr || !io || !io->work) return kb::set_error(KB_ERR_ARG, "null argument");
-  if (int rc = dtype_ok(io->dtype)) return rc;
-  if (io->G <= 0) return kb::set_error(KB_ERR_ARG, "G must be positive");
+}  // extern "C"
+
+namespace {
+
+// The E-step VJP launches with `work` ([G, S] float64) as the grad_col staging rows.
+int estep_vjp_launch(const kb_tree* tr, const kb_estep_vjp_io* io, double* work, void* stream) {
   const int S = tr->S;
   const size_t lds = (size_t)2 * S * sizeof(double);
   if (int rc = check_lds(lds, S, KB_F64)) return rc;
@@ -1263,16 +1289,40 @@ int kb_estep_vjp(const kb_tree* tr, const kb_estep_vjp_io* io, void* stream) {
                      (const T*)io->log_pS, (const T*)io->log_pD, (const T*)io->log_pL, (const T*)io->col_log_probs,
                      (const T*)io->g_E_new, (const T*)io->g_E_s1, (const T*)io->g_E_s2, (const T*)io->g_Ebar,
                      (T*)io->grad_E, (T*)io->grad_log_pS, (T*)io->grad_log_pD, (T*)io->grad_log_pL,
-                     (T*)io->grad_max_coupling, io->work};
+                     (T*)io->grad_max_coupling, work};
     auto k = kbo::estep_vjp_kernel<T, CPT>;
     if (int rc = set_lds(k, lds)) return rc;
     hipLaunchKernelGGL(k, dim3(io->G), dim3(kbo::NT), lds, st_of(stream), t, a);
-    // grad_col = sum over item rows of the per-row contributions (written, not accumulated)
+    // grad_col += sum over item rows of the per-row contributions (fixed row order)
     hipLaunchKernelGGL((kbo::rows_sum_stage2<T>), dim3((S + 255) / 256), dim3(256), 0, st_of(stream), S, io->G,
-                       (const double*)io->work, (T*)io->grad_col_log_probs);
+                       (const double*)work, (T*)io->grad_col_log_probs);
   });
   KBO_HIP(hipGetLastError());
   return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kb_estep_vjp(const kb_tree* tr, const kb_estep_vjp_io* io, void* stream) {
+  if (!tr || !io || !io->work) return kb::set_error(KB_ERR_ARG, "null argument");
+  if (int rc = dtype_ok(io->dtype)) return rc;
+  if (io->G <= 0) return kb::set_error(KB_ERR_ARG, "G must be positive");
+  return estep_vjp_launch(tr, io, io->work, stream);
+}
+
+int kb_estep_vjp_noalloc(const kb_tree* tr, const kb_estep_vjp_io* io, void* stream) {
+  if (!tr || !io) return kb::set_error(KB_ERR_ARG, "null argument");
+  if (io->work) return kb::set_error(KB_ERR_ARG, "kb_estep_vjp_noalloc takes no work buffer (io->work must be NULL)");
+  if (int rc = dtype_ok(io->dtype)) return rc;
+  if (io->G <= 0) return kb::set_error(KB_ERR_ARG, "G must be positive");
+  if ((int64_t)io->G * tr->S > (int64_t)KB_ESTEP_VJP_NOALLOC_MAX)
+    return kb::set_error(KB_ERR_ARG, "kb_estep_vjp_noalloc: G * S = %lld exceeds its scratch of %d doubles",
+                         (long long)io->G * tr->S, (int)KB_ESTEP_VJP_NOALLOC_MAX);
+  double* work = nullptr;
+  if (int rc = scratch_on_current_device(&work)) return rc;
+  return estep_vjp_launch(tr, io, work, stream);
 }
 
 int kb_wave_step(const kb_tree* tr, const kb_wave_step_io* io, void* stream) {

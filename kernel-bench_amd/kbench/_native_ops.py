@@ -132,6 +132,7 @@ def declare(lib) -> None:
     fn("kb_ops_max_states", [ct.c_int])
     fn("kb_estep", [vp, ct.POINTER(KbEStepIO), vp])
     fn("kb_estep_vjp", [vp, ct.POINTER(KbEStepVjpIO), vp])
+    fn("kb_estep_vjp_noalloc", [vp, ct.POINTER(KbEStepVjpIO), vp])
     fn("kb_wave_step", [vp, ct.POINTER(KbWaveStepIO), vp])
     fn("kb_leaf_init", [ct.POINTER(KbLeafInitIO), vp])
     fn("kb_dts_forward", [ct.POINTER(KbDtsIO), vp])

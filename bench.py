@@ -2,21 +2,34 @@
 """Benchmark of the log-space solver path on one MI355X.
 
 Workload: Yule species tree with 1024 leaves (S = 2047 state
-columns), 500 DTL-simulated families with 3 NNI variants each (C ~ 33.7k clade
-rows in size-waves), per-species theta, fp32, pi_iters = 16, neumann_terms = 16.
-A step is one whole solve: forward (E-step fixed point, all waves, loss) plus
-backward (adjoint over all waves, E adjoint, theta / column VJP), run through
-the native whole-pass driver with every input already in HBM.
+columns), 500 DTL-simulated families with 3 NNI variants each (C = 33686 clade
+rows in 144 size-waves), per-species theta, fp32, pi_iters = 16,
+neumann_terms = 16.  A step is one whole solve: forward (E-step fixed point,
+every row's sweeps, loss) plus backward (adjoint over every row, E adjoint,
+theta / column VJP), run through the native whole-pass driver with every
+input already in HBM.  Rows with identical inputs (row classes) are computed
+once in the forward; the line states how many rows that is and also times the
+solve with every row computed (``KB_DEDUP=0``).
 
-Prints ONE JSON line (rank 0).  ``value`` is ms per solve (fwd + bwd), lower is
-better.  ``roofline`` reports the dominant wave kernel: algorithmic HBM bytes
-per launch (S*4 bytes per row: forward writes Pi and Pibar and reads four child
-rows per split; backward reads Pi*, Pibar* and the adjoint per row and four
-child rows plus two adjoint rows per split) divided by its launch durations,
-measured with HIP events on the launch stream in a second timed pass.
-``cpu_baseline`` times the float64 CPU oracle on a bounded sample of the same
-workload (the config-3 species tree with its first 20 families) and scales it
-by row count to one full solve.
+Prints ONE JSON line.  ``value`` is ms per solve (fwd + bwd, HIP events),
+lower is better.
+
+* ``roofline``: the dominant row kernel's algorithmic HBM bytes per launch
+  (S*4 bytes per row: the backward reads Pi*, Pibar* and the adjoint of every
+  row and four child rows plus two adjoint rows per split) over its launch
+  durations, measured with HIP events on the launch stream in a second timed
+  pass; ``traffic`` and the VALU / LDS figures come from the committed
+  rocprofv3 counter summaries of this command (profiles/).
+* ``cpu_baseline``: the float64 CPU oracle on the box's host cores, computed
+  before the GPU is touched: a bounded sample of the config-3 families packed
+  by rows into one shard per worker process (the loss and gradients of a
+  problem are sums over its family shards), scaled by rows to a full solve;
+  beside it, config 1 (BASELINE's CPU case) solved in full the same way.
+* ``per_call``: the same solve through the per-call wrappers in the reference
+  glue's call sequence (``tests/dropin``): one launch per sweep and per wave
+  as the reference launches them (the pristine-structure proxy), the same with
+  each wave's sweep chain collapsed into one launch (``KBENCH_FUSE_SWEEPS``),
+  and the driver's own floor (every wrapper replaced by a no-op).
 """
 
 from __future__ import annotations
@@ -34,6 +47,7 @@ sys.path.insert(0, str(ROOT / "kernel-bench_amd"))
 
 HBM_PEAK_GBS = 8000.0
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_config3.json"
+COUNTERS_FILE = ROOT / "profiles" / "sq_counters_config3.json"
 
 
 def parse():
@@ -43,15 +57,24 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-families", type=int, default=20)
+    ap.add_argument("--cpu-workers", type=int, default=0,
+                    help="worker processes of the CPU baseline (default: the host cores, at most 16)")
+    ap.add_argument("--cpu-families-per-worker", type=int, default=2)
+    ap.add_argument("--no-per-call", action="store_true", help="skip the per-call (drop-in) timings")
+    ap.add_argument("--no-dedup-off", action="store_true", help="skip the KB_DEDUP=0 timing")
     ap.add_argument("--verbose", action="store_true")
     ap.add_argument("--workload", choices=("solve", "glue", "hvp"), default="solve",
-                    help="solve: whole-pass driver (the metric); glue: the same solve through the per-wrapper "
-                         "drop-in path; hvp: exact Hessian-vector products of the config-5 Newton-CG setup")
+                    help="solve: whole-pass driver (the metric); glue: only the per-call drop-in timings; "
+                         "hvp: exact Hessian-vector products of the config-5 Newton-CG setup")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 5 plain copy kernels of MIB MiB (read + write), the reference point "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters to HBM bytes")
     return ap.parse_args()
+
+
+def log(args, msg):
+    if args.verbose:
+        print(msg, file=sys.stderr, flush=True)
 
 
 def calibrate_copy(mib: int) -> None:
@@ -68,98 +91,222 @@ def calibrate_copy(mib: int) -> None:
                       "bytes_read_per_launch": n * 4, "bytes_written_per_launch": n * 4}))
 
 
-def log(args, msg):
-    if args.verbose:
-        print(msg, file=sys.stderr, flush=True)
-
-
-def cpu_baseline(args, full_rows: int) -> dict:
-    """Oracle fwd+bwd on the config's tree with its first families, scaled by rows."""
-    import dataclasses
-
-    os.environ.setdefault("OMP_NUM_THREADS", "1")
-    sys.path.insert(0, str(ROOT / "oracle"))
+# ---------------------------------------------------------------------- CPU baseline
+def _oracle_solve(sub: dict) -> tuple:
+    """Oracle forward + backward of one family shard (runs in a worker process, one thread)."""
     import numpy as np
+    from threadpoolctl import threadpool_limits
 
     import kbench_oracle as O
+
+    with threadpool_limits(1):
+        t0 = time.perf_counter()
+        prob = O.Problem.from_dict(sub)
+        th = np.asarray(sub["inputs"]["theta"], dtype=np.float64)
+        cw = np.asarray(sub["inputs"]["col_weights"], dtype=np.float64)
+        loss, saved = O.forward(prob, th, cw)
+        gt, gc, _ = O.backward(prob, th, cw, saved)
+        return loss, gt, gc, time.perf_counter() - t0
+
+
+def _sharded_oracle(problem: dict, families, workers: int) -> dict:
+    """Wall time of the oracle over ``families`` split into ``workers`` family shards."""
+    import multiprocessing as mp
+
     from kbench import synth
 
-    cfg = dataclasses.replace(synth.config(args.config), n_families=args.cpu_sample_families)
-    p = synth.build_problem(cfg)
-    prob = O.Problem.from_dict(p)
-    theta = np.asarray(p["inputs"]["theta"], dtype=np.float64)
-    cw = np.asarray(p["inputs"]["col_weights"], dtype=np.float64)
-    t0 = time.perf_counter()
-    _, saved = O.forward(prob, theta, cw)
-    O.backward(prob, theta, cw, saved)
-    dt = time.perf_counter() - t0
-    rows = int(p["meta"]["C"])
+    import numpy as np
+
+    fams = list(families)
+    # greedy packing by rows, largest family first, onto the least loaded shard
+    fam_rows = np.bincount(np.asarray(problem["static"]["wave_layout"]["item_idx"]))
+    shards, load = [[] for _ in range(workers)], [0] * workers
+    for f in sorted(fams, key=lambda f: -int(fam_rows[f])):
+        i = load.index(min(load))
+        shards[i].append(f)
+        load[i] += int(fam_rows[f])
+    subs = [synth.family_subset(problem, sorted(s)) for s in shards if s]
+    rows = sum(int(s["meta"]["C"]) for s in subs)
+    # fork before the process touches the GPU (main() calls this first)
+    with mp.get_context("fork").Pool(len(subs)) as pool:
+        t0 = time.perf_counter()
+        parts = pool.map(_oracle_solve, subs)
+        wall = time.perf_counter() - t0
+    return {"wall_s": wall, "rows": rows, "families": len(fams), "shards": len(subs),
+            "loss": float(sum(p[0] for p in parts)), "busiest_shard_s": max(p[3] for p in parts),
+            "cpu_s": sum(p[3] for p in parts)}
+
+
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(args, problem: dict) -> dict:
+    """The CPU path on this host's cores (see the module docstring)."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    from kbench import synth
+
+    avail = len(os.sched_getaffinity(0))
+    workers = args.cpu_workers or min(16, avail)
+    C = int(problem["meta"]["C"])
+    sample = _sharded_oracle(problem, range(min(int(problem["meta"]["n_items"]),
+                                                 workers * args.cpu_families_per_worker)), workers)
+    # a full solve's 500 families pack evenly onto the workers: its time is the
+    # sample's CPU seconds per row times C rows over the workers
+    value = sample["cpu_s"] * 1e3 * C / sample["rows"] / workers
+    p1 = synth.build_problem(synth.config("1"))
+    full1 = _sharded_oracle(p1, range(int(p1["meta"]["n_items"])), workers)
     return {
-        "value": dt * 1e3 * full_rows / rows,
-        "unit": "ms per solve (fwd+bwd, scaled by rows)",
-        "cores": 1,
+        "value": round(value, 1),
+        "unit": f"ms per config-{args.config} solve (fwd+bwd) on {workers} cores, scaled by rows from the sample",
+        "cores": workers,
         "kind": "port",
-        "sample": (f"float64 numpy oracle, config-{args.config} species tree with its first "
-                   f"{args.cpu_sample_families} families ({rows} of {full_rows} rows), fwd+bwd "
-                   f"{dt:.2f} s on 1 host core, scaled by {full_rows}/{rows}"),
+        "sample": (f"float64 numpy oracle (one thread per process), the first {sample['families']} of the "
+                   f"config-{args.config} families packed by rows into {sample['shards']} shards on {workers} worker "
+                   f"processes: {sample['rows']} of {C} rows, {sample['cpu_s']:.1f} worker CPU-s "
+                   f"({sample['wall_s']:.2f} s wall, busiest shard {sample['busiest_shard_s']:.2f} s); "
+                   f"value = CPU-s per row x {C} rows / {workers} workers"),
+        "host": {"affinity_cores": avail, "workers": workers, "cpu": _cpu_model()},
+        "config1_full": {"ms": round(full1["wall_s"] * 1e3, 1), "rows": full1["rows"],
+                         "families": full1["families"], "workers": full1["shards"],
+                         "note": "BASELINE config 1 (S=127, fp64 oracle) solved in full, fwd+bwd, wall time"},
     }
 
 
-def bench_other(args, static, theta, cw, summ) -> None:
-    """Secondary workloads (not the metric): the per-wrapper solve and the exact HVP."""
-    import numpy as np
+# ---------------------------------------------------------------------- per-call (drop-in) path
+def _time_host(step, warmup: int, steps: int) -> float:
     import torch
 
-    sys.path.insert(0, str(ROOT / "tests"))  # the call-sequence drivers of the per-call wrappers
-    from dropin.solve import plan_of, run_backward, run_forward
-
-    cfg = {"S_columns": summ["S"], "C": summ["C"], "n_waves": summ["n_waves"], "n_splits": summ["n_splits"]}
-    if args.workload == "glue":
-        def step():
-            loss, sv = run_forward(static, theta, cw)
-            run_backward(static, theta, cw, sv)
-            return loss
-
-        metric = "fwd+bwd ms per solve through the per-wrapper drop-in path (reference glue call sequence)"
-    else:
-        from dropin.hvp import HvpPlan
-
-        loss, sv = run_forward(static, theta, cw)
-        t0 = time.perf_counter()
-        hvp = HvpPlan(plan_of(static), theta, cw, sv)
-        torch.cuda.synchronize()
-        cfg["point_cache_ms"] = round((time.perf_counter() - t0) * 1e3, 3)
-        g = np.random.default_rng(0)
-        us = [torch.as_tensor(g.normal(size=tuple(theta.shape)), dtype=theta.dtype, device=theta.device).reshape(-1)
-              for _ in range(4)]
-        k = [0]
-
-        def step():
-            k[0] += 1
-            return hvp(us[k[0] % len(us)])
-
-        metric = "exact Hessian-vector product ms (config 5: per-species theta, forward tangent + tangent adjoint)"
-    for i in range(args.warmup):
+    for _ in range(warmup):
         step()
-        torch.cuda.synchronize()
-        log(args, f"[bench] warmup {i + 1}/{args.warmup}")
-    times = []
-    for i in range(args.steps):
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(steps):
         torch.cuda.synchronize()
         t = time.perf_counter()
         step()
         torch.cuda.synchronize()
-        times.append((time.perf_counter() - t) * 1e3)
-        log(args, f"[bench] step {i + 1}/{args.steps}: {times[-1]:.3f} ms")
-    ms = statistics.mean(times)
-    out = {"metric": metric, "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
-           "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
-           "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
-           "config": dict(workload=f"config{args.config} {args.workload}", **cfg),
-           "median_ms": round(statistics.median(times), 4), "min_ms": round(min(times), 4)}
-    if args.workload == "hvp":
-        out["ms_per_newton_cg_step_50_hvps"] = round(50 * ms, 2)
-    print(json.dumps(out))
+        ts.append((time.perf_counter() - t) * 1e3)
+    return statistics.median(ts)
+
+
+def per_call_timings(static, theta, cw, steps: int = 3) -> dict:
+    """ms per solve through the per-call wrappers in the reference glue's call sequence."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from dropin.kernels import noop
+    from dropin.solve import SolvePlan
+    from kbench.core.kernels import wave_step
+
+    plan = SolvePlan(static)
+    floor_plan = SolvePlan(static, kernels=noop())
+
+    def solve(p):
+        def step():
+            loss, sv = p.forward(theta, cw)
+            p.backward(theta, cw, sv)
+        return step
+
+    old = wave_step.FUSE_SWEEPS
+    try:
+        wave_step.FUSE_SWEEPS = False
+        per_launch = _time_host(solve(plan), 1, steps)
+        wave_step.FUSE_SWEEPS = True
+        fused = _time_host(solve(plan), 1, steps)
+    finally:
+        wave_step.FUSE_SWEEPS = old
+    floor = _time_host(solve(floor_plan), 1, steps)
+    return {
+        "ms_one_launch_per_sweep": round(per_launch, 3),
+        "ms_sweep_chains_fused": round(fused, 3),
+        "ms_glue_floor": round(floor, 3),
+        "note": ("host wall time (median of %d) of a fwd+bwd solve through the per-call wrappers in the "
+                 "reference glue's call sequence: one launch per sweep and wave as the reference launches "
+                 "them (the pristine-structure proxy); the same with KBENCH_FUSE_SWEEPS=1 (each wave's sweep "
+                 "chain in one launch); the driver alone with no-op wrappers" % steps),
+    }
+
+
+def bench_hvp(args, static, theta, cw, summ) -> None:
+    """Exact Hessian-vector products (config 5) through the per-call wrappers."""
+    import numpy as np
+    import torch
+
+    sys.path.insert(0, str(ROOT / "tests"))
+    from dropin.hvp import HvpPlan
+    from dropin.solve import plan_of, run_forward
+
+    _, sv = run_forward(static, theta, cw)
+    t0 = time.perf_counter()
+    hvp = HvpPlan(plan_of(static), theta, cw, sv)
+    torch.cuda.synchronize()
+    cache_ms = (time.perf_counter() - t0) * 1e3
+    g = np.random.default_rng(0)
+    us = [torch.as_tensor(g.normal(size=tuple(theta.shape)), dtype=theta.dtype, device=theta.device).reshape(-1)
+          for _ in range(4)]
+    k = [0]
+
+    def step():
+        k[0] += 1
+        hvp(us[k[0] % len(us)])
+
+    ms = _time_host(step, args.warmup, args.steps)
+    print(json.dumps({
+        "metric": "exact Hessian-vector product ms (config 5: per-species theta, forward tangent + tangent adjoint)",
+        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": f"config{args.config} exact HVP through the per-call wrappers", "S": summ["S"],
+                   "C": summ["C"], "point_cache_ms": round(cache_ms, 3)},
+        "ms_per_newton_cg_step_50_hvps": round(50 * ms, 2),
+    }))
+
+
+# ---------------------------------------------------------------------- the solve metric
+def _counters(kernel_symbol: str):
+    """VALU / LDS figures of the committed rocprofv3 SQ-counter summary for ``kernel_symbol``."""
+    if not COUNTERS_FILE.exists():
+        return None
+    rec = json.loads(COUNTERS_FILE.read_text()).get("kernels", {})
+    hits = {k: v for k, v in rec.items() if kernel_symbol in k}
+    return hits or None
+
+
+def _traffic(kernel_symbol: str):
+    if not TRAFFIC_FILE.exists():
+        return None
+    # HBM bytes per dispatch from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this command,
+    # scaled by a copy kernel of known size; a kernel launched in several shapes: the
+    # dispatch-weighted mean over them
+    rec = json.loads(TRAFFIC_FILE.read_text()).get("kernels", {})
+    hits = [v for k, v in rec.items() if kernel_symbol in k]
+    n = sum(float(v["dispatches"]) for v in hits)
+    return round(sum(float(v["traffic"]) * float(v["dispatches"]) for v in hits) / n, 1) if n else None
+
+
+def _timed_solves(solver, theta, cw, steps: int):
+    """HIP-event times (total, fwd, bwd) of ``steps`` solves; a failed E-adjoint solve raises."""
+    import torch
+
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    for a, m, b in ev:
+        a.record()
+        loss, saved = solver.run_forward(theta, cw)
+        m.record()
+        solver.run_backward(theta, cw, saved, check_solve=False)
+        b.record()
+        solver.backward_stats()  # raises RuntimeError if the E-adjoint BiCGSTAB failed
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t_wall) * 1e3 / steps
+    return ([a.elapsed_time(b) for a, _, b in ev], [a.elapsed_time(m) for a, m, _ in ev],
+            [m.elapsed_time(b) for _, m, b in ev], wall, loss)
 
 
 def main():
@@ -172,10 +319,18 @@ def main():
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)
         return
+    from kbench import synth
+
+    t0 = time.time()
+    problem = synth.build_problem(synth.config(args.config))
+    summ = synth.summary(problem)
+    # the CPU baseline forks its workers before anything touches the GPU
+    cpu = None if (args.no_cpu_baseline or args.workload != "solve") else cpu_baseline(args, problem)
+    log(args, f"[bench] problem + cpu baseline {time.time() - t0:.1f}s {summ}")
+
     import numpy as np
     import torch
 
-    from kbench import synth
     from kbench.fused import FusedSolver, problem_to_captured
     from kbench.runtime import make_static
 
@@ -184,58 +339,34 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    t0 = time.time()
-    problem = synth.build_problem(synth.config(args.config))
-    summ = synth.summary(problem)
     cap = problem_to_captured(problem)
     static = make_static(cap, dev)
-    solver = FusedSolver(static, static.solver_options)
     theta = cap["inputs"]["theta"].to(dev)
     cw = cap["inputs"]["col_weights"].to(dev)
-    log(args, f"[bench] setup {time.time() - t0:.1f}s {summ}")
-    if args.workload != "solve":
-        return bench_other(args, static, theta, cw, summ)
-
-    def step():
-        loss, saved = solver.run_forward(theta, cw)
-        gt, gc = solver.run_backward(theta, cw, saved)
-        return loss, gt, gc
-
+    if args.workload == "hvp":
+        return bench_hvp(args, static, theta, cw, summ)
+    if args.workload == "glue":
+        print(json.dumps({"config": f"config{args.config}", **per_call_timings(static, theta, cw, args.steps)}))
+        return
+    solver = FusedSolver(static, static.solver_options)
     for i in range(args.warmup):
-        step()
-        torch.cuda.synchronize()
+        _timed_solves(solver, theta, cw, 1)
         log(args, f"[bench] warmup {i + 1}/{args.warmup}")
     fstats = solver.forward_stats()
-    bstats = solver.backward_stats()
 
     # ---- timed region 1: whole solves (value)
-    torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
-           torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    t_wall = time.perf_counter()
-    for i in range(args.steps):
-        a, m, b = ev[i]
-        a.record()
-        loss, saved = solver.run_forward(theta, cw)
-        m.record()
-        gt, gc = solver.run_backward(theta, cw, saved)
-        b.record()
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t_wall) * 1e3 / args.steps
-    tot = [a.elapsed_time(b) for a, _, b in ev]
-    fwd = [a.elapsed_time(m) for a, m, _ in ev]
-    bwd = [m.elapsed_time(b) for _, m, b in ev]
+    tot, fwd, bwd, wall, loss = _timed_solves(solver, theta, cw, args.steps)
     ms = statistics.mean(tot)
+    bstats = solver.backward_stats()
     log(args, f"[bench] timed {args.steps} steps: {ms:.3f} ms/solve (fwd {statistics.mean(fwd):.3f}, "
               f"bwd {statistics.mean(bwd):.3f}), wall {wall:.3f}")
-    bstats = solver.backward_stats()
 
-    # ---- timed region 2: per-launch HIP events around every wave kernel (roofline)
+    # ---- timed region 2: per-launch HIP events around every row-kernel launch (roofline)
     solver.profile(True)
     fw_ms, bw_ms = [], []
-    for i in range(args.steps):
-        loss, saved = solver.run_forward(theta, cw)
-        gt, gc = solver.run_backward(theta, cw, saved)
+    for _ in range(args.steps):
+        _, saved = solver.run_forward(theta, cw)
+        solver.run_backward(theta, cw, saved)
         fw_ms.append(solver.level_launch_ms("forward"))
         bw_ms.append(solver.level_launch_ms("backward"))
     solver.profile(False)
@@ -245,25 +376,13 @@ def main():
     B = 4.0 * solver.S
     fwd_bytes = B * (2 * W + 4 * Nw)
     bwd_bytes = B * (3 * W + 8 * Nw)
-    kernels = {
-        "fwd_wave_kernel": (fw, fwd_bytes),
-        "bwd_wave_kernel": (bw, bwd_bytes),
-    }
-    symbol = {"fwd_wave_kernel": "fwd_row_kernel", "bwd_wave_kernel": "bwd_row_kernel"}
+    kernels = {"fwd_row_kernel": (fw, fwd_bytes), "bwd_row_kernel": (bw, bwd_bytes)}
     dom = max(kernels, key=lambda k: kernels[k][0].sum())
     dur, byt = kernels[dom]
     avg_ms = float(dur.mean())
     avg_bytes = float(byt.mean())
     achieved = avg_bytes / (avg_ms * 1e-3) / 1e9
-    traffic = None
-    if TRAFFIC_FILE.exists() and args.config == "3":
-        # HBM bytes per dispatch from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this
-        # command, scaled by a copy kernel of known size (kbench.rocprof_summary)
-        rec = json.loads(TRAFFIC_FILE.read_text()).get("kernels", {})
-        # (a kernel launched in several shapes: dispatch-weighted mean over them)
-        hits = [v for k, v in rec.items() if symbol[dom] in k]
-        n = sum(float(v["dispatches"]) for v in hits)
-        traffic = round(sum(float(v["traffic"]) * float(v["dispatches"]) for v in hits) / n, 1) if n else None
+    counters = _counters(dom)
     roofline = {
         "bound": "hbm",
         "kernel": dom,
@@ -271,16 +390,38 @@ def main():
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 6),
-        "traffic": traffic,
+        "traffic": _traffic(dom) if args.config == "3" else None,
         "launches": int(len(dur)),
         "launch_unit": "one launch per clade-DAG dependency level",
         "avg_launch_ms": round(avg_ms, 5),
         "algorithmic_bytes_per_launch": round(avg_bytes, 1),
         "kernel_ms_per_solve": {k: round(float(v[0].sum()), 4) for k, v in kernels.items()},
+        "limiter": ("latency: HBM bytes are the roofline the kernel is priced against, but its time goes to "
+                    "barriers, LDS and VALU issue (counters: per-shape VALU-active and LDS-wait fractions of "
+                    "wave cycles)"),
+        "counters": counters if args.config == "3" else None,
     }
     whole_bytes = float(fwd_bytes.sum() + bwd_bytes.sum())
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline(args, int(summ["C"]))
+    # ---- the same solve with every row computed (row classes off)
+    dedup_off = None
+    if not args.no_dedup_off:
+        old = os.environ.get("KB_DEDUP")
+        os.environ["KB_DEDUP"] = "0"
+        try:
+            flat = FusedSolver(static, static.solver_options)
+        finally:
+            if old is None:
+                os.environ.pop("KB_DEDUP")
+            else:
+                os.environ["KB_DEDUP"] = old
+        _timed_solves(flat, theta, cw, 2)
+        t_all, f_all, b_all, _, _ = _timed_solves(flat, theta, cw, max(3, args.steps // 2))
+        dedup_off = {"ms": round(statistics.mean(t_all), 4), "fwd_ms": round(statistics.mean(f_all), 4),
+                     "bwd_ms": round(statistics.mean(b_all), 4)}
+        del flat
+    per_call = None if args.no_per_call else per_call_timings(static, theta, cw)
+
     out = {
         "metric": "fwd+bwd ms per solve at S=1024,C=32k; achieved HBM GB/s vs roofline",
         "value": round(ms, 4),
@@ -295,27 +436,33 @@ def main():
         "dtype": "fp32",
         "data": "synthetic (seeded Yule tree + DTL families + NNI variants; random theta in [-3,-1])",
         "config": {
-            "workload": f"config{args.config}: fwd+bwd solve, S={summ['S']} columns "
-                        f"({(summ['S'] + 1) // 2} leaves), C={summ['C']} rows, {summ['n_waves']} waves, "
-                        f"{summ['n_splits']} splits, per-species theta, pi_iters=16, neumann_terms=16",
+            "workload": (f"config{args.config}: fwd+bwd solve, S={summ['S']} columns ({(summ['S'] + 1) // 2} "
+                         f"leaves), C={summ['C']} rows, {summ['n_waves']} waves, {summ['n_splits']} splits, "
+                         f"per-species theta, pi_iters=16, neumann_terms=16; row classes: the forward computes "
+                         f"{solver.n_forward_rows} of {summ['C']} rows (identical rows written from one "
+                         f"computation), the backward solves {solver.n_backward_rows}"),
             "S_leaves": (summ["S"] + 1) // 2,
             "S_columns": summ["S"],
             "C": summ["C"],
             "n_waves": summ["n_waves"],
             "n_splits": summ["n_splits"],
             "n_families": summ["n_families"],
+            "forward_rows_computed": solver.n_forward_rows,
+            "backward_rows_solved": solver.n_backward_rows,
         },
         "fwd_ms": round(statistics.mean(fwd), 4),
         "bwd_ms": round(statistics.mean(bwd), 4),
         "median_ms": round(statistics.median(tot), 4),
         "min_ms": round(min(tot), 4),
         "host_wall_ms_per_step": round(wall, 4),
+        "dedup_off": dedup_off,
         "hbm_gbps_whole_solve": round(whole_bytes / (ms * 1e-3) / 1e9, 3),
         "e_step_iters": fstats["n_e_iter"],
         "bicgstab_iters": bstats["n_bicgstab"],
         "loss": float(loss),
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "per_call": per_call,
     }
     print(json.dumps(out))
 

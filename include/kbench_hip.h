@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define KB_ABI_VERSION 2
+#define KB_ABI_VERSION 3
 
 #define KB_ERR_ARG (-1)    /* invalid argument / layout (reference raises ValueError) */
 #define KB_ERR_HIP (-2)    /* HIP runtime error (reference: RuntimeError) */
@@ -69,7 +69,9 @@ typedef struct kb_plan kb_plan;
 /* Build the device-resident layout tables (allocates device memory). */
 int kb_plan_create(const kb_layout* layout, kb_plan** out);
 void kb_plan_destroy(kb_plan* plan);
-/* out[0..n): S, C, n_fam, n_waves, pointer-jump rounds, bottom-up levels. */
+/* out[0..n), n <= 10: S, C, n_fam, n_waves, pointer-jump rounds, bottom-up
+ * levels, dependency levels, rows the forward computes (one per class of
+ * identical rows), classes of level-0 rows, level-0 rows. */
 int kb_plan_info(const kb_plan* plan, int32_t* out, int n);
 
 /*

@@ -125,9 +125,12 @@ int kb_estep_vjp_noalloc(const kb_tree* tree, const kb_estep_vjp_io* io, void* s
  * also writes Pibar row ws + w and pibar_row_max[ws + w] from the new row;
  * pi_residual (nullable, float32 [C]) gets max |Pi_new - Pi_in| over finite
  * entries.  In-place use (Pi_in == Pi_out, Pi_out == Pibar) is allowed.
+ * n_sweeps > 1 runs that many sweeps in one launch with the row kept on chip
+ * (bitwise equal to n_sweeps one-sweep calls chained through Pi_out; only the
+ * last sweep is written, and pi_residual is the last sweep's); 0 or 1 is one.
  */
 typedef struct kb_wave_step_io {
-  int32_t dtype, S, W, use_col_weights, use_leaf_index, store_final_pibar;
+  int32_t dtype, S, W, use_col_weights, use_leaf_index, store_final_pibar, n_sweeps;
   int64_t ws, pi_ws, const_stride;
   const void* Pi_in;                               /* [*, S] */
   void* Pi_out;                                    /* [C, S] (rows ws..ws+W written) */

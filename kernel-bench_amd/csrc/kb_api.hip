@@ -660,8 +660,10 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
 
 int kb_plan_info(const kb_plan* p, int32_t* out, int n) {
   if (!p || !out) return set_error(KB_ERR_ARG, "null argument");
-  int32_t v[7] = {p->S, p->C, p->n_fam, p->n_waves, p->n_jump, p->n_blevels, p->n_levels};
-  for (int i = 0; i < n && i < 7; ++i) out[i] = v[i];
+  const int32_t n_fwd = p->f_level_ptr.empty() ? 0 : p->f_level_ptr.back();
+  const int32_t rows0 = p->level_ptr.size() > 1 ? p->level_ptr[1] : 0;
+  int32_t v[10] = {p->S, p->C, p->n_fam, p->n_waves, p->n_jump, p->n_blevels, p->n_levels, n_fwd, p->n_cls0, rows0};
+  for (int i = 0; i < n && i < 10; ++i) out[i] = v[i];
   return 0;
 }
 

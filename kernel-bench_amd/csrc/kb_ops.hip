@@ -261,7 +261,7 @@ __global__ __launch_bounds__(NT) void estep_vjp_kernel(OpsTree t, EvArgs<T> a) {
 
 template <typename T>
 struct WsArgs {
-  int S, W, use_col, use_leaf, store_final;
+  int S, W, use_col, use_leaf, store_final, n_sweeps;
   long long ws, pi_ws, cstride;
   const T* Pi_in;
   T *Pi_out, *Pibar, *rowmax;
@@ -271,6 +271,8 @@ struct WsArgs {
   const T* leaf_logp;
 };
 
+// n_sweeps self-loop sweeps of one row; between sweeps the row stays in LDS
+// (Pr), so the result equals n_sweeps one-sweep launches bit for bit.
 template <typename T, int CPT>
 __global__ __launch_bounds__(NT) void wave_step_kernel(OpsTree t, WsArgs<T> a) {
   extern __shared__ unsigned char smraw[];
@@ -291,70 +293,80 @@ __global__ __launch_bounds__(NT) void wave_step_kernel(OpsTree t, WsArgs<T> a) {
     if (s < S) Pr[s] = in[s];
   }
   __syncthreads();
-  // row max / sum of (col +) Pi, then Pibar(Pi) = log2(rowsum - pathsum) + M + mt
-  T wv[CPT];
-  T lm = NI;
-#pragma unroll
-  for (int k = 0; k < CPT; ++k) {
-    const int s = threadIdx.x + k * NT;
-    wv[k] = NI;
-    if (s < S) {
-      wv[k] = a.use_col ? a.col[s] + Pr[s] : Pr[s];
-      lm = tmax(lm, wv[k]);
-    }
-  }
-  const T M = block_max(lm, red);
-  const T Ms = msafe(M);
-  T ls = 0;
-#pragma unroll
-  for (int k = 0; k < CPT; ++k) {
-    const int s = threadIdx.x + k * NT;
-    if (s < S) {
-      const T x = xexp2(wv[k] - Ms);
-      X[s] = x;
-      ls += x;
-    }
-  }
-  const T rowsum = block_sum(ls, red);
-  path_sums(t, X, EV, X, red);
   const long long lstate = a.use_leaf ? a.leaf_state[grow] : -1;
-  T res[CPT];
+  T wv[CPT], res[CPT];
   T ldiff = 0;
+  for (int sweep = 0; sweep < a.n_sweeps; ++sweep) {
+    // row max / sum of (col +) Pi, then Pibar(Pi) = log2(rowsum - pathsum) + M + mt
+    T lm = NI;
 #pragma unroll
-  for (int k = 0; k < CPT; ++k) {
-    const int s = threadIdx.x + k * NT;
-    res[k] = NI;
-    if (s < S) {
-      const size_t ci = cb + s;
-      const T denom = rowsum - X[s];
-      const T pibar_w = denom > T(0) ? xlog2(denom) + M + a.mt[ci] : NI;
-      const T pi_w = Pr[s];
-      const int c1 = t.c1[s], c2 = t.c2[s];
-      const T ps1 = c1 >= 0 ? Pr[c1] : NI;
-      const T ps2 = c2 >= 0 ? Pr[c2] : NI;
-      const T t0 = a.DL[ci] + pi_w;
-      const T t1 = pi_w + a.Ebar[ci];
-      const T t2 = pibar_w + a.E[ci];
-      const T t3 = a.SL1[ci] + ps1;
-      const T t4 = a.SL2[ci] + ps2;
-      const T t5 = (lstate == s) ? a.leaf_logp[(size_t)item * S + s] : NI;
-      T m = tmax(tmax(tmax(t0, t1), tmax(t2, t3)), tmax(t4, t5));
-      T d = NI;
-      if (a.dts) {
-        d = a.dts[(size_t)w * S + s];
-        m = tmax(m, d);
-      }
-      const T ms = msafe(m);
-      T sum = xexp2(t0 - ms) + xexp2(t1 - ms) + xexp2(t2 - ms) + xexp2(t3 - ms) + xexp2(t4 - ms) + xexp2(t5 - ms);
-      if (a.dts) sum += xexp2(d - ms);
-      res[k] = xlog2(sum) + m;
-      if (res[k] != NI && pi_w != NI) {
-        const T df = res[k] - pi_w;
-        ldiff = tmax(ldiff, df < T(0) ? -df : df);
+    for (int k = 0; k < CPT; ++k) {
+      const int s = threadIdx.x + k * NT;
+      wv[k] = NI;
+      if (s < S) {
+        wv[k] = a.use_col ? a.col[s] + Pr[s] : Pr[s];
+        lm = tmax(lm, wv[k]);
       }
     }
+    const T M = block_max(lm, red);
+    const T Ms = msafe(M);
+    T ls = 0;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int s = threadIdx.x + k * NT;
+      if (s < S) {
+        const T x = xexp2(wv[k] - Ms);
+        X[s] = x;
+        ls += x;
+      }
+    }
+    const T rowsum = block_sum(ls, red);
+    path_sums(t, X, EV, X, red);
+    ldiff = 0;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int s = threadIdx.x + k * NT;
+      res[k] = NI;
+      if (s < S) {
+        const size_t ci = cb + s;
+        const T denom = rowsum - X[s];
+        const T pibar_w = denom > T(0) ? xlog2(denom) + M + a.mt[ci] : NI;
+        const T pi_w = Pr[s];
+        const int c1 = t.c1[s], c2 = t.c2[s];
+        const T ps1 = c1 >= 0 ? Pr[c1] : NI;
+        const T ps2 = c2 >= 0 ? Pr[c2] : NI;
+        const T t0 = a.DL[ci] + pi_w;
+        const T t1 = pi_w + a.Ebar[ci];
+        const T t2 = pibar_w + a.E[ci];
+        const T t3 = a.SL1[ci] + ps1;
+        const T t4 = a.SL2[ci] + ps2;
+        const T t5 = (lstate == s) ? a.leaf_logp[(size_t)item * S + s] : NI;
+        T m = tmax(tmax(tmax(t0, t1), tmax(t2, t3)), tmax(t4, t5));
+        T d = NI;
+        if (a.dts) {
+          d = a.dts[(size_t)w * S + s];
+          m = tmax(m, d);
+        }
+        const T ms = msafe(m);
+        T sum = xexp2(t0 - ms) + xexp2(t1 - ms) + xexp2(t2 - ms) + xexp2(t3 - ms) + xexp2(t4 - ms) + xexp2(t5 - ms);
+        if (a.dts) sum += xexp2(d - ms);
+        res[k] = xlog2(sum) + m;
+        if (res[k] != NI && pi_w != NI) {
+          const T df = res[k] - pi_w;
+          ldiff = tmax(ldiff, df < T(0) ? -df : df);
+        }
+      }
+    }
+    __syncthreads();  // every read of X / Pr above is done
+    if (sweep + 1 < a.n_sweeps) {
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        const int s = threadIdx.x + k * NT;
+        if (s < S) Pr[s] = res[k];
+      }
+      __syncthreads();
+    }
   }
-  __syncthreads();  // every read of X / Pr above is done
   T* out = a.Pi_out + (size_t)grow * S;
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
@@ -1335,7 +1347,8 @@ int kb_wave_step(const kb_tree* tr, const kb_wave_step_io* io, void* stream) {
   if (int rc = check_lds(lds, S, io->dtype)) return rc;
   const kbo::OpsTree t = tr->dev();
   KBO_DISPATCH(io->dtype, S, {
-    kbo::WsArgs<T> a{S, io->W, io->use_col_weights, io->use_leaf_index, io->store_final_pibar, io->ws, io->pi_ws,
+    kbo::WsArgs<T> a{S, io->W, io->use_col_weights, io->use_leaf_index, io->store_final_pibar,
+                     io->n_sweeps > 1 ? io->n_sweeps : 1, io->ws, io->pi_ws,
                      io->const_stride, (const T*)io->Pi_in, (T*)io->Pi_out, (T*)io->Pibar, (T*)io->pibar_row_max,
                      io->pi_residual, (const T*)io->dts, (const T*)io->max_coupling, (const T*)io->DL,
                      (const T*)io->Ebar, (const T*)io->E, (const T*)io->SL1, (const T*)io->SL2,

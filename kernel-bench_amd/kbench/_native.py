@@ -12,7 +12,7 @@ import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libkbench_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib = None
 _load_error: str | None = None

@@ -36,7 +36,8 @@ class KbEStepVjpIO(ct.Structure):
 
 class KbWaveStepIO(ct.Structure):
     _fields_ = [("dtype", i32), ("S", i32), ("W", i32), ("use_col_weights", i32), ("use_leaf_index", i32),
-                ("store_final_pibar", i32), ("ws", i64), ("pi_ws", i64), ("const_stride", i64)] + _ptrs(
+                ("store_final_pibar", i32), ("n_sweeps", i32), ("ws", i64), ("pi_ws", i64),
+                ("const_stride", i64)] + _ptrs(
         "Pi_in", "Pi_out", "Pibar", "pibar_row_max", "pi_residual", "dts",
         "max_coupling", "DL", "Ebar", "E", "SL1", "SL2", "col_log_probs", "item_idx", "leaf_state", "leaf_logp")
 

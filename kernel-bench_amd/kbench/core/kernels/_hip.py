@@ -27,13 +27,37 @@ __all__ = [
     "KB_BF16", "KB_F32", "KB_F64", "KbDtsCrossIO", "KbDtsIO", "KbEStepIO", "KbEStepVjpIO", "KbLeafInitIO",
     "KbPibarVjpIO", "KbWaveBwdIO", "KbWaveStepIO", "KbETanIO", "KbDtsTanIO", "KbWaveTanIO", "KbEStepSoIO",
     "KbWaveSoIO", "KbDtsSoIO",
-    "lib", "check", "ptr", "stream", "dtype_code", "require_device", "f", "i64", "tree_from_parent",
+    "lib", "check", "ptr", "stream", "dtype_code", "defer", "flush", "require_device", "f", "i64", "tree_from_parent",
     "tree_from_levels", "scatter_add_rows", "sum_rows_into", "static_cached",
 ]
 
-lib = N.lib
 check = N.check
 ptr = N.ptr
+
+# a callable that launches work held back by a wrapper (the chained sweeps of
+# compute_wave_step under KBENCH_FUSE_SWEEPS), or None
+_deferred = None
+
+
+def defer(run) -> None:
+    """Register held-back work; it runs before the next launch of any wrapper."""
+    global _deferred
+    _deferred = run
+
+
+def flush() -> None:
+    """Launch any held-back work now (the wrappers do this before their own launches)."""
+    global _deferred
+    run, _deferred = _deferred, None
+    if run is not None:
+        run()
+
+
+def lib():
+    """The HIP library, after launching any held-back work (stream order is kept)."""
+    if _deferred is not None:
+        flush()
+    return N.lib()
 
 
 def stream(device) -> int:

@@ -12,13 +12,29 @@ Same positional / keyword signatures and in-place semantics: rows
 [W, S] split buffer (``input_ws=0``) are allowed.  One 1024-thread workgroup
 per row; the Pibar ancestor sums are one Euler-tour prefix scan in LDS instead
 of the reference's bounded ancestor chase (same sum).
+
+Launch collapse (``KBENCH_FUSE_SWEEPS=1``).  A caller that sweeps a wave
+``pi_iters - 1`` times (reference kbench/core/inference/forward.py:81-115)
+issues one call per sweep, each reading the previous call's ``Pi_out``.
+With the variable set, a call without ``store_final_pibar`` that continues
+such a chain (same rows, constants and split term; its ``Pi_in`` is the
+previous call's ``Pi_out``) is held back, and the chain runs as one launch of
+``n`` sweeps with the row on chip when its final call arrives -- bitwise the
+same final Pi, Pibar, row maxima and residual.  Held-back calls leave their
+own ``Pi_out`` rows unwritten: a caller must not read a chain's intermediate
+buffers before its final call (the reference glue never does).  Any other
+wrapper call, or a call that breaks the chain, first runs what is held back.
 """
 
 from __future__ import annotations
 
+import os
+
 import torch
 
 from . import _hip as H
+
+FUSE_SWEEPS = os.environ.get("KBENCH_FUSE_SWEEPS", "0").strip() not in ("", "0")
 
 __all__ = ["compute_leaf_initial_wave_step", "compute_wave_step"]
 
@@ -96,19 +112,92 @@ def compute_wave_step(Pi_in, Pi_out, Pibar, ws, W, S, max_coupling_mat, DL_const
         dts = DTS_reduced
         if not dts.is_contiguous() or tuple(dts.shape) != (W, S) or dts.dtype != dt:
             raise ValueError("DTS_reduced must be a contiguous [W, S] tensor of the Pi dtype")
-    tree = H.tree_from_parent(node_parent, node_child1, node_child2)
-    mt, DL, Eb, Ev, SL1, SL2 = _consts(dt, dev, max_coupling_mat, DL_const, Ebar, E, SL1_const, SL2_const)
-    col = H.f(col_log_probs, dt, dev)
-    item = H.i64(item_idx, dev)
-    leaf = H.i64(leaf_state_idx, dev)
-    lp = H.f(leaf_logp, dt, dev)
+    pi_ws = ws if input_ws is None else int(input_ws)
+    # the chain identity: everything a held-back sweep shares with the next one
+    key = (ws, W, S, dt, dev, bool(has_leaf_term), bool(use_col_weights), dts, max_coupling_mat, DL_const, Ebar,
+           E, SL1_const, SL2_const, col_log_probs, node_parent, node_child1, node_child2, item_idx, leaf_state_idx,
+           leaf_logp)
+    chain = _chain
+    if chain is not None and not chain.continued_by(key, Pi_in, pi_ws):
+        H.flush()  # runs and clears the held-back chain
+        chain = None
+    if FUSE_SWEEPS and not store_final_pibar and pi_residual_out is None:
+        if chain is None:
+            chain = _Chain(key, Pi_in, pi_ws)
+        chain.extend(Pi_out, Pibar, pibar_row_max)
+        _hold(chain)
+        return
+    first_in, first_ws, n_held = (chain.first_in, chain.first_ws, chain.n) if chain is not None else (Pi_in, pi_ws, 0)
+    _drop_held()
+    _launch_sweeps(first_in, first_ws, n_held + 1, Pi_out, Pibar, pibar_row_max, pi_residual_out,
+                   bool(store_final_pibar), key, dts)
+
+
+class _Chain:
+    """Sweeps of one wave held back under KBENCH_FUSE_SWEEPS, waiting for the chain's final call."""
+
+    __slots__ = ("key", "first_in", "first_ws", "n", "last_out", "last_pibar", "last_rmax")
+
+    def __init__(self, key, Pi_in, pi_ws):
+        self.key, self.first_in, self.first_ws, self.n = key, Pi_in, pi_ws, 0
+        self.last_out = self.last_pibar = self.last_rmax = None
+
+    def extend(self, Pi_out, Pibar, rmax):
+        self.n += 1
+        self.last_out, self.last_pibar, self.last_rmax = Pi_out, Pibar, rmax
+
+    def continued_by(self, key, Pi_in, pi_ws) -> bool:
+        """The next sweep reads this chain's last output rows with the same rows and constants."""
+        if Pi_in is not self.last_out or pi_ws != key[0] or len(key) != len(self.key):
+            return False
+        return all(a is b or (type(a) is type(b) and not torch.is_tensor(a) and a == b)
+                   for a, b in zip(key, self.key))
+
+    def run(self):
+        """Launch the held-back sweeps alone (a chain broken before its final call)."""
+        _launch_sweeps(self.first_in, self.first_ws, self.n, self.last_out, self.last_pibar, self.last_rmax,
+                       None, False, self.key, self.key[7])
+
+
+_chain = None
+
+
+def _hold(chain):
+    global _chain
+    _chain = chain
+    H.defer(_run_held)
+
+
+def _run_held():
+    global _chain
+    chain, _chain = _chain, None
+    if chain is not None:
+        chain.run()
+
+
+def _drop_held():
+    global _chain
+    if _chain is not None:
+        _chain = None
+        H.defer(None)
+
+
+def _launch_sweeps(Pi_in, pi_ws, n_sweeps, Pi_out, Pibar, pibar_row_max, pi_residual_out, store_final, key, dts):
+    """One kb_wave_step launch of ``n_sweeps`` sweeps from ``Pi_in`` rows ``pi_ws..``."""
+    (ws, W, S, dt, dev, has_leaf, use_col, _, mt_c, DL_c, Ebar_c, E_c, SL1_c, SL2_c, col_c, parent, c1, c2, item_c,
+     leaf_c, lp_c) = key
+    tree = H.tree_from_parent(parent, c1, c2)
+    mt, DL, Eb, Ev, SL1, SL2 = _consts(dt, dev, mt_c, DL_c, Ebar_c, E_c, SL1_c, SL2_c)
+    col = H.f(col_c, dt, dev)
+    item = H.i64(item_c, dev)
+    leaf = H.i64(leaf_c, dev)
+    lp = H.f(lp_c, dt, dev)
     io = H.KbWaveStepIO(
-        dtype=H.dtype_code(dt), S=S, W=W, use_col_weights=int(bool(use_col_weights)),
-        use_leaf_index=int(bool(has_leaf_term)), store_final_pibar=int(bool(store_final_pibar)), ws=ws,
-        pi_ws=ws if input_ws is None else int(input_ws), const_stride=_const_stride(DL),
-        Pi_in=H.ptr(Pi_in), Pi_out=H.ptr(Pi_out), Pibar=H.ptr(Pibar), pibar_row_max=H.ptr(pibar_row_max),
-        pi_residual=H.ptr(pi_residual_out), dts=H.ptr(dts), max_coupling=H.ptr(mt), DL=H.ptr(DL), Ebar=H.ptr(Eb),
-        E=H.ptr(Ev), SL1=H.ptr(SL1), SL2=H.ptr(SL2), col_log_probs=H.ptr(col), item_idx=H.ptr(item),
-        leaf_state=H.ptr(leaf), leaf_logp=H.ptr(lp),
+        dtype=H.dtype_code(dt), S=S, W=W, use_col_weights=int(use_col), use_leaf_index=int(has_leaf),
+        store_final_pibar=int(store_final), n_sweeps=int(n_sweeps), ws=ws, pi_ws=int(pi_ws),
+        const_stride=_const_stride(DL), Pi_in=H.ptr(Pi_in), Pi_out=H.ptr(Pi_out), Pibar=H.ptr(Pibar),
+        pibar_row_max=H.ptr(pibar_row_max), pi_residual=H.ptr(pi_residual_out), dts=H.ptr(dts),
+        max_coupling=H.ptr(mt), DL=H.ptr(DL), Ebar=H.ptr(Eb), E=H.ptr(Ev), SL1=H.ptr(SL1), SL2=H.ptr(SL2),
+        col_log_probs=H.ptr(col), item_idx=H.ptr(item), leaf_state=H.ptr(leaf), leaf_logp=H.ptr(lp),
     )
-    H.check(H.lib().kb_wave_step(tree.handle, io, H.stream(dev)))
+    H.check(H.N.lib().kb_wave_step(tree.handle, io, H.stream(dev)))

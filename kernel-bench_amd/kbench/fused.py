@@ -177,9 +177,13 @@ class FusedSolver:
         self.root_row_ids = torch.as_tensor(roots, device=self.device)
         self.n_waves = len(ws)
         self.n_splits = L.n_splits
-        info = (ct.c_int32 * 7)()
-        N.check(lib.kb_plan_info(handle, info, 7))
+        info = (ct.c_int32 * 10)()
+        N.check(lib.kb_plan_info(handle, info, 10))
         self.n_levels = int(info[6])
+        # row classes: the forward computes one row per class of identical rows;
+        # the backward solves every split row and one row per class of level-0 rows
+        self.n_forward_rows = int(info[7])
+        self.n_backward_rows = C - int(info[9]) + int(info[8])
         self.last_n_e_iter = None
         self.last_n_bicgstab = None
         self._use_col_cache = None  # (_TensorKey of the caller's col_weights, answer)

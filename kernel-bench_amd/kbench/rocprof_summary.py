@@ -7,8 +7,12 @@ Two sub-commands, both reading the CSV files rocprofv3 writes with
     Per-kernel table from ``DIR/*_kernel_stats.csv`` (calls, average and total
     duration, share of GPU time), as Markdown.
 
-``sq CSV``
-    Per-kernel SQ counters of one ``--pmc`` run divided by ``SQ_WAVES``.
+``sq CSV [--json]``
+    Per-kernel SQ counters of one ``--pmc`` run divided by ``SQ_WAVES``; with
+    ``--json`` also the fractions of wave cycles spent issuing VALU
+    (``SQ_ACTIVE_INST_VALU / SQ_WAVE_CYCLES``) and waiting on LDS
+    (``SQ_WAIT_INST_LDS / SQ_WAVE_CYCLES``), both counters in the same
+    (quad-cycle) units.
 
 ``traffic --fetch F --write W --cal-fetch CF --cal-write CW``
     HBM bytes per dispatch of each solver kernel from two ``--pmc`` runs
@@ -107,8 +111,7 @@ def traffic(fetch: str, write: str, cal_fetch: str, cal_write: str, cal_bytes: f
     return out
 
 
-def sq_markdown(path: str, prefix: str = "kb::") -> str:
-    """Per-kernel SQ counter totals of one ``--pmc`` run, normalised per wave."""
+def _sq_totals(path: str, prefix: str):
     tot = defaultdict(lambda: defaultdict(float))
     disp = defaultdict(set)
     with open(path, newline="") as fh:
@@ -118,6 +121,30 @@ def sq_markdown(path: str, prefix: str = "kb::") -> str:
             k = _short(r["Kernel_Name"])
             tot[k][r["Counter_Name"]] += float(r["Counter_Value"])
             disp[k].add(r["Dispatch_Id"])
+    return tot, disp
+
+
+def sq_json(path: str, prefix: str = "kb::") -> dict:
+    """Per-kernel SQ counters per wave and the VALU-issue / LDS-wait fractions of wave cycles."""
+    tot, disp = _sq_totals(path, prefix)
+    out = {}
+    for k, v in tot.items():
+        w = v.get("SQ_WAVES", 0.0)
+        cyc = v.get("SQ_WAVE_CYCLES", 0.0)
+        rec = {"dispatches": len(disp[k]), "waves": w}
+        rec.update({f"{c}_per_wave": v[c] / w for c in v if c != "SQ_WAVES" and w})
+        if cyc:
+            if "SQ_ACTIVE_INST_VALU" in v:
+                rec["valu_active_frac"] = v["SQ_ACTIVE_INST_VALU"] / cyc
+            if "SQ_WAIT_INST_LDS" in v:
+                rec["lds_wait_frac"] = v["SQ_WAIT_INST_LDS"] / cyc
+        out[k] = rec
+    return {"source": "rocprofv3 --pmc SQ counters", "kernels": out}
+
+
+def sq_markdown(path: str, prefix: str = "kb::") -> str:
+    """Per-kernel SQ counter totals of one ``--pmc`` run, normalised per wave."""
+    tot, disp = _sq_totals(path, prefix)
     names = sorted({c for v in tot.values() for c in v})
     per_wave = [c for c in names if c != "SQ_WAVES"]
     head = "| kernel | dispatches | waves | " + " | ".join(f"{c} / wave" for c in per_wave) + " |"
@@ -143,11 +170,12 @@ def main(argv=None):
     b.add_argument("--cal-mib", type=float, default=512.0)
     c = sub.add_parser("sq")
     c.add_argument("csv")
+    c.add_argument("--json", action="store_true")
     args = ap.parse_args(argv)
     if args.cmd == "stats":
         print(stats_markdown(args.dir, args.top))
     elif args.cmd == "sq":
-        print(sq_markdown(args.csv))
+        print(json.dumps(sq_json(args.csv), indent=1) if args.json else sq_markdown(args.csv))
     else:
         print(json.dumps(traffic(args.fetch, args.write, args.cal_fetch, args.cal_write, args.cal_mib * (1 << 20)),
                          indent=1))

@@ -567,3 +567,77 @@ def summary(problem: dict) -> dict:
         "max_wave_rows": max(m["W"] for m in wl["wave_metas"]),
         "max_ancestor_depth": problem["static"]["state_helpers"]["max_ancestor_depth"],
     }
+
+
+def family_subset(problem: dict, families) -> dict:
+    """The problem restricted to ``families`` (family ids, in order): same tree, theta and options.
+
+    Rows of other families are dropped and the kept rows renumbered in their
+    order; waves keep their order and lose their dropped rows (empty waves
+    vanish); every kept parent keeps all of its splits, so the eq1-first /
+    ge2-grouped split order survives and its offsets are recomputed.  Rows of
+    different families never interact, so a solve over the subset is the
+    solve of those families alone (the loss and gradients of a whole problem
+    are the sums over a partition of its families).
+    """
+    fams = [int(f) for f in families]
+    wl = problem["static"]["wave_layout"]
+    item = np.asarray(wl["item_idx"])
+    pos = {f: i for i, f in enumerate(fams)}
+    keep = np.isin(item, np.asarray(fams, dtype=item.dtype))
+    new_id = np.cumsum(keep) - 1  # new row id of a kept row
+    metas = []
+    for m in wl["wave_metas"]:
+        s0, W = int(m["start"]), int(m["W"])
+        kw = keep[s0:s0 + W]
+        if not kw.any():
+            continue
+        local = np.cumsum(kw) - 1  # new wave-local index of a kept row
+        meta = {"start": int(new_id[s0:s0 + W][kw][0]), "W": int(kw.sum())}
+        if "sl" in m:
+            red = np.asarray(m["reduce_idx"])
+            on = kw[red]
+            n_eq1 = int(m["n_eq1"])
+            ge2_ptr = np.asarray(m["ge2_ptr"])
+            ge2_parent = np.asarray(m["ge2_parent_ids"])
+            new_ptr, new_parent = [0], []
+            for g in range(ge2_parent.shape[0]):
+                if kw[ge2_parent[g]]:
+                    new_ptr.append(new_ptr[-1] + int(ge2_ptr[g + 1] - ge2_ptr[g]))
+                    new_parent.append(int(local[ge2_parent[g]]))
+            sel_red = local[red[on]]
+            n_eq1_new = int(on[:n_eq1].sum())
+            meta.update({
+                "sl": new_id[np.asarray(m["sl"])[on]].astype(np.int64),
+                "sr": new_id[np.asarray(m["sr"])[on]].astype(np.int64),
+                "reduce_idx": sel_red.astype(np.int64),
+                "log_split_probs": np.asarray(m["log_split_probs"])[on],
+                "n_eq1": n_eq1_new,
+                "eq1_reduce_idx": sel_red[:n_eq1_new].astype(np.int64),
+                "ge2_ptr": np.asarray(new_ptr, dtype=np.int64),
+                "ge2_parent_ids": np.asarray(new_parent, dtype=np.int64),
+                "ge2_max_fanout": int(max(np.diff(new_ptr), default=0)),
+            })
+        metas.append(meta)
+    roots = np.asarray(wl["root_row_ids"])
+    st = problem["static"]
+    C = int(keep.sum())
+    out = {
+        "meta": dict(problem["meta"], C=C, n_items=len(fams)),
+        "static": {
+            "wave_layout": {
+                "leaf_state_index": np.asarray(wl["leaf_state_index"])[keep],
+                "root_row_ids": new_id[roots[fams]].astype(np.int64),
+                "item_idx": np.asarray([pos[int(f)] for f in item[keep]], dtype=np.int64),
+                "wave_metas": metas,
+            },
+            "state_helpers": st["state_helpers"],
+            "rate_item_idx": np.zeros(C, dtype=np.int64),
+            "itemwise": st["itemwise"],
+            "statewise": st["statewise"],
+        },
+        "inputs": problem["inputs"],
+    }
+    if "tree" in problem:
+        out["tree"] = problem["tree"]
+    return out

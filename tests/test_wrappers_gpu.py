@@ -164,3 +164,64 @@ def test_glue_config3_forward_matches_fused():
     ok, ma, mr = kbtest.compare_inf_safe(s1["pi_wave"].cpu().numpy(), s2["pi_wave"].cpu().numpy())
     print(f"  loss rel={rel:.3e} pi ok={ok} max_abs={ma:.3e} max_rel={mr:.3e}")
     assert rel <= 1e-5 and ok
+
+
+@pytest.mark.parametrize("name", ["1", "3"])
+def test_fused_sweep_chains_are_bitwise_equal(name, monkeypatch):
+    """KBENCH_FUSE_SWEEPS: a wave's chained sweeps run as one launch with the same results, bit for bit."""
+    import dropin
+    from kbench.core.kernels import wave_step
+
+    print(f"[fuse-sweeps] config={name}", flush=True)
+    static, theta, cw = _static(name, True if name == "1" else None)
+    monkeypatch.setattr(wave_step, "FUSE_SWEEPS", False)
+    la, sa = dropin.run_forward(static, theta, cw)
+    monkeypatch.setattr(wave_step, "FUSE_SWEEPS", True)
+    lb, sb = dropin.run_forward(static, theta, cw)
+    torch.cuda.synchronize()
+    assert wave_step._chain is None  # every chain ended with its final call
+    assert torch.equal(la, lb)
+    for k in ("pi_wave", "pibar_wave", "pibar_row_max"):
+        assert torch.equal(sa[k], sb[k]), k
+
+
+def test_held_sweeps_run_before_other_work(monkeypatch):
+    """A chain broken before its final call (an explicit flush, another wrapper) still yields every sweep."""
+    from dropin.solve import plan_of
+    from kbench.core.kernels import _hip as H
+    from kbench.core.kernels import wave_step
+    from kbench.core.kernels.wave_backward import active_mask_from_rhs_absmax_fused
+
+    static, theta, cw = _static("1", True)
+    plan = plan_of(static)
+    _, sv = plan.forward(theta, cw)
+    c = plan._row_consts(sv["E"], sv["Ebar"], sv["E_s1"], sv["E_s2"], sv["log_pS"], sv["log_pD"],
+                         sv["max_coupling"])
+    w = next(w for w in plan.waves if not w.split)
+    h = static.state_helpers
+    C, S = sv["pi_wave"].shape
+    args = (w.ws, w.W, S, c.mt, c.DL, c.Ebar, c.E, c.SL1, c.SL2, sv["col_log_probs"], h["node_child1"],
+            h["node_child2"], h["node_parent"], int(h["max_ancestor_depth"]), None)
+    kw = dict(leaf_state_idx=plan.leaf_idx, leaf_logp=c.leaf, item_idx=plan.item_idx,
+              pibar_row_max=sv["pibar_row_max"].clone(), has_leaf_term=True, use_col_weights=False)
+
+    def three_sweeps(broken_by):
+        a, b = sv["pi_wave"].clone(), torch.empty_like(sv["pi_wave"])
+        bufs = [a, b, a]
+        for i in range(3):
+            wave_step.compute_wave_step(bufs[i], bufs[i + 1] if i < 2 else b, b, *args, **kw)
+        if broken_by == "flush":
+            H.flush()
+        elif broken_by == "wrapper":
+            active_mask_from_rhs_absmax_fused(a, 1e-6)
+        return a.clone(), b.clone()
+
+    monkeypatch.setattr(wave_step, "FUSE_SWEEPS", False)
+    ref = three_sweeps(None)
+    monkeypatch.setattr(wave_step, "FUSE_SWEEPS", True)
+    for how in ("flush", "wrapper"):
+        got = three_sweeps(how)
+        torch.cuda.synchronize()
+        assert wave_step._chain is None
+        rows = slice(w.ws, w.ws + w.W)
+        assert torch.equal(got[1][rows], ref[1][rows]), how  # the last sweep's output rows

@@ -60,7 +60,11 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   // The narrow 1024 x 2 shape runs the levels with about one row per
   // workgroup: it fetches rows when needed instead of one row ahead (128
   // VGPRs at 16 waves).
-  constexpr bool AHEAD = !(NT == 1024 && CPT == 2);
+  constexpr bool AHEAD = NT < 1024;
+  // the first split's child rows are prefetched into registers during the
+  // Neumann loop, except where 1024 threads (128 VGPRs) own four or more
+  // positions each: there the registers spill to scratch memory
+  constexpr bool PF = !(NT == 1024 && CPT >= 4);
   OwnTablesC<NT, CPT> O;
   O.load(T);
   if (tid < 64) {
@@ -528,7 +532,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   // The first split's four child rows (Pi, Pibar of both children) are loaded
   // into registers here, so their latency overlaps the Neumann loop.
   float pf[4][CPT];
-  if (se > sb) {
+  if (PF && se > sb) {
     const size_t l = (size_t)(cm ? P.split_l[sb] : f_l0) * S;
     const size_t r = (size_t)(cm ? P.split_r[sb] : f_r0) * S;
 #pragma unroll
@@ -652,7 +656,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     const float rml = s0 ? rml0 : P.rowmax[lrow], rmr = s0 ? rmr0 : P.rowmax[rrow];
     const float rmsl = fsafe(rml), rmsr = fsafe(rmr);
     __syncthreads();  // previous readers of R0..R3 are done
-    if (si == sb) {
+    if (PF && si == sb) {
 #pragma unroll
       for (int j = 0; j < CPT; ++j)
         if (spre[j] >= 0) {

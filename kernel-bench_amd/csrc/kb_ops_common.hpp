@@ -6,6 +6,9 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "../../include/kbench_ops.h"
 #include "kb_kernels.hpp"
@@ -305,11 +308,22 @@ inline int dtype_ok(int dtype) {
     }                                                                        \
   } while (0)
 
+// Raise a kernel's dynamic-LDS limit to what this launch needs.  The limit set
+// so far is remembered per kernel and device, so a launch at or below it makes
+// no runtime call (the per-call wrappers launch thousands of times per solve).
 template <typename F>
 inline int set_lds(F* kernel, size_t bytes) {
-  if (bytes > 64 * 1024)
-    KBO_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)bytes));
+  if (bytes <= 64 * 1024) return 0;
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, size_t> raised;
+  int dev = 0;
+  KBO_HIP(hipGetDevice(&dev));
+  const auto key = std::make_pair(reinterpret_cast<const void*>(kernel), dev);
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = raised.find(key);
+  if (it != raised.end() && it->second >= bytes) return 0;
+  KBO_HIP(hipFuncSetAttribute(key.first, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
+  raised[key] = bytes;
   return 0;
 }
 

@@ -139,6 +139,17 @@ def ptr(t) -> int:
 
 
 def stream_handle(device=None) -> int:
+    """The raw ``hipStream_t`` of torch's current stream on ``device`` (default: the current device).
+
+    Read through torch's raw-stream accessor (one C call, no Stream object):
+    the per-call wrappers ask for it on every launch.
+    """
     import torch
 
-    return int(torch.cuda.current_stream(device).cuda_stream)
+    if device is None:
+        idx = torch.cuda.current_device()
+    elif isinstance(device, torch.device):
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+    else:
+        idx = int(device)
+    return int(torch._C._cuda_getCurrentRawStream(idx))

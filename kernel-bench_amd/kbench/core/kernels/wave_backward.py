@@ -172,7 +172,7 @@ def wave_backward_uniform_fused(Pi_star, Pibar_star, ws, W, S, dts_r, rhs, mt_sq
         raise RuntimeError("the self-loop backward requires HIP device tensors")
     if Pi_star.dtype not in (torch.float32, torch.float64):
         raise RuntimeError("the self-loop backward supports fp32/fp64 only")
-    if None in (compact_level_ptr, compact_level_parents, compact_level_child1, compact_level_child2):
+    if any(t is None for t in (compact_level_ptr, compact_level_parents, compact_level_child1, compact_level_child2)):
         raise ValueError("compact state levels are required for the retained 2D self-loop path")
     solver = str(self_loop_solver).strip().lower()
     if solver == "gmres":
@@ -429,7 +429,7 @@ def uniform_cross_pibar_vjp_tree_from_ud_fused(Pi_star, col_log_probs, pibar_ud,
         side_active = side_active.to(device=dev, dtype=torch.bool).contiguous()
     elif skip_zero_sides:
         side_active = _side_active_from_ud(pibar_ud, thr)
-    if None in (compact_level_ptr, compact_level_parents, compact_level_child1, compact_level_child2):
+    if any(t is None for t in (compact_level_ptr, compact_level_parents, compact_level_child1, compact_level_child2)):
         raise ValueError("compact state levels are required for Pibar VJP")
     if compact_level_ptr.numel() < 2:
         raise ValueError("compact_level_ptr must contain at least start and end offsets")

@@ -13,6 +13,7 @@ under any wrapper implementation.
 from __future__ import annotations
 
 import importlib
+import sys
 
 import torch
 
@@ -37,13 +38,21 @@ WRAPPERS = {
 
 
 class _Late:
-    """Attribute access resolves ``module.name`` on every lookup."""
+    """Attribute access resolves ``module.name`` on every lookup.
+
+    The module object is found in ``sys.modules`` (imported once), so a lookup
+    costs a dict access and a ``getattr`` -- as cheap as the glue's own
+    module-level imports, while a replaced module attribute is still seen.
+    """
 
     def __getattr__(self, name):
-        mod = WRAPPERS.get(name)
-        if mod is None:
+        modname = WRAPPERS.get(name)
+        if modname is None:
             raise AttributeError(name)
-        return getattr(importlib.import_module(mod), name)
+        mod = sys.modules.get(modname)
+        if mod is None:
+            mod = importlib.import_module(modname)
+        return getattr(mod, name)
 
 
 def real():

@@ -157,7 +157,7 @@ def test_fused_weighted_columns_match_oracle(name, statewise):
 
 
 def _big_tree_problem(leaves, families, statewise):
-    """Large species tree, few families: the 2048- and 8192-position row kernels at an oracle-sized C."""
+    """Large species tree, few families: the 2048-, 4096- and 8192-position row kernels at an oracle-sized C."""
     from kbench import synth
 
     cfg = synth.ProblemConfig(leaves, families, n_nni=1, family_leaves_median=21.0, family_leaves_sigma=0.6,
@@ -166,11 +166,12 @@ def _big_tree_problem(leaves, families, statewise):
 
 
 @pytest.mark.parametrize("leaves,families,statewise,weighted", [(1024, 6, True, False), (1024, 6, False, True),
+                                                                (2048, 4, True, False), (2048, 4, False, True),
                                                                 (4096, 3, False, False), (4096, 3, True, True)])
 @pytest.mark.parametrize("shapes", ["default", "wide"])
 def test_fused_large_trees_match_oracle(leaves, families, statewise, weighted, shapes, monkeypatch):
-    """S = 2047 and 8191: forward rows, loss and gradients against the oracle, with the default launch
-    shapes (narrow shapes on these small levels) and with the wide ones forced."""
+    """S = 2047, 4095 and 8191: forward rows, loss and gradients against the oracle, with the default
+    launch shapes (narrow shapes on these small levels) and with the wide ones forced."""
     import kbench_oracle as O
     from kbench.fused import FusedSolver, problem_to_captured
     from kbench.runtime import make_static

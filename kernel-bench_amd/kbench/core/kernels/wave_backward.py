@@ -18,8 +18,14 @@ per-row contribution rows (``kb_rows_scatter_add`` / ``kb_rows_sum_into``)
 instead of the reference's ``tl.atomic_add``, so repeated calls give
 bitwise-identical gradients.
 
-Not implemented (raise NotImplementedError): the GMRES self-loop solver and
-``self_loop_grad_targets``; the glue's path uses neither.
+Self-loop solvers: ``"neumann"`` (the truncated series, one launch) and
+``"gmres"`` (fixed-iteration GMRES over the whole wave, pristine
+wave_backward.py:574-653: the Krylov loop runs on the host side in torch, each
+operator application is one launch of the HIP kernel as one fixed-point step
+from the basis vector with a zero right-hand side, which gives J^T x).
+``self_loop_grad_targets`` adds the wave's bucket sums into the caller's
+gradient accumulators (fixed-order row sums) instead of returning the bucket
+rows (pristine wave_backward.py:1300-1395).
 """
 
 from __future__ import annotations
@@ -175,12 +181,13 @@ def wave_backward_uniform_fused(Pi_star, Pibar_star, ws, W, S, dts_r, rhs, mt_sq
     if any(t is None for t in (compact_level_ptr, compact_level_parents, compact_level_child1, compact_level_child2)):
         raise ValueError("compact state levels are required for the retained 2D self-loop path")
     solver = str(self_loop_solver).strip().lower()
-    if solver == "gmres":
-        raise NotImplementedError("the GMRES self-loop solver is not implemented by the HIP backward")
-    if solver != "neumann":
+    if solver not in ("neumann", "gmres"):
         raise ValueError(f"unsupported self-loop solver {self_loop_solver!r}")
-    if self_loop_grad_targets is not None:
-        raise NotImplementedError("self_loop_grad_targets is not implemented by the HIP backward")
+    if solver == "gmres" and initial_v is not None:
+        raise ValueError("GMRES self-loop solve does not support initial_v")
+    if self_loop_grad_targets is not None and len(self_loop_grad_targets) != 8:
+        raise ValueError("self_loop_grad_targets must hold grad_log_pD, grad_log_pS, grad_E, grad_Ebar, grad_E_s1, "
+                         "grad_E_s2, grad_mt and param_grad_vector")
     ok, need, budget = proposal0_memory_gate(W, S, Pi_star.dtype, device=Pi_star.device)
     if not ok:
         raise RuntimeError(f"2D self-loop fast path estimated scratch {need / 1024 ** 3:.2f} GiB above memory "
@@ -210,25 +217,141 @@ def wave_backward_uniform_fused(Pi_star, Pibar_star, ws, W, S, dts_r, rhs, mt_sq
     lp = H.f(leaf_logp, dt, dev) if use_leaf_index else None
     lterm = H.f(leaf_term_wt, dt, dev) if (leaf_term_wt is not None and not use_leaf_index and has_leaf_term) else None
     col_rows = torch.empty((W, S), device=dev, dtype=dt)
-    relres = torch.empty((W,), device=dev, dtype=torch.float32) if return_last_increment else None
-    io = H.KbWaveBwdIO(
-        dtype=H.dtype_code(dt), S=S, W=W, n_terms=int(neumann_terms), const_layout=const_layout, leaf_mode=leaf_mode,
-        use_leaf_index=int(use_leaf_index), use_col_weights=int(bool(use_col_weights)), ws=ws,
-        Pi=H.ptr(Pi_star), Pibar=H.ptr(Pibar_star), pibar_row_max=H.ptr(rmax), dts=H.ptr(dts), rhs=H.ptr(rhs_c),
-        initial_v=H.ptr(v0), active=H.ptr(act), max_coupling=H.ptr(consts[0]), DL=H.ptr(consts[1]),
-        Ebar=H.ptr(consts[2]), E=H.ptr(consts[3]), SL1=H.ptr(consts[4]), SL2=H.ptr(consts[5]),
-        col_log_probs=H.ptr(col), item_idx=H.ptr(item), leaf_state=H.ptr(leaf), leaf_logp=H.ptr(lp),
-        leaf_term=H.ptr(lterm), v=H.ptr(outs[0]), aw0=H.ptr(outs[1]), aw1=H.ptr(outs[2]), aw2=H.ptr(outs[3]),
-        aw345=H.ptr(outs[4]), aw3=H.ptr(outs[5]), aw4=H.ptr(outs[6]), col_rows=H.ptr(col_rows),
-        relres=H.ptr(relres),
-    )
-    H.check(H.lib().kb_wave_backward(tree.handle, io, H.stream(dev)))
+    relres = (torch.empty((W,), device=dev, dtype=torch.float32)
+              if return_last_increment and solver == "neumann" else None)
+
+    def launch(rhs_t, v0_t, n_terms, out, col_out, relres_t):
+        io = H.KbWaveBwdIO(
+            dtype=H.dtype_code(dt), S=S, W=W, n_terms=int(n_terms), const_layout=const_layout, leaf_mode=leaf_mode,
+            use_leaf_index=int(use_leaf_index), use_col_weights=int(bool(use_col_weights)), ws=ws,
+            Pi=H.ptr(Pi_star), Pibar=H.ptr(Pibar_star), pibar_row_max=H.ptr(rmax), dts=H.ptr(dts), rhs=H.ptr(rhs_t),
+            initial_v=H.ptr(v0_t), active=H.ptr(act), max_coupling=H.ptr(consts[0]), DL=H.ptr(consts[1]),
+            Ebar=H.ptr(consts[2]), E=H.ptr(consts[3]), SL1=H.ptr(consts[4]), SL2=H.ptr(consts[5]),
+            col_log_probs=H.ptr(col), item_idx=H.ptr(item), leaf_state=H.ptr(leaf), leaf_logp=H.ptr(lp),
+            leaf_term=H.ptr(lterm), v=H.ptr(out[0]), aw0=H.ptr(out[1]), aw1=H.ptr(out[2]), aw2=H.ptr(out[3]),
+            aw345=H.ptr(out[4]), aw3=H.ptr(out[5]), aw4=H.ptr(out[6]), col_rows=H.ptr(col_out),
+            relres=H.ptr(relres_t),
+        )
+        H.check(H.lib().kb_wave_backward(tree.handle, io, H.stream(dev)))
+
+    if solver == "neumann":
+        launch(rhs_c, v0, neumann_terms, outs, col_rows, relres)
+    else:
+        # A x = x - J^T x on the active rows (the kernel zeroes inactive rows)
+        zero = torch.zeros_like(rhs_c)
+        scratch = [torch.empty((W, S), device=dev, dtype=dt) for _ in range(8)]
+
+        def apply_a(x):
+            launch(zero, x, 1, scratch, scratch[7], None)
+            return x - scratch[0]
+
+        g_rhs = rhs_c if act is None else rhs_c * act[:, None].to(dt)
+        v_sol = _gmres_fixed(apply_a, g_rhs.contiguous(), int(neumann_terms))
+        # outputs from the solution: no further step (n_terms = 0 keeps v = v_sol)
+        launch(rhs_c, v_sol.contiguous(), 0, outs, col_rows, None)
     if grad_col_log_probs is not None:
         H.sum_rows_into(grad_col_log_probs, col_rows)
+    if self_loop_grad_targets is not None:
+        _accumulate_grad_targets(self_loop_grad_targets, outs, S)
+        base = (outs[0], None, None, None, None, None, None)
+    else:
+        base = tuple(outs)
     if return_last_increment:
-        last = relres if (initial_v is None and int(neumann_terms) > 0) else None
-        return (*outs, last)
-    return tuple(outs)
+        last = relres if (solver == "neumann" and initial_v is None and int(neumann_terms) > 0) else None
+        return (*base, last)
+    return base
+
+
+def _gmres_fixed(apply_a, b, max_iter):
+    """Fixed-iteration unrestarted GMRES over the whole wave (pristine wave_backward.py:574-653).
+
+    Classical Gram-Schmidt with one reorthogonalisation; stops early when the
+    new basis norm falls to eps * max(|b|, 1); the (at most 17 x 16)
+    Hessenberg least-squares problem is solved on the host in float64.
+    """
+    m = int(max_iter)
+    if m < 1:
+        return torch.zeros_like(b)
+    b_norm = torch.linalg.vector_norm(b)
+    bn = float(b_norm)
+    if bn == 0.0:
+        return torch.zeros_like(b)
+    flat = b.reshape(-1)
+    Q = torch.empty((m + 1, flat.numel()), dtype=b.dtype, device=b.device)
+    Hs = torch.zeros((m + 1, m), dtype=b.dtype, device=b.device)
+    Q[0] = flat / b_norm
+    tol = torch.finfo(b.dtype).eps * max(bn, 1.0)
+    tiny = torch.finfo(b.dtype).tiny
+    k = m
+    for j in range(m):
+        w = apply_a(Q[j].view_as(b)).reshape(-1)
+        q = Q[: j + 1]
+        c = torch.mv(q, w)
+        w = torch.addmv(w, q.t(), c, alpha=-1.0)
+        c2 = torch.mv(q, w)
+        w = torch.addmv(w, q.t(), c2, alpha=-1.0)
+        Hs[: j + 1, j] = c + c2
+        h = torch.linalg.vector_norm(w)
+        Hs[j + 1, j] = h
+        if float(h) <= tol:
+            k = j + 1
+            break
+        if j + 1 < m:
+            Q[j + 1] = w / torch.clamp(h, min=tiny)
+    Hh = Hs[: k + 1, :k].double().cpu()
+    e1 = torch.zeros((k + 1,), dtype=torch.float64)
+    e1[0] = bn
+    y = torch.linalg.lstsq(Hh, e1.unsqueeze(-1)).solution.squeeze(-1)
+    return torch.mv(Q[:k].t(), y.to(device=b.device, dtype=b.dtype)).view_as(b)
+
+
+def _accumulate_grad_targets(targets, outs, S):
+    """Add the wave's bucket sums over rows into the caller's accumulators (pristine wave_backward.py:906-953).
+
+    Per state s: grad_E += aw0 + aw2, grad_Ebar += aw1, grad_E_s1 += aw4,
+    grad_E_s2 += aw3, grad_mt += aw2; grad_log_pD += aw0 and grad_log_pS +=
+    aw345 per state with ``param_grad_vector``, else summed over states into
+    their first element.  Accumulators are addressed by state (their first S
+    elements), as the reference's pointer arithmetic does.
+    """
+    gpD, gpS, gE, gEbar, gEs1, gEs2, gmt, vec = targets
+    _v, aw0, aw1, aw2, aw345, aw3, aw4 = outs
+
+    def add_states(dst, src):
+        if dst is None:
+            return
+        flat = dst.reshape(-1)
+        if flat.numel() < S:
+            raise ValueError("self-loop gradient targets need at least S elements")
+        view = flat[:S]
+        if view.dtype == src.dtype and view.is_contiguous():
+            H.sum_rows_into(view, src)
+        else:
+            tmp = torch.zeros((S,), device=src.device, dtype=src.dtype)
+            H.sum_rows_into(tmp, src)
+            view.add_(tmp.to(view.dtype))
+
+    def add_scalar(dst, src):
+        if dst is None:
+            return
+        tmp = torch.zeros((S,), device=src.device, dtype=src.dtype)
+        H.sum_rows_into(tmp, src)
+        tot = torch.zeros((1,), device=src.device, dtype=src.dtype)
+        H.sum_rows_into(tot, tmp.reshape(S, 1))
+        dst.reshape(-1)[:1].add_(tot.to(dst.dtype))
+
+    add_states(gE, aw0)
+    add_states(gE, aw2)
+    add_states(gEbar, aw1)
+    add_states(gEs1, aw4)
+    add_states(gEs2, aw3)
+    add_states(gmt, aw2)
+    if bool(vec):
+        add_states(gpD, aw0)
+        add_states(gpS, aw345)
+    else:
+        add_scalar(gpD, aw0)
+        add_scalar(gpS, aw345)
 
 
 # ------------------------------------------------------------------ split adjoint

@@ -647,18 +647,67 @@ def apply_JT(term, co: SelfLoopCoeffs, tree: Tree):
     return base + parent_term * np.where(pv[None, :], edge, 0.0)
 
 
-def wave_backward_uniform(Pi_s, Pibar_s, row_max, rhs, items, consts, tree, neumann_terms, *, active,
-                          leaf_state=None, dts_r=None):
-    """``wave_backward_uniform_fused`` (pristine wave_backward.py:969-1395, neumann solver).
+def gmres_fixed(apply_a, b, max_iter):
+    """Fixed-iteration unrestarted GMRES (pristine wave_backward.py:574-653).
 
+    ``b`` is flattened into one vector (a whole wave), the Arnoldi basis is
+    orthogonalised by classical Gram-Schmidt with one reorthogonalisation, the
+    iteration stops early when the new basis norm falls to eps * max(|b|, 1),
+    and the solution is the basis combination of the least-squares solution of
+    the Hessenberg system against |b| e1.  max_iter < 1 or b = 0 give 0.
+    """
+    shape = b.shape
+    b = np.asarray(b, dtype=np.float64).reshape(-1)
+    m = int(max_iter)
+    if m < 1:
+        return np.zeros(shape)
+    bn = float(np.linalg.norm(b))
+    if bn == 0.0:
+        return np.zeros(shape)
+    Q = np.zeros((m + 1, b.size))
+    H = np.zeros((m + 1, m))
+    Q[0] = b / bn
+    tol = np.finfo(np.float64).eps * max(bn, 1.0)
+    k = m
+    for j in range(m):
+        w = np.asarray(apply_a(Q[j].reshape(shape)), dtype=np.float64).reshape(-1)
+        c = Q[: j + 1] @ w
+        w = w - Q[: j + 1].T @ c
+        c2 = Q[: j + 1] @ w
+        w = w - Q[: j + 1].T @ c2
+        H[: j + 1, j] = c + c2
+        h = float(np.linalg.norm(w))
+        H[j + 1, j] = h
+        if h <= tol:
+            k = j + 1
+            break
+        if j + 1 < m:
+            Q[j + 1] = w / max(h, np.finfo(np.float64).tiny)
+    e1 = np.zeros(k + 1)
+    e1[0] = bn
+    y = np.linalg.lstsq(H[: k + 1, :k], e1, rcond=None)[0]
+    return (Q[:k].T @ y).reshape(shape)
+
+
+def wave_backward_uniform(Pi_s, Pibar_s, row_max, rhs, items, consts, tree, neumann_terms, *, active,
+                          leaf_state=None, dts_r=None, solver="neumann"):
+    """``wave_backward_uniform_fused`` (pristine wave_backward.py:969-1395).
+
+    ``solver="neumann"``: v = sum_{n <= N} (J^T)^n rhs; ``"gmres"``: v solves
+    (I - J^T) v = rhs over the wave's active rows by ``gmres_fixed`` with
+    N = ``neumann_terms`` iterations (pristine wave_backward.py:1136-1188).
     Returns ``(v_k, aw0, aw1, aw2, aw345, aw3, aw4, col_grad)``; inactive rows
     of every output are zero (``v_k`` inactive rows are "don't care" in the reference).
     """
     co = self_loop_coeffs(Pi_s, Pibar_s, row_max, items, consts, tree, leaf_state=leaf_state, dts_r=dts_r)
     act = np.asarray(active, dtype=bool)[:, None]
     v = np.where(act, rhs, 0.0)
+    if solver == "gmres":
+        v = gmres_fixed(lambda x: np.where(act, x - apply_JT(x, co, tree), 0.0), v, neumann_terms)
+    elif solver != "neumann":
+        raise ValueError(f"unsupported self-loop solver {solver!r}")
     term = v.copy()
-    for _ in range(int(neumann_terms)):
+    for _ in range(int(neumann_terms) if solver == "neumann" else 0):
         term = np.where(act, apply_JT(term, co, tree), 0.0)
         v = v + term
     u = v * co.pcoef
@@ -832,8 +881,9 @@ def backward(prob: Problem, theta, col_weights, saved, *, collect=False, cache=N
     thr = float(so["adjoint_pruning_threshold"])
     prune = bool(so["use_adjoint_pruning"])
     N_terms = int(so["neumann_terms"])
-    if str(so["self_loop_solver"]).lower() != "neumann":
-        raise NotImplementedError("oracle covers the neumann self-loop solver")
+    solver = str(so["self_loop_solver"]).strip().lower()
+    if solver not in ("neumann", "gmres"):
+        raise ValueError(f"unsupported self-loop solver {solver!r}")
     for meta in reversed(prob.wave_metas):
         ws, W = int(meta["start"]), int(meta["W"])
         rows = np.arange(ws, ws + W)
@@ -847,7 +897,7 @@ def backward(prob: Problem, theta, col_weights, saved, *, collect=False, cache=N
         leaf = None if has_splits else prob.leaf_state[rows]
         v, aw0, aw1, aw2, aw345, aw3, aw4, cg = wave_backward_uniform(
             Pi_s[rows], Pibar_s[rows], row_max[rows], rhs, items, consts, tree, N_terms,
-            active=act, leaf_state=leaf, dts_r=dts_r)
+            active=act, leaf_state=leaf, dts_r=dts_r, solver=solver)
         g_col += cg
         if cache is not None:
             cache.setdefault("waves", []).append(dict(

@@ -64,6 +64,40 @@ def test_glue_backward_matches_oracle(name, statewise):
     assert rt <= 1e-4 and rc <= 1e-4
 
 
+@pytest.mark.parametrize("name,statewise", [("tiny", None), ("1", True)])
+def test_glue_backward_with_gmres_matches_oracle(name, statewise):
+    """self_loop_solver="gmres" through the per-call path against the oracle's GMRES backward."""
+    import dataclasses
+
+    import kbench_oracle as O
+    from dropin import run_backward, run_forward
+    from kbench.fused import problem_to_captured
+    from kbench.runtime import make_static
+
+    print(f"[glue-backward gmres] config={name} statewise={statewise}", flush=True)
+    p = kbtest.problem(name, statewise)
+    cap = problem_to_captured(p)
+    cap["meta"] = dict(cap["meta"], solver_options=dict(cap["meta"]["solver_options"], self_loop_solver="gmres"))
+    static = make_static(cap, "cuda")
+    assert static.solver_options.self_loop_solver == "gmres"
+    theta, cw = cap["inputs"]["theta"].cuda(), cap["inputs"]["col_weights"].cuda()
+    loss, saved = run_forward(static, theta, cw)
+    gt, gc = run_backward(static, theta, cw, saved)
+    torch.cuda.synchronize()
+    prob = O.Problem.from_dict(p)
+    prob.so.update(self_loop_solver="gmres")
+    th64 = np.asarray(p["inputs"]["theta"], dtype=np.float32).astype(np.float64)
+    cw64 = np.asarray(p["inputs"]["col_weights"], dtype=np.float64)
+    _, ref = O.forward(prob, th64, cw64)
+    ref_gt, ref_gc, _ = O.backward(prob, th64, cw64, ref)
+    neu = kbtest.oracle_backward(name, statewise)[0]
+    rt = kbtest.norm_rel(gt.cpu().numpy(), ref_gt)
+    rc = kbtest.norm_rel(gc.cpu().numpy(), ref_gc)
+    dn = kbtest.norm_rel(ref_gt, neu)
+    print(f"  grad_theta normrel={rt:.3e} grad_col normrel={rc:.3e} (gmres vs neumann oracle: {dn:.3e})")
+    assert rt <= 1e-4 and rc <= 1e-4
+
+
 def test_glue_backward_is_deterministic():
     from dropin import run_backward, run_forward
 

@@ -259,7 +259,7 @@ def test_leaf_init_and_sweeps_match_oracle(dt):
 
 
 # ---------------------------------------------------------------------- backward
-def _wave_backward_case(P, dt, m, use_col, neumann_terms=5):
+def _wave_backward_case(P, dt, m, use_col, neumann_terms=5, solver="neumann", grad_targets=None):
     """(device outputs, oracle outputs, active mask) of one wave_backward_uniform_fused call."""
     from kbench.core.kernels.dts_fused import compute_dts_forward
     from kbench.core.kernels.wave_backward import active_mask_from_rhs_absmax_fused, wave_backward_uniform_fused
@@ -288,7 +288,7 @@ def _wave_backward_case(P, dt, m, use_col, neumann_terms=5):
         dts = _np(dts_d)  # same values within tolerance; the oracle continues from the device's
     leaf = None if has_splits else P.prob.leaf_state[rows]
     ref = O.wave_backward_uniform(P.Pi[rows], P.Pb[rows], P.rmax[rows], rhs, items, P.oconsts(use_col),
-                                  P.prob.tree, neumann_terms, active=act, leaf_state=leaf, dts_r=dts)
+                                  P.prob.tree, neumann_terms, active=act, leaf_state=leaf, dts_r=dts, solver=solver)
     mt, DL, Eb, Ev, SL1, SL2 = P.dconsts()
     gcol = torch.zeros((S,), dtype=dt, device="cuda")
     got = wave_backward_uniform_fused(
@@ -296,9 +296,10 @@ def _wave_backward_case(P, dt, m, use_col, neumann_terms=5):
         h["node_child1"], h["node_child2"], None, neumann_terms=neumann_terms, leaf_state_idx=P.leaf_idx,
         leaf_logp=_t(P.pS, dt), has_leaf_term=not has_splits, active_mask=act_d, node_parent=h["node_parent"],
         max_ancestor_depth=int(h["max_ancestor_depth"]), pibar_row_max=_t(P.rmax, dt), item_idx=P.item_idx,
-        item_indexed_consts=True, grad_col_log_probs=gcol, use_col_weights=use_col, **P.levels())
+        item_indexed_consts=True, grad_col_log_probs=gcol, use_col_weights=use_col, self_loop_solver=solver,
+        self_loop_grad_targets=grad_targets, **P.levels())
     torch.cuda.synchronize()
-    return [_np(x) for x in got] + [_np(gcol)], list(ref), act
+    return [None if x is None else _np(x) for x in got] + [_np(gcol)], list(ref), act
 
 
 @pytest.mark.parametrize("dt", [torch.float64, torch.float32])
@@ -318,6 +319,50 @@ def test_wave_backward_uniform_outputs_match_oracle(dt, use_col):
             e = _rel(g, r)
             print(f"  wave@{int(m['start'])} {name}: rel={e:.3e}")
             assert e <= TOL[dt], name
+
+
+@pytest.mark.parametrize("dt", [torch.float64, torch.float32])
+def test_wave_backward_gmres_matches_oracle(dt):
+    """self_loop_solver="gmres": the wave's GMRES solution (host Krylov loop over HIP J^T applications)
+    and every output computed from it, against the oracle's GMRES (pristine wave_backward.py:574-653)."""
+    P = point(dt)
+    print(f"[unit wave_backward gmres] config={NAME} statewise={STATEWISE} dtype={dt}", flush=True)
+    names = ("v_k", "aw0", "aw1", "aw2", "aw345", "aw3", "aw4", "grad_col")
+    for m in (P.leaf_waves()[0], *P.wide_split_waves(2)):
+        got, ref, act = _wave_backward_case(P, dt, m, True, neumann_terms=6, solver="gmres")
+        for name, g, r in zip(names, got, ref):
+            if name == "v_k":
+                g, r = g[act], r[act]
+            elif name != "grad_col":
+                assert (g[~act] == 0).all(), f"{name}: inactive rows must be zero"
+            e = _rel(g, r)
+            print(f"  wave@{int(m['start'])} {name}: rel={e:.3e}")
+            assert e <= TOL[dt], name
+
+
+@pytest.mark.parametrize("vector", [True, False])
+def test_self_loop_grad_targets_receive_the_bucket_sums(vector):
+    """self_loop_grad_targets: the buckets are added into the caller's accumulators, summed over the
+    wave's rows per state (pD / pS per state or in total), and not returned."""
+    dt = torch.float64
+    P = point(dt)
+    S = P.prob.S
+    print(f"[unit wave_backward grad targets] param_grad_vector={vector}", flush=True)
+    m = P.wide_split_waves(1)[0]
+    base, _, _ = _wave_backward_case(P, dt, m, False)
+    v, aw0, aw1, aw2, aw345, aw3, aw4, _ = base
+    z = lambda n: torch.zeros((n,), dtype=dt, device="cuda")
+    tg = [z(S if vector else 1), z(S if vector else 1), z(S), z(S), z(S), z(S), z(S)]
+    got, _, _ = _wave_backward_case(P, dt, m, False, grad_targets=(*tg, vector))
+    assert all(x is None for x in got[1:7])
+    assert _rel(got[0], v) == 0.0
+    want = [aw0.sum(0), aw345.sum(0), (aw0 + aw2).sum(0), aw1.sum(0), aw4.sum(0), aw3.sum(0), aw2.sum(0)]
+    if not vector:
+        want[0], want[1] = want[0].sum(keepdims=True), want[1].sum(keepdims=True)
+    for name, t, w in zip(("pD", "pS", "E", "Ebar", "E_s1", "E_s2", "mt"), tg, want):
+        e = _rel(_np(t), w)
+        print(f"  {name}: rel={e:.3e}")
+        assert e <= 1e-12, name
 
 
 @pytest.mark.parametrize("dt", [torch.float64, torch.float32])

@@ -29,7 +29,10 @@ lower is better.
   glue's call sequence (``tests/dropin``): one launch per sweep and per wave
   as the reference launches them (the pristine-structure proxy), the same with
   each wave's sweep chain collapsed into one launch (``KBENCH_FUSE_SWEEPS``),
-  and the driver's own floor (every wrapper replaced by a no-op).
+  and the driver's own floor (every wrapper replaced by a no-op); and the
+  ratio of the first of these to ``value`` (the speedup against the
+  pristine-structure proxy on the same GPU; ``vs_baseline`` stays null, no
+  published number exists for this metric).
 """
 
 from __future__ import annotations
@@ -196,15 +199,16 @@ def _time_host(step, warmup: int, steps: int) -> float:
     return statistics.median(ts)
 
 
-def per_call_timings(static, theta, cw, steps: int = 3) -> dict:
-    """ms per solve through the per-call wrappers in the reference glue's call sequence."""
+def per_call_timings(static, theta, cw, steps: int = 3, static_levels=None) -> dict:
+    """ms per solve through the per-call wrappers in the reference glue's call sequence.
+
+    With ``static_levels`` (the same problem regrouped by ``synth.level_waves``)
+    the three timings are repeated on one wave per dependency level.
+    """
     sys.path.insert(0, str(ROOT / "tests"))
     from dropin.kernels import noop
     from dropin.solve import SolvePlan
     from kbench.core.kernels import wave_step
-
-    plan = SolvePlan(static)
-    floor_plan = SolvePlan(static, kernels=noop())
 
     def solve(p):
         def step():
@@ -212,28 +216,44 @@ def per_call_timings(static, theta, cw, steps: int = 3) -> dict:
             p.backward(theta, cw, sv)
         return step
 
-    old = wave_step.FUSE_SWEEPS
-    try:
-        wave_step.FUSE_SWEEPS = False
-        per_launch = _time_host(solve(plan), 1, steps)
-        wave_step.FUSE_SWEEPS = True
-        fused = _time_host(solve(plan), 1, steps)
-    finally:
-        wave_step.FUSE_SWEEPS = old
-    floor = _time_host(solve(floor_plan), 1, steps)
-    return {
-        "ms_one_launch_per_sweep": round(per_launch, 3),
-        "ms_sweep_chains_fused": round(fused, 3),
-        "ms_glue_floor": round(floor, 3),
+    def three(st):
+        plan = SolvePlan(st)
+        floor_plan = SolvePlan(st, kernels=noop())
+        old = wave_step.FUSE_SWEEPS
+        try:
+            wave_step.FUSE_SWEEPS = False
+            per_launch = _time_host(solve(plan), 1, steps)
+            wave_step.FUSE_SWEEPS = True
+            fused = _time_host(solve(plan), 1, steps)
+        finally:
+            wave_step.FUSE_SWEEPS = old
+        floor = _time_host(solve(floor_plan), 1, steps)
+        return round(per_launch, 3), round(fused, 3), round(floor, 3)
+
+    per_launch, fused, floor = three(static)
+    out = {
+        "ms_one_launch_per_sweep": per_launch,
+        "ms_sweep_chains_fused": fused,
+        "ms_glue_floor": floor,
         "note": ("host wall time (median of %d) of a fwd+bwd solve through the per-call wrappers in the "
                  "reference glue's call sequence: one launch per sweep and wave as the reference launches "
                  "them (the pristine-structure proxy); the same with KBENCH_FUSE_SWEEPS=1 (each wave's sweep "
                  "chain in one launch); the driver alone with no-op wrappers" % steps),
     }
+    if static_levels is not None:
+        lp, lf, lfl = three(static_levels)
+        out["level_waves"] = {
+            "n_waves": len(static_levels.wave_layout["wave_metas"]),
+            "ms_one_launch_per_sweep": lp, "ms_sweep_chains_fused": lf, "ms_glue_floor": lfl,
+            "note": ("the same three timings with the rows regrouped into one wave per dependency level "
+                     "(synth.level_waves: same rows, same per-row results, fewer waves, so fewer wrapper calls)"),
+        }
+    return out
 
 
-def bench_hvp(args, static, theta, cw, summ) -> None:
-    """Exact Hessian-vector products (config 5) through the per-call wrappers."""
+def bench_hvp(args, static, theta, cw, summ, static_levels) -> None:
+    """Exact Hessian-vector products (config 5) through the per-call wrappers, on the size waves and on
+    one wave per dependency level (``synth.level_waves``; the same HVP, fewer wrapper calls)."""
     import numpy as np
     import torch
 
@@ -241,29 +261,36 @@ def bench_hvp(args, static, theta, cw, summ) -> None:
     from dropin.hvp import HvpPlan
     from dropin.solve import plan_of, run_forward
 
-    _, sv = run_forward(static, theta, cw)
-    t0 = time.perf_counter()
-    hvp = HvpPlan(plan_of(static), theta, cw, sv)
-    torch.cuda.synchronize()
-    cache_ms = (time.perf_counter() - t0) * 1e3
     g = np.random.default_rng(0)
     us = [torch.as_tensor(g.normal(size=tuple(theta.shape)), dtype=theta.dtype, device=theta.device).reshape(-1)
           for _ in range(4)]
-    k = [0]
 
-    def step():
-        k[0] += 1
-        hvp(us[k[0] % len(us)])
+    def timed(st):
+        _, sv = run_forward(st, theta, cw)
+        t0 = time.perf_counter()
+        hvp = HvpPlan(plan_of(st), theta, cw, sv)
+        torch.cuda.synchronize()
+        cache_ms = (time.perf_counter() - t0) * 1e3
+        k = [0]
 
-    ms = _time_host(step, args.warmup, args.steps)
+        def step():
+            k[0] += 1
+            hvp(us[k[0] % len(us)])
+
+        return _time_host(step, args.warmup, args.steps), cache_ms
+
+    ms_size, cache_size = timed(static)
+    ms, cache_ms = timed(static_levels)
     print(json.dumps({
         "metric": "exact Hessian-vector product ms (config 5: per-species theta, forward tangent + tangent adjoint)",
         "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp32", "data": "synthetic",
-        "config": {"workload": f"config{args.config} exact HVP through the per-call wrappers", "S": summ["S"],
-                   "C": summ["C"], "point_cache_ms": round(cache_ms, 3)},
+        "config": {"workload": (f"config{args.config} exact HVP through the per-call wrappers, rows in one wave per "
+                                f"dependency level ({len(static_levels.wave_layout['wave_metas'])} waves)"),
+                   "S": summ["S"], "C": summ["C"], "point_cache_ms": round(cache_ms, 3)},
         "ms_per_newton_cg_step_50_hvps": round(50 * ms, 2),
+        "size_waves": {"n_waves": summ["n_waves"], "ms": round(ms_size, 4), "point_cache_ms": round(cache_size, 3)},
     }))
 
 
@@ -343,10 +370,14 @@ def main():
     static = make_static(cap, dev)
     theta = cap["inputs"]["theta"].to(dev)
     cw = cap["inputs"]["col_weights"].to(dev)
+    static_levels = None
+    if args.workload != "solve" or not args.no_per_call:
+        static_levels = make_static(problem_to_captured(synth.level_waves(problem)[0]), dev)
     if args.workload == "hvp":
-        return bench_hvp(args, static, theta, cw, summ)
+        return bench_hvp(args, static, theta, cw, summ, static_levels)
     if args.workload == "glue":
-        print(json.dumps({"config": f"config{args.config}", **per_call_timings(static, theta, cw, args.steps)}))
+        print(json.dumps({"config": f"config{args.config}",
+                          **per_call_timings(static, theta, cw, args.steps, static_levels)}))
         return
     solver = FusedSolver(static, static.solver_options)
     for i in range(args.warmup):
@@ -420,7 +451,10 @@ def main():
         dedup_off = {"ms": round(statistics.mean(t_all), 4), "fwd_ms": round(statistics.mean(f_all), 4),
                      "bwd_ms": round(statistics.mean(b_all), 4)}
         del flat
-    per_call = None if args.no_per_call else per_call_timings(static, theta, cw)
+    per_call = None if args.no_per_call else per_call_timings(static, theta, cw, static_levels=static_levels)
+    if per_call is not None:
+        # the whole-pass solve against the pristine-structure proxy on the same GPU
+        per_call["speedup_vs_pristine_structure_proxy"] = round(per_call["ms_one_launch_per_sweep"] / ms, 2)
 
     out = {
         "metric": "fwd+bwd ms per solve at S=1024,C=32k; achieved HBM GB/s vs roofline",

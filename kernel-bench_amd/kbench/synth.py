@@ -641,3 +641,98 @@ def family_subset(problem: dict, families) -> dict:
     if "tree" in problem:
         out["tree"] = problem["tree"]
     return out
+
+
+def level_waves(problem: dict, max_wave_rows: int | None = None) -> tuple[dict, np.ndarray]:
+    """The same problem with its rows regrouped into one wave per clade-DAG level -> (problem, new_of_old).
+
+    A row's level is 0 without splits, else one more than the highest level
+    among its splits' children.  Rows are renumbered by (level, old row id);
+    each level becomes one wave (chunked to ``max_wave_rows`` if given), in
+    increasing level.  Every row keeps its splits (eq1 parents first, then the
+    ge2 parents, each parent's splits in their old order), its leaf state, its
+    item and root status.  Since a row of the truncated forward and of its
+    adjoint depends only on its own children, which lie on lower levels, every
+    row's result is the same as under the size waves (summation order across
+    parents aside); only the number of waves (wrapper calls and launches per
+    solve) changes: 144 -> 19 at config 3.  ``new_of_old[r]`` is the new id
+    of old row r (row-indexed outputs map back with ``out[new_of_old]``).
+    """
+    wl = problem["static"]["wave_layout"]
+    C = int(np.asarray(wl["leaf_state_index"]).shape[0])
+    splits_of = [[] for _ in range(C)]  # old parent -> [(old l, old r, lsp)] in old split order
+    for m in wl["wave_metas"]:
+        if "sl" not in m:
+            continue
+        s0 = int(m["start"])
+        lsp = np.asarray(m.get("log_split_probs", np.zeros(len(m["sl"]))), dtype=np.float64)
+        for a, b, w, p in zip(np.asarray(m["sl"]), np.asarray(m["sr"]), np.asarray(m["reduce_idx"]), lsp):
+            splits_of[s0 + int(w)].append((int(a), int(b), float(p)))
+    level = np.zeros(C, dtype=np.int64)
+    for m in wl["wave_metas"]:  # waves are in dependency order: children first
+        s0, W = int(m["start"]), int(m["W"])
+        for r in range(s0, s0 + W):
+            if splits_of[r]:
+                level[r] = 1 + max(max(level[a], level[b]) for a, b, _ in splits_of[r])
+    order = np.lexsort((np.arange(C), level))  # new -> old
+    new_of_old = np.empty(C, dtype=np.int64)
+    new_of_old[order] = np.arange(C)
+    cap = int(max_wave_rows) if max_wave_rows else C
+    metas = []
+    start = 0
+    while start < C:
+        lv = level[order[start]]
+        end = start
+        while end < C and level[order[end]] == lv and end - start < cap:
+            end += 1
+        W = end - start
+        meta = {"start": start, "W": W}
+        if lv > 0:
+            eq1, ge2 = [], []
+            for w in range(W):
+                sp = [(int(new_of_old[a]), int(new_of_old[b]), p) for a, b, p in splits_of[int(order[start + w])]]
+                (eq1 if len(sp) == 1 else ge2).append((w, sp))
+            sl, sr, red, lsp = [], [], [], []
+            for w, sp in eq1:
+                for a, b, p in sp:
+                    sl.append(a); sr.append(b); red.append(w); lsp.append(p)
+            n_eq1 = len(sl)
+            ge2_ptr, ge2_parent = [0], []
+            for w, sp in ge2:
+                for a, b, p in sp:
+                    sl.append(a); sr.append(b); red.append(w); lsp.append(p)
+                ge2_ptr.append(len(sl) - n_eq1)
+                ge2_parent.append(w)
+            meta.update({
+                "sl": np.asarray(sl, dtype=np.int64),
+                "sr": np.asarray(sr, dtype=np.int64),
+                "reduce_idx": np.asarray(red, dtype=np.int64),
+                "log_split_probs": np.asarray(lsp, dtype=np.float64),
+                "n_eq1": n_eq1,
+                "eq1_reduce_idx": np.asarray(red[:n_eq1], dtype=np.int64),
+                "ge2_ptr": np.asarray(ge2_ptr, dtype=np.int64),
+                "ge2_parent_ids": np.asarray(ge2_parent, dtype=np.int64),
+                "ge2_max_fanout": int(max(np.diff(ge2_ptr), default=0)),
+            })
+        metas.append(meta)
+        start = end
+    st = problem["static"]
+    out = {
+        "meta": dict(problem["meta"]),
+        "static": {
+            "wave_layout": {
+                "leaf_state_index": np.asarray(wl["leaf_state_index"])[order],
+                "root_row_ids": new_of_old[np.asarray(wl["root_row_ids"])].astype(np.int64),
+                "item_idx": np.asarray(wl["item_idx"])[order],
+                "wave_metas": metas,
+            },
+            "state_helpers": st["state_helpers"],
+            "rate_item_idx": np.asarray(st["rate_item_idx"])[order],
+            "itemwise": st["itemwise"],
+            "statewise": st["statewise"],
+        },
+        "inputs": problem["inputs"],
+    }
+    if "tree" in problem:
+        out["tree"] = problem["tree"]
+    return out, new_of_old

@@ -98,6 +98,41 @@ def test_glue_backward_with_gmres_matches_oracle(name, statewise):
     assert rt <= 1e-4 and rc <= 1e-4
 
 
+def test_level_waves_give_the_same_per_call_solve_and_hvp():
+    """Rows regrouped into one wave per dependency level (synth.level_waves): the per-call forward gives
+    bitwise the same rows, the gradients and an exact HVP agree with the size-wave layout."""
+    from dropin import run_backward, run_forward
+    from dropin.hvp import HvpPlan
+    from dropin.solve import plan_of
+    from kbench import synth
+    from kbench.fused import problem_to_captured
+    from kbench.runtime import make_static
+
+    print("[level waves] config=1 statewise per-call solve + exact HVP", flush=True)
+    p = kbtest.problem("1", True)
+    q, new_of_old = synth.level_waves(p)
+    out = []
+    for prob in (p, q):
+        cap = problem_to_captured(prob)
+        static = make_static(cap, "cuda")
+        theta, cw = cap["inputs"]["theta"].cuda(), cap["inputs"]["col_weights"].cuda()
+        loss, saved = run_forward(static, theta, cw)
+        gt, gc = run_backward(static, theta, cw, saved)
+        u = torch.linspace(-1.0, 1.0, theta.numel(), dtype=theta.dtype, device="cuda")
+        hv = HvpPlan(plan_of(static), theta, cw, saved)(u)
+        torch.cuda.synchronize()
+        out.append((loss, saved, gt, gc, hv, len(prob["static"]["wave_layout"]["wave_metas"])))
+    (la, sa, ga, gca, ha, na), (lb, sb, gb, gcb, hb, nb) = out
+    idx = torch.as_tensor(new_of_old, device="cuda")
+    print(f"  waves {na} -> {nb}; loss {float(la):.9g} vs {float(lb):.9g}")
+    assert float(la) == float(lb)
+    for k in ("pi_wave", "pibar_wave", "pibar_row_max"):
+        assert torch.equal(sa[k], sb[k].index_select(0, idx)), k
+    rt, rc, rh = kbtest.norm_rel_t(gb, ga), kbtest.norm_rel_t(gcb, gca), kbtest.norm_rel_t(hb, ha)
+    print(f"  grad_theta rel={rt:.3e} grad_col rel={rc:.3e} hvp rel={rh:.3e}")
+    assert rt <= 1e-6 and rc <= 1e-6 and rh <= 1e-5
+
+
 def test_glue_backward_is_deterministic():
     from dropin import run_backward, run_forward
 

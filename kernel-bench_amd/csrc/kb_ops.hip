@@ -272,7 +272,9 @@ struct WsArgs {
 };
 
 // n_sweeps self-loop sweeps of one row; between sweeps the row stays in LDS
-// (Pr), so the result equals n_sweeps one-sweep launches bit for bit.
+// (Pr), so the result equals n_sweeps one-sweep launches bit for bit.  The
+// thread's tree entries (children, Euler events, entry events) and the row's
+// constants are read once, before the first sweep.
 template <typename T, int CPT>
 __global__ __launch_bounds__(NT) void wave_step_kernel(OpsTree t, WsArgs<T> a) {
   extern __shared__ unsigned char smraw[];
@@ -292,8 +294,60 @@ __global__ __launch_bounds__(NT) void wave_step_kernel(OpsTree t, WsArgs<T> a) {
     const int s = threadIdx.x + k * NT;
     if (s < S) Pr[s] = in[s];
   }
-  __syncthreads();
   const long long lstate = a.use_leaf ? a.leaf_state[grow] : -1;
+  int c1v[CPT], c2v[CPT], tinv[CPT], evv[2 * CPT];
+  T kmt[CPT], kDL[CPT], kEb[CPT], kE[CPT], kS1[CPT], kS2[CPT], klf[CPT], kd[CPT], kcol[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int s = threadIdx.x + k * NT;
+    c1v[k] = c2v[k] = -1;
+    tinv[k] = 0;
+    kmt[k] = kDL[k] = kEb[k] = kE[k] = kS1[k] = kS2[k] = kcol[k] = T(0);
+    klf[k] = kd[k] = NI;
+    if (s < S) {
+      const size_t ci = cb + s;
+      c1v[k] = t.c1[s];
+      c2v[k] = t.c2[s];
+      tinv[k] = t.tin[s];
+      kmt[k] = a.mt[ci];
+      kDL[k] = a.DL[ci];
+      kEb[k] = a.Ebar[ci];
+      kE[k] = a.E[ci];
+      kS1[k] = a.SL1[ci];
+      kS2[k] = a.SL2[ci];
+      if (lstate == s) klf[k] = a.leaf_logp[(size_t)item * S + s];
+      if (a.dts) kd[k] = a.dts[(size_t)w * S + s];
+      if (a.use_col) kcol[k] = a.col[s];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 2 * CPT; ++j) {
+    const int q = threadIdx.x + j * NT;
+    evv[j] = q < 2 * S ? t.ev[q] : 0;
+  }
+  // ancestors-or-self path sums of x (LDS, column order) into ps (may alias x):
+  // +x at the entry event and -x at the exit event of each column, scanned,
+  // read back at the entry event
+  auto path_sums_own = [&](const T* x, T* ps) {
+#pragma unroll
+    for (int j = 0; j < 2 * CPT; ++j) {
+      const int q = threadIdx.x + j * NT;
+      if (q < 2 * S) {
+        const int e = evv[j];
+        const T v = x[e >> 1];
+        EV[q] = (e & 1) ? -v : v;
+      }
+    }
+    __syncthreads();
+    block_scan(EV, 2 * S, red);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int s = threadIdx.x + k * NT;
+      if (s < S) ps[s] = EV[tinv[k]];
+    }
+    __syncthreads();
+  };
+  __syncthreads();
   T wv[CPT], res[CPT];
   T ldiff = 0;
   for (int sweep = 0; sweep < a.n_sweeps; ++sweep) {
@@ -304,7 +358,7 @@ __global__ __launch_bounds__(NT) void wave_step_kernel(OpsTree t, WsArgs<T> a) {
       const int s = threadIdx.x + k * NT;
       wv[k] = NI;
       if (s < S) {
-        wv[k] = a.use_col ? a.col[s] + Pr[s] : Pr[s];
+        wv[k] = a.use_col ? kcol[k] + Pr[s] : Pr[s];
         lm = tmax(lm, wv[k]);
       }
     }
@@ -321,32 +375,27 @@ __global__ __launch_bounds__(NT) void wave_step_kernel(OpsTree t, WsArgs<T> a) {
       }
     }
     const T rowsum = block_sum(ls, red);
-    path_sums(t, X, EV, X, red);
+    path_sums_own(X, X);
     ldiff = 0;
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int s = threadIdx.x + k * NT;
       res[k] = NI;
       if (s < S) {
-        const size_t ci = cb + s;
         const T denom = rowsum - X[s];
-        const T pibar_w = denom > T(0) ? xlog2(denom) + M + a.mt[ci] : NI;
+        const T pibar_w = denom > T(0) ? xlog2(denom) + M + kmt[k] : NI;
         const T pi_w = Pr[s];
-        const int c1 = t.c1[s], c2 = t.c2[s];
-        const T ps1 = c1 >= 0 ? Pr[c1] : NI;
-        const T ps2 = c2 >= 0 ? Pr[c2] : NI;
-        const T t0 = a.DL[ci] + pi_w;
-        const T t1 = pi_w + a.Ebar[ci];
-        const T t2 = pibar_w + a.E[ci];
-        const T t3 = a.SL1[ci] + ps1;
-        const T t4 = a.SL2[ci] + ps2;
-        const T t5 = (lstate == s) ? a.leaf_logp[(size_t)item * S + s] : NI;
+        const T ps1 = c1v[k] >= 0 ? Pr[c1v[k]] : NI;
+        const T ps2 = c2v[k] >= 0 ? Pr[c2v[k]] : NI;
+        const T t0 = kDL[k] + pi_w;
+        const T t1 = pi_w + kEb[k];
+        const T t2 = pibar_w + kE[k];
+        const T t3 = kS1[k] + ps1;
+        const T t4 = kS2[k] + ps2;
+        const T t5 = klf[k];
         T m = tmax(tmax(tmax(t0, t1), tmax(t2, t3)), tmax(t4, t5));
-        T d = NI;
-        if (a.dts) {
-          d = a.dts[(size_t)w * S + s];
-          m = tmax(m, d);
-        }
+        const T d = kd[k];
+        if (a.dts) m = tmax(m, d);
         const T ms = msafe(m);
         T sum = xexp2(t0 - ms) + xexp2(t1 - ms) + xexp2(t2 - ms) + xexp2(t3 - ms) + xexp2(t4 - ms) + xexp2(t5 - ms);
         if (a.dts) sum += xexp2(d - ms);
@@ -385,7 +434,7 @@ __global__ __launch_bounds__(NT) void wave_step_kernel(OpsTree t, WsArgs<T> a) {
     const int s = threadIdx.x + k * NT;
     wv[k] = NI;
     if (s < S) {
-      wv[k] = a.use_col ? a.col[s] + res[k] : res[k];
+      wv[k] = a.use_col ? kcol[k] + res[k] : res[k];
       lm2 = tmax(lm2, wv[k]);
     }
   }
@@ -402,14 +451,14 @@ __global__ __launch_bounds__(NT) void wave_step_kernel(OpsTree t, WsArgs<T> a) {
     }
   }
   const T rowsum2 = block_sum(ls2, red);
-  path_sums(t, Pr, EV, Pr, red);
+  path_sums_own(Pr, Pr);
   T* pb = a.Pibar + (size_t)grow * S;
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int s = threadIdx.x + k * NT;
     if (s < S) {
       const T denom = rowsum2 - Pr[s];
-      pb[s] = denom > T(0) ? xlog2(denom) + M2 + a.mt[cb + s] : NI;
+      pb[s] = denom > T(0) ? xlog2(denom) + M2 + kmt[k] : NI;
     }
   }
   if (threadIdx.x == 0) a.rowmax[grow] = M2;

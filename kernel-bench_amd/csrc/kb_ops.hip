@@ -19,6 +19,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "kb_ops_common.hpp"
@@ -462,6 +463,200 @@ __global__ __launch_bounds__(NT) void wave_step_kernel(OpsTree t, WsArgs<T> a) {
     }
   }
   if (threadIdx.x == 0) a.rowmax[grow] = M2;
+}
+
+// Chains of float sweeps: the same sweeps with the row's positions in
+// preorder, thread t owning positions t*CPT + k.  A sweep's ancestor path sums are a register scan
+// over preorder positions minus an exclusive scan over postorder slots,
+// ps(i) = Pre(i) - PostEx(tin(i) - i), so a sweep takes three barriers (row
+// maximum, preorder totals, postorder totals) instead of the Euler-tour scan's
+// eight.  The arithmetic per position is the one-sweep formula above; the
+// row sums come in a different order, so results agree with it to rounding.
+template <int CPT>
+__global__ __launch_bounds__(NT) void wave_step_pre_kernel(OpsTree t, WsArgs<float> a) {
+  constexpr int MAXS = NT * CPT;
+  constexpr int LD = MAXS + 64;
+  constexpr int ZERO = MAXS;     // padding slot: 0 in X
+  constexpr int SEG = 64 * CPT;  // postorder slots per wavefront
+  extern __shared__ __align__(16) unsigned char smraw[];
+  float* R = reinterpret_cast<float*>(smraw);  // Pi at preorder positions: input, children, outputs
+  float* X = R + LD;                           // 2^(col + Pi - M) at preorder positions
+  float* Q = X + LD;                           // exclusive postorder scan
+  __shared__ float wM[NW], wA[NW], wB[NW];
+  const int S = t.S;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int w = blockIdx.x;
+  const long long grow = a.ws + w;
+  const float NI = -__builtin_inff();
+  const long long item = a.item[grow];
+  const size_t cb = (size_t)(item * a.cstride);
+  const float* in = a.Pi_in + (size_t)(a.pi_ws + w) * S;
+  const long long lstate = a.use_leaf ? a.leaf_state[grow] : -1;
+  // the input row, read by column (coalesced), to its preorder positions
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int sc = tid + j * NT;
+    if (sc < S) R[t.ppos[sc]] = in[sc];
+  }
+  if (tid < 64) X[MAXS + tid] = 0.0f;
+  // own positions: tables and the row's constants (read once for all sweeps)
+  int c1p[CPT], c2p[CPT], nex[CPT], qp[CPT];
+  bool okp[CPT];
+  float kmt[CPT], kDL[CPT], kEb[CPT], kE[CPT], kS1[CPT], kS2[CPT], klf[CPT], kd[CPT], kcol[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int i = kb::own_pos_c<NT, CPT>(k);
+    okp[k] = i < S;
+    c1p[k] = c2p[k] = -1;
+    nex[k] = 0;
+    qp[k] = ZERO;
+    kmt[k] = kDL[k] = kEb[k] = kE[k] = kS1[k] = kS2[k] = kcol[k] = 0.0f;
+    klf[k] = kd[k] = NI;
+    if (okp[k]) {
+      const int col = t.pcol[i];
+      const size_t ci = cb + col;
+      c1p[k] = t.pc1[i];
+      c2p[k] = t.pc2[i];
+      nex[k] = t.pnex[i];
+      qp[k] = t.ppost[i];
+      kmt[k] = a.mt[ci];
+      kDL[k] = a.DL[ci];
+      kEb[k] = a.Ebar[ci];
+      kE[k] = a.E[ci];
+      kS1[k] = a.SL1[ci];
+      kS2[k] = a.SL2[ci];
+      if (lstate == col) klf[k] = a.leaf_logp[(size_t)item * S + col];
+      if (a.dts) kd[k] = a.dts[(size_t)w * S + col];
+      if (a.use_col) kcol[k] = a.col[col];
+    }
+  }
+  __syncthreads();
+  float pr[CPT];
+  kb::lds_load_own<CPT>(R, pr);
+#pragma unroll
+  for (int k = 0; k < CPT; ++k)
+    if (!okp[k]) pr[k] = NI;
+
+  // One path-sum pass over x (own positions, log2): M = max(col + x), the row
+  // sum and ps(i) of 2^(col + x - M); x is published in R for the child
+  // gathers (ch1, ch2), read before the third barrier.  Callers separate R's
+  // previous readers from this write by a barrier.
+  float ps[CPT], ch1[CPT], ch2[CPT], rowsum = 0.0f, M = NI;
+  auto pass = [&](const float (&x)[CPT]) {
+    float lm = NI;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k)
+      if (okp[k]) lm = fmaxf(lm, kcol[k] + x[k]);
+    kb::lds_store_own<CPT>(R, x);
+    M = kb::block_max1<NT>(lm, wM);  // barrier 1: also publishes R
+    const float Ms = M == NI ? 0.0f : M;
+    float y[CPT], sp[CPT], ta = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      y[k] = okp[k] ? exp2f(kcol[k] + x[k] - Ms) : 0.0f;
+      ta += y[k];
+      sp[k] = ta;
+    }
+    const float wa = kb::wave_scan_incl(ta);
+    kb::lds_store_own<CPT>(X, y);
+    if (lane == 63) wA[wv] = wa;
+    __syncthreads();  // barrier 2
+    const float tp = kb::lds_wave_values<NW>(wA, lane, 0.0f);
+    float yq[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      yq[k] = X[qp[k]];
+      ch1[k] = c1p[k] >= 0 ? R[c1p[k]] : NI;
+      ch2[k] = c2p[k] >= 0 ? R[c2p[k]] : NI;
+    }
+    const float ip = kb::wave_scan_first<NW>(tp);
+    rowsum = kb::lane_value(ip, NW - 1);
+    const float offp = kb::lane_value(ip - tp, wv) + (wa - ta);
+    float sq[CPT], tb = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      sq[k] = tb;
+      tb += yq[k];
+    }
+    const float wb = kb::wave_scan_incl(tb);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) sq[k] += wb - tb;
+    kb::lds_store_own<CPT>(Q, sq);
+    if (lane == 63) wB[wv] = wb;
+    __syncthreads();  // barrier 3
+    const float tq = kb::lds_wave_values<NW>(wB, lane, 0.0f);
+    const float eq = kb::wave_scan_first<NW>(tq) - tq;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int n = nex[k];
+      ps[k] = (sp[k] + offp) - (Q[n] + __shfl(eq, n / SEG, 64));
+    }
+  };
+
+  __syncthreads();  // every thread has read its input positions from R
+  float res[CPT];
+  float ldiff = 0.0f;
+  for (int sweep = 0; sweep < a.n_sweeps; ++sweep) {
+    pass(pr);
+    ldiff = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      res[k] = NI;
+      if (okp[k]) {
+        const float denom = rowsum - ps[k];
+        const float pibar_w = denom > 0.0f ? log2f(denom) + M + kmt[k] : NI;
+        const float pi_w = pr[k];
+        const float t0 = kDL[k] + pi_w;
+        const float t1 = pi_w + kEb[k];
+        const float t2 = pibar_w + kE[k];
+        const float t3 = kS1[k] + ch1[k];
+        const float t4 = kS2[k] + ch2[k];
+        const float t5 = klf[k];
+        float m = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, t5));
+        const float d = kd[k];
+        if (a.dts) m = fmaxf(m, d);
+        const float ms = m == NI ? 0.0f : m;
+        float sum = exp2f(t0 - ms) + exp2f(t1 - ms) + exp2f(t2 - ms) + exp2f(t3 - ms) + exp2f(t4 - ms) +
+                    exp2f(t5 - ms);
+        if (a.dts) sum += exp2f(d - ms);
+        res[k] = log2f(sum) + m;
+        if (res[k] != NI && pi_w != NI) ldiff = fmaxf(ldiff, fabsf(res[k] - pi_w));
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) pr[k] = res[k];
+  }
+  // outputs by column (coalesced): Pi_out, then the final Pibar and row max
+  kb::lds_store_own<CPT>(R, res);  // R's readers (the last children) finished before barrier 3
+  __syncthreads();
+  float* out = a.Pi_out + (size_t)grow * S;
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int sc = tid + j * NT;
+    if (sc < S) out[sc] = R[t.ppos[sc]];
+  }
+  if (a.resid) {
+    const float md = kb::block_max1<NT>(ldiff, wM);
+    if (tid == 0) a.resid[grow] = md;
+  }
+  if (!a.store_final) return;
+  __syncthreads();  // the outputs' reads of R are done
+  pass(res);
+  float pb[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const float denom = rowsum - ps[k];
+    pb[k] = (okp[k] && denom > 0.0f) ? log2f(denom) + M + kmt[k] : NI;
+  }
+  kb::lds_store_own<CPT>(X, pb);  // X's readers finished before barrier 3
+  __syncthreads();
+  float* pbo = a.Pibar + (size_t)grow * S;
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int sc = tid + j * NT;
+    if (sc < S) pbo[sc] = X[t.ppos[sc]];
+  }
+  if (tid == 0) a.rowmax[grow] = M;
 }
 
 template <typename T>
@@ -1274,6 +1469,17 @@ int kb_tree_create(int32_t S, const int64_t* parent, const int64_t* child1, cons
     std::vector<int> fill(lvl_ptr.begin(), lvl_ptr.end() - 1);
     for (int s = 0; s < S; ++s) lvl_node[fill[depth[s]]++] = s;
   }
+  // preorder-position tables of the contiguous-ownership sweeps
+  std::vector<int> pc1(S), pc2(S), pnex(S), ppost;
+  ppost.reserve(S);
+  for (int i = 0; i < S; ++i) {
+    const int n = pcol[i];
+    pc1[i] = c1[n] >= 0 ? ppos[c1[n]] : -1;
+    pc2[i] = c2[n] >= 0 ? ppos[c2[n]] : -1;
+    pnex[i] = tin[n] - i;
+  }
+  for (int e : ev)
+    if (e & 1) ppost.push_back(ppos[e >> 1]);
   kb_tree* t = new kb_tree();
   t->S = S;
   t->n_levels = max_d + 1;
@@ -1288,6 +1494,10 @@ int kb_tree_create(int32_t S, const int64_t* parent, const int64_t* child1, cons
   rc |= put(&t->pend, pend);
   rc |= put(&t->lvl_ptr, lvl_ptr);
   rc |= put(&t->lvl_node, lvl_node);
+  rc |= put(&t->pc1, pc1);
+  rc |= put(&t->pc2, pc2);
+  rc |= put(&t->pnex, pnex);
+  rc |= put(&t->ppost, ppost);
   if (rc) {
     kb_tree_destroy(t);
     return KB_ERR_HIP;
@@ -1298,7 +1508,8 @@ int kb_tree_create(int32_t S, const int64_t* parent, const int64_t* child1, cons
 
 void kb_tree_destroy(kb_tree* t) {
   if (!t) return;
-  for (int* p : {t->par, t->c1, t->c2, t->ev, t->tin, t->pcol, t->ppos, t->pend, t->lvl_ptr, t->lvl_node})
+  for (int* p : {t->par, t->c1, t->c2, t->ev, t->tin, t->pcol, t->ppos, t->pend, t->lvl_ptr, t->lvl_node, t->pc1,
+                 t->pc2, t->pnex, t->ppost})
     if (p) (void)hipFree(p);
   delete t;
 }
@@ -1364,6 +1575,31 @@ int estep_vjp_launch(const kb_tree* tr, const kb_estep_vjp_io* io, double* work,
 
 }  // namespace
 
+namespace {
+// Chains of float sweeps run the preorder-ownership kernel (three LDS rows of
+// NT * CPT + 64 floats; its set-up -- tables, the row permuted through LDS --
+// pays off over several sweeps); single sweeps and float64 rows the
+// Euler-tour one.  The two sum the path sums in different orders, so a chain
+// agrees with the same sweeps launched one at a time to rounding.
+template <typename T, int CPT>
+int launch_wave_step(const kbo::OpsTree& t, const kbo::WsArgs<T>& a, int W, size_t lds, hipStream_t st) {
+  if constexpr (std::is_same_v<T, float>) {
+    if (a.n_sweeps > 1) {
+      const size_t lds_pre = (size_t)3 * (kbo::NT * CPT + 64) * sizeof(float);
+      auto k = kbo::wave_step_pre_kernel<CPT>;
+      if (int rc = set_lds(k, lds_pre)) return rc;
+      hipLaunchKernelGGL(k, dim3(W), dim3(kbo::NT), lds_pre, st, t, a);
+      return 0;
+    }
+  }
+  auto k = kbo::wave_step_kernel<T, CPT>;
+  if (int rc = set_lds(k, lds)) return rc;
+  hipLaunchKernelGGL(k, dim3(W), dim3(kbo::NT), lds, st, t, a);
+  return 0;
+}
+
+}  // namespace
+
 extern "C" {
 
 int kb_estep_vjp(const kb_tree* tr, const kb_estep_vjp_io* io, void* stream) {
@@ -1402,9 +1638,7 @@ int kb_wave_step(const kb_tree* tr, const kb_wave_step_io* io, void* stream) {
                      io->pi_residual, (const T*)io->dts, (const T*)io->max_coupling, (const T*)io->DL,
                      (const T*)io->Ebar, (const T*)io->E, (const T*)io->SL1, (const T*)io->SL2,
                      (const T*)io->col_log_probs, io->item_idx, io->leaf_state, (const T*)io->leaf_logp};
-    auto k = kbo::wave_step_kernel<T, CPT>;
-    if (int rc = set_lds(k, lds)) return rc;
-    hipLaunchKernelGGL(k, dim3(io->W), dim3(kbo::NT), lds, st_of(stream), t, a);
+    if (int rc = launch_wave_step<T, CPT>(t, a, io->W, lds, st_of(stream))) return rc;
   });
   KBO_HIP(hipGetLastError());
   return 0;

@@ -30,6 +30,10 @@ struct OpsTree {
   const int* pend;      // [S] column -> exclusive end of its subtree (preorder)
   const int* lvl_ptr;   // [n_levels + 1] depth levels, root level first
   const int* lvl_node;  // [S]
+  const int* pc1;       // [S] preorder position -> position of child1, -1 if none
+  const int* pc2;       // [S] preorder position -> position of child2, -1 if none
+  const int* pnex;      // [S] preorder position i -> tin(column) - i, the postorder slots before entering i
+  const int* ppost;     // [S] postorder slot -> preorder position (the order of the Euler exit events)
 };
 
 // ---- scalar helpers -------------------------------------------------------
@@ -245,8 +249,10 @@ struct kb_tree {
   int S = 0, n_levels = 0;
   int *par = nullptr, *c1 = nullptr, *c2 = nullptr, *ev = nullptr, *tin = nullptr;
   int *pcol = nullptr, *ppos = nullptr, *pend = nullptr, *lvl_ptr = nullptr, *lvl_node = nullptr;
+  int *pc1 = nullptr, *pc2 = nullptr, *pnex = nullptr, *ppost = nullptr;
   kbo::OpsTree dev() const {
-    return kbo::OpsTree{S, n_levels, par, c1, c2, ev, tin, pcol, ppos, pend, lvl_ptr, lvl_node};
+    return kbo::OpsTree{S, n_levels, par, c1, c2, ev, tin, pcol, ppos, pend, lvl_ptr, lvl_node,
+                        pc1, pc2, pnex, ppost};
   }
 };
 

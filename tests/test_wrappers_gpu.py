@@ -236,8 +236,10 @@ def test_glue_config3_forward_matches_fused():
 
 
 @pytest.mark.parametrize("name", ["1", "3"])
-def test_fused_sweep_chains_are_bitwise_equal(name, monkeypatch):
-    """KBENCH_FUSE_SWEEPS: a wave's chained sweeps run as one launch with the same results, bit for bit."""
+def test_fused_sweep_chains_match_one_launch_per_sweep(name, monkeypatch):
+    """KBENCH_FUSE_SWEEPS: a wave's chained sweeps run as one launch (the preorder-ownership kernel for float
+    rows) and agree with one launch per sweep to float32 rounding: same -inf pattern, loss 1e-6, rows
+    2e-4 absolute or 1e-5 relative."""
     import dropin
     from kbench.core.kernels import wave_step
 
@@ -249,13 +251,20 @@ def test_fused_sweep_chains_are_bitwise_equal(name, monkeypatch):
     lb, sb = dropin.run_forward(static, theta, cw)
     torch.cuda.synchronize()
     assert wave_step._chain is None  # every chain ended with its final call
-    assert torch.equal(la, lb)
+    rel = abs(float(la) - float(lb)) / abs(float(la))
+    print(f"  loss one-per-sweep={float(la):.9g} chained={float(lb):.9g} rel={rel:.3e}")
+    assert rel <= 1e-6
     for k in ("pi_wave", "pibar_wave", "pibar_row_max"):
-        assert torch.equal(sa[k], sb[k]), k
+        ok, ma, mr = kbtest.compare_inf_safe(sb[k].cpu().numpy(), sa[k].cpu().numpy())
+        print(f"  {k}: pattern={ok} max_abs={ma:.3e} max_rel={mr:.3e}")
+        assert ok and (ma <= 2e-4 or mr <= 1e-5), k
 
 
 def test_held_sweeps_run_before_other_work(monkeypatch):
-    """A chain broken before its final call (an explicit flush, another wrapper) still yields every sweep."""
+    """A chain broken before its final call (an explicit flush, another wrapper) still yields every sweep.
+
+    The rows agree with one launch per sweep to float32 rounding.
+    """
     from dropin.solve import plan_of
     from kbench.core.kernels import _hip as H
     from kbench.core.kernels import wave_step
@@ -293,4 +302,7 @@ def test_held_sweeps_run_before_other_work(monkeypatch):
         torch.cuda.synchronize()
         assert wave_step._chain is None
         rows = slice(w.ws, w.ws + w.W)
-        assert torch.equal(got[1][rows], ref[1][rows]), how  # the last sweep's output rows
+        # the last sweep's output rows; a held chain of several sweeps runs the
+        # preorder-ownership kernel, whose path sums add in another order
+        ok, ma, mr = kbtest.compare_inf_safe(got[1][rows].cpu().numpy(), ref[1][rows].cpu().numpy())
+        assert ok and (ma <= 2e-4 or mr <= 1e-5), (how, ma, mr)

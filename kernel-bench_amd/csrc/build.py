@@ -23,7 +23,7 @@ INCLUDE = HERE.parent.parent / "include"
 OUT = PKG / "libkbench_hip.so"
 BUILD = HERE / "_build"
 
-SOURCES = ["kb_estep.hip", "kb_fwd.hip", "kb_bwd.hip", "kb_epi.hip", "kb_ops.hip", "kb_tangent.hip", "kb_so.hip", "kb_api.hip"]
+SOURCES = ["kb_estep.hip", "kb_fwd.hip", "kb_bwd.hip", "kb_bwd_large.hip", "kb_epi.hip", "kb_ops.hip", "kb_tangent.hip", "kb_so.hip", "kb_api.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

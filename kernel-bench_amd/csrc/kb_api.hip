@@ -134,7 +134,8 @@ struct kb_plan {
   int* h_status = nullptr;  // pinned host copy of b_status (kb_backward_stats)
   float* b_DL = nullptr; float* b_SL1 = nullptr; float* b_SL2 = nullptr; float* b_pS = nullptr; float* b_pD = nullptr;
   float* b_Ebar = nullptr; float* b_E = nullptr; float* b_mt = nullptr; float* b_col = nullptr; double* b_acc_pre = nullptr;
-  int b_nb_max = 0, b_n_partials = 0, b_variant = 0;
+  int b_nb_max = 0, b_n_partials = 0, b_variant = 0, b_large = 1;
+  size_t b_slot = 0;  // floats per workgroup slot of b_contrib
   std::vector<int> b_poff;
   // optional per-launch timing of the wave kernels (HIP events on the launch stream)
   int prof = 0;
@@ -780,6 +781,11 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
   return 0;
 }
 
+// floats per workgroup slot of the backward row kernels
+static size_t bwd_slot_floats(int S, int large) {
+  return kb::kb_use_large(S, large) ? (size_t)kb::KB_LARGE_SLOT_ROWS * kb::kb_large_ld(S) : (size_t)8 * S;
+}
+
 static int ensure_backward_work(kb_plan* p, int use_col) {
   const int S = p->S, C = p->C;
   // resident workgroups of the backward row kernel: its per-level grid
@@ -791,9 +797,15 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   // smaller levels; KB_BWD_VARIANT=0 / 2 forces one shape everywhere
   const char* vv = getenv("KB_BWD_VARIANT");
   const int variant = (vv && vv[0] == '2') ? 2 : (vv && vv[0] == '0') ? 0 : 1;
-  const int nb_max = std::max(1, n_cu * kb::bwd_blocks_per_cu(S, use_col, variant));
+  // rows of 2049..8192 states: the low-register kernel (KB_BWD_LARGE=0: the
+  // general row kernel)
+  const char* lv = getenv("KB_BWD_LARGE");
+  const int large = (lv && lv[0] == '0') ? 0 : 1;
+  const int nb_max = std::max(1, n_cu * kb::bwd_blocks_per_cu(S, use_col, variant, large));
   p->b_variant = variant;
-  if (p->b_contrib && p->b_nb_max == nb_max) return 0;
+  p->b_large = large;
+  if (p->b_contrib && p->b_nb_max == nb_max && p->b_slot == bwd_slot_floats(S, large)) return 0;
+  p->b_slot = bwd_slot_floats(S, large);
   p->b_nb_max = nb_max;
   p->b_n_partials = nb_max;  // one persistent bucket slot per workgroup of the per-level grids
   if (p->b_contrib) {
@@ -804,7 +816,7 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
     p->b_contrib = nullptr;
     p->b_partial = nullptr;
     int rc = 0;
-    rc |= alloc(&p->b_contrib, (size_t)std::max(1, p->b_n_partials) * 8 * S);
+    rc |= alloc(&p->b_contrib, (size_t)std::max(1, p->b_n_partials) * p->b_slot);
     rc |= alloc(&p->b_partial, (size_t)kb::reduce_chunks(std::max(1, p->b_n_partials)) * 8 * S);
     p->owned.push_back(p->b_contrib);
     p->owned.push_back(p->b_partial);
@@ -820,7 +832,7 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   rc |= alloc(&p->b_m_mask, (size_t)std::max(1, C > 0 ? p->level_ptr[1] : 1));
   rc |= alloc(&p->b_cls_active, (size_t)std::max(1, p->n_cls0));
   rc |= alloc(&p->b_ck_any, (size_t)std::max(1, p->n_chunks0));
-  rc |= alloc(&p->b_contrib, (size_t)std::max(1, p->b_n_partials) * 8 * S);
+  rc |= alloc(&p->b_contrib, (size_t)std::max(1, p->b_n_partials) * p->b_slot);
   rc |= alloc(&p->b_partial, (size_t)kb::reduce_chunks(std::max(1, p->b_n_partials)) * 8 * S);
   rc |= alloc(&p->b_acc, (size_t)8 * S);
   rc |= alloc(&p->b_work, (size_t)kb::epilogue_work_vectors() * S);
@@ -915,6 +927,7 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   B.sched_rows = p->d_sched_rows;
   B.row_kind = p->d_row_kind;
   B.variant = p->b_variant;
+  B.large = p->b_large;
   B.rhs0 = p->b_rhs0;
   B.n_chunks0 = p->n_chunks0;
   B.ck_ptr = p->d_ck_ptr;
@@ -933,7 +946,7 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   B.rep_of = p->d_rep_of;
   B.cls_ptr = p->d_cls_ptr;
   B.cls_rows = p->d_cls_rows;
-  kb::launch_fill_zero(p->b_contrib, (size_t)p->b_n_partials * 8 * S, st);
+  kb::launch_fill_zero(p->b_contrib, (size_t)p->b_n_partials * p->b_slot, st);
   for (int d = p->n_levels - 1; d >= 0; --d) {
     if (p->prof) KB_HIP(hipEventRecord(p->ev_bwd[2 * d], st));
     // level 0 (rows without splits) runs by class: one adjoint solve per class of identical rows
@@ -945,7 +958,8 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
     if (p->prof) KB_HIP(hipEventRecord(p->ev_bwd[2 * d + 1], st));
   }
   KB_HIP(hipGetLastError());
-  kb::launch_bwd_reduce(p->b_contrib, p->b_n_partials, S, p->b_partial, p->b_acc_pre, st);
+  kb::launch_bwd_reduce(p->b_contrib, p->b_n_partials, S, p->b_slot,
+                        kb::kb_use_large(S, p->b_large) ? kb::kb_large_ld(S) : S, p->b_partial, p->b_acc_pre, st);
   kb::launch_bwd_unpermute(p->b_acc_pre, p->d_pre, S, p->b_acc, st);
   KB_HIP(hipGetLastError());
   if (io->acc_out)

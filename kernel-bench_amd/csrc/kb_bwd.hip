@@ -1009,6 +1009,7 @@ void launch_fill_zero(float* p, size_t n, hipStream_t st) {
 
 void launch_bwd_wave(const BwdParams& P, int first, int W, int nb, int poff, hipStream_t st) {
   if (W <= 0 || nb <= 0) return;
+  if (launch_bwd_large(P, first, W, nb, st)) return;
   const int S = P.S;
   if (P.variant == 2) {
     KB_BWD_CASE(1024, 2)
@@ -1032,7 +1033,8 @@ void launch_bwd_wave(const BwdParams& P, int first, int W, int nb, int poff, hip
     return n > 0 ? n : 1;                                                                              \
   }
 
-int bwd_blocks_per_cu(int S, int use_col, int variant) {
+int bwd_blocks_per_cu(int S, int use_col, int variant, int large) {
+  if (kb_use_large(S, large)) return bwd_large_blocks_per_cu(S, use_col);
   if (variant == 2) {
     KB_BWD_OCC(1024, 2)
   }
@@ -1075,13 +1077,15 @@ void launch_bwd_consts(const BwdConstArgs& A, hipStream_t st) {
 // The result is in preorder-position order: out[j*S + pre(s)].
 constexpr int RED_CHUNK = 16;
 
-__global__ void bwd_reduce_stage1(const float* contrib, int C, int S, double* partial) {
+__global__ void bwd_reduce_stage1(const float* contrib, int C, int S, size_t slot_stride, int ld, double* partial) {
   const int j = blockIdx.x * blockDim.x + threadIdx.x;  // index in [0, 8S)
   const int chunk = blockIdx.y;
   if (j >= 8 * S) return;
+  const int a = j / S;
+  const size_t off = (size_t)a * ld + (j - a * S);
   const int r0 = chunk * RED_CHUNK, r1 = min(C, r0 + RED_CHUNK);
   double acc = 0.0;
-  for (int r = r0; r < r1; ++r) acc += (double)contrib[(size_t)r * 8 * S + j];
+  for (int r = r0; r < r1; ++r) acc += (double)contrib[(size_t)r * slot_stride + off];
   partial[(size_t)chunk * 8 * S + j] = acc;
 }
 
@@ -1100,10 +1104,11 @@ __global__ void bwd_unpermute(const double* in, const int* pre, int S, double* o
   out[j] = in[(size_t)a * S + pre[s]];
 }
 
-void launch_bwd_reduce(const float* contrib, int C, int S, double* partial, double* out, hipStream_t st) {
+void launch_bwd_reduce(const float* contrib, int C, int S, size_t slot_stride, int ld, double* partial, double* out,
+                       hipStream_t st) {
   const int n_chunks = (C + RED_CHUNK - 1) / RED_CHUNK;
   dim3 g1((8 * S + 255) / 256, n_chunks);
-  hipLaunchKernelGGL(bwd_reduce_stage1, g1, dim3(256), 0, st, contrib, C, S, partial);
+  hipLaunchKernelGGL(bwd_reduce_stage1, g1, dim3(256), 0, st, contrib, C, S, slot_stride, ld, partial);
   hipLaunchKernelGGL(bwd_reduce_stage2, dim3((8 * S + 255) / 256), dim3(256), 0, st, partial, n_chunks, S, out);
 }
 

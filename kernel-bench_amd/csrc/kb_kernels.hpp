@@ -131,6 +131,7 @@ struct BwdParams {
   const int* row_kind;
   int class_mode;             // 1: entries are classes of identical rows (cls_ptr / cls_rows)
   int variant;                // launch shape: 0 default, 2 narrow (1024 threads x 2 states)
+  int large;                  // 1: rows of 2049..8192 states run bwd_row_large_kernel
   float* rhs0;                // [rows of level 0, S] preorder adjoint rows, in cls_rows order
   float* rhsc;                // [classes of level 0, S] summed adjoint of each class
   const int* m_side_ptr;      // [members + 1] staging sides of each level-0 member (cls_rows order)
@@ -150,6 +151,12 @@ struct BwdParams {
 };
 
 constexpr int KB_CHUNK0 = 8;
+// Workgroup slot of bwd_row_large_kernel: KB_LARGE_SLOT_ROWS rows of
+// kb_large_ld(S) floats (8 bucket rows, then the row's split term, Pi* and
+// Pibar*); other row kernels use 8 rows of S.
+constexpr int KB_LARGE_SLOT_ROWS = 11;
+inline bool kb_use_large(int S, int large) { return large && S > 2048 && S <= 8192; }
+inline int kb_large_ld(int S) { return S <= 4096 ? 4096 : 8192; }
 
 struct EpiParams {
   TreeDev tr;
@@ -181,11 +188,18 @@ void launch_bwd_consts(const BwdConstArgs& A, hipStream_t st);
 // Rows sched_rows[first .. first + n) on nb workgroups (round-robin); partial
 // bucket rows poff .. poff + nb.
 void launch_bwd_wave(const BwdParams& P, int first, int n, int nb, int poff, hipStream_t st);
-int bwd_blocks_per_cu(int S, int use_col, int variant);
+int bwd_blocks_per_cu(int S, int use_col, int variant, int large);
+// Rows of 2049..8192 states on the low-register kernel (kb_bwd_large.hip);
+// false if P.large is off or S is outside that range.
+bool launch_bwd_large(const BwdParams& P, int first, int n, int nb, hipStream_t st);
+int bwd_large_blocks_per_cu(int S, int use_col);
 // Level-0 adjoint rows, masks and class sums.
 void launch_bwd_level0_prep(const BwdParams& P, int n_members, int n_cls, hipStream_t st);
 void launch_fill_zero(float* p, size_t n, hipStream_t st);
-void launch_bwd_reduce(const float* contrib, int C, int S, double* partial, double* out, hipStream_t st);
+// Sums the bucket rows of C workgroup slots (slot_stride floats apart, bucket
+// rows ld floats apart) in slot order.
+void launch_bwd_reduce(const float* contrib, int C, int S, size_t slot_stride, int ld, double* partial, double* out,
+                       hipStream_t st);
 void launch_bwd_unpermute(const double* in, const int* pre, int S, double* out, hipStream_t st);
 int reduce_chunks(int C);
 void launch_epilogue(const EpiParams& P, hipStream_t st);

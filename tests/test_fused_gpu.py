@@ -207,6 +207,37 @@ def test_fused_large_trees_match_oracle(leaves, families, statewise, weighted, s
     assert rt <= 1e-4 and rc <= 1e-4
 
 
+@pytest.mark.parametrize("leaves,weighted", [(2048, False), (4096, True)])
+def test_large_tree_backward_kernels_agree(leaves, weighted, monkeypatch):
+    """S = 4095 and 8191: the low-register backward row kernel against the general one
+    (KB_BWD_LARGE=0) on the same forward; each run twice is bitwise reproducible."""
+    from kbench.fused import FusedSolver, problem_to_captured
+    from kbench.runtime import make_static
+
+    print(f"[fused-large-ab] leaves={leaves} weighted={weighted}", flush=True)
+    p = _big_tree_problem(leaves, 3, True)
+    cap = problem_to_captured(p)
+    static = make_static(cap, "cuda")
+    solver = FusedSolver(static, static.solver_options)
+    theta = cap["inputs"]["theta"].cuda()
+    n = int(cap["inputs"]["col_weights"].numel())
+    cw32 = (np.random.default_rng(7).normal(0.0, 0.5, size=n) if weighted else np.zeros(n)).astype(np.float32)
+    cw = torch.from_numpy(cw32).cuda()
+    _, saved = solver.run_forward(theta, cw)
+    runs = {}
+    for large in ("1", "0", "1"):
+        monkeypatch.setenv("KB_BWD_LARGE", large)
+        gt, gc = solver.run_backward(theta, cw, saved)
+        torch.cuda.synchronize()
+        if large in runs:
+            assert torch.equal(gt, runs[large][0]) and torch.equal(gc, runs[large][1])
+        runs[large] = (gt.clone(), gc.clone())
+    rt = kbtest.norm_rel(runs["1"][0].cpu().numpy(), runs["0"][0].cpu().numpy())
+    rc = kbtest.norm_rel(runs["1"][1].cpu().numpy(), runs["0"][1].cpu().numpy())
+    print(f"  low-register vs general kernel: grad_theta rel={rt:.3e} grad_col rel={rc:.3e}")
+    assert rt <= 1e-5 and rc <= 1e-5
+
+
 @pytest.mark.parametrize("statewise", [False, True])
 def test_fused_single_leaf_families_match_oracle(statewise):
     """Families of one gene leaf: their root row is a leaf row, so level 0 holds root members (the root

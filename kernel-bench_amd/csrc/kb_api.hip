@@ -118,6 +118,7 @@ struct kb_plan {
   int* d_pre = nullptr; int* d_pcol = nullptr; int* d_c1pos = nullptr; int* d_c2pos = nullptr; int* d_ppos = nullptr;
   int* d_pflag = nullptr; int* d_endpos = nullptr; int* d_tin = nullptr; int* d_euler = nullptr;
   int* d_post = nullptr;
+  int* d_om_tab = nullptr;  // owner-major position tables of the large backward kernel (2048 < S <= 8192)
   int* d_euler_col = nullptr; int* d_tin_col = nullptr;  // the Euler tour in column terms
   kb::TreeScanDev tscan() const { return kb::TreeScanDev{S, d_pre, d_endpos, d_euler_col, d_tin_col}; }
   double* E64 = nullptr; int* n_e_iter = nullptr; double* loss_terms = nullptr; double* loss64 = nullptr;
@@ -130,6 +131,7 @@ struct kb_plan {
   unsigned char* b_m_mask = nullptr;
   unsigned char* b_cls_active = nullptr;
   float* b_contrib = nullptr; double* b_partial = nullptr; double* b_acc = nullptr; double* b_work = nullptr;
+  float* b_om_const = nullptr;  // owner-major constants of the large backward kernel
   int* b_status = nullptr;
   int* h_status = nullptr;  // pinned host copy of b_status (kb_backward_stats)
   float* b_DL = nullptr; float* b_SL1 = nullptr; float* b_SL2 = nullptr; float* b_pS = nullptr; float* b_pD = nullptr;
@@ -608,6 +610,22 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
     for (int e : euler)
       if (e & 1) post.push_back(e >> 1);
     rc |= upload(&p->d_post, post);
+    if (S > 2048 && S <= 8192) {
+      // owner-major position tables of bwd_row_large_kernel (kb::OmTab)
+      const int ld = kb::kb_large_ld(S), cpt = ld / 1024, zero = ld;
+      std::vector<int> om((size_t)kb::KB_OM_TABS * ld);
+      for (int i = 0; i < ld; ++i) {
+        const size_t o = (size_t)(i % cpt) * 1024 + i / cpt;
+        const bool ok = i < S;
+        om[kb::OMT_C1 * (size_t)ld + o] = ok ? c1pos[i] : -1;
+        om[kb::OMT_C2 * (size_t)ld + o] = ok ? c2pos[i] : -1;
+        const int pa = ok && ppos[i] >= 0 ? ppos[i] : zero;
+        const int e1 = ok ? endpos[i] - 1 : zero;
+        om[kb::OMT_PK * (size_t)ld + o] = pa | (e1 << 16) | ((ok && ppos[i] >= 0 && pflag[i]) ? (1 << 30) : 0);
+        om[kb::OMT_PN * (size_t)ld + o] = ok ? (post[i] | ((tin[i] - i) << 16)) : zero;
+      }
+      rc |= upload(&p->d_om_tab, om);
+    }
   }
   {
     std::vector<int> ecol(euler.size()), tcol(S);
@@ -648,7 +666,7 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
                     (void*)p->d_dup_rows, (void*)p->d_cls_ptr, (void*)p->d_cls_rows, (void*)p->d_ck_ptr, (void*)p->d_cls_ck_ptr, (void*)p->d_rep_of, (void*)p->d_m_side_ptr, (void*)p->d_m_side, (void*)p->d_m_root,
                     (void*)p->d_dts,
                     (void*)p->d_c1pos, (void*)p->d_c2pos, (void*)p->d_ppos, (void*)p->d_pflag, (void*)p->d_endpos,
-                    (void*)p->d_tin, (void*)p->d_euler, (void*)p->d_post, (void*)p->d_euler_col, (void*)p->d_tin_col, (void*)p->c_Ebar, (void*)p->c_E, (void*)p->c_mt,
+                    (void*)p->d_tin, (void*)p->d_euler, (void*)p->d_post, (void*)p->d_om_tab, (void*)p->d_euler_col, (void*)p->d_tin_col, (void*)p->c_Ebar, (void*)p->c_E, (void*)p->c_mt,
                     (void*)p->c_col})
     p->owned.push_back(ptr);
   if (rc) {
@@ -847,6 +865,11 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   rc |= alloc(&p->b_mt, S);
   rc |= alloc(&p->b_col, S);
   rc |= alloc(&p->b_acc_pre, (size_t)8 * S);
+  if (S > 2048 && S <= 8192) {
+    rc |= alloc(&p->b_om_const, (size_t)kb::KB_OM_CONSTS * kb::kb_large_ld(S));
+    if (!rc) KB_HIP(hipMemset(p->b_om_const, 0, (size_t)kb::KB_OM_CONSTS * kb::kb_large_ld(S) * sizeof(float)));
+    p->owned.push_back(p->b_om_const);
+  }
   for (void* ptr : {(void*)p->b_Ebar, (void*)p->b_E, (void*)p->b_mt, (void*)p->b_col, (void*)p->b_acc_pre,
                     (void*)p->b_staging, (void*)p->b_split_on, (void*)p->b_mask, (void*)p->b_contrib,
                     (void*)p->b_rhs0, (void*)p->b_rhsc, (void*)p->b_cls_active, (void*)p->b_ck_any, (void*)p->b_m_mask,
@@ -889,6 +912,7 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   K.SL2 = p->b_SL2;
   K.pS_state = p->b_pS;
   K.pD_state = p->b_pD;
+  K.om = kb::kb_use_large(S, p->b_large) ? p->b_om_const : nullptr;
   kb::launch_bwd_consts(K, st);
 
   kb::BwdParams B{};
@@ -928,6 +952,8 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   B.row_kind = p->d_row_kind;
   B.variant = p->b_variant;
   B.large = p->b_large;
+  B.om_tab = p->d_om_tab;
+  B.om_const = p->b_om_const;
   B.rhs0 = p->b_rhs0;
   B.n_chunks0 = p->n_chunks0;
   B.ck_ptr = p->d_ck_ptr;

@@ -1057,15 +1057,29 @@ __global__ void bwd_consts_kernel(BwdConstArgs A) {
   const int i = A.pre[s];
   const float pS = A.log_pS[A.statewise ? s : 0];
   const float pD = A.log_pD[A.statewise ? s : 0];
-  A.DL[i] = (1.0f + pD) + A.E[s];
-  A.SL1[i] = pS + A.E_s2[s];
-  A.SL2[i] = pS + A.E_s1[s];
+  const float dl = (1.0f + pD) + A.E[s], sl1 = pS + A.E_s2[s], sl2 = pS + A.E_s1[s];
+  A.DL[i] = dl;
+  A.SL1[i] = sl1;
+  A.SL2[i] = sl2;
   A.pS_state[i] = pS;
   A.pD_state[i] = pD;
   A.Ebar_pre[i] = A.Ebar[s];
   A.E_pre[i] = A.E[s];
   A.mt_pre[i] = A.mt[s];
   A.col_pre[i] = A.col[s];
+  if (A.om) {
+    const int cpt = A.S <= 4096 ? 4 : 8, ld = 1024 * cpt;
+    float* o = A.om + (i % cpt) * 1024 + i / cpt;
+    o[OMC_DL * ld] = dl;
+    o[OMC_EBAR * ld] = A.Ebar[s];
+    o[OMC_E * ld] = A.E[s];
+    o[OMC_SL1 * ld] = sl1;
+    o[OMC_SL2 * ld] = sl2;
+    o[OMC_PD * ld] = pD;
+    o[OMC_PS * ld] = pS;
+    o[OMC_MT * ld] = A.mt[s];
+    o[OMC_COL * ld] = A.col[s];
+  }
 }
 
 void launch_bwd_consts(const BwdConstArgs& A, hipStream_t st) {

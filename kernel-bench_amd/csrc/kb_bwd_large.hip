@@ -39,24 +39,24 @@ __device__ __forceinline__ void stg(T* b, int i, T x) {
   *reinterpret_cast<T*>(reinterpret_cast<char*>(b) + (unsigned)i * (unsigned)sizeof(T)) = x;
 }
 
-// The same uniform pointer, opaque to the optimiser.  Each phase takes its
-// table and constant pointers through this, so per-lane addresses are formed
-// where they are used: otherwise they are computed once per row (or hoisted
-// out of the row loop) and held in register pairs across the Neumann series.
+// The same uniform pointer, opaque to the optimiser for each value of
+// `epoch`.  Each phase of a row passes its own epoch (the row and phase, or
+// split and step), so the per-lane addresses of its tables are formed in that
+// phase: with plain pointers they are computed once per row, or hoisted out of
+// the row loop, and held in register pairs across the Neumann series.  The
+// asm has no side effects, so loads around it still issue together.
 template <typename T>
-__device__ __forceinline__ T* fresh(T* p) {
+__device__ __forceinline__ T* fresh(T* p, int epoch) {
   unsigned long long x = reinterpret_cast<unsigned long long>(p);
-  asm volatile("" : "+s"(x));
+  asm("; %1" : "+s"(x) : "s"(epoch));
   // a global-memory pointer again, so the accesses stay global (not flat)
   return (T*)reinterpret_cast<__attribute__((address_space(1))) T*>(x);
 }
 
-struct CoefPtrs {
-  const float *DL, *Ebar, *E, *SL1, *SL2, *pS;
+// the per-position constants the coefficients read
+struct CoefK {
+  float DL, Ebar, E, SL1, SL2, pS;
 };
-__device__ __forceinline__ CoefPtrs coef_ptrs(const BwdParams& P) {
-  return CoefPtrs{fresh(P.DL), fresh(P.Ebar), fresh(P.E), fresh(P.SL1), fresh(P.SL2), fresh(P.pS)};
-}
 
 // q_0..q_5 of own position i: the self-loop terms' shares of the row's
 // log-sum (wave_backward.py:264-416), with the split mixing weight folded into
@@ -65,14 +65,14 @@ struct Coef6 {
   float q[6];
 };
 
-__device__ __forceinline__ Coef6 coef_at(const CoefPtrs& K, int i, float piv, float pbv, float dts, float pc1,
-                                         float pc2, bool leaf_row, bool is_leaf_pos) {
-  const float t0 = ldg(K.DL, i) + piv;
-  const float t1 = piv + ldg(K.Ebar, i);
-  const float t2 = pbv + ldg(K.E, i);
-  const float t3 = ldg(K.SL1, i) + pc1;
-  const float t4 = ldg(K.SL2, i) + pc2;
-  const float t5 = is_leaf_pos ? ldg(K.pS, i) : KB_NEG_INF;
+__device__ __forceinline__ Coef6 coef_at(const CoefK& K, float piv, float pbv, float dts, float pc1, float pc2,
+                                         bool leaf_row, bool is_leaf_pos) {
+  const float t0 = K.DL + piv;
+  const float t1 = piv + K.Ebar;
+  const float t2 = pbv + K.E;
+  const float t3 = K.SL1 + pc1;
+  const float t4 = K.SL2 + pc2;
+  const float t5 = is_leaf_pos ? K.pS : KB_NEG_INF;
   const float m = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, t5));
   const float msf = fsafe(m);
   Coef6 c;
@@ -110,14 +110,15 @@ __device__ __forceinline__ void vst(float* p, const float (&x)[N]) {
   for (int k = 0; k < N; k += 4) *reinterpret_cast<float4*>(p + k) = make_float4(x[k], x[k + 1], x[k + 2], x[k + 3]);
 }
 
-// p[0..3] += x[0..3]
-__device__ __forceinline__ void vadd4(float* p, const float (&x)[4]) {
-  float4 q = *reinterpret_cast<const float4*>(p);
-  q.x += x[0];
-  q.y += x[1];
-  q.z += x[2];
-  q.w += x[3];
-  *reinterpret_cast<float4*>(p) = q;
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float f4(const float4& v, int j) { return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w; }
+// *p = b + x (four floats)
+__device__ __forceinline__ void st4_add(float* p, float4 b, const float (&x)[4]) {
+  b.x += x[0];
+  b.y += x[1];
+  b.z += x[2];
+  b.w += x[3];
+  *reinterpret_cast<float4*>(p) = b;
 }
 
 template <int CPT, bool WEIGHTED>
@@ -152,8 +153,9 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
   // positions): the eight bucket rows, then the current row's split term, Pi*
   // and Pibar*.  srow(j) is this thread's first own position of row j.
   float* const slot = P.contrib + (size_t)blockIdx.x * KB_LARGE_SLOT_ROWS * MAXS;
+  int ep = 0;  // epoch of the current phase (see fresh)
   auto srow = [&](int j) {
-    return reinterpret_cast<float*>(reinterpret_cast<char*>(fresh(slot + (size_t)j * MAXS)) +
+    return reinterpret_cast<float*>(reinterpret_cast<char*>(fresh(slot + (size_t)j * MAXS, ep)) +
                                     (unsigned)(tid * CPT) * 4u);
   };
   enum { SL_DTS = 8, SL_PI = 9, SL_PIBAR = 10 };
@@ -162,18 +164,31 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
   // held across the row loop)
   auto pos = [&](int k) {
     int b = tid * CPT;
-    if constexpr (CPT > 4) asm volatile("" : "+v"(b));
+    if constexpr (CPT > 4) asm("; %1" : "+v"(b) : "s"(ep));
     return b + k;
   };
   // a global row in column order -> LDS at preorder positions (coalesced reads)
   auto stage = [&](float* dst, const float* src) {
+    int sp[CPT];
+    float x[CPT];
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
       const int s = tid + j * NT;
-      if (s < S) dst[ldg(fresh(T.pre), s)] = ldg(fresh(src), s);
+      sp[j] = s < S ? ldg(fresh(T.pre, ep), s) : -1;
+      x[j] = s < S ? ldg(fresh(src, ep), s) : 0.0f;
     }
+#pragma unroll
+    for (int j = 0; j < CPT; ++j)
+      if (sp[j] >= 0) dst[sp[j]] = x[j];
   };
   auto field = [](int rec, int f) { return __builtin_amdgcn_readlane(rec, f); };
+  // row j of the owner-major tables / constants at own position k (one
+  // contiguous read per wavefront)
+  auto omi = [&](int j, int k) { return ldg(fresh(P.om_tab + (size_t)j * MAXS + k * NT, ep), tid); };
+  auto omf = [&](int j, int k) { return ldg(fresh(P.om_const + (size_t)j * MAXS + k * NT, ep), tid); };
+  auto coef_k = [&](int k) {
+    return CoefK{omf(OMC_DL, k), omf(OMC_EBAR, k), omf(OMC_E, k), omf(OMC_SL1, k), omf(OMC_SL2, k), omf(OMC_PS, k)};
+  };
   // subtree-sum offsets of a scan published by local_scan_publish: the block
   // total A, this wavefront's offset, and lane x < NW holding wavefront x's
   auto scan_offsets = [&](const float* wt, float& A, float& woff, float& wexcl) {
@@ -186,6 +201,7 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
 
   for (int rr = blockIdx.x; rr < n_rows; rr += gridDim.x) {
     __syncthreads();  // LDS of the previous row is no longer read
+    ep = rr * 16 + 1;
     const int cm = P.class_mode;
     const int rec = cm ? 0 : P.bslot[(size_t)KB_BREC * (first + rr) + (tid & (KB_BREC - 1))];
     const int f_row = field(rec, BR_ROW), f_leaf = field(rec, BR_LEAF), f_sb = field(rec, BR_SB);
@@ -198,27 +214,61 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
     const size_t rb = (size_t)row * S;
 
     // ---- 1. adjoint: the class's summed adjoint, the root seed (below), or the
-    // fixed-order gather of the live staging rows of the row's child sides
-    float rhs[CPT];
+    // fixed-order gather of the live staging rows of the row's child sides.
+    // The row's loads are issued together: Pi* / Pibar* (columns tid + j*NT,
+    // to LDS below), the first two child sides' flags and staging rows (added
+    // when live), and the stored split term.
+    float nPi[CPT], nPb[CPT];
+    int spre[CPT];
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) rhs[k] = 0.0f;
+    for (int j = 0; j < CPT; ++j) {
+      const int s = tid + j * NT;
+      spre[j] = s < S ? ldg(fresh(T.pre, ep), s) : -1;
+      nPi[j] = s < S ? ldg(fresh(P.pi + rb, ep), s) : 0.0f;
+      nPb[j] = s < S ? ldg(fresh(P.pibar + rb, ep), s) : 0.0f;
+    }
+    float rhs[CPT], dts[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) dts[k] = KB_NEG_INF;
+    if (!leaf_row && P.dts_in) {
+      const float* src = P.dts_in + (size_t)(cm ? P.rep_of[row] : f_rep) * S;
+#pragma unroll
+      for (int k = 0; k < CPT; ++k)
+        if (pos(k) < S) dts[k] = ldg(fresh(src, ep), pos(k));
+    }
     bool any_active = false;
     if (cm) {
       any_active = P.cls_active[rr] != 0;
       const float* src = P.rhsc + (size_t)rr * S;
 #pragma unroll
-      for (int k = 0; k < CPT; ++k)
-        if (pos(k) < S) rhs[k] = ldg(fresh(src), pos(k));
+      for (int k = 0; k < CPT; ++k) rhs[k] = pos(k) < S ? ldg(fresh(src, ep), pos(k)) : 0.0f;
     } else {
       const int s1 = f_s1 < 0 ? -1 : (f_s1 & ((1 << 30) - 1));
+      const bool on0 = f_s0 >= 0 && P.split_on[f_s0 >> 1];
+      const bool on1 = s1 >= 0 && P.split_on[s1 >> 1];
+      const float* st0 = P.staging + (size_t)(f_s0 >= 0 ? f_s0 : 0) * S;
+      const float* st1 = P.staging + (size_t)(s1 >= 0 ? s1 : 0) * S;
+      float a0[CPT], a1[CPT];
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        const bool ok = pos(k) < S;
+        a0[k] = ok && f_s0 >= 0 ? ldg(fresh(st0, ep), pos(k)) : 0.0f;
+        a1[k] = ok && s1 >= 0 ? ldg(fresh(st1, ep), pos(k)) : 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        rhs[k] = 0.0f;
+        if (on0) rhs[k] += a0[k];
+        if (on1) rhs[k] += a1[k];
+      }
       const int n2 = (f_s1 >= 0 && (f_s1 >> 30) != 0) ? P.child_ptr[row + 1] - P.child_ptr[row] - 2 : 0;
-      for (int j = -2; j < n2; ++j) {
-        const int side = j == -2 ? f_s0 : j == -1 ? s1 : P.child_in[P.child_ptr[row] + 2 + j];
-        if (side < 0 || !P.split_on[side >> 1]) continue;
+      for (int j = 0; j < n2; ++j) {
+        const int side = P.child_in[P.child_ptr[row] + 2 + j];
+        if (!P.split_on[side >> 1]) continue;
         const float* st = P.staging + (size_t)side * S;
 #pragma unroll
         for (int k = 0; k < CPT; ++k)
-          if (pos(k) < S) rhs[k] += ldg(fresh(st), pos(k));
+          if (pos(k) < S) rhs[k] += ldg(fresh(st, ep), pos(k));
       }
     }
     const bool mask_early = !cm && fam < 0;
@@ -229,8 +279,12 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
       const float wm = wave_reduce_max(am);
       if (lane == 0) wMk[wv] = wm;
     }
-    stage(R0, P.pi + rb);
-    stage(R1, P.pibar + rb);
+#pragma unroll
+    for (int j = 0; j < CPT; ++j)
+      if (spre[j] >= 0) {
+        R0[spre[j]] = nPi[j];
+        R1[spre[j]] = nPb[j];
+      }
     __syncthreads();
     float piv[CPT];
     lds_load_own<CPT>(R0, piv);
@@ -290,15 +344,9 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
     if (fam >= 0 || (!leaf_row && !P.dts_in)) __syncthreads();
 
     // ---- 3. split term at Pi* (split rows)
-    float dts[CPT];
-#pragma unroll
-    for (int k = 0; k < CPT; ++k) dts[k] = KB_NEG_INF;
-    if (!leaf_row && P.dts_in) {
-      const float* src = P.dts_in + (size_t)(cm ? P.rep_of[row] : f_rep) * S;
-#pragma unroll
-      for (int k = 0; k < CPT; ++k)
-        if (pos(k) < S) dts[k] = ldg(fresh(src), pos(k));
-    } else if (!leaf_row) {
+    // (a stored split term was loaded with the row)
+    ep = rr * 16 + 3;
+    if (!leaf_row && !P.dts_in) {
       float acc[CPT];
 #pragma unroll
       for (int k = 0; k < CPT; ++k) acc[k] = 0.0f;
@@ -314,14 +362,14 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
         for (int k = 0; k < CPT; ++k) {
           const int i = pos(k);
           if (i < S) {
-            const int c1 = ldg(fresh(T.c1pos), i), c2 = ldg(fresh(T.c2pos), i);
+            const int c1 = omi(OMT_C1, k), c2 = omi(OMT_C2, k);
             const float pl = R0[i], pr = R1[i];
             const float l1 = c1 >= 0 ? R0[c1] : KB_NEG_INF, r1 = c1 >= 0 ? R1[c1] : KB_NEG_INF;
             const float l2 = c2 >= 0 ? R0[c2] : KB_NEG_INF, r2 = c2 >= 0 ? R1[c2] : KB_NEG_INF;
-            const float t0 = lsp + ldg(fresh(P.pD), i) + pl + pr;
+            const float t0 = lsp + omf(OMC_PD, k) + pl + pr;
             const float t1 = lsp + pl + R3[i];
             const float t2 = lsp + pr + R2[i];
-            const float sp = ldg(fresh(P.pS), i);
+            const float sp = omf(OMC_PS, k);
             const float t3 = lsp + sp + l1 + r2;
             const float t4 = lsp + sp + r1 + l2;
             const float m5 = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), t4);
@@ -338,6 +386,7 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
     vst<CPT>(srow(SL_DTS), dts);
 
     // ---- 4. J^T coefficients at Pi* (wave_backward.py:264-416)
+    ep = rr * 16 + 4;
     // p' = 2^(col + Pi* - rowmax) and its root-path sums ps(i) = Pre(i) -
     // PostEx(tin(i) - i): inclusive preorder scan in registers, exclusive
     // postorder scan through LDS (R3), two barriers.  Pi* goes to R0 for the
@@ -347,7 +396,7 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int i = pos(k);
-      pp[k] = i < S ? exp2_hw((WEIGHTED ? ldg(fresh(P.col), i) : 0.0f) + piv[k] - rms) : 0.0f;
+      pp[k] = i < S ? exp2_hw((WEIGHTED ? omf(OMC_COL, k) : 0.0f) + piv[k] - rms) : 0.0f;
       ta += pp[k];
       pcoef[k] = ta;  // the running preorder sum, until the coefficients below
     }
@@ -364,7 +413,7 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
       for (int k = 0; k < CPT; ++k) {
         const int i = pos(k);
         sq[k] = tb;
-        tb += R2[i < S ? ldg(fresh(T.post), i) : ZERO];
+        tb += R2[i < S ? (omi(OMT_PN, k) & 0xffff) : ZERO];
       }
       const float ip = wave_scan_first<NW>(tp);
       const float rowsum = lane_value(ip, NW - 1);
@@ -380,7 +429,7 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
 #pragma unroll
       for (int k = 0; k < CPT; ++k) {
         const int i = pos(k);
-        const int n = i < S ? ldg(fresh(T.tin), i) - i : 0;
+        const int n = i < S ? (omi(OMT_PN, k) >> 16) : 0;
         const float ps = (pcoef[k] + offp) - (R3[n] + __shfl(eq, n / SEG, 64));
         const float denom = rowsum - ps;
         pcoef[k] = denom > 0.0f ? rcp_hw(denom) : 0.0f;  // 1 / (rowsum - ps) for now
@@ -391,15 +440,14 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
     // parent's owner into R1 (Pibar* was read above), then read back.  The
     // barrier also ends the reads of R2 / R3, which become scan buffers.
     float diag[CPT];
-    const CoefPtrs K = coef_ptrs(P);
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int i = pos(k);
       diag[k] = 0.0f;
       if (i < S) {
-        const int c1 = ldg(fresh(T.c1pos), i), c2 = ldg(fresh(T.c2pos), i);
-        const Coef6 c = coef_at(K, i, piv[k], pbv[k], dts[k], c1 >= 0 ? R0[c1] : KB_NEG_INF,
-                                          c2 >= 0 ? R0[c2] : KB_NEG_INF, leaf_row, i == lpos);
+        const int c1 = omi(OMT_C1, k), c2 = omi(OMT_C2, k);
+        const Coef6 c = coef_at(coef_k(k), piv[k], pbv[k], dts[k], c1 >= 0 ? R0[c1] : KB_NEG_INF,
+                                c2 >= 0 ? R0[c2] : KB_NEG_INF, leaf_row, i == lpos);
         diag[k] = c.q[0] + c.q[1];
         pcoef[k] = c.q[2] * pcoef[k];
         if (c1 >= 0) R1[c1] = c.q[3];
@@ -409,30 +457,27 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
       }
     }
     __syncthreads();
-    // parent position and subtree end - 1 of each own position, packed
-    // (ppos | endm1 << 16; ZERO for none)
+    // parent position, subtree end - 1 and child-1 flag of each own position,
+    // packed (OMT_PK)
     float edge[CPT];
     int pk[CPT];
     lds_load_own<CPT>(R1, edge);
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const int i = pos(k);
-      const int pa = i < S ? ldg(fresh(T.ppos), i) : -1;
-      const int e1 = i < S ? ldg(fresh(T.endpos), i) - 1 : ZERO;
-      pk[k] = (pa >= 0 ? pa : ZERO) | (e1 << 16);
-      edge[k] = pa >= 0 ? edge[k] : 0.0f;
+      pk[k] = omi(OMT_PK, k);
+      edge[k] = (pk[k] & 0xffff) != ZERO ? edge[k] : 0.0f;
     }
     // pk as values the optimiser cannot hoist out of the loops below (the LDS
     // addresses derived from it would otherwise stay live across them)
-    auto pk_now = [&](int (&o)[CPT]) {
+    auto pk_now = [&](int (&o)[CPT], int epoch) {
 #pragma unroll
       for (int k = 0; k < CPT; ++k) {
         o[k] = pk[k];
-        if constexpr (CPT > 4) asm volatile("" : "+v"(o[k]));
+        if constexpr (CPT > 4) asm("; %1" : "+v"(o[k]) : "s"(epoch));
       }
     };
     auto ppos_of = [](int x) { return x & 0xffff; };
-    auto endm1_of = [](int x) { return x >> 16; };
+    auto endm1_of = [](int x) { return (x >> 16) & 0x3fff; };
     auto wend_of = [](int x) { return (x >> (16 + SEGSH)) & (NW - 1); };  // ZERO -> wavefront 0
 
     // ---- 5. Neumann series v = sum_{n<=N} (J^T)^n rhs with the row on chip:
@@ -444,11 +489,11 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
       v[k] = rhs[k];
       term[k] = rhs[k];
     }
-    auto neumann_term = [&](float* Tb, float* Lb, float* wt) {
+    auto neumann_term = [&](float* Tb, float* Lb, float* wt, int n_term) {
       // the LDS addresses come from the packed tables in every term: held
       // across the loop they would take 3 x CPT registers
       int pkt[CPT];
-      pk_now(pkt);
+      pk_now(pkt, n_term);
       float sc[CPT];
 #pragma unroll
       for (int k = 0; k < CPT; ++k) sc[k] = term[k] * pcoef[k] + (k > 0 ? sc[k - 1] : 0.0f);
@@ -481,12 +526,13 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
     {
       int n = 0;
       for (; n + 2 <= P.n_terms; n += 2) {
-        neumann_term(R0, R2, wA);
-        neumann_term(R1, R3, wB);
+        neumann_term(R0, R2, wA, n);
+        neumann_term(R1, R3, wB, n + 1);
       }
-      if (n < P.n_terms) neumann_term(R0, R2, wA);
+      if (n < P.n_terms) neumann_term(R0, R2, wA, n);
     }
 
+    ep = rr * 16 + 6;
     // ---- 6. self-loop column gradient and parameter buckets.  The buffers of
     // the next term's parity are free: Pi* goes back to its Tb buffer for the
     // recomputed coefficients' child gathers, the scan of u = v * pcoef to its
@@ -509,7 +555,7 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
         scan_offsets(wt, A, woff, wexcl);
         const float p0 = wave_prev_lane(sc[CPT - 1]) + woff;
         int pkt[CPT];
-        pk_now(pkt);
+        pk_now(pkt, ep);
         // the column-gradient term p' (P(i-1) + A - P(end(i)-1)), in pcoef's
         // registers (pcoef is not needed after this)
 #pragma unroll
@@ -519,12 +565,17 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
           pcoef[k] = pos(k) < S ? pp[k] * (pm1 + rest) : 0.0f;
         }
       }
-      const CoefPtrs K = coef_ptrs(P);
+      // a group's bucket loads are all issued before its stores (a load after a
+      // store to the slot would wait for that store)
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
+        float4 bk[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) bk[j] = ld4(srow(j) + 4 * g);
         float pb4[4], dt4[4];
         vld<4>(srow(SL_PIBAR) + 4 * g, pb4);
         vld<4>(srow(SL_DTS) + 4 * g, dt4);
+        const float4 pt4 = ld4(Pt + tid * CPT + 4 * g);  // own positions of Pi* (vector LDS read)
         float x[8][4];
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
@@ -533,9 +584,9 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
 #pragma unroll
           for (int j = 0; j < 8; ++j) x[j][kk] = 0.0f;
           if (i < S) {
-            const int c1 = ldg(fresh(T.c1pos), i), c2 = ldg(fresh(T.c2pos), i);
-            const Coef6 c = coef_at(K, i, Pt[i], pb4[kk], dt4[kk], c1 >= 0 ? Pt[c1] : KB_NEG_INF,
-                                              c2 >= 0 ? Pt[c2] : KB_NEG_INF, leaf_row, i == lpos);
+            const int c1 = omi(OMT_C1, k), c2 = omi(OMT_C2, k);
+            const Coef6 c = coef_at(coef_k(k), f4(pt4, kk), pb4[kk], dt4[kk], c1 >= 0 ? Pt[c1] : KB_NEG_INF,
+                                    c2 >= 0 ? Pt[c2] : KB_NEG_INF, leaf_row, i == lpos);
             const float aw0 = v[k] * c.q[0], aw1 = v[k] * c.q[1], aw2 = v[k] * c.q[2];
             const float aw3 = v[k] * c.q[3], aw4 = v[k] * c.q[4], aw5 = v[k] * c.q[5];
             x[0][kk] = aw0;
@@ -549,7 +600,7 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
           }
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) vadd4(srow(j) + 4 * g, x[j]);
+        for (int j = 0; j < 8; ++j) st4_add(srow(j) + 4 * g, bk[j], x[j]);
       }
     }
 
@@ -560,12 +611,14 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
       const float lsp = P.split_lsp[si];
       const float rml = P.rowmax[lrow], rmr = P.rowmax[rrow];
       const float rmsl = fsafe(rml), rmsr = fsafe(rmr);
+      ep = -4 * si - 1;
       __syncthreads();  // previous readers of R0..R3 are done
       stage(R0, P.pi + l);
       stage(R1, P.pi + r);
       stage(R2, P.pibar + l);
       stage(R3, P.pibar + r);
       __syncthreads();
+      ep = -4 * si - 2;
       // pass 1 (own positions, four at a time): the five split-term shares
       // vd_j; vd3 / vd4 replace the own positions of the children's Pibar
       // rows (R2 / R3, read only at own positions) for the child positions'
@@ -573,8 +626,12 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
       float av[CPT], bv[CPT], udl[CPT], udr[CPT], ppl[CPT], ppr[CPT];
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
+        const float4 b0 = ld4(srow(0) + 4 * g), b1 = ld4(srow(1) + 4 * g), b6 = ld4(srow(6) + 4 * g);
         float pv4[4];
         vld<4>(srow(SL_PI) + 4 * g, pv4);
+        // own positions of the four staged child rows (vector LDS reads)
+        const float4 pl4 = ld4(R0 + tid * CPT + 4 * g), pr4 = ld4(R1 + tid * CPT + 4 * g);
+        const float4 bl4 = ld4(R2 + tid * CPT + 4 * g), br4 = ld4(R3 + tid * CPT + 4 * g);
         float y0[4], y1[4], y2[4], d3[4], d4[4];
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
@@ -583,11 +640,11 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
           float vd0 = 0.0f, vd1 = 0.0f, vd2 = 0.0f, vd3 = 0.0f, vd4 = 0.0f;
           udl[k] = udr[k] = ppl[k] = ppr[k] = 0.0f;
           if (i < S) {
-            const int c1 = ldg(fresh(T.c1pos), i), c2 = ldg(fresh(T.c2pos), i);
-            const float pl = R0[i], pr = R1[i], bl = R2[i], br = R3[i];
+            const int c1 = omi(OMT_C1, k), c2 = omi(OMT_C2, k);
+            const float pl = f4(pl4, kk), pr = f4(pr4, kk), bl = f4(bl4, kk), br = f4(br4, kk);
             const float l1 = c1 >= 0 ? R0[c1] : KB_NEG_INF, r1 = c1 >= 0 ? R1[c1] : KB_NEG_INF;
             const float l2 = c2 >= 0 ? R0[c2] : KB_NEG_INF, r2 = c2 >= 0 ? R1[c2] : KB_NEG_INF;
-            const float d = ldg(fresh(P.pD), i), sp = ldg(fresh(P.pS), i);
+            const float d = omf(OMC_PD, k), sp = omf(OMC_PS, k);
             const bool pv = pv4[kk] != KB_NEG_INF;
             const float base = pv ? lsp - pv4[kk] : 0.0f;
             vd0 = pv ? v[k] * exp2_hw(base + (d + pl + pr)) : 0.0f;
@@ -595,12 +652,12 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
             vd2 = pv ? v[k] * exp2_hw(base + (pr + bl)) : 0.0f;
             vd3 = pv ? v[k] * exp2_hw(base + (sp + l1 + r2)) : 0.0f;
             vd4 = pv ? v[k] * exp2_hw(base + (sp + r1 + l2)) : 0.0f;
-            const float mts = ldg(fresh(P.mt), i);
+            const float mts = omf(OMC_MT, k);
             const float inv_l = bl != KB_NEG_INF ? exp2_hw(rml + mts - bl) : 0.0f;
             const float inv_r = br != KB_NEG_INF ? exp2_hw(rmr + mts - br) : 0.0f;
             udl[k] = vd2 * inv_l;
             udr[k] = vd1 * inv_r;
-            const float cw = WEIGHTED ? ldg(fresh(P.col), i) : 0.0f;
+            const float cw = WEIGHTED ? omf(OMC_COL, k) : 0.0f;
             ppl[k] = exp2_hw(cw + pl - rmsl);
             ppr[k] = exp2_hw(cw + pr - rmsr);
           }
@@ -614,11 +671,14 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
         }
         *reinterpret_cast<float4*>(R2 + tid * CPT + 4 * g) = make_float4(d3[0], d3[1], d3[2], d3[3]);
         *reinterpret_cast<float4*>(R3 + tid * CPT + 4 * g) = make_float4(d4[0], d4[1], d4[2], d4[3]);
-        vadd4(srow(0) + 4 * g, y0);
-        vadd4(srow(1) + 4 * g, y1);
-        vadd4(srow(6) + 4 * g, y2);
+        st4_add(srow(0) + 4 * g, b0, y0);
+        st4_add(srow(1) + 4 * g, b1, y1);
+        st4_add(srow(6) + 4 * g, b6, y2);
       }
       __syncthreads();  // the staged children (R0, R1) fully read; vd3 / vd4 published
+      float4 b7[NG];
+#pragma unroll
+      for (int g = 0; g < NG; ++g) b7[g] = ld4(srow(7) + 4 * g);
       float scl[CPT], scr[CPT];
       local_scan_publish<NT, CPT>(scl, udl, R0, wA);
       local_scan_publish<NT, CPT>(scr, udr, R1, wA + NW);
@@ -628,10 +688,11 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
       scan_offsets(wA + NW, Ar, woffr, wexr);
       const float p0l = wave_prev_lane(scl[CPT - 1]) + woffl;
       const float p0r = wave_prev_lane(scr[CPT - 1]) + woffr;
+      ep = -4 * si - 3;
       float* stl = P.staging + (size_t)(2 * si) * S;
       float* str = P.staging + (size_t)(2 * si + 1) * S;
       int pkt[CPT];
-      pk_now(pkt);
+      pk_now(pkt, ep);
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
         float y3[4];
@@ -649,7 +710,7 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
             const float tl = ppl[k] * (pml + rsl);
             const float tr = ppr[k] * (pmr + rsr);
             const int pa = ppos_of(pkt[k]);
-            const bool first_child = pa != ZERO && ldg(fresh(T.pflag), i) != 0;
+            const bool first_child = (pkt[k] >> 30) & 1;
             const float sh3 = R2[pa], sh4 = R3[pa];  // padding slot holds 0
             const float shl = first_child ? sh3 : sh4;
             const float shr = first_child ? sh4 : sh3;
@@ -658,7 +719,7 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
             y3[kk] = tl + tr;
           }
         }
-        vadd4(srow(7) + 4 * g, y3);
+        st4_add(srow(7) + 4 * g, b7[g], y3);
       }
       if (tid == 0) P.split_on[si] = 1;
     }

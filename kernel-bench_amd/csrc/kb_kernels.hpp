@@ -93,7 +93,19 @@ struct BwdConstArgs {
   // outputs at preorder positions
   float* DL; float* SL1; float* SL2; float* pS_state; float* pD_state;
   float* Ebar_pre; float* E_pre; float* mt_pre; float* col_pre;
+  float* om;                  // also in the owner-major layout (KB_OM_CONSTS rows), or null
 };
+
+// Owner-major layout of bwd_row_large_kernel's per-position tables: with
+// 1024 threads owning CPT positions each (thread t: t*CPT .. t*CPT+CPT-1),
+// row j holds position t*CPT + k at [j*1024*CPT + k*1024 + t], so a
+// wavefront's reads of one slot k are contiguous.
+enum OmConst { OMC_DL, OMC_EBAR, OMC_E, OMC_SL1, OMC_SL2, OMC_PD, OMC_PS, OMC_MT, OMC_COL, KB_OM_CONSTS };
+// position tables: child-1 / child-2 positions (-1: leaf); parent position
+// (ZERO = 1024*CPT for the root) | (subtree end - 1) << 16 | child-1 flag << 30;
+// postorder slot's position | (tin(i) - i) << 16.  Positions >= S: -1, -1,
+// ZERO | ZERO << 16, ZERO.
+enum OmTab { OMT_C1, OMT_C2, OMT_PK, OMT_PN, KB_OM_TABS };
 
 // The backward's record of a schedule slot (KB_BREC ints): the row's first
 // two child sides (-1: none; bit 30 of the second: more sides follow), the
@@ -132,6 +144,8 @@ struct BwdParams {
   int class_mode;             // 1: entries are classes of identical rows (cls_ptr / cls_rows)
   int variant;                // launch shape: 0 default, 2 narrow (1024 threads x 2 states)
   int large;                  // 1: rows of 2049..8192 states run bwd_row_large_kernel
+  const int* om_tab;          // [KB_OM_TABS, kb_large_ld(S)] owner-major position tables (OmTab)
+  const float* om_const;      // [KB_OM_CONSTS, kb_large_ld(S)] owner-major constants (OmConst)
   float* rhs0;                // [rows of level 0, S] preorder adjoint rows, in cls_rows order
   float* rhsc;                // [classes of level 0, S] summed adjoint of each class
   const int* m_side_ptr;      // [members + 1] staging sides of each level-0 member (cls_rows order)

@@ -784,6 +784,13 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
   F.row_kind = p->d_row_kind;
   F.dup_ptr = p->d_dup_ptr;
   F.dup_rows = p->d_dup_rows;
+  F.om_tab = p->d_om_tab;
+  {
+    // rows of 4097..8192 states: the contiguous-ownership kernel on the
+    // owner-major tables (KB_FWD_LARGE=0: the Euler-tour kernel)
+    const char* lv = getenv("KB_FWD_LARGE");
+    F.large = (lv && lv[0] == '0') ? 0 : 1;
+  }
   F.dts_out = p->d_dts;
   p->fwd_token += 1;
   p->fwd_pi = io->pi;

@@ -29,30 +29,6 @@ namespace kb {
 
 namespace {
 
-// b[i] through a 32-bit byte offset from a uniform base.
-template <typename T>
-__device__ __forceinline__ T ldg(const T* b, int i) {
-  return *reinterpret_cast<const T*>(reinterpret_cast<const char*>(b) + (unsigned)i * (unsigned)sizeof(T));
-}
-template <typename T>
-__device__ __forceinline__ void stg(T* b, int i, T x) {
-  *reinterpret_cast<T*>(reinterpret_cast<char*>(b) + (unsigned)i * (unsigned)sizeof(T)) = x;
-}
-
-// The same uniform pointer, opaque to the optimiser for each value of
-// `epoch`.  Each phase of a row passes its own epoch (the row and phase, or
-// split and step), so the per-lane addresses of its tables are formed in that
-// phase: with plain pointers they are computed once per row, or hoisted out of
-// the row loop, and held in register pairs across the Neumann series.  The
-// asm has no side effects, so loads around it still issue together.
-template <typename T>
-__device__ __forceinline__ T* fresh(T* p, int epoch) {
-  unsigned long long x = reinterpret_cast<unsigned long long>(p);
-  asm("; %1" : "+s"(x) : "s"(epoch));
-  // a global-memory pointer again, so the accesses stay global (not flat)
-  return (T*)reinterpret_cast<__attribute__((address_space(1))) T*>(x);
-}
-
 // the per-position constants the coefficients read
 struct CoefK {
   float DL, Ebar, E, SL1, SL2, pS;

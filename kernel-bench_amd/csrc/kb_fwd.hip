@@ -275,7 +275,11 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
 
   // Tables of the own positions i = tid*CPT + k and of the own postorder slots.
   // In preorder (child1 first) child1 of i is i + 1: from registers, except
-  // for the last own position, whose child1 is read from X.
+  // for the last own position, whose child1 is read from X.  With 8 positions
+  // per thread (and the owner-major tables given) the sweeps read child2, the
+  // postorder slot and tin(i) - i from those tables in every sweep instead of
+  // holding them in registers.
+  constexpr bool OMT = CPT == 8;
   int c2p[CPT], nex[CPT], qp[CPT], pre_s[CPT];
   bool h1[CPT];
 #pragma unroll
@@ -451,6 +455,16 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
   float ps[CPT], rowsum = 0.0f, f = 1.0f;
 
   for (int sweep = 0;; ++sweep) {
+    if constexpr (OMT) {  // (the launcher requires the tables for this shape)
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        const int c2 = ldg(fresh(P.om_tab + (size_t)OMT_C2 * MAXS + k * NT, sweep), tid);
+        const int pn = ldg(fresh(P.om_tab + (size_t)OMT_PN * MAXS + k * NT, sweep), tid);
+        c2p[k] = c2 >= 0 ? c2 : ZERO;
+        qp[k] = pn & 0xffff;
+        nex[k] = pn >> 16;
+      }
+    }
     // phase A: publish y; inclusive preorder scan (wavefront-local) in registers
     float sp[CPT], ta = 0.0f;
 #pragma unroll
@@ -593,6 +607,9 @@ void launch_fwd_wave(const FwdParams& P, int first, int W, hipStream_t st) {
   KB_FWD_CASE(256, 4, fwd_row_kernel)
   KB_FWD_CASE(512, 4, fwd_row_kernel)
   KB_FWD_CASE(1024, 4, fwd_row_kernel)
+  if (P.om_tab && P.large) {
+    KB_FWD_CASE(1024, 8, fwd_row_kernel)
+  }
   KB_FWD_CASE(1024, 8, fwd_row_kernel_euler)
 }
 

@@ -72,6 +72,8 @@ struct FwdParams {
   const int* row_kind;        // 1: leaf row, 0: split row
   const int* dup_ptr;         // [slots + 1] rows identical to the row of each slot ...
   const int* dup_rows;        // ... which receive the same outputs
+  const int* om_tab;          // owner-major position tables (OmTab) for rows of 4097..8192 states, or null
+  int large;                  // 1: rows of 4097..8192 states run fwd_row_kernel on om_tab (else the Euler kernel)
   // outputs
   float* pi; float* pibar; float* rowmax;
   float* dts_out;             // [C, S] preorder split term of every computed split row

@@ -78,6 +78,32 @@ __device__ __forceinline__ float wave_reduce_max(float x) {
   return x;
 }
 
+// ---- global accesses of the large-row kernels ----------------------------------
+
+// b[i] through a 32-bit byte offset from a uniform base.
+template <typename T>
+__device__ __forceinline__ T ldg(const T* b, int i) {
+  return *reinterpret_cast<const T*>(reinterpret_cast<const char*>(b) + (unsigned)i * (unsigned)sizeof(T));
+}
+template <typename T>
+__device__ __forceinline__ void stg(T* b, int i, T x) {
+  *reinterpret_cast<T*>(reinterpret_cast<char*>(b) + (unsigned)i * (unsigned)sizeof(T)) = x;
+}
+
+// The same uniform pointer, opaque to the optimiser for each value of
+// `epoch`.  A kernel passes a different epoch in each phase or iteration (the
+// row and phase, the split, the sweep), so the per-lane addresses of its
+// tables are formed where they are used: with plain pointers they are computed
+// once and hoisted out of the loops, held in register pairs across them.  The
+// asm has no side effects, so loads around it still issue together.
+template <typename T>
+__device__ __forceinline__ T* fresh(T* p, int epoch) {
+  unsigned long long x = reinterpret_cast<unsigned long long>(p);
+  asm("; %1" : "+s"(x) : "s"(epoch));
+  // a global-memory pointer again, so the accesses stay global (not flat)
+  return (T*)reinterpret_cast<__attribute__((address_space(1))) T*>(x);
+}
+
 // ---- float64 wavefront primitives (DPP on the two 32-bit halves) -------------
 
 template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>

@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "kb_ops_common.hpp"
 
@@ -428,9 +429,279 @@ __global__ __launch_bounds__(NT) void wave_tan_kernel(OpsTree t, WtArgs<T> a) {
   }
 }
 
+// float32 rows: the same update at preorder ownership (thread t owns
+// positions t*CPT + k, as the forward row kernels), computed in float32 as the
+// reference's Triton kernel computes it.  The path sums come from an
+// inclusive preorder scan and an exclusive postorder scan,
+//   dAS(i) = Pre(i) - PostEx(tin(i) - i),
+// so one tangent update takes two barriers (the float64 kernel above takes an
+// Euler-tour scan and two more barriers per update).
+template <int CPT>
+__global__ __launch_bounds__(NT) void wave_tan_pre_kernel(OpsTree t, WtArgs<float> a) {
+  constexpr int MAXS = NT * CPT;
+  constexpr int LD = MAXS + 64;
+  constexpr int ZERO = MAXS;     // padding slot: 0 in X
+  constexpr int SEG = 64 * CPT;  // postorder slots per wavefront
+  extern __shared__ __align__(16) unsigned char smraw[];
+  float* R = reinterpret_cast<float*>(smraw);  // the row at preorder positions: Pi, then the tangent
+  float* X = R + LD;                           // the scanned values at preorder positions
+  float* Q = X + LD;                           // exclusive postorder scan
+  __shared__ float wM[NW], wA[NW], wB[NW];
+  const int S = t.S;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const float NI = -__builtin_inff();
+  const int w = blockIdx.x;
+  const long long grow = a.ws + w;
+  const long long item = a.item[grow];
+  const size_t cb = (size_t)(item * a.cstride);
+  const size_t lb = (size_t)item * S;
+  const size_t ib = (size_t)(a.pi_ws + w) * S;
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int sc = tid + j * NT;
+    if (sc < S) R[t.ppos[sc]] = a.Pi[ib + sc];
+  }
+  if (tid < 64) X[MAXS + tid] = 0.0f;
+  int c1p[CPT], c2p[CPT], nex[CPT], qp[CPT], colk[CPT];
+  bool okp[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int i = kb::own_pos_c<NT, CPT>(k);
+    okp[k] = i < S;
+    c1p[k] = okp[k] ? t.pc1[i] : -1;
+    c2p[k] = okp[k] ? t.pc2[i] : -1;
+    nex[k] = okp[k] ? t.pnex[i] : 0;
+    qp[k] = okp[k] ? t.ppost[i] : ZERO;
+    colk[k] = okp[k] ? t.pcol[i] : 0;
+  }
+  __syncthreads();
+  // ---- primal set-up at Pi: r = 2^(col + Pi - M), its row sum and path sums
+  float pv[CPT], r[CPT];
+  kb::lds_load_own<CPT>(R, pv);
+  float lm = NI;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    if (!okp[k]) pv[k] = NI;
+    lm = fmaxf(lm, (a.use_col && okp[k] ? a.col[colk[k]] : 0.0f) + pv[k]);
+  }
+  const float M = kb::block_max1<NT>(lm, wM);
+  const float Ms = M == NI ? 0.0f : M;
+  // one path-sum pass over x (own positions): tot = sum x, ps = Pre - PostEx;
+  // x is published in X for the postorder reads.  Two barriers.
+  float ps[CPT], tot = 0.0f;
+  auto path_pass = [&](const float (&x)[CPT]) {
+    float sp[CPT], ta = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      ta += x[k];
+      sp[k] = ta;
+    }
+    const float wa = kb::wave_scan_incl(ta);
+    kb::lds_store_own<CPT>(X, x);
+    if (lane == 63) wA[wv] = wa;
+    __syncthreads();
+    const float tp = kb::lds_wave_values<NW>(wA, lane, 0.0f);
+    float yq[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) yq[k] = X[qp[k]];
+    const float ip = kb::wave_scan_first<NW>(tp);
+    tot = kb::lane_value(ip, NW - 1);
+    const float offp = kb::lane_value(ip - tp, wv) + (wa - ta);
+    float sq[CPT], tb = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      sq[k] = tb;
+      tb += yq[k];
+    }
+    const float wb = kb::wave_scan_incl(tb);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) sq[k] += wb - tb;
+    kb::lds_store_own<CPT>(Q, sq);
+    if (lane == 63) wB[wv] = wb;
+    __syncthreads();
+    const float tq = kb::lds_wave_values<NW>(wB, lane, 0.0f);
+    const float eq = kb::wave_scan_first<NW>(tq) - tq;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int n = nex[k];
+      ps[k] = (sp[k] + offp) - (Q[n] + __shfl(eq, n / SEG, 64));
+    }
+  };
+#pragma unroll
+  for (int k = 0; k < CPT; ++k)
+    r[k] = okp[k] ? exp2f((a.use_col ? a.col[colk[k]] : 0.0f) + pv[k] - Ms) : 0.0f;
+  path_pass(r);
+  const float rowsum = tot;
+  const long long lstate = a.use_leaf ? a.leaf_state[grow] : -1;
+  float K[CPT], lin[CPT], wbk[CPT], w3[CPT], w4[CPT], den[CPT], dm[CPT];
+  bool pos[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    K[k] = lin[k] = wbk[k] = w3[k] = w4[k] = dm[k] = 0.0f;
+    den[k] = 1.0f;
+    pos[k] = false;
+    if (okp[k]) {
+      const int s = colk[k];
+      const size_t ci = cb + s;
+      const float pi = pv[k];
+      const float ps1 = c1p[k] >= 0 ? R[c1p[k]] : NI, ps2 = c2p[k] >= 0 ? R[c2p[k]] : NI;
+      const float denom = rowsum - ps[k];
+      pos[k] = denom > 0.0f;
+      den[k] = pos[k] ? denom : 1.0f;
+      const float pibar = pos[k] ? log2f(den[k]) + M + a.mt[ci] : NI;
+      dm[k] = pos[k] ? a.dmt[ci] : 0.0f;
+      const bool hit = lstate == s;
+      const float t0 = a.DL[ci] + pi;
+      const float t1 = pi + a.Ebar[ci];
+      const float t2 = pibar + a.E[ci];
+      const float t3 = a.SL1[ci] + ps1;
+      const float t4 = a.SL2[ci] + ps2;
+      const float t5 = hit ? a.leaf_logp[lb + s] : NI;
+      float m = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, t5));
+      float td = NI;
+      if (a.dts) {
+        td = a.dts[(size_t)w * S + s];
+        m = fmaxf(m, td);
+      }
+      const float ms = m == NI ? 0.0f : m;
+      const float e0 = exp2f(t0 - ms), e1 = exp2f(t1 - ms), e2 = exp2f(t2 - ms), e3 = exp2f(t3 - ms);
+      const float e4 = exp2f(t4 - ms), e5 = exp2f(t5 - ms), ed = a.dts ? exp2f(td - ms) : 0.0f;
+      const float total = e0 + e1 + e2 + e3 + e4 + e5 + ed;
+      const float res = log2f(total) + m;
+      if (res != NI && total > 0.0f) {
+        const float inv = 1.0f / total;
+        float k0 = e0 * a.dDL[ci] + e1 * a.dEbar[ci] + e2 * (a.dE[ci] + dm[k]) + e3 * a.dSL1[ci] + e4 * a.dSL2[ci];
+        if (hit) k0 += e5 * a.dleaf_logp[lb + s];
+        if (a.dts) k0 += ed * a.ddts[(size_t)w * S + s];
+        K[k] = k0 * inv;
+        lin[k] = (e0 + e1) * inv;
+        wbk[k] = pos[k] ? e2 * inv : 0.0f;
+        w3[k] = e3 * inv;
+        w4[k] = e4 * inv;
+      }
+    }
+  }
+  __syncthreads();  // every read of the Pi row in R is done
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int sc = tid + j * NT;
+    if (sc < S) R[t.ppos[sc]] = a.dPi_in[ib + sc];
+  }
+  __syncthreads();
+  float dv[CPT], dpb[CPT];
+  kb::lds_load_own<CPT>(R, dv);
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    if (!okp[k]) dv[k] = 0.0f;
+    dpb[k] = 0.0f;
+  }
+  // ---- tangent updates.  The tangent row is published in R with the first
+  // barrier of the pass (for the child reads, done before its second
+  // barrier); the next update's writes follow that second barrier.
+  const int n_it = a.n_iters < 1 ? 1 : a.n_iters;
+  for (int it = 0; it < n_it; ++it) {
+    if (it > 0) kb::lds_store_own<CPT>(R, dv);
+    float x[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) x[k] = r[k] * dv[k];
+    float ch1[CPT], ch2[CPT];
+    {
+      // (the pass's first barrier publishes R; the child reads precede its second)
+      float sp[CPT], ta = 0.0f;
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        ta += x[k];
+        sp[k] = ta;
+      }
+      const float wa = kb::wave_scan_incl(ta);
+      kb::lds_store_own<CPT>(X, x);
+      if (lane == 63) wA[wv] = wa;
+      __syncthreads();
+      const float tp = kb::lds_wave_values<NW>(wA, lane, 0.0f);
+      float yq[CPT];
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        yq[k] = X[qp[k]];
+        ch1[k] = c1p[k] >= 0 ? R[c1p[k]] : 0.0f;
+        ch2[k] = c2p[k] >= 0 ? R[c2p[k]] : 0.0f;
+      }
+      const float ip = kb::wave_scan_first<NW>(tp);
+      tot = kb::lane_value(ip, NW - 1);
+      const float offp = kb::lane_value(ip - tp, wv) + (wa - ta);
+      float sq[CPT], tb = 0.0f;
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        sq[k] = tb;
+        tb += yq[k];
+      }
+      const float wb = kb::wave_scan_incl(tb);
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) sq[k] += wb - tb;
+      kb::lds_store_own<CPT>(Q, sq);
+      if (lane == 63) wB[wv] = wb;
+      __syncthreads();
+      const float tq = kb::lds_wave_values<NW>(wB, lane, 0.0f);
+      const float eq = kb::wave_scan_first<NW>(tq) - tq;
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        const int n = nex[k];
+        ps[k] = (sp[k] + offp) - (Q[n] + __shfl(eq, n / SEG, 64));
+      }
+    }
+    const float dRS = tot;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      float nx = 0.0f;
+      dpb[k] = 0.0f;
+      if (okp[k]) {
+        const float qd = (dRS - ps[k]) / den[k];
+        dpb[k] = pos[k] ? qd + dm[k] : 0.0f;
+        nx = K[k] + lin[k] * dv[k] + wbk[k] * qd + w3[k] * ch1[k] + w4[k] * ch2[k];
+      }
+      dv[k] = nx;
+    }
+  }
+  // outputs by column (coalesced): R and X were last read before the last
+  // pass's second barrier
+  kb::lds_store_own<CPT>(R, dv);
+  kb::lds_store_own<CPT>(X, dpb);
+  __syncthreads();
+  float* out = a.dPi_out + (size_t)grow * S;
+  float* pb = a.dPibar ? a.dPibar + (size_t)grow * S : nullptr;
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int sc = tid + j * NT;
+    if (sc < S) {
+      const int i = t.ppos[sc];
+      out[sc] = R[i];
+      if (pb) pb[sc] = X[i];
+    }
+  }
+}
+
 }  // namespace kbo
 
 using namespace kbo_host;
+
+namespace {
+
+// float32 rows run the preorder-ownership kernel, float64 rows the float64 one
+template <typename T, int CPT>
+int launch_wave_tan(const kbo::OpsTree& t, const kbo::WtArgs<T>& a, int W, size_t lds, hipStream_t st) {
+  if constexpr (std::is_same_v<T, float>) {
+    const size_t lds_pre = (size_t)3 * (kbo::NT * CPT + 64) * sizeof(float);
+    auto k = kbo::wave_tan_pre_kernel<CPT>;
+    if (int rc = set_lds(k, lds_pre)) return rc;
+    hipLaunchKernelGGL(k, dim3(W), dim3(kbo::NT), lds_pre, st, t, a);
+    return 0;
+  }
+  auto k = kbo::wave_tan_kernel<T, CPT>;
+  if (int rc = set_lds(k, lds)) return rc;
+  hipLaunchKernelGGL(k, dim3(W), dim3(kbo::NT), lds, st, t, a);
+  return 0;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -498,8 +769,7 @@ int kb_wave_step_tangent(const kb_tree* tr, const kb_wave_tan_io* io, void* stre
                      (const T*)io->SL1, (const T*)io->dSL1, (const T*)io->SL2, (const T*)io->dSL2,
                      (const T*)io->col_log_probs, io->item_idx, io->leaf_state, (const T*)io->leaf_logp,
                      (const T*)io->dleaf_logp};
-    if (int rc = set_lds(kbo::wave_tan_kernel<T, CPT>, lds)) return rc;
-    hipLaunchKernelGGL((kbo::wave_tan_kernel<T, CPT>), dim3(io->W), dim3(kbo::NT), lds, st_of(stream), t, a);
+    if (int rc = launch_wave_tan<T, CPT>(t, a, io->W, lds, st_of(stream))) return rc;
   });
   KBO_HIP(hipGetLastError());
   return 0;

@@ -207,6 +207,37 @@ def test_fused_large_trees_match_oracle(leaves, families, statewise, weighted, s
     assert rt <= 1e-4 and rc <= 1e-4
 
 
+@pytest.mark.parametrize("weighted", [False, True])
+def test_large_tree_forward_kernels_agree(weighted, monkeypatch):
+    """S = 8191: the contiguous-ownership forward on the owner-major tables against the Euler-tour
+    kernel (KB_FWD_LARGE=0): same loss and Pi rows to float32 rounding."""
+    from kbench.fused import FusedSolver, problem_to_captured
+    from kbench.runtime import make_static
+
+    print(f"[fused-large-fwd-ab] weighted={weighted}", flush=True)
+    p = _big_tree_problem(4096, 3, True)
+    cap = problem_to_captured(p)
+    static = make_static(cap, "cuda")
+    solver = FusedSolver(static, static.solver_options)
+    theta = cap["inputs"]["theta"].cuda()
+    n = int(cap["inputs"]["col_weights"].numel())
+    cw32 = (np.random.default_rng(9).normal(0.0, 0.5, size=n) if weighted else np.zeros(n)).astype(np.float32)
+    cw = torch.from_numpy(cw32).cuda()
+    runs = {}
+    for large in ("1", "0"):
+        monkeypatch.setenv("KB_FWD_LARGE", large)
+        loss, saved = solver.run_forward(theta, cw)
+        torch.cuda.synchronize()
+        runs[large] = (float(loss), saved["pi_wave"].cpu().numpy(), saved["pibar_wave"].cpu().numpy())
+    rel = abs(runs["1"][0] - runs["0"][0]) / abs(runs["0"][0])
+    for j, name in ((1, "pi_wave"), (2, "pibar_wave")):
+        ok, ma, mr = kbtest.compare_inf_safe(runs["1"][j], runs["0"][j])
+        print(f"  {name}: pattern={ok} max_abs={ma:.3e} max_rel={mr:.3e}")
+        assert ok and (ma <= 2e-4 or mr <= 1e-5)
+    print(f"  loss rel={rel:.3e}")
+    assert rel <= 1e-6
+
+
 @pytest.mark.parametrize("leaves,weighted", [(2048, False), (4096, True)])
 def test_large_tree_backward_kernels_agree(leaves, weighted, monkeypatch):
     """S = 4095 and 8191: the low-register backward row kernel against the general one

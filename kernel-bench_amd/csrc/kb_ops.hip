@@ -1029,6 +1029,329 @@ __global__ __launch_bounds__(NT) void wave_bwd_kernel(OpsTree t, WbArgs<T> a) {
   }
 }
 
+// float32 rows at preorder ownership (thread t owns positions t*CPT + k, as
+// the whole-pass backward row kernel): the root-path sums of p' from an
+// inclusive preorder and an exclusive postorder scan, one barrier per Neumann
+// term (wavefront-local scans published, the readers add the wavefront
+// offsets), and the [W, S] outputs written back in column order through LDS.
+// Same mathematics as wave_bwd_kernel.
+template <int CPT>
+__global__ __launch_bounds__(NT) void wave_bwd_pre_kernel(OpsTree t, WbArgs<float> a) {
+  constexpr int MAXS = NT * CPT;
+  constexpr int LD = MAXS + 64;  // [MAXS] is the padding slot, kept at 0
+  constexpr int ZERO = MAXS;
+  constexpr int SEG = 64 * CPT;  // postorder slots per wavefront
+  extern __shared__ __align__(16) unsigned char smraw[];
+  float* L0 = reinterpret_cast<float*>(smraw);
+  float* L1 = L0 + LD;
+  float* L2 = L1 + LD;
+  float* L3 = L2 + LD;
+  __shared__ float wA[NW], wB[NW];
+  const int S = a.S;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int w = blockIdx.x;
+  const long long grow = a.ws + w;
+  const size_t ob = (size_t)w * S;
+  const float NI = -__builtin_inff();
+  const bool act = a.active ? a.active[w] != 0 : true;
+  if (!act) {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int s = tid + k * NT;
+      if (s < S) {
+        a.v[ob + s] = 0;
+        a.aw0[ob + s] = 0;
+        a.aw1[ob + s] = 0;
+        a.aw2[ob + s] = 0;
+        a.aw345[ob + s] = 0;
+        a.aw3[ob + s] = 0;
+        a.aw4[ob + s] = 0;
+        a.col_rows[ob + s] = 0;
+      }
+    }
+    if (a.relres && tid == 0) a.relres[w] = 0.0f;
+    return;
+  }
+  const long long item = a.item ? a.item[grow] : 0;
+  const size_t cb = a.clayout == 1 ? ob : (a.clayout == 2 ? (size_t)item * S : 0);
+  const float* pirow = a.Pi + (size_t)grow * S;
+  const float* pbrow = a.Pibar + (size_t)grow * S;
+  const float rms = msafe(a.rowmax[grow]);
+  // Pi and Pibar to their preorder positions (coalesced column reads)
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int sc = tid + j * NT;
+    if (sc < S) {
+      const int p = t.ppos[sc];
+      L0[p] = pirow[sc];
+      L1[p] = pbrow[sc];
+    }
+  }
+  if (tid < 64) {
+    L0[MAXS + tid] = 0.0f;
+    L1[MAXS + tid] = 0.0f;
+    L2[MAXS + tid] = 0.0f;
+    L3[MAXS + tid] = 0.0f;
+  }
+  // own positions: column, children, parent, subtree end - 1, postorder slot, tin - i
+  int colk[CPT], c1p[CPT], c2p[CPT], ppar[CPT], endm1[CPT], wend[CPT], qp[CPT], nex[CPT];
+  bool okp[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int i = kb::own_pos_c<NT, CPT>(k);
+    okp[k] = i < S;
+    colk[k] = okp[k] ? t.pcol[i] : 0;
+    c1p[k] = okp[k] ? t.pc1[i] : -1;
+    c2p[k] = okp[k] ? t.pc2[i] : -1;
+    const int par = okp[k] ? t.par[colk[k]] : -1;
+    ppar[k] = par >= 0 ? t.ppos[par] : ZERO;
+    endm1[k] = okp[k] ? t.pend[colk[k]] - 1 : ZERO;
+    wend[k] = endm1[k] < ZERO ? endm1[k] / SEG : 0;
+    qp[k] = okp[k] ? t.ppost[i] : ZERO;
+    nex[k] = okp[k] ? t.pnex[i] : 0;
+  }
+  __syncthreads();
+  float piv[CPT], pbv[CPT];
+  kb::lds_load_own<CPT>(L0, piv);
+  kb::lds_load_own<CPT>(L1, pbv);
+  // p' = 2^(col + Pi - rowmax) and its root-path sums ps(i) = Pre(i) - PostEx(tin(i) - i)
+  float pp[CPT], sp[CPT], ta = 0.0f;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    pp[k] = okp[k] ? xexp2((a.use_col ? a.col[colk[k]] + piv[k] : piv[k]) - rms) : 0.0f;
+    ta += pp[k];
+    sp[k] = ta;
+  }
+  const float wa = kb::wave_scan_incl(ta);
+  kb::lds_store_own<CPT>(L2, pp);
+  if (lane == 63) wA[wv] = wa;
+  __syncthreads();
+  float ps[CPT], ch1[CPT], ch2[CPT], row_sum;
+  {
+    const float tp = kb::lds_wave_values<NW>(wA, lane, 0.0f);
+    float yq[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      yq[k] = L2[qp[k]];
+      ch1[k] = c1p[k] >= 0 ? L0[c1p[k]] : NI;
+      ch2[k] = c2p[k] >= 0 ? L0[c2p[k]] : NI;
+    }
+    const float ip = kb::wave_scan_first<NW>(tp);
+    row_sum = kb::lane_value(ip, NW - 1);
+    const float offp = kb::lane_value(ip - tp, wv) + (wa - ta);
+    float sq[CPT], tb = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      sq[k] = tb;
+      tb += yq[k];
+    }
+    const float wb = kb::wave_scan_incl(tb);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) sq[k] += wb - tb;
+    kb::lds_store_own<CPT>(L3, sq);
+    if (lane == 63) wB[wv] = wb;
+    __syncthreads();
+    const float tq = kb::lds_wave_values<NW>(wB, lane, 0.0f);
+    const float eq = kb::wave_scan_first<NW>(tq) - tq;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int n = nex[k];
+      ps[k] = (sp[k] + offp) - (L3[n] + __shfl(eq, n / SEG, 64));
+    }
+  }
+  // J^T coefficients; the child-edge weights (q3 into child1, q4 into child2)
+  // scattered by the parent's owner into L1; the rhs and initial rows staged
+  // into L2 / L0 (free since the scans above), all under one barrier
+  const long long lstate = a.use_leaf ? a.leaf_state[grow] : -1;
+  float diag[CPT], pcoef[CPT], q[6][CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    diag[k] = pcoef[k] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 6; ++j) q[j][k] = 0.0f;
+    if (okp[k]) {
+      const int s = colk[k];
+      const size_t ci = cb + s;
+      const float pi = piv[k];
+      const float t0 = a.DL[ci] + pi;
+      const float t1 = pi + a.Ebar[ci];
+      const float t2 = pbv[k] + a.E[ci];
+      const float t3 = a.SL1[ci] + ch1[k];
+      const float t4 = a.SL2[ci] + ch2[k];
+      float t5 = NI;
+      if (a.use_leaf) {
+        if (lstate == s) {
+          if (a.leaf_mode == 3) t5 = a.leaf_logp[0];
+          else if (a.leaf_mode == 1) t5 = a.leaf_logp[item];
+          else if (a.leaf_mode == 2) t5 = a.leaf_logp[(size_t)item * S + s];
+          else t5 = a.leaf_logp[s];
+        }
+      } else if (a.leaf_term) {
+        t5 = a.leaf_term[ob + s];
+      }
+      const float m = tmax(tmax(tmax(t0, t1), tmax(t2, t3)), tmax(t4, t5));
+      const float ms = msafe(m);
+      const float e0 = xexp2(t0 - ms), e1 = xexp2(t1 - ms), e2 = xexp2(t2 - ms);
+      const float e3 = xexp2(t3 - ms), e4 = xexp2(t4 - ms), e5 = xexp2(t5 - ms);
+      const float sum = e0 + e1 + e2 + e3 + e4 + e5;
+      const float isum = sum > 0.0f ? 1.0f / sum : 0.0f;
+      float wl = 1.0f;
+      if (a.dts) {
+        const float dl = xlog2(sum) + m;
+        const float dr = a.dts[ob + s];
+        const float pm = tmax(dl, dr);
+        const float pms = msafe(pm);
+        const float pnew = xlog2(xexp2(dl - pms) + xexp2(dr - pms)) + pm;
+        wl = dl != NI ? xexp2(dl - pnew) : 0.0f;
+      }
+      const float denom = row_sum - ps[k];
+      const float idn = denom > 0.0f ? 1.0f / denom : 0.0f;
+      diag[k] = wl * (e0 + e1) * isum;
+      pcoef[k] = wl * e2 * isum * idn;
+      const float c = wl * isum;
+      q[0][k] = c * e0;
+      q[1][k] = c * e1;
+      q[2][k] = c * e2;
+      q[3][k] = c * e3;
+      q[4][k] = c * e4;
+      q[5][k] = c * e5;
+      if (c1p[k] >= 0) L1[c1p[k]] = wl * e3 * isum;
+      if (c2p[k] >= 0) L1[c2p[k]] = wl * e4 * isum;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int sc = tid + j * NT;
+    if (sc < S) {
+      const int p = t.ppos[sc];
+      L2[p] = a.rhs[ob + sc];
+      if (a.v0) L0[p] = a.v0[ob + sc];
+    }
+  }
+  __syncthreads();
+  float edge[CPT], rh[CPT], v[CPT], term[CPT];
+  kb::lds_load_own<CPT>(L1, edge);
+  kb::lds_load_own<CPT>(L2, rh);
+  if (a.v0) kb::lds_load_own<CPT>(L0, v);
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    edge[k] = ppar[k] != ZERO ? edge[k] : 0.0f;
+    if (!okp[k]) rh[k] = 0.0f;
+    // Neumann: term_0 = rhs; fixed point from initial_v: the term is v itself
+    v[k] = a.v0 ? (okp[k] ? v[k] : 0.0f) : rh[k];
+    term[k] = v[k];
+  }
+  // Neumann series v = sum_{n <= N} (J^T)^n rhs, or N steps of v <- rhs + J^T v.
+  // Buffers alternate by parity: (Tb, Lb) = (L0, L2) for even terms, (L1, L3)
+  // for odd ones; every thread read its own L0..L2 entries above, and the
+  // other threads' entries are read only after each term's barrier.
+  auto neumann_term = [&](float* Tb, float* Lb, float* wt) {
+    float sc[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) sc[k] = term[k] * pcoef[k] + (k > 0 ? sc[k - 1] : 0.0f);
+    const float tsum = sc[CPT - 1];
+    const float ws = kb::wave_scan_incl(tsum);
+    if (lane == 63) wt[wv] = ws;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) sc[k] += ws - tsum;
+    kb::lds_store_own<CPT>(Lb, sc);
+    kb::lds_store_own<CPT>(Tb, term);
+    __syncthreads();
+    float le[CPT], tpar[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      le[k] = Lb[endm1[k]];
+      tpar[k] = Tb[ppar[k]];
+    }
+    const float wtot = lane < NW ? wt[lane] : 0.0f;
+    const float wincl = kb::wave_scan_first<NW>(wtot);
+    const float wexcl = wincl - wtot;
+    const float A = kb::lane_value(wincl, NW - 1);
+    const float woff = kb::lane_value(wexcl, wv);
+    const float p0 = kb::wave_prev_lane(sc[CPT - 1]) + woff;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const float pm1 = k == 0 ? p0 : sc[k - 1] + woff;
+      const float nt = term[k] * diag[k] + pp[k] * (pm1 + (A - (le[k] + __shfl(wexcl, wend[k], 64)))) +
+                       tpar[k] * edge[k];
+      if (a.v0) {
+        v[k] = rh[k] + nt;
+        term[k] = v[k];
+      } else {
+        term[k] = nt;
+        v[k] += nt;
+      }
+    }
+  };
+  {
+    int n = 0;
+    for (; n + 2 <= a.n_terms; n += 2) {
+      neumann_term(L0, L2, wA);
+      neumann_term(L1, L3, wB);
+    }
+    if (n < a.n_terms) neumann_term(L0, L2, wA);
+  }
+  // column gradient p' (A - subtree(v pcoef)), in the next parity's buffers
+  float colg[CPT];
+  {
+    const int n = a.n_terms;
+    float* Pb = (n & 1) ? L3 : L2;
+    float* wt = (n & 1) ? wB : wA;
+    float u[CPT], sc[CPT], pm1[CPT], rest[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) u[k] = v[k] * pcoef[k];
+    kb::local_scan_publish<NT, CPT>(sc, u, Pb, wt);
+    __syncthreads();
+    kb::subtree_terms<NT, CPT>(sc, Pb, wt, endm1, wend, pm1, rest);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) colg[k] = okp[k] ? pp[k] * (pm1[k] + rest[k]) : 0.0f;
+  }
+  // outputs in column order, four rows at a time through L0..L3
+  float* const outs[8] = {a.v, a.aw0, a.aw1, a.aw2, a.aw3, a.aw4, a.aw345, a.col_rows};
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    __syncthreads();  // the previous readers of L0..L3 are done
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int o = 4 * half + r;
+      float x[CPT];
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        if (o == 0) x[k] = v[k];
+        else if (o == 7) x[k] = colg[k];
+        else if (o == 6) x[k] = v[k] * (q[3][k] + q[4][k] + q[5][k]);
+        else x[k] = v[k] * q[o - 1][k];
+      }
+      kb::lds_store_own<CPT>(L0 + r * LD, x);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float* dst = outs[4 * half + r] + ob;
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) {
+        const int sc = tid + j * NT;
+        if (sc < S) dst[sc] = L0[r * LD + t.ppos[sc]];
+      }
+    }
+  }
+  if (a.relres) {
+    float ln = 0.0f, lv = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      ln += term[k] * term[k];
+      lv += v[k] * v[k];
+    }
+    const float n2 = block_sum(ln, wA);
+    const float v2 = block_sum(lv, wB);
+    if (tid == 0) {
+      const float tiny = 1.17549435e-38f;
+      const float den = fmaxf(sqrtf(v2), tiny);
+      a.relres[w] = a.n_terms > 0 ? sqrtf(n2) / den : 0.0f;
+    }
+  }
+}
+
 // ---- cross-wave split adjoint ----------------------------------------------------------------
 
 template <typename T>
@@ -1598,6 +1921,22 @@ int launch_wave_step(const kbo::OpsTree& t, const kbo::WsArgs<T>& a, int W, size
   return 0;
 }
 
+// float32 rows of the per-call wave backward run the preorder-ownership kernel
+template <typename T, int CPT>
+int launch_wave_bwd(const kbo::OpsTree& t, const kbo::WbArgs<T>& a, int W, size_t lds, hipStream_t st) {
+  if constexpr (std::is_same_v<T, float>) {
+    const size_t lds_pre = (size_t)4 * (kbo::NT * CPT + 64) * sizeof(float);
+    auto k = kbo::wave_bwd_pre_kernel<CPT>;
+    if (int rc = set_lds(k, lds_pre)) return rc;
+    hipLaunchKernelGGL(k, dim3(W), dim3(kbo::NT), lds_pre, st, t, a);
+    return 0;
+  }
+  auto k = kbo::wave_bwd_kernel<T, CPT>;
+  if (int rc = set_lds(k, lds)) return rc;
+  hipLaunchKernelGGL(k, dim3(W), dim3(kbo::NT), lds, st, t, a);
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1726,9 +2065,7 @@ int kb_wave_backward(const kb_tree* tr, const kb_wave_bwd_io* io, void* stream) 
                      (const T*)io->col_log_probs, io->item_idx, io->leaf_state, (const T*)io->leaf_logp,
                      (const T*)io->leaf_term, (T*)io->v, (T*)io->aw0, (T*)io->aw1, (T*)io->aw2, (T*)io->aw345,
                      (T*)io->aw3, (T*)io->aw4, (T*)io->col_rows, io->relres};
-    auto k = kbo::wave_bwd_kernel<T, CPT>;
-    if (int rc = set_lds(k, lds)) return rc;
-    hipLaunchKernelGGL(k, dim3(io->W), dim3(kbo::NT), lds, st_of(stream), t, a);
+    if (int rc = launch_wave_bwd<T, CPT>(t, a, io->W, lds, st_of(stream))) return rc;
   });
   KBO_HIP(hipGetLastError());
   return 0;

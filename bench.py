@@ -66,6 +66,8 @@ def parse():
     ap.add_argument("--no-per-call", action="store_true", help="skip the per-call (drop-in) timings")
     ap.add_argument("--no-dedup-off", action="store_true", help="skip the KB_DEDUP=0 timing")
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--hvp-layout", choices=("both", "levels"), default="both",
+                    help="--workload hvp: time the size waves and the level waves, or the level waves only")
     ap.add_argument("--workload", choices=("solve", "glue", "hvp"), default="solve",
                     help="solve: whole-pass driver (the metric); glue: only the per-call drop-in timings; "
                          "hvp: exact Hessian-vector products of the config-5 Newton-CG setup")
@@ -279,7 +281,9 @@ def bench_hvp(args, static, theta, cw, summ, static_levels) -> None:
 
         return _time_host(step, args.warmup, args.steps), cache_ms
 
-    ms_size, cache_size = timed(static)
+    ms_size = cache_size = None
+    if args.hvp_layout == "both":
+        ms_size, cache_size = timed(static)
     ms, cache_ms = timed(static_levels)
     print(json.dumps({
         "metric": "exact Hessian-vector product ms (config 5: per-species theta, forward tangent + tangent adjoint)",
@@ -290,7 +294,8 @@ def bench_hvp(args, static, theta, cw, summ, static_levels) -> None:
                                 f"dependency level ({len(static_levels.wave_layout['wave_metas'])} waves)"),
                    "S": summ["S"], "C": summ["C"], "point_cache_ms": round(cache_ms, 3)},
         "ms_per_newton_cg_step_50_hvps": round(50 * ms, 2),
-        "size_waves": {"n_waves": summ["n_waves"], "ms": round(ms_size, 4), "point_cache_ms": round(cache_size, 3)},
+        "size_waves": None if ms_size is None else {"n_waves": summ["n_waves"], "ms": round(ms_size, 4),
+                                                    "point_cache_ms": round(cache_size, 3)},
     }))
 
 

@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "kb_ops_common.hpp"
 
@@ -293,6 +294,263 @@ __global__ __launch_bounds__(NT) void wso_kernel(OpsTree t, WsoArgs<T> a) {
   }
 }
 
+// float32 rows at preorder ownership (thread t owns positions t*CPT + k, as
+// the forward and backward row kernels), computed in float32 as the
+// reference's Triton kernel computes it: the two root-path sums from one
+// pair of preorder / postorder scans, the two subtree sums from one pair of
+// published wavefront-local scans, the outputs written back in column order
+// through LDS.  Same mathematics as wso_kernel.
+template <int CPT>
+__global__ __launch_bounds__(NT) void wso_pre_kernel(OpsTree t, WsoArgs<float> a) {
+  constexpr int MAXS = NT * CPT;
+  constexpr int LD = MAXS + 64;  // [MAXS] is the padding slot, kept at 0
+  constexpr int ZERO = MAXS;
+  constexpr int SEG = 64 * CPT;  // postorder slots per wavefront
+  constexpr float LN2F = 0.69314718055994531f;
+  extern __shared__ __align__(16) unsigned char smraw[];
+  float* Lr = reinterpret_cast<float*>(smraw);  // 8 rows of LD
+  auto row = [&](int j) { return Lr + (size_t)j * LD; };
+  __shared__ float wA[2 * NW], wB[2 * NW];
+  const int S = t.S;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const float NI = -__builtin_inff();
+  const int w = blockIdx.x;
+  const long long grow = a.ws + w;
+  const long long item = a.item[grow];
+  const size_t cb = (size_t)(item * a.cstride);
+  const size_t lb = (size_t)item * S;
+  const size_t rb = (size_t)grow * S;
+  const size_t wb = (size_t)w * S;
+  const float rm = a.rowmax[grow];
+  const float rms = rm == NI ? 0.0f : rm;
+  const long long lstate = a.use_leaf ? a.leaf_state[grow] : -1;
+  // Pi, dPi, Pibar, dPibar and v to their preorder positions (rows 0..4)
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int sc = tid + j * NT;
+    if (sc < S) {
+      const int p = t.ppos[sc];
+      row(0)[p] = a.Pi[rb + sc];
+      row(1)[p] = a.dPi[rb + sc];
+      row(2)[p] = a.Pb[rb + sc];
+      row(3)[p] = a.dPb[rb + sc];
+      row(4)[p] = a.v[wb + sc];
+    }
+  }
+  if (tid < 64)
+    for (int j = 0; j < 8; ++j) row(j)[MAXS + tid] = 0.0f;
+  int colk[CPT], c1p[CPT], c2p[CPT], endm1[CPT], wend[CPT], qp[CPT], nex[CPT];
+  bool okp[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int i = kb::own_pos_c<NT, CPT>(k);
+    okp[k] = i < S;
+    colk[k] = okp[k] ? t.pcol[i] : 0;
+    c1p[k] = okp[k] ? t.pc1[i] : -1;
+    c2p[k] = okp[k] ? t.pc2[i] : -1;
+    endm1[k] = okp[k] ? t.pend[colk[k]] - 1 : ZERO;
+    wend[k] = endm1[k] < ZERO ? endm1[k] / SEG : 0;
+    qp[k] = okp[k] ? t.ppost[i] : ZERO;
+    nex[k] = okp[k] ? t.pnex[i] : 0;
+  }
+  {
+    // row 7 collects the child-edge terms, written by the parents' owners
+    // after the scans below: 0 where a position has no parent
+    float zero[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) zero[k] = 0.0f;
+    kb::lds_store_own<CPT>(row(7), zero);
+  }
+  __syncthreads();
+  float piv[CPT], dpiv[CPT], pbv[CPT], dpbv[CPT], vv[CPT];
+  kb::lds_load_own<CPT>(row(0), piv);
+  kb::lds_load_own<CPT>(row(1), dpiv);
+  kb::lds_load_own<CPT>(row(2), pbv);
+  kb::lds_load_own<CPT>(row(3), dpbv);
+  kb::lds_load_own<CPT>(row(4), vv);
+  // p' = 2^(Pi + col - rowmax), dp' = ln2 p' dPi and their root-path sums:
+  // both preorder scans in registers, rows 5 / 6 hold p' / dp' for the
+  // postorder reads, rows 2 / 3 (read above at own positions only) the
+  // exclusive postorder scans
+  float pp[CPT], dpp[CPT], sa[CPT], sb[CPT], ta = 0.0f, tb = 0.0f;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    pp[k] = okp[k] ? exp2f(piv[k] + (a.use_col ? a.col[colk[k]] : 0.0f) - rms) : 0.0f;
+    dpp[k] = okp[k] ? LN2F * pp[k] * dpiv[k] : 0.0f;
+    ta += pp[k];
+    tb += dpp[k];
+    sa[k] = ta;
+    sb[k] = tb;
+  }
+  const float wa = kb::wave_scan_incl(ta), wb2 = kb::wave_scan_incl(tb);
+  kb::lds_store_own<CPT>(row(5), pp);
+  kb::lds_store_own<CPT>(row(6), dpp);
+  if (lane == 63) {
+    wA[wv] = wa;
+    wA[NW + wv] = wb2;
+  }
+  __syncthreads();
+  float anc[CPT], danc[CPT], p1[CPT], p2[CPT], dp1[CPT], dp2[CPT], rowsum, drowsum;
+  {
+    const float tpa = kb::lds_wave_values<NW>(wA, lane, 0.0f);
+    const float tpb = kb::lds_wave_values<NW>(wA + NW, lane, 0.0f);
+    float ya[CPT], yb[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      ya[k] = row(5)[qp[k]];
+      yb[k] = row(6)[qp[k]];
+      p1[k] = c1p[k] >= 0 ? row(0)[c1p[k]] : NI;
+      p2[k] = c2p[k] >= 0 ? row(0)[c2p[k]] : NI;
+      dp1[k] = c1p[k] >= 0 ? row(1)[c1p[k]] : 0.0f;
+      dp2[k] = c2p[k] >= 0 ? row(1)[c2p[k]] : 0.0f;
+    }
+    const float ipa = kb::wave_scan_first<NW>(tpa), ipb = kb::wave_scan_first<NW>(tpb);
+    rowsum = kb::lane_value(ipa, NW - 1);
+    drowsum = kb::lane_value(ipb, NW - 1);
+    const float offa = kb::lane_value(ipa - tpa, wv) + (wa - ta);
+    const float offb = kb::lane_value(ipb - tpb, wv) + (wb2 - tb);
+    float qa[CPT], qb[CPT], ua = 0.0f, ub = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      qa[k] = ua;
+      qb[k] = ub;
+      ua += ya[k];
+      ub += yb[k];
+    }
+    const float xa = kb::wave_scan_incl(ua), xb = kb::wave_scan_incl(ub);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      qa[k] += xa - ua;
+      qb[k] += xb - ub;
+    }
+    kb::lds_store_own<CPT>(row(2), qa);
+    kb::lds_store_own<CPT>(row(3), qb);
+    if (lane == 63) {
+      wB[wv] = xa;
+      wB[NW + wv] = xb;
+    }
+    __syncthreads();
+    const float tqa = kb::lds_wave_values<NW>(wB, lane, 0.0f), tqb = kb::lds_wave_values<NW>(wB + NW, lane, 0.0f);
+    const float eqa = kb::wave_scan_first<NW>(tqa) - tqa, eqb = kb::wave_scan_first<NW>(tqb) - tqb;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int n = nex[k];
+      anc[k] = (sa[k] + offa) - (row(2)[n] + __shfl(eqa, n / SEG, 64));
+      danc[k] = (sb[k] + offb) - (row(3)[n] + __shfl(eqb, n / SEG, 64));
+    }
+  }
+  // per position: the second-order bucket terms, the child-edge terms (into
+  // row 7 at the child positions) and u = v pc, du = v dpc
+  float da[6][CPT], dself[CPT], u[CPT], du[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+#pragma unroll
+    for (int j = 0; j < 6; ++j) da[j][k] = 0.0f;
+    dself[k] = u[k] = du[k] = 0.0f;
+    if (okp[k]) {
+      const int s = colk[k];
+      const size_t ci = cb + s;
+      const float denom = rowsum - anc[k];
+      const float ddenom = drowsum - danc[k];
+      const float invd = denom > 0.0f ? 1.0f / denom : 0.0f;
+      const float pi = piv[k], dpi = dpiv[k];
+      const bool hit = lstate == s;
+      float tk[6], dtk[6];
+      tk[0] = a.DL[ci] + pi;
+      dtk[0] = a.dDL[ci] + dpi;
+      tk[1] = pi + a.Ebar[ci];
+      dtk[1] = dpi + a.dEbar[ci];
+      tk[2] = pbv[k] + a.E[ci];
+      dtk[2] = dpbv[k] + a.dE[ci];
+      tk[3] = a.SL1[ci] + p1[k];
+      dtk[3] = a.dSL1[ci] + dp1[k];
+      tk[4] = a.SL2[ci] + p2[k];
+      dtk[4] = a.dSL2[ci] + dp2[k];
+      tk[5] = hit ? a.leaf_logp[lb + s] : NI;
+      dtk[5] = hit ? a.dleaf_logp[lb + s] : 0.0f;
+      float m = tk[0];
+#pragma unroll
+      for (int j = 1; j < 6; ++j) m = fmaxf(m, tk[j]);
+      const float ms = m == NI ? 0.0f : m;
+      float wk[6], tot = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 6; ++j) {
+        wk[j] = exp2f(tk[j] - ms);
+        tot += wk[j];
+      }
+      const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
+      float dlse = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 6; ++j) {
+        wk[j] *= inv;
+        if (wk[j] != 0.0f) dlse += wk[j] * dtk[j];
+      }
+      float dw[6];
+#pragma unroll
+      for (int j = 0; j < 6; ++j) dw[j] = wk[j] != 0.0f ? LN2F * wk[j] * (dtk[j] - dlse) : 0.0f;
+      float wL = 1.0f, dwL = 0.0f;
+      if (a.dts) {
+        const float dr = a.dts[wb + s];
+        const float dl = tot > 0.0f ? log2f(tot) + m : NI;
+        const float pm = fmaxf(dl, dr);
+        const float pms = pm == NI ? 0.0f : pm;
+        const float pnew = log2f(exp2f(dl - pms) + exp2f(dr - pms)) + pm;
+        wL = dl != NI ? exp2f(dl - pnew) : 0.0f;
+        dwL = (dr != NI && dl != NI) ? LN2F * wL * (1.0f - wL) * (dlse - a.ddts[wb + s]) : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < 6; ++j) da[j][k] = vv[k] * (dwL * wk[j] + wL * dw[j]);
+      if (c1p[k] >= 0) row(7)[c1p[k]] = da[3][k];
+      if (c2p[k] >= 0) row(7)[c2p[k]] = da[4][k];
+      const float pc = wL * wk[2] * invd;
+      const float dpc = (dwL * wk[2] + wL * dw[2]) * invd - pc * invd * ddenom;
+      u[k] = vv[k] * pc;
+      du[k] = vv[k] * dpc;
+      dself[k] = da[0][k] + da[1][k];
+    }
+  }
+  // subtree sums of u and du: wavefront-local scans published in rows 5 / 6
+  // (their postorder reads finished before the second barrier above)
+  float scu[CPT], scd[CPT];
+  kb::local_scan_publish<NT, CPT>(scu, u, row(5), wA);
+  kb::local_scan_publish<NT, CPT>(scd, du, row(6), wA + NW);
+  __syncthreads();  // also publishes the child-edge terms in row 7
+  float pmu[CPT], rsu[CPT], pmd[CPT], rsd[CPT], z[CPT];
+  kb::subtree_terms<NT, CPT>(scu, row(5), wA, endm1, wend, pmu, rsu);
+  kb::subtree_terms<NT, CPT>(scd, row(6), wA + NW, endm1, wend, pmd, rsd);
+  kb::lds_load_own<CPT>(row(7), z);
+  // the output row: dself + dp' (A - sub u) + p' (dA - sub du) + the child-edge
+  // term from the parent (+ rhs)
+  float o[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) o[k] = okp[k] ? dself[k] + dpp[k] * (pmu[k] + rsu[k]) + pp[k] * (pmd[k] + rsd[k]) + z[k] : 0.0f;
+  // outputs in column order through rows 0..6, once every thread has read
+  // rows 5 / 6 (the subtree terms) and its own entries of row 7
+  __syncthreads();
+  kb::lds_store_own<CPT>(row(0), o);
+#pragma unroll
+  for (int j = 0; j < 6; ++j) {
+    float x[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) x[k] = j < 5 ? da[j][k] : da[3][k] + da[4][k] + da[5][k];
+    kb::lds_store_own<CPT>(row(1 + j), x);
+  }
+  __syncthreads();
+  float* const outs[7] = {a.out, a.aw0, a.aw1, a.aw2, a.aw3, a.aw4, a.aw345};
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int sc = tid + j * NT;
+    if (sc < S) {
+      const int p = t.ppos[sc];
+      float ov = row(0)[p];
+      if (a.rhs) ov += a.rhs[rb + sc];
+      outs[0][wb + sc] = ov;
+#pragma unroll
+      for (int r = 1; r < 7; ++r) outs[r][wb + sc] = row(r)[p];
+    }
+  }
+}
+
 // ---- split-term backward and its Pibar tree VJP --------------------------------------------
 
 template <typename T>
@@ -447,6 +705,27 @@ __global__ __launch_bounds__(NT) void dso_tree_kernel(OpsTree t, DsoArgs<T> a) {
 
 using namespace kbo_host;
 
+namespace {
+
+// float32 rows of up to 4096 states run the preorder-ownership kernel, the
+// others the float64 one
+template <typename T, int CPT>
+int launch_wso(const kbo::OpsTree& t, const kbo::WsoArgs<T>& a, int W, size_t lds, hipStream_t st) {
+  if constexpr (std::is_same_v<T, float> && CPT <= 4) {  // (eight LDS rows: up to 4096 positions)
+    const size_t lds_pre = (size_t)8 * (kbo::NT * CPT + 64) * sizeof(float);
+    auto k = kbo::wso_pre_kernel<CPT>;
+    if (int rc = set_lds(k, lds_pre)) return rc;
+    hipLaunchKernelGGL(k, dim3(W), dim3(kbo::NT), lds_pre, st, t, a);
+    return 0;
+  }
+  auto k = kbo::wso_kernel<T, CPT>;
+  if (int rc = set_lds(k, lds)) return rc;
+  hipLaunchKernelGGL(k, dim3(W), dim3(kbo::NT), lds, st, t, a);
+  return 0;
+}
+
+}  // namespace
+
 extern "C" {
 
 int kb_estep_backward_so(const kb_tree* tr, const kb_estep_so_io* io, void* stream) {
@@ -496,8 +775,7 @@ int kb_wave_backward_so(const kb_tree* tr, const kb_wave_so_io* io, void* stream
                       (const T*)io->dleaf_logp, (const T*)io->dts, (const T*)io->d_dts, (const T*)io->d_rhs,
                       (T*)io->d_out, (T*)io->d_aw0, (T*)io->d_aw1, (T*)io->d_aw2, (T*)io->d_aw345,
                       (T*)io->d_aw3, (T*)io->d_aw4};
-    if (int rc = set_lds(kbo::wso_kernel<T, CPT>, lds)) return rc;
-    hipLaunchKernelGGL((kbo::wso_kernel<T, CPT>), dim3(io->W), dim3(kbo::NT), lds, st_of(stream), t, a);
+    if (int rc = launch_wso<T, CPT>(t, a, io->W, lds, st_of(stream))) return rc;
   });
   KBO_HIP(hipGetLastError());
   return 0;

@@ -319,6 +319,18 @@ int kb_rows_scatter_add(int32_t dtype, int32_t S, int64_t n, const void* src, co
  */
 int kb_rows_sum_into(int32_t dtype, int32_t S, int64_t n, const void* src, void* dst, double* work, void* stream);
 
+/*
+ * Column sums of m <= 8 row blocks in one launch (two above 64 rows):
+ * out[j * S + s] = sum over r < n of (a[j][r * S + s] + b[j][r * S + s]),
+ * b (or b[j]) null for a single addend, in row order with float64 partial
+ * sums (work: m * ceil(n / 64) * S doubles, unused for n <= 64).  a and b
+ * are host arrays of device pointers.  No reference kernel: it replaces the
+ * glue's per-wave torch reductions of the aw tensors
+ * (kbench/api/_implicit_grad.py:288-296, one .sum(0) per tensor).
+ */
+int kb_rows_sum_multi(int32_t dtype, int32_t S, int64_t n, int32_t m, const void* const* a, const void* const* b,
+                      void* out, double* work, void* stream);
+
 /* ---- forward tangents (JVP) of the forward maps, for the Newton HVP path ---- */
 
 /*

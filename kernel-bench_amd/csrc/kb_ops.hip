@@ -1672,6 +1672,46 @@ __global__ __launch_bounds__(256) void rows_sum_single(int S, long long n, const
   dst[s] = (T)((double)dst[s] + acc);
 }
 
+// Column sums of up to 8 row blocks in one launch (grid z = block): row chunk
+// y of block j, summed in row order in float64; one chunk writes the result,
+// more write partials that rows_sum_multi_stage2 adds in chunk order.
+struct RsmArgs {
+  int S, m, chunks;
+  long long n;
+  const void* a[8];
+  const void* b[8];  // optional second addend of each block
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void rows_sum_multi_stage1(RsmArgs p, double* work, T* out) {
+  const int s = blockIdx.x * 256 + threadIdx.x;
+  if (s >= p.S) return;
+  const int j = blockIdx.z, c = blockIdx.y;
+  const T* A = static_cast<const T*>(p.a[j]);
+  const T* B = static_cast<const T*>(p.b[j]);
+  const long long r0 = (long long)c * SUM_CHUNK, r1 = min(p.n, r0 + SUM_CHUNK);
+  double acc = 0.0;
+  for (long long r = r0; r < r1; ++r) {
+    double x = (double)A[(size_t)r * p.S + s];
+    if (B) x += (double)B[(size_t)r * p.S + s];
+    acc += x;
+  }
+  if (p.chunks == 1)
+    out[(size_t)j * p.S + s] = (T)acc;
+  else
+    work[((size_t)j * p.chunks + c) * p.S + s] = acc;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void rows_sum_multi_stage2(RsmArgs p, const double* work, T* out) {
+  const int s = blockIdx.x * 256 + threadIdx.x;
+  if (s >= p.S) return;
+  const int j = blockIdx.z;
+  double acc = 0.0;
+  for (int c = 0; c < p.chunks; ++c) acc += work[((size_t)j * p.chunks + c) * p.S + s];
+  out[(size_t)j * p.S + s] = (T)acc;
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void rows_sum_stage2(int S, int n_chunks, const double* work, T* dst) {
   const int s = blockIdx.x * 256 + threadIdx.x;
@@ -2135,6 +2175,37 @@ int kb_rows_scatter_add(int32_t dtype, int32_t S, int64_t n, const void* src, co
   else
     hipLaunchKernelGGL(kbo::scatter_add_kernel<float>, g, dim3(256), 0, st_of(stream), S, (long long)n,
                        (const float*)src, order, keys_sorted, (float*)dst, (long long)dst_stride);
+  KBO_HIP(hipGetLastError());
+  return 0;
+}
+
+int kb_rows_sum_multi(int32_t dtype, int32_t S, int64_t n, int32_t m, const void* const* a, const void* const* b,
+                      void* out, double* work, void* stream) {
+  if (S <= 0 || m <= 0) return 0;
+  if (m > 8) return kb::set_error(KB_ERR_ARG, "at most 8 row blocks per call (m=%d)", m);
+  if (!a || !out) return kb::set_error(KB_ERR_ARG, "null argument");
+  if (int rc = dtype_ok(dtype)) return rc;
+  kbo::RsmArgs p{};
+  p.S = S;
+  p.m = m;
+  p.n = n;
+  p.chunks = (int)std::max<int64_t>(1, (n + kbo::SUM_CHUNK - 1) / kbo::SUM_CHUNK);
+  for (int j = 0; j < m; ++j) {
+    if (!a[j] && n > 0) return kb::set_error(KB_ERR_ARG, "row block %d is null", j);
+    p.a[j] = a[j];
+    p.b[j] = b ? b[j] : nullptr;
+  }
+  if (p.chunks > 1 && !work) return kb::set_error(KB_ERR_ARG, "work is required for more than 64 rows");
+  const dim3 g1((S + 255) / 256, p.chunks, m), g2((S + 255) / 256, 1, m);
+  if (dtype == KB_F64) {
+    hipLaunchKernelGGL(kbo::rows_sum_multi_stage1<double>, g1, dim3(256), 0, st_of(stream), p, work, (double*)out);
+    if (p.chunks > 1)
+      hipLaunchKernelGGL(kbo::rows_sum_multi_stage2<double>, g2, dim3(256), 0, st_of(stream), p, work, (double*)out);
+  } else {
+    hipLaunchKernelGGL(kbo::rows_sum_multi_stage1<float>, g1, dim3(256), 0, st_of(stream), p, work, (float*)out);
+    if (p.chunks > 1)
+      hipLaunchKernelGGL(kbo::rows_sum_multi_stage2<float>, g2, dim3(256), 0, st_of(stream), p, work, (float*)out);
+  }
   KBO_HIP(hipGetLastError());
   return 0;
 }

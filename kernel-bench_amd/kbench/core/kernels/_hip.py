@@ -228,6 +228,27 @@ def scatter_add_rows(dst: torch.Tensor, src: torch.Tensor, keys, *, row_stride=N
                                     ptr(dst), stride, stream(src.device)))
 
 
+def rows_sum_multi(blocks) -> torch.Tensor:
+    """[m, S] column sums of up to 8 [n, S] row blocks, in row order with float64 partial sums.
+
+    Each entry of ``blocks`` is a tensor or a pair of tensors (summed elementwise in the
+    reduction); all share n, S, dtype and device.
+    """
+    import ctypes as ct
+
+    pairs = [b if isinstance(b, (tuple, list)) else (b, None) for b in blocks]
+    first = pairs[0][0]
+    n, S = int(first.shape[0]), int(first.shape[1])
+    m = len(pairs)
+    out = torch.empty((m, S), device=first.device, dtype=first.dtype)
+    chunks = (n + 63) // 64
+    work = torch.empty((m * chunks * S if chunks > 1 else 1,), device=first.device, dtype=torch.float64)
+    a = (ct.c_void_p * m)(*[ptr(x) for x, _ in pairs])
+    b = (ct.c_void_p * m)(*[ptr(y) if y is not None else None for _, y in pairs])
+    check(lib().kb_rows_sum_multi(dtype_code(first.dtype), S, n, m, a, b, ptr(out), ptr(work), stream(first.device)))
+    return out
+
+
 def sum_rows_into(dst: torch.Tensor, src: torch.Tensor) -> None:
     """dst += src.sum(0), in row order with float64 partial sums."""
     n = int(src.shape[0])

@@ -272,7 +272,7 @@ class HvpPlan:
                 max_ancestor_depth=p.topo[3], pibar_row_max=prm, item_idx=p.item_idx, item_indexed_consts=True,
                 grad_col_log_probs=dacc.col, use_col_weights=False, self_loop_solver=so.self_loop_solver,
                 **p.levels)
-            p._fold_buckets([x + y for x, y in zip(so_aw, lin_aw)], targets, w, G)
+            p._fold_buckets(list(zip(so_aw, lin_aw)), targets, w, G)
             if w.split:
                 lsp = w.lsp if w.lsp is not None else w.sl.new_zeros((int(w.sl.numel()),), dtype=Pi.dtype)
                 ud, A, side_on, _, _ = p.k.dts_cross_backward_accum_fused(

@@ -44,6 +44,8 @@ from kbench.api.solver_options import SolverOptions
 from kbench.core.parameters.extract_parameters import (as_item_param, as_item_state, extract_parameters_uniform,
                                                        extract_parameters_weighted_cols)
 
+from kbench.core.kernels import _hip as H
+
 from . import kernels as K
 from .krylov import bicgstab
 
@@ -267,9 +269,12 @@ class SolvePlan:
         return acc
 
     def _fold_buckets(self, aw, targets, w, G):
-        """Add the wave's per-element contributions (aw0, aw1, aw2, aw345, aw3, aw4) into the cotangents."""
+        """Add the wave's per-element contributions (aw0, aw1, aw2, aw345, aw3, aw4) into the cotangents.
+
+        An entry of ``aw`` may be a pair of tensors whose sum is the contribution.
+        """
         if G == 1:
-            col_sums = torch.stack(aw).sum(dim=1)            # [6, S]: one reduction for all buckets
+            col_sums = H.rows_sum_multi(aw)                  # [6, S]: one reduction for all buckets
             for acc, ks in targets:
                 s = col_sums[ks[0]] if len(ks) == 1 else col_sums[ks[0]] + col_sums[ks[1]]
                 if acc.ndim == 2 and int(acc.shape[1]) == 1:
@@ -277,6 +282,7 @@ class SolvePlan:
                 else:
                     acc.view(-1, acc.shape[-1])[0] += s.to(acc.dtype)
             return
+        aw = [x[0] + x[1] if isinstance(x, (tuple, list)) else x for x in aw]
         items = self.item_idx[w.ws: w.ws + w.W]
         for acc, ks in targets:
             contrib = aw[ks[0]] if len(ks) == 1 else aw[ks[0]] + aw[ks[1]]

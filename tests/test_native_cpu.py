@@ -30,7 +30,8 @@ def test_headers_declare_entry_points():
     names = _declared()
     for must in ("kb_plan_create", "kb_forward", "kb_backward", "kb_tree_create", "kb_wave_step",
                  "kb_dts_forward", "kb_wave_backward", "kb_dts_cross_backward", "kb_pibar_vjp", "kb_estep",
-                 "kb_estep_vjp", "kb_active_mask", "kb_leaf_init", "kb_rows_scatter_add", "kb_rows_sum_into"):
+                 "kb_estep_vjp", "kb_active_mask", "kb_leaf_init", "kb_rows_scatter_add", "kb_rows_sum_into",
+                 "kb_rows_sum_multi"):
         assert must in names
 
 
@@ -46,6 +47,9 @@ def test_host_only_entry_points():
     assert lib.kb_ops_max_states(0) == 8192
     assert 4096 <= lib.kb_ops_max_states(1) < 8192
     assert isinstance(lib.kb_last_error(), bytes)
+    # argument checks that precede any device call
+    assert lib.kb_rows_sum_multi(0, 4, 2, 9, None, None, None, None, None) != 0
+    assert b"at most 8" in lib.kb_last_error()
 
 
 def test_wrappers_refuse_host_tensors():

@@ -480,3 +480,26 @@ def test_e_step_autograd_matches_oracle(dt, use_col):
         e = _rel(_np(a).reshape(np.shape(b)), b)
         print(f"  {name}: rel={e:.3e}")
         assert e <= TOL[dt], name
+
+
+@pytest.mark.parametrize("n", [1, 64, 300])
+@pytest.mark.parametrize("dt", [torch.float32, torch.float64])
+def test_rows_sum_multi_matches_float64_column_sums(n, dt):
+    """kb_rows_sum_multi: column sums of single and paired row blocks, against float64 sums, and run
+    twice bitwise (fixed order)."""
+    from kbench.core.kernels import _hip as H
+
+    g = torch.Generator(device="cpu").manual_seed(n)
+    S = 37
+    xs = [torch.randn((n, S), generator=g, dtype=torch.float64).to(device="cuda", dtype=dt) for _ in range(7)]
+    blocks = [xs[0], (xs[1], xs[2]), xs[3], (xs[4], xs[5]), xs[6]]
+    out = H.rows_sum_multi(blocks)
+    again = H.rows_sum_multi(blocks)
+    torch.cuda.synchronize()
+    assert out.shape == (5, S) and out.dtype == dt
+    assert torch.equal(out, again)
+    ref = torch.stack([(b[0].double() + b[1].double()) if isinstance(b, tuple) else b.double() for b in blocks])
+    ref = ref.sum(dim=1)
+    err = float((out.double() - ref).abs().max() / ref.abs().max())
+    print(f"[rows-sum-multi] n={n} dtype={dt} rel={err:.3e}")
+    assert err <= (1e-6 if dt == torch.float32 else 1e-13)

@@ -465,24 +465,26 @@ __global__ __launch_bounds__(NT) void wave_step_kernel(OpsTree t, WsArgs<T> a) {
   if (threadIdx.x == 0) a.rowmax[grow] = M2;
 }
 
-// Chains of float sweeps: the same sweeps with the row's positions in
-// preorder, thread t owning positions t*CPT + k.  A sweep's ancestor path sums are a register scan
-// over preorder positions minus an exclusive scan over postorder slots,
-// ps(i) = Pre(i) - PostEx(tin(i) - i), so a sweep takes three barriers (row
-// maximum, preorder totals, postorder totals) instead of the Euler-tour scan's
-// eight.  The arithmetic per position is the one-sweep formula above; the
-// row sums come in a different order, so results agree with it to rounding.
+// Sweep chains (n_sweeps > 1) of float32 rows in linear space, as the
+// whole-pass forward row kernel runs its sweeps: x = 2^(Pi - M) with a row
+// exponent M renormalised by an exact power of two every sweep, so a sweep is
+//   y' = a y + emc (rowsum - ps) + k1 y[c1] + k2 y[c2] + (leaf | dts) 2^-M
+// with a = 2^DL + 2^Ebar, emc = 2^(E + mt), k1 = 2^SL1, k2 = 2^SL2 formed
+// once per launch, and no exponential or logarithm inside the chain.  The
+// path sums come from an inclusive preorder scan and an exclusive postorder
+// scan (two barriers per sweep).  The outputs equal the log-space sweeps to
+// float32 rounding.
 template <int CPT>
-__global__ __launch_bounds__(NT) void wave_step_pre_kernel(OpsTree t, WsArgs<float> a) {
+__global__ __launch_bounds__(NT) void wave_step_lin_kernel(OpsTree t, WsArgs<float> a) {
   constexpr int MAXS = NT * CPT;
   constexpr int LD = MAXS + 64;
   constexpr int ZERO = MAXS;     // padding slot: 0 in X
   constexpr int SEG = 64 * CPT;  // postorder slots per wavefront
   extern __shared__ __align__(16) unsigned char smraw[];
-  float* R = reinterpret_cast<float*>(smraw);  // Pi at preorder positions: input, children, outputs
-  float* X = R + LD;                           // 2^(col + Pi - M) at preorder positions
+  float* X = reinterpret_cast<float*>(smraw);  // y of the sweep at preorder positions
   float* Q = X + LD;                           // exclusive postorder scan
-  __shared__ float wM[NW], wA[NW], wB[NW];
+  float* O = Q + LD;                           // the input row, then the outputs, at preorder positions
+  __shared__ float wP[NW], wQ[NW], wM[NW];
   const int S = t.S;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int w = blockIdx.x;
@@ -492,171 +494,178 @@ __global__ __launch_bounds__(NT) void wave_step_pre_kernel(OpsTree t, WsArgs<flo
   const size_t cb = (size_t)(item * a.cstride);
   const float* in = a.Pi_in + (size_t)(a.pi_ws + w) * S;
   const long long lstate = a.use_leaf ? a.leaf_state[grow] : -1;
-  // the input row, read by column (coalesced), to its preorder positions
 #pragma unroll
   for (int j = 0; j < CPT; ++j) {
     const int sc = tid + j * NT;
-    if (sc < S) R[t.ppos[sc]] = in[sc];
+    if (sc < S) O[t.ppos[sc]] = in[sc];
   }
-  if (tid < 64) X[MAXS + tid] = 0.0f;
-  // own positions: tables and the row's constants (read once for all sweeps)
+  if (tid < 64) {
+    X[MAXS + tid] = 0.0f;
+    Q[MAXS + tid] = 0.0f;
+  }
+  // own positions: tables, the linear constants, and the log2 terms of the outputs
   int c1p[CPT], c2p[CPT], nex[CPT], qp[CPT];
   bool okp[CPT];
-  float kmt[CPT], kDL[CPT], kEb[CPT], kE[CPT], kS1[CPT], kS2[CPT], klf[CPT], kd[CPT], kcol[CPT];
+  float ca[CPT], ce[CPT], ck1[CPT], ck2[CPT], cw[CPT], cwq[CPT], kmt[CPT], kcol[CPT], klf[CPT], kd[CPT];
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int i = kb::own_pos_c<NT, CPT>(k);
     okp[k] = i < S;
-    c1p[k] = c2p[k] = -1;
+    c1p[k] = c2p[k] = ZERO;
     nex[k] = 0;
     qp[k] = ZERO;
-    kmt[k] = kDL[k] = kEb[k] = kE[k] = kS1[k] = kS2[k] = kcol[k] = 0.0f;
+    ca[k] = ce[k] = ck1[k] = ck2[k] = kmt[k] = kcol[k] = 0.0f;
+    cw[k] = cwq[k] = a.use_col ? 0.0f : 1.0f;
     klf[k] = kd[k] = NI;
     if (okp[k]) {
       const int col = t.pcol[i];
       const size_t ci = cb + col;
-      c1p[k] = t.pc1[i];
-      c2p[k] = t.pc2[i];
+      const int c1 = t.pc1[i], c2 = t.pc2[i];
+      c1p[k] = c1 >= 0 ? c1 : ZERO;
+      c2p[k] = c2 >= 0 ? c2 : ZERO;
       nex[k] = t.pnex[i];
       qp[k] = t.ppost[i];
+      ca[k] = (float)(exp2((double)a.DL[ci]) + exp2((double)a.Ebar[ci]));
+      ce[k] = (float)exp2((double)a.E[ci] + (double)a.mt[ci]);
+      ck1[k] = c1 >= 0 ? (float)exp2((double)a.SL1[ci]) : 0.0f;
+      ck2[k] = c2 >= 0 ? (float)exp2((double)a.SL2[ci]) : 0.0f;
       kmt[k] = a.mt[ci];
-      kDL[k] = a.DL[ci];
-      kEb[k] = a.Ebar[ci];
-      kE[k] = a.E[ci];
-      kS1[k] = a.SL1[ci];
-      kS2[k] = a.SL2[ci];
+      if (a.use_col) {
+        kcol[k] = a.col[col];
+        cw[k] = exp2f(kcol[k]);
+        cwq[k] = exp2f(a.col[t.pcol[qp[k]]]);
+      }
       if (lstate == col) klf[k] = a.leaf_logp[(size_t)item * S + col];
       if (a.dts) kd[k] = a.dts[(size_t)w * S + col];
-      if (a.use_col) kcol[k] = a.col[col];
     }
   }
   __syncthreads();
   float pr[CPT];
-  kb::lds_load_own<CPT>(R, pr);
+  kb::lds_load_own<CPT>(O, pr);
+  float lm = NI;
 #pragma unroll
-  for (int k = 0; k < CPT; ++k)
+  for (int k = 0; k < CPT; ++k) {
     if (!okp[k]) pr[k] = NI;
-
-  // One path-sum pass over x (own positions, log2): M = max(col + x), the row
-  // sum and ps(i) of 2^(col + x - M); x is published in R for the child
-  // gathers (ch1, ch2), read before the third barrier.  Callers separate R's
-  // previous readers from this write by a barrier.
-  float ps[CPT], ch1[CPT], ch2[CPT], rowsum = 0.0f, M = NI;
-  auto pass = [&](const float (&x)[CPT]) {
-    float lm = NI;
+    lm = fmaxf(lm, pr[k]);
+  }
+  // linear space relative to the input's row maximum Ms
+  const float Ms = kb::fsafe(kb::block_max1<NT>(lm, wM));
+  float y[CPT], dl[CPT];
 #pragma unroll
-    for (int k = 0; k < CPT; ++k)
-      if (okp[k]) lm = fmaxf(lm, kcol[k] + x[k]);
-    kb::lds_store_own<CPT>(R, x);
-    M = kb::block_max1<NT>(lm, wM);  // barrier 1: also publishes R
-    const float Ms = M == NI ? 0.0f : M;
-    float y[CPT], sp[CPT], ta = 0.0f;
+  for (int k = 0; k < CPT; ++k) {
+    y[k] = okp[k] ? exp2f(pr[k] - Ms) : 0.0f;
+    dl[k] = (klf[k] != NI ? exp2f(klf[k] - Ms) : 0.0f) + (kd[k] != NI ? exp2f(kd[k] - Ms) : 0.0f);
+  }
+  int kexp = 0, kexp_prev = 0;
+  float ps[CPT], yprev[CPT], rowsum = 0.0f, tsum = 0.0f, f = 1.0f;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) yprev[k] = y[k];
+  for (int sweep = 0;; ++sweep) {
+    // phase A: publish y; inclusive (column-weighted) preorder scan in registers
+    float sp[CPT], ta = 0.0f;
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      y[k] = okp[k] ? exp2f(kcol[k] + x[k] - Ms) : 0.0f;
-      ta += y[k];
+      ta += cw[k] * y[k];
       sp[k] = ta;
     }
     const float wa = kb::wave_scan_incl(ta);
     kb::lds_store_own<CPT>(X, y);
-    if (lane == 63) wA[wv] = wa;
-    __syncthreads();  // barrier 2
-    const float tp = kb::lds_wave_values<NW>(wA, lane, 0.0f);
-    float yq[CPT];
+    if (lane == 63) wP[wv] = wa;
+    __syncthreads();
+    // phase B: row sum (renormalised by an exact power of two), the postorder
+    // values and children (read before the next barrier), exclusive postorder scan
+    const float tp = kb::lds_wave_values<NW>(wP, lane, 0.0f);
+    float yq[CPT], x1[CPT], x2[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       yq[k] = X[qp[k]];
-      ch1[k] = c1p[k] >= 0 ? R[c1p[k]] : NI;
-      ch2[k] = c2p[k] >= 0 ? R[c2p[k]] : NI;
+      x1[k] = X[c1p[k]];
+      x2[k] = X[c2p[k]];
     }
     const float ip = kb::wave_scan_first<NW>(tp);
-    rowsum = kb::lane_value(ip, NW - 1);
+    tsum = kb::lane_value(ip, NW - 1);
     const float offp = kb::lane_value(ip - tp, wv) + (wa - ta);
     float sq[CPT], tb = 0.0f;
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       sq[k] = tb;
-      tb += yq[k];
+      tb += cwq[k] * yq[k];
     }
     const float wb = kb::wave_scan_incl(tb);
 #pragma unroll
     for (int k = 0; k < CPT; ++k) sq[k] += wb - tb;
     kb::lds_store_own<CPT>(Q, sq);
-    if (lane == 63) wB[wv] = wb;
-    __syncthreads();  // barrier 3
-    const float tq = kb::lds_wave_values<NW>(wB, lane, 0.0f);
+    if (lane == 63) wQ[wv] = wb;
+    const int e = tsum > 0.0f ? __builtin_amdgcn_frexp_expf(tsum) : 0;
+    f = __builtin_amdgcn_ldexpf(1.0f, -e);
+    kexp += e;
+    rowsum = tsum * f;
+    __syncthreads();
+    // phase C: path sums ps(i) = Pre(i) - PostEx(tin(i) - i)
+    const float tq = kb::lds_wave_values<NW>(wQ, lane, 0.0f);
     const float eq = kb::wave_scan_first<NW>(tq) - tq;
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int n = nex[k];
       ps[k] = (sp[k] + offp) - (Q[n] + __shfl(eq, n / SEG, 64));
     }
-  };
-
-  __syncthreads();  // every thread has read its input positions from R
-  float res[CPT];
-  float ldiff = 0.0f;
-  for (int sweep = 0; sweep < a.n_sweeps; ++sweep) {
-    pass(pr);
-    ldiff = 0.0f;
+    if (sweep == a.n_sweeps) break;
+    if (sweep == a.n_sweeps - 1) {  // the row before the last sweep, for the residual
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) yprev[k] = y[k];
+      kexp_prev = kexp - e;
+    }
+    const float scale = __builtin_amdgcn_ldexpf(1.0f, -kexp);
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      res[k] = NI;
-      if (okp[k]) {
-        const float denom = rowsum - ps[k];
-        const float pibar_w = denom > 0.0f ? log2f(denom) + M + kmt[k] : NI;
-        const float pi_w = pr[k];
-        const float t0 = kDL[k] + pi_w;
-        const float t1 = pi_w + kEb[k];
-        const float t2 = pibar_w + kE[k];
-        const float t3 = kS1[k] + ch1[k];
-        const float t4 = kS2[k] + ch2[k];
-        const float t5 = klf[k];
-        float m = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, t5));
-        const float d = kd[k];
-        if (a.dts) m = fmaxf(m, d);
-        const float ms = m == NI ? 0.0f : m;
-        float sum = exp2f(t0 - ms) + exp2f(t1 - ms) + exp2f(t2 - ms) + exp2f(t3 - ms) + exp2f(t4 - ms) +
-                    exp2f(t5 - ms);
-        if (a.dts) sum += exp2f(d - ms);
-        res[k] = log2f(sum) + m;
-        if (res[k] != NI && pi_w != NI) ldiff = fmaxf(ldiff, fabsf(res[k] - pi_w));
-      }
+      float z = ca[k] * y[k];
+      z += ck1[k] * x1[k];
+      z += ck2[k] * x2[k];
+      z += ce[k] * fmaxf(tsum - ps[k], 0.0f);
+      y[k] = z * f + dl[k] * scale;
     }
-#pragma unroll
-    for (int k = 0; k < CPT; ++k) pr[k] = res[k];
   }
-  // outputs by column (coalesced): Pi_out, then the final Pibar and row max
-  kb::lds_store_own<CPT>(R, res);  // R's readers (the last children) finished before barrier 3
+  // ---- outputs: Pi, the residual of the last sweep, Pibar and the row max
+  const float M = Ms + (float)kexp;  // relative exponent of x = y f
+  float po[CPT], pb[CPT];
+  float ldiff = 0.0f, lmax = NI;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    po[k] = pb[k] = NI;
+    if (okp[k]) {
+      const float x = y[k] * f;
+      po[k] = x > 0.0f ? log2f(x) + M : NI;
+      const float prev = yprev[k] > 0.0f ? log2f(yprev[k]) + (Ms + (float)kexp_prev) : NI;
+      if (po[k] != NI && prev != NI) ldiff = fmaxf(ldiff, fabsf(po[k] - prev));
+      const float na = rowsum - ps[k] * f;
+      pb[k] = na > 0.0f ? log2f(na) + M + kmt[k] : NI;
+      lmax = fmaxf(lmax, kcol[k] + po[k]);
+    }
+  }
+  // O (the input) was last read before the first sweep's barrier; X's readers
+  // finished before the last pass's second barrier
+  kb::lds_store_own<CPT>(O, po);
+  kb::lds_store_own<CPT>(X, pb);
   __syncthreads();
   float* out = a.Pi_out + (size_t)grow * S;
+  float* pbo = a.store_final ? a.Pibar + (size_t)grow * S : nullptr;
 #pragma unroll
   for (int j = 0; j < CPT; ++j) {
     const int sc = tid + j * NT;
-    if (sc < S) out[sc] = R[t.ppos[sc]];
+    if (sc < S) {
+      const int i = t.ppos[sc];
+      out[sc] = O[i];
+      if (pbo) pbo[sc] = X[i];
+    }
   }
   if (a.resid) {
     const float md = kb::block_max1<NT>(ldiff, wM);
     if (tid == 0) a.resid[grow] = md;
   }
-  if (!a.store_final) return;
-  __syncthreads();  // the outputs' reads of R are done
-  pass(res);
-  float pb[CPT];
-#pragma unroll
-  for (int k = 0; k < CPT; ++k) {
-    const float denom = rowsum - ps[k];
-    pb[k] = (okp[k] && denom > 0.0f) ? log2f(denom) + M + kmt[k] : NI;
+  if (a.store_final) {
+    const float rmax = kb::block_max1<NT>(lmax, wP);
+    if (tid == 0) a.rowmax[grow] = rmax;
   }
-  kb::lds_store_own<CPT>(X, pb);  // X's readers finished before barrier 3
-  __syncthreads();
-  float* pbo = a.Pibar + (size_t)grow * S;
-#pragma unroll
-  for (int j = 0; j < CPT; ++j) {
-    const int sc = tid + j * NT;
-    if (sc < S) pbo[sc] = X[t.ppos[sc]];
-  }
-  if (tid == 0) a.rowmax[grow] = M;
 }
 
 template <typename T>
@@ -1939,19 +1948,19 @@ int estep_vjp_launch(const kb_tree* tr, const kb_estep_vjp_io* io, double* work,
 }  // namespace
 
 namespace {
-// Chains of float sweeps run the preorder-ownership kernel (three LDS rows of
-// NT * CPT + 64 floats; its set-up -- tables, the row permuted through LDS --
-// pays off over several sweeps); single sweeps and float64 rows the
-// Euler-tour one.  The two sum the path sums in different orders, so a chain
-// agrees with the same sweeps launched one at a time to rounding.
+// Chains of float sweeps run the linear-space preorder-ownership kernel (three
+// LDS rows of NT * CPT + 64 floats; its set-up -- tables, linear constants, the
+// row permuted through LDS -- pays off over several sweeps); single sweeps and
+// float64 rows the log-space Euler-tour one.  A chain agrees with the same
+// sweeps launched one at a time to float32 rounding.
 template <typename T, int CPT>
 int launch_wave_step(const kbo::OpsTree& t, const kbo::WsArgs<T>& a, int W, size_t lds, hipStream_t st) {
   if constexpr (std::is_same_v<T, float>) {
     if (a.n_sweeps > 1) {
-      const size_t lds_pre = (size_t)3 * (kbo::NT * CPT + 64) * sizeof(float);
-      auto k = kbo::wave_step_pre_kernel<CPT>;
-      if (int rc = set_lds(k, lds_pre)) return rc;
-      hipLaunchKernelGGL(k, dim3(W), dim3(kbo::NT), lds_pre, st, t, a);
+      const size_t lds_lin = (size_t)3 * (kbo::NT * CPT + 64) * sizeof(float);
+      auto k = kbo::wave_step_lin_kernel<CPT>;
+      if (int rc = set_lds(k, lds_lin)) return rc;
+      hipLaunchKernelGGL(k, dim3(W), dim3(kbo::NT), lds_lin, st, t, a);
       return 0;
     }
   }

@@ -21,8 +21,8 @@ such a chain (same rows, constants and split term; its ``Pi_in`` is the
 previous call's ``Pi_out``) is held back, and the chain runs as one launch of
 ``n`` sweeps with the row on chip when its final call arrives: the same
 final Pi, Pibar, row maxima and residual up to float32 rounding (a float
-chain runs the preorder-ownership kernel, whose path sums add in another
-order; float64 chains are bitwise those of single sweeps).  Held-back calls leave their
+chain runs in linear space at preorder positions, with its path sums added in
+another order; float64 chains are bitwise those of single sweeps).  Held-back calls leave their
 own ``Pi_out`` rows unwritten: a caller must not read a chain's intermediate
 buffers before its final call (the reference glue never does).  Any other
 wrapper call, or a call that breaks the chain, first runs what is held back.

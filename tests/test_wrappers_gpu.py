@@ -237,8 +237,8 @@ def test_glue_config3_forward_matches_fused():
 
 @pytest.mark.parametrize("name", ["1", "3"])
 def test_fused_sweep_chains_match_one_launch_per_sweep(name, monkeypatch):
-    """KBENCH_FUSE_SWEEPS: a wave's chained sweeps run as one launch (the preorder-ownership kernel for float
-    rows) and agree with one launch per sweep to float32 rounding: same -inf pattern, loss 1e-6, rows
+    """KBENCH_FUSE_SWEEPS: a wave's chained sweeps run as one launch (the linear-space preorder-ownership kernel
+    for float rows) and agree with one launch per sweep to float32 rounding: same -inf pattern, loss 1e-6, rows
     2e-4 absolute or 1e-5 relative."""
     import dropin
     from kbench.core.kernels import wave_step
@@ -302,7 +302,7 @@ def test_held_sweeps_run_before_other_work(monkeypatch):
         torch.cuda.synchronize()
         assert wave_step._chain is None
         rows = slice(w.ws, w.ws + w.W)
-        # the last sweep's output rows; a held chain of several sweeps runs the
-        # preorder-ownership kernel, whose path sums add in another order
+        # the last sweep's output rows; a held chain of several sweeps runs in
+        # linear space at preorder positions, with its sums added in another order
         ok, ma, mr = kbtest.compare_inf_safe(got[1][rows].cpu().numpy(), ref[1][rows].cpu().numpy())
         assert ok and (ma <= 2e-4 or mr <= 1e-5), (how, ma, mr)

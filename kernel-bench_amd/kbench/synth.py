@@ -643,6 +643,77 @@ def family_subset(problem: dict, families) -> dict:
     return out
 
 
+def _host(x):
+    """A layout field as a numpy array (device tensors are copied to the host)."""
+    if hasattr(x, "detach"):
+        return x.detach().cpu().numpy()
+    return np.asarray(x)
+
+
+def _splits_by_parent(wl: dict, C: int) -> list:
+    """Row -> [(child l, child r, split log-probability)] in stored split order."""
+    splits_of = [[] for _ in range(C)]
+    for m in wl["wave_metas"]:
+        if "sl" not in m:
+            continue
+        s0 = int(m["start"])
+        sl, sr, red = _host(m["sl"]), _host(m["sr"]), _host(m["reduce_idx"])
+        lsp = m.get("log_split_probs")
+        lsp = np.zeros(len(sl)) if lsp is None else _host(lsp).reshape(-1)
+        for a, b, w, p in zip(sl, sr, red, lsp):
+            splits_of[s0 + int(w)].append((int(a), int(b), float(p)))
+    return splits_of
+
+
+def _level_metas(level: np.ndarray, splits: list, cap: int, lsp_dtype=np.float64) -> list:
+    """Wave metas of rows already numbered by level: one wave per level (chunked to ``cap`` rows).
+
+    ``splits[r]`` lists row r's splits with children in the same numbering; a
+    level-0 wave has no split fields, every other wave lists its parents'
+    splits, parents with one split first (``eq1``), then the others (``ge2``).
+    """
+    C = int(level.shape[0])
+    metas = []
+    start = 0
+    while start < C:
+        lv = level[start]
+        end = start
+        while end < C and level[end] == lv and end - start < cap:
+            end += 1
+        W = end - start
+        meta = {"start": start, "W": W}
+        if lv > 0:
+            eq1, ge2 = [], []
+            for w in range(W):
+                sp = splits[start + w]
+                (eq1 if len(sp) == 1 else ge2).append((w, sp))
+            sl, sr, red, lsp = [], [], [], []
+            for w, sp in eq1:
+                for a, b, p in sp:
+                    sl.append(a); sr.append(b); red.append(w); lsp.append(p)
+            n_eq1 = len(sl)
+            ge2_ptr, ge2_parent = [0], []
+            for w, sp in ge2:
+                for a, b, p in sp:
+                    sl.append(a); sr.append(b); red.append(w); lsp.append(p)
+                ge2_ptr.append(len(sl) - n_eq1)
+                ge2_parent.append(w)
+            meta.update({
+                "sl": np.asarray(sl, dtype=np.int64),
+                "sr": np.asarray(sr, dtype=np.int64),
+                "reduce_idx": np.asarray(red, dtype=np.int64),
+                "log_split_probs": np.asarray(lsp, dtype=lsp_dtype),
+                "n_eq1": n_eq1,
+                "eq1_reduce_idx": np.asarray(red[:n_eq1], dtype=np.int64),
+                "ge2_ptr": np.asarray(ge2_ptr, dtype=np.int64),
+                "ge2_parent_ids": np.asarray(ge2_parent, dtype=np.int64),
+                "ge2_max_fanout": int(max(np.diff(ge2_ptr), default=0)),
+            })
+        metas.append(meta)
+        start = end
+    return metas
+
+
 def level_waves(problem: dict, max_wave_rows: int | None = None) -> tuple[dict, np.ndarray]:
     """The same problem with its rows regrouped into one wave per clade-DAG level -> (problem, new_of_old).
 
@@ -660,14 +731,7 @@ def level_waves(problem: dict, max_wave_rows: int | None = None) -> tuple[dict, 
     """
     wl = problem["static"]["wave_layout"]
     C = int(np.asarray(wl["leaf_state_index"]).shape[0])
-    splits_of = [[] for _ in range(C)]  # old parent -> [(old l, old r, lsp)] in old split order
-    for m in wl["wave_metas"]:
-        if "sl" not in m:
-            continue
-        s0 = int(m["start"])
-        lsp = np.asarray(m.get("log_split_probs", np.zeros(len(m["sl"]))), dtype=np.float64)
-        for a, b, w, p in zip(np.asarray(m["sl"]), np.asarray(m["sr"]), np.asarray(m["reduce_idx"]), lsp):
-            splits_of[s0 + int(w)].append((int(a), int(b), float(p)))
+    splits_of = _splits_by_parent(wl, C)
     level = np.zeros(C, dtype=np.int64)
     for m in wl["wave_metas"]:  # waves are in dependency order: children first
         s0, W = int(m["start"]), int(m["W"])
@@ -678,44 +742,8 @@ def level_waves(problem: dict, max_wave_rows: int | None = None) -> tuple[dict, 
     new_of_old = np.empty(C, dtype=np.int64)
     new_of_old[order] = np.arange(C)
     cap = int(max_wave_rows) if max_wave_rows else C
-    metas = []
-    start = 0
-    while start < C:
-        lv = level[order[start]]
-        end = start
-        while end < C and level[order[end]] == lv and end - start < cap:
-            end += 1
-        W = end - start
-        meta = {"start": start, "W": W}
-        if lv > 0:
-            eq1, ge2 = [], []
-            for w in range(W):
-                sp = [(int(new_of_old[a]), int(new_of_old[b]), p) for a, b, p in splits_of[int(order[start + w])]]
-                (eq1 if len(sp) == 1 else ge2).append((w, sp))
-            sl, sr, red, lsp = [], [], [], []
-            for w, sp in eq1:
-                for a, b, p in sp:
-                    sl.append(a); sr.append(b); red.append(w); lsp.append(p)
-            n_eq1 = len(sl)
-            ge2_ptr, ge2_parent = [0], []
-            for w, sp in ge2:
-                for a, b, p in sp:
-                    sl.append(a); sr.append(b); red.append(w); lsp.append(p)
-                ge2_ptr.append(len(sl) - n_eq1)
-                ge2_parent.append(w)
-            meta.update({
-                "sl": np.asarray(sl, dtype=np.int64),
-                "sr": np.asarray(sr, dtype=np.int64),
-                "reduce_idx": np.asarray(red, dtype=np.int64),
-                "log_split_probs": np.asarray(lsp, dtype=np.float64),
-                "n_eq1": n_eq1,
-                "eq1_reduce_idx": np.asarray(red[:n_eq1], dtype=np.int64),
-                "ge2_ptr": np.asarray(ge2_ptr, dtype=np.int64),
-                "ge2_parent_ids": np.asarray(ge2_parent, dtype=np.int64),
-                "ge2_max_fanout": int(max(np.diff(ge2_ptr), default=0)),
-            })
-        metas.append(meta)
-        start = end
+    splits_new = [[(int(new_of_old[a]), int(new_of_old[b]), p) for a, b, p in splits_of[int(o)]] for o in order]
+    metas = _level_metas(level[order], splits_new, cap)
     st = problem["static"]
     out = {
         "meta": dict(problem["meta"]),
@@ -736,3 +764,83 @@ def level_waves(problem: dict, max_wave_rows: int | None = None) -> tuple[dict, 
     if "tree" in problem:
         out["tree"] = problem["tree"]
     return out, new_of_old
+
+
+def row_classes(wave_layout: dict, rate_item_idx, active=None) -> tuple[dict, np.ndarray, np.ndarray]:
+    """Rows that compute the same values, one row per class -> (class layout, class_of_row, rep_of_class).
+
+    Two rows share a class when they have the same parameter row
+    (``rate_item_idx``) and the same wave kind (split or leaf wave, and its
+    ``phase``), and either both are leaf-wave rows with the same leaf state, or
+    both are split rows whose splits, as (class of one child, class of the
+    other, split log-probability) with the two children unordered, form the
+    same multiset.  By induction from the leaves, rows of one class have the
+    same truncated forward rows (Pi, Pibar, row maxima, split term) and the
+    same forward tangents: the only differences are the order in which a
+    row's splits are merged.  With ``active`` (one flag per row, e.g. the
+    backward's active mask at a point), the flag is part of the key as well,
+    so that every member of a class has the same flag and so do the children
+    of every member along each split: the adjoint maps of all members of a
+    class are then one linear map, applied to each member's own right-hand
+    side.
+
+    The class layout is a wave layout whose rows are the classes: class c is
+    row c, numbered by (level, first member); one wave per level as
+    ``level_waves`` builds them; each class row has the leaf state and the
+    splits (children mapped to their classes, in the representative's order)
+    of its representative, the first member in row order of the layout's
+    waves.  ``root_row_ids`` maps every family's root row to its class (two
+    families with equal root rows share one).
+    """
+    wl = wave_layout
+    leaf = _host(wl["leaf_state_index"]).astype(np.int64)
+    C = int(leaf.shape[0])
+    item = _host(rate_item_idx).astype(np.int64).reshape(-1)
+    if item.shape[0] == 1 and C != 1:
+        item = np.broadcast_to(item, (C,))
+    act = None if active is None else _host(active).astype(bool).reshape(-1)
+    splits_of = _splits_by_parent(wl, C)
+    cls = np.full(C, -1, dtype=np.int64)
+    ids: dict = {}
+    reps, level = [], []
+    for m in wl["wave_metas"]:  # children first
+        s0, W = int(m["start"]), int(m["W"])
+        split_wave = "sl" in m
+        phase = m.get("phase")
+        phase = None if phase is None else int(phase)
+        for r in range(s0, s0 + W):
+            flag = True if act is None else bool(act[r])
+            if split_wave:
+                body = tuple(sorted((min(cls[a], cls[b]), max(cls[a], cls[b]), p) for a, b, p in splits_of[r]))
+            else:
+                body = int(leaf[r])
+            key = (split_wave, phase, int(item[r]), flag, body)
+            c = ids.get(key)
+            if c is None:
+                c = ids[key] = len(reps)
+                reps.append(r)
+                level.append(1 + max(max(level[cls[a]], level[cls[b]]) for a, b, _ in splits_of[r])
+                             if split_wave and splits_of[r] else 0)
+            cls[r] = c
+    if (cls < 0).any():
+        raise ValueError("the wave layout does not cover every row")
+    reps = np.asarray(reps, dtype=np.int64)
+    level = np.asarray(level, dtype=np.int64)
+    Cc = int(reps.shape[0])
+    order = np.lexsort((reps, level))  # new class id -> old class id
+    new_of = np.empty(Cc, dtype=np.int64)
+    new_of[order] = np.arange(Cc)
+    rep = reps[order]
+    lsp_dtype = np.float64
+    for m in wl["wave_metas"]:
+        if "sl" in m and m.get("log_split_probs") is not None:
+            lsp_dtype = _host(m["log_split_probs"]).dtype
+            break
+    splits_new = [[(int(new_of[cls[a]]), int(new_of[cls[b]]), p) for a, b, p in splits_of[int(r)]] for r in rep]
+    layout = {
+        "leaf_state_index": leaf[rep],
+        "root_row_ids": new_of[cls[_host(wl["root_row_ids"]).astype(np.int64)]],
+        "item_idx": _host(wl["item_idx"])[rep],
+        "wave_metas": _level_metas(level[order], splits_new, Cc, lsp_dtype),
+    }
+    return layout, new_of[cls], rep

@@ -27,17 +27,32 @@ E side and head
 The point cache (one backward at theta keeping every wave's adjoint, split
 term and mask, the accumulated cotangents and the E adjoint) is built once per
 theta by ``SolvePlan.reverse_sweep`` / ``e_adjoint_and_vjp``.
+
+Row classes (``HvpPlan(..., row_classes=True)``): rows with the same inputs
+(``synth.row_classes``) have the same forward rows and the same forward
+tangents, so the tangent forward runs on one row per class (config 3: 11253
+of 33686 rows).  The tangent reverse is linear in the point adjoint v and in
+the right-hand sides it propagates, and members of a class whose active flags
+agree, and whose children along each split agree in class and flag, share
+one adjoint map; so it runs on one row per such class (the classes of
+``row_classes`` with the point's active mask), from the members' summed
+adjoints and root seeds (fixed-order sums).  The bucket sums, and through them
+H u, are those of the row-by-row reverse up to the order of the sums.
 """
 
 from __future__ import annotations
 
 from types import SimpleNamespace
 
+import numpy as np
 import torch
 from torch.func import jvp
 
 from kbench.core.parameters.extract_parameters import (as_item_param, as_item_state, extract_parameters_uniform,
                                                        extract_parameters_weighted_cols)
+
+from kbench import synth
+from kbench.core.kernels import _hip as H
 
 from .krylov import bicgstab
 from .solve import LN2, SolvePlan, root_softmax2
@@ -153,6 +168,88 @@ class TangentForward:
         return dpi.index_select(0, p.roots), SimpleNamespace(dPi=dpi, dPibar=dpibar, d=d)
 
 
+def _class_static(static, layout, rep):
+    """A static namespace whose rows are the class rows of ``layout`` (tensors on the static's device)."""
+    dev = static.rate_item_idx.device
+
+    def conv(x):
+        if isinstance(x, np.ndarray):
+            return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+        if isinstance(x, dict):
+            return {k: conv(v) for k, v in x.items()}
+        if isinstance(x, list):
+            return [conv(v) for v in x]
+        return x
+
+    item = static.rate_item_idx
+    if int(item.numel()) > 1:
+        item = item.index_select(0, torch.from_numpy(rep).to(dev))
+    return SimpleNamespace(wave_layout=conv(layout), state_helpers=static.state_helpers, rate_item_idx=item,
+                           itemwise=static.itemwise, statewise=static.statewise,
+                           solver_options=static.solver_options, warm_E=None)
+
+
+def _forward_classes(plan: SolvePlan):
+    """(class plan, class_of_row, rep_of_class) of the rows' forward classes, kept on the plan."""
+    fc = getattr(plan, "_hvp_forward_classes", None)
+    if fc is None:
+        st = plan.static
+        layout, class_of, rep = synth.row_classes(st.wave_layout, st.rate_item_idx)
+        dev = st.rate_item_idx.device
+        fc = (SolvePlan(_class_static(st, layout, rep), kernels=plan.k), torch.from_numpy(class_of).to(dev),
+              torch.from_numpy(rep).to(dev))
+        plan._hvp_forward_classes = fc
+    return fc
+
+
+class _ClassSchedule:
+    """The tangent forward and reverse of ``HvpPlan`` on class rows (see the module docstring).
+
+    ``fplan`` / ``fsaved``: the forward classes and their saved rows;
+    ``rplan``: the reverse classes (forward classes split by the point's
+    active mask); ``cache``: per reverse-class wave, in reverse order,
+    (wave, summed point adjoint of the members, split term, active flag);
+    ``root_keys``: the reverse class of every family's root row (-1 if the
+    root is inactive); ``fc_of_rc``: the forward class of each reverse class.
+    """
+
+    def __init__(self, plan: SolvePlan, saved, waves):
+        if float(plan.so.pibar_side_threshold) != 0.0:
+            raise ValueError("row classes need pibar_side_threshold == 0 (a side rule linear in the adjoint)")
+        st = plan.static
+        dev = saved["pi_wave"].device
+        self.fplan, fc_of_row, frep = _forward_classes(plan)
+        self.fsaved = dict(saved, pi_wave=saved["pi_wave"].index_select(0, frep),
+                           pibar_wave=saved["pibar_wave"].index_select(0, frep),
+                           pibar_row_max=saved["pibar_row_max"].index_select(0, frep))
+        active = torch.zeros((plan.C,), dtype=torch.bool, device=dev)
+        for w, _, _, mask in waves:
+            active[w.ws: w.ws + w.W] = mask
+        layout, rc_of_row, rrep = synth.row_classes(st.wave_layout, st.rate_item_idx, active=active)
+        rp = self.rplan = SolvePlan(_class_static(st, layout, rrep), kernels=plan.k)
+        rc_of_row = torch.from_numpy(rc_of_row).to(dev)
+        rrep = torch.from_numpy(rrep).to(dev)
+        self.fc_of_rc = fc_of_row.index_select(0, rrep)
+        self.Pi = saved["pi_wave"].index_select(0, rrep)
+        self.Pibar = saved["pibar_wave"].index_select(0, rrep)
+        self.prm = saved["pibar_row_max"].index_select(0, rrep)
+        on = active.index_select(0, rrep)
+        none = torch.full_like(rc_of_row, -1)
+        V = torch.zeros_like(self.Pi)
+        for w, v, _, mask in waves:  # members' adjoints, summed per class in a fixed order
+            H.scatter_add_rows(V, v, torch.where(mask, rc_of_row[w.ws: w.ws + w.W], none[: w.W]))
+        roots = plan.roots
+        self.root_keys = torch.where(active.index_select(0, roots), rc_of_row.index_select(0, roots),
+                                     none[: int(roots.numel())])
+        c = rp._row_consts(saved["E"], saved["Ebar"], saved["E_s1"], saved["E_s2"], saved["log_pS"],
+                           saved["log_pD"], saved["max_coupling"])
+        self.cache = []
+        for w in reversed(rp.waves):
+            mask = on[w.ws: w.ws + w.W].contiguous()
+            dts = rp._dts(w, self.Pi, self.Pibar, c, active=mask) if w.split else None
+            self.cache.append((w, V[w.ws: w.ws + w.W], dts, mask))
+
+
 class _EGraph:
     """One E step at (E*, parameters) kept as an autograd graph: its transposed products."""
 
@@ -192,7 +289,7 @@ class _EGraph:
 class HvpPlan:
     """H u of the summed loss at theta (uniform column weights), through the wrappers."""
 
-    def __init__(self, plan: SolvePlan, theta, col_weights, saved, *, tangent_sweeps=None):
+    def __init__(self, plan: SolvePlan, theta, col_weights, saved, *, tangent_sweeps=None, row_classes=False):
         self.p, self.sv = plan, saved
         self.theta, self.cw = theta, col_weights
         self.sweeps = int(plan.so.pi_iters if tangent_sweeps is None else tangent_sweeps)
@@ -206,7 +303,10 @@ class HvpPlan:
         e_out = {}
         self.grad = plan.e_adjoint_and_vjp(theta, col_weights, saved, self.acc, use_col=False, out=e_out)
         self.wE = e_out["wE"]
-        self.tan = TangentForward(plan, saved)
+        self.q = root_softmax2(saved["pi_wave"].index_select(0, plan.roots))
+        self.cls = _ClassSchedule(plan, saved, self.waves) if row_classes else None
+        self.tan = TangentForward(plan, saved) if self.cls is None else TangentForward(self.cls.fplan,
+                                                                                        self.cls.fsaved)
         self.eg = _EGraph(plan, saved)
         a = self.acc
         base = self.eg.params_t(self.wE, a.Ebar)
@@ -237,17 +337,29 @@ class HvpPlan:
         return hu.reshape(-1)
 
     def _tangent_cotangents(self, u):
-        p, sv, a = self.p, self.sv, self.acc
-        S, G, C = p.S, self.G, p.C
+        sv, a = self.sv, self.acc
+        S, G = self.p.S, self.G
         t_root, tf = self.tan.run(self.theta, u, sweeps=self.sweeps)
-        d, dPi, dPibar = tf.d, tf.dPi, tf.dPibar
-        Pi, Pibar, prm, col = sv["pi_wave"], sv["pibar_wave"], sv["pibar_row_max"], sv["col_log_probs"]
+        d = tf.d
+        col = sv["col_log_probs"]
         b = self.tan.base
-        h = p.h
         # tangent of the root seed -softmax2(root): -ln2 q (t - <q, t>)
-        q = root_softmax2(Pi.index_select(0, p.roots))
-        d_rhs = torch.zeros((C, S), dtype=Pi.dtype, device=Pi.device)
-        d_rhs.index_copy_(0, p.roots, -LN2 * q * (t_root - (q * t_root).sum(dim=-1, keepdim=True)))
+        q = self.q
+        seed = -LN2 * q * (t_root - (q * t_root).sum(dim=-1, keepdim=True))
+        k = self.cls
+        if k is None:
+            p, waves = self.p, self.waves
+            Pi, Pibar, prm = sv["pi_wave"], sv["pibar_wave"], sv["pibar_row_max"]
+            dPi, dPibar = tf.dPi, tf.dPibar
+            d_rhs = torch.zeros((p.C, S), dtype=Pi.dtype, device=Pi.device)
+            d_rhs.index_copy_(0, p.roots, seed)
+        else:
+            p, waves = k.rplan, k.cache
+            Pi, Pibar, prm = k.Pi, k.Pibar, k.prm
+            dPi, dPibar = tf.dPi.index_select(0, k.fc_of_rc), tf.dPibar.index_select(0, k.fc_of_rc)
+            d_rhs = torch.zeros((p.C, S), dtype=Pi.dtype, device=Pi.device)
+            H.scatter_add_rows(d_rhs, seed, k.root_keys, static=(k.root_keys,))
+        h = p.h
         dacc = SimpleNamespace(pD=torch.zeros_like(a.pD), pS=torch.zeros_like(a.pS), mt=torch.zeros_like(a.mt),
                                col=torch.zeros_like(a.col), E=torch.zeros_like(a.E), Ebar=torch.zeros_like(a.E),
                                Es1=torch.zeros_like(a.E), Es2=torch.zeros_like(a.E))
@@ -255,7 +367,7 @@ class HvpPlan:
                    (dacc.Es2, (4,)), (dacc.mt, (2,)))
         cst_so = (b.mc,) + self.tan.interleaved(d)[2:]  # the contraction takes mt without its tangent
         so = p.so
-        for w, v, dts, mask in self.waves:
+        for w, v, dts, mask in waves:
             d_dts = None
             if w.split:
                 d_dts = p.k.compute_dts_tangent(Pi, Pibar, dPi, dPibar, w.sl, w.sr, h["node_child1"],

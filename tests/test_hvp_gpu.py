@@ -186,15 +186,17 @@ def test_dts_backward_so_matches_oracle(dt, statewise):
     assert worst <= TOL[dt]
 
 
-@pytest.mark.parametrize("name,statewise", [("tiny", None), ("tiny", True), ("1", True)])
-def test_exact_hvp_matches_oracle(name, statewise):
+@pytest.mark.parametrize("name,statewise,row_classes", [("tiny", None, False), ("tiny", True, False),
+                                                         ("1", True, False), ("tiny", None, True),
+                                                         ("1", True, True), ("1", None, True)])
+def test_exact_hvp_matches_oracle(name, statewise, row_classes):
     from dropin.hvp import HvpPlan
     from dropin.solve import plan_of, run_forward
 
-    print(f"[hvp] config={name} statewise={statewise}", flush=True)
+    print(f"[hvp] config={name} statewise={statewise} row_classes={row_classes}", flush=True)
     static, theta, cw = _static(name, statewise)
     _, sv = run_forward(static, theta, cw)
-    hvp = HvpPlan(plan_of(static), theta, cw, sv)
+    hvp = HvpPlan(plan_of(static), theta, cw, sv, row_classes=row_classes)
     u = np.random.default_rng(34).normal(size=tuple(theta.shape))
     Hu = hvp(torch.as_tensor(u, dtype=theta.dtype).cuda().reshape(-1))
     torch.cuda.synchronize()
@@ -241,6 +243,37 @@ def test_exact_hvp_config3_symmetric_linear_deterministic():
     lin = _rel(H12.cpu().numpy(), (H1 + 2.0 * H2).cpu().numpy())
     print(f"  linearity rel={lin:.3e}")
     assert lin <= 1e-4
+
+
+def test_exact_hvp_config3_on_row_classes_matches_row_by_row():
+    """Config 3 on level waves (the bench's HVP): the tangent forward on one row per class and the
+    tangent reverse on one row per masked class give the row-by-row H u (rel 1e-4 of max |H u|),
+    bitwise the same on a second call."""
+    from dropin.hvp import HvpPlan
+    from dropin.solve import plan_of, run_forward
+    from kbench import synth
+    from kbench.fused import problem_to_captured
+    from kbench.runtime import make_static
+
+    print("[hvp] config=3 statewise=True level waves, row classes vs rows", flush=True)
+    q, _ = synth.level_waves(kbtest.problem("3", True))
+    cap = problem_to_captured(q)
+    static = make_static(cap, "cuda")
+    theta, cw = cap["inputs"]["theta"].cuda(), cap["inputs"]["col_weights"].cuda()
+    _, sv = run_forward(static, theta, cw)
+    plan = plan_of(static)
+    u = torch.as_tensor(np.random.default_rng(37).normal(size=tuple(theta.shape)), dtype=theta.dtype).cuda()
+    u = u.reshape(-1)
+    ref = HvpPlan(plan, theta, cw, sv)(u)
+    hc = HvpPlan(plan, theta, cw, sv, row_classes=True)
+    n_rc = hc.cls.rplan.C
+    got, again = hc(u), hc(u)
+    torch.cuda.synchronize()
+    e = kbtest.norm_rel_t(got, ref)
+    print(f"  rows {plan.C}, forward classes {hc.cls.fplan.C}, reverse classes {n_rc}; rel={e:.3e}")
+    assert hc.cls.fplan.C < plan.C and n_rc < plan.C
+    assert torch.equal(got, again)
+    assert e <= 1e-4
 
 
 def test_ggn_hvp_is_symmetric_and_psd():

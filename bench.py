@@ -267,10 +267,10 @@ def bench_hvp(args, static, theta, cw, summ, static_levels) -> None:
     us = [torch.as_tensor(g.normal(size=tuple(theta.shape)), dtype=theta.dtype, device=theta.device).reshape(-1)
           for _ in range(4)]
 
-    def timed(st, row_classes=False):
+    def timed(st, row_classes=False, graph=False):
         _, sv = run_forward(st, theta, cw)
         t0 = time.perf_counter()
-        hvp = HvpPlan(plan_of(st), theta, cw, sv, row_classes=row_classes)
+        hvp = HvpPlan(plan_of(st), theta, cw, sv, row_classes=row_classes, graph=graph)
         torch.cuda.synchronize()
         cache_ms = (time.perf_counter() - t0) * 1e3
         k = [0]
@@ -285,7 +285,8 @@ def bench_hvp(args, static, theta, cw, summ, static_levels) -> None:
     if args.hvp_layout == "both":
         ms_size, cache_size = timed(static)
     ms_rows, cache_rows = timed(static_levels)
-    ms, cache_ms = timed(static_levels, row_classes=True)
+    ms_eager, _ = timed(static_levels, row_classes=True)
+    ms, cache_ms = timed(static_levels, row_classes=True, graph=True)
     print(json.dumps({
         "metric": "exact Hessian-vector product ms (config 5: per-species theta, forward tangent + tangent adjoint)",
         "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -293,10 +294,12 @@ def bench_hvp(args, static, theta, cw, summ, static_levels) -> None:
         "dtype": "fp32", "data": "synthetic",
         "config": {"workload": (f"config{args.config} exact HVP through the per-call wrappers, rows in one wave per "
                                 f"dependency level ({len(static_levels.wave_layout['wave_metas'])} waves), tangent "
-                                "forward and reverse on one row per class of identical rows"),
+                                "forward and reverse on one row per class of identical rows, replayed as one HIP "
+                                "graph"),
                    "S": summ["S"], "C": summ["C"], "point_cache_ms": round(cache_ms, 3)},
         "ms_per_newton_cg_step_50_hvps": round(50 * ms, 2),
         "row_by_row": {"ms": round(ms_rows, 4), "point_cache_ms": round(cache_rows, 3)},
+        "row_classes_without_graph_ms": round(ms_eager, 4),
         "size_waves": None if ms_size is None else {"n_waves": summ["n_waves"], "ms": round(ms_size, 4),
                                                     "point_cache_ms": round(cache_size, 3)},
     }))

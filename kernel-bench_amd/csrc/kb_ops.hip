@@ -1653,12 +1653,68 @@ __global__ __launch_bounds__(256) void scatter_add_kernel(int S, long long n, co
   if (s >= S) return;
   const long long key = keys[k];
   if (key < 0 || (k > 0 && keys[k - 1] == key)) return;
+  long long e = k + 1;  // end of the run of this key (the same for every thread)
+  while (e < n && keys[e] == key) ++e;
+  // the run's rows added in order; the loads of eight rows are issued before their adds
   T acc = 0;
-  for (long long j = k; j < n && keys[j] == key; ++j) acc += src[(size_t)order[j] * S + s];
+  long long j = k;
+  for (; j + 8 <= e; j += 8) {
+    T x[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = src[(size_t)order[j + i] * S + s];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc += x[i];
+  }
+  for (; j < e; ++j) acc += src[(size_t)order[j] * S + s];
   dst[(size_t)(key * dst_stride) + s] += acc;
 }
 
 constexpr int SUM_CHUNK = 64;
+
+// Sum over rows r0 <= r < r1 of column s of a row-major block with S columns,
+// added in row order in float64 (with a second block B, each row's A + B is
+// formed first).  The loads of eight rows are issued before their adds: the
+// adds keep their order, so the sum is the one of the plain loop.
+template <typename T>
+__device__ __forceinline__ double col_sum(const T* A, const T* B, int S, long long r0, long long r1, int s) {
+  double acc = 0.0;
+  long long r = r0;
+  for (; r + 8 <= r1; r += 8) {
+    T x[8], y[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = A[(size_t)(r + i) * S + s];
+    if (B) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = B[(size_t)(r + i) * S + s];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc += (double)x[i] + (double)y[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc += (double)x[i];
+    }
+  }
+  for (; r < r1; ++r) {
+    double x = (double)A[(size_t)r * S + s];
+    if (B) x += (double)B[(size_t)r * S + s];
+    acc += x;
+  }
+  return acc;
+}
+
+// Sum over chunks c < n of work[c * S + s], in chunk order, eight loads ahead.
+__device__ __forceinline__ double chunk_sum(const double* work, int S, int n, int s) {
+  double acc = 0.0;
+  int c = 0;
+  for (; c + 8 <= n; c += 8) {
+    double x[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = work[(size_t)(c + i) * S + s];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc += x[i];
+  }
+  for (; c < n; ++c) acc += work[(size_t)c * S + s];
+  return acc;
+}
 
 template <typename T>
 __global__ __launch_bounds__(256) void rows_sum_stage1(int S, long long n, const T* src, double* work) {
@@ -1666,9 +1722,7 @@ __global__ __launch_bounds__(256) void rows_sum_stage1(int S, long long n, const
   if (s >= S) return;
   const long long r0 = (long long)blockIdx.y * SUM_CHUNK;
   const long long r1 = min(n, r0 + SUM_CHUNK);
-  double acc = 0.0;
-  for (long long r = r0; r < r1; ++r) acc += (double)src[(size_t)r * S + s];
-  work[(size_t)blockIdx.y * S + s] = acc;
+  work[(size_t)blockIdx.y * S + s] = col_sum<T>(src, nullptr, S, r0, r1, s);
 }
 
 // One chunk or fewer rows: both stages in one launch (same sums).
@@ -1676,8 +1730,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void rows_sum_single(int S, long long n, const T* src, T* dst) {
   const int s = blockIdx.x * 256 + threadIdx.x;
   if (s >= S) return;
-  double acc = 0.0;
-  for (long long r = 0; r < n; ++r) acc += (double)src[(size_t)r * S + s];
+  const double acc = col_sum<T>(src, nullptr, S, 0, n, s);
   dst[s] = (T)((double)dst[s] + acc);
 }
 
@@ -1699,12 +1752,7 @@ __global__ __launch_bounds__(256) void rows_sum_multi_stage1(RsmArgs p, double* 
   const T* A = static_cast<const T*>(p.a[j]);
   const T* B = static_cast<const T*>(p.b[j]);
   const long long r0 = (long long)c * SUM_CHUNK, r1 = min(p.n, r0 + SUM_CHUNK);
-  double acc = 0.0;
-  for (long long r = r0; r < r1; ++r) {
-    double x = (double)A[(size_t)r * p.S + s];
-    if (B) x += (double)B[(size_t)r * p.S + s];
-    acc += x;
-  }
+  const double acc = col_sum<T>(A, B, p.S, r0, r1, s);
   if (p.chunks == 1)
     out[(size_t)j * p.S + s] = (T)acc;
   else
@@ -1716,17 +1764,14 @@ __global__ __launch_bounds__(256) void rows_sum_multi_stage2(RsmArgs p, const do
   const int s = blockIdx.x * 256 + threadIdx.x;
   if (s >= p.S) return;
   const int j = blockIdx.z;
-  double acc = 0.0;
-  for (int c = 0; c < p.chunks; ++c) acc += work[((size_t)j * p.chunks + c) * p.S + s];
-  out[(size_t)j * p.S + s] = (T)acc;
+  out[(size_t)j * p.S + s] = (T)chunk_sum(work + (size_t)j * p.chunks * p.S, p.S, p.chunks, s);
 }
 
 template <typename T>
 __global__ __launch_bounds__(256) void rows_sum_stage2(int S, int n_chunks, const double* work, T* dst) {
   const int s = blockIdx.x * 256 + threadIdx.x;
   if (s >= S) return;
-  double acc = 0.0;
-  for (int c = 0; c < n_chunks; ++c) acc += work[(size_t)c * S + s];
+  const double acc = chunk_sum(work, S, n_chunks, s);
   dst[s] = (T)((double)dst[s] + acc);
 }
 

@@ -38,6 +38,12 @@ one adjoint map; so it runs on one row per such class (the classes of
 ``row_classes`` with the point's active mask), from the members' summed
 adjoints and root seeds (fixed-order sums).  The bucket sums, and through them
 H u, are those of the row-by-row reverse up to the order of the sums.
+
+HIP graph (``HvpPlan(..., graph=True)``): for a fixed point the tangent
+forward and reverse launch the same kernels on the same buffers for every u,
+with no host read in between; they are captured once into a graph and
+replayed (the E side, whose BiCGSTAB tests convergence on the host, and the
+parameter head run eagerly).  A replay gives bitwise the eager result.
 """
 
 from __future__ import annotations
@@ -289,8 +295,12 @@ class _EGraph:
 class HvpPlan:
     """H u of the summed loss at theta (uniform column weights), through the wrappers."""
 
-    def __init__(self, plan: SolvePlan, theta, col_weights, saved, *, tangent_sweeps=None, row_classes=False):
+    def __init__(self, plan: SolvePlan, theta, col_weights, saved, *, tangent_sweeps=None, row_classes=False,
+                 graph=False):
+        if graph and plan.so.self_loop_solver != "neumann":
+            raise ValueError("a captured HVP needs the Neumann self-loop solver (GMRES reads its residuals on the host)")
         self.p, self.sv = plan, saved
+        self.graph, self._graph = bool(graph), None
         self.theta, self.cw = theta, col_weights
         self.sweeps = int(plan.so.pi_iters if tangent_sweeps is None else tangent_sweeps)
         S = plan.S
@@ -331,12 +341,29 @@ class HvpPlan:
     def __call__(self, u_flat):
         u = u_flat.reshape(self.theta.shape).to(self.theta.dtype)
         with torch.no_grad():
-            dcot = self._tangent_cotangents(u)
+            d, dacc = self._replay(u) if self.graph else self._tangent_reverse(u)
+            dcot = self._e_side(d, dacc)
         with torch.enable_grad():
             (hu,) = torch.autograd.grad((self.g1 * u).sum() + self._pair(dcot), self.th, retain_graph=True)
         return hu.reshape(-1)
 
-    def _tangent_cotangents(self, u):
+    def _replay(self, u):
+        """The tangent forward and reverse as one HIP graph: captured on the first call (after one
+        eager call that creates every cached layout table and kernel attribute), replayed after."""
+        if self._graph is None:
+            self._u_in = u.clone()
+            self._tangent_reverse(self._u_in)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self._graph_out = self._tangent_reverse(self._u_in)
+            self._graph = g
+        self._u_in.copy_(u)
+        self._graph.replay()
+        return self._graph_out
+
+    def _tangent_reverse(self, u):
+        """(constant tangents, tangent cotangents accumulated over the waves) along u."""
         sv, a = self.sv, self.acc
         S, G = self.p.S, self.G
         t_root, tf = self.tan.run(self.theta, u, sweeps=self.sweeps)
@@ -403,8 +430,7 @@ class HvpPlan:
                     Pi, dPi, Pibar, dPibar, v, w.ws, w.meta, S, b.pd_par, b.ps_par, d.dpd_par, d.dps_par, b.mc,
                     d.dMC, col, h["node_child1"], h["node_child2"], p.topo[0], p.topo[3], prm, p.item_idx, d_rhs,
                     dacc.pD, dacc.pS, dacc.mt, dacc.col, use_col_weights=False, **p.levels)
-        del tf, dPi, dPibar
-        return self._e_side(d, dacc)
+        return d, dacc
 
     def _e_side(self, d, dacc):
         """Tangent E adjoint and the tangent parameter cotangents."""

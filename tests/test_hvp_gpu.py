@@ -276,6 +276,38 @@ def test_exact_hvp_config3_on_row_classes_matches_row_by_row():
     assert e <= 1e-4
 
 
+@pytest.mark.parametrize("name,levels", [("1", False), ("3", True)])
+def test_exact_hvp_graph_replays_match_eager(name, levels):
+    """HvpPlan(graph=True): the tangent forward and reverse captured once and replayed; every replay
+    (new u each time, eager HVPs and host syncs in between) is bitwise the eager HVP."""
+    from dropin.hvp import HvpPlan
+    from dropin.solve import plan_of, run_forward
+    from kbench import synth
+    from kbench.fused import problem_to_captured
+    from kbench.runtime import make_static
+
+    print(f"[hvp graph] config={name} level_waves={levels}", flush=True)
+    p = kbtest.problem(name, True)
+    if levels:
+        p, _ = synth.level_waves(p)
+    cap = problem_to_captured(p)
+    static = make_static(cap, "cuda")
+    theta, cw = cap["inputs"]["theta"].cuda(), cap["inputs"]["col_weights"].cuda()
+    _, sv = run_forward(static, theta, cw)
+    plan = plan_of(static)
+    eager = HvpPlan(plan, theta, cw, sv, row_classes=True)
+    graphed = HvpPlan(plan, theta, cw, sv, row_classes=True, graph=True)
+    g = np.random.default_rng(38)
+    for i in range(4):
+        u = torch.as_tensor(g.normal(size=tuple(theta.shape)), dtype=theta.dtype).cuda().reshape(-1)
+        got = graphed(u)
+        ref = eager(u)
+        torch.cuda.synchronize()
+        e = kbtest.norm_rel_t(got, ref)
+        print(f"  call {i}: rel={e:.3e}", flush=True)
+        assert torch.equal(got, ref), e
+
+
 def test_ggn_hvp_is_symmetric_and_psd():
     from dropin.hvp import ggn_hvp
     from dropin.solve import plan_of, run_forward

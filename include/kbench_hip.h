@@ -165,6 +165,44 @@ typedef struct kb_backward_io {
 
 int kb_backward(kb_plan* plan, const kb_backward_io* io, void* stream);
 
+/*
+ * The E adjoint of the backward's epilogue for given cotangents, without the
+ * theta / column VJP: solves (I - J_E^T) w = q by BiCGSTAB (one workgroup,
+ * float64, the stopping and breakdown rules of kb_backward's epilogue) with
+ * q = acc_E + (E_s1, E_s2, Ebar cotangents pulled back to E) + q_extra
+ * (+ the loss normaliser's E gradient when with_norm), then writes w and the
+ * per-state cotangents of (log_pS, log_pD, log_pL, max_coupling,
+ * col_log_probs) of one E step at (w, acc_Ebar), plus acc's pS, pD, mt and
+ * col rows.  Replaces the Python BiCGSTAB of the reference's
+ * _implicit_grad.py:28-94 and its E-step VJP / parameter pull-back
+ * (_implicit_grad.py:373-430) where a caller solves the E adjoint for other
+ * cotangents than the backward's own (the exact HVP's tangent E adjoint,
+ * newton/hvp_exact.py:330-381).  One item row (itemwise=False) only.
+ */
+#define KB_E_ADJOINT_WORK_VECTORS 16
+typedef struct kb_e_adjoint_io {
+  int32_t statewise;
+  int32_t use_col_weights;
+  int32_t with_norm;         /* add d/dE n_fam log2(1 - mean 2^E) to q */
+  int32_t bicgstab_max_iter;
+  double bicgstab_tol;
+  double bicgstab_breakdown_tol;
+  const float* E;            /* [S] the E fixed point and the rates (kb_forward_io shapes) */
+  const float* log_pS;
+  const float* log_pD;
+  const float* log_pL;
+  const float* max_coupling;
+  const float* col_log_probs;
+  const double* acc;         /* [8,S] cotangents (pD, pS, E, Ebar, E_s1, E_s2, max_coupling, col) */
+  const double* q_extra;     /* [S] added to q, or null */
+  double* w_out;             /* [S] the E adjoint, or null */
+  double* g_out;             /* [5,S] cotangents of (pS, pD, pL, max_coupling, col) per state */
+  double* work;              /* [KB_E_ADJOINT_WORK_VECTORS, S] scratch */
+  int32_t* status;           /* [2] device: iterations, failure flag */
+} kb_e_adjoint_io;
+
+int kb_e_adjoint(kb_plan* plan, const kb_e_adjoint_io* io, void* stream);
+
 /* Token of the last kb_forward on this plan (a counter; 0 before the first). */
 int64_t kb_forward_token(const kb_plan* plan);
 

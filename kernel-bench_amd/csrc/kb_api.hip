@@ -1031,6 +1031,49 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   return 0;
 }
 
+int kb_e_adjoint(kb_plan* p, const kb_e_adjoint_io* io, void* stream) {
+  if (!p || !io) return set_error(KB_ERR_ARG, "null argument");
+  if (!io->E || !io->log_pS || !io->log_pD || !io->log_pL || !io->max_coupling || !io->col_log_probs || !io->acc ||
+      !io->g_out || !io->work || !io->status)
+    return set_error(KB_ERR_ARG, "null argument");
+  if (io->bicgstab_max_iter < 1) return set_error(KB_ERR_ARG, "max_iter must be at least 1");
+  if (!(io->bicgstab_tol > 0.0)) return set_error(KB_ERR_ARG, "tol must be positive");
+  if (!(io->bicgstab_breakdown_tol > 0.0)) return set_error(KB_ERR_ARG, "breakdown_tol must be positive");
+  if (kb::epilogue_work_vectors() > KB_E_ADJOINT_WORK_VECTORS)
+    return set_error(KB_ERR_HIP, "the epilogue needs %d work vectors", kb::epilogue_work_vectors());
+  kb::EpiParams X{};
+  X.tr = p->tree();
+  X.ts = p->tscan();
+  X.pd = p->predev();
+  X.S = p->S;
+  X.n_tlevels = p->n_tlevels;
+  X.tlevel_ptr = p->d_tlevel_ptr;
+  X.tlevel_node = p->d_tlevel_node;
+  X.E = io->E;
+  X.log_pS = io->log_pS;
+  X.log_pD = io->log_pD;
+  X.log_pL = io->log_pL;
+  X.mt = io->max_coupling;
+  X.col = io->col_log_probs;
+  X.statewise = io->statewise;
+  X.use_col = io->use_col_weights;
+  X.acc = io->acc;
+  X.n_fam = p->n_fam;
+  X.n_items_rows = 1;
+  X.max_iter = io->bicgstab_max_iter;
+  X.tol = io->bicgstab_tol;
+  X.breakdown = io->bicgstab_breakdown_tol;
+  X.work = io->work;
+  X.status = io->status;
+  X.q_extra = io->q_extra;
+  X.no_norm = io->with_norm ? 0 : 1;
+  X.w_out = io->w_out;
+  X.g_out = io->g_out;
+  kb::launch_epilogue(X, (hipStream_t)stream);
+  KB_HIP(hipGetLastError());
+  return 0;
+}
+
 int64_t kb_forward_token(const kb_plan* p) { return p ? p->fwd_token : 0; }
 
 int kb_backward_stats(kb_plan* p, int32_t* n_iter, void* stream) {

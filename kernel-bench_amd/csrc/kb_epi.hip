@@ -208,8 +208,8 @@ __global__ __launch_bounds__(XNT) void epilogue_kernel(EpiParams P) {
   double* qE = wv(P, V_Q);
   estep_vjp(c, nullptr, a_Es1, a_Es2, a_Ebar, qE, nullptr, nullptr, nullptr, nullptr, nullptr);
   for (int s = tid; s < S; s += XNT) {
-    const double dd = (norm >= TINY) ? -scale * exp2(Ev[s]) / ((double)S * norm) : 0.0;
-    qE[s] = a_E[s] + qE[s] + dd;
+    const double dd = (!P.no_norm && norm >= TINY) ? -scale * exp2(Ev[s]) / ((double)S * norm) : 0.0;
+    qE[s] = a_E[s] + qE[s] + dd + (P.q_extra ? P.q_extra[s] : 0.0);
   }
   __syncthreads();
 
@@ -304,6 +304,17 @@ __global__ __launch_bounds__(XNT) void epilogue_kernel(EpiParams P) {
     G_col[s] += a_col[s];
   }
   __syncthreads();
+  if (P.g_out) {  // E adjoint and per-state parameter cotangents only
+    for (int s = tid; s < S; s += XNT) {
+      P.g_out[s] = G_pS[s];
+      P.g_out[(size_t)S + s] = G_pD[s];
+      P.g_out[2 * (size_t)S + s] = G_pL[s];
+      P.g_out[3 * (size_t)S + s] = G_mt[s];
+      P.g_out[4 * (size_t)S + s] = G_col[s];
+      if (P.w_out) P.w_out[s] = tmp[s];
+    }
+    return;
+  }
 
   // theta VJP through log2-softmax of [0, theta] (extract_parameters.py:71-74)
   if (P.statewise) {
@@ -637,8 +648,9 @@ __global__ __launch_bounds__(NT) void epilogue_pre_kernel(EpiParams P) {
     vjp(zero, a_Es1, a_Es2, a_Ebar, gE, wb, pv);
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const double dd = (norm >= TINY) ? -scale * exp2(Ev[k]) / ((double)S * norm) : 0.0;
-      qE[k] = okp[k] ? a_E[colk[k]] + gE[k] + dd : 0.0;
+      const double dd = (!P.no_norm && norm >= TINY) ? -scale * exp2(Ev[k]) / ((double)S * norm) : 0.0;
+      const double qx = (okp[k] && P.q_extra) ? P.q_extra[colk[k]] : 0.0;
+      qE[k] = okp[k] ? a_E[colk[k]] + gE[k] + dd + qx : 0.0;
     }
   }
 
@@ -744,6 +756,20 @@ __global__ __launch_bounds__(NT) void epilogue_pre_kernel(EpiParams P) {
       G_pL[k] = okp[k] ? ws[k] * W3[k] : 0.0;
       G_mt[k] = okp[k] ? wb[k] + a_mt[s] : 0.0;
       G_col[k] = okp[k] ? pv[k] + a_col[s] : 0.0;
+    }
+    if (P.g_out) {  // E adjoint and per-state parameter cotangents only
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        if (!okp[k]) continue;
+        const int s = colk[k];
+        P.g_out[s] = G_pS[k];
+        P.g_out[(size_t)S + s] = G_pD[k];
+        P.g_out[2 * (size_t)S + s] = G_pL[k];
+        P.g_out[3 * (size_t)S + s] = G_mt[k];
+        P.g_out[4 * (size_t)S + s] = G_col[k];
+        if (P.w_out) P.w_out[s] = ws[k];
+      }
+      return;
     }
   }
 

@@ -198,6 +198,11 @@ struct EpiParams {
   float* grad_col;
   double* work;               // [N_WORK, S]
   int* status;                // [0] iterations, [1] failure flag
+  const double* q_extra;      // [S] added to q_E, or null
+  int no_norm;                // 1: q_E without the loss normaliser's term
+  double* w_out;              // [S] E adjoint out (with g_out), or null
+  double* g_out;              // [5, S] cotangents of (pS, pD, pL, mt, col) per state; when set the
+                              // kernel ends after them (no theta / column VJP)
 };
 
 void launch_bwd_consts(const BwdConstArgs& A, hipStream_t st);

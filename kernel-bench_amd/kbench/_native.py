@@ -74,6 +74,18 @@ class KbBackwardIO(ct.Structure):
     ]
 
 
+class KbEAdjointIO(ct.Structure):
+    _fields_ = [
+        ("statewise", i32), ("use_col_weights", i32), ("with_norm", i32), ("bicgstab_max_iter", i32),
+        ("bicgstab_tol", f64), ("bicgstab_breakdown_tol", f64),
+        ("E", vp), ("log_pS", vp), ("log_pD", vp), ("log_pL", vp), ("max_coupling", vp), ("col_log_probs", vp),
+        ("acc", vp), ("q_extra", vp), ("w_out", vp), ("g_out", vp), ("work", vp), ("status", vp),
+    ]
+
+
+E_ADJOINT_WORK_VECTORS = 16
+
+
 def _declare(lib):
     lib.kb_last_error.restype = ct.c_char_p
     lib.kb_abi_version.restype = ct.c_int
@@ -96,6 +108,9 @@ def _declare(lib):
     lib.kb_profile_read.restype = ct.c_int
     lib.kb_forward_token.argtypes = [vp]
     lib.kb_forward_token.restype = ct.c_int64
+    if hasattr(lib, "kb_e_adjoint"):
+        lib.kb_e_adjoint.argtypes = [vp, ct.POINTER(KbEAdjointIO), vp]
+        lib.kb_e_adjoint.restype = ct.c_int
     if hasattr(lib, "kb_backward_stats"):
         lib.kb_backward_stats.argtypes = [vp, P_i32, vp]
         lib.kb_backward_stats.restype = ct.c_int

@@ -359,6 +359,51 @@ class FusedSolver:
             return grad_theta, grad_col, {"active_mask": mask, "acc": acc}
         return grad_theta, grad_col
 
+    def e_adjoint(self, saved, acc, *, q_extra=None, with_norm=False, use_col_weights=False, check_solve=True):
+        """The E adjoint for the cotangents ``acc`` -> (w [S], g [5, S]), float64 (``kb_e_adjoint``).
+
+        Solves (I - J_E^T) w = q at the saved E fixed point, q = acc_E + the (E_s1,
+        E_s2, Ebar) cotangents pulled back to E + ``q_extra`` (+ the loss normaliser's
+        E gradient with ``with_norm``); g holds the per-state cotangents of (log_pS,
+        log_pD, log_pL, max_coupling, col_log_probs) of one E step at (w, acc_Ebar),
+        plus acc's pS, pD, mt and col rows.  ``acc``: [8, S] (pD, pS, E, Ebar, E_s1,
+        E_s2, max_coupling, col).  A failed BiCGSTAB raises ``RuntimeError`` (one
+        status read, skipped with ``check_solve=False``).
+        """
+        lib = N.lib()
+        if not hasattr(lib, "kb_e_adjoint"):
+            raise N.NativeLibraryMissing("libkbench_hip was built without kb_e_adjoint")
+        so, dev, S = self.so, self.device, self.S
+        f64 = dict(device=dev, dtype=torch.float64)
+        acc = acc.detach().to(**f64).contiguous()
+        if tuple(acc.shape) != (8, S):
+            raise ValueError(f"acc must be [8, {S}]")
+        qx = None if q_extra is None else q_extra.detach().to(**f64).reshape(S).contiguous()
+        c = lambda name: saved[name].detach().to(device=dev, dtype=torch.float32).contiguous()
+        tens = {k: c(k) for k in ("E", "log_pS", "log_pD", "log_pL", "max_coupling", "col_log_probs")}
+        if int(tens["E"].numel()) != S:
+            raise NotImplementedError("kb_e_adjoint solves one item row (itemwise=False)")
+        w = torch.empty((S,), **f64)
+        g = torch.empty((5, S), **f64)
+        work = torch.empty((N.E_ADJOINT_WORK_VECTORS * S,), **f64)
+        status = torch.zeros((2,), device=dev, dtype=torch.int32)
+        io = N.KbEAdjointIO(
+            statewise=int(self.statewise), use_col_weights=int(bool(use_col_weights)), with_norm=int(bool(with_norm)),
+            bicgstab_max_iter=int(so["bicgstab_max_iter"]), bicgstab_tol=float(so["bicgstab_tol"]),
+            bicgstab_breakdown_tol=float(so["bicgstab_breakdown_tol"]),
+            E=N.ptr(tens["E"]), log_pS=N.ptr(tens["log_pS"]), log_pD=N.ptr(tens["log_pD"]),
+            log_pL=N.ptr(tens["log_pL"]), max_coupling=N.ptr(tens["max_coupling"]),
+            col_log_probs=N.ptr(tens["col_log_probs"]), acc=N.ptr(acc), q_extra=N.ptr(qx), w_out=N.ptr(w),
+            g_out=N.ptr(g), work=N.ptr(work), status=N.ptr(status))
+        with torch.cuda.device(dev):
+            N.check(lib.kb_e_adjoint(self._plan, ct.byref(io), N.stream_handle(dev)))
+        self._keep_e = (tens, acc, qx, work)
+        if check_solve:
+            it, failed = (int(x) for x in status.cpu())
+            if failed:
+                raise RuntimeError(f"E-adjoint BiCGSTAB solve failed after {it} iterations")
+        return w, g
+
     def backward_stats(self):
         n = ct.c_int32()
         with torch.cuda.device(self.device):

@@ -296,11 +296,16 @@ class HvpPlan:
     """H u of the summed loss at theta (uniform column weights), through the wrappers."""
 
     def __init__(self, plan: SolvePlan, theta, col_weights, saved, *, tangent_sweeps=None, row_classes=False,
-                 graph=False):
+                 graph=False, native_e_adjoint=None):
         if graph and plan.so.self_loop_solver != "neumann":
             raise ValueError("a captured HVP needs the Neumann self-loop solver (GMRES reads its residuals on the host)")
         self.p, self.sv = plan, saved
         self.graph, self._graph = bool(graph), None
+        # the tangent E adjoint in one launch (kb_e_adjoint) for one float32 item row; else
+        # BiCGSTAB over autograd E-step products
+        self.native_e = (native_e_adjoint if native_e_adjoint is not None else
+                         (saved["E"].dtype == torch.float32 and int(saved["E"].shape[0]) == 1
+                          and int(saved["E"].numel()) == plan.S))
         self.theta, self.cw = theta, col_weights
         self.sweeps = int(plan.so.pi_iters if tangent_sweeps is None else tangent_sweeps)
         S = plan.S
@@ -346,6 +351,11 @@ class HvpPlan:
         with torch.enable_grad():
             (hu,) = torch.autograd.grad((self.g1 * u).sum() + self._pair(dcot), self.th, retain_graph=True)
         return hu.reshape(-1)
+
+    def _fused(self):
+        from kbench.runtime import fused_solver
+
+        return fused_solver(self.p.static)
 
     def _replay(self, u):
         """The tangent forward and reverse as one HIP graph: captured on the first call (after one
@@ -452,13 +462,23 @@ class HvpPlan:
         per_row = 1.0 if G == p.n_fam else float(p.n_fam)
         d_survive = -LN2 * (e2 * dE).mean(dim=-1, keepdim=True)
         d_norm_grad = per_row * (e2 * d_survive / (S * survive * survive) - LN2 * e2 * dE / (S * survive))
-        rhs = (dacc.E + eg.aux_t(dacc.Es1, dacc.Es2, dacc.Ebar) + so2(zero, a.Es1, a.Es2, a.Ebar)[0] + d_norm_grad
-               + so2(self.wE, zero, zero, zero)[0])
         so_p = so2(self.wE, zero, zero, a.Ebar)
-        dwE = bicgstab(lambda x: x - eg.jt(x.view_as(E)).reshape(-1), rhs.reshape(-1),
-                       max_iter=int(p.so.bicgstab_max_iter), tol=float(p.so.bicgstab_tol),
-                       breakdown_tol=float(p.so.bicgstab_breakdown_tol)).view_as(E)
-        lin = eg.params_t(dwE, dacc.Ebar)
+        extra = so2(zero, a.Es1, a.Es2, a.Ebar)[0] + d_norm_grad + so2(self.wE, zero, zero, zero)[0]
+        if self.native_e:
+            # q = dacc.E + (Es1, Es2, Ebar cotangents pulled back to E) + extra, solved and pulled back
+            # to the rates by the backward epilogue's float64 BiCGSTAB in one launch
+            z = torch.zeros((S,), dtype=torch.float64, device=E.device)
+            acc8 = torch.stack([z, z, dacc.E.reshape(S).double(), dacc.Ebar.reshape(S).double(),
+                                dacc.Es1.reshape(S).double(), dacc.Es2.reshape(S).double(), z, z])
+            _, gs = self._fused().e_adjoint(self.sv, acc8, q_extra=extra.reshape(S))
+            gs = gs.to(E.dtype)
+            lin = [gs[0].view_as(E), gs[1].view_as(E), gs[2].view_as(E), gs[3].view_as(E), gs[4]]
+        else:
+            rhs = dacc.E + eg.aux_t(dacc.Es1, dacc.Es2, dacc.Ebar) + extra
+            dwE = bicgstab(lambda x: x - eg.jt(x.view_as(E)).reshape(-1), rhs.reshape(-1),
+                           max_iter=int(p.so.bicgstab_max_iter), tol=float(p.so.bicgstab_tol),
+                           breakdown_tol=float(p.so.bicgstab_breakdown_tol)).view_as(E)
+            lin = eg.params_t(dwE, dacc.Ebar)
         return SimpleNamespace(pS=_fold(dacc.pS, lin[0] + so_p[1], G, S), pD=_fold(dacc.pD, lin[1] + so_p[2], G, S),
                                pL=lin[2] + so_p[3], mt=dacc.mt + lin[3] + so_p[4], col=dacc.col + lin[4] + so_p[5])
 

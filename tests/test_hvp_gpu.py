@@ -308,6 +308,59 @@ def test_exact_hvp_graph_replays_match_eager(name, levels):
         assert torch.equal(got, ref), e
 
 
+@pytest.mark.parametrize("statewise", [True, False])
+def test_e_adjoint_entry_solves_the_e_system(statewise):
+    """kb_e_adjoint (FusedSolver.e_adjoint) against the oracle's E-step VJP at the same float32 E*:
+    w - J_E^T w = q with q = acc_E + VJP(acc_Es1, acc_Es2, acc_Ebar) + q_extra, and the parameter
+    cotangents of one E step at (w, acc_Ebar) plus acc's rows (float64, 1e-9 relative)."""
+    from dropin.solve import run_forward
+    from kbench.runtime import fused_solver
+
+    print(f"[e adjoint] config=1 statewise={statewise}", flush=True)
+    static, theta, cw = _static("1", statewise)
+    _, sv = run_forward(static, theta, cw)
+    S = int(sv["E"].numel())
+    g = np.random.default_rng(39)
+    acc = g.normal(size=(8, S)) * 1e-2
+    qx = g.normal(size=S) * 1e-2
+    w, gout = fused_solver(static).e_adjoint(sv, torch.as_tensor(acc).cuda(), q_extra=torch.as_tensor(qx).cuda())
+    torch.cuda.synchronize()
+    w, gout = w.cpu().numpy()[None], gout.cpu().numpy()
+    prob = O.Problem.from_dict(kbtest.problem("1", statewise))
+    row = lambda k: np.broadcast_to(sv[k].detach().double().cpu().numpy().reshape(-1), (S,))[None].copy()
+    E, pS, pD, pL, mt = (row(k) for k in ("E", "log_pS", "log_pD", "log_pL", "max_coupling"))
+    col = sv["col_log_probs"].double().cpu().numpy().reshape(S)
+    vjp = lambda gn, g1, g2, gb: O.e_step_vjp(E, pS, pD, pL, mt, col, prob.tree, False, gn, g1, g2, gb)
+    z = np.zeros((1, S))
+    q = acc[2][None] + vjp(z, acc[4][None], acc[5][None], acc[3][None])[0] + qx[None]
+    res = w - vjp(w, z, z, z)[0] - q
+    print(f"  |q|={np.abs(q).max():.3e} residual={np.abs(res).max():.3e}")
+    assert np.abs(res).max() <= 1e-6 * np.abs(q).max()  # BiCGSTAB tol 1e-7 on the 2-norm
+    _, q0, q1, q3, wbar, gcol = vjp(w, z, z, acc[3][None])
+    want = [q0[0] + acc[1], q1[0] + acc[0], q3[0], wbar[0] + acc[6], gcol + acc[7]]
+    for i, ref in enumerate(want):
+        e = np.abs(gout[i] - ref).max() / max(np.abs(ref).max(), 1e-300)
+        print(f"  cotangent {i}: rel={e:.3e}")
+        assert e <= 1e-9
+
+
+def test_native_tangent_e_adjoint_matches_autograd_bicgstab():
+    """The HVP's tangent E side through kb_e_adjoint agrees with BiCGSTAB over autograd E-step products."""
+    from dropin.hvp import HvpPlan
+    from dropin.solve import plan_of, run_forward
+
+    static, theta, cw = _static("1", True)
+    _, sv = run_forward(static, theta, cw)
+    plan = plan_of(static)
+    u = torch.as_tensor(np.random.default_rng(40).normal(size=tuple(theta.shape)), dtype=theta.dtype).cuda()
+    a = HvpPlan(plan, theta, cw, sv, native_e_adjoint=True)(u.reshape(-1))
+    b = HvpPlan(plan, theta, cw, sv, native_e_adjoint=False)(u.reshape(-1))
+    torch.cuda.synchronize()
+    e = kbtest.norm_rel_t(a, b)
+    print(f"  native vs autograd E side: rel={e:.3e}")
+    assert e <= 1e-4
+
+
 def test_ggn_hvp_is_symmetric_and_psd():
     from dropin.hvp import ggn_hvp
     from dropin.solve import plan_of, run_forward

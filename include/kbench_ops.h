@@ -331,6 +331,23 @@ int kb_rows_sum_into(int32_t dtype, int32_t S, int64_t n, const void* src, void*
 int kb_rows_sum_multi(int32_t dtype, int32_t S, int64_t n, int32_t m, const void* const* a, const void* const* b,
                       void* out, double* work, void* stream);
 
+/*
+ * Column sums of m <= 8 row blocks, each added into its own accumulator:
+ * dst[j][s] += sum over r < n[j] of (a[4j][r*S+s] + ... + a[4j+k[j]-1][r*S+s])
+ * with k[j] in 1..4 addends per block (each row's addends summed first, in
+ * order), rows summed in order in float64 (work: m * max_j ceil(n[j] / 64) * S
+ * doubles, unused when every block has at most 64 rows).  The accumulators
+ * must be distinct.  n, k, a and dst are host arrays (a: 4 entries per block,
+ * device pointers).  A block of one addend gives dst exactly what
+ * kb_rows_sum_into gives.  No reference kernel: it replaces the per-wave
+ * sequences of fixed-order sums (and the adds folding their results) that
+ * stand in for the reference's atomic accumulations into grad_log_pD / pS /
+ * mt / col (pristine wave_backward.py:1747-1853, 2320-2327) and the glue's
+ * bucket reductions (kbench/api/_implicit_grad.py:288-296).
+ */
+int kb_rows_sum_accum(int32_t dtype, int32_t S, int32_t m, const int64_t* n, const int32_t* k, const void* const* a,
+                      void* const* dst, double* work, void* stream);
+
 /* ---- forward tangents (JVP) of the forward maps, for the Newton HVP path ---- */
 
 /*

@@ -1767,6 +1767,83 @@ __global__ __launch_bounds__(256) void rows_sum_multi_stage2(RsmArgs p, const do
   out[(size_t)j * p.S + s] = (T)chunk_sum(work + (size_t)j * p.chunks * p.S, p.S, p.chunks, s);
 }
 
+// Column sums of up to 8 row blocks, each added into its own accumulator row:
+// block j has n[j] rows of k[j] <= 4 addends (each row's addends summed first,
+// in order), summed in row order in float64.  Blocks of one chunk add into
+// their accumulator in stage 1 when no block has more (one launch); otherwise
+// stage 1 writes every block's chunk partials and stage 2 adds them in chunk
+// order, so each accumulator gets dst + sum, as rows_sum_single /
+// rows_sum_stage2 form it.
+struct RsaArgs {
+  int S, m, chunks;  // chunks: the most any block has
+  long long n[8];
+  int k[8];
+  const void* a[8][4];
+  void* dst[8];
+};
+
+template <typename T>
+__device__ __forceinline__ double col_sum_k(const RsaArgs& p, int j, long long r0, long long r1, int s) {
+  const int S = p.S;
+  const T* A0 = static_cast<const T*>(p.a[j][0]);
+  if (p.k[j] == 1) return col_sum<T>(A0, nullptr, S, r0, r1, s);
+  if (p.k[j] == 2) return col_sum<T>(A0, static_cast<const T*>(p.a[j][1]), S, r0, r1, s);
+  const T* A1 = static_cast<const T*>(p.a[j][1]);
+  const T* A2 = static_cast<const T*>(p.a[j][2]);
+  const T* A3 = p.k[j] > 3 ? static_cast<const T*>(p.a[j][3]) : nullptr;
+  double acc = 0.0;
+  long long r = r0;
+  for (; r + 4 <= r1; r += 4) {
+    T x[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const size_t o = (size_t)(r + i) * S + s;
+      x[i][0] = A0[o];
+      x[i][1] = A1[o];
+      x[i][2] = A2[o];
+      x[i][3] = A3 ? A3[o] : T(0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      double v = (double)x[i][0] + (double)x[i][1] + (double)x[i][2];
+      if (A3) v += (double)x[i][3];
+      acc += v;
+    }
+  }
+  for (; r < r1; ++r) {
+    const size_t o = (size_t)r * S + s;
+    double v = (double)A0[o] + (double)A1[o] + (double)A2[o];
+    if (A3) v += (double)A3[o];
+    acc += v;
+  }
+  return acc;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void rows_sum_accum_stage1(RsaArgs p, double* work) {
+  const int s = blockIdx.x * 256 + threadIdx.x;
+  const int j = blockIdx.z, c = blockIdx.y;
+  if (s >= p.S) return;
+  const long long r0 = (long long)c * SUM_CHUNK, r1 = min(p.n[j], r0 + SUM_CHUNK);
+  if (p.chunks == 1) {
+    T* D = static_cast<T*>(p.dst[j]);
+    D[s] = (T)((double)D[s] + col_sum_k<T>(p, j, 0, p.n[j], s));
+    return;
+  }
+  if (r0 >= p.n[j]) return;
+  work[((size_t)j * p.chunks + c) * p.S + s] = col_sum_k<T>(p, j, r0, r1, s);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void rows_sum_accum_stage2(RsaArgs p, const double* work) {
+  const int s = blockIdx.x * 256 + threadIdx.x;
+  const int j = blockIdx.z;
+  if (s >= p.S || p.n[j] <= 0) return;
+  const int nc = (int)((p.n[j] + SUM_CHUNK - 1) / SUM_CHUNK);
+  T* D = static_cast<T*>(p.dst[j]);
+  D[s] = (T)((double)D[s] + chunk_sum(work + (size_t)j * p.chunks * p.S, p.S, nc, s));
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void rows_sum_stage2(int S, int n_chunks, const double* work, T* dst) {
   const int s = blockIdx.x * 256 + threadIdx.x;
@@ -2259,6 +2336,46 @@ int kb_rows_sum_multi(int32_t dtype, int32_t S, int64_t n, int32_t m, const void
     hipLaunchKernelGGL(kbo::rows_sum_multi_stage1<float>, g1, dim3(256), 0, st_of(stream), p, work, (float*)out);
     if (p.chunks > 1)
       hipLaunchKernelGGL(kbo::rows_sum_multi_stage2<float>, g2, dim3(256), 0, st_of(stream), p, work, (float*)out);
+  }
+  KBO_HIP(hipGetLastError());
+  return 0;
+}
+
+int kb_rows_sum_accum(int32_t dtype, int32_t S, int32_t m, const int64_t* n, const int32_t* k, const void* const* a,
+                      void* const* dst, double* work, void* stream) {
+  if (S <= 0 || m <= 0) return 0;
+  if (m > 8) return kb::set_error(KB_ERR_ARG, "at most 8 row blocks per call (m=%d)", m);
+  if (!n || !k || !a || !dst) return kb::set_error(KB_ERR_ARG, "null argument");
+  if (int rc = dtype_ok(dtype)) return rc;
+  kbo::RsaArgs p{};
+  p.S = S;
+  p.m = m;
+  p.chunks = 1;
+  for (int j = 0; j < m; ++j) {
+    if (n[j] < 0) return kb::set_error(KB_ERR_ARG, "row block %d has %lld rows", j, (long long)n[j]);
+    if (k[j] < 1 || k[j] > 4) return kb::set_error(KB_ERR_ARG, "row block %d has %d addends (1..4)", j, k[j]);
+    if (!dst[j]) return kb::set_error(KB_ERR_ARG, "row block %d has no accumulator", j);
+    for (int i = 0; i < j; ++i)
+      if (dst[i] == dst[j]) return kb::set_error(KB_ERR_ARG, "row blocks %d and %d share an accumulator", i, j);
+    p.n[j] = n[j];
+    p.k[j] = k[j];
+    p.dst[j] = dst[j];
+    for (int i = 0; i < k[j]; ++i) {
+      if (!a[4 * j + i] && n[j] > 0) return kb::set_error(KB_ERR_ARG, "row block %d addend %d is null", j, i);
+      p.a[j][i] = a[4 * j + i];
+    }
+    p.chunks = (int)std::max<int64_t>(p.chunks, (n[j] + kbo::SUM_CHUNK - 1) / kbo::SUM_CHUNK);
+  }
+  if (p.chunks > 1 && !work) return kb::set_error(KB_ERR_ARG, "work is required for blocks of more than 64 rows");
+  const dim3 g1((S + 255) / 256, p.chunks, m), g2((S + 255) / 256, 1, m);
+  if (dtype == KB_F64) {
+    hipLaunchKernelGGL(kbo::rows_sum_accum_stage1<double>, g1, dim3(256), 0, st_of(stream), p, work);
+    if (p.chunks > 1)
+      hipLaunchKernelGGL(kbo::rows_sum_accum_stage2<double>, g2, dim3(256), 0, st_of(stream), p, (const double*)work);
+  } else {
+    hipLaunchKernelGGL(kbo::rows_sum_accum_stage1<float>, g1, dim3(256), 0, st_of(stream), p, work);
+    if (p.chunks > 1)
+      hipLaunchKernelGGL(kbo::rows_sum_accum_stage2<float>, g2, dim3(256), 0, st_of(stream), p, (const double*)work);
   }
   KBO_HIP(hipGetLastError());
   return 0;

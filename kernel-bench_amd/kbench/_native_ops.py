@@ -144,6 +144,8 @@ def declare(lib) -> None:
     fn("kb_rows_scatter_add", [i32, i32, i64, vp, vp, vp, vp, i64, vp])
     fn("kb_rows_sum_into", [i32, i32, i64, vp, vp, vp, vp])
     fn("kb_rows_sum_multi", [i32, i32, i64, i32, ct.POINTER(vp), ct.POINTER(vp), vp, vp, vp])
+    fn("kb_rows_sum_accum", [i32, i32, i32, ct.POINTER(i64), ct.POINTER(i32), ct.POINTER(vp), ct.POINTER(vp), vp,
+                             vp])
     fn("kb_e_tangent_fixed_point", [vp, ct.POINTER(KbETanIO), vp])
     fn("kb_dts_tangent", [ct.POINTER(KbDtsTanIO), vp])
     fn("kb_wave_step_tangent", [vp, ct.POINTER(KbWaveTanIO), vp])

@@ -28,7 +28,7 @@ __all__ = [
     "KbPibarVjpIO", "KbWaveBwdIO", "KbWaveStepIO", "KbETanIO", "KbDtsTanIO", "KbWaveTanIO", "KbEStepSoIO",
     "KbWaveSoIO", "KbDtsSoIO",
     "lib", "check", "ptr", "stream", "dtype_code", "defer", "flush", "require_device", "f", "i64", "tree_from_parent",
-    "tree_from_levels", "scatter_add_rows", "sum_rows_into", "static_cached",
+    "tree_from_levels", "scatter_add_rows", "sum_rows_into", "rows_sum_accum", "static_cached",
 ]
 
 check = N.check
@@ -247,6 +247,33 @@ def rows_sum_multi(blocks) -> torch.Tensor:
     b = (ct.c_void_p * m)(*[ptr(y) if y is not None else None for _, y in pairs])
     check(lib().kb_rows_sum_multi(dtype_code(first.dtype), S, n, m, a, b, ptr(out), ptr(work), stream(first.device)))
     return out
+
+
+def rows_sum_accum(blocks) -> None:
+    """dst += column sums of row blocks, all in one launch (two above 64 rows).
+
+    ``blocks``: up to 8 pairs (dst, addends): dst a contiguous [S] tensor (distinct
+    per block), addends a [n, S] tensor or a tuple of up to 4 of them whose sum is
+    the block's rows; rows summed in order in float64, as ``sum_rows_into`` does.
+    """
+    import ctypes as ct
+
+    blocks = [(d, a if isinstance(a, (tuple, list)) else (a,)) for d, a in blocks]
+    m = len(blocks)
+    if m == 0:
+        return
+    first = blocks[0][1][0]
+    S = int(first.shape[1])
+    n = [int(a[0].shape[0]) for _, a in blocks]
+    chunks = max((x + 63) // 64 for x in n)
+    work = torch.empty((m * chunks * S if chunks > 1 else 1,), device=first.device, dtype=torch.float64)
+    addends = []
+    for _, a in blocks:
+        addends += [ptr(x) for x in a] + [None] * (4 - len(a))
+    check(lib().kb_rows_sum_accum(
+        dtype_code(first.dtype), S, m, (ct.c_int64 * m)(*n), (ct.c_int32 * m)(*[len(a) for _, a in blocks]),
+        (ct.c_void_p * (4 * m))(*addends), (ct.c_void_p * m)(*[ptr(d) for d, _ in blocks]), ptr(work),
+        stream(first.device)))
 
 
 def sum_rows_into(dst: torch.Tensor, src: torch.Tensor) -> None:

@@ -94,8 +94,17 @@ def dts_backward_so(Pi, dPi, Pibar, dPibar, v, ws, meta, S, log_pD_param, log_pS
     )
     H.check(H.lib().kb_dts_backward_so(tree.handle, io, H.stream(dev)))
     H.scatter_add_rows(d_rhs, side, lambda: torch.cat((sl64, sr64)), static=(sl64, sr64))
-    H.sum_rows_into(d_grad_col, colrows)
+    # accumulators that are one row of S states take their column sums in one launch
+    blocks, rest = [], []
+    for acc, rows in ((d_grad_col, colrows), (d_grad_pD, pDr), (d_grad_pS, pSr), (d_grad_mt, mtr)):
+        row = acc.numel() == S and acc.is_contiguous() and acc.dtype == dt
+        (blocks if row else rest).append((acc.view(-1) if row else acc, rows))
+    if len({int(a.data_ptr()) for a, _ in blocks}) < len(blocks):
+        rest, blocks = blocks + rest, []
+    H.rows_sum_accum(blocks)
     parent_items = item[start + red]
-    _accum_param(d_grad_pD, pDr, parent_items)
-    _accum_param(d_grad_pS, pSr, parent_items)
-    _accum_param(d_grad_mt, mtr, parent_items)
+    for acc, rows in rest:
+        if acc is d_grad_col:
+            H.sum_rows_into(d_grad_col, colrows)
+        else:
+            _accum_param(acc, rows, parent_items)

@@ -466,11 +466,11 @@ def dts_cross_backward_accum_fused(Pi_star, Pibar_star, v_k, ws, sl, sr, reduce_
 
     # children's adjoint rows: side r of split i goes to row sl[i] (r < n) or sr[i]
     H.scatter_add_rows(accumulated_rhs, side_rows, lambda: torch.cat((sl64, sr64)), static=(sl64, sr64))
+    sums = []  # (accumulator row, contribution rows): one fixed-order launch for all of them
     if accum_param_reductions:
         if glayout == 1 or (glayout == 3 and int(grad_log_pD.shape[0]) == 1):
             # one parameter row: every split adds into it (parallel fixed-order row sum)
-            H.sum_rows_into(grad_log_pD.reshape(-1), param_rows[:n])
-            H.sum_rows_into(grad_log_pS.reshape(-1), param_rows[n:])
+            sums += [(grad_log_pD.reshape(-1), param_rows[:n]), (grad_log_pS.reshape(-1), param_rows[n:])]
         elif glayout == 0:
             H.sum_rows_into(grad_log_pD.reshape(-1), param_sums[:n].reshape(n, 1))
             H.sum_rows_into(grad_log_pS.reshape(-1), param_sums[n:].reshape(n, 1))
@@ -491,7 +491,7 @@ def dts_cross_backward_accum_fused(Pi_star, Pibar_star, v_k, ws, sl, sr, reduce_
         param_pD, param_pS = param_sums[:n].clone(), param_sums[n:].clone()
     if accum_mt_reduction:
         if gmt_layout == 1 and int(grad_mt.shape[0]) == 1:
-            H.sum_rows_into(grad_mt.reshape(-1), mt_rows)
+            sums.append((grad_mt.reshape(-1), mt_rows))
         elif gmt_layout == 1:
             H.scatter_add_rows(grad_mt.reshape(-1), mt_rows,
                                lambda: torch.cat((item.index_select(0, sl64), item.index_select(0, sr64))),
@@ -502,6 +502,11 @@ def dts_cross_backward_accum_fused(Pi_star, Pibar_star, v_k, ws, sl, sr, reduce_
             H.sum_rows_into(grad_mt.reshape(1, 1), tmp.reshape(S, 1))
         else:
             H.sum_rows_into(grad_mt.reshape(-1), mt_rows)
+    if len({int(d.data_ptr()) for d, _ in sums}) == len(sums):
+        H.rows_sum_accum(sums)
+    else:  # accumulators that share storage: one at a time
+        for d, rows in sums:
+            H.sum_rows_into(d, rows)
     return _cross_result(output_pibar_ud, output_pibar_side_active, ud, A, side_active, gPl, gPr, param_pD, param_pS)
 
 

@@ -274,9 +274,20 @@ class SolvePlan:
         An entry of ``aw`` may be a pair of tensors whose sum is the contribution.
         """
         if G == 1:
-            col_sums = H.rows_sum_multi(aw)                  # [6, S]: one reduction for all buckets
+            # every target's column sums added in one launch; [G, 1] targets (one value per
+            # item row) and targets of another dtype go through a state row first
+            S = int((aw[0][0] if isinstance(aw[0], (tuple, list)) else aw[0]).shape[1])
+            blocks, later = [], []
             for acc, ks in targets:
-                s = col_sums[ks[0]] if len(ks) == 1 else col_sums[ks[0]] + col_sums[ks[1]]
+                add = tuple(x for k in ks for x in (aw[k] if isinstance(aw[k], (tuple, list)) else (aw[k],)))
+                if acc.numel() == S and acc.is_contiguous() and acc.dtype == add[0].dtype:
+                    blocks.append((acc.view(-1), add))
+                else:
+                    tmp = torch.zeros((S,), dtype=add[0].dtype, device=add[0].device)
+                    blocks.append((tmp, add))
+                    later.append((acc, tmp))
+            H.rows_sum_accum(blocks)
+            for acc, s in later:
                 if acc.ndim == 2 and int(acc.shape[1]) == 1:
                     acc[0, 0] += s.sum()
                 else:

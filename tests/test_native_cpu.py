@@ -50,6 +50,18 @@ def test_host_only_entry_points():
     # argument checks that precede any device call
     assert lib.kb_rows_sum_multi(0, 4, 2, 9, None, None, None, None, None) != 0
     assert b"at most 8" in lib.kb_last_error()
+    import ctypes as ct
+
+    n, k = (ct.c_int64 * 2)(3, 3), (ct.c_int32 * 2)(1, 5)
+    a, d = (ct.c_void_p * 8)(*([16] * 8)), (ct.c_void_p * 2)(32, 64)
+    assert lib.kb_rows_sum_accum(0, 4, 9, n, k, a, d, None, None) != 0
+    assert b"at most 8" in lib.kb_last_error()
+    assert lib.kb_rows_sum_accum(0, 4, 2, n, k, a, d, None, None) != 0
+    assert b"addends" in lib.kb_last_error()
+    k[1] = 1
+    d[1] = 32
+    assert lib.kb_rows_sum_accum(0, 4, 2, n, k, a, d, None, None) != 0
+    assert b"share an accumulator" in lib.kb_last_error()
 
 
 def test_wrappers_refuse_host_tensors():

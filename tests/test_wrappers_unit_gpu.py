@@ -484,6 +484,32 @@ def test_e_step_autograd_matches_oracle(dt, use_col):
 
 @pytest.mark.parametrize("n", [1, 64, 300])
 @pytest.mark.parametrize("dt", [torch.float32, torch.float64])
+def test_rows_sum_accum_adds_float64_column_sums(n, dt):
+    """kb_rows_sum_accum: blocks of 1..4 addends and different row counts added into their own
+    accumulators, against float64 sums; one addend gives bitwise what kb_rows_sum_into gives."""
+    from kbench.core.kernels import _hip as H
+
+    g = torch.Generator(device="cpu").manual_seed(n + 1)
+    S = 37
+    rows = lambda m: torch.randn((m, S), generator=g, dtype=torch.float64).to(device="cuda", dtype=dt)
+    xs = [rows(n) for _ in range(7)] + [rows(2 * n + 5)]
+    groups = [(xs[0],), (xs[1], xs[2]), (xs[3], xs[4], xs[5]), (xs[0], xs[2], xs[4], xs[6]), (xs[7],)]
+    base = [torch.randn((S,), generator=g, dtype=torch.float64).to(device="cuda", dtype=dt) for _ in groups]
+    dst = [b.clone() for b in base]
+    H.rows_sum_accum(list(zip(dst, groups)))
+    one = base[4].clone()
+    H.sum_rows_into(one, xs[7])
+    torch.cuda.synchronize()
+    assert torch.equal(dst[4], one)
+    for d, b, grp in zip(dst, base, groups):
+        ref = b.double() + sum(x.double() for x in grp).sum(dim=0)
+        err = float((d.double() - ref).abs().max() / ref.abs().max())
+        print(f"[rows-sum-accum] n={n} k={len(grp)} dtype={dt} rel={err:.3e}")
+        assert err <= (1e-6 if dt == torch.float32 else 1e-13)
+
+
+@pytest.mark.parametrize("n", [1, 64, 300])
+@pytest.mark.parametrize("dt", [torch.float32, torch.float64])
 def test_rows_sum_multi_matches_float64_column_sums(n, dt):
     """kb_rows_sum_multi: column sums of single and paired row blocks, against float64 sums, and run
     twice bitwise (fixed order)."""

@@ -68,6 +68,9 @@ def parse():
     ap.add_argument("--verbose", action="store_true")
     ap.add_argument("--hvp-layout", choices=("both", "levels"), default="both",
                     help="--workload hvp: time the size waves and the level waves, or the level waves only")
+    ap.add_argument("--hvp-variants", choices=("all", "fast"), default="all",
+                    help="--workload hvp: also time the row-by-row and the uncaptured class HVPs (all), or only "
+                         "the class HVP replayed as a graph (fast)")
     ap.add_argument("--workload", choices=("solve", "glue", "hvp"), default="solve",
                     help="solve: whole-pass driver (the metric); glue: only the per-call drop-in timings; "
                          "hvp: exact Hessian-vector products of the config-5 Newton-CG setup")
@@ -284,8 +287,10 @@ def bench_hvp(args, static, theta, cw, summ, static_levels) -> None:
     ms_size = cache_size = None
     if args.hvp_layout == "both":
         ms_size, cache_size = timed(static)
-    ms_rows, cache_rows = timed(static_levels)
-    ms_eager, _ = timed(static_levels, row_classes=True)
+    ms_rows = cache_rows = ms_eager = None
+    if args.hvp_variants == "all":
+        ms_rows, cache_rows = timed(static_levels)
+        ms_eager, _ = timed(static_levels, row_classes=True)
     ms, cache_ms = timed(static_levels, row_classes=True, graph=True)
     print(json.dumps({
         "metric": "exact Hessian-vector product ms (config 5: per-species theta, forward tangent + tangent adjoint)",
@@ -298,8 +303,8 @@ def bench_hvp(args, static, theta, cw, summ, static_levels) -> None:
                                 "graph"),
                    "S": summ["S"], "C": summ["C"], "point_cache_ms": round(cache_ms, 3)},
         "ms_per_newton_cg_step_50_hvps": round(50 * ms, 2),
-        "row_by_row": {"ms": round(ms_rows, 4), "point_cache_ms": round(cache_rows, 3)},
-        "row_classes_without_graph_ms": round(ms_eager, 4),
+        "row_by_row": None if ms_rows is None else {"ms": round(ms_rows, 4), "point_cache_ms": round(cache_rows, 3)},
+        "row_classes_without_graph_ms": None if ms_eager is None else round(ms_eager, 4),
         "size_waves": None if ms_size is None else {"n_waves": summ["n_waves"], "ms": round(ms_size, 4),
                                                     "point_cache_ms": round(cache_size, 3)},
     }))

@@ -610,12 +610,12 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
     for (int e : euler)
       if (e & 1) post.push_back(e >> 1);
     rc |= upload(&p->d_post, post);
-    if (S > 2048 && S <= 8192) {
+    if (S > 1024 && S <= 8192) {
       // owner-major position tables of bwd_row_large_kernel (kb::OmTab)
-      const int ld = kb::kb_large_ld(S), cpt = ld / 1024, zero = ld;
+      const int ld = kb::kb_large_ld(S), nt = kb::kb_large_nt(S), cpt = ld / nt, zero = ld;
       std::vector<int> om((size_t)kb::KB_OM_TABS * ld);
       for (int i = 0; i < ld; ++i) {
-        const size_t o = (size_t)(i % cpt) * 1024 + i / cpt;
+        const size_t o = (size_t)(i % cpt) * nt + i / cpt;
         const bool ok = i < S;
         om[kb::OMT_C1 * (size_t)ld + o] = ok ? c1pos[i] : -1;
         om[kb::OMT_C2 * (size_t)ld + o] = ok ? c2pos[i] : -1;
@@ -823,12 +823,19 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   const char* vv = getenv("KB_BWD_VARIANT");
   const int variant = (vv && vv[0] == '2') ? 2 : (vv && vv[0] == '0') ? 0 : 1;
   // rows of 2049..8192 states: the low-register kernel (KB_BWD_LARGE=0: the
-  // general row kernel)
+  // general row kernel; =2: also rows of 1025..2048 states)
   const char* lv = getenv("KB_BWD_LARGE");
-  const int large = (lv && lv[0] == '0') ? 0 : 1;
+  const int large = (lv && lv[0] == '0') ? 0 : (lv && lv[0] == '2') ? 2 : 1;
   const int nb_max = std::max(1, n_cu * kb::bwd_blocks_per_cu(S, use_col, variant, large));
   p->b_variant = variant;
   p->b_large = large;
+  // owner-major constants of the low-register kernel (allocated once, when it first runs)
+  if (kb::kb_use_large(S, large) && !p->b_om_const) {
+    const size_t n_om = (size_t)kb::KB_OM_CONSTS * kb::kb_large_ld(S);
+    if (alloc(&p->b_om_const, n_om)) return KB_ERR_HIP;
+    p->owned.push_back(p->b_om_const);
+    KB_HIP(hipMemset(p->b_om_const, 0, n_om * sizeof(float)));
+  }
   if (p->b_contrib && p->b_nb_max == nb_max && p->b_slot == bwd_slot_floats(S, large)) return 0;
   p->b_slot = bwd_slot_floats(S, large);
   p->b_nb_max = nb_max;
@@ -872,11 +879,6 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   rc |= alloc(&p->b_mt, S);
   rc |= alloc(&p->b_col, S);
   rc |= alloc(&p->b_acc_pre, (size_t)8 * S);
-  if (S > 2048 && S <= 8192) {
-    rc |= alloc(&p->b_om_const, (size_t)kb::KB_OM_CONSTS * kb::kb_large_ld(S));
-    if (!rc) KB_HIP(hipMemset(p->b_om_const, 0, (size_t)kb::KB_OM_CONSTS * kb::kb_large_ld(S) * sizeof(float)));
-    p->owned.push_back(p->b_om_const);
-  }
   for (void* ptr : {(void*)p->b_Ebar, (void*)p->b_E, (void*)p->b_mt, (void*)p->b_col, (void*)p->b_acc_pre,
                     (void*)p->b_staging, (void*)p->b_split_on, (void*)p->b_mask, (void*)p->b_contrib,
                     (void*)p->b_rhs0, (void*)p->b_rhsc, (void*)p->b_cls_active, (void*)p->b_ck_any, (void*)p->b_m_mask,

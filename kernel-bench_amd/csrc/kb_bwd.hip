@@ -1068,8 +1068,8 @@ __global__ void bwd_consts_kernel(BwdConstArgs A) {
   A.mt_pre[i] = A.mt[s];
   A.col_pre[i] = A.col[s];
   if (A.om) {
-    const int cpt = A.S <= 4096 ? 4 : 8, ld = 1024 * cpt;
-    float* o = A.om + (i % cpt) * 1024 + i / cpt;
+    const int ld = kb_large_ld(A.S), nt = kb_large_nt(A.S), cpt = ld / nt;
+    float* o = A.om + (i % cpt) * nt + i / cpt;
     o[OMC_DL * ld] = dl;
     o[OMC_EBAR * ld] = A.Ebar[s];
     o[OMC_E * ld] = A.E[s];

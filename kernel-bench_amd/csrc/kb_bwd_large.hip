@@ -97,9 +97,12 @@ __device__ __forceinline__ void st4_add(float* p, float4 b, const float (&x)[4])
   *reinterpret_cast<float4*>(p) = b;
 }
 
-template <int CPT, bool WEIGHTED>
-__global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int first, int n_rows) {
-  constexpr int NT = 1024;
+// NT threads (1024, or 512 for rows of at most 2048 states) own CPT positions
+// each; at most 128 VGPRs, so 16 wavefronts per CU are resident (two
+// workgroups of 512).
+template <int NT, int CPT, bool WEIGHTED>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4)))
+void bwd_row_large_kernel(BwdParams P, int first, int n_rows) {
   constexpr int MAXS = NT * CPT;
   constexpr int LD = MAXS + 64;  // [MAXS] is the padding slot, kept at 0
   constexpr int NW = NT / 64;
@@ -107,6 +110,7 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
   constexpr int SEGSH = CPT == 4 ? 8 : 9;  // log2 of the positions per wavefront
   constexpr int NG = CPT / 4;              // groups of four own positions
   static_assert(CPT == 4 || CPT == 8, "4 or 8 positions per thread");
+  static_assert(NT == 512 || NT == 1024, "512 or 1024 threads");
   __shared__ float L[4 * LD];
   __shared__ float wA[2 * NW], wB[2 * NW];
   __shared__ float wMk[NW];
@@ -702,31 +706,36 @@ __global__ __launch_bounds__(1024) void bwd_row_large_kernel(BwdParams P, int fi
   }  // rows
 }
 
-#define KB_BWD_LARGE_CASE(CPT_)                                                                             \
-  if (S <= 1024 * CPT_) {                                                                                   \
+#define KB_BWD_LARGE_CASE(NT_, CPT_)                                                                        \
+  if (S <= NT_ * CPT_) {                                                                                    \
     if (P.use_col)                                                                                          \
-      hipLaunchKernelGGL((bwd_row_large_kernel<CPT_, true>), dim3(nb), dim3(1024), 0, st, P, first, W);     \
+      hipLaunchKernelGGL((bwd_row_large_kernel<NT_, CPT_, true>), dim3(nb), dim3(NT_), 0, st, P, first, W); \
     else                                                                                                    \
-      hipLaunchKernelGGL((bwd_row_large_kernel<CPT_, false>), dim3(nb), dim3(1024), 0, st, P, first, W);    \
+      hipLaunchKernelGGL((bwd_row_large_kernel<NT_, CPT_, false>), dim3(nb), dim3(NT_), 0, st, P, first, W);\
     return true;                                                                                            \
   }
 
 bool launch_bwd_large(const BwdParams& P, int first, int W, int nb, hipStream_t st) {
   const int S = P.S;
   if (!kb_use_large(S, P.large)) return false;
-  KB_BWD_LARGE_CASE(4)
-  KB_BWD_LARGE_CASE(8)
+  // the shape kb_large_nt / kb_large_ld give the owner-major tables
+  if (kb_large_nt(S) == 512) {
+    KB_BWD_LARGE_CASE(512, 4)
+  }
+  KB_BWD_LARGE_CASE(1024, 4)
+  KB_BWD_LARGE_CASE(1024, 8)
   return false;
 }
 
 int bwd_large_blocks_per_cu(int S, int use_col) {
   int n = 0;
-  if (S <= 4096)
-    (void)(use_col ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, bwd_row_large_kernel<4, true>, 1024, 0)
-                   : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, bwd_row_large_kernel<4, false>, 1024, 0));
+  auto occ = [&](auto kernel, int nt) { (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, nt, 0); };
+  if (kb_large_nt(S) == 512)
+    use_col ? occ(bwd_row_large_kernel<512, 4, true>, 512) : occ(bwd_row_large_kernel<512, 4, false>, 512);
+  else if (S <= 4096)
+    use_col ? occ(bwd_row_large_kernel<1024, 4, true>, 1024) : occ(bwd_row_large_kernel<1024, 4, false>, 1024);
   else
-    (void)(use_col ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, bwd_row_large_kernel<8, true>, 1024, 0)
-                   : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, bwd_row_large_kernel<8, false>, 1024, 0));
+    use_col ? occ(bwd_row_large_kernel<1024, 8, true>, 1024) : occ(bwd_row_large_kernel<1024, 8, false>, 1024);
   return n > 0 ? n : 1;
 }
 

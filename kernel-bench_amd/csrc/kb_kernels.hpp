@@ -171,8 +171,14 @@ constexpr int KB_CHUNK0 = 8;
 // kb_large_ld(S) floats (8 bucket rows, then the row's split term, Pi* and
 // Pibar*); other row kernels use 8 rows of S.
 constexpr int KB_LARGE_SLOT_ROWS = 11;
-inline bool kb_use_large(int S, int large) { return large && S > 2048 && S <= 8192; }
-inline int kb_large_ld(int S) { return S <= 4096 ? 4096 : 8192; }
+// large = 1: rows of 2049..8192 states; large = 2: also rows of 1025..2048
+// states (512 threads x 4 positions)
+inline bool kb_use_large(int S, int large) {
+  return (large && S > 2048 && S <= 8192) || (large == 2 && S > 1024 && S <= 2048);
+}
+// threads and positions (owner-major row length) of the low-register kernel's shape for S states
+__host__ __device__ inline int kb_large_nt(int S) { return S <= 2048 ? 512 : 1024; }
+__host__ __device__ inline int kb_large_ld(int S) { return S <= 2048 ? 2048 : (S <= 4096 ? 4096 : 8192); }
 
 struct EpiParams {
   TreeDev tr;

@@ -238,10 +238,11 @@ def test_large_tree_forward_kernels_agree(weighted, monkeypatch):
     assert rel <= 1e-6
 
 
-@pytest.mark.parametrize("leaves,weighted", [(2048, False), (4096, True)])
+@pytest.mark.parametrize("leaves,weighted", [(1024, True), (2048, False), (4096, True)])
 def test_large_tree_backward_kernels_agree(leaves, weighted, monkeypatch):
-    """S = 4095 and 8191: the low-register backward row kernel against the general one
-    (KB_BWD_LARGE=0) on the same forward; each run twice is bitwise reproducible."""
+    """S = 2047, 4095 and 8191: the low-register backward row kernel (at S = 2047 its 512-thread shape,
+    KB_BWD_LARGE=2) against the general one (KB_BWD_LARGE=0) on the same forward; each run twice is
+    bitwise reproducible."""
     from kbench.fused import FusedSolver, problem_to_captured
     from kbench.runtime import make_static
 
@@ -256,15 +257,16 @@ def test_large_tree_backward_kernels_agree(leaves, weighted, monkeypatch):
     cw = torch.from_numpy(cw32).cuda()
     _, saved = solver.run_forward(theta, cw)
     runs = {}
-    for large in ("1", "0", "1"):
+    on = "2" if leaves <= 1024 else "1"
+    for large in (on, "0", on):
         monkeypatch.setenv("KB_BWD_LARGE", large)
         gt, gc = solver.run_backward(theta, cw, saved)
         torch.cuda.synchronize()
         if large in runs:
             assert torch.equal(gt, runs[large][0]) and torch.equal(gc, runs[large][1])
         runs[large] = (gt.clone(), gc.clone())
-    rt = kbtest.norm_rel(runs["1"][0].cpu().numpy(), runs["0"][0].cpu().numpy())
-    rc = kbtest.norm_rel(runs["1"][1].cpu().numpy(), runs["0"][1].cpu().numpy())
+    rt = kbtest.norm_rel(runs[on][0].cpu().numpy(), runs["0"][0].cpu().numpy())
+    rc = kbtest.norm_rel(runs[on][1].cpu().numpy(), runs["0"][1].cpu().numpy())
     print(f"  low-register vs general kernel: grad_theta rel={rt:.3e} grad_col rel={rc:.3e}")
     assert rt <= 1e-5 and rc <= 1e-5
 

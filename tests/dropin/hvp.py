@@ -231,10 +231,14 @@ class _ClassSchedule:
         active = torch.zeros((plan.C,), dtype=torch.bool, device=dev)
         for w, _, _, mask in waves:
             active[w.ws: w.ws + w.W] = mask
-        layout, rc_of_row, rrep = synth.row_classes(st.wave_layout, st.rate_item_idx, active=active)
-        rp = self.rplan = SolvePlan(_class_static(st, layout, rrep), kernels=plan.k)
-        rc_of_row = torch.from_numpy(rc_of_row).to(dev)
-        rrep = torch.from_numpy(rrep).to(dev)
+        if bool(active.all()):  # no member dropped: the reverse classes are the forward classes
+            rp = self.rplan = self.fplan
+            rc_of_row, rrep = fc_of_row, frep
+        else:
+            layout, rc_of_row, rrep = synth.row_classes(st.wave_layout, st.rate_item_idx, active=active)
+            rp = self.rplan = SolvePlan(_class_static(st, layout, rrep), kernels=plan.k)
+            rc_of_row = torch.from_numpy(rc_of_row).to(dev)
+            rrep = torch.from_numpy(rrep).to(dev)
         self.fc_of_rc = fc_of_row.index_select(0, rrep)
         self.Pi = saved["pi_wave"].index_select(0, rrep)
         self.Pibar = saved["pibar_wave"].index_select(0, rrep)

@@ -276,6 +276,38 @@ def test_exact_hvp_config3_on_row_classes_matches_row_by_row():
     assert e <= 1e-4
 
 
+@pytest.mark.parametrize("threshold", [0.3, 0.5])
+def test_exact_hvp_row_classes_with_pruned_rows(threshold):
+    """Adjoint pruning that drops rows at the point (config 1: 11 and 100 rows in the oracle): the reverse
+    classes split forward classes by the active flag (more reverse than forward classes) and the class
+    HVP still equals the row-by-row one."""
+    from dropin.hvp import HvpPlan
+    from dropin.solve import plan_of, run_forward
+    from kbench import synth
+    from kbench.fused import problem_to_captured
+    from kbench.runtime import make_static
+
+    print(f"[hvp pruned] config=1 adjoint_pruning_threshold={threshold}", flush=True)
+    p, _ = synth.level_waves(kbtest.problem("1", True))
+    cap = problem_to_captured(p)
+    cap["meta"]["solver_options"] = dict(cap["meta"]["solver_options"], adjoint_pruning_threshold=threshold)
+    static = make_static(cap, "cuda")
+    theta, cw = cap["inputs"]["theta"].cuda(), cap["inputs"]["col_weights"].cuda()
+    _, sv = run_forward(static, theta, cw)
+    plan = plan_of(static)
+    u = torch.as_tensor(np.random.default_rng(41).normal(size=tuple(theta.shape)), dtype=theta.dtype).cuda()
+    ref = HvpPlan(plan, theta, cw, sv)(u.reshape(-1))
+    hc = HvpPlan(plan, theta, cw, sv, row_classes=True)
+    got = hc(u.reshape(-1))
+    torch.cuda.synchronize()
+    n_off = sum(int((~m).sum()) for _, _, _, m in hc.waves)
+    e = kbtest.norm_rel_t(got, ref)
+    print(f"  rows {plan.C} inactive {n_off}; forward classes {hc.cls.fplan.C}, reverse classes {hc.cls.rplan.C};"
+          f" rel={e:.3e}")
+    assert n_off > 0 and hc.cls.rplan.C > hc.cls.fplan.C
+    assert e <= 1e-4
+
+
 @pytest.mark.parametrize("name,levels", [("1", False), ("3", True)])
 def test_exact_hvp_graph_replays_match_eager(name, levels):
     """HvpPlan(graph=True): the tangent forward and reverse captured once and replayed; every replay

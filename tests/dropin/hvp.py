@@ -36,8 +36,12 @@ the right-hand sides it propagates, and members of a class whose active flags
 agree, and whose children along each split agree in class and flag, share
 one adjoint map; so it runs on one row per such class (the classes of
 ``row_classes`` with the point's active mask), from the members' summed
-adjoints and root seeds (fixed-order sums).  The bucket sums, and through them
-H u, are those of the row-by-row reverse up to the order of the sums.
+adjoints and root seeds (fixed-order sums).  On the classes the reverse's
+second-order terms, which read the point adjoint and the tangent rows but not
+the tangent adjoint, run first as one launch each over all split rows; the
+level loop then carries the first-order adjoint only.  The bucket sums, and
+through them H u, are those of the row-by-row reverse up to the order of the
+sums.
 
 HIP graph (``HvpPlan(..., graph=True)``): for a fixed point the tangent
 forward and reverse launch the same kernels on the same buffers for every u,
@@ -258,6 +262,25 @@ class _ClassSchedule:
             mask = on[w.ws: w.ws + w.W].contiguous()
             dts = rp._dts(w, self.Pi, self.Pibar, c, active=mask) if w.split else None
             self.cache.append((w, V[w.ws: w.ws + w.W], dts, mask))
+        # every split row as one wave (the class layout is level ordered: the leaf level first, then
+        # the split levels, contiguous), for the second-order terms that need no level order
+        fwd = self.cache[::-1]
+        self.leaf = [(w, v) for w, v, _, _ in fwd if not w.split]
+        sw = [(w, dts) for w, _, dts, _ in fwd if w.split]
+        self.split_all = None
+        if sw:
+            ws1 = sw[0][0].ws
+            if any(a.ws + a.W != b_.ws for (a, _), (b_, _) in zip(sw, sw[1:])) or sw[-1][0].ws + sw[-1][0].W != rp.C:
+                raise ValueError("the class layout's split waves are not contiguous")
+            dt = self.Pi.dtype
+            lsp = torch.cat([w.lsp.reshape(-1).to(dt) if w.lsp is not None else
+                             torch.zeros((int(w.sl.numel()),), dtype=dt, device=dev) for w, _ in sw])
+            sl, sr = torch.cat([w.sl for w, _ in sw]), torch.cat([w.sr for w, _ in sw])
+            red = torch.cat([w.reduce_idx + (w.ws - ws1) for w, _ in sw])
+            self.split_all = SimpleNamespace(
+                ws=ws1, W=rp.C - ws1, sl=sl, sr=sr, reduce_idx=red, lsp=lsp, v=V[ws1:],
+                dts=torch.cat([dts for _, dts in sw]),
+                meta={"start": ws1, "W": rp.C - ws1, "sl": sl, "sr": sr, "reduce_idx": red, "log_split_probs": lsp})
 
 
 class _EGraph:
@@ -376,6 +399,69 @@ class HvpPlan:
         self._graph.replay()
         return self._graph_out
 
+    def _class_reverse(self, d, dPi, dPibar, d_rhs, dacc, targets, cst_so):
+        """The tangent reverse on the reverse classes, in two parts.
+
+        The second-order terms (``compute_dts_tangent``, ``dts_backward_so``,
+        ``wave_backward_so``) read the point adjoint v and the tangent rows, not the tangent
+        adjoint, so they run first, each as one launch over all split rows (and the leaf
+        level): the split terms' contributions go into the children's right-hand sides, the
+        self-loop contraction into every row's own.  The level loop then carries only the
+        first-order adjoint (Neumann series, split adjoint, Pibar VJP).  The right-hand side
+        a level's solve reads is the same sum as in the level-by-level order.
+        """
+        k = self.cls
+        p, sv, b = k.rplan, self.sv, self.tan.base
+        S, G, h, so = p.S, self.G, p.h, p.so
+        Pi, Pibar, prm, col = k.Pi, k.Pibar, k.prm, sv["col_log_probs"]
+        c1, c2 = h["node_child1"], h["node_child2"]
+        sa = k.split_all
+        parts = [(w.ws, w.W, v, None, None, True) for w, v in k.leaf]
+        if sa is not None:
+            d_dts = p.k.compute_dts_tangent(Pi, Pibar, dPi, dPibar, sa.sl, sa.sr, c1, c2, sa.W, sa.reduce_idx,
+                                            b.pd_par, b.ps_par, d.dpd_par, d.dps_par, sa.dts, p.item_idx,
+                                            log_split_probs=sa.lsp, item_offset=sa.ws)
+            p.k.dts_backward_so(
+                Pi, dPi, Pibar, dPibar, sa.v, sa.ws, sa.meta, S, b.pd_par, b.ps_par, d.dpd_par, d.dps_par, b.mc,
+                d.dMC, col, c1, c2, p.topo[0], p.topo[3], prm, p.item_idx, d_rhs, dacc.pD, dacc.pS, dacc.mt,
+                dacc.col, use_col_weights=False, **p.levels)
+            parts.append((sa.ws, sa.W, sa.v, sa.dts, d_dts, False))
+        for ws, W, v, dts, d_dts, leaf_term in parts:
+            seed, *so_aw = p.k.wave_backward_so(
+                Pi, dPi, Pibar, dPibar, v, ws, W, S, prm, *cst_so, col, c1, c2, p.topo[0], p.topo[3], dts, d_dts,
+                leaf_state_idx=p.leaf_idx, leaf_logp=b.leaf, dleaf_logp=d.dleaf, item_idx=p.item_idx,
+                has_leaf_term=leaf_term, use_col_weights=False, d_rhs=d_rhs)
+            d_rhs.narrow(0, ws, W).copy_(seed)
+            p._fold_buckets(so_aw, targets, SimpleNamespace(ws=ws, W=W), G)
+        for w, _, dts, mask in k.cache:
+            dv, *lin_aw = p.k.wave_backward_uniform_fused(
+                Pi, Pibar, w.ws, w.W, S, dts, d_rhs.narrow(0, w.ws, w.W), b.mc, b.dl, b.ebar, b.e, b.sl1, b.sl2, col,
+                c1, c2, None, neumann_terms=int(so.neumann_terms), leaf_state_idx=p.leaf_idx, leaf_logp=b.leaf,
+                has_leaf_term=w.leaf_term, active_mask=mask, node_parent=p.topo[0], max_ancestor_depth=p.topo[3],
+                pibar_row_max=prm, item_idx=p.item_idx, item_indexed_consts=True, grad_col_log_probs=dacc.col,
+                use_col_weights=False, self_loop_solver=so.self_loop_solver, **p.levels)
+            p._fold_buckets(lin_aw, targets, w, G)
+            if w.split:
+                self._split_adjoint(p, w, dv, mask, d_rhs, dacc, Pi, Pibar, prm, col)
+        return dacc
+
+    def _split_adjoint(self, p, w, dv, mask, d_rhs, dacc, Pi, Pibar, prm, col):
+        """The split wave's cross adjoint and Pibar VJP of the tangent adjoint dv into the children."""
+        b, h, so, S = self.tan.base, p.h, p.so, p.S
+        lsp = w.lsp if w.lsp is not None else w.sl.new_zeros((int(w.sl.numel()),), dtype=Pi.dtype)
+        ud, A, side_on, _, _ = p.k.dts_cross_backward_accum_fused(
+            Pi, Pibar, dv, w.ws, w.sl, w.sr, w.reduce_idx, lsp, b.pd_par, b.ps_par, h["node_child1"],
+            h["node_child2"], d_rhs, S, active_mask=mask, merge_s_term=True, grad_log_pD=dacc.pD,
+            grad_log_pS=dacc.pS, grad_mt=dacc.mt, accum_param_reductions=True, accum_mt_reduction=True,
+            output_pibar_ud=True, output_pibar_side_active=True,
+            pibar_side_threshold=so.pibar_side_threshold, mt_squeezed=b.mc, pibar_row_max=prm,
+            grad_mt_two_stage=bool(dacc.mt.ndim == 2 and int(dacc.mt.shape[0]) == 1),
+            grad_mt_two_stage_tile_splits=128, skip_inactive_pibar_output_zero=True, item_idx=p.item_idx)
+        p.k.uniform_cross_pibar_vjp_tree_from_ud_fused(
+            Pi, col, ud, A, w.sl, w.sr, d_rhs, S, active_mask=mask, reduce_idx=w.reduce_idx,
+            pibar_row_max=prm, skip_zero_sides=True, side_active=side_on, grad_col_log_probs=dacc.col,
+            use_col_weights=False, side_active_threshold=so.pibar_side_threshold, **p.levels)
+
     def _tangent_reverse(self, u):
         """(constant tangents, tangent cotangents accumulated over the waves) along u."""
         sv, a = self.sv, self.acc
@@ -407,6 +493,8 @@ class HvpPlan:
         targets = ((dacc.pD, (0,)), (dacc.pS, (3,)), (dacc.E, (0, 2)), (dacc.Ebar, (1,)), (dacc.Es1, (5,)),
                    (dacc.Es2, (4,)), (dacc.mt, (2,)))
         cst_so = (b.mc,) + self.tan.interleaved(d)[2:]  # the contraction takes mt without its tangent
+        if k is not None:
+            return d, self._class_reverse(d, dPi, dPibar, d_rhs, dacc, targets, cst_so)
         so = p.so
         for w, v, dts, mask in waves:
             d_dts = None
@@ -427,19 +515,7 @@ class HvpPlan:
                 **p.levels)
             p._fold_buckets(list(zip(so_aw, lin_aw)), targets, w, G)
             if w.split:
-                lsp = w.lsp if w.lsp is not None else w.sl.new_zeros((int(w.sl.numel()),), dtype=Pi.dtype)
-                ud, A, side_on, _, _ = p.k.dts_cross_backward_accum_fused(
-                    Pi, Pibar, dv, w.ws, w.sl, w.sr, w.reduce_idx, lsp, b.pd_par, b.ps_par, h["node_child1"],
-                    h["node_child2"], d_rhs, S, active_mask=mask, merge_s_term=True, grad_log_pD=dacc.pD,
-                    grad_log_pS=dacc.pS, grad_mt=dacc.mt, accum_param_reductions=True, accum_mt_reduction=True,
-                    output_pibar_ud=True, output_pibar_side_active=True,
-                    pibar_side_threshold=so.pibar_side_threshold, mt_squeezed=b.mc, pibar_row_max=prm,
-                    grad_mt_two_stage=bool(dacc.mt.ndim == 2 and int(dacc.mt.shape[0]) == 1),
-                    grad_mt_two_stage_tile_splits=128, skip_inactive_pibar_output_zero=True, item_idx=p.item_idx)
-                p.k.uniform_cross_pibar_vjp_tree_from_ud_fused(
-                    Pi, col, ud, A, w.sl, w.sr, d_rhs, S, active_mask=mask, reduce_idx=w.reduce_idx,
-                    pibar_row_max=prm, skip_zero_sides=True, side_active=side_on, grad_col_log_probs=dacc.col,
-                    use_col_weights=False, side_active_threshold=so.pibar_side_threshold, **p.levels)
+                self._split_adjoint(p, w, dv, mask, d_rhs, dacc, Pi, Pibar, prm, col)
                 p.k.dts_backward_so(
                     Pi, dPi, Pibar, dPibar, v, w.ws, w.meta, S, b.pd_par, b.ps_par, d.dpd_par, d.dps_par, b.mc,
                     d.dMC, col, h["node_child1"], h["node_child2"], p.topo[0], p.topo[3], prm, p.item_idx, d_rhs,

@@ -81,11 +81,16 @@ def _fold(acc, x, G, S):
 
 
 class TangentForward:
-    """d(Pi)/d(theta) . u through the forward solve, at the saved point of ``plan``."""
+    """d(Pi)/d(theta) . u through the forward solve, at the saved point of ``plan``.
 
-    def __init__(self, plan: SolvePlan, saved):
+    ``split_terms`` (optional): the split term of each split wave at the point, keyed by the
+    wave's first row, used instead of recomputing it from the saved rows.
+    """
+
+    def __init__(self, plan: SolvePlan, saved, split_terms=None):
         self.p = plan
         self.sv = saved
+        self.split_terms = split_terms
         S, G = plan.S, int(saved["E"].shape[0])
         item = lambda t: as_item_state(t, S, G)
         E, pS, pD = item(saved["E"]), item(saved["log_pS"]), item(saved["log_pD"])
@@ -142,16 +147,20 @@ class TangentForward:
         h = p.h
         kw = dict(leaf_state_idx=p.leaf_idx, leaf_logp=self.base.leaf, dleaf_logp=d.dleaf, item_idx=p.item_idx,
                   use_col_weights=False)
+        d_dts_of = {}
         for w in p.waves:
             dts = d_dts = None
             if w.split:
                 lay = dict(log_split_probs=w.lsp, item_offset=w.ws, **w.extra)
-                dts = p.k.compute_dts_forward(pi, pibar, w.sl, w.sr, h["node_child1"], h["node_child2"], w.W,
-                                              w.reduce_idx, self.base.pd_par, self.base.ps_par, item_idx=p.item_idx,
-                                              **lay)
+                dts = self.split_terms.get(w.ws) if self.split_terms is not None else None
+                if dts is None:
+                    dts = p.k.compute_dts_forward(pi, pibar, w.sl, w.sr, h["node_child1"], h["node_child2"], w.W,
+                                                  w.reduce_idx, self.base.pd_par, self.base.ps_par,
+                                                  item_idx=p.item_idx, **lay)
                 d_dts = p.k.compute_dts_tangent(pi, pibar, dpi, dpibar, w.sl, w.sr, h["node_child1"],
                                                 h["node_child2"], w.W, w.reduce_idx, self.base.pd_par,
                                                 self.base.ps_par, d.dpd_par, d.dps_par, dts, p.item_idx, **lay)
+                d_dts_of[w.ws] = d_dts
 
             def sweep(store):
                 p.k.compute_wave_step_tangent(pi, dpi, dpi, w.ws, w.W, p.S, *cst, col, h["node_child1"],
@@ -175,7 +184,7 @@ class TangentForward:
                         break
                     prev = cur.clone()
                 sweep(store=True)
-        return dpi.index_select(0, p.roots), SimpleNamespace(dPi=dpi, dPibar=dpibar, d=d)
+        return dpi.index_select(0, p.roots), SimpleNamespace(dPi=dpi, dPibar=dpibar, d=d, d_dts=d_dts_of)
 
 
 def _class_static(static, layout, rep):
@@ -265,6 +274,9 @@ class _ClassSchedule:
         # every split row as one wave (the class layout is level ordered: the leaf level first, then
         # the split levels, contiguous), for the second-order terms that need no level order
         fwd = self.cache[::-1]
+        # with no row pruned the reverse classes are the forward ones: the tangent forward reads
+        # these split terms, and the reverse the forward's split-term tangents
+        self.split_terms = ({w.ws: dts for w, _, dts, _ in fwd if w.split} if rp is self.fplan else None)
         self.leaf = [(w, v) for w, v, _, _ in fwd if not w.split]
         sw = [(w, dts) for w, _, dts, _ in fwd if w.split]
         self.split_all = None
@@ -347,8 +359,8 @@ class HvpPlan:
         self.wE = e_out["wE"]
         self.q = root_softmax2(saved["pi_wave"].index_select(0, plan.roots))
         self.cls = _ClassSchedule(plan, saved, self.waves) if row_classes else None
-        self.tan = TangentForward(plan, saved) if self.cls is None else TangentForward(self.cls.fplan,
-                                                                                        self.cls.fsaved)
+        self.tan = (TangentForward(plan, saved) if self.cls is None else
+                    TangentForward(self.cls.fplan, self.cls.fsaved, split_terms=self.cls.split_terms))
         self.eg = _EGraph(plan, saved)
         a = self.acc
         base = self.eg.params_t(self.wE, a.Ebar)
@@ -399,7 +411,7 @@ class HvpPlan:
         self._graph.replay()
         return self._graph_out
 
-    def _class_reverse(self, d, dPi, dPibar, d_rhs, dacc, targets, cst_so):
+    def _class_reverse(self, d, dPi, dPibar, d_rhs, dacc, targets, cst_so, tan_d_dts):
         """The tangent reverse on the reverse classes, in two parts.
 
         The second-order terms (``compute_dts_tangent``, ``dts_backward_so``,
@@ -418,9 +430,12 @@ class HvpPlan:
         sa = k.split_all
         parts = [(w.ws, w.W, v, None, None, True) for w, v in k.leaf]
         if sa is not None:
-            d_dts = p.k.compute_dts_tangent(Pi, Pibar, dPi, dPibar, sa.sl, sa.sr, c1, c2, sa.W, sa.reduce_idx,
-                                            b.pd_par, b.ps_par, d.dpd_par, d.dps_par, sa.dts, p.item_idx,
-                                            log_split_probs=sa.lsp, item_offset=sa.ws)
+            if k.split_terms is not None:  # the tangent forward's, on the same rows
+                d_dts = torch.cat([tan_d_dts[w.ws] for w in p.waves if w.split])
+            else:
+                d_dts = p.k.compute_dts_tangent(Pi, Pibar, dPi, dPibar, sa.sl, sa.sr, c1, c2, sa.W, sa.reduce_idx,
+                                                b.pd_par, b.ps_par, d.dpd_par, d.dps_par, sa.dts, p.item_idx,
+                                                log_split_probs=sa.lsp, item_offset=sa.ws)
             p.k.dts_backward_so(
                 Pi, dPi, Pibar, dPibar, sa.v, sa.ws, sa.meta, S, b.pd_par, b.ps_par, d.dpd_par, d.dps_par, b.mc,
                 d.dMC, col, c1, c2, p.topo[0], p.topo[3], prm, p.item_idx, d_rhs, dacc.pD, dacc.pS, dacc.mt,
@@ -494,7 +509,7 @@ class HvpPlan:
                    (dacc.Es2, (4,)), (dacc.mt, (2,)))
         cst_so = (b.mc,) + self.tan.interleaved(d)[2:]  # the contraction takes mt without its tangent
         if k is not None:
-            return d, self._class_reverse(d, dPi, dPibar, d_rhs, dacc, targets, cst_so)
+            return d, self._class_reverse(d, dPi, dPibar, d_rhs, dacc, targets, cst_so, tf.d_dts)
         so = p.so
         for w, v, dts, mask in waves:
             d_dts = None

@@ -368,7 +368,8 @@ class FusedSolver:
         log_pD, log_pL, max_coupling, col_log_probs) of one E step at (w, acc_Ebar),
         plus acc's pS, pD, mt and col rows.  ``acc``: [8, S] (pD, pS, E, Ebar, E_s1,
         E_s2, max_coupling, col).  A failed BiCGSTAB raises ``RuntimeError`` (one
-        status read, skipped with ``check_solve=False``).
+        status read, skipped with ``check_solve=False``: ``last_e_status`` then holds the
+        device status words [iterations, failed] once the launch has run).
         """
         lib = N.lib()
         if not hasattr(lib, "kb_e_adjoint"):
@@ -398,6 +399,7 @@ class FusedSolver:
         with torch.cuda.device(dev):
             N.check(lib.kb_e_adjoint(self._plan, ct.byref(io), N.stream_handle(dev)))
         self._keep_e = (tens, acc, qx, work)
+        self.last_e_status = status  # [iterations, failed] of this solve, once it has run
         if check_solve:
             it, failed = (int(x) for x in status.cpu())
             if failed:

@@ -385,8 +385,7 @@ class HvpPlan:
     def __call__(self, u_flat):
         u = u_flat.reshape(self.theta.shape).to(self.theta.dtype)
         with torch.no_grad():
-            d, dacc = self._replay(u) if self.graph else self._tangent_reverse(u)
-            dcot = self._e_side(d, dacc)
+            dcot = self._replay(u) if self.graph else self._tangent_cotangents(u)
         with torch.enable_grad():
             (hu,) = torch.autograd.grad((self.g1 * u).sum() + self._pair(dcot), self.th, retain_graph=True)
         return hu.reshape(-1)
@@ -396,19 +395,32 @@ class HvpPlan:
 
         return fused_solver(self.p.static)
 
+    def _tangent_cotangents(self, u, *, check_solve=True):
+        d, dacc = self._tangent_reverse(u)
+        return self._e_side(d, dacc, check_solve=check_solve)
+
     def _replay(self, u):
-        """The tangent forward and reverse as one HIP graph: captured on the first call (after one
-        eager call that creates every cached layout table and kernel attribute), replayed after."""
+        """The tangent forward, reverse and (with the native E adjoint) E side as one HIP graph:
+        captured on the first call, after one eager call that creates every cached layout table
+        and kernel attribute; replayed after, with the E adjoint's status read once per call."""
         if self._graph is None:
             self._u_in = u.clone()
-            self._tangent_reverse(self._u_in)
+            self._tangent_cotangents(self._u_in)
             torch.cuda.synchronize()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                self._graph_out = self._tangent_reverse(self._u_in)
+                if self.native_e:
+                    self._graph_out = self._tangent_cotangents(self._u_in, check_solve=False)
+                else:
+                    self._graph_out = self._tangent_reverse(self._u_in)
             self._graph = g
         self._u_in.copy_(u)
         self._graph.replay()
+        if not self.native_e:
+            return self._e_side(*self._graph_out)
+        it, failed = (int(x) for x in self._fused().last_e_status.cpu())
+        if failed:
+            raise RuntimeError(f"E-adjoint BiCGSTAB solve failed after {it} iterations")
         return self._graph_out
 
     def _class_reverse(self, d, dPi, dPibar, d_rhs, dacc, targets, cst_so, tan_d_dts):
@@ -537,7 +549,7 @@ class HvpPlan:
                     dacc.pD, dacc.pS, dacc.mt, dacc.col, use_col_weights=False, **p.levels)
         return d, dacc
 
-    def _e_side(self, d, dacc):
+    def _e_side(self, d, dacc, *, check_solve=True):
         """Tangent E adjoint and the tangent parameter cotangents."""
         p, sv, a, eg = self.p, self.sv, self.acc, self.eg
         S, G = p.S, self.G
@@ -565,7 +577,7 @@ class HvpPlan:
             z = torch.zeros((S,), dtype=torch.float64, device=E.device)
             acc8 = torch.stack([z, z, dacc.E.reshape(S).double(), dacc.Ebar.reshape(S).double(),
                                 dacc.Es1.reshape(S).double(), dacc.Es2.reshape(S).double(), z, z])
-            _, gs = self._fused().e_adjoint(self.sv, acc8, q_extra=extra.reshape(S))
+            _, gs = self._fused().e_adjoint(self.sv, acc8, q_extra=extra.reshape(S), check_solve=check_solve)
             gs = gs.to(E.dtype)
             lin = [gs[0].view_as(E), gs[1].view_as(E), gs[2].view_as(E), gs[3].view_as(E), gs[4]]
         else:

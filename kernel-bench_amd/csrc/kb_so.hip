@@ -569,11 +569,19 @@ struct DsoArgs {
 // f = 2^(rowmax_child + mt - Pibar).
 template <typename T, int CPT>
 __global__ __launch_bounds__(NT) void dso_split_kernel(DsoArgs<T> a) {
+  // float rows are computed in float32 (hardware exp2), double rows in float64
+  using C = typename std::conditional<std::is_same<T, float>::value, float, double>::type;
+  const C LN2C = (C)LN2D;
+  auto ex2 = [](C x) -> C {
+    if constexpr (std::is_same<C, float>::value) return __builtin_amdgcn_exp2f(x);
+    else return exp2(x);
+  };
+  auto ldc = [](const T* p, size_t i) -> C { return (C)p[i]; };
   extern __shared__ double smd[];
   const int S = a.S;
-  double* L = smd;
-  double* R = smd + S;
-  const double NI = -__builtin_inf();
+  C* L = reinterpret_cast<C*>(smd);
+  C* R = L + S;
+  const C NI = -__builtin_inf();
   const long long n = blockIdx.x, N = a.N;
   const long long pw = a.red[n];
   const long long item = a.item[a.item_offset + pw];
@@ -581,54 +589,54 @@ __global__ __launch_bounds__(NT) void dso_split_kernel(DsoArgs<T> a) {
   const size_t mb = (size_t)(item * a.mrow);
   const long long l = a.sl[n], r = a.sr[n];
   const size_t bl = (size_t)l * S, br = (size_t)r * S, bp = (size_t)(a.ws + pw) * S, bv = (size_t)pw * S;
-  const double lsp = ld(a.lsp, n);
-  const double rml = ld(a.rowmax, l), rmr = ld(a.rowmax, r);
-  double d3[CPT], d4[CPT];
+  const C lsp = ldc(a.lsp, n);
+  const C rml = ldc(a.rowmax, l), rmr = ldc(a.rowmax, r);
+  C d3[CPT], d4[CPT];
   int c1v[CPT], c2v[CPT];
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int s = threadIdx.x + k * NT;
-    d3[k] = d4[k] = 0.0;
+    d3[k] = d4[k] = 0;
     c1v[k] = c2v[k] = -1;
     if (s < S) {
-      const double d = a.by_state ? ld(a.pD, pb + s) : ld(a.pD, pb);
-      const double sp = a.by_state ? ld(a.pS, pb + s) : ld(a.pS, pb);
-      const double dd = a.by_state ? ld(a.dpD, pb + s) : ld(a.dpD, pb);
-      const double dsp = a.by_state ? ld(a.dpS, pb + s) : ld(a.dpS, pb);
+      const C d = a.by_state ? ldc(a.pD, pb + s) : ldc(a.pD, pb);
+      const C sp = a.by_state ? ldc(a.pS, pb + s) : ldc(a.pS, pb);
+      const C dd = a.by_state ? ldc(a.dpD, pb + s) : ldc(a.dpD, pb);
+      const C dsp = a.by_state ? ldc(a.dpS, pb + s) : ldc(a.dpS, pb);
       const int c1 = child_at(a.c1, s, S), c2 = child_at(a.c2, s, S);
       c1v[k] = c1;
       c2v[k] = c2;
-      const double pl = ld(a.Pi, bl + s), pr = ld(a.Pi, br + s);
-      const double dpl = ld(a.dPi, bl + s), dpr = ld(a.dPi, br + s);
-      const double l1 = c1 >= 0 ? ld(a.Pi, bl + c1) : NI, r1 = c1 >= 0 ? ld(a.Pi, br + c1) : NI;
-      const double l2 = c2 >= 0 ? ld(a.Pi, bl + c2) : NI, r2 = c2 >= 0 ? ld(a.Pi, br + c2) : NI;
-      const double dl1 = c1 >= 0 ? ld(a.dPi, bl + c1) : 0.0, dr1 = c1 >= 0 ? ld(a.dPi, br + c1) : 0.0;
-      const double dl2 = c2 >= 0 ? ld(a.dPi, bl + c2) : 0.0, dr2 = c2 >= 0 ? ld(a.dPi, br + c2) : 0.0;
-      const double pbl = ld(a.Pb, bl + s), pbr = ld(a.Pb, br + s);
-      const double dpbl = ld(a.dPb, bl + s), dpbr = ld(a.dPb, br + s);
-      const double dk[5] = {d + pl + pr, pl + pbr, pr + pbl, sp + l1 + r2, sp + r1 + l2};
-      const double ddk[5] = {dd + dpl + dpr, dpl + dpbr, dpr + dpbl, dsp + dl1 + dr2, dsp + dr1 + dl2};
-      const double pp = ld(a.Pi, bp + s), dpp = ld(a.dPi, bp + s);
-      const double vv = ld(a.v, bv + s);
-      double wk[5], dv[5];
+      const C pl = ldc(a.Pi, bl + s), pr = ldc(a.Pi, br + s);
+      const C dpl = ldc(a.dPi, bl + s), dpr = ldc(a.dPi, br + s);
+      const C l1 = c1 >= 0 ? ldc(a.Pi, bl + c1) : NI, r1 = c1 >= 0 ? ldc(a.Pi, br + c1) : NI;
+      const C l2 = c2 >= 0 ? ldc(a.Pi, bl + c2) : NI, r2 = c2 >= 0 ? ldc(a.Pi, br + c2) : NI;
+      const C dl1 = c1 >= 0 ? ldc(a.dPi, bl + c1) : (C)0, dr1 = c1 >= 0 ? ldc(a.dPi, br + c1) : (C)0;
+      const C dl2 = c2 >= 0 ? ldc(a.dPi, bl + c2) : (C)0, dr2 = c2 >= 0 ? ldc(a.dPi, br + c2) : (C)0;
+      const C pbl = ldc(a.Pb, bl + s), pbr = ldc(a.Pb, br + s);
+      const C dpbl = ldc(a.dPb, bl + s), dpbr = ldc(a.dPb, br + s);
+      const C dk[5] = {d + pl + pr, pl + pbr, pr + pbl, sp + l1 + r2, sp + r1 + l2};
+      const C ddk[5] = {dd + dpl + dpr, dpl + dpbr, dpr + dpbl, dsp + dl1 + dr2, dsp + dr1 + dl2};
+      const C pp = ldc(a.Pi, bp + s), dpp = ldc(a.dPi, bp + s);
+      const C vv = ldc(a.v, bv + s);
+      C wk[5], dv[5];
 #pragma unroll
       for (int j = 0; j < 5; ++j) {
-        wk[j] = pp != NI ? exp2(lsp + dk[j] - pp) : 0.0;
-        dv[j] = wk[j] != 0.0 ? vv * LN2D * wk[j] * (ddk[j] - dpp) : 0.0;
+        wk[j] = pp != NI ? ex2(lsp + dk[j] - pp) : (C)0;
+        dv[j] = wk[j] != (C)0 ? vv * LN2C * wk[j] * (ddk[j] - dpp) : (C)0;
       }
       L[s] = dv[0] + dv[1];
       R[s] = dv[0] + dv[2];
       d3[k] = dv[3];
       d4[k] = dv[4];
-      const double mt = ld(a.mt, mb + s), dmt = ld(a.dmt, mb + s);
-      const double fl = pbl != NI ? exp2(rml + mt - pbl) : 0.0;
-      const double fr = pbr != NI ? exp2(rmr + mt - pbr) : 0.0;
-      const double vd1 = vv * wk[1], vd2 = vv * wk[2];
+      const C mt = ldc(a.mt, mb + s), dmt = ldc(a.dmt, mb + s);
+      const C fl = pbl != NI ? ex2(rml + mt - pbl) : (C)0;
+      const C fr = pbr != NI ? ex2(rmr + mt - pbr) : (C)0;
+      const C vd1 = vv * wk[1], vd2 = vv * wk[2];
       const size_t ol = (size_t)n * S + s, orr = (size_t)(N + n) * S + s;
       a.ud[ol] = (T)(vd2 * fl);
       a.ud[orr] = (T)(vd1 * fr);
-      a.dud[ol] = (T)(dv[2] * fl + (fl != 0.0 ? vd2 * LN2D * fl * (dmt - dpbl) : 0.0));
-      a.dud[orr] = (T)(dv[1] * fr + (fr != 0.0 ? vd1 * LN2D * fr * (dmt - dpbr) : 0.0));
+      a.dud[ol] = (T)(dv[2] * fl + (fl != (C)0 ? vd2 * LN2C * fl * (dmt - dpbl) : (C)0));
+      a.dud[orr] = (T)(dv[1] * fr + (fr != (C)0 ? vd1 * LN2C * fr * (dmt - dpbr) : (C)0));
       a.pDrows[(size_t)n * S + s] = (T)dv[0];
       a.pSrows[(size_t)n * S + s] = (T)(dv[3] + dv[4]);
       a.mtrows[(size_t)n * S + s] = (T)(dv[1] + dv[2]);
@@ -701,6 +709,92 @@ __global__ __launch_bounds__(NT) void dso_tree_kernel(OpsTree t, DsoArgs<T> a) {
   }
 }
 
+// dso_tree_kernel for float32 rows at preorder ownership (thread t owns the
+// contiguous positions t*CPT + k): ud / dud and the child's Pi / dPi rows are
+// staged to their preorder positions, both subtree complements A - sub come
+// from wavefront-local scans published behind one barrier, and the outputs go
+// back to column order through LDS.  Same terms as dso_tree_kernel, in
+// float32 with the hardware exp2.
+template <int CPT>
+__global__ __launch_bounds__(NT) void dso_tree_pre_kernel(OpsTree t, DsoArgs<float> a) {
+  constexpr int MAXS = NT * CPT;
+  constexpr int LD = MAXS + 64;  // [MAXS] is the padding slot, kept at 0
+  constexpr int ZERO = MAXS;
+  constexpr int SEG = 64 * CPT;  // positions per wavefront
+  constexpr float LN2F = 0.69314718055994531f;
+  extern __shared__ __align__(16) unsigned char smraw[];
+  float* Lr = reinterpret_cast<float*>(smraw);  // rows: ud, dud (then their scans), Pi (then the output), dPi
+  auto row = [&](int j) { return Lr + (size_t)j * LD; };
+  __shared__ float wA[NW], wB[NW];
+  const int S = t.S;
+  const int tid = threadIdx.x;
+  const float NI = -__builtin_inff();
+  const long long i = blockIdx.x, N = a.N;
+  const long long child = i < N ? a.sl[i] : a.sr[i - N];
+  const size_t rb = (size_t)i * S, cbase = (size_t)child * S;
+  const float rm = a.rowmax[child];
+  const float rms = rm == NI ? 0.0f : rm;
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int sc = tid + j * NT;
+    if (sc < S) {
+      const int p = t.ppos[sc];
+      row(0)[p] = a.ud[rb + sc];
+      row(1)[p] = a.dud[rb + sc];
+      row(2)[p] = a.Pi[cbase + sc];
+      row(3)[p] = a.dPi[cbase + sc];
+    }
+  }
+  if (tid < 64)
+    for (int j = 0; j < 4; ++j) row(j)[MAXS + tid] = 0.0f;
+  int colk[CPT], endm1[CPT], wend[CPT];
+  bool okp[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int q = kb::own_pos_c<NT, CPT>(k);
+    okp[k] = q < S;
+    colk[k] = okp[k] ? t.pcol[q] : 0;
+    endm1[k] = okp[k] ? t.pend[colk[k]] - 1 : ZERO;
+    wend[k] = endm1[k] < ZERO ? endm1[k] / SEG : 0;
+  }
+  __syncthreads();
+  float x[CPT], dx[CPT], pi[CPT], dpi[CPT];
+  kb::lds_load_own<CPT>(row(0), x);
+  kb::lds_load_own<CPT>(row(1), dx);
+  kb::lds_load_own<CPT>(row(2), pi);
+  kb::lds_load_own<CPT>(row(3), dpi);
+#pragma unroll
+  for (int k = 0; k < CPT; ++k)
+    if (!okp[k]) x[k] = dx[k] = 0.0f;  // positions past S were not written: out of the scans
+  float sx[CPT], sdx[CPT];
+  kb::local_scan_publish<NT, CPT>(sx, x, row(0), wA);
+  kb::local_scan_publish<NT, CPT>(sdx, dx, row(1), wB);
+  __syncthreads();
+  float pm1[CPT], rest[CPT], dpm1[CPT], drest[CPT];
+  kb::subtree_terms<NT, CPT>(sx, row(0), wA, endm1, wend, pm1, rest);
+  kb::subtree_terms<NT, CPT>(sdx, row(1), wB, endm1, wend, dpm1, drest);
+  float c[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    c[k] = 0.0f;
+    if (okp[k]) {
+      const float pp = pi[k] != NI ? __builtin_amdgcn_exp2f(pi[k] + (a.use_col ? a.col[colk[k]] : 0.0f) - rms) : 0.0f;
+      c[k] = LN2F * pp * dpi[k] * (pm1[k] + rest[k]) + pp * (dpm1[k] + drest[k]);
+    }
+  }
+  kb::lds_store_own<CPT>(row(2), c);  // row 2 was read only at own positions
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int sc = tid + j * NT;
+    if (sc < S) {
+      const float v = row(2)[t.ppos[sc]];
+      a.side[rb + sc] += v;
+      a.colrows[rb + sc] = v;
+    }
+  }
+}
+
 }  // namespace kbo
 
 using namespace kbo_host;
@@ -721,6 +815,23 @@ int launch_wso(const kbo::OpsTree& t, const kbo::WsoArgs<T>& a, int W, size_t ld
   auto k = kbo::wso_kernel<T, CPT>;
   if (int rc = set_lds(k, lds)) return rc;
   hipLaunchKernelGGL(k, dim3(W), dim3(kbo::NT), lds, st, t, a);
+  return 0;
+}
+
+// float32 rows: the preorder-ownership tree kernel; the others the float64 one
+template <typename T, int CPT>
+int launch_dso_tree(const kbo::OpsTree& t, const kbo::DsoArgs<T>& a, size_t lds, hipStream_t st) {
+  const dim3 grid((unsigned)(2 * a.N));
+  if constexpr (std::is_same_v<T, float>) {
+    const size_t lds_pre = (size_t)4 * (kbo::NT * CPT + 64) * sizeof(float);
+    auto k = kbo::dso_tree_pre_kernel<CPT>;
+    if (int rc = set_lds(k, lds_pre)) return rc;
+    hipLaunchKernelGGL(k, grid, dim3(kbo::NT), lds_pre, st, t, a);
+    return 0;
+  }
+  auto k = kbo::dso_tree_kernel<T, CPT>;
+  if (int rc = set_lds(k, lds)) return rc;
+  hipLaunchKernelGGL(k, grid, dim3(kbo::NT), lds, st, t, a);
   return 0;
 }
 
@@ -805,9 +916,7 @@ int kb_dts_backward_so(const kb_tree* tr, const kb_dts_so_io* io, void* stream) 
     if (int rc = set_lds(kbo::dso_split_kernel<T, CPT>, lds2)) return rc;
     hipLaunchKernelGGL((kbo::dso_split_kernel<T, CPT>), dim3((unsigned)io->N), dim3(kbo::NT), lds2,
                        st_of(stream), a);
-    if (int rc = set_lds(kbo::dso_tree_kernel<T, CPT>, lds1)) return rc;
-    hipLaunchKernelGGL((kbo::dso_tree_kernel<T, CPT>), dim3((unsigned)(2 * io->N)), dim3(kbo::NT), lds1,
-                       st_of(stream), t, a);
+    if (int rc = launch_dso_tree<T, CPT>(t, a, lds1, st_of(stream))) return rc;
   });
   KBO_HIP(hipGetLastError());
   return 0;

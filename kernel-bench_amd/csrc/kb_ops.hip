@@ -475,7 +475,7 @@ __global__ __launch_bounds__(NT) void wave_step_kernel(OpsTree t, WsArgs<T> a) {
 // scan (two barriers per sweep).  The outputs equal the log-space sweeps to
 // float32 rounding.
 template <int CPT>
-__global__ __launch_bounds__(NT) void wave_step_lin_kernel(OpsTree t, WsArgs<float> a) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(kb::pre_waves_per_eu(CPT)))) void wave_step_lin_kernel(OpsTree t, WsArgs<float> a) {
   constexpr int MAXS = NT * CPT;
   constexpr int LD = MAXS + 64;
   constexpr int ZERO = MAXS;     // padding slot: 0 in X
@@ -1045,7 +1045,7 @@ __global__ __launch_bounds__(NT) void wave_bwd_kernel(OpsTree t, WbArgs<T> a) {
 // offsets), and the [W, S] outputs written back in column order through LDS.
 // Same mathematics as wave_bwd_kernel.
 template <int CPT>
-__global__ __launch_bounds__(NT) void wave_bwd_pre_kernel(OpsTree t, WbArgs<float> a) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(kb::pre_waves_per_eu(CPT)))) void wave_bwd_pre_kernel(OpsTree t, WbArgs<float> a) {
   constexpr int MAXS = NT * CPT;
   constexpr int LD = MAXS + 64;  // [MAXS] is the padding slot, kept at 0
   constexpr int ZERO = MAXS;

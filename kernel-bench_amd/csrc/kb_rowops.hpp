@@ -324,6 +324,11 @@ struct OwnTables {
 // position i-1 of slot 0 is the previous lane's last value.  Own positions are
 // moved to and from LDS with vector accesses (conflict-free).
 
+// Minimum waves per SIMD asked of the 1024-thread preorder-ownership sweep and
+// adjoint kernels: eight (two resident workgroups per CU, at most 64 VGPRs)
+// when a thread owns at most two positions, else no constraint.
+constexpr int pre_waves_per_eu(int cpt) { return cpt <= 2 ? 8 : 1; }
+
 template <int NT, int CPT>
 __device__ __forceinline__ int own_pos_c(int k) {
   return threadIdx.x * CPT + k;

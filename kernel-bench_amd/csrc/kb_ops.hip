@@ -1378,7 +1378,8 @@ struct DcArgs {
 };
 
 template <typename T, int CPT>
-__global__ __launch_bounds__(NT) void dts_cross_kernel(DcArgs<T> a) {
+__global__ __launch_bounds__(NT)
+__attribute__((amdgpu_waves_per_eu(sizeof(T) == 4 ? kb::pre_waves_per_eu(CPT) : 1))) void dts_cross_kernel(DcArgs<T> a) {
   extern __shared__ unsigned char smraw[];
   T* Lr = reinterpret_cast<T*>(smraw);
   T* Rr = Lr + a.S;

@@ -376,6 +376,26 @@ def test_e_adjoint_entry_solves_the_e_system(statewise):
         assert e <= 1e-9
 
 
+def test_e_adjoint_entry_reports_a_failed_solve(monkeypatch):
+    """kb_e_adjoint with one BiCGSTAB iteration and an unreachable tolerance: the status words say
+    failed, FusedSolver.e_adjoint raises RuntimeError (as the backward does), and check_solve=False
+    leaves the status for the caller."""
+    from dropin.solve import run_forward
+    from kbench.fused import FusedSolver
+
+    static, theta, cw = _static("1", True)
+    _, sv = run_forward(static, theta, cw)
+    so = dict(static.solver_options.__dict__, bicgstab_max_iter=1, bicgstab_tol=1e-30)
+    solver = FusedSolver(static, so)
+    S = int(sv["E"].numel())
+    acc = torch.as_tensor(np.random.default_rng(42).normal(size=(8, S))).cuda()
+    with pytest.raises(RuntimeError, match="BiCGSTAB"):
+        solver.e_adjoint(sv, acc)
+    solver.e_adjoint(sv, acc, check_solve=False)
+    it, failed = (int(x) for x in solver.last_e_status.cpu())
+    assert failed == 1 and it == 1
+
+
 def test_native_tangent_e_adjoint_matches_autograd_bicgstab():
     """The HVP's tangent E side through kb_e_adjoint agrees with BiCGSTAB over autograd E-step products."""
     from dropin.hvp import HvpPlan

@@ -284,6 +284,8 @@ class _ClassSchedule:
             ws1 = sw[0][0].ws
             if any(a.ws + a.W != b_.ws for (a, _), (b_, _) in zip(sw, sw[1:])) or sw[-1][0].ws + sw[-1][0].W != rp.C:
                 raise ValueError("the class layout's split waves are not contiguous")
+            if any(w.leaf_term for w, _ in sw):
+                raise ValueError("a split wave of the class layout carries the leaf term")
             dt = self.Pi.dtype
             lsp = torch.cat([w.lsp.reshape(-1).to(dt) if w.lsp is not None else
                              torch.zeros((int(w.sl.numel()),), dtype=dt, device=dev) for w, _ in sw])
@@ -440,7 +442,7 @@ class HvpPlan:
         Pi, Pibar, prm, col = k.Pi, k.Pibar, k.prm, sv["col_log_probs"]
         c1, c2 = h["node_child1"], h["node_child2"]
         sa = k.split_all
-        parts = [(w.ws, w.W, v, None, None, True) for w, v in k.leaf]
+        parts = [(w.ws, w.W, v, None, None, w.leaf_term) for w, v in k.leaf]
         if sa is not None:
             if k.split_terms is not None:  # the tangent forward's, on the same rows
                 d_dts = torch.cat([tan_d_dts[w.ws] for w in p.waves if w.split])

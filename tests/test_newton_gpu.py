@@ -33,12 +33,17 @@ def _setup():
         _, sv = dropin.run_forward(static, th, cw)
         return HvpPlan(plan_of(static), th, cw, sv)
 
+    def exact_classes(obj, x):  # the fast HVP: row classes, tangent passes replayed as one graph
+        th = obj.theta(x)
+        _, sv = dropin.run_forward(static, th, cw)
+        return HvpPlan(plan_of(static), th, cw, sv, row_classes=True, graph=True)
+
     def ggn(obj, x):
         th = obj.theta(x)
         _, sv = dropin.run_forward(static, th, cw)
         return ggn_hvp(plan_of(static), th, cw, sv)
 
-    obj = Objective(static, cw, curvatures={"exact": exact, "ggn": ggn})
+    obj = Objective(static, cw, curvatures={"exact": exact, "exact_classes": exact_classes, "ggn": ggn})
     return static, theta, cw, obj
 
 
@@ -66,8 +71,26 @@ def test_fd_hessian_agrees_with_the_exact_hvp():
     assert rels[Objective_default_eps()] <= 5e-3
 
 
-@pytest.mark.parametrize("driver,curv", [("newton_cg", "exact"), ("newton_cg", "ggn"), ("newton_tr", "fd_hessian"),
-                                         ("newton_lanczos", "fd_hessian")])
+def test_newton_cg_steps_on_the_fast_hvp_match_the_row_by_row_ones():
+    """Newton-CG on the class / graph HVP (a new point, so a new capture, every step) takes the steps the
+    row-by-row HVP gives, to float32 rounding of the CG iterates."""
+    from kbench import newton
+
+    print("[newton] newton_cg exact vs exact_classes, config=1 statewise", flush=True)
+    static, theta, cw, obj = _setup()
+    out = {}
+    for curv in ("exact", "exact_classes"):
+        x, _ = newton.newton_cg(static, theta, cw, curvature=curv, objective=obj, max_newton=3, gtol=1e-12,
+                                max_cg=20)
+        out[curv] = x.reshape(-1).double()
+    torch.cuda.synchronize()
+    e = float((out["exact_classes"] - out["exact"]).abs().max()) / float(out["exact"].abs().max())
+    print(f"  x after 3 steps: rel diff {e:.3e}")
+    assert e <= 1e-4
+
+
+@pytest.mark.parametrize("driver,curv", [("newton_cg", "exact"), ("newton_cg", "exact_classes"), ("newton_cg", "ggn"),
+                                         ("newton_tr", "fd_hessian"), ("newton_lanczos", "fd_hessian")])
 def test_driver_steps_decrease_the_loss(driver, curv):
     from kbench import newton
 

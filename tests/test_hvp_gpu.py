@@ -209,6 +209,45 @@ def test_exact_hvp_matches_oracle(name, statewise, row_classes):
     assert e <= 1e-3
 
 
+def test_exact_hvp_on_a_large_tree_matches_oracle():
+    """S = 4095 (three small families): the class / graph HVP against the oracle's HVP (1e-3 of max
+    |H u|), through the kernels' 4-position shapes."""
+    from dropin.hvp import HvpPlan
+    from dropin.solve import plan_of, run_forward
+
+    print("[hvp] large tree leaves=2048 (S=4095)", flush=True)
+    problem, static, theta, cw = _big_tree(2048, True)
+    _, sv = run_forward(static, theta, cw)
+    u = np.random.default_rng(43).normal(size=tuple(theta.shape))
+    hvp = HvpPlan(plan_of(static), theta, cw, sv, row_classes=True, graph=True)
+    Hu = hvp(torch.as_tensor(u, dtype=theta.dtype).cuda().reshape(-1))
+    Hu2 = hvp(torch.as_tensor(u, dtype=theta.dtype).cuda().reshape(-1))
+    torch.cuda.synchronize()
+    assert torch.equal(Hu, Hu2)
+    prob = O.Problem.from_dict(problem)
+    th = np.asarray(problem["inputs"]["theta"], dtype=np.float32).astype(np.float64)
+    cw64 = np.asarray(problem["inputs"]["col_weights"], dtype=np.float64)
+    _, saved = O.forward(prob, th, cw64)
+    _, _, cache = O.build_point_cache(prob, th, cw64, saved)
+    ref = O.hvp_exact(prob, th, saved, u, cache)
+    e = _rel(Hu.cpu().numpy(), ref.reshape(-1))
+    print(f"  |H u| = {np.abs(ref).max():.4e} rel={e:.3e}")
+    assert e <= 1e-3
+
+
+def test_exact_hvp_refuses_trees_beyond_its_lds_rows():
+    """S = 8191: the E-step second-order kernel keeps three float64 rows of S in LDS (S <= 6741); the HVP
+    stops with the wrappers' ValueError before any launch instead of running past the LDS limit."""
+    from dropin.hvp import HvpPlan
+    from dropin.solve import plan_of, run_forward
+
+    _, static, theta, cw = _big_tree(4096, True)
+    _, sv = run_forward(static, theta, cw)
+    hvp = HvpPlan(plan_of(static), theta, cw, sv, row_classes=True)
+    with pytest.raises(ValueError, match="LDS"):
+        hvp(torch.ones(theta.numel(), dtype=theta.dtype, device="cuda"))
+
+
 def test_exact_hvp_config3_symmetric_linear_deterministic():
     """Full size (config 3 with per-species theta, the Newton-CG setup): symmetry, linearity, determinism."""
     import time

@@ -695,6 +695,8 @@ int launch_wave_tan(const kbo::OpsTree& t, const kbo::WtArgs<T>& a, int W, size_
     hipLaunchKernelGGL(k, dim3(W), dim3(kbo::NT), lds_pre, st, t, a);
     return 0;
   }
+  // the float64 kernel keeps three float64 rows of S in LDS
+  if (int rc = check_lds(lds, a.S, KB_F64)) return rc;
   auto k = kbo::wave_tan_kernel<T, CPT>;
   if (int rc = set_lds(k, lds)) return rc;
   hipLaunchKernelGGL(k, dim3(W), dim3(kbo::NT), lds, st, t, a);
@@ -758,7 +760,6 @@ int kb_wave_step_tangent(const kb_tree* tr, const kb_wave_tan_io* io, void* stre
   if (io->W == 0) return 0;
   const int S = tr->S;
   const size_t lds = (size_t)3 * S * sizeof(double);
-  if (int rc = check_lds(lds, S, KB_F64)) return rc;
   const kbo::OpsTree t = tr->dev();
   KBO_DISPATCH(io->dtype, S, {
     kbo::WtArgs<T> a{S, io->W, io->use_col_weights, io->use_leaf_index, io->n_iters, io->ws, io->pi_ws,

@@ -73,7 +73,23 @@ def test_e_tangent_fixed_point_matches_oracle(dt, statewise):
 
 
 def _wave_fixture(name, statewise, dt):
-    """(static on the GPU, oracle problem, oracle forward intermediates) of one configuration."""
+    """(static on the GPU, oracle problem, oracle forward intermediates) of one configuration.
+
+    ``name`` "big": a 4096-leaf species tree (S = 8191) with three small families.
+    """
+    if name == "big":
+        from kbench import synth
+        from kbench.fused import problem_to_captured
+        from kbench.runtime import make_static
+
+        cfg = synth.ProblemConfig(4096, 3, n_nni=1, family_leaves_median=21.0, family_leaves_sigma=0.6,
+                                  family_leaves_max=80, statewise=bool(statewise), seed=17)
+        p = synth.build_problem(cfg)
+        static = make_static(problem_to_captured(p), "cuda")
+        prob = O.Problem.from_dict(p)
+        theta = np.asarray(p["inputs"]["theta"], dtype=np.float32).astype(np.float64)
+        _, saved = O.forward(prob, theta, np.asarray(p["inputs"]["col_weights"], dtype=np.float64))
+        return static, prob, saved
     static, _, _ = _static(name, statewise)
     prob, _, saved = kbtest.oracle_forward(name, statewise)
     return static, prob, saved
@@ -114,13 +130,16 @@ def test_dts_tangent_matches_oracle(dt):
     assert worst <= TOL[dt]
 
 
-@pytest.mark.parametrize("dt", [torch.float64, torch.float32])
-@pytest.mark.parametrize("n_iters", [1, 7])
-def test_wave_step_tangent_matches_oracle(dt, n_iters):
+@pytest.mark.parametrize("name,dt,n_iters", [("1", torch.float64, 1), ("1", torch.float64, 7),
+                                             ("1", torch.float32, 1), ("1", torch.float32, 7),
+                                             ("big", torch.float32, 7)])
+def test_wave_step_tangent_matches_oracle(name, dt, n_iters):
+    """Tangent sweeps against the oracle; "big" (S = 8191) runs the float32 preorder kernel at eight
+    positions per thread."""
     from kbench.core.kernels.wave_tangent import compute_wave_step_tangent, compute_wave_step_tangent_selfloop
 
-    print(f"[wave-tangent] config=1 dtype={dt} n_iters={n_iters}", flush=True)
-    static, prob, saved = _wave_fixture("1", None, dt)
+    print(f"[wave-tangent] config={name} dtype={dt} n_iters={n_iters}", flush=True)
+    static, prob, saved = _wave_fixture(name, None, dt)
     rng = np.random.default_rng(13)
     S, G, C = prob.S, 1, prob.C
     E = np.asarray(saved["E"])

@@ -188,10 +188,10 @@ __device__ void level_subtree_sums(const OpsTree& t, double* x) {
 // Ancestors-or-self path sums of per-state register values x[k] (state
 // threadIdx.x + k * NT): written as +x at the entry event and -x at the exit
 // event of each column, scanned, read back at the entry event.  Enters with
-// ev2 free; ends with a barrier after which ev2 may be reused.
-template <int CPT>
-__device__ void reg_path_sums(const OpsTree& t, const double (&x)[CPT], double (&ps)[CPT], double* ev2,
-                              double* red) {
+// ev2 free; ends with a barrier after which ev2 may be reused.  V: the value
+// type (double, or float for rows too long for three double rows of LDS).
+template <int CPT, typename V>
+__device__ void reg_path_sums(const OpsTree& t, const V (&x)[CPT], V (&ps)[CPT], V* ev2, V* red) {
   const int S = t.S;
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
@@ -208,17 +208,16 @@ __device__ void reg_path_sums(const OpsTree& t, const double (&x)[CPT], double (
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int s = threadIdx.x + k * NT;
-    ps[k] = s < S ? ev2[t.tin[s]] : 0.0;
+    ps[k] = s < S ? ev2[t.tin[s]] : V(0);
   }
   __syncthreads();
 }
 
 // Subtree-or-self sums of per-state register values x[k]: x scattered to
 // preorder positions, scanned, differenced over each subtree's range.
-// Enters with buf (S doubles) free; ends with a barrier.
-template <int CPT>
-__device__ void reg_subtree_sums(const OpsTree& t, const double (&x)[CPT], double (&sub)[CPT], double* buf,
-                                 double* red) {
+// Enters with buf (S values) free; ends with a barrier.
+template <int CPT, typename V>
+__device__ void reg_subtree_sums(const OpsTree& t, const V (&x)[CPT], V (&sub)[CPT], V* buf, V* red) {
   const int S = t.S;
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
@@ -230,10 +229,10 @@ __device__ void reg_subtree_sums(const OpsTree& t, const double (&x)[CPT], doubl
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int s = threadIdx.x + k * NT;
-    sub[k] = 0.0;
+    sub[k] = V(0);
     if (s < S) {
       const int p = t.ppos[s], e = t.pend[s];
-      sub[k] = buf[e - 1] - (p > 0 ? buf[p - 1] : 0.0);
+      sub[k] = buf[e - 1] - (p > 0 ? buf[p - 1] : V(0));
     }
   }
   __syncthreads();
@@ -281,6 +280,17 @@ inline int check_lds(size_t bytes, int S, int dtype) {
     return kb::set_error(KB_ERR_ARG, "S=%d needs %zu bytes of LDS per row for dtype %s (limit %zu)", S, bytes,
                          dtype == KB_F64 ? "float64" : "float32", LDS_BYTES);
   return 0;
+}
+
+// LDS of the kernels that keep three rows of S (a row and a 2S scan buffer):
+// float64 arithmetic while three float64 rows fit, float32 arithmetic in three
+// float32 rows for longer float32 rows (they need CPT = 8), an error for
+// longer float64 rows.
+inline int three_row_lds(int S, int dtype, size_t* lds, bool* f32) {
+  const size_t b64 = (size_t)3 * S * sizeof(double);
+  *f32 = dtype == KB_F32 && b64 > LDS_BYTES;
+  *lds = *f32 ? (size_t)3 * S * sizeof(float) : b64;
+  return check_lds(*lds, S, *f32 ? KB_F32 : KB_F64);
 }
 
 inline hipStream_t st_of(void* s) { return reinterpret_cast<hipStream_t>(s); }

@@ -29,6 +29,11 @@ __device__ __forceinline__ double ld(const T* p, size_t i) {
   return (double)p[i];
 }
 
+template <typename C, typename T>
+__device__ __forceinline__ C ldc(const T* p, size_t i) {
+  return (C)p[i];
+}
+
 // ---- E-step ------------------------------------------------------------------------
 
 template <typename T>
@@ -42,98 +47,98 @@ struct EsoArgs {
 // One workgroup per item row.  q_k = g_new 2^(t_k - E_new), dq_k = ln2 q_k (dt_k - dE_new);
 // d_grad_E = 2 dq1 + dq2 + dq0[parent] + dr (tot - excl) + r (dtot - dexcl) with
 // u = (q2 + g_ebar) / denom, du = (dq2 - u ddenom) / denom, excl = subtree sums of u.
-template <typename T, int CPT>
+template <typename T, int CPT, typename C = double>
 __global__ __launch_bounds__(NT) void eso_kernel(OpsTree t, EsoArgs<T> a) {
-  extern __shared__ double smd[];
+  extern __shared__ double smd[];  // raw storage: C values
   const int S = t.S;
-  double* X = smd;       // dq0 by column
-  double* EV = smd + S;  // 2S scan buffer
-  __shared__ double red[NW];
-  const double NI = -__builtin_inf();
+  C* X = reinterpret_cast<C*>(smd);       // dq0 by column
+  C* EV = reinterpret_cast<C*>(smd) + S;  // 2S scan buffer
+  __shared__ C red[NW];
+  const C NI = ninf<C>();
   const size_t base = (size_t)blockIdx.x * S;
-  double gE[CPT], wE[CPT], dwE[CPT], dq2[CPT], q2g[CPT];
-  double lm = NI;
+  C gE[CPT], wE[CPT], dwE[CPT], dq2[CPT], q2g[CPT];
+  C lm = NI;
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int s = threadIdx.x + k * NT;
-    gE[k] = dq2[k] = q2g[k] = dwE[k] = 0.0;
+    gE[k] = dq2[k] = q2g[k] = dwE[k] = C(0);
     wE[k] = NI;
     if (s < S) {
       const size_t i = base + s;
-      const double E = ld(a.E, i), En = ld(a.En, i), dE = ld(a.dE, i), dEn = ld(a.dEn, i), g = ld(a.gN, i);
-      const double t0 = ld(a.pS, i) + ld(a.Es1, i) + ld(a.Es2, i);
-      const double t1 = ld(a.pD, i) + 2.0 * E;
-      const double t2 = E + ld(a.Eb, i);
-      const double t3 = ld(a.pL, i);
-      const double dt0 = ld(a.dpS, i) + ld(a.dEs1, i) + ld(a.dEs2, i);
-      const double dt1 = ld(a.dpD, i) + 2.0 * dE;
-      const double dt2 = dE + ld(a.dEb, i);
-      const double dt3 = ld(a.dpL, i);
-      double q[4] = {g * exp2(t0 - En), g * exp2(t1 - En), g * exp2(t2 - En), g * exp2(t3 - En)};
-      const double dt[4] = {dt0, dt1, dt2, dt3};
-      double dq[4];
+      const C E = ldc<C>(a.E, i), En = ldc<C>(a.En, i), dE = ldc<C>(a.dE, i), dEn = ldc<C>(a.dEn, i), g = ldc<C>(a.gN, i);
+      const C t0 = ldc<C>(a.pS, i) + ldc<C>(a.Es1, i) + ldc<C>(a.Es2, i);
+      const C t1 = ldc<C>(a.pD, i) + C(2) * E;
+      const C t2 = E + ldc<C>(a.Eb, i);
+      const C t3 = ldc<C>(a.pL, i);
+      const C dt0 = ldc<C>(a.dpS, i) + ldc<C>(a.dEs1, i) + ldc<C>(a.dEs2, i);
+      const C dt1 = ldc<C>(a.dpD, i) + C(2) * dE;
+      const C dt2 = dE + ldc<C>(a.dEb, i);
+      const C dt3 = ldc<C>(a.dpL, i);
+      C q[4] = {g * xexp2(t0 - En), g * xexp2(t1 - En), g * xexp2(t2 - En), g * xexp2(t3 - En)};
+      const C dt[4] = {dt0, dt1, dt2, dt3};
+      C dq[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        if (q[j] != q[j]) q[j] = 0.0;  // 0 * inf
-        dq[j] = q[j] != 0.0 ? LN2D * q[j] * (dt[j] - dEn) : 0.0;
+        if (q[j] != q[j]) q[j] = C(0);  // 0 * inf
+        dq[j] = q[j] != C(0) ? (C)LN2D * q[j] * (dt[j] - dEn) : C(0);
       }
       a.opS[i] = (T)dq[0];
       a.opD[i] = (T)dq[1];
       a.opL[i] = (T)dq[3];
       a.omc[i] = (T)dq[2];
       X[s] = dq[0];
-      gE[k] = 2.0 * dq[1] + dq[2];
+      gE[k] = C(2) * dq[1] + dq[2];
       dq2[k] = dq[2];
-      q2g[k] = q[2] + ld(a.gB, i);
-      wE[k] = E + (a.use_col ? ld(a.col, s) : 0.0);
-      dwE[k] = dE + ((a.use_col && a.dcol) ? ld(a.dcol, s) : 0.0);
+      q2g[k] = q[2] + ldc<C>(a.gB, i);
+      wE[k] = E + (a.use_col ? ldc<C>(a.col, s) : C(0));
+      dwE[k] = dE + ((a.use_col && a.dcol) ? ldc<C>(a.dcol, s) : C(0));
       lm = fmax(lm, wE[k]);
     }
   }
-  const double M = block_max(lm, red);  // its barriers publish X
-  const double Ms = M == NI ? 0.0 : M;
-  double r[CPT], dr[CPT];
-  double ls = 0.0, lds = 0.0;
+  const C M = block_max(lm, red);  // its barriers publish X
+  const C Ms = M == NI ? C(0) : M;
+  C r[CPT], dr[CPT];
+  C ls = C(0), lds = C(0);
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int s = threadIdx.x + k * NT;
-    r[k] = dr[k] = 0.0;
+    r[k] = dr[k] = C(0);
     if (s < S) {
       const int p = t.par[s];
       if (p >= 0) gE[k] += X[p];
-      r[k] = exp2(wE[k] - Ms);
-      dr[k] = LN2D * r[k] * dwE[k];
+      r[k] = xexp2(wE[k] - Ms);
+      dr[k] = (C)LN2D * r[k] * dwE[k];
     }
     ls += r[k];
     lds += dr[k];
   }
-  const double rowsum = block_sum(ls, red);
-  const double drowsum = block_sum(lds, red);
-  double anc[CPT], danc[CPT];
+  const C rowsum = block_sum(ls, red);
+  const C drowsum = block_sum(lds, red);
+  C anc[CPT], danc[CPT];
   reg_path_sums<CPT>(t, r, anc, EV, red);
   reg_path_sums<CPT>(t, dr, danc, EV, red);
-  double u[CPT], du[CPT];
-  double lu = 0.0, ldu = 0.0;
+  C u[CPT], du[CPT];
+  C lu = C(0), ldu = C(0);
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
-    const double denom = rowsum - anc[k];
-    const double dden = drowsum - danc[k];
-    const bool pos = denom > 0.0;
-    u[k] = pos ? q2g[k] / denom : 0.0;
-    du[k] = pos ? (dq2[k] - u[k] * dden) / denom : 0.0;
+    const C denom = rowsum - anc[k];
+    const C dden = drowsum - danc[k];
+    const bool pos = denom > C(0);
+    u[k] = pos ? q2g[k] / denom : C(0);
+    du[k] = pos ? (dq2[k] - u[k] * dden) / denom : C(0);
     lu += u[k];
     ldu += du[k];
   }
-  const double tot = block_sum(lu, red);
-  const double dtot = block_sum(ldu, red);
-  double ex[CPT], dex[CPT];
+  const C tot = block_sum(lu, red);
+  const C dtot = block_sum(ldu, red);
+  C ex[CPT], dex[CPT];
   reg_subtree_sums<CPT>(t, u, ex, EV, red);
   reg_subtree_sums<CPT>(t, du, dex, EV, red);
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int s = threadIdx.x + k * NT;
     if (s < S) {
-      const double pv = dr[k] * (tot - ex[k]) + r[k] * (dtot - dex[k]);
+      const C pv = dr[k] * (tot - ex[k]) + r[k] * (dtot - dex[k]);
       a.oE[base + s] = (T)(gE[k] + pv);
       a.ocol[base + s] = (T)pv;
     }
@@ -160,14 +165,14 @@ struct WsoArgs {
 //   d_aw_k = v (dw_L w~_k + w_L dw~_k)
 //   d_out  = v d(diag) + dp' (A - sub) + p' (dA - dsub) + [v d(sl_wt)] at the parent,
 // u = v w_L w~_2 / denom, A = sum u, sub = subtree sums of u, p' = 2^((col +) Pi - rowmax).
-template <typename T, int CPT>
+template <typename T, int CPT, typename C = double>
 __global__ __launch_bounds__(NT) void wso_kernel(OpsTree t, WsoArgs<T> a) {
-  extern __shared__ double smd[];
+  extern __shared__ double smd[];  // raw storage: C values
   const int S = t.S;
-  double* Z = smd;       // child-edge contributions by column
-  double* EV = smd + S;  // 2S scan buffer
-  __shared__ double red[NW];
-  const double NI = -__builtin_inf();
+  C* Z = reinterpret_cast<C*>(smd);       // child-edge contributions by column
+  C* EV = reinterpret_cast<C*>(smd) + S;  // 2S scan buffer
+  __shared__ C red[NW];
+  const C NI = ninf<C>();
   const int w = blockIdx.x;
   const long long grow = a.ws + w;
   const long long item = a.item[grow];
@@ -175,90 +180,90 @@ __global__ __launch_bounds__(NT) void wso_kernel(OpsTree t, WsoArgs<T> a) {
   const size_t lb = (size_t)item * S;
   const size_t rb = (size_t)grow * S;
   const size_t wb = (size_t)w * S;
-  const double rm = ld(a.rowmax, grow);
-  const double rms = rm == NI ? 0.0 : rm;
+  const C rm = ldc<C>(a.rowmax, grow);
+  const C rms = rm == NI ? C(0) : rm;
   const long long lstate = a.use_leaf ? a.leaf_state[grow] : -1;
-  double pp[CPT], dpp[CPT], vv[CPT];
-  double lsum = 0.0, ldsum = 0.0;
+  C pp[CPT], dpp[CPT], vv[CPT];
+  C lsum = C(0), ldsum = C(0);
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int s = threadIdx.x + k * NT;
-    pp[k] = dpp[k] = vv[k] = 0.0;
+    pp[k] = dpp[k] = vv[k] = C(0);
     if (s < S) {
-      const double pi = ld(a.Pi, rb + s);
-      pp[k] = exp2(pi + (a.use_col ? ld(a.col, s) : 0.0) - rms);
-      dpp[k] = LN2D * pp[k] * ld(a.dPi, rb + s);
-      vv[k] = ld(a.v, wb + s);
-      Z[s] = 0.0;
+      const C pi = ldc<C>(a.Pi, rb + s);
+      pp[k] = xexp2(pi + (a.use_col ? ldc<C>(a.col, s) : C(0)) - rms);
+      dpp[k] = (C)LN2D * pp[k] * ldc<C>(a.dPi, rb + s);
+      vv[k] = ldc<C>(a.v, wb + s);
+      Z[s] = C(0);
     }
     lsum += pp[k];
     ldsum += dpp[k];
   }
-  const double rowsum = block_sum(lsum, red);
-  const double drowsum = block_sum(ldsum, red);
-  double anc[CPT], danc[CPT];
+  const C rowsum = block_sum(lsum, red);
+  const C drowsum = block_sum(ldsum, red);
+  C anc[CPT], danc[CPT];
   reg_path_sums<CPT>(t, pp, anc, EV, red);
   reg_path_sums<CPT>(t, dpp, danc, EV, red);
-  double dself[CPT], u[CPT], du[CPT];
-  double lu = 0.0, ldu = 0.0;
+  C dself[CPT], u[CPT], du[CPT];
+  C lu = C(0), ldu = C(0);
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int s = threadIdx.x + k * NT;
-    dself[k] = u[k] = du[k] = 0.0;
+    dself[k] = u[k] = du[k] = C(0);
     if (s < S) {
       const size_t ci = cb + s;
-      const double denom = rowsum - anc[k];
-      const double ddenom = drowsum - danc[k];
-      const double invd = denom > 0.0 ? 1.0 / denom : 0.0;
-      const double pi = ld(a.Pi, rb + s), dpi = ld(a.dPi, rb + s);
+      const C denom = rowsum - anc[k];
+      const C ddenom = drowsum - danc[k];
+      const C invd = denom > C(0) ? C(1) / denom : C(0);
+      const C pi = ldc<C>(a.Pi, rb + s), dpi = ldc<C>(a.dPi, rb + s);
       const int c1 = t.c1[s], c2 = t.c2[s];
-      const double p1 = c1 >= 0 ? ld(a.Pi, rb + c1) : NI, p2 = c2 >= 0 ? ld(a.Pi, rb + c2) : NI;
-      const double dp1 = c1 >= 0 ? ld(a.dPi, rb + c1) : 0.0, dp2 = c2 >= 0 ? ld(a.dPi, rb + c2) : 0.0;
+      const C p1 = c1 >= 0 ? ldc<C>(a.Pi, rb + c1) : NI, p2 = c2 >= 0 ? ldc<C>(a.Pi, rb + c2) : NI;
+      const C dp1 = c1 >= 0 ? ldc<C>(a.dPi, rb + c1) : C(0), dp2 = c2 >= 0 ? ldc<C>(a.dPi, rb + c2) : C(0);
       const bool hit = lstate == s;
-      double tk[6], dtk[6];
-      tk[0] = ld(a.DL, ci) + pi;
-      dtk[0] = ld(a.dDL, ci) + dpi;
-      tk[1] = pi + ld(a.Ebar, ci);
-      dtk[1] = dpi + ld(a.dEbar, ci);
-      tk[2] = ld(a.Pb, rb + s) + ld(a.E, ci);
-      dtk[2] = ld(a.dPb, rb + s) + ld(a.dE, ci);
-      tk[3] = ld(a.SL1, ci) + p1;
-      dtk[3] = ld(a.dSL1, ci) + dp1;
-      tk[4] = ld(a.SL2, ci) + p2;
-      dtk[4] = ld(a.dSL2, ci) + dp2;
-      tk[5] = hit ? ld(a.leaf_logp, lb + s) : NI;
-      dtk[5] = hit ? ld(a.dleaf_logp, lb + s) : 0.0;
-      double m = tk[0];
+      C tk[6], dtk[6];
+      tk[0] = ldc<C>(a.DL, ci) + pi;
+      dtk[0] = ldc<C>(a.dDL, ci) + dpi;
+      tk[1] = pi + ldc<C>(a.Ebar, ci);
+      dtk[1] = dpi + ldc<C>(a.dEbar, ci);
+      tk[2] = ldc<C>(a.Pb, rb + s) + ldc<C>(a.E, ci);
+      dtk[2] = ldc<C>(a.dPb, rb + s) + ldc<C>(a.dE, ci);
+      tk[3] = ldc<C>(a.SL1, ci) + p1;
+      dtk[3] = ldc<C>(a.dSL1, ci) + dp1;
+      tk[4] = ldc<C>(a.SL2, ci) + p2;
+      dtk[4] = ldc<C>(a.dSL2, ci) + dp2;
+      tk[5] = hit ? ldc<C>(a.leaf_logp, lb + s) : NI;
+      dtk[5] = hit ? ldc<C>(a.dleaf_logp, lb + s) : C(0);
+      C m = tk[0];
 #pragma unroll
       for (int j = 1; j < 6; ++j) m = fmax(m, tk[j]);
-      const double ms = m == NI ? 0.0 : m;
-      double wk[6], tot = 0.0;
+      const C ms = m == NI ? C(0) : m;
+      C wk[6], tot = C(0);
 #pragma unroll
       for (int j = 0; j < 6; ++j) {
-        wk[j] = exp2(tk[j] - ms);
+        wk[j] = xexp2(tk[j] - ms);
         tot += wk[j];
       }
-      const double inv = tot > 0.0 ? 1.0 / tot : 0.0;
-      double dlse = 0.0;
+      const C inv = tot > C(0) ? C(1) / tot : C(0);
+      C dlse = C(0);
 #pragma unroll
       for (int j = 0; j < 6; ++j) {
         wk[j] *= inv;
-        if (wk[j] != 0.0) dlse += wk[j] * dtk[j];
+        if (wk[j] != C(0)) dlse += wk[j] * dtk[j];
       }
-      double dw[6];
+      C dw[6];
 #pragma unroll
-      for (int j = 0; j < 6; ++j) dw[j] = wk[j] != 0.0 ? LN2D * wk[j] * (dtk[j] - dlse) : 0.0;
-      double wL = 1.0, dwL = 0.0;
+      for (int j = 0; j < 6; ++j) dw[j] = wk[j] != C(0) ? (C)LN2D * wk[j] * (dtk[j] - dlse) : C(0);
+      C wL = C(1), dwL = C(0);
       if (a.dts) {
-        const double dr = ld(a.dts, wb + s);
-        const double dl = tot > 0.0 ? log2(tot) + m : NI;
-        const double pm = fmax(dl, dr);
-        const double pms = pm == NI ? 0.0 : pm;
-        const double pnew = log2(exp2(dl - pms) + exp2(dr - pms)) + pm;
-        wL = dl != NI ? exp2(dl - pnew) : 0.0;
-        dwL = (dr != NI && dl != NI) ? LN2D * wL * (1.0 - wL) * (dlse - ld(a.ddts, wb + s)) : 0.0;
+        const C dr = ldc<C>(a.dts, wb + s);
+        const C dl = tot > C(0) ? xlog2(tot) + m : NI;
+        const C pm = fmax(dl, dr);
+        const C pms = pm == NI ? C(0) : pm;
+        const C pnew = xlog2(xexp2(dl - pms) + xexp2(dr - pms)) + pm;
+        wL = dl != NI ? xexp2(dl - pnew) : C(0);
+        dwL = (dr != NI && dl != NI) ? (C)LN2D * wL * (C(1) - wL) * (dlse - ldc<C>(a.ddts, wb + s)) : C(0);
       }
-      double da[6];
+      C da[6];
 #pragma unroll
       for (int j = 0; j < 6; ++j) da[j] = vv[k] * (dwL * wk[j] + wL * dw[j]);
       a.aw0[wb + s] = (T)da[0];
@@ -269,8 +274,8 @@ __global__ __launch_bounds__(NT) void wso_kernel(OpsTree t, WsoArgs<T> a) {
       a.aw4[wb + s] = (T)da[4];
       if (c1 >= 0) Z[c1] = da[3];
       if (c2 >= 0) Z[c2] = da[4];
-      const double pc = wL * wk[2] * invd;
-      const double dpc = (dwL * wk[2] + wL * dw[2]) * invd - pc * invd * ddenom;
+      const C pc = wL * wk[2] * invd;
+      const C dpc = (dwL * wk[2] + wL * dw[2]) * invd - pc * invd * ddenom;
       u[k] = vv[k] * pc;
       du[k] = vv[k] * dpc;
       dself[k] = da[0] + da[1];
@@ -278,17 +283,17 @@ __global__ __launch_bounds__(NT) void wso_kernel(OpsTree t, WsoArgs<T> a) {
     lu += u[k];
     ldu += du[k];
   }
-  const double A = block_sum(lu, red);  // its barriers publish Z
-  const double dA = block_sum(ldu, red);
-  double sub[CPT], dsub[CPT];
+  const C A = block_sum(lu, red);  // its barriers publish Z
+  const C dA = block_sum(ldu, red);
+  C sub[CPT], dsub[CPT];
   reg_subtree_sums<CPT>(t, u, sub, EV, red);
   reg_subtree_sums<CPT>(t, du, dsub, EV, red);
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int s = threadIdx.x + k * NT;
     if (s < S) {
-      double o = dself[k] + dpp[k] * (A - sub[k]) + pp[k] * (dA - dsub[k]) + Z[s];
-      if (a.rhs) o += ld(a.rhs, rb + s);
+      C o = dself[k] + dpp[k] * (A - sub[k]) + pp[k] * (dA - dsub[k]) + Z[s];
+      if (a.rhs) o += ldc<C>(a.rhs, rb + s);
       a.out[wb + s] = (T)o;
     }
   }
@@ -804,7 +809,7 @@ namespace {
 // float32 rows of up to 4096 states run the preorder-ownership kernel, the
 // others the float64 one
 template <typename T, int CPT>
-int launch_wso(const kbo::OpsTree& t, const kbo::WsoArgs<T>& a, int W, size_t lds, hipStream_t st) {
+int launch_wso(const kbo::OpsTree& t, const kbo::WsoArgs<T>& a, int W, bool f32, size_t lds, hipStream_t st) {
   if constexpr (std::is_same_v<T, float> && CPT <= 4) {  // (eight LDS rows: up to 4096 positions)
     const size_t lds_pre = (size_t)8 * (kbo::NT * CPT + 64) * sizeof(float);
     auto k = kbo::wso_pre_kernel<CPT>;
@@ -812,9 +817,33 @@ int launch_wso(const kbo::OpsTree& t, const kbo::WsoArgs<T>& a, int W, size_t ld
     hipLaunchKernelGGL(k, dim3(W), dim3(kbo::NT), lds_pre, st, t, a);
     return 0;
   }
+  if constexpr (std::is_same_v<T, float> && CPT == 8) {
+    if (f32) {  // rows too long for three float64 LDS rows
+      auto k = kbo::wso_kernel<T, CPT, float>;
+      if (int rc = set_lds(k, lds)) return rc;
+      hipLaunchKernelGGL(k, dim3(W), dim3(kbo::NT), lds, st, t, a);
+      return 0;
+    }
+  }
   auto k = kbo::wso_kernel<T, CPT>;
   if (int rc = set_lds(k, lds)) return rc;
   hipLaunchKernelGGL(k, dim3(W), dim3(kbo::NT), lds, st, t, a);
+  return 0;
+}
+
+template <typename T, int CPT>
+int launch_eso(const kbo::OpsTree& t, const kbo::EsoArgs<T>& a, bool f32, size_t lds, hipStream_t st) {
+  if constexpr (std::is_same_v<T, float> && CPT == 8) {
+    if (f32) {  // rows too long for three float64 LDS rows
+      auto k = kbo::eso_kernel<T, CPT, float>;
+      if (int rc = set_lds(k, lds)) return rc;
+      hipLaunchKernelGGL(k, dim3(a.G), dim3(kbo::NT), lds, st, t, a);
+      return 0;
+    }
+  }
+  auto k = kbo::eso_kernel<T, CPT>;
+  if (int rc = set_lds(k, lds)) return rc;
+  hipLaunchKernelGGL(k, dim3(a.G), dim3(kbo::NT), lds, st, t, a);
   return 0;
 }
 
@@ -845,8 +874,9 @@ int kb_estep_backward_so(const kb_tree* tr, const kb_estep_so_io* io, void* stre
   if (io->G < 0) return kb::set_error(KB_ERR_ARG, "G must be non-negative");
   if (io->G == 0) return 0;
   const int S = tr->S;
-  const size_t lds = (size_t)3 * S * sizeof(double);
-  if (int rc = check_lds(lds, S, KB_F64)) return rc;
+  size_t lds;
+  bool f32;
+  if (int rc = three_row_lds(S, io->dtype, &lds, &f32)) return rc;
   const kbo::OpsTree t = tr->dev();
   KBO_DISPATCH(io->dtype, S, {
     kbo::EsoArgs<T> a{io->G, S, io->use_col_weights,
@@ -857,8 +887,7 @@ int kb_estep_backward_so(const kb_tree* tr, const kb_estep_so_io* io, void* stre
                       (const T*)io->dEbar, (const T*)io->dlog_pS, (const T*)io->dlog_pD, (const T*)io->dlog_pL,
                       (const T*)io->dcol, (T*)io->d_grad_E, (T*)io->d_grad_pS, (T*)io->d_grad_pD,
                       (T*)io->d_grad_pL, (T*)io->d_grad_mc, (T*)io->col_rows};
-    if (int rc = set_lds(kbo::eso_kernel<T, CPT>, lds)) return rc;
-    hipLaunchKernelGGL((kbo::eso_kernel<T, CPT>), dim3(io->G), dim3(kbo::NT), lds, st_of(stream), t, a);
+    if (int rc = launch_eso<T, CPT>(t, a, f32, lds, st_of(stream))) return rc;
   });
   KBO_HIP(hipGetLastError());
   return 0;
@@ -873,8 +902,9 @@ int kb_wave_backward_so(const kb_tree* tr, const kb_wave_so_io* io, void* stream
     return kb::set_error(KB_ERR_ARG, "dts and d_dts must be given together");
   if (io->W == 0) return 0;
   const int S = tr->S;
-  const size_t lds = (size_t)3 * S * sizeof(double);
-  if (int rc = check_lds(lds, S, KB_F64)) return rc;
+  size_t lds;
+  bool f32;
+  if (int rc = three_row_lds(S, io->dtype, &lds, &f32)) return rc;
   const kbo::OpsTree t = tr->dev();
   KBO_DISPATCH(io->dtype, S, {
     kbo::WsoArgs<T> a{S, io->W, io->use_col_weights, io->use_leaf_index, io->ws, io->const_stride,
@@ -886,7 +916,7 @@ int kb_wave_backward_so(const kb_tree* tr, const kb_wave_so_io* io, void* stream
                       (const T*)io->dleaf_logp, (const T*)io->dts, (const T*)io->d_dts, (const T*)io->d_rhs,
                       (T*)io->d_out, (T*)io->d_aw0, (T*)io->d_aw1, (T*)io->d_aw2, (T*)io->d_aw345,
                       (T*)io->d_aw3, (T*)io->d_aw4};
-    if (int rc = launch_wso<T, CPT>(t, a, io->W, lds, st_of(stream))) return rc;
+    if (int rc = launch_wso<T, CPT>(t, a, io->W, f32, lds, st_of(stream))) return rc;
   });
   KBO_HIP(hipGetLastError());
   return 0;

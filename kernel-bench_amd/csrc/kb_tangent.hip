@@ -40,79 +40,79 @@ struct EtArgs {
 //   dE_new = w0 (dpS + dE[c1] + dE[c2]) + w1 (dpD + 2 dE) + w2 (dE + dEbar) + w3 dpL
 // (0 where E_new = -inf), iterated from dE0 (or 0) until
 // max|dE_new - dE| <= tol * max(1, max|dE_new|) or max_iter steps.
-template <typename T, int CPT>
+template <typename T, int CPT, typename C = double>
 __global__ __launch_bounds__(NT) void etan_kernel(OpsTree t, EtArgs<T> a) {
-  extern __shared__ double smd[];
+  extern __shared__ double smd[];  // raw storage: C values
   const int S = t.S;
-  double* D = smd;       // E row, then the tangent row
-  double* EV = smd + S;  // 2S Euler scan
-  __shared__ double red[NW];
-  const double NI = -__builtin_inf();
+  C* D = reinterpret_cast<C*>(smd);       // E row, then the tangent row
+  C* EV = reinterpret_cast<C*>(smd) + S;  // 2S Euler scan
+  __shared__ C red[NW];
+  const C NI = ninf<C>();
   const size_t base = (size_t)blockIdx.x * S;
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int s = threadIdx.x + k * NT;
-    if (s < S) D[s] = (double)a.E[base + s];
+    if (s < S) D[s] = (C)a.E[base + s];
   }
   __syncthreads();
-  double r[CPT], K[CPT], w0[CPT], lin[CPT], wb[CPT], den[CPT], dm[CPT];
+  C r[CPT], K[CPT], w0[CPT], lin[CPT], wb[CPT], den[CPT], dm[CPT];
   bool pos[CPT];
   {
-    double wE[CPT];
-    double lm = NI;
+    C wE[CPT];
+    C lm = NI;
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int s = threadIdx.x + k * NT;
       wE[k] = NI;
       if (s < S) {
-        wE[k] = D[s] + (a.use_col ? (double)a.col[s] : 0.0);
+        wE[k] = D[s] + (a.use_col ? (C)a.col[s] : C(0));
         lm = fmax(lm, wE[k]);
       }
     }
-    const double M = block_max(lm, red);
-    const double Ms = M == NI ? 0.0 : M;
-    double ls = 0.0;
+    const C M = block_max(lm, red);
+    const C Ms = M == NI ? C(0) : M;
+    C ls = C(0);
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int s = threadIdx.x + k * NT;
-      r[k] = s < S ? exp2(wE[k] - Ms) : 0.0;
+      r[k] = s < S ? xexp2(wE[k] - Ms) : C(0);
       ls += r[k];
     }
-    const double rowsum = block_sum(ls, red);
-    double anc[CPT];
+    const C rowsum = block_sum(ls, red);
+    C anc[CPT];
     reg_path_sums<CPT>(t, r, anc, EV, red);
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int s = threadIdx.x + k * NT;
-      K[k] = w0[k] = lin[k] = wb[k] = dm[k] = 0.0;
-      den[k] = 1.0;
+      K[k] = w0[k] = lin[k] = wb[k] = dm[k] = C(0);
+      den[k] = C(1);
       pos[k] = false;
       if (s < S) {
         const size_t i = base + s;
-        const double E = D[s];
+        const C E = D[s];
         const int c1 = t.c1[s], c2 = t.c2[s];
-        const double Es1 = c1 >= 0 ? D[c1] : NI, Es2 = c2 >= 0 ? D[c2] : NI;
-        const double denom = rowsum - anc[k];
-        pos[k] = denom > 0.0;
-        den[k] = pos[k] ? denom : 1.0;
-        const double Eb = pos[k] ? log2(den[k]) + M + (double)a.mt[i] : NI;
-        const double t0 = (double)a.pS[i] + Es1 + Es2;
-        const double t1 = (double)a.pD[i] + 2.0 * E;
-        const double t2 = E + Eb;
-        const double t3 = (double)a.pL[i];
-        const double m = fmax(fmax(t0, t1), fmax(t2, t3));
-        const double ms = m == NI ? 0.0 : m;
-        const double e0 = exp2(t0 - ms), e1 = exp2(t1 - ms), e2 = exp2(t2 - ms), e3 = exp2(t3 - ms);
-        const double total = e0 + e1 + e2 + e3;
-        const double En = log2(total) + m;
-        dm[k] = pos[k] ? (double)a.dmt[i] : 0.0;
-        if (En != NI && total > 0.0) {
-          const double inv = 1.0 / total;
+        const C Es1 = c1 >= 0 ? D[c1] : NI, Es2 = c2 >= 0 ? D[c2] : NI;
+        const C denom = rowsum - anc[k];
+        pos[k] = denom > C(0);
+        den[k] = pos[k] ? denom : C(1);
+        const C Eb = pos[k] ? xlog2(den[k]) + M + (C)a.mt[i] : NI;
+        const C t0 = (C)a.pS[i] + Es1 + Es2;
+        const C t1 = (C)a.pD[i] + C(2) * E;
+        const C t2 = E + Eb;
+        const C t3 = (C)a.pL[i];
+        const C m = fmax(fmax(t0, t1), fmax(t2, t3));
+        const C ms = m == NI ? C(0) : m;
+        const C e0 = xexp2(t0 - ms), e1 = xexp2(t1 - ms), e2 = xexp2(t2 - ms), e3 = xexp2(t3 - ms);
+        const C total = e0 + e1 + e2 + e3;
+        const C En = xlog2(total) + m;
+        dm[k] = pos[k] ? (C)a.dmt[i] : C(0);
+        if (En != NI && total > C(0)) {
+          const C inv = C(1) / total;
           w0[k] = e0 * inv;
-          const double w1 = e1 * inv, w2 = e2 * inv, w3 = e3 * inv;
-          K[k] = w0[k] * (double)a.dpS[i] + w1 * (double)a.dpD[i] + w3 * (double)a.dpL[i] + w2 * dm[k];
-          lin[k] = 2.0 * w1 + w2;
-          wb[k] = pos[k] ? w2 : 0.0;
+          const C w1 = e1 * inv, w2 = e2 * inv, w3 = e3 * inv;
+          K[k] = w0[k] * (C)a.dpS[i] + w1 * (C)a.dpD[i] + w3 * (C)a.dpL[i] + w2 * dm[k];
+          lin[k] = C(2) * w1 + w2;
+          wb[k] = pos[k] ? w2 : C(0);
         }
       }
     }
@@ -121,22 +121,22 @@ __global__ __launch_bounds__(NT) void etan_kernel(OpsTree t, EtArgs<T> a) {
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int s = threadIdx.x + k * NT;
-    if (s < S) D[s] = a.dE0 ? (double)a.dE0[base + s] : 0.0;
+    if (s < S) D[s] = a.dE0 ? (C)a.dE0[base + s] : C(0);
   }
   __syncthreads();
 
   // q[k] = dRS - dAS[s]; reads D, leaves it untouched.
-  auto tangent_q = [&](double (&q)[CPT]) {
-    double x[CPT];
-    double lsum = 0.0;
+  auto tangent_q = [&](C (&q)[CPT]) {
+    C x[CPT];
+    C lsum = C(0);
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int s = threadIdx.x + k * NT;
-      x[k] = s < S ? r[k] * D[s] : 0.0;
+      x[k] = s < S ? r[k] * D[s] : C(0);
       lsum += x[k];
     }
-    const double dRS = block_sum(lsum, red);
-    double dAS[CPT];
+    const C dRS = block_sum(lsum, red);
+    C dAS[CPT];
     reg_path_sums<CPT>(t, x, dAS, EV, red);
 #pragma unroll
     for (int k = 0; k < CPT; ++k) q[k] = dRS - dAS[k];
@@ -144,16 +144,16 @@ __global__ __launch_bounds__(NT) void etan_kernel(OpsTree t, EtArgs<T> a) {
 
   int it = 0;
   for (;;) {
-    double q[CPT], nx[CPT];
+    C q[CPT], nx[CPT];
     tangent_q(q);
-    double ld = 0.0, lsc = 0.0;
+    C ld = C(0), lsc = C(0);
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int s = threadIdx.x + k * NT;
-      nx[k] = 0.0;
+      nx[k] = C(0);
       if (s < S) {
         const int c1 = t.c1[s], c2 = t.c2[s];
-        const double ch = (c1 >= 0 ? D[c1] : 0.0) + (c2 >= 0 ? D[c2] : 0.0);
+        const C ch = (c1 >= 0 ? D[c1] : C(0)) + (c2 >= 0 ? D[c2] : C(0));
         nx[k] = K[k] + w0[k] * ch + lin[k] * D[s] + wb[k] * (q[k] / den[k]);
         ld = fmax(ld, fabs(nx[k] - D[s]));
         lsc = fmax(lsc, fabs(nx[k]));
@@ -166,12 +166,12 @@ __global__ __launch_bounds__(NT) void etan_kernel(OpsTree t, EtArgs<T> a) {
       if (s < S) D[s] = nx[k];
     }
     ++it;
-    const double md = block_max(ld, red);  // its barriers also publish D
-    const double sc = block_max(lsc, red);
-    if (md <= a.tol * fmax(1.0, sc) || it >= a.max_iter) break;
+    const C md = block_max(ld, red);  // its barriers also publish D
+    const C sc = block_max(lsc, red);
+    if (md <= a.tol * fmax(C(1), sc) || it >= a.max_iter) break;
   }
   // children and Ebar tangents at the final dE
-  double q[CPT];
+  C q[CPT];
   tangent_q(q);
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
@@ -180,9 +180,9 @@ __global__ __launch_bounds__(NT) void etan_kernel(OpsTree t, EtArgs<T> a) {
       const size_t i = base + s;
       const int c1 = t.c1[s], c2 = t.c2[s];
       a.dE[i] = (T)D[s];
-      a.dEs1[i] = (T)(c1 >= 0 ? D[c1] : 0.0);
-      a.dEs2[i] = (T)(c2 >= 0 ? D[c2] : 0.0);
-      a.dEbar[i] = (T)(pos[k] ? q[k] / den[k] + dm[k] : 0.0);
+      a.dEs1[i] = (T)(c1 >= 0 ? D[c1] : C(0));
+      a.dEs2[i] = (T)(c2 >= 0 ? D[c2] : C(0));
+      a.dEbar[i] = (T)(pos[k] ? q[k] / den[k] + dm[k] : C(0));
     }
   }
   if (a.n_iter && threadIdx.x == 0) a.n_iter[blockIdx.x] = it;
@@ -685,6 +685,22 @@ using namespace kbo_host;
 
 namespace {
 
+template <typename T, int CPT>
+int launch_etan(const kbo::OpsTree& t, const kbo::EtArgs<T>& a, bool f32, size_t lds, hipStream_t st) {
+  if constexpr (std::is_same_v<T, float> && CPT == 8) {
+    if (f32) {  // rows too long for three float64 LDS rows
+      auto k = kbo::etan_kernel<T, CPT, float>;
+      if (int rc = set_lds(k, lds)) return rc;
+      hipLaunchKernelGGL(k, dim3(a.G), dim3(kbo::NT), lds, st, t, a);
+      return 0;
+    }
+  }
+  auto k = kbo::etan_kernel<T, CPT>;
+  if (int rc = set_lds(k, lds)) return rc;
+  hipLaunchKernelGGL(k, dim3(a.G), dim3(kbo::NT), lds, st, t, a);
+  return 0;
+}
+
 // float32 rows run the preorder-ownership kernel, float64 rows the float64 one
 template <typename T, int CPT>
 int launch_wave_tan(const kbo::OpsTree& t, const kbo::WtArgs<T>& a, int W, size_t lds, hipStream_t st) {
@@ -714,8 +730,9 @@ int kb_e_tangent_fixed_point(const kb_tree* tr, const kb_etan_io* io, void* stre
   if (io->max_iter < 1 || !(io->tol >= 0.0)) return kb::set_error(KB_ERR_ARG, "max_iter must be >= 1 and tol >= 0");
   if (io->G == 0) return 0;
   const int S = tr->S;
-  const size_t lds = (size_t)3 * S * sizeof(double);
-  if (int rc = check_lds(lds, S, KB_F64)) return rc;
+  size_t lds;
+  bool f32;
+  if (int rc = three_row_lds(S, io->dtype, &lds, &f32)) return rc;
   const kbo::OpsTree t = tr->dev();
   KBO_DISPATCH(io->dtype, S, {
     kbo::EtArgs<T> a{io->G, S, io->use_col_weights, io->max_iter, io->tol,
@@ -723,8 +740,7 @@ int kb_e_tangent_fixed_point(const kb_tree* tr, const kb_etan_io* io, void* stre
                      (const T*)io->max_coupling, (const T*)io->col_log_probs, (const T*)io->dlog_pS,
                      (const T*)io->dlog_pD, (const T*)io->dlog_pL, (const T*)io->dmax_coupling, (const T*)io->dE0,
                      (T*)io->dE, (T*)io->dE_s1, (T*)io->dE_s2, (T*)io->dEbar, io->n_iter};
-    if (int rc = set_lds(kbo::etan_kernel<T, CPT>, lds)) return rc;
-    hipLaunchKernelGGL((kbo::etan_kernel<T, CPT>), dim3(io->G), dim3(kbo::NT), lds, st_of(stream), t, a);
+    if (int rc = launch_etan<T, CPT>(t, a, f32, lds, st_of(stream))) return rc;
   });
   KBO_HIP(hipGetLastError());
   return 0;

@@ -45,11 +45,28 @@ def _rel(got, ref):
 @pytest.mark.parametrize("dt", [torch.float64, torch.float32])
 @pytest.mark.parametrize("use_col", [False, True])
 def test_e_step_backward_so_matches_oracle(dt, use_col):
-    from kbench.core.kernels.e_step_so import e_step_backward_so
-
     print(f"[e-so] dtype={dt} use_col={use_col}", flush=True)
     static, _, _ = _static("1")
     prob, _, _ = kbtest.oracle_forward("1")
+    _eso_case(prob, static.state_helpers, dt, use_col)
+
+
+@pytest.mark.parametrize("use_col", [False, True])
+def test_e_step_backward_so_on_long_float32_rows(use_col):
+    """S = 8191: float32 rows too long for three float64 LDS rows compute in float32 (1e-4 of the max
+    against the float64 oracle); float64 rows of that length stop with the wrappers' ValueError."""
+    print(f"[e-so] S=8191 float32 use_col={use_col}", flush=True)
+    problem, static, _, _ = _big_tree(4096, True)
+    prob = O.Problem.from_dict(problem)
+    assert prob.S == 8191
+    _eso_case(prob, static.state_helpers, torch.float32, use_col)
+    with pytest.raises(ValueError, match="LDS"):
+        _eso_case(prob, static.state_helpers, torch.float64, use_col, check=False)
+
+
+def _eso_case(prob, h, dt, use_col, check=True):
+    from kbench.core.kernels.e_step_so import e_step_backward_so
+
     rng = np.random.default_rng(31)
     S, G, tree = prob.S, 3, prob.tree
     E = np.log2(rng.uniform(0.05, 0.6, (G, S)))
@@ -62,14 +79,15 @@ def test_e_step_backward_so_matches_oracle(dt, use_col):
     dEs2 = np.where(np.isfinite(Es2), dEs2, 0.0)
     dEb = np.where(np.isfinite(Eb), dEb, 0.0)
     dcol = rng.normal(size=S)
-    ref = O.e_step_backward_so(E, En, Es1, Es2, Eb, pS, pD, pL, col, tree, gN, gB, dE, dEn, dEs1, dEs2, dEb, dpS, dpD,
-                               dpL, dcol, use_col)
-    h = static.state_helpers
+    ref = None if not check else O.e_step_backward_so(E, En, Es1, Es2, Eb, pS, pD, pL, col, tree, gN, gB, dE, dEn,
+                                                        dEs1, dEs2, dEb, dpS, dpD, dpL, dcol, use_col)
     got = e_step_backward_so(*(_t(x, dt) for x in (E, En, Es1, Es2, Eb, pS, pD, pL, col)), h["node_parent"],
                              h["node_child1"], h["node_child2"], int(h["max_ancestor_depth"]), _t(gN, dt), None, None,
                              _t(gB, dt), *(_t(x, dt) for x in (dE, dEn, dEs1, dEs2, dEb, dpS, dpD, dpL, dcol)),
                              use_col_weights=use_col)
     torch.cuda.synchronize()
+    if not check:
+        return
     for name, g, r in zip(("dE", "dpS", "dpD", "dpL", "dmc", "dcol"), got, ref):
         e = _rel(g.cpu().numpy(), r)
         print(f"  {name}: rel={e:.3e}")
@@ -209,14 +227,16 @@ def test_exact_hvp_matches_oracle(name, statewise, row_classes):
     assert e <= 1e-3
 
 
-def test_exact_hvp_on_a_large_tree_matches_oracle():
-    """S = 4095 (three small families): the class / graph HVP against the oracle's HVP (1e-3 of max
-    |H u|), through the kernels' 4-position shapes."""
+@pytest.mark.parametrize("leaves", [2048, 4096])
+def test_exact_hvp_on_a_large_tree_matches_oracle(leaves):
+    """S = 4095 and 8191 (three small families): the class / graph HVP against the oracle's HVP (1e-3 of
+    max |H u|), through the kernels' 4- and 8-position shapes; at S = 8191 the E-step second-order,
+    E tangent and self-loop contractions compute in float32 (three float64 rows of S exceed the LDS)."""
     from dropin.hvp import HvpPlan
     from dropin.solve import plan_of, run_forward
 
-    print("[hvp] large tree leaves=2048 (S=4095)", flush=True)
-    problem, static, theta, cw = _big_tree(2048, True)
+    print(f"[hvp] large tree leaves={leaves} (S={2 * leaves - 1})", flush=True)
+    problem, static, theta, cw = _big_tree(leaves, True)
     _, sv = run_forward(static, theta, cw)
     u = np.random.default_rng(43).normal(size=tuple(theta.shape))
     hvp = HvpPlan(plan_of(static), theta, cw, sv, row_classes=True, graph=True)
@@ -233,150 +253,6 @@ def test_exact_hvp_on_a_large_tree_matches_oracle():
     e = _rel(Hu.cpu().numpy(), ref.reshape(-1))
     print(f"  |H u| = {np.abs(ref).max():.4e} rel={e:.3e}")
     assert e <= 1e-3
-
-
-def test_exact_hvp_refuses_trees_beyond_its_lds_rows():
-    """S = 8191: the E-step second-order kernel keeps three float64 rows of S in LDS (S <= 6741); the HVP
-    stops with the wrappers' ValueError before any launch instead of running past the LDS limit."""
-    from dropin.hvp import HvpPlan
-    from dropin.solve import plan_of, run_forward
-
-    _, static, theta, cw = _big_tree(4096, True)
-    _, sv = run_forward(static, theta, cw)
-    hvp = HvpPlan(plan_of(static), theta, cw, sv, row_classes=True)
-    with pytest.raises(ValueError, match="LDS"):
-        hvp(torch.ones(theta.numel(), dtype=theta.dtype, device="cuda"))
-
-
-def test_exact_hvp_config3_symmetric_linear_deterministic():
-    """Full size (config 3 with per-species theta, the Newton-CG setup): symmetry, linearity, determinism."""
-    import time
-
-    from dropin.hvp import HvpPlan
-    from dropin.solve import plan_of, run_forward
-
-    print("[hvp] config=3 statewise=True", flush=True)
-    static, theta, cw = _static("3", True)
-    _, sv = run_forward(static, theta, cw)
-    t0 = time.perf_counter()
-    hvp = HvpPlan(plan_of(static), theta, cw, sv)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    g = np.random.default_rng(35)
-    u1 = torch.as_tensor(g.normal(size=tuple(theta.shape)), dtype=theta.dtype).cuda().reshape(-1)
-    u2 = torch.as_tensor(g.normal(size=tuple(theta.shape)), dtype=theta.dtype).cuda().reshape(-1)
-    H1 = hvp(u1)
-    torch.cuda.synchronize()
-    t2 = time.perf_counter()
-    H1b = hvp(u1)
-    H2 = hvp(u2)
-    H12 = hvp(u1 + 2.0 * u2)
-    torch.cuda.synchronize()
-    print(f"  point cache {1e3 * (t1 - t0):.1f} ms, one HVP {1e3 * (t2 - t1):.1f} ms")
-    assert torch.equal(H1, H1b)
-    assert torch.isfinite(H1).all() and torch.isfinite(H2).all()
-    a, b = float((u2.double() * H1.double()).sum()), float((u1.double() * H2.double()).sum())
-    scale = max(abs(a), abs(b), 1e-30)
-    print(f"  u2.H u1={a:.6e} u1.H u2={b:.6e} asym={abs(a - b) / scale:.3e}")
-    assert abs(a - b) <= 5e-3 * scale
-    lin = _rel(H12.cpu().numpy(), (H1 + 2.0 * H2).cpu().numpy())
-    print(f"  linearity rel={lin:.3e}")
-    assert lin <= 1e-4
-
-
-def test_exact_hvp_config3_on_row_classes_matches_row_by_row():
-    """Config 3 on level waves (the bench's HVP): the tangent forward on one row per class and the
-    tangent reverse on one row per masked class give the row-by-row H u (rel 1e-4 of max |H u|),
-    bitwise the same on a second call."""
-    from dropin.hvp import HvpPlan
-    from dropin.solve import plan_of, run_forward
-    from kbench import synth
-    from kbench.fused import problem_to_captured
-    from kbench.runtime import make_static
-
-    print("[hvp] config=3 statewise=True level waves, row classes vs rows", flush=True)
-    q, _ = synth.level_waves(kbtest.problem("3", True))
-    cap = problem_to_captured(q)
-    static = make_static(cap, "cuda")
-    theta, cw = cap["inputs"]["theta"].cuda(), cap["inputs"]["col_weights"].cuda()
-    _, sv = run_forward(static, theta, cw)
-    plan = plan_of(static)
-    u = torch.as_tensor(np.random.default_rng(37).normal(size=tuple(theta.shape)), dtype=theta.dtype).cuda()
-    u = u.reshape(-1)
-    ref = HvpPlan(plan, theta, cw, sv)(u)
-    hc = HvpPlan(plan, theta, cw, sv, row_classes=True)
-    n_rc = hc.cls.rplan.C
-    got, again = hc(u), hc(u)
-    torch.cuda.synchronize()
-    e = kbtest.norm_rel_t(got, ref)
-    print(f"  rows {plan.C}, forward classes {hc.cls.fplan.C}, reverse classes {n_rc}; rel={e:.3e}")
-    assert hc.cls.fplan.C < plan.C and n_rc < plan.C
-    assert torch.equal(got, again)
-    assert e <= 1e-4
-
-
-@pytest.mark.parametrize("threshold", [0.3, 0.5])
-def test_exact_hvp_row_classes_with_pruned_rows(threshold):
-    """Adjoint pruning that drops rows at the point (config 1: 11 and 100 rows in the oracle): the reverse
-    classes split forward classes by the active flag (more reverse than forward classes) and the class
-    HVP still equals the row-by-row one."""
-    from dropin.hvp import HvpPlan
-    from dropin.solve import plan_of, run_forward
-    from kbench import synth
-    from kbench.fused import problem_to_captured
-    from kbench.runtime import make_static
-
-    print(f"[hvp pruned] config=1 adjoint_pruning_threshold={threshold}", flush=True)
-    p, _ = synth.level_waves(kbtest.problem("1", True))
-    cap = problem_to_captured(p)
-    cap["meta"]["solver_options"] = dict(cap["meta"]["solver_options"], adjoint_pruning_threshold=threshold)
-    static = make_static(cap, "cuda")
-    theta, cw = cap["inputs"]["theta"].cuda(), cap["inputs"]["col_weights"].cuda()
-    _, sv = run_forward(static, theta, cw)
-    plan = plan_of(static)
-    u = torch.as_tensor(np.random.default_rng(41).normal(size=tuple(theta.shape)), dtype=theta.dtype).cuda()
-    ref = HvpPlan(plan, theta, cw, sv)(u.reshape(-1))
-    hc = HvpPlan(plan, theta, cw, sv, row_classes=True)
-    got = hc(u.reshape(-1))
-    torch.cuda.synchronize()
-    n_off = sum(int((~m).sum()) for _, _, _, m in hc.waves)
-    e = kbtest.norm_rel_t(got, ref)
-    print(f"  rows {plan.C} inactive {n_off}; forward classes {hc.cls.fplan.C}, reverse classes {hc.cls.rplan.C};"
-          f" rel={e:.3e}")
-    assert n_off > 0 and hc.cls.rplan.C > hc.cls.fplan.C
-    assert e <= 1e-4
-
-
-@pytest.mark.parametrize("name,levels", [("1", False), ("3", True)])
-def test_exact_hvp_graph_replays_match_eager(name, levels):
-    """HvpPlan(graph=True): the tangent forward and reverse captured once and replayed; every replay
-    (new u each time, eager HVPs and host syncs in between) is bitwise the eager HVP."""
-    from dropin.hvp import HvpPlan
-    from dropin.solve import plan_of, run_forward
-    from kbench import synth
-    from kbench.fused import problem_to_captured
-    from kbench.runtime import make_static
-
-    print(f"[hvp graph] config={name} level_waves={levels}", flush=True)
-    p = kbtest.problem(name, True)
-    if levels:
-        p, _ = synth.level_waves(p)
-    cap = problem_to_captured(p)
-    static = make_static(cap, "cuda")
-    theta, cw = cap["inputs"]["theta"].cuda(), cap["inputs"]["col_weights"].cuda()
-    _, sv = run_forward(static, theta, cw)
-    plan = plan_of(static)
-    eager = HvpPlan(plan, theta, cw, sv, row_classes=True)
-    graphed = HvpPlan(plan, theta, cw, sv, row_classes=True, graph=True)
-    g = np.random.default_rng(38)
-    for i in range(4):
-        u = torch.as_tensor(g.normal(size=tuple(theta.shape)), dtype=theta.dtype).cuda().reshape(-1)
-        got = graphed(u)
-        ref = eager(u)
-        torch.cuda.synchronize()
-        e = kbtest.norm_rel_t(got, ref)
-        print(f"  call {i}: rel={e:.3e}", flush=True)
-        assert torch.equal(got, ref), e
 
 
 def _big_tree(leaves, statewise):

@@ -807,7 +807,8 @@ using namespace kbo_host;
 namespace {
 
 // float32 rows of up to 4096 states run the preorder-ownership kernel, the
-// others the float64 one
+// others the generic one (float64 arithmetic, float32 for float32 rows too
+// long for three float64 LDS rows)
 template <typename T, int CPT>
 int launch_wso(const kbo::OpsTree& t, const kbo::WsoArgs<T>& a, int W, bool f32, size_t lds, hipStream_t st) {
   if constexpr (std::is_same_v<T, float> && CPT <= 4) {  // (eight LDS rows: up to 4096 positions)

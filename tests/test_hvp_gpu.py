@@ -105,13 +105,21 @@ def _wave_consts(prob, saved, rng):
     return consts, dc
 
 
-@pytest.mark.parametrize("dt", [torch.float64, torch.float32])
-def test_wave_backward_so_matches_oracle(dt):
+@pytest.mark.parametrize("name,dt", [("1", torch.float64), ("1", torch.float32), ("big", torch.float32)])
+def test_wave_backward_so_matches_oracle(name, dt):
+    """Config 1, and S = 8191 ("big") in float32, where the generic kernel's rows are too long for three
+    float64 LDS rows and it computes in float32."""
     from kbench.core.kernels.wave_so import wave_backward_so
 
-    print(f"[wave-so] config=1 dtype={dt}", flush=True)
-    static, _, _ = _static("1")
-    prob, _, saved = kbtest.oracle_forward("1")
+    print(f"[wave-so] config={name} dtype={dt}", flush=True)
+    if name == "big":
+        problem, static, _, _ = _big_tree(4096, True)
+        prob = O.Problem.from_dict(problem)
+        th = np.asarray(problem["inputs"]["theta"], dtype=np.float32).astype(np.float64)
+        _, saved = O.forward(prob, th, np.asarray(problem["inputs"]["col_weights"], dtype=np.float64))
+    else:
+        static, _, _ = _static(name)
+        prob, _, saved = kbtest.oracle_forward(name)
     rng = np.random.default_rng(32)
     S, G, C = prob.S, 1, prob.C
     consts, dc = _wave_consts(prob, saved, rng)

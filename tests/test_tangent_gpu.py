@@ -9,6 +9,8 @@ forward (rel 1e-4), and at config 3 by size-independent properties:
 linearity in v and bitwise determinism.
 """
 
+import functools
+
 import numpy as np
 import pytest
 import torch
@@ -44,16 +46,18 @@ def _rel(got, ref):
 TOL = {torch.float64: 1e-9, torch.float32: 1e-4}
 
 
-@pytest.mark.parametrize("dt", [torch.float64, torch.float32])
-@pytest.mark.parametrize("statewise", [False, True])
-def test_e_tangent_fixed_point_matches_oracle(dt, statewise):
+@pytest.mark.parametrize("name,dt,statewise", [("1", torch.float64, False), ("1", torch.float32, False),
+                                               ("1", torch.float64, True), ("1", torch.float32, True),
+                                               ("big", torch.float32, True)])
+def test_e_tangent_fixed_point_matches_oracle(name, dt, statewise):
+    """Config 1, and S = 8191 ("big") in float32, where the rows are too long for three float64 LDS rows
+    and the kernel computes in float32."""
     from kbench.core.kernels.e_step_tangent import e_tangent_fixed_point
 
-    print(f"[e-tangent] config=1 statewise={statewise} dtype={dt}", flush=True)
-    static, theta, _ = _static("1", statewise)
-    prob, _, saved = kbtest.oracle_forward("1", statewise)
+    print(f"[e-tangent] config={name} statewise={statewise} dtype={dt}", flush=True)
+    static, prob, saved = _wave_fixture(name, statewise, dt)
     S, G = prob.S, 1
-    th = np.asarray(kbtest.problem("1", statewise)["inputs"]["theta"], dtype=np.float32).astype(np.float64)
+    th = _theta(name, statewise, prob)
     v = np.random.default_rng(11).normal(size=th.shape)
     d = O.param_jvp_uniform(th, v, prob.unnorm_row_max, prob.statewise, prob.itemwise)
     st = lambda x: np.broadcast_to(O.as_item_state(np.asarray(x, dtype=np.float64), S, G), (G, S)).copy()
@@ -72,19 +76,32 @@ def test_e_tangent_fixed_point_matches_oracle(dt, statewise):
         assert e <= TOL[dt]
 
 
+def _theta(name, statewise, prob):
+    """The fixture's theta as float64 (rounded through float32, as the GPU side holds it)."""
+    p = _big_problem(bool(statewise)) if name == "big" else kbtest.problem(name, statewise)
+    return np.asarray(p["inputs"]["theta"], dtype=np.float32).astype(np.float64)
+
+
+@functools.lru_cache(maxsize=2)
+def _big_problem(statewise):
+    """A 4096-leaf species tree (S = 8191) with three small families."""
+    from kbench import synth
+
+    cfg = synth.ProblemConfig(4096, 3, n_nni=1, family_leaves_median=21.0, family_leaves_sigma=0.6,
+                              family_leaves_max=80, statewise=statewise, seed=17)
+    return synth.build_problem(cfg)
+
+
 def _wave_fixture(name, statewise, dt):
     """(static on the GPU, oracle problem, oracle forward intermediates) of one configuration.
 
     ``name`` "big": a 4096-leaf species tree (S = 8191) with three small families.
     """
     if name == "big":
-        from kbench import synth
         from kbench.fused import problem_to_captured
         from kbench.runtime import make_static
 
-        cfg = synth.ProblemConfig(4096, 3, n_nni=1, family_leaves_median=21.0, family_leaves_sigma=0.6,
-                                  family_leaves_max=80, statewise=bool(statewise), seed=17)
-        p = synth.build_problem(cfg)
+        p = _big_problem(bool(statewise))
         static = make_static(problem_to_captured(p), "cuda")
         prob = O.Problem.from_dict(p)
         theta = np.asarray(p["inputs"]["theta"], dtype=np.float32).astype(np.float64)

@@ -49,8 +49,9 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "kernel-bench_amd"))
 
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_FILE = ROOT / "profiles" / "traffic_config3.json"
-COUNTERS_FILE = ROOT / "profiles" / "sq_counters_config3.json"
+def _profile_file(kind: str, config: str):
+    """The committed rocprofv3 summary (``traffic`` or ``sq_counters``) of one configuration."""
+    return ROOT / "profiles" / f"{kind}_config{config}.json"
 
 
 def parse():
@@ -311,22 +312,24 @@ def bench_hvp(args, static, theta, cw, summ, static_levels) -> None:
 
 
 # ---------------------------------------------------------------------- the solve metric
-def _counters(kernel_symbol: str):
+def _counters(kernel_symbol: str, config: str):
     """VALU / LDS figures of the committed rocprofv3 SQ-counter summary for ``kernel_symbol``."""
-    if not COUNTERS_FILE.exists():
+    f = _profile_file("sq_counters", config)
+    if not f.exists():
         return None
-    rec = json.loads(COUNTERS_FILE.read_text()).get("kernels", {})
+    rec = json.loads(f.read_text()).get("kernels", {})
     hits = {k: v for k, v in rec.items() if kernel_symbol in k}
     return hits or None
 
 
-def _traffic(kernel_symbol: str):
-    if not TRAFFIC_FILE.exists():
+def _traffic(kernel_symbol: str, config: str):
+    f = _profile_file("traffic", config)
+    if not f.exists():
         return None
     # HBM bytes per dispatch from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this command,
     # scaled by a copy kernel of known size; a kernel launched in several shapes: the
     # dispatch-weighted mean over them
-    rec = json.loads(TRAFFIC_FILE.read_text()).get("kernels", {})
+    rec = json.loads(f.read_text()).get("kernels", {})
     hits = [v for k, v in rec.items() if kernel_symbol in k]
     n = sum(float(v["dispatches"]) for v in hits)
     return round(sum(float(v["traffic"]) * float(v["dispatches"]) for v in hits) / n, 1) if n else None
@@ -426,18 +429,20 @@ def main():
     kernels = {"fwd_row_kernel": (fw, fwd_bytes), "bwd_row_kernel": (bw, bwd_bytes)}
     dom = max(kernels, key=lambda k: kernels[k][0].sum())
     dur, byt = kernels[dom]
+    # rows of more than 2048 states run the backward's low-register kernel
+    sym = "bwd_row_large_kernel" if dom == "bwd_row_kernel" and solver.S > 2048 else dom
     avg_ms = float(dur.mean())
     avg_bytes = float(byt.mean())
     achieved = avg_bytes / (avg_ms * 1e-3) / 1e9
-    counters = _counters(dom)
+    counters = _counters(sym, args.config)
     roofline = {
         "bound": "hbm",
-        "kernel": dom,
+        "kernel": sym,
         "achieved": round(achieved, 3),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 6),
-        "traffic": _traffic(dom) if args.config == "3" else None,
+        "traffic": _traffic(sym, args.config),
         "launches": int(len(dur)),
         "launch_unit": "one launch per clade-DAG dependency level",
         "avg_launch_ms": round(avg_ms, 5),
@@ -446,7 +451,7 @@ def main():
         "limiter": ("latency: HBM bytes are the roofline the kernel is priced against, but its time goes to "
                     "barriers, LDS and VALU issue (counters: per-shape VALU-active and LDS-wait fractions of "
                     "wave cycles)"),
-        "counters": counters if args.config == "3" else None,
+        "counters": counters,
     }
     whole_bytes = float(fwd_bytes.sum() + bwd_bytes.sum())
 

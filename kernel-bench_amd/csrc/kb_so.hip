@@ -826,6 +826,7 @@ int launch_wso(const kbo::OpsTree& t, const kbo::WsoArgs<T>& a, int W, bool f32,
       return 0;
     }
   }
+  if (f32) return kb::set_error(KB_ERR_ARG, "S=%d: no float32 wso_kernel for %d positions per thread", a.S, CPT);
   auto k = kbo::wso_kernel<T, CPT>;
   if (int rc = set_lds(k, lds)) return rc;
   hipLaunchKernelGGL(k, dim3(W), dim3(kbo::NT), lds, st, t, a);
@@ -842,6 +843,7 @@ int launch_eso(const kbo::OpsTree& t, const kbo::EsoArgs<T>& a, bool f32, size_t
       return 0;
     }
   }
+  if (f32) return kb::set_error(KB_ERR_ARG, "S=%d: no float32 eso_kernel for %d positions per thread", a.S, CPT);
   auto k = kbo::eso_kernel<T, CPT>;
   if (int rc = set_lds(k, lds)) return rc;
   hipLaunchKernelGGL(k, dim3(a.G), dim3(kbo::NT), lds, st, t, a);

@@ -695,6 +695,7 @@ int launch_etan(const kbo::OpsTree& t, const kbo::EtArgs<T>& a, bool f32, size_t
       return 0;
     }
   }
+  if (f32) return kb::set_error(KB_ERR_ARG, "S=%d: no float32 etan_kernel for %d positions per thread", a.S, CPT);
   auto k = kbo::etan_kernel<T, CPT>;
   if (int rc = set_lds(k, lds)) return rc;
   hipLaunchKernelGGL(k, dim3(a.G), dim3(kbo::NT), lds, st, t, a);

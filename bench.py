@@ -25,14 +25,19 @@ lower is better.
   by rows into one shard per worker process (the loss and gradients of a
   problem are sums over its family shards), scaled by rows to a full solve;
   beside it, config 1 (BASELINE's CPU case) solved in full the same way.
-* ``per_call``: the same solve through the per-call wrappers in the reference
-  glue's call sequence (``tests/dropin``): one launch per sweep and per wave
-  as the reference launches them (the pristine-structure proxy), the same with
-  each wave's sweep chain collapsed into one launch (``KBENCH_FUSE_SWEEPS``),
-  and the driver's own floor (every wrapper replaced by a no-op); and the
-  ratio of the first of these to ``value`` (the speedup against the
-  pristine-structure proxy on the same GPU; ``vs_baseline`` stays null, no
-  published number exists for this metric).
+* ``per_call``: the same solve through the builder's call-sequence drivers
+  (``kbench.percall``: the per-call wrappers in the reference glue's order,
+  wave buckets folded by native fixed-order row sums): one launch per sweep
+  and per wave as the reference launches them (the pristine-structure proxy),
+  the same with each wave's sweep chain collapsed into one launch
+  (``KBENCH_FUSE_SWEEPS``), and the driver alone (every wrapper a no-op), all
+  three over the forward and the per-wave reverse sweep, with the glue's E
+  adjoint timed apart; and the whole-solve ratio of the first to ``value``
+  (the speedup against the pristine-structure proxy on the same GPU;
+  ``vs_baseline`` stays null, no published number exists for this metric).
+* ``config5``: BASELINE config 5 on the same problem: the 50 exact
+  Hessian-vector products of one Newton-CG step (``kbench.newton.make_exact_hvp``),
+  timed as one block, with the roofline of its largest kernel.
 """
 
 from __future__ import annotations
@@ -49,6 +54,9 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "kernel-bench_amd"))
 
 HBM_PEAK_GBS = 8000.0
+# quarter-rate transcendentals (v_exp_f32 / v_log_f32 / v_rcp_f32): 16 lanes per CU per clock,
+# 256 CUs at 2.4 GHz
+TRANS_PEAK_PER_S = 256 * 16 * 2.4e9
 def _profile_file(kind: str, config: str):
     """The committed rocprofv3 summary (``traffic`` or ``sq_counters``) of one configuration."""
     return ROOT / "profiles" / f"{kind}_config{config}.json"
@@ -66,6 +74,7 @@ def parse():
     ap.add_argument("--cpu-families-per-worker", type=int, default=2)
     ap.add_argument("--no-per-call", action="store_true", help="skip the per-call (drop-in) timings")
     ap.add_argument("--no-dedup-off", action="store_true", help="skip the KB_DEDUP=0 timing")
+    ap.add_argument("--no-config5", action="store_true", help="skip the config-5 Hessian-vector product timing")
     ap.add_argument("--verbose", action="store_true")
     ap.add_argument("--hvp-layout", choices=("both", "levels"), default="both",
                     help="--workload hvp: time the size waves and the level waves, or the level waves only")
@@ -205,22 +214,37 @@ def _time_host(step, warmup: int, steps: int) -> float:
     return statistics.median(ts)
 
 
-def per_call_timings(static, theta, cw, steps: int = 3, static_levels=None) -> dict:
-    """ms per solve through the per-call wrappers in the reference glue's call sequence.
+def per_call_timings(static, theta, cw, steps: int = 5, static_levels=None) -> dict:
+    """ms per solve through the builder's per-call drivers (``kbench.percall``: the wrappers called in the
+    reference glue's call sequence, with the wave buckets folded by the library's fixed-order row sums).
 
-    With ``static_levels`` (the same problem regrouped by ``synth.level_waves``)
-    the three timings are repeated on one wave per dependency level.
+    Three timings of the same scope, the forward plus the backward's per-wave reverse sweep, so that
+    they compare: one launch per sweep (the pristine-structure proxy), each wave's sweep chain in one
+    launch (``KBENCH_FUSE_SWEEPS``), and the same driver with every wrapper replaced by a no-op (its
+    Python, torch glue and host syncs alone).  The glue's E adjoint and theta VJP, which follow the
+    reverse sweep and do not depend on the wave launches (a BiCGSTAB over E-step products whose
+    iteration count depends on the cotangents, so a no-op run would not repeat it), are timed apart;
+    the whole solve is the sum.  With ``static_levels`` (the same problem regrouped by
+    ``synth.level_waves``) the timings are repeated on one wave per dependency level.
     """
-    sys.path.insert(0, str(ROOT / "tests"))
-    from dropin.kernels import noop
-    from dropin.solve import SolvePlan
-    from kbench.core.kernels import wave_step
+    import torch
 
-    def solve(p):
+    from kbench.core.kernels import wave_step
+    from kbench.percall.kernels import noop
+    from kbench.percall.solve import SolvePlan, root_softmax2
+
+    def waves(p):
         def step():
-            loss, sv = p.forward(theta, cw)
-            p.backward(theta, cw, sv)
+            _, sv = p.forward(theta, cw)
+            with torch.no_grad():
+                p.reverse_sweep(sv, -root_softmax2(sv["pi_wave"].index_select(0, p.roots)), use_col=False)
         return step
+
+    def e_side(p):
+        _, sv = p.forward(theta, cw)
+        with torch.no_grad():
+            acc = p.reverse_sweep(sv, -root_softmax2(sv["pi_wave"].index_select(0, p.roots)), use_col=False)
+        return lambda: p.e_adjoint_and_vjp(theta, cw, sv, acc, use_col=False)
 
     def three(st):
         plan = SolvePlan(st)
@@ -228,53 +252,149 @@ def per_call_timings(static, theta, cw, steps: int = 3, static_levels=None) -> d
         old = wave_step.FUSE_SWEEPS
         try:
             wave_step.FUSE_SWEEPS = False
-            per_launch = _time_host(solve(plan), 1, steps)
+            per_launch = _time_host(waves(plan), 2, steps)
             wave_step.FUSE_SWEEPS = True
-            fused = _time_host(solve(plan), 1, steps)
+            fused = _time_host(waves(plan), 2, steps)
         finally:
             wave_step.FUSE_SWEEPS = old
-        floor = _time_host(solve(floor_plan), 1, steps)
-        return round(per_launch, 3), round(fused, 3), round(floor, 3)
+        floor = _time_host(waves(floor_plan), 2, steps)
+        e_ms = _time_host(e_side(plan), 2, steps)
+        return {"ms_one_launch_per_sweep": round(per_launch, 3), "ms_sweep_chains_fused": round(fused, 3),
+                "ms_glue_floor": round(floor, 3), "ms_e_adjoint_and_theta_vjp": round(e_ms, 3),
+                "ms_solve_one_launch_per_sweep": round(per_launch + e_ms, 3),
+                "ms_solve_sweep_chains_fused": round(fused + e_ms, 3)}
 
-    per_launch, fused, floor = three(static)
-    out = {
-        "ms_one_launch_per_sweep": per_launch,
-        "ms_sweep_chains_fused": fused,
-        "ms_glue_floor": floor,
-        "note": ("host wall time (median of %d) of a fwd+bwd solve through the per-call wrappers in the "
-                 "reference glue's call sequence: one launch per sweep and wave as the reference launches "
-                 "them (the pristine-structure proxy); the same with KBENCH_FUSE_SWEEPS=1 (each wave's sweep "
-                 "chain in one launch); the driver alone with no-op wrappers" % steps),
-    }
+    out = three(static)
+    out["note"] = (
+        "host wall time (median of %d) through the builder's call-sequence driver (kbench.percall: the "
+        "per-call wrappers in the reference glue's order, wave buckets folded by native fixed-order row sums, "
+        "where the frozen glue calls _scatter_accum per bucket): ms_one_launch_per_sweep / "
+        "ms_sweep_chains_fused / ms_glue_floor time the forward plus the per-wave reverse sweep with one "
+        "launch per sweep and wave (the pristine-structure proxy), with each wave's sweep chain in one launch "
+        "(KBENCH_FUSE_SWEEPS=1), and with every wrapper a no-op (same driver code and calls); the glue's "
+        "E adjoint and theta VJP (ms_e_adjoint_and_theta_vjp) are timed apart and added in ms_solve_*" % steps)
     if static_levels is not None:
-        lp, lf, lfl = three(static_levels)
-        out["level_waves"] = {
-            "n_waves": len(static_levels.wave_layout["wave_metas"]),
-            "ms_one_launch_per_sweep": lp, "ms_sweep_chains_fused": lf, "ms_glue_floor": lfl,
-            "note": ("the same three timings with the rows regrouped into one wave per dependency level "
-                     "(synth.level_waves: same rows, same per-row results, fewer waves, so fewer wrapper calls)"),
-        }
+        lv = three(static_levels)
+        lv["n_waves"] = len(static_levels.wave_layout["wave_metas"])
+        lv["note"] = ("the same timings with the rows regrouped into one wave per dependency level "
+                      "(synth.level_waves: same rows, same per-row results, fewer waves, so fewer wrapper calls)")
+        out["level_waves"] = lv
     return out
+
+
+def _unit_directions(theta, n: int, seed: int = 0):
+    """``n`` seeded Gaussian directions of theta's size, each normalised to unit length (config 5)."""
+    import numpy as np
+    import torch
+
+    g = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        u = g.normal(size=int(theta.numel()))
+        out.append(torch.as_tensor(u / np.linalg.norm(u), dtype=theta.dtype, device=theta.device))
+    return out
+
+
+def _tangent_sweep_launches(hvp, u):
+    """HIP-event time and algorithmic bytes of every tangent-sweep launch (``wave_tan_pre_kernel``, one per
+    level: the HVP's largest kernel) in one eager HVP of ``hvp`` -> (ms list, bytes list).
+
+    The wrapper is looked up by the drivers on every call, so it is replaced for this one HVP; events go
+    on torch's current stream, where the wrappers launch.  Bytes per launch: 4*S per row for Pi*, the
+    incoming dPi and the outgoing dPi and dPibar rows, plus the split term and its tangent on split rows
+    (the constant rows are one [1, S] row each, shared by the launch).
+    """
+    import inspect
+
+    import torch
+
+    from kbench.core.kernels import wave_tangent as WT
+
+    orig = WT.compute_wave_step_tangent_selfloop
+    sig = inspect.signature(orig)
+    rec = []
+
+    def timed(*a, **k):
+        b = sig.bind(*a, **k)
+        W, S = int(b.arguments["W"]), int(b.arguments["S"])
+        split = b.arguments.get("DTS_reduced") is not None
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        orig(*a, **k)
+        e1.record()
+        rec.append((e0, e1, 4.0 * S * W * (6 if split else 4)))
+
+    WT.compute_wave_step_tangent_selfloop = timed
+    try:
+        with torch.no_grad():
+            hvp._tangent_cotangents(u.reshape(hvp.theta.shape).to(hvp.theta.dtype))
+        torch.cuda.synchronize()
+    finally:
+        WT.compute_wave_step_tangent_selfloop = orig
+    return [a.elapsed_time(b) for a, b, _ in rec], [x for _, _, x in rec]
+
+
+def config5_timing(static_levels, theta, cw, warmup: int = 3, n_hvp: int = 50) -> dict:
+    """BASELINE config 5 on the config-3 problem: one Newton-CG step's 50 exact HVPs along seeded unit
+    Gaussian directions, timed as one block (host wall, synchronised at both ends), through
+    ``kbench.newton.make_exact_hvp`` (row classes, one HIP graph per point) on the level waves."""
+    import statistics as st
+
+    import torch
+
+    from kbench.newton.hvp import make_exact_hvp
+    from kbench.percall.solve import run_forward
+
+    us = _unit_directions(theta, n_hvp + warmup, seed=5)
+    _, sv = run_forward(static_levels, theta, cw)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    hvp = make_exact_hvp(static_levels, theta, cw, sv)
+    hvp(us[0])  # the first call captures the graph
+    torch.cuda.synchronize()
+    cache_ms = (time.perf_counter() - t0) * 1e3
+    for u in us[1:warmup]:
+        hvp(u)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for u in us[warmup:]:
+        hvp(u)
+    torch.cuda.synchronize()
+    block_ms = (time.perf_counter() - t0) * 1e3
+    dur, byt = _tangent_sweep_launches(hvp, us[0])
+    avg_ms, avg_b = st.mean(dur), st.mean(byt)
+    achieved = avg_b / (avg_ms * 1e-3) / 1e9
+    return {
+        "ms_per_hvp": round(block_ms / n_hvp, 4),
+        "ms_per_newton_cg_step_50_hvps": round(block_ms * 50.0 / n_hvp, 2),
+        "point_cache_ms": round(cache_ms, 2),
+        "roofline": {"bound": "hbm", "kernel": "wave_tan_pre_kernel", "achieved": round(achieved, 3),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 6),
+                     "launches": len(dur), "launch_unit": "one tangent-sweep launch per dependency level",
+                     "avg_launch_ms": round(avg_ms, 5), "algorithmic_bytes_per_launch": round(avg_b, 1),
+                     "kernel_ms_per_hvp": round(sum(dur), 4)},
+        "note": (f"{n_hvp} exact HVPs (seeded unit Gaussian directions) after {warmup} warm-up HVPs, timed as "
+                 "one block; make_exact_hvp on the level waves: tangent forward and reverse on one row per class "
+                 "of identical rows, replayed as one HIP graph; point_cache_ms = the point cache, the class "
+                 "schedule and the first (captured) HVP; the kernel roofline from HIP events around each "
+                 "tangent-sweep launch of one eager HVP"),
+    }
 
 
 def bench_hvp(args, static, theta, cw, summ, static_levels) -> None:
     """Exact Hessian-vector products (config 5) through the per-call wrappers, on the size waves and on
     one wave per dependency level (``synth.level_waves``; the same HVP, fewer wrapper calls)."""
-    import numpy as np
     import torch
 
-    sys.path.insert(0, str(ROOT / "tests"))
-    from dropin.hvp import HvpPlan
-    from dropin.solve import plan_of, run_forward
+    from kbench.newton.hvp import make_exact_hvp
+    from kbench.percall.solve import run_forward
 
-    g = np.random.default_rng(0)
-    us = [torch.as_tensor(g.normal(size=tuple(theta.shape)), dtype=theta.dtype, device=theta.device).reshape(-1)
-          for _ in range(4)]
+    us = _unit_directions(theta, 4)
 
     def timed(st, row_classes=False, graph=False):
         _, sv = run_forward(st, theta, cw)
         t0 = time.perf_counter()
-        hvp = HvpPlan(plan_of(st), theta, cw, sv, row_classes=row_classes, graph=graph)
+        hvp = make_exact_hvp(st, theta, cw, sv, row_classes=row_classes, graph=graph)
         torch.cuda.synchronize()
         cache_ms = (time.perf_counter() - t0) * 1e3
         k = [0]
@@ -390,7 +510,7 @@ def main():
     theta = cap["inputs"]["theta"].to(dev)
     cw = cap["inputs"]["col_weights"].to(dev)
     static_levels = None
-    if args.workload != "solve" or not args.no_per_call:
+    if args.workload != "solve" or not args.no_per_call or not args.no_config5:
         static_levels = make_static(problem_to_captured(synth.level_waves(problem)[0]), dev)
     if args.workload == "hvp":
         return bench_hvp(args, static, theta, cw, summ, static_levels)
@@ -426,6 +546,13 @@ def main():
     B = 4.0 * solver.S
     fwd_bytes = B * (2 * W + 4 * Nw)
     bwd_bytes = B * (3 * W + 8 * Nw)
+    # transcendental instructions per position: backward row 8 for the J^T coefficients (six exp2,
+    # two reciprocals) and 1 for p', per split 9 (five split shares, two Pibar factors, two p');
+    # forward (linear-space sweeps) 2 per row for the row's leaf / merge terms, 6 per split
+    # (five exp2 and the merge's log2)
+    fwd_trans = solver.S * (2.0 * W + 6.0 * Nw)
+    bwd_trans = solver.S * (9.0 * W + 9.0 * Nw)
+    trans = {"fwd_row_kernel": fwd_trans, "bwd_row_kernel": bwd_trans}
     kernels = {"fwd_row_kernel": (fw, fwd_bytes), "bwd_row_kernel": (bw, bwd_bytes)}
     dom = max(kernels, key=lambda k: kernels[k][0].sum())
     dur, byt = kernels[dom]
@@ -435,6 +562,19 @@ def main():
     avg_bytes = float(byt.mean())
     achieved = avg_bytes / (avg_ms * 1e-3) / 1e9
     counters = _counters(sym, args.config)
+    trans_rate = float(trans[dom].mean()) / (avg_ms * 1e-3)
+    valu = None
+    if counters:
+        nd = sum(float(c["dispatches"]) for c in counters.values())
+        valu = sum(float(c["valu_active_frac"]) * float(c["dispatches"]) for c in counters.values()) / nd
+    roofs = {"hbm": achieved / HBM_PEAK_GBS, "transcendental": trans_rate / TRANS_PEAK_PER_S}
+    if valu is not None:
+        roofs["valu_issue"] = valu
+    nearest = max(roofs, key=roofs.get)
+    limiter = (f"{nearest} ({roofs[nearest]:.2f} of its peak)" if roofs[nearest] >= 0.5 else
+               f"latency: no roof above half of its peak (HBM {roofs['hbm']:.2f}, transcendental "
+               f"{roofs['transcendental']:.2f}" + (f", VALU active {valu:.2f} of wave cycles" if valu is not None
+                                                   else "") + "); the time goes to barriers, LDS and memory latency")
     roofline = {
         "bound": "hbm",
         "kernel": sym,
@@ -448,9 +588,14 @@ def main():
         "avg_launch_ms": round(avg_ms, 5),
         "algorithmic_bytes_per_launch": round(avg_bytes, 1),
         "kernel_ms_per_solve": {k: round(float(v[0].sum()), 4) for k, v in kernels.items()},
-        "limiter": ("latency: HBM bytes are the roofline the kernel is priced against, but its time goes to "
-                    "barriers, LDS and VALU issue (counters: per-shape VALU-active and LDS-wait fractions of "
-                    "wave cycles)"),
+        "compute": {"transcendental_ops_per_launch": round(float(trans[dom].mean()), 1),
+                    "achieved_per_s": round(trans_rate, 1), "peak_per_s": TRANS_PEAK_PER_S,
+                    "frac": round(trans_rate / TRANS_PEAK_PER_S, 6),
+                    "valu_active_frac": None if valu is None else round(valu, 4),
+                    "note": ("no dense contraction, so no MFMA roof: the compute side is the quarter-rate "
+                             "transcendental unit (algorithmic count per position from the kernel's formulas) "
+                             "and VALU issue (SQ counters of the committed profile, dispatch-weighted)")},
+        "limiter": limiter,
         "counters": counters,
     }
     whole_bytes = float(fwd_bytes.sum() + bwd_bytes.sum())
@@ -475,7 +620,12 @@ def main():
     per_call = None if args.no_per_call else per_call_timings(static, theta, cw, static_levels=static_levels)
     if per_call is not None:
         # the whole-pass solve against the pristine-structure proxy on the same GPU
-        per_call["speedup_vs_pristine_structure_proxy"] = round(per_call["ms_one_launch_per_sweep"] / ms, 2)
+        per_call["speedup_vs_pristine_structure_proxy"] = round(per_call["ms_solve_one_launch_per_sweep"] / ms, 2)
+    config5 = None
+    if not args.no_config5 and not solver.statewise:
+        config5 = {"skipped": "config 5 asks for per-species theta"}
+    elif not args.no_config5:
+        config5 = config5_timing(static_levels, theta, cw)
 
     out = {
         "metric": "fwd+bwd ms per solve at S=1024,C=32k; achieved HBM GB/s vs roofline",
@@ -518,6 +668,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "per_call": per_call,
+        "config5": config5,
     }
     print(json.dumps(out))
 

@@ -272,24 +272,40 @@ def compare(got, ref, *, rtol, atol, noise_abs=0.0, noise_rel=0.0, margin=NOISE_
     return {"ok": ok, "max_abs": ma, "max_rel": mr, "reason": "" if ok else "tolerance"}
 
 
-def replay(rec, pool, *, device="cuda", fn=None, rtol=2e-3, atol=2e-3) -> list[dict]:
-    """Re-run one recorded call and compare every output with the recorded post-call state."""
+def replay(rec, pool, *, device="cuda", fn=None, rtol=2e-3, atol=2e-3, scale_atol=False,
+           dont_care=None) -> list[dict]:
+    """Re-run one recorded call and compare every output with the recorded post-call state.
+
+    ``fn`` replaces the recorded wrapper (another implementation with the same signature: the gate
+    then compares it with the recorded outputs).  ``scale_atol`` measures ``atol`` against each
+    output's largest finite magnitude (at least 1).  ``dont_care`` maps an output path to a boolean
+    mask of positions to leave out (the caller's don't-care regions, beside the unwritten ones that
+    ``measure_noise`` finds).
+    """
     got = _run(rec, pool, device, fn=fn)
     want = dict(named_tensors(rebuild(rec["post"], pool, "cpu")))
     out = []
     valid, noise = rec.get("valid", {}), rec.get("noise", {})
+    dont_care = dont_care or {}
     for path, t in got:
         if path not in want or not torch.is_tensor(want[path]):
             continue
         g, r = t.detach().cpu(), want[path]
-        if path in valid:
-            m = valid[path]
+        m = valid.get(path)
+        if path in dont_care:
+            keep = ~dont_care[path].to(torch.bool).cpu()
+            m = keep if m is None else (m & keep)
+        if m is not None:
             g, r = g[m], r[m]
         if not g.is_floating_point():
             v = {"ok": bool(torch.equal(g, r)), "max_abs": 0.0, "max_rel": 0.0, "reason": "exact"}
         else:
             na, nr = noise.get(path, (0.0, 0.0))
-            v = compare(g, r, rtol=rtol, atol=atol, noise_abs=na, noise_rel=nr)
+            a_eff = atol
+            if scale_atol:
+                fin = r.double()[torch.isfinite(r.double())]
+                a_eff = atol * max(1.0, float(fin.abs().max()) if fin.numel() else 1.0)
+            v = compare(g, r, rtol=rtol, atol=a_eff, noise_abs=na, noise_rel=nr)
         v["path"] = path
         out.append(v)
     return out

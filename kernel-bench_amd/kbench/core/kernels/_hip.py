@@ -6,7 +6,12 @@
   and cached with a strong reference to those tensors, so a cached handle can
   never be matched by a different tensor reusing the same memory;
 * fixed-order row accumulation (``kb_rows_scatter_add``, ``kb_rows_sum_into``),
-  which replaces the reference's atomic adds.
+  which replaces the reference's atomic adds;
+* version counters: a kernel that writes a caller's tensor through a raw
+  pointer is invisible to torch, so every wrapper bumps the version of each
+  tensor it writes in place (``wrote``), as torch's own in-place ops do.  A
+  cache keyed on a tensor's version (the whole-pass driver's reuse of a
+  forward's split terms, ``static_cached``) then sees the change.
 
 There is no CPU path: every launcher raises if the HIP library is missing.
 """
@@ -28,7 +33,7 @@ __all__ = [
     "KbPibarVjpIO", "KbWaveBwdIO", "KbWaveStepIO", "KbETanIO", "KbDtsTanIO", "KbWaveTanIO", "KbEStepSoIO",
     "KbWaveSoIO", "KbDtsSoIO",
     "lib", "check", "ptr", "stream", "dtype_code", "defer", "flush", "require_device", "f", "i64", "tree_from_parent",
-    "tree_from_levels", "scatter_add_rows", "sum_rows_into", "rows_sum_accum", "static_cached",
+    "tree_from_levels", "scatter_add_rows", "sum_rows_into", "rows_sum_accum", "static_cached", "wrote",
 ]
 
 check = N.check
@@ -90,6 +95,16 @@ def f(t, dtype, device):
     elif t.dtype is dtype and t.device == device and t.is_contiguous():
         return t
     return t.to(device=device, dtype=dtype).contiguous()
+
+
+def wrote(*ts) -> None:
+    """Bump the version counter of every tensor a kernel has written in place (None skipped).
+
+    Inference-mode tensors carry no version counter and are skipped.
+    """
+    for t in ts:
+        if t is not None and not t.is_inference():
+            torch.autograd.graph.increment_version(t)
 
 
 def i64(t, device):
@@ -226,6 +241,7 @@ def scatter_add_rows(dst: torch.Tensor, src: torch.Tensor, keys, *, row_stride=N
     stride = int(dst.shape[-1]) if row_stride is None else int(row_stride)
     check(lib().kb_rows_scatter_add(dtype_code(src.dtype), S, n, ptr(src), ptr(order32), ptr(keys_sorted),
                                     ptr(dst), stride, stream(src.device)))
+    wrote(dst)
 
 
 def rows_sum_multi(blocks) -> torch.Tensor:
@@ -240,6 +256,11 @@ def rows_sum_multi(blocks) -> torch.Tensor:
     first = pairs[0][0]
     n, S = int(first.shape[0]), int(first.shape[1])
     m = len(pairs)
+    if not 1 <= m <= 8:
+        raise ValueError(f"rows_sum_multi takes 1..8 blocks, got {m}")
+    for x, y in pairs:
+        for t in (x,) if y is None else (x, y):
+            _check_rows(t, n, S, first, "rows_sum_multi")
     out = torch.empty((m, S), device=first.device, dtype=first.dtype)
     chunks = (n + 63) // 64
     work = torch.empty((m * chunks * S if chunks > 1 else 1,), device=first.device, dtype=torch.float64)
@@ -262,9 +283,20 @@ def rows_sum_accum(blocks) -> None:
     m = len(blocks)
     if m == 0:
         return
+    if m > 8:
+        raise ValueError(f"rows_sum_accum takes at most 8 blocks, got {m}")
     first = blocks[0][1][0]
     S = int(first.shape[1])
     n = [int(a[0].shape[0]) for _, a in blocks]
+    for (d, a), nb in zip(blocks, n):
+        if not 1 <= len(a) <= 4:
+            raise ValueError(f"rows_sum_accum takes 1..4 addends per block, got {len(a)}")
+        for t in a:
+            _check_rows(t, nb, S, first, "rows_sum_accum")
+        if (not torch.is_tensor(d) or d.dtype != first.dtype or d.device != first.device or not d.is_contiguous()
+                or d.numel() != S):
+            raise ValueError("rows_sum_accum: every accumulator must be a contiguous tensor of S elements with the "
+                             "addends' dtype and device")
     chunks = max((x + 63) // 64 for x in n)
     work = torch.empty((m * chunks * S if chunks > 1 else 1,), device=first.device, dtype=torch.float64)
     addends = []
@@ -274,6 +306,16 @@ def rows_sum_accum(blocks) -> None:
         dtype_code(first.dtype), S, m, (ct.c_int64 * m)(*n), (ct.c_int32 * m)(*[len(a) for _, a in blocks]),
         (ct.c_void_p * (4 * m))(*addends), (ct.c_void_p * m)(*[ptr(d) for d, _ in blocks]), ptr(work),
         stream(first.device)))
+    wrote(*[d for d, _ in blocks])
+
+
+def _check_rows(t, n, S, first, what):
+    """``t`` is a contiguous [n, S] tensor with ``first``'s dtype and device (the C entry points take raw
+    pointers and cannot check what they read)."""
+    if (not torch.is_tensor(t) or t.ndim != 2 or int(t.shape[0]) != n or int(t.shape[1]) != S
+            or t.dtype != first.dtype or t.device != first.device or not t.is_contiguous()):
+        raise ValueError(f"{what}: every addend must be a contiguous [{n}, {S}] tensor of dtype {first.dtype} "
+                         f"on {first.device}")
 
 
 def sum_rows_into(dst: torch.Tensor, src: torch.Tensor) -> None:
@@ -284,3 +326,4 @@ def sum_rows_into(dst: torch.Tensor, src: torch.Tensor) -> None:
     S = int(src.shape[1])
     work = torch.empty(((n + 63) // 64) * S, device=src.device, dtype=torch.float64)
     check(lib().kb_rows_sum_into(dtype_code(src.dtype), S, n, ptr(src), ptr(dst), ptr(work), stream(src.device)))
+    wrote(dst)

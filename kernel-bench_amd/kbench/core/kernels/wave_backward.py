@@ -579,6 +579,7 @@ def uniform_cross_pibar_vjp_tree_from_ud_fused(Pi_star, col_log_probs, pibar_ud,
         contrib=H.ptr(contrib),
     )
     H.check(H.lib().kb_pibar_vjp(tree.handle, io, H.stream(dev)))
+    H.wrote(pibar_ud)
     H.scatter_add_rows(accumulated_rhs, contrib, lambda: torch.cat((sl64, sr64)), static=(sl64, sr64))
     if grad_col_log_probs is not None:
         H.sum_rows_into(grad_col_log_probs, contrib)

@@ -79,6 +79,7 @@ def compute_leaf_initial_wave_step(Pi_out, ws, W, S, max_coupling_mat, DL_const,
         leaf_logp=H.ptr(keep["lp"]),
     )
     H.check(H.lib().kb_leaf_init(io, H.stream(dev)))
+    H.wrote(Pi_out)
 
 
 def compute_wave_step(Pi_in, Pi_out, Pibar, ws, W, S, max_coupling_mat, DL_const, Ebar, E, SL1_const, SL2_const,
@@ -203,3 +204,4 @@ def _launch_sweeps(Pi_in, pi_ws, n_sweeps, Pi_out, Pibar, pibar_row_max, pi_resi
         col_log_probs=H.ptr(col), item_idx=H.ptr(item), leaf_state=H.ptr(leaf), leaf_logp=H.ptr(lp),
     )
     H.check(H.N.lib().kb_wave_step(tree.handle, io, H.stream(dev)))
+    H.wrote(Pi_out, Pibar if store_final else None, pibar_row_max if store_final else None, pi_residual_out)

@@ -78,6 +78,7 @@ def _launch(Pi_in, dPi_in, dPi_out, ws, W, S, n_iters, pi_ws, consts, col_log_pr
         item_idx=H.ptr(item), leaf_state=H.ptr(leaf), leaf_logp=H.ptr(lp), dleaf_logp=H.ptr(dlp),
     )
     H.check(H.lib().kb_wave_step_tangent(tree.handle, io, H.stream(dev)))
+    H.wrote(dPi_out, dPibar_out)
 
 
 def compute_wave_step_tangent_selfloop(Pi_in, dPi_io, ws, W, S, n_iters, max_coupling_mat, dMC, DL, dDL, Ebar, dEbar,

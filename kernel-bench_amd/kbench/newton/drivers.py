@@ -9,10 +9,12 @@ loss, or the trust-region ratio test).
 
 The loss and gradient come from an ``Objective``: by default the native
 whole-pass driver (``kbench.runtime``, a few ms per evaluation at config 3).
-Curvature is a named provider of the objective: ``"fd_hessian"`` (central
-differences of two native gradients along the unit direction) is built in;
-the Gauss-Newton (``"ggn"``) and exact (``"exact"``) Hessian-vector products of
-the per-call wrapper path are registered by the caller (``curvatures=``).
+Curvature is a named provider of the objective, built at the current point:
+``"ggn"`` (the Gauss-Newton product, the default of ``newton_cg`` as in the
+reference), ``"exact"`` (the exact Hessian-vector product) -- both from
+``kbench.newton.hvp`` over the per-call wrappers -- and ``"fd_hessian"``
+(central differences of two native gradients along the unit direction).  A
+caller may add or replace providers (``curvatures=``).
 Newton vectors are float64; theta is evaluated in float32.  The forward is not
 warm-started from the previous E (the native E fixed point starts at e_init).
 """
@@ -30,7 +32,9 @@ class Objective:
     """The summed loss of one static problem as a function of flat theta vectors.
 
     ``curvatures`` maps a name to ``factory(objective, x) -> hvp`` (``hvp(v)`` of
-    flat float64 vectors); ``"fd_hessian"`` is always available.  Its step
+    flat float64 vectors); ``"ggn"``, ``"exact"`` and ``"fd_hessian"`` are always
+    available.  The first two evaluate the forward at x and build the product there
+    (``make_ggn_hvp`` / ``make_exact_hvp``; uniform column weights).  The step
     ``fd_eps`` trades the float32 gradient's rounding (large for small steps)
     against the O(step^2) truncation: at config 1 a step of 1e-2 agrees with
     the exact HVP to 2e-3 (1e-3 only to 4e-2).
@@ -47,7 +51,7 @@ class Objective:
         self.fd_eps = float(fd_eps)
         self.evals = 0   # loss + gradient evaluations
         self.values = 0  # loss-only evaluations
-        self.curvatures = {"fd_hessian": _fd_hessian, **(curvatures or {})}
+        self.curvatures = {"ggn": _ggn, "exact": _exact, "fd_hessian": _fd_hessian, **(curvatures or {})}
 
     def theta(self, x):
         return x.to(torch.float32).reshape(self.shape).contiguous()
@@ -70,6 +74,31 @@ class Objective:
         if kind not in self.curvatures:
             raise ValueError(f"unknown curvature {kind!r}; available: {sorted(self.curvatures)}")
         return self.curvatures[kind](self, x)
+
+
+def _at_point(obj: Objective, x):
+    """(theta, forward intermediates) at x, from the whole-pass forward."""
+    th = obj.theta(x)
+    with torch.no_grad():
+        _, saved = obj.solver.run_forward(th, obj.col_weights)
+    saved.pop("_use_col_weights", None)
+    return th, saved
+
+
+def _ggn(obj: Objective, x):
+    """The Gauss-Newton product at x (reference newton_cg.py:351-352 -> ggn.py:280)."""
+    from .hvp import make_ggn_hvp
+
+    th, saved = _at_point(obj, x)
+    return make_ggn_hvp(obj.static, th, obj.col_weights, saved)
+
+
+def _exact(obj: Objective, x):
+    """The exact Hessian-vector product at x (reference hvp_exact.py:66)."""
+    from .hvp import make_exact_hvp
+
+    th, saved = _at_point(obj, x)
+    return make_exact_hvp(obj.static, th, obj.col_weights, saved)
 
 
 def _fd_hessian(obj: Objective, x):

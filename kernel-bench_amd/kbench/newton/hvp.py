@@ -64,8 +64,8 @@ from kbench.core.parameters.extract_parameters import (as_item_param, as_item_st
 from kbench import synth
 from kbench.core.kernels import _hip as H
 
-from .krylov import bicgstab
-from .solve import LN2, SolvePlan, root_softmax2
+from kbench.percall.krylov import bicgstab
+from kbench.percall.solve import LN2, SolvePlan, root_softmax2
 
 
 def _fold(acc, x, G, S):
@@ -593,12 +593,14 @@ class HvpPlan:
                                pL=lin[2] + so_p[3], mt=dacc.mt + lin[3] + so_p[4], col=dacc.col + lin[4] + so_p[5])
 
 
-def ggn_hvp(plan: SolvePlan, theta, col_weights, saved, *, tol=None, max_sweeps=200):
+def ggn_hvp(plan: SolvePlan, theta, col_weights, saved, *, tol=None, max_sweeps=200, neumann_terms=None,
+            use_pruning=None, bicgstab_tol=None):
     """v -> J^T B J v, the Gauss-Newton product with B_f = ln2 (diag q_f - q_f q_f^T) per family.
 
     J = d(root rows)/d(theta) by ``TangentForward`` (sweeping each wave to convergence);
     J^T by the backward's reverse sweep from a root-row cotangent, without the loss's
-    normaliser term.
+    normaliser term.  ``neumann_terms`` / ``use_pruning`` / ``bicgstab_tol`` override
+    the solver options of that reverse sweep and its E adjoint.
     """
     tan = TangentForward(plan, saved)
     q = root_softmax2(saved["pi_wave"].index_select(0, plan.roots))
@@ -608,11 +610,72 @@ def ggn_hvp(plan: SolvePlan, theta, col_weights, saved, *, tol=None, max_sweeps=
         with torch.no_grad():
             t, _ = tan.run(theta, v, tol=tol, max_sweeps=max_sweeps)
             cot = LN2 * q * (t - (q * t).sum(dim=-1, keepdim=True))
-            acc = plan.reverse_sweep(saved, cot, use_col=False)
-        g, _ = plan.e_adjoint_and_vjp(theta, col_weights, saved, acc, use_col=False, with_norm=False)
+            acc = plan.reverse_sweep(saved, cot, use_col=False, neumann_terms=neumann_terms, use_pruning=use_pruning)
+        g, _ = plan.e_adjoint_and_vjp(theta, col_weights, saved, acc, use_col=False, with_norm=False,
+                                      bicgstab_tol=bicgstab_tol)
         return g.reshape(-1)
 
     return hvp
 
 
-__all__ = ["TangentForward", "HvpPlan", "ggn_hvp"]
+# ---------------------------------------------------------------------------- entry points
+def _require_uniform_columns(col_weights):
+    from kbench.percall.solve import uniform_columns
+
+    if not uniform_columns(col_weights):
+        raise ValueError("the Hessian-vector products take uniform column weights (use_col_weights=False), "
+                         "as the reference's newton path does")
+
+
+def make_exact_hvp(static, theta, col_weights, sv, *, cache=None, tangent_self_iters=None, row_classes=True,
+                   graph=None):
+    """``hvp(u_flat) -> H u``: the exact Hessian of the summed loss at theta, analytically
+    (reference newton/hvp_exact.py:66-383, same arguments).
+
+    ``sv`` holds the forward intermediates at theta (``kbench.runtime.run_forward`` or the
+    per-call ``kbench.percall.run_forward``; the same names on both).  ``cache`` is an
+    earlier return value of this function at the same point, whose point cache (one
+    backward keeping every adjoint, the E adjoint, the class schedule) is reused.
+    ``tangent_self_iters``, the tangent forward's sweeps per wave, resolves as in the
+    reference: this argument, then ``NEWTON_TANGENT_SELF_ITERS``, then
+    ``solver_options.pi_iters``.  ``row_classes`` runs the tangent pass on one row per
+    class of identical rows (same result up to the order of sums); ``graph`` replays that
+    pass as one HIP graph (default: with the Neumann self-loop solver, which reads
+    nothing back on the host).
+    """
+    import os
+
+    if cache is not None:
+        if not isinstance(cache, HvpPlan):
+            raise TypeError("cache must be a value returned by make_exact_hvp")
+        return cache
+    _require_uniform_columns(col_weights)
+    from kbench.percall.solve import plan_of
+
+    plan = plan_of(static)
+    if tangent_self_iters is None:
+        env = os.environ.get("NEWTON_TANGENT_SELF_ITERS")
+        tangent_self_iters = int(env) if env else int(plan.so.pi_iters)
+    if graph is None:
+        graph = plan.so.self_loop_solver == "neumann" and theta.device.type == "cuda"
+    return HvpPlan(plan, theta, col_weights, sv, tangent_sweeps=int(tangent_self_iters), row_classes=bool(row_classes),
+                   graph=bool(graph))
+
+
+def make_ggn_hvp(static, theta, col_weights, sv, *, self_tol=None, self_max_iter=200, vjp_neumann_terms=None,
+                 vjp_use_pruning=None, vjp_bicgstab_tol=None):
+    """``hvp(v_flat) -> M v``: the Gauss-Newton (Fisher) product at theta, positive semi-definite
+    (reference newton/ggn.py:280-303, same arguments).
+
+    The tangent forward sweeps each wave until max|change| <= ``self_tol`` * max(1, max|dPi|)
+    (default 1e-6 for float32 rows, 1e-12 for float64), at most ``self_max_iter`` sweeps; the ``vjp_*``
+    arguments override the solver options of the reverse sweep and its E adjoint.
+    """
+    _require_uniform_columns(col_weights)
+    from kbench.percall.solve import plan_of
+
+    return ggn_hvp(plan_of(static), theta, col_weights, sv, tol=self_tol, max_sweeps=int(self_max_iter),
+                   neumann_terms=vjp_neumann_terms, use_pruning=vjp_use_pruning, bicgstab_tol=vjp_bicgstab_tol)
+
+
+__all__ = ["TangentForward", "HvpPlan", "ggn_hvp", "make_exact_hvp", "make_ggn_hvp"]

@@ -14,6 +14,15 @@ device-resident layout tables per ``static`` (created on first use and kept
 with it), then a few kernels per dependency level.  The reference's own Python
 glue is not part of this package; its per-call wrappers (``kbench.core.kernels``)
 are, for callers that drive them one call at a time.
+
+Two backward options change what is computed per wave, and the whole-pass
+driver does not implement them: ``self_loop_solver="gmres"`` (its Krylov space
+spans a wave, so the result depends on the wave grouping, which the driver
+replaces by dependency levels) and ``pibar_side_threshold > 0`` (split sides
+whose staged Pibar adjoint has a small abs-sum are dropped).  With either set,
+``run_backward`` runs the per-call drivers of ``kbench.percall`` instead, which
+call the same HIP wrappers wave by wave in the reference glue's order (the
+forward intermediates have the same names and meaning on both paths).
 """
 
 from __future__ import annotations
@@ -26,7 +35,7 @@ from kbench.api.solver_options import SolverOptions
 from kbench.fused import FORWARD_SAVED_NAMES, FusedSolver
 
 __all__ = ["FORWARD_SAVED_NAMES", "make_static", "run_forward", "run_backward", "fused_solver",
-           "run_forward_fused", "run_backward_fused"]
+           "needs_per_call_backward", "run_forward_fused", "run_backward_fused"]
 
 
 def _on_device(x, device):
@@ -69,12 +78,29 @@ def run_forward(static, theta: torch.Tensor, col_weights: torch.Tensor):
     return loss, saved
 
 
+def needs_per_call_backward(static) -> bool:
+    """True when the solver options ask for a backward the whole-pass driver does not implement."""
+    so = static.solver_options
+    return (str(so.self_loop_solver).strip().lower() != "neumann"
+            or float(so.pibar_side_threshold) > 0.0)
+
+
 def run_backward(static, theta: torch.Tensor, col_weights: torch.Tensor, saved: dict):
     """(saved forward intermediates) -> (grad_theta, grad_col); a failed E-adjoint solve raises RuntimeError."""
+    if needs_per_call_backward(static):
+        from kbench import percall
+
+        return percall.run_backward(static, theta, col_weights, saved)
     with torch.no_grad():
         return fused_solver(static).run_backward(theta, col_weights, saved)
 
 
-# names kept for callers that ask for the whole-pass driver explicitly
+def run_backward_fused(static, theta: torch.Tensor, col_weights: torch.Tensor, saved: dict):
+    """``run_backward`` on the whole-pass driver only: options it does not implement raise
+    ``NotImplementedError`` instead of selecting the per-call path."""
+    with torch.no_grad():
+        return fused_solver(static).run_backward(theta, col_weights, saved)
+
+
+# the forward always runs on the whole-pass driver
 run_forward_fused = run_forward
-run_backward_fused = run_backward

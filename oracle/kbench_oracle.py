@@ -721,12 +721,19 @@ def wave_backward_uniform(Pi_s, Pibar_s, row_max, rhs, items, consts, tree, neum
 
 
 def dts_cross_backward(Pi_s, Pibar_s, row_max, v, ws, meta, pD_param, pS_param, mt_item, item_idx, tree,
-                       active, col, use_col_weights):
+                       active, col, use_col_weights, side_thr=0.0):
     """``dts_cross_backward_accum_fused`` + ``uniform_cross_pibar_vjp_tree_from_ud_fused``.
 
     Pristine wave_backward.py:1529-1945 (cross accumulation, merged S term) and
     2229-2327 (Pibar VJP through the subtree sums).  Returns per-split-side
     contributions to the children's adjoint rows and parameter gradients.
+
+    ``side_thr`` is the glue's ``pibar_side_threshold`` (_implicit_grad.py:300-353):
+    above 0 a split side takes part in the Pibar VJP only when the abs-sum of its
+    staged u_d over the states exceeds it (pristine wave_backward.py:1777-1779,
+    1877-1884; the tree kernel returns early for an inactive side, 2263-2266).
+    At 0 the sides whose u_d is all zero are skipped, which changes nothing: their
+    A and subtree sums are 0.
     """
     S = tree.S
     sl = np.asarray(meta["sl"])
@@ -768,7 +775,9 @@ def dts_cross_backward(Pi_s, Pibar_s, row_max, v, ws, meta, pD_param, pS_param, 
         sub = tree.subtree_sum(ud)
         wPi = Pi_s[child] + col if use_col_weights else Pi_s[child]
         pp = np.exp2(wPi - _safe(row_max[child])[:, None])
-        contrib = np.where(act[:, None], pp * (A - sub), 0.0)
+        on = act if side_thr <= 0.0 else act & (np.abs(ud).sum(axis=1) > side_thr)
+        sums["side_on_" + side] = on
+        contrib = np.where(on[:, None], pp * (A - sub), 0.0)
         acc += contrib
         col_grad += contrib.sum(axis=0)
         sums["A_" + side], sums["sub_" + side], sums["tree_" + side] = A[:, 0], sub, contrib
@@ -878,9 +887,11 @@ def backward(prob: Problem, theta, col_weights, saved, *, collect=False, cache=N
     if G != 1:
         raise NotImplementedError("oracle backward covers item_rows == 1 (itemwise=False)")
     masks = []
+    side_bounds = []  # per split wave: abs-sums of the staged u_d, left sides then right sides
     thr = float(so["adjoint_pruning_threshold"])
     prune = bool(so["use_adjoint_pruning"])
     N_terms = int(so["neumann_terms"])
+    side_thr = float(so.get("pibar_side_threshold", 0.0))
     solver = str(so["self_loop_solver"]).strip().lower()
     if solver not in ("neumann", "gmres"):
         raise ValueError(f"unsupported self-loop solver {solver!r}")
@@ -911,7 +922,8 @@ def backward(prob: Problem, theta, col_weights, saved, *, collect=False, cache=N
         scatter(g_mt, aw2)
         if has_splits:
             out = dts_cross_backward(Pi_s, Pibar_s, row_max, v, ws, meta, pD_param, pS_param, mt_i,
-                                     prob.item_idx, tree, act, col, use_col)
+                                     prob.item_idx, tree, act, col, use_col, side_thr=side_thr)
+            side_bounds.append(np.concatenate([np.abs(out["ud_l"]).sum(axis=1), np.abs(out["ud_r"]).sum(axis=1)]))
             np.add.at(acc_rhs, np.asarray(meta["sl"]), out["rhs_l"])
             np.add.at(acc_rhs, np.asarray(meta["sr"]), out["rhs_r"])
             scatter(g_pD, out["g_pD"])
@@ -925,8 +937,9 @@ def backward(prob: Problem, theta, col_weights, saved, *, collect=False, cache=N
                           "g_pS": g_pS, "g_mt": g_mt, "g_col": g_col}
         cache["wE"] = grads[2]["wE"]
     if collect:
-        grads = grads + ({"masks": masks, "acc": {"g_E": g_E, "g_Ebar": g_Ebar, "g_Es1": g_Es1, "g_Es2": g_Es2,
-                                                  "g_pD": g_pD, "g_pS": g_pS, "g_mt": g_mt, "g_col": g_col}},)
+        acc = {"g_E": g_E, "g_Ebar": g_Ebar, "g_Es1": g_Es1, "g_Es2": g_Es2, "g_pD": g_pD, "g_pS": g_pS,
+               "g_mt": g_mt, "g_col": g_col}
+        grads = grads + ({"masks": masks, "side_bounds": side_bounds, "acc": acc},)
     return grads
 
 

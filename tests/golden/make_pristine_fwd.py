@@ -13,9 +13,15 @@ neither and only reads the fixtures.
 Fixtures (tests/golden/pristine_fwd_<case>.npz): the problem's layout digest
 and theta, pi_iters, and the reference's loss, E, E_s1, E_s2, Ebar, pi_wave,
 pibar_wave and pibar_row_max.  Cases: config 1 with global theta at
-pi_iters 16 and 4, config 1 with per-species theta at 16.
+pi_iters 16 and 4, config 1 with per-species theta at 16; config 2 (S = 511,
+multi-split rows, e_tol 1e-6) at pi_iters 16, whose fixture keeps every row
+maximum, the root rows of pi_wave and a seeded sample of 192 other rows of
+pi_wave and pibar_wave (``rows``), to stay small.
 
-    python tests/golden/make_pristine_fwd.py
+    python tests/golden/make_pristine_fwd.py [case ...]
+
+Python's bytecode cache is off, so the run writes nothing into the reference
+tree.
 """
 
 from __future__ import annotations
@@ -24,6 +30,8 @@ import importlib.util
 import os
 import sys
 from pathlib import Path
+
+sys.dont_write_bytecode = True  # nothing written under /root/reference
 
 HERE = Path(__file__).resolve().parent
 REPO = HERE.parents[1]
@@ -80,9 +88,12 @@ def main():
         _load(f"kbench.core.kernels.{mod}", pristine / f"{mod}.py")
     from kbench.runtime import make_static, run_forward
 
-    cases = [("config1", None, 16), ("config1_pi4", None, 4), ("config1_statewise", True, 16)]
-    for name, statewise, pi_iters in cases:
-        cfg = synth.config("1")
+    cases = {"config1": ("1", None, 16), "config1_pi4": ("1", None, 4), "config1_statewise": ("1", True, 16),
+             "config2": ("2", None, 16)}
+    chosen = sys.argv[1:] or list(cases)
+    for name in chosen:
+        cfg_name, statewise, pi_iters = cases[name]
+        cfg = synth.config(cfg_name)
         if statewise is not None:
             cfg = dataclasses.replace(cfg, statewise=statewise)
         problem = synth.build_problem(cfg)
@@ -91,10 +102,18 @@ def main():
         loss, saved = run_forward(static, cap["inputs"]["theta"], cap["inputs"]["col_weights"])
         out = {k: saved[k].detach().cpu().numpy() for k in ("E", "E_s1", "E_s2", "Ebar", "pi_wave", "pibar_wave",
                                                             "pibar_row_max")}
+        if cfg_name != "1":
+            C = int(out["pi_wave"].shape[0])
+            roots = np.asarray(problem["static"]["wave_layout"]["root_row_ids"], dtype=np.int64)
+            rest = np.setdiff1d(np.arange(C), roots)
+            rows = np.sort(np.concatenate([roots, np.random.default_rng(2).choice(rest, 192, replace=False)]))
+            out["rows"] = rows
+            out["pi_wave"] = out["pi_wave"][rows]
+            out["pibar_wave"] = out["pibar_wave"][rows]
         np.savez_compressed(HERE / f"pristine_fwd_{name}.npz", digest=np.array(synth.layout_digest(problem)),
                             theta=np.asarray(cap["inputs"]["theta"].numpy()), pi_iters=np.array(pi_iters),
                             loss=np.array(float(loss)), **out)
-        print(f"{name}: pi_iters={pi_iters} loss={float(loss):.7f}")
+        print(f"{name}: pi_iters={pi_iters} loss={float(loss):.7f}", flush=True)
 
 
 if __name__ == "__main__":

@@ -65,7 +65,7 @@ def _fused_solve(solver, theta, cw):
 # ---------------------------------------------------------------------- config 3
 def test_config3_fused_solve_matches_wrappers():
     """Config 3 (the bench workload): whole-pass forward + backward vs the per-call path."""
-    import dropin
+    from kbench import percall as dropin
     from kbench.runtime import fused_solver
 
     print("[fullsize] config=3 fused vs per-call wrappers (fwd + bwd)", flush=True)
@@ -144,7 +144,7 @@ def test_config4_fused_reproducible_and_row_classes_exact(config4):
 
 def test_config4_fused_solve_matches_wrappers(config4):
     """Config 4: whole-pass forward + backward vs the per-call path."""
-    import dropin
+    from kbench import percall as dropin
     from kbench.fused import FusedSolver
 
     static, theta, cw = config4
@@ -172,7 +172,7 @@ def test_config4_fused_solve_matches_wrappers(config4):
 @pytest.mark.parametrize("path", ["fused", "per-call"])
 def test_failed_e_adjoint_solve_raises(path):
     """One BiCGSTAB step at an unreachable tolerance: the backward raises RuntimeError (_implicit_grad.py:94)."""
-    import dropin
+    from kbench import percall as dropin
     from kbench.runtime import run_backward, run_forward
 
     static, theta, cw = _static("1", True, bicgstab_max_iter=1, bicgstab_tol=1e-30)
@@ -184,12 +184,14 @@ def test_failed_e_adjoint_solve_raises(path):
 
 
 def test_fused_backward_refuses_a_pibar_side_threshold():
-    from kbench.runtime import run_backward, run_forward
+    """The whole-pass backward alone refuses the option (``kbench.runtime.run_backward`` then takes the
+    per-call path: tests/test_runtime_options_gpu.py)."""
+    from kbench.runtime import run_backward_fused, run_forward
 
     static, theta, cw = _static("1", True, pibar_side_threshold=1e-3)
     _, saved = run_forward(static, theta, cw)
     with pytest.raises(NotImplementedError):
-        run_backward(static, theta, cw, saved)
+        run_backward_fused(static, theta, cw, saved)
 
 
 def test_fused_backward_never_reuses_a_freed_forward():
@@ -200,7 +202,7 @@ def test_fused_backward_never_reuses_a_freed_forward():
     the fused backward of that second point must equal the one after a fresh
     fused forward at the second theta.
     """
-    import dropin
+    from kbench import percall as dropin
     from kbench.runtime import fused_solver
 
     static, theta, cw = _static("1", True)
@@ -222,7 +224,7 @@ def test_fused_backward_never_reuses_a_freed_forward():
 
 def test_fused_column_weight_check_follows_each_tensor():
     """float64 column weights (converted by the driver) are classified afresh for every new tensor."""
-    import dropin
+    from kbench import percall as dropin
     from kbench.runtime import fused_solver
 
     static, theta, cw = _static("1", True)

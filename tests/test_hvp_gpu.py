@@ -1,11 +1,12 @@
 """GPU parity of the second-order wrappers (kbench.core.kernels.{e_step,wave,dts}_so) and of the
-exact / Gauss-Newton HVP call sequences (tests/dropin/hvp.py) against the float64 CPU oracle.
+exact / Gauss-Newton HVP call sequences (kbench/newton/hvp.py) against the float64 CPU oracle.
 
 Kernel tests feed the oracle's primal point and random tangents / cotangents
 to the HIP wrappers in float64 (tight tolerance) and float32 (rel 1e-4).  The
 exact HVP runs the glue on the GPU's own fp32 forward and is compared with
-the oracle's HVP at the oracle's forward; at config 3 (the S = 2047 per-species
-setup of the Newton-CG benchmark) by symmetry, linearity and determinism.
+the oracle's HVP at the oracle's forward.  The config-3 checks (the S = 2047
+per-species setup of the Newton-CG benchmark, where the oracle is out of
+reach) are in test_hvp_config3_gpu.py.
 """
 
 import numpy as np
@@ -216,8 +217,8 @@ def test_dts_backward_so_matches_oracle(dt, statewise):
                                                          ("1", True, False), ("tiny", None, True),
                                                          ("1", True, True), ("1", None, True)])
 def test_exact_hvp_matches_oracle(name, statewise, row_classes):
-    from dropin.hvp import HvpPlan
-    from dropin.solve import plan_of, run_forward
+    from kbench.newton.hvp import HvpPlan
+    from kbench.percall.solve import plan_of, run_forward
 
     print(f"[hvp] config={name} statewise={statewise} row_classes={row_classes}", flush=True)
     static, theta, cw = _static(name, statewise)
@@ -240,8 +241,8 @@ def test_exact_hvp_on_a_large_tree_matches_oracle(leaves):
     """S = 4095 and 8191 (three small families): the class / graph HVP against the oracle's HVP (1e-3 of
     max |H u|), through the kernels' 4- and 8-position shapes; at S = 8191 the E-step second-order,
     E tangent and self-loop contractions compute in float32 (three float64 rows of S exceed the LDS)."""
-    from dropin.hvp import HvpPlan
-    from dropin.solve import plan_of, run_forward
+    from kbench.newton.hvp import HvpPlan
+    from kbench.percall.solve import plan_of, run_forward
 
     print(f"[hvp] large tree leaves={leaves} (S={2 * leaves - 1})", flush=True)
     problem, static, theta, cw = _big_tree(leaves, True)
@@ -282,7 +283,7 @@ def test_e_adjoint_entry_solves_the_e_system(name, statewise):
     w - J_E^T w = q with q = acc_E + VJP(acc_Es1, acc_Es2, acc_Ebar) + q_extra, and the parameter
     cotangents of one E step at (w, acc_Ebar) plus acc's rows (float64, 1e-9 relative).  "big": S = 4095,
     the epilogue's LDS kernel (the register-resident one serves trees of up to 2048 nodes)."""
-    from dropin.solve import run_forward
+    from kbench.percall.solve import run_forward
     from kbench.runtime import fused_solver
 
     print(f"[e adjoint] config={name} statewise={statewise}", flush=True)
@@ -322,7 +323,7 @@ def test_e_adjoint_entry_reports_a_failed_solve(monkeypatch):
     """kb_e_adjoint with one BiCGSTAB iteration and an unreachable tolerance: the status words say
     failed, FusedSolver.e_adjoint raises RuntimeError (as the backward does), and check_solve=False
     leaves the status for the caller."""
-    from dropin.solve import run_forward
+    from kbench.percall.solve import run_forward
     from kbench.fused import FusedSolver
 
     static, theta, cw = _static("1", True)
@@ -340,8 +341,8 @@ def test_e_adjoint_entry_reports_a_failed_solve(monkeypatch):
 
 def test_native_tangent_e_adjoint_matches_autograd_bicgstab():
     """The HVP's tangent E side through kb_e_adjoint agrees with BiCGSTAB over autograd E-step products."""
-    from dropin.hvp import HvpPlan
-    from dropin.solve import plan_of, run_forward
+    from kbench.newton.hvp import HvpPlan
+    from kbench.percall.solve import plan_of, run_forward
 
     static, theta, cw = _static("1", True)
     _, sv = run_forward(static, theta, cw)
@@ -356,8 +357,8 @@ def test_native_tangent_e_adjoint_matches_autograd_bicgstab():
 
 
 def test_ggn_hvp_is_symmetric_and_psd():
-    from dropin.hvp import ggn_hvp
-    from dropin.solve import plan_of, run_forward
+    from kbench.newton.hvp import ggn_hvp
+    from kbench.percall.solve import plan_of, run_forward
 
     static, theta, cw = _static("1", True)
     _, sv = run_forward(static, theta, cw)

@@ -43,11 +43,16 @@ def _check(tag, z, loss, saved):
         assert pattern and (ma <= 2e-4 or err <= 1e-5), k
 
 
+@pytest.mark.parametrize("fuse", [False, True], ids=["one_launch_per_sweep", "fused_sweep_chains"])
 @pytest.mark.parametrize("case", sorted(CASES))
-def test_dropin_forward_matches_reference_fixture(case):
-    from dropin.solve import plan_of
+def test_dropin_forward_matches_reference_fixture(case, fuse, monkeypatch):
+    """The per-call path, with one launch per sweep and with each wave's sweep chain in one launch
+    (KBENCH_FUSE_SWEEPS: float chains in linear space, reference forward.py:60-108)."""
+    from kbench.core.kernels import wave_step
+    from kbench.percall.solve import plan_of
 
-    print(f"[pristine-fwd dropin] case={case}", flush=True)
+    monkeypatch.setattr(wave_step, "FUSE_SWEEPS", fuse)
+    print(f"[pristine-fwd dropin] case={case} fuse_sweeps={fuse}", flush=True)
     z, static, theta, cw = _inputs(case)
     loss, saved = plan_of(static).forward(theta, cw, pi_iters=int(z["pi_iters"]))
     torch.cuda.synchronize()

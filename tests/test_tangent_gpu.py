@@ -1,5 +1,5 @@
 """GPU parity of the forward-tangent wrappers (kbench.core.kernels.{e_step,dts,wave}_tangent) and of the
-forward-tangent call sequence (tests/dropin/hvp.py ``TangentForward``) against the float64 CPU oracle.
+forward-tangent call sequence (kbench/newton/hvp.py ``TangentForward``) against the float64 CPU oracle.
 
 Kernel tests feed the oracle's own primal point (Pi*, E*, ...) to the HIP
 wrappers, in float64 (tight tolerance: same arithmetic up to summation order)
@@ -212,8 +212,8 @@ def test_wave_step_tangent_matches_oracle(name, dt, n_iters):
 
 @pytest.mark.parametrize("name,statewise", [("tiny", None), ("1", None), ("1", True)])
 def test_jvp_root_scores_matches_oracle(name, statewise):
-    from dropin.hvp import TangentForward
-    from dropin.solve import plan_of, run_forward
+    from kbench.newton.hvp import TangentForward
+    from kbench.percall.solve import plan_of, run_forward
 
     print(f"[jvp] config={name} statewise={statewise}", flush=True)
     static, theta, cw = _static(name, statewise)
@@ -235,8 +235,8 @@ def test_jvp_root_scores_matches_oracle(name, statewise):
 
 def test_jvp_root_scores_adaptive_and_unfused_paths_agree():
     """The three self-loop modes of the tangent forward solve the same tangent (config 1)."""
-    from dropin.hvp import TangentForward
-    from dropin.solve import plan_of, run_forward
+    from kbench.newton.hvp import TangentForward
+    from kbench.percall.solve import plan_of, run_forward
 
     static, theta, cw = _static("1", True)
     _, sv = run_forward(static, theta, cw)
@@ -253,8 +253,8 @@ def test_jvp_root_scores_adaptive_and_unfused_paths_agree():
 
 def test_jvp_root_scores_config3_linear_and_deterministic():
     """Full size (config 3): the JVP is linear in v and bitwise reproducible."""
-    from dropin.hvp import TangentForward
-    from dropin.solve import plan_of, run_forward
+    from kbench.newton.hvp import TangentForward
+    from kbench.percall.solve import plan_of, run_forward
 
     print("[jvp] config=3", flush=True)
     static, theta, cw = _static("3")

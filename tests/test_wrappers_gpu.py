@@ -1,6 +1,6 @@
 """GPU parity of the drop-in wrappers (kbench.core.kernels.*) driven in the reference glue's call sequence.
 
-``dropin.run_forward`` / ``run_backward`` (tests/dropin/solve.py) call the
+``kbench.percall.run_forward`` / ``run_backward`` call the
 HIP-backed wrappers with the reference glue's sequence and arguments.  Checked
 against the float64 CPU oracle (loss rel 1e-5, gradients rel 1e-4, active masks
 exact), for determinism, and against the native whole-pass driver
@@ -26,11 +26,18 @@ def _static(name, statewise=None):
     return static, cap["inputs"]["theta"].cuda(), cap["inputs"]["col_weights"].cuda()
 
 
-@pytest.mark.parametrize("name,statewise", [("tiny", None), ("1", None), ("1", True), ("2", None)])
-def test_glue_forward_matches_oracle(name, statewise):
-    from dropin import run_forward
+FUSE = pytest.mark.parametrize("fuse", [False, True], ids=["one_launch_per_sweep", "fused_sweep_chains"])
 
-    print(f"[glue-forward] config={name} statewise={statewise}", flush=True)
+
+@FUSE
+@pytest.mark.parametrize("name,statewise", [("tiny", None), ("1", None), ("1", True), ("2", None)])
+def test_glue_forward_matches_oracle(name, statewise, fuse, monkeypatch):
+    """With one launch per sweep and with each wave's sweep chain in one launch (KBENCH_FUSE_SWEEPS)."""
+    from kbench.core.kernels import wave_step
+    from kbench.percall import run_forward
+
+    monkeypatch.setattr(wave_step, "FUSE_SWEEPS", fuse)
+    print(f"[glue-forward] config={name} statewise={statewise} fuse_sweeps={fuse}", flush=True)
     static, theta, cw = _static(name, statewise)
     loss, saved = run_forward(static, theta, cw)
     torch.cuda.synchronize()
@@ -48,11 +55,15 @@ def test_glue_forward_matches_oracle(name, statewise):
         assert ok and (ma <= 2e-4 or mr <= 1e-5)
 
 
+@FUSE
 @pytest.mark.parametrize("name,statewise", [("tiny", None), ("1", None), ("1", True)])
-def test_glue_backward_matches_oracle(name, statewise):
-    from dropin import run_backward, run_forward
+def test_glue_backward_matches_oracle(name, statewise, fuse, monkeypatch):
+    """The backward at the per-call forward's point, that forward run both ways (KBENCH_FUSE_SWEEPS)."""
+    from kbench.core.kernels import wave_step
+    from kbench.percall import run_backward, run_forward
 
-    print(f"[glue-backward] config={name} statewise={statewise}", flush=True)
+    monkeypatch.setattr(wave_step, "FUSE_SWEEPS", fuse)
+    print(f"[glue-backward] config={name} statewise={statewise} fuse_sweeps={fuse}", flush=True)
     static, theta, cw = _static(name, statewise)
     loss, saved = run_forward(static, theta, cw)
     gt, gc = run_backward(static, theta, cw, saved)
@@ -70,7 +81,7 @@ def test_glue_backward_with_gmres_matches_oracle(name, statewise):
     import dataclasses
 
     import kbench_oracle as O
-    from dropin import run_backward, run_forward
+    from kbench.percall import run_backward, run_forward
     from kbench.fused import problem_to_captured
     from kbench.runtime import make_static
 
@@ -101,9 +112,9 @@ def test_glue_backward_with_gmres_matches_oracle(name, statewise):
 def test_level_waves_give_the_same_per_call_solve_and_hvp():
     """Rows regrouped into one wave per dependency level (synth.level_waves): the per-call forward gives
     bitwise the same rows, the gradients and an exact HVP agree with the size-wave layout."""
-    from dropin import run_backward, run_forward
-    from dropin.hvp import HvpPlan
-    from dropin.solve import plan_of
+    from kbench.percall import run_backward, run_forward
+    from kbench.newton.hvp import HvpPlan
+    from kbench.percall.solve import plan_of
     from kbench import synth
     from kbench.fused import problem_to_captured
     from kbench.runtime import make_static
@@ -134,7 +145,7 @@ def test_level_waves_give_the_same_per_call_solve_and_hvp():
 
 
 def test_glue_backward_is_deterministic():
-    from dropin import run_backward, run_forward
+    from kbench.percall import run_backward, run_forward
 
     static, theta, cw = _static("1", True)
     loss, saved = run_forward(static, theta, cw)
@@ -146,7 +157,7 @@ def test_glue_backward_is_deterministic():
 
 def test_glue_matches_fused_driver_config2():
     """The per-wrapper path and the whole-pass driver solve the same problem (forward, config 2)."""
-    from dropin import run_forward
+    from kbench.percall import run_forward
     from kbench.runtime import run_forward as run_forward_fused
 
     static, theta, cw = _static("2")
@@ -186,7 +197,7 @@ def test_active_mask_bit_exact():
 def test_wave_step_in_place_matches_out_of_place():
     """Pi_out may alias Pi_in and Pibar (the glue's even sweeps write into the Pibar buffer)."""
     from kbench.core.kernels.wave_step import compute_wave_step
-    from dropin import run_forward
+    from kbench.percall import run_forward
 
     static, theta, cw = _static("1", True)
     loss, saved = run_forward(static, theta, cw)
@@ -221,7 +232,7 @@ def test_wave_step_in_place_matches_out_of_place():
 
 def test_glue_config3_forward_matches_fused():
     """Full-size drop-in check: config 3 forward through the wrappers equals the whole-pass driver."""
-    from dropin import run_forward
+    from kbench.percall import run_forward
     from kbench.runtime import run_forward as run_forward_fused
 
     print("[glue-forward] config=3", flush=True)
@@ -240,7 +251,7 @@ def test_fused_sweep_chains_match_one_launch_per_sweep(name, monkeypatch):
     """KBENCH_FUSE_SWEEPS: a wave's chained sweeps run as one launch (the linear-space preorder-ownership kernel
     for float rows) and agree with one launch per sweep to float32 rounding: same -inf pattern, loss 1e-6, rows
     2e-4 absolute or 1e-5 relative."""
-    import dropin
+    from kbench import percall as dropin
     from kbench.core.kernels import wave_step
 
     print(f"[fuse-sweeps] config={name}", flush=True)
@@ -265,7 +276,7 @@ def test_held_sweeps_run_before_other_work(monkeypatch):
 
     The rows agree with one launch per sweep to float32 rounding.
     """
-    from dropin.solve import plan_of
+    from kbench.percall.solve import plan_of
     from kbench.core.kernels import _hip as H
     from kbench.core.kernels import wave_step
     from kbench.core.kernels.wave_backward import active_mask_from_rhs_absmax_fused

@@ -65,6 +65,12 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   // Neumann loop, except where 1024 threads (128 VGPRs) own four or more
   // positions each: there the registers spill to scratch memory
   constexpr bool PF = !(NT == 1024 && CPT >= 4);
+  // The set-up's loads (the first row's record, the position tables, the
+  // bucket slot, the constant rows) are all issued before any of them is
+  // consumed, and the first row's fetch before the LDS stores that wait for
+  // them: two memory round trips in all.
+  const bool first_rec = AHEAD && !P.class_mode && (int)blockIdx.x < n_rows;
+  const int rec0 = first_rec ? P.bslot[(size_t)KB_BREC * (first + blockIdx.x) + (tid & (KB_BREC - 1))] : 0;
   OwnTablesC<NT, CPT> O;
   O.load(T);
   if (tid < 64) {
@@ -87,27 +93,28 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     qp[k] = okp[k] ? T.post[i] : ZERO;
     nex[k] = okp[k] ? T.tin[i] - i : 0;
     const int pa = okp[k] ? T.ppos[i] : -1;
+    const int pf = okp[k] ? T.pflag[i] : 0;  // loaded with ppos, not after it
     ppos[k] = pa >= 0 ? pa : ZERO;
-    pfl[k] = pa >= 0 ? T.pflag[i] : 0;
+    pfl[k] = pa >= 0 ? pf : 0;
     endm1[k] = okp[k] ? T.endpos[i] - 1 : ZERO;
   }
   // gradient buckets of every row this workgroup processes (static round-robin
-  // assignment, so the summation order is fixed)
+  // assignment, so the summation order is fixed), starting from this
+  // workgroup's slot (preorder layout): slot b is carried by workgroup b of
+  // every level in turn.  Its values are read here, with the other set-up
+  // loads, and the launch ends with plain stores.
   // (in LDS for rows of up to 2048 states, own positions only: each thread
   // reads and writes just its own entries, so the accumulation needs no
   // barrier; in registers for longer rows, whose LDS rows leave no room)
   constexpr bool BK_LDS = MAXS <= 2048;
   __shared__ float Bk[BK_LDS ? 8 * MAXS : 1];
   float cacc[BK_LDS ? 1 : 8][CPT];
+  float* const cr = P.contrib + (size_t)blockIdx.x * 8 * S;
+  float old[8][CPT];
 #pragma unroll
   for (int j = 0; j < 8; ++j)
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-      if constexpr (BK_LDS)
-        Bk[j * MAXS + own_pos_c<NT, CPT>(k)] = 0.0f;
-      else
-        cacc[j][k] = 0.0f;
-    }
+    for (int k = 0; k < CPT; ++k) old[j][k] = okp[k] ? cr[(size_t)j * S + own_pos_c<NT, CPT>(k)] : 0.0f;
   // Per-position constants, one [S] row shared by every row: for rows of up
   // to 2048 states, seven of them stay in LDS for the whole launch (own
   // positions, so each thread reads back only what it wrote), and the per-row
@@ -117,6 +124,13 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   enum { K_DL, K_EBAR, K_E, K_SL1, K_SL2, K_PD, K_PS, K_N };
   __shared__ float Kc[CK_LDS ? K_N * MAXS : 1];
   const float* const kg[K_N] = {P.DL, P.Ebar, P.E, P.SL1, P.SL2, P.pD, P.pS};
+  float kx[CK_LDS ? K_N : 1][CPT];
+  if constexpr (CK_LDS) {
+#pragma unroll
+    for (int j = 0; j < K_N; ++j)
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) kx[j][k] = okp[k] ? kg[j][own_pos_c<NT, CPT>(k)] : 0.0f;
+  }
   // constant j at own position k (0 at padding positions)
   auto kc_own = [&](int j, float (&x)[CPT]) {
     if constexpr (CK_LDS) {
@@ -204,7 +218,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     if (P.class_mode) {
       fetch_rows(row_of(blockIdx.x));
     } else {
-      crec = load_rec(blockIdx.x);
+      crec = rec0;
       fetch_rows(field(crec, BR_ROW));
       fetch_row_data(crec);
       nrec = load_rec(min((int)(blockIdx.x + gridDim.x), n_rows - 1));
@@ -220,15 +234,20 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     fetch_rows(field(crec, BR_ROW));
     fetch_row_data(crec);
   };
+  // the set-up's LDS stores, after every load above is in flight
   if constexpr (CK_LDS) {
 #pragma unroll
-    for (int j = 0; j < K_N; ++j) {
-      float x[CPT];
-#pragma unroll
-      for (int k = 0; k < CPT; ++k) x[k] = okp[k] ? kg[j][own_pos_c<NT, CPT>(k)] : 0.0f;
-      lds_store_own<CPT>(Kc + j * MAXS, x);
-    }
+    for (int j = 0; j < K_N; ++j) lds_store_own<CPT>(Kc + j * MAXS, kx[j]);
   }
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      if constexpr (BK_LDS)
+        Bk[j * MAXS + own_pos_c<NT, CPT>(k)] = old[j][k];
+      else
+        cacc[j][k] = old[j][k];
+    }
 
   for (int rr = blockIdx.x; rr < n_rows; rr += gridDim.x) {
   __syncthreads();  // LDS of the previous row is no longer read
@@ -753,14 +772,12 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
 
   }  // rows
 
-  // add into this workgroup's bucket slot (preorder layout): slot b is updated
-  // by workgroup b of every level in turn, so the summation order is fixed
-  float* cr = P.contrib + (size_t)blockIdx.x * 8 * S;
+  // this workgroup's slot holds the buckets carried through this level
 #pragma unroll
   for (int j = 0; j < 8; ++j)
 #pragma unroll
     for (int k = 0; k < CPT; ++k)
-      if (okp[k]) cr[(size_t)j * S + own_pos_c<NT, CPT>(k)] += bucket(j, k);
+      if (okp[k]) cr[(size_t)j * S + own_pos_c<NT, CPT>(k)] = bucket(j, k);
 }
 
 #define KB_BWD_CASE(NT_, CPT_)                                                                      \

@@ -230,6 +230,7 @@ def per_call_timings(static, theta, cw, steps: int = 5, static_levels=None) -> d
     import torch
 
     from kbench.core.kernels import wave_step
+    from kbench.percall.graph import GraphedSolve
     from kbench.percall.kernels import noop
     from kbench.percall.solve import SolvePlan, root_softmax2
 
@@ -255,14 +256,25 @@ def per_call_timings(static, theta, cw, steps: int = 5, static_levels=None) -> d
             per_launch = _time_host(waves(plan), 2, steps)
             wave_step.FUSE_SWEEPS = True
             fused = _time_host(waves(plan), 2, steps)
+            gs = GraphedSolve(plan, theta, cw)  # captured in the first warm-up call, chains fused
+
+            def graphed():
+                _, sv = gs.forward(theta, cw)
+                gs.reverse(sv)
+
+            graph_ms = _time_host(graphed, 2, steps)
+            del gs
         finally:
             wave_step.FUSE_SWEEPS = old
+        torch.cuda.empty_cache()
         floor = _time_host(waves(floor_plan), 2, steps)
         e_ms = _time_host(e_side(plan), 2, steps)
         return {"ms_one_launch_per_sweep": round(per_launch, 3), "ms_sweep_chains_fused": round(fused, 3),
+                "ms_graph_replay": round(graph_ms, 3),
                 "ms_glue_floor": round(floor, 3), "ms_e_adjoint_and_theta_vjp": round(e_ms, 3),
                 "ms_solve_one_launch_per_sweep": round(per_launch + e_ms, 3),
-                "ms_solve_sweep_chains_fused": round(fused + e_ms, 3)}
+                "ms_solve_sweep_chains_fused": round(fused + e_ms, 3),
+                "ms_solve_graph_replay": round(graph_ms + e_ms, 3)}
 
     out = three(static)
     out["note"] = (
@@ -271,8 +283,10 @@ def per_call_timings(static, theta, cw, steps: int = 5, static_levels=None) -> d
         "where the frozen glue calls _scatter_accum per bucket): ms_one_launch_per_sweep / "
         "ms_sweep_chains_fused / ms_glue_floor time the forward plus the per-wave reverse sweep with one "
         "launch per sweep and wave (the pristine-structure proxy), with each wave's sweep chain in one launch "
-        "(KBENCH_FUSE_SWEEPS=1), and with every wrapper a no-op (same driver code and calls); the glue's "
-        "E adjoint and theta VJP (ms_e_adjoint_and_theta_vjp) are timed apart and added in ms_solve_*" % steps)
+        "(KBENCH_FUSE_SWEEPS=1), and with every wrapper a no-op (same driver code and calls); ms_graph_replay "
+        "times the same fused-chain call sequence captured once as two HIP graphs (kbench.percall.graph: "
+        "forward and reverse wave loops) and replayed; the glue's E adjoint and theta VJP "
+        "(ms_e_adjoint_and_theta_vjp) are timed apart and added in ms_solve_*" % steps)
     if static_levels is not None:
         lv = three(static_levels)
         lv["n_waves"] = len(static_levels.wave_layout["wave_metas"])

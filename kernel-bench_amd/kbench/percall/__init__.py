@@ -13,10 +13,13 @@ driver does not implement (GMRES self-loop solves, a positive
 * ``solve``: ``SolvePlan`` -- forward (E fixed point, per-wave split term and
   ``pi_iters - 1`` sweeps, loss) and backward (per-wave adjoint in reverse,
   E adjoint, theta / column VJP);
+* ``graph``: ``GraphedSolve`` -- the same forward and reverse wave loops
+  captured once as two HIP graphs and replayed (the E adjoint stays eager);
 * ``krylov``: the E adjoint's BiCGSTAB (the reference's stopping and
   breakdown rules);
 * ``kernels``: the wrapper namespaces a plan calls through (the real wrappers,
   and no-op stand-ins that time the driver alone).
 """
 
+from .graph import GraphedSolve  # noqa: F401
 from .solve import SolvePlan, plan_of, run_backward, run_forward  # noqa: F401

@@ -127,9 +127,11 @@ class SolvePlan:
             self.waves.append(w)
 
     # ------------------------------------------------------------------ shared
-    def _parameters(self, theta, col_weights):
-        """(pS, pD, pL, mt, col, weighted) of theta, as the forward extracts them."""
-        weighted = not uniform_columns(col_weights)
+    def _parameters(self, theta, col_weights, weighted=None):
+        """(pS, pD, pL, mt, col, weighted) of theta, as the forward extracts them (``weighted``, when
+        given, is the caller's reading of the column weights: no host read here)."""
+        if weighted is None:
+            weighted = not uniform_columns(col_weights)
         st = self.static
         if weighted:
             pS, pD, pL, mt, col = extract_parameters_weighted_cols(
@@ -163,11 +165,11 @@ class SolvePlan:
         with torch.no_grad():
             return self._forward(theta, col_weights, int(self.so.pi_iters if pi_iters is None else pi_iters))
 
-    def _forward(self, theta, col_weights, P):
+    def _forward(self, theta, col_weights, P, weighted=None):
         if P < 2 or P % 2:
             raise ValueError("pi_iters must be an even integer at least 2")
         so, S, C, G = self.so, self.S, self.C, self.G
-        pS, pD, pL, mt, col, weighted = self._parameters(theta, col_weights)
+        pS, pD, pL, mt, col, weighted = self._parameters(theta, col_weights, weighted)
         E0 = theta.new_full((G, S), float(so.e_init))
         E, Es1, Es2, Ebar = self.k.e_fixed_point_triton(
             E0, log_pS=pS, log_pD=pD, log_pL=pL, max_coupling=mt, col_log_probs=col, use_col_weights=weighted,

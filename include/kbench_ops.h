@@ -359,6 +359,8 @@ int kb_rows_sum_accum(int32_t dtype, int32_t S, int32_t m, const int64_t* n, con
  * parameter tensors are [G, S] item-state matrices.  The stopping test is
  * applied per item row (the reference applies it to the max over rows; the
  * two agree for G = 1).  n_iter [G] (nullable) gets the step count.
+ * Float32 rows too long for three float64 LDS rows are iterated in float32
+ * arithmetic, with tol floored at 8 float32 epsilons (9.5e-7).
  */
 typedef struct kb_etan_io {
   int32_t dtype, G, use_col_weights, max_iter;

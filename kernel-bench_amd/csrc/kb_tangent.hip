@@ -13,9 +13,12 @@
 // with dRS = sum_s r[s] dX[s] and dAS[s] = sum over the path root..s of
 // r dX (one prefix scan over the Euler tour in LDS).  Fixed points and fixed
 // iteration counts run inside one launch with the primal coefficients kept in
-// registers and the tangent row in LDS, in float64 whatever the tensor dtype.
+// registers and the tangent row in LDS, in float64 whatever the tensor dtype,
+// except float32 rows too long for three float64 LDS rows (S > 6741), which
+// run in float32.
 #include <hip/hip_runtime.h>
 
+#include <cfloat>
 #include <cstdint>
 #include <type_traits>
 
@@ -142,6 +145,10 @@ __global__ __launch_bounds__(NT) void etan_kernel(OpsTree t, EtArgs<T> a) {
     for (int k = 0; k < CPT; ++k) q[k] = dRS - dAS[k];
   };
 
+  // Float32 arithmetic cannot resolve a relative change below its own
+  // rounding: its tolerance is floored at 8 float32 epsilons (9.5e-7), or a
+  // tol below that would run every row to max_iter on 1-ulp oscillations.
+  const C tol = std::is_same_v<C, float> ? (C)fmax(a.tol, 8.0 * (double)FLT_EPSILON) : (C)a.tol;
   int it = 0;
   for (;;) {
     C q[CPT], nx[CPT];
@@ -168,7 +175,7 @@ __global__ __launch_bounds__(NT) void etan_kernel(OpsTree t, EtArgs<T> a) {
     ++it;
     const C md = block_max(ld, red);  // its barriers also publish D
     const C sc = block_max(lsc, red);
-    if (md <= a.tol * fmax(C(1), sc) || it >= a.max_iter) break;
+    if (md <= tol * fmax(C(1), sc) || it >= a.max_iter) break;
   }
   // children and Ebar tangents at the final dE
   C q[CPT];

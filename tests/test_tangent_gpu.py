@@ -76,6 +76,38 @@ def test_e_tangent_fixed_point_matches_oracle(name, dt, statewise):
         assert e <= TOL[dt]
 
 
+def test_e_tangent_float32_long_rows_stop_on_their_rounding_floor():
+    """At S = 8191 in float32 the kernel iterates in float32; with the default tol (1e-9, far below
+    float32 rounding) it stops on the 9.5e-7 floor well before max_iter, as accurate as at tol 1e-7."""
+    from kbench.core.kernels.e_step_tangent import e_tangent_fixed_point
+
+    print("[e-tangent] big float32, default tol: step count", flush=True)
+    dt = torch.float32
+    static, prob, saved = _wave_fixture("big", True, dt)
+    S, G = prob.S, 1
+    th = _theta("big", True, prob)
+    v = np.random.default_rng(11).normal(size=th.shape)
+    d = O.param_jvp_uniform(th, v, prob.unnorm_row_max, prob.statewise, prob.itemwise)
+    st = lambda x: np.broadcast_to(O.as_item_state(np.asarray(x, dtype=np.float64), S, G), (G, S)).copy()
+    prim = [st(saved[k]) for k in ("log_pS", "log_pD", "log_pL", "max_coupling")]
+    ref = O.e_tangent_fixed_point(np.asarray(saved["E"]), *(st(x) for x in d), *prim, np.zeros(S), prob.tree,
+                                  max_iter=2000, tol=1e-13, use_col_weights=False)
+    h = static.state_helpers
+    n_iter = torch.zeros(G, dtype=torch.int32, device="cuda")
+    got = e_tangent_fixed_point(_t(saved["E"], dt), *(_t(st(x), dt) for x in d), *(_t(x, dt) for x in prim),
+                                torch.zeros(S, dtype=dt, device="cuda"), h["node_parent"], h["node_child1"],
+                                h["node_child2"], int(h["max_ancestor_depth"]), n_iter_out=n_iter,
+                                use_col_weights=False)
+    torch.cuda.synchronize()
+    steps = int(n_iter[0])
+    print(f"  steps={steps} of max_iter=2000")
+    assert 1 <= steps < 200
+    for name, g, r in zip(("dE", "dE_s1", "dE_s2", "dEbar"), got, ref):
+        e = _rel(g.cpu().numpy(), r)
+        print(f"  {name}: rel={e:.3e}")
+        assert e <= TOL[dt]
+
+
 def _theta(name, statewise, prob):
     """The fixture's theta as float64 (rounded through float32, as the GPU side holds it)."""
     p = _big_problem(bool(statewise)) if name == "big" else kbtest.problem(name, statewise)

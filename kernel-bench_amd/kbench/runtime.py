@@ -23,6 +23,9 @@ whose staged Pibar adjoint has a small abs-sum are dropped).  With either set,
 ``run_backward`` runs the per-call drivers of ``kbench.percall`` instead, which
 call the same HIP wrappers wave by wave in the reference glue's order (the
 forward intermediates have the same names and meaning on both paths).
+Problems with one parameter row per item (``itemwise``: G = number of items,
+each clade row reading its item's rates through ``rate_item_idx``) run both
+passes on the per-call drivers: the whole-pass driver covers one row.
 """
 
 from __future__ import annotations
@@ -72,6 +75,10 @@ def fused_solver(static) -> FusedSolver:
 
 def run_forward(static, theta: torch.Tensor, col_weights: torch.Tensor):
     """theta -> (loss, saved forward intermediates)."""
+    if static.itemwise:
+        from kbench.percall import run_forward as run_forward_per_call
+
+        return run_forward_per_call(static, theta, col_weights)
     with torch.no_grad():
         loss, saved = fused_solver(static).run_forward(theta, col_weights)
     saved.pop("_use_col_weights", None)
@@ -79,10 +86,11 @@ def run_forward(static, theta: torch.Tensor, col_weights: torch.Tensor):
 
 
 def needs_per_call_backward(static) -> bool:
-    """True when the solver options ask for a backward the whole-pass driver does not implement."""
+    """True when the solver options ask for a backward the whole-pass driver does not implement,
+    or the problem has one parameter row per item."""
     so = static.solver_options
     return (str(so.self_loop_solver).strip().lower() != "neumann"
-            or float(so.pibar_side_threshold) > 0.0)
+            or float(so.pibar_side_threshold) > 0.0 or bool(static.itemwise))
 
 
 def run_backward(static, theta: torch.Tensor, col_weights: torch.Tensor, saved: dict):
@@ -102,5 +110,10 @@ def run_backward_fused(static, theta: torch.Tensor, col_weights: torch.Tensor, s
         return fused_solver(static).run_backward(theta, col_weights, saved)
 
 
-# the forward always runs on the whole-pass driver
-run_forward_fused = run_forward
+def run_forward_fused(static, theta: torch.Tensor, col_weights: torch.Tensor):
+    """``run_forward`` on the whole-pass driver only (``itemwise`` problems raise
+    ``NotImplementedError`` instead of selecting the per-call path)."""
+    with torch.no_grad():
+        loss, saved = fused_solver(static).run_forward(theta, col_weights)
+    saved.pop("_use_col_weights", None)
+    return loss, saved

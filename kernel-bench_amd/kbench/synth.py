@@ -352,6 +352,11 @@ class ProblemConfig:
     # families of one gene leaf (their root row is a leaf row), appended after
     # the simulated ones from a separate random stream
     single_leaf_families: int = 0
+    # one parameter row per family (item): theta [n_families, 3], every clade
+    # row reads its family's rates (rate_item_idx = the row's family); global
+    # rates only, as the reference's extraction defines no per-item per-state
+    # layout
+    itemwise: bool = False
 
 
 def build_problem(cfg: ProblemConfig) -> dict:
@@ -361,6 +366,8 @@ def build_problem(cfg: ProblemConfig) -> dict:
     (reference kbench/runtime.py:47-60): ``wave_layout``, ``state_helpers``,
     ``rate_item_idx``, ``itemwise``, ``statewise``.
     """
+    if cfg.itemwise and cfg.statewise:
+        raise ValueError("itemwise problems take one global rate row per item (statewise=False)")
     rng = np.random.default_rng(cfg.seed)
     tree = yule_tree(cfg.n_species_leaves, rng)
     S = tree.S
@@ -486,7 +493,7 @@ def build_problem(cfg: ProblemConfig) -> dict:
         "item_idx": item_idx,
         "wave_metas": wave_metas,
     }
-    theta_shape = (S, 3) if cfg.statewise else (3,)
+    theta_shape = (n_fam, 3) if cfg.itemwise else ((S, 3) if cfg.statewise else (3,))
     theta = rng.uniform(-3.0, -1.0, size=theta_shape)
     col_weights = np.zeros(S, dtype=np.float64)
     so = {"pi_iters": 16, "neumann_terms": 16, "e_tol": 1e-8}
@@ -496,8 +503,8 @@ def build_problem(cfg: ProblemConfig) -> dict:
         "static": {
             "wave_layout": wave_layout,
             "state_helpers": helpers,
-            "rate_item_idx": np.zeros(C, dtype=np.int64),
-            "itemwise": False,
+            "rate_item_idx": item_idx.copy() if cfg.itemwise else np.zeros(C, dtype=np.int64),
+            "itemwise": bool(cfg.itemwise),
             "statewise": bool(cfg.statewise),
         },
         "inputs": {"theta": theta, "col_weights": col_weights},
@@ -580,6 +587,8 @@ def family_subset(problem: dict, families) -> dict:
     solve of those families alone (the loss and gradients of a whole problem
     are the sums over a partition of its families).
     """
+    if problem["static"]["itemwise"]:
+        raise ValueError("family_subset takes problems with one parameter row (itemwise=False)")
     fams = [int(f) for f in families]
     wl = problem["static"]["wave_layout"]
     item = np.asarray(wl["item_idx"])

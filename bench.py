@@ -218,10 +218,11 @@ def per_call_timings(static, theta, cw, steps: int = 5, static_levels=None) -> d
     """ms per solve through the builder's per-call drivers (``kbench.percall``: the wrappers called in the
     reference glue's call sequence, with the wave buckets folded by the library's fixed-order row sums).
 
-    Three timings of the same scope, the forward plus the backward's per-wave reverse sweep, so that
+    Four timings of the same scope, the forward plus the backward's per-wave reverse sweep, so that
     they compare: one launch per sweep (the pristine-structure proxy), each wave's sweep chain in one
-    launch (``KBENCH_FUSE_SWEEPS``), and the same driver with every wrapper replaced by a no-op (its
-    Python, torch glue and host syncs alone).  The glue's E adjoint and theta VJP, which follow the
+    launch (``KBENCH_FUSE_SWEEPS``), that fused-chain call sequence captured once as two HIP graphs
+    and replayed (``kbench.percall.graph.GraphedSolve``), and the same driver with every wrapper
+    replaced by a no-op (its Python, torch glue and host syncs alone).  The glue's E adjoint and theta VJP, which follow the
     reverse sweep and do not depend on the wave launches (a BiCGSTAB over E-step products whose
     iteration count depends on the cotangents, so a no-op run would not repeat it), are timed apart;
     the whole solve is the sum.  With ``static_levels`` (the same problem regrouped by

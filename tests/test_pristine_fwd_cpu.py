@@ -1,4 +1,4 @@
-"""The oracle reproduces the reference's own forward on config 1 (tests/golden/pristine_fwd_*.npz).
+"""The oracle reproduces the reference's own forward on configs 1 and 2 (tests/golden/pristine_fwd_*.npz).
 
 The fixtures hold the outputs of the reference's frozen glue over its pristine
 Triton kernels (kbench/runtime.py:63-75, experiments/pristine_kernels/*.py),
@@ -8,7 +8,10 @@ They pin what no closed form fixes: the truncated forward schedule
 (``pi_iters - 1`` sweeps per wave, leaf waves from the leaf initialisation,
 split waves from their split term, forward.py:60-117), at two sweep counts
 whose losses differ by 1.4e-3 relative, so a wrong sweep count, a dropped
-split term or a wrong starting row fails here.
+split term or a wrong starting row fails here.  Config 2 (S = 511, rows with
+several splits, E stopping tolerance 1e-6) adds the split reduction over
+several splits and a second E tolerance; its fixture keeps every row maximum,
+the root rows of Pi and Pibar and 192 seeded other rows (``rows``).
 
 Tolerances follow from the reference's float32 arithmetic: loss relative
 1e-6, arrays |a - b| <= 1e-5 max(1, |b|), and the same non-finite pattern
@@ -25,7 +28,8 @@ import kbench_oracle as O
 from kbench import synth
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
-CASES = {"config1": None, "config1_pi4": None, "config1_statewise": True}
+CASES = {"config1": ("1", None), "config1_pi4": ("1", None), "config1_statewise": ("1", True),
+         "config2": ("2", None)}
 ARRAYS = ("E", "E_s1", "E_s2", "Ebar", "pi_wave", "pibar_wave", "pibar_row_max")
 
 
@@ -34,10 +38,19 @@ def fixture(case: str):
 
 
 def problem(case: str) -> dict:
-    cfg = synth.config("1")
-    if CASES[case] is not None:
-        cfg = dataclasses.replace(cfg, statewise=CASES[case])
+    name, statewise = CASES[case]
+    cfg = synth.config(name)
+    if statewise is not None:
+        cfg = dataclasses.replace(cfg, statewise=statewise)
     return synth.build_problem(cfg)
+
+
+def rows_of(z, k, got):
+    """``got`` restricted to the rows the fixture keeps for array ``k`` (all rows unless it has ``rows``)."""
+    got = np.asarray(got)
+    if "rows" in z.files and k in ("pi_wave", "pibar_wave"):
+        return got[np.asarray(z["rows"])]
+    return got
 
 
 def close_to_fixture(got, ref, rel=1e-5):
@@ -60,7 +73,7 @@ def test_oracle_reproduces_the_reference_forward(case):
     loss, saved = O.forward(prob, z["theta"].astype(np.float64), cw, pi_iters=int(z["pi_iters"]))
     assert abs(loss - float(z["loss"])) <= 1e-6 * abs(float(z["loss"]))
     for k in ARRAYS:
-        pattern, err = close_to_fixture(saved[k], z[k])
+        pattern, err = close_to_fixture(rows_of(z, k, saved[k]), z[k])
         assert pattern and err <= 1e-5, (k, pattern, err)
 
 

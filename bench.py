@@ -379,10 +379,24 @@ def config5_timing(static_levels, theta, cw, warmup: int = 3, n_hvp: int = 50) -
     dur, byt = _tangent_sweep_launches(hvp, us[0])
     avg_ms, avg_b = st.mean(dur), st.mean(byt)
     achieved = avg_b / (avg_ms * 1e-3) / 1e9
+    del hvp
+    # a Newton step moves theta: the next point's forward, point cache and first (captured) HVP, with
+    # the process's one-off set-up (layouts, plans, first launches) already done
+    theta2 = theta + 1e-3 * us[0].reshape(theta.shape)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    _, sv2 = run_forward(static_levels, theta2, cw)
+    hvp2 = make_exact_hvp(static_levels, theta2, cw, sv2)
+    hvp2(us[1])
+    torch.cuda.synchronize()
+    point_ms = (time.perf_counter() - t0) * 1e3
+    del hvp2, sv2
     return {
         "ms_per_hvp": round(block_ms / n_hvp, 4),
         "ms_per_newton_cg_step_50_hvps": round(block_ms * 50.0 / n_hvp, 2),
         "point_cache_ms": round(cache_ms, 2),
+        "ms_new_point": round(point_ms, 2),
+        "ms_per_newton_cg_step_with_new_point": round(point_ms + block_ms * 50.0 / n_hvp, 2),
         "roofline": {"bound": "hbm", "kernel": "wave_tan_pre_kernel", "achieved": round(achieved, 3),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 6),
                      "launches": len(dur), "launch_unit": "one tangent-sweep launch per dependency level",
@@ -391,8 +405,10 @@ def config5_timing(static_levels, theta, cw, warmup: int = 3, n_hvp: int = 50) -
         "note": (f"{n_hvp} exact HVPs (seeded unit Gaussian directions) after {warmup} warm-up HVPs, timed as "
                  "one block; make_exact_hvp on the level waves: tangent forward and reverse on one row per class "
                  "of identical rows, replayed as one HIP graph; point_cache_ms = the point cache, the class "
-                 "schedule and the first (captured) HVP; the kernel roofline from HIP events around each "
-                 "tangent-sweep launch of one eager HVP"),
+                 "schedule and the first (captured) HVP, including the process's one-off set-up; ms_new_point = the "
+                 "same at the next point (theta moved by 1e-3 along a unit direction: per-call forward, point "
+                 "cache, class schedule, first HVP), which a Newton-CG step pays once besides its 50 HVPs; the "
+                 "kernel roofline from HIP events around each tangent-sweep launch of one eager HVP"),
     }
 
 

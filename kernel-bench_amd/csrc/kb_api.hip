@@ -808,7 +808,8 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
 
 // floats per workgroup slot of the backward row kernels
 static size_t bwd_slot_floats(int S, int large) {
-  return kb::kb_use_large(S, large) ? (size_t)kb::KB_LARGE_SLOT_ROWS * kb::kb_large_ld(S) : (size_t)8 * S;
+  return kb::kb_use_large(S, large) ? (size_t)kb::KB_LARGE_SLOT_ROWS * kb::kb_large_ld(S)
+                                    : (size_t)8 * kb::kb_slot_ld(S, large);
 }
 
 static int ensure_backward_work(kb_plan* p, int use_col) {
@@ -993,8 +994,8 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
     if (p->prof) KB_HIP(hipEventRecord(p->ev_bwd[2 * d + 1], st));
   }
   KB_HIP(hipGetLastError());
-  kb::launch_bwd_reduce(p->b_contrib, p->b_n_partials, S, p->b_slot,
-                        kb::kb_use_large(S, p->b_large) ? kb::kb_large_ld(S) : S, p->b_partial, p->b_acc_pre, st);
+  kb::launch_bwd_reduce(p->b_contrib, p->b_n_partials, S, p->b_slot, kb::kb_slot_ld(S, p->b_large), p->b_partial,
+                        p->b_acc_pre, st);
   kb::launch_bwd_unpermute(p->b_acc_pre, p->d_pre, S, p->b_acc, st);
   KB_HIP(hipGetLastError());
   if (io->acc_out)

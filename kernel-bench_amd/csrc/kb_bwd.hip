@@ -71,8 +71,13 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   // them: two memory round trips in all.
   const bool first_rec = AHEAD && !P.class_mode && (int)blockIdx.x < n_rows;
   const int rec0 = first_rec ? P.bslot[(size_t)KB_BREC * (first + blockIdx.x) + (tid & (KB_BREC - 1))] : 0;
+  // The wide shape's set-up reads its per-position rows with one vector load
+  // each (16-byte rows: the tables and constants start their allocations, the
+  // slot rows are kb_slot_ld(S) floats apart); the narrow shape (128 VGPRs)
+  // keeps one load per position, as the vector loads' registers spill there.
+  constexpr bool VEC = NT < 1024;
   OwnTablesC<NT, CPT> O;
-  O.load(T);
+  O.template load<VEC>(T);
   if (tid < 64) {
     R0[MAXS + tid] = 0.0f;
     R1[MAXS + tid] = 0.0f;
@@ -87,16 +92,31 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   // and, for the root-path sums, the position at own postorder slot k (the
   // padding slot ZERO past the row) and tin(i) - i
   int ppos[CPT], endm1[CPT], pfl[CPT], qp[CPT], nex[CPT];
+  if constexpr (VEC) {
+    int tpa[CPT], tpf[CPT], tend[CPT];
+    gld_own<CPT>(T.post, S, qp, ZERO);
+    gld_own<CPT>(T.ppos, S, tpa, -1);
+    gld_own<CPT>(T.pflag, S, tpf, 0);
+    gld_own<CPT>(T.endpos, S, tend, ZERO + 1);
 #pragma unroll
-  for (int k = 0; k < CPT; ++k) {
-    const int i = own_pos_c<NT, CPT>(k);
-    qp[k] = okp[k] ? T.post[i] : ZERO;
-    nex[k] = okp[k] ? T.tin[i] - i : 0;
-    const int pa = okp[k] ? T.ppos[i] : -1;
-    const int pf = okp[k] ? T.pflag[i] : 0;  // loaded with ppos, not after it
-    ppos[k] = pa >= 0 ? pa : ZERO;
-    pfl[k] = pa >= 0 ? pf : 0;
-    endm1[k] = okp[k] ? T.endpos[i] - 1 : ZERO;
+    for (int k = 0; k < CPT; ++k) {
+      nex[k] = okp[k] ? O.tin[k] - own_pos_c<NT, CPT>(k) : 0;
+      ppos[k] = tpa[k] >= 0 ? tpa[k] : ZERO;
+      pfl[k] = tpa[k] >= 0 ? tpf[k] : 0;
+      endm1[k] = tend[k] - 1;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int i = own_pos_c<NT, CPT>(k);
+      qp[k] = okp[k] ? T.post[i] : ZERO;
+      nex[k] = okp[k] ? T.tin[i] - i : 0;
+      const int pa = okp[k] ? T.ppos[i] : -1;
+      const int pf = okp[k] ? T.pflag[i] : 0;  // loaded with ppos, not after it
+      ppos[k] = pa >= 0 ? pa : ZERO;
+      pfl[k] = pa >= 0 ? pf : 0;
+      endm1[k] = okp[k] ? T.endpos[i] - 1 : ZERO;
+    }
   }
   // gradient buckets of every row this workgroup processes (static round-robin
   // assignment, so the summation order is fixed), starting from this
@@ -109,12 +129,20 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   constexpr bool BK_LDS = MAXS <= 2048;
   __shared__ float Bk[BK_LDS ? 8 * MAXS : 1];
   float cacc[BK_LDS ? 1 : 8][CPT];
-  float* const cr = P.contrib + (size_t)blockIdx.x * 8 * S;
+  // (slot rows are kb_slot_ld(S) floats apart, a multiple of four, so a
+  // thread's positions are one vector access)
+  const int SL = kb_slot_ld(S, 0);
+  float* const cr = P.contrib + (size_t)blockIdx.x * 8 * SL;
   float old[8][CPT];
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
+  for (int j = 0; j < 8; ++j) {
+    if constexpr (VEC) {
+      gld_own<CPT>(cr + (size_t)j * SL, S, old[j], 0.0f);
+    } else {
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) old[j][k] = okp[k] ? cr[(size_t)j * S + own_pos_c<NT, CPT>(k)] : 0.0f;
+      for (int k = 0; k < CPT; ++k) old[j][k] = okp[k] ? cr[(size_t)j * SL + own_pos_c<NT, CPT>(k)] : 0.0f;
+    }
+  }
   // Per-position constants, one [S] row shared by every row: for rows of up
   // to 2048 states, seven of them stay in LDS for the whole launch (own
   // positions, so each thread reads back only what it wrote), and the per-row
@@ -127,9 +155,14 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   float kx[CK_LDS ? K_N : 1][CPT];
   if constexpr (CK_LDS) {
 #pragma unroll
-    for (int j = 0; j < K_N; ++j)
+    for (int j = 0; j < K_N; ++j) {
+      if constexpr (VEC) {
+        gld_own<CPT>(kg[j], S, kx[j], 0.0f);
+      } else {
 #pragma unroll
-      for (int k = 0; k < CPT; ++k) kx[j][k] = okp[k] ? kg[j][own_pos_c<NT, CPT>(k)] : 0.0f;
+        for (int k = 0; k < CPT; ++k) kx[j][k] = okp[k] ? kg[j][own_pos_c<NT, CPT>(k)] : 0.0f;
+      }
+    }
   }
   // constant j at own position k (0 at padding positions)
   auto kc_own = [&](int j, float (&x)[CPT]) {
@@ -774,10 +807,18 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
 
   // this workgroup's slot holds the buckets carried through this level
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
+  for (int j = 0; j < 8; ++j) {
+    if constexpr (VEC) {
+      float x[CPT];
 #pragma unroll
-    for (int k = 0; k < CPT; ++k)
-      if (okp[k]) cr[(size_t)j * S + own_pos_c<NT, CPT>(k)] = bucket(j, k);
+      for (int k = 0; k < CPT; ++k) x[k] = bucket(j, k);
+      gst_own<CPT>(cr + (size_t)j * SL, S, x);
+    } else {
+#pragma unroll
+      for (int k = 0; k < CPT; ++k)
+        if (okp[k]) cr[(size_t)j * SL + own_pos_c<NT, CPT>(k)] = bucket(j, k);
+    }
+  }
 }
 
 #define KB_BWD_CASE(NT_, CPT_)                                                                      \

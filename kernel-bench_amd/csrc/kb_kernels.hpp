@@ -140,7 +140,7 @@ struct BwdParams {
   float* staging;             // [2 * n_splits, S]
   unsigned char* split_on;    // [n_splits]
   unsigned char* mask;        // [C]
-  float* contrib;             // [n_partials, 8, S] gradient buckets, one row per workgroup and level
+  float* contrib;             // [n_partials, 8, kb_slot_ld(S)] gradient buckets, one slot per workgroup
   const int* sched_rows;
   const int* row_kind;
   int class_mode;             // 1: entries are classes of identical rows (cls_ptr / cls_rows)
@@ -169,16 +169,21 @@ struct BwdParams {
 constexpr int KB_CHUNK0 = 8;
 // Workgroup slot of bwd_row_large_kernel: KB_LARGE_SLOT_ROWS rows of
 // kb_large_ld(S) floats (8 bucket rows, then the row's split term, Pi* and
-// Pibar*); other row kernels use 8 rows of S.
+// Pibar*); other row kernels use 8 rows of kb_slot_ld(S).
 constexpr int KB_LARGE_SLOT_ROWS = 11;
 // large = 1: rows of 2049..8192 states; large = 2: also rows of 1025..2048
 // states (512 threads x 4 positions)
-inline bool kb_use_large(int S, int large) {
+__host__ __device__ inline bool kb_use_large(int S, int large) {
   return (large && S > 2048 && S <= 8192) || (large == 2 && S > 1024 && S <= 2048);
 }
 // threads and positions (owner-major row length) of the low-register kernel's shape for S states
 __host__ __device__ inline int kb_large_nt(int S) { return S <= 2048 ? 512 : 1024; }
 __host__ __device__ inline int kb_large_ld(int S) { return S <= 2048 ? 2048 : (S <= 4096 ? 4096 : 8192); }
+// row stride (floats) of the workgroup bucket slots: kb_large_ld for the
+// low-register kernel, else S rounded up to a multiple of four (16-byte rows)
+__host__ __device__ inline int kb_slot_ld(int S, int large) {
+  return kb_use_large(S, large) ? kb_large_ld(S) : ((S + 3) & ~3);
+}
 
 struct EpiParams {
   TreeDev tr;

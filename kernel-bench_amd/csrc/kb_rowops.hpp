@@ -334,6 +334,65 @@ __device__ __forceinline__ int own_pos_c(int k) {
   return threadIdx.x * CPT + k;
 }
 
+// Own positions t*CPT .. t*CPT+CPT-1 of a global row p[0..n): one vector load
+// (16 bytes per four positions, 8 bytes for two) where all of them are below
+// n, else element by element with `fill` past n.  p must be 16-byte aligned
+// (every row these read starts its own allocation or a multiple of four
+// elements into one), so the vector accesses never cross the row's end.
+template <int CPT, typename T>
+__device__ __forceinline__ void gld_own(const T* p, int n, T (&v)[CPT], T fill) {
+  static_assert(sizeof(T) == 4, "32-bit elements");
+  const int b = threadIdx.x * CPT;
+  if (b + CPT <= n) {
+    if constexpr (CPT % 4 == 0) {
+#pragma unroll
+      for (int k = 0; k < CPT; k += 4) {
+        const int4 q = *reinterpret_cast<const int4*>(p + b + k);
+        v[k] = __builtin_bit_cast(T, q.x);
+        v[k + 1] = __builtin_bit_cast(T, q.y);
+        v[k + 2] = __builtin_bit_cast(T, q.z);
+        v[k + 3] = __builtin_bit_cast(T, q.w);
+      }
+    } else if constexpr (CPT % 2 == 0) {
+#pragma unroll
+      for (int k = 0; k < CPT; k += 2) {
+        const int2 q = *reinterpret_cast<const int2*>(p + b + k);
+        v[k] = __builtin_bit_cast(T, q.x);
+        v[k + 1] = __builtin_bit_cast(T, q.y);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) v[k] = p[b + k];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) v[k] = b + k < n ? p[b + k] : fill;
+  }
+}
+
+// The store counterpart of gld_own: positions at or past n are not written.
+template <int CPT>
+__device__ __forceinline__ void gst_own(float* p, int n, const float (&v)[CPT]) {
+  const int b = threadIdx.x * CPT;
+  if (b + CPT <= n) {
+    if constexpr (CPT % 4 == 0) {
+#pragma unroll
+      for (int k = 0; k < CPT; k += 4)
+        *reinterpret_cast<float4*>(p + b + k) = make_float4(v[k], v[k + 1], v[k + 2], v[k + 3]);
+    } else if constexpr (CPT % 2 == 0) {
+#pragma unroll
+      for (int k = 0; k < CPT; k += 2) *reinterpret_cast<float2*>(p + b + k) = make_float2(v[k], v[k + 1]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) p[b + k] = v[k];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k)
+      if (b + k < n) p[b + k] = v[k];
+  }
+}
+
 template <int CPT>
 __device__ __forceinline__ void lds_store_own(float* lds, const float (&v)[CPT]) {
   float* p = lds + threadIdx.x * CPT;
@@ -486,21 +545,38 @@ struct OwnTablesC {
   static constexpr int ZERO = NT * CPT;
   int col[CPT], c1p[CPT], c2p[CPT], tin[CPT];
   int ev[2 * CPT];
+  // VEC: one vector load per table (fewer memory instructions in flight, more
+  // registers live at once); else one load per position
+  template <bool VEC = false>
   __device__ __forceinline__ void load(const PreDev& T) {
+    if constexpr (VEC) {
+      int a[CPT], b[CPT];
+      gld_own<CPT>(T.col, T.S, col, -1);
+      gld_own<CPT>(T.c1pos, T.S, a, -1);
+      gld_own<CPT>(T.c2pos, T.S, b, -1);
+      gld_own<CPT>(T.tin, T.S, tin, 0);
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-      const int i = own_pos_c<NT, CPT>(k);
-      const bool ok = i < T.S;
-      col[k] = ok ? T.col[i] : -1;
-      const int a = ok ? T.c1pos[i] : -1, b = ok ? T.c2pos[i] : -1;
-      c1p[k] = a >= 0 ? a : ZERO;
-      c2p[k] = b >= 0 ? b : ZERO;
-      tin[k] = ok ? T.tin[i] : 0;
-    }
+      for (int k = 0; k < CPT; ++k) {
+        c1p[k] = a[k] >= 0 ? a[k] : ZERO;
+        c2p[k] = b[k] >= 0 ? b[k] : ZERO;
+      }
+      gld_own<2 * CPT>(T.euler, 2 * T.S, ev, ZERO << 1);
+    } else {
 #pragma unroll
-    for (int j = 0; j < 2 * CPT; ++j) {
-      const int q = threadIdx.x * (2 * CPT) + j;
-      ev[j] = q < 2 * T.S ? T.euler[q] : (ZERO << 1);
+      for (int k = 0; k < CPT; ++k) {
+        const int i = own_pos_c<NT, CPT>(k);
+        const bool ok = i < T.S;
+        col[k] = ok ? T.col[i] : -1;
+        const int a = ok ? T.c1pos[i] : -1, b = ok ? T.c2pos[i] : -1;
+        c1p[k] = a >= 0 ? a : ZERO;
+        c2p[k] = b >= 0 ? b : ZERO;
+        tin[k] = ok ? T.tin[i] : 0;
+      }
+#pragma unroll
+      for (int j = 0; j < 2 * CPT; ++j) {
+        const int q = threadIdx.x * (2 * CPT) + j;
+        ev[j] = q < 2 * T.S ? T.euler[q] : (ZERO << 1);
+      }
     }
   }
 };

@@ -607,6 +607,8 @@ def main():
                f"{roofs['transcendental']:.2f}" + (f", VALU active {valu:.2f} of wave cycles" if valu is not None
                                                    else "") + "); the time goes to barriers, LDS and memory latency")
     roofline = {
+        # the line's roofs are HBM or MFMA; the row kernels issue no MFMA, so the memory roof is the one
+        # quoted, and `limiter` says which of the measured roofs (HBM, transcendental, VALU issue) is nearest
         "bound": "hbm",
         "kernel": sym,
         "achieved": round(achieved, 3),

@@ -282,8 +282,11 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
   constexpr bool OMT = CPT == 8;
   int c2p[CPT], nex[CPT], qp[CPT], pre_s[CPT];
   bool h1[CPT];
-  {
-    // one vector load per table (the tables start their allocations)
+  // Below 1024 threads the tables and row constants are read with one vector
+  // load per row (they start their allocations); the 1024 x 2 shape keeps one
+  // load per position, which measured faster there.
+  constexpr bool VEC = NT < 1024;
+  if constexpr (VEC) {
     int a[CPT], tn[CPT];
     gld_own<CPT>(T.c1pos, S, a, -1);
     gld_own<CPT>(T.c2pos, S, c2p, -1);
@@ -298,6 +301,19 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
       const int sj = tid + k * NT;
       pre_s[k] = sj < S ? T.pre[sj] : 0;
     }
+  } else {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int i = own_pos_c<NT, CPT>(k);
+      const bool ok = i < S;
+      const int a = ok ? T.c1pos[i] : -1, b = ok ? T.c2pos[i] : -1;
+      h1[k] = a >= 0;
+      c2p[k] = b >= 0 ? b : ZERO;
+      nex[k] = ok ? T.tin[i] - i : 0;
+      qp[k] = ok ? T.post[i] : ZERO;
+      const int sj = tid + k * NT;
+      pre_s[k] = sj < S ? T.pre[sj] : 0;
+    }
   }
   const int c1last = h1[CPT - 1] ? own_pos_c<NT, CPT>(CPT - 1) + 1 : ZERO;
 
@@ -308,17 +324,33 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
   constexpr bool EARLY = CPT == 2;
   float kd[CPT], ks[CPT], ca[CPT], ce[CPT], ck1[CPT], ck2[CPT];
   auto load_lin = [&]() {
-    gld_own<CPT>(P.lin_a, S, ca, 0.0f);
-    gld_own<CPT>(P.lin_emc, S, ce, 0.0f);
-    gld_own<CPT>(P.lin_k1, S, ck1, 0.0f);
-    gld_own<CPT>(P.lin_k2, S, ck2, 0.0f);
+    if constexpr (VEC) {
+      gld_own<CPT>(P.lin_a, S, ca, 0.0f);
+      gld_own<CPT>(P.lin_emc, S, ce, 0.0f);
+      gld_own<CPT>(P.lin_k1, S, ck1, 0.0f);
+      gld_own<CPT>(P.lin_k2, S, ck2, 0.0f);
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) ck1[k] = h1[k] ? ck1[k] : 0.0f;  // 0 without child1: the x1 operand is then unused
+      for (int k = 0; k < CPT; ++k) ck1[k] = h1[k] ? ck1[k] : 0.0f;  // 0 without child1: the x1 operand is then unused
+    } else {
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        const int i = own_pos_c<NT, CPT>(k);
+        const bool ok = i < S;
+        ca[k] = ok ? P.lin_a[i] : 0.0f;
+        ce[k] = ok ? P.lin_emc[i] : 0.0f;
+        ck1[k] = h1[k] ? P.lin_k1[i] : 0.0f;  // 0 without child1: the x1 operand is then unused
+        ck2[k] = ok ? P.lin_k2[i] : 0.0f;
+      }
+    }
   };
   if constexpr (EARLY) {
     load_lin();
-    gld_own<CPT>(P.pD, S, kd, 0.0f);
-    gld_own<CPT>(P.pS, S, ks, 0.0f);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int i = own_pos_c<NT, CPT>(k);
+      kd[k] = i < S ? P.pD[i] : 0.0f;
+      ks[k] = i < S ? P.pS[i] : 0.0f;
+    }
   }
 
   // ---- initial row (log2), own positions
@@ -331,15 +363,6 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
     const int lend = T.endpos[lpos];
     leaf_obs = P.pS[lpos];
     const float leaf_col = WEIGHTED ? P.col[lpos] : 0.0f;
-    // the row constants at the own positions, one vector load per row
-    float kmt[CPT], kdl[CPT], keb[CPT], ke[CPT], ks1[CPT], ks2[CPT], kps[CPT];
-    gld_own<CPT>(P.mt, S, kmt, 0.0f);
-    gld_own<CPT>(P.DL, S, kdl, 0.0f);
-    gld_own<CPT>(P.Ebar, S, keb, 0.0f);
-    gld_own<CPT>(P.E, S, ke, 0.0f);
-    gld_own<CPT>(P.SL1, S, ks1, 0.0f);
-    gld_own<CPT>(P.SL2, S, ks2, 0.0f);
-    gld_own<CPT>(P.pS, S, kps, 0.0f);
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int i = own_pos_c<NT, CPT>(k);
@@ -347,16 +370,17 @@ __global__ __launch_bounds__(NT, FWD_MIN_WAVES(NT, CPT, WEIGHTED)) void fwd_row_
       if (i < S) {
         const bool hit = i == lpos;
         const bool desc = i >= lpos && i < lend;
+        const int ci = i;
         const float pi_w = hit ? leaf_obs : KB_NEG_INF;
-        const float pibar_w = desc ? KB_NEG_INF : kmt[k] + leaf_col + leaf_obs;
+        const float pibar_w = desc ? KB_NEG_INF : P.mt[ci] + leaf_col + leaf_obs;
         const float pi_s1 = (h1[k] && i + 1 == lpos) ? leaf_obs : KB_NEG_INF;
         const float pi_s2 = c2p[k] == lpos ? leaf_obs : KB_NEG_INF;  // padding ZERO never equals lpos
-        const float t0 = kdl[k] + pi_w;
-        const float t1 = pi_w + keb[k];
-        const float t2 = pibar_w + ke[k];
-        const float t3 = ks1[k] + pi_s1;
-        const float t4 = ks2[k] + pi_s2;
-        const float t5 = hit ? kps[k] : KB_NEG_INF;
+        const float t0 = P.DL[ci] + pi_w;
+        const float t1 = pi_w + P.Ebar[ci];
+        const float t2 = pibar_w + P.E[ci];
+        const float t3 = P.SL1[ci] + pi_s1;
+        const float t4 = P.SL2[ci] + pi_s2;
+        const float t5 = hit ? P.pS[ci] : KB_NEG_INF;
         const float m = fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, t5));
         const float ms = fsafe(m);
         const float sum = exp2_hw(t0 - ms) + exp2_hw(t1 - ms) + exp2_hw(t2 - ms) + exp2_hw(t3 - ms) +

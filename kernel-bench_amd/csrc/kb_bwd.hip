@@ -472,56 +472,25 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   }
 
   // ---- 4. J^T coefficients at Pi* (precompute kernel, wave_backward.py:264-416)
-  // p' = 2^(col + Pi* - rowmax) and its root-path sums ps(i) = Pre(i) -
-  // PostEx(tin(i) - i) (inclusive preorder scan, exclusive postorder scan;
-  // the postorder slots of position i's left context end at tin(i) - i).
-  // The preorder scan runs in registers; one barrier publishes Pi* (R0, for
-  // the child gathers), p' (R2, for the postorder gathers) and the wavefront
-  // totals, a second one the postorder scan (R3).  The row sum is the
-  // preorder total.
-  float pp[CPT], sp[CPT], ta = 0.0f;
+  // p' = 2^(col + Pi* - rowmax).  The Pibar coefficient's denominator,
+  // rowsum - pathsum(i) = the sum of p' over the non-ancestors of i (the
+  // reference's ancestor chase, wave_backward.py:364-389), is the row's own
+  // Pibar* in linear units: Pibar*_i = log2(sum_{j not anc(i)} 2^(col_j +
+  // Pi*_j)) + mt_i, written by the forward's last sweep from the same Pi*, so
+  // the sum is 2^(Pibar*_i - mt_i - rowmax) and needs no scan.  Pi* is in R0
+  // at preorder positions (the child gathers) since the row's staging, unless
+  // the split-term recompute restaged R0.
+  float pp[CPT], pmt[CPT];
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int i = own_pos_c<NT, CPT>(k);
     pp[k] = okp[k] ? exp2_hw((WEIGHTED ? P.col[i] : 0.0f) + piv[k] - rms) : 0.0f;
-    ta += pp[k];
-    sp[k] = ta;
+    pmt[k] = okp[k] ? P.mt[i] : 0.0f;
   }
   const int wv = tid >> 6, lane = tid & 63;
-  const float wa = wave_scan_incl(ta);
-  lds_store_own<CPT>(R0, piv);  // padding positions: -inf
-  lds_store_own<CPT>(R2, pp);
-  if (lane == 63) wA[wv] = wa;
-  __syncthreads();
-  float ps[CPT], rowsum;
-  {
-    constexpr int SEG = 64 * CPT;  // postorder slots per wavefront
-    const float tp = lds_wave_values<NW>(wA, lane, 0.0f);
-    float yq[CPT];
-#pragma unroll
-    for (int k = 0; k < CPT; ++k) yq[k] = R2[qp[k]];
-    const float ip = wave_scan_first<NW>(tp);
-    rowsum = lane_value(ip, NW - 1);
-    const float offp = lane_value(ip - tp, wv) + (wa - ta);
-    float sq[CPT], tb = 0.0f;
-#pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-      sq[k] = tb;
-      tb += yq[k];
-    }
-    const float wb = wave_scan_incl(tb);
-#pragma unroll
-    for (int k = 0; k < CPT; ++k) sq[k] += wb - tb;
-    lds_store_own<CPT>(R3, sq);
-    if (lane == 63) wB[wv] = wb;
+  if (!leaf_row && !P.dts_in) {
+    lds_store_own<CPT>(R0, piv);  // padding positions: -inf
     __syncthreads();
-    const float tq = lds_wave_values<NW>(wB, lane, 0.0f);
-    const float eq = wave_scan_first<NW>(tq) - tq;
-#pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-      const int n = nex[k];
-      ps[k] = (sp[k] + offp) - (R3[n] + __shfl(eq, n / SEG, 64));
-    }
   }
   const int lpos = cm ? (leaf_row ? T.pre[P.leaf_state[row]] : -1) : f_lpos;
   float q[6][CPT], pcoef[CPT];
@@ -539,7 +508,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     for (int j = 0; j < 6; ++j) q[j][k] = 0.0f;
     pcoef[k] = 0.0f;
     if (okp[k]) {
-      const float denom = rowsum - ps[k];
+      const float denom = exp2_hw(pbv[k] - pmt[k] - rms);
       const float inv_denom = denom > 0.0f ? rcp_hw(denom) : 0.0f;
       const bool h1 = O.c1p[k] != ZERO, h2 = O.c2p[k] != ZERO;
       const float t0 = kDL[k] + piv[k];
@@ -565,8 +534,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   // child-edge weights into position i from its parent: q3 if i is child1,
   // else q4.  The parent's owner scatters them into R1 (free since Pibar* was
   // read; every position has one parent, the root none), one barrier, and
-  // each thread reads its own positions.  The barrier also ends the reads of
-  // R2 / R3, which become the scan buffers.
+  // each thread reads its own positions.
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     if (O.c1p[k] != ZERO) R1[O.c1p[k]] = q[3][k];

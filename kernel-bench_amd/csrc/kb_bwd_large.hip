@@ -367,53 +367,24 @@ void bwd_row_large_kernel(BwdParams P, int first, int n_rows) {
 
     // ---- 4. J^T coefficients at Pi* (wave_backward.py:264-416)
     ep = rr * 16 + 4;
-    // p' = 2^(col + Pi* - rowmax) and its root-path sums ps(i) = Pre(i) -
-    // PostEx(tin(i) - i): inclusive preorder scan in registers, exclusive
-    // postorder scan through LDS (R3), two barriers.  Pi* goes to R0 for the
-    // child gathers, p' to R2 for the postorder gathers.
+    // p' = 2^(col + Pi* - rowmax).  The Pibar coefficient's denominator,
+    // rowsum - pathsum(i) = the sum of p' over the non-ancestors of i (the
+    // reference's ancestor chase, wave_backward.py:364-389), is the row's own
+    // Pibar* in linear units, 2^(Pibar*_i - mt_i - rowmax): the forward's last
+    // sweep wrote Pibar* from the same Pi*, so no scan is needed.  Pi* is in
+    // R0 at preorder positions (the child gathers) since the row's staging,
+    // unless the split term above restaged R0.
     float pp[CPT], pcoef[CPT];
-    float ta = 0.0f;
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int i = pos(k);
       pp[k] = i < S ? exp2_hw((WEIGHTED ? omf(OMC_COL, k) : 0.0f) + piv[k] - rms) : 0.0f;
-      ta += pp[k];
-      pcoef[k] = ta;  // the running preorder sum, until the coefficients below
+      const float denom = i < S ? exp2_hw(pbv[k] - omf(OMC_MT, k) - rms) : 0.0f;
+      pcoef[k] = denom > 0.0f ? rcp_hw(denom) : 0.0f;  // 1 / (rowsum - ps) for now
     }
-    const float wa = wave_scan_incl(ta);
-    lds_store_own<CPT>(R0, piv);  // padding positions: -inf
-    lds_store_own<CPT>(R2, pp);
-    if (lane == 63) wA[wv] = wa;
-    __syncthreads();
-    {
-      constexpr int SEG = 64 * CPT;  // postorder slots per wavefront
-      const float tp = lds_wave_values<NW>(wA, lane, 0.0f);
-      float sq[CPT], tb = 0.0f;
-#pragma unroll
-      for (int k = 0; k < CPT; ++k) {
-        const int i = pos(k);
-        sq[k] = tb;
-        tb += R2[i < S ? (omi(OMT_PN, k) & 0xffff) : ZERO];
-      }
-      const float ip = wave_scan_first<NW>(tp);
-      const float rowsum = lane_value(ip, NW - 1);
-      const float offp = lane_value(ip - tp, wv) + (wa - ta);
-      const float wb = wave_scan_incl(tb);
-#pragma unroll
-      for (int k = 0; k < CPT; ++k) sq[k] += wb - tb;
-      lds_store_own<CPT>(R3, sq);
-      if (lane == 63) wB[wv] = wb;
+    if (!leaf_row && !P.dts_in) {
+      lds_store_own<CPT>(R0, piv);  // padding positions: -inf
       __syncthreads();
-      const float tq = lds_wave_values<NW>(wB, lane, 0.0f);
-      const float eq = wave_scan_first<NW>(tq) - tq;
-#pragma unroll
-      for (int k = 0; k < CPT; ++k) {
-        const int i = pos(k);
-        const int n = i < S ? (omi(OMT_PN, k) >> 16) : 0;
-        const float ps = (pcoef[k] + offp) - (R3[n] + __shfl(eq, n / SEG, 64));
-        const float denom = rowsum - ps;
-        pcoef[k] = denom > 0.0f ? rcp_hw(denom) : 0.0f;  // 1 / (rowsum - ps) for now
-      }
     }
     // diag = q0 + q1, pcoef = q2 / (rowsum - ps); child-edge weights into
     // position i from its parent (q3 if i is child1, else q4) scattered by the

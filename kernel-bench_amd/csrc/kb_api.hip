@@ -857,7 +857,7 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   }
   const int64_t NS = p->n_splits;
   int rc = 0;
-  rc |= alloc(&p->b_staging, (size_t)std::max<int64_t>(1, 2 * NS) * S);
+  rc |= alloc(&p->b_staging, (size_t)std::max<int64_t>(1, 2 * NS) * kb::kb_stage_ld(S) + kb::KB_STAGE_TAIL);
   rc |= alloc(&p->b_split_on, (size_t)std::max<int64_t>(1, NS));
   rc |= alloc(&p->b_mask, (size_t)std::max(1, C));
   rc |= alloc(&p->b_rhs0, (size_t)std::max(1, C > 0 ? p->level_ptr[1] : 1) * S);

@@ -132,6 +132,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   // (slot rows are kb_slot_ld(S) floats apart, a multiple of four, so a
   // thread's positions are one vector access)
   const int SL = kb_slot_ld(S, 0);
+  const int SG = kb_stage_ld(S);  // child staging rows likewise
   float* const cr = P.contrib + (size_t)blockIdx.x * 8 * SL;
   float old[8][CPT];
 #pragma unroll
@@ -179,17 +180,25 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     else
       return cacc[j][k];
   };
-  // bucket j += x at the own positions (vector LDS read-modify-write)
-  auto bucket_add = [&](int j, const float (&x)[CPT]) {
+  // buckets j[0..3] += x[0..3] at the own positions (vector LDS
+  // read-modify-writes; the four reads are issued before the first write, so
+  // their latencies overlap instead of queueing behind each write)
+  auto bucket_add4 = [&](const int (&j)[4], const float (&x)[4][CPT]) {
     if constexpr (BK_LDS) {
-      float cur[CPT];
-      lds_load_own<CPT>(Bk + j * MAXS, cur);
+      float cur[4][CPT];
 #pragma unroll
-      for (int k = 0; k < CPT; ++k) cur[k] += x[k];
-      lds_store_own<CPT>(Bk + j * MAXS, cur);
+      for (int b = 0; b < 4; ++b) lds_load_own<CPT>(Bk + j[b] * MAXS, cur[b]);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) cur[b][k] += x[b][k];
+        lds_store_own<CPT>(Bk + j[b] * MAXS, cur[b]);
+      }
     } else {
 #pragma unroll
-      for (int k = 0; k < CPT; ++k) cacc[j][k] += x[k];
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) cacc[j[b]][k] += x[b][k];
     }
   };
 
@@ -241,9 +250,36 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int i = own_pos_c<NT, CPT>(k);
-      nst0[k] = (s0 >= 0 && okp[k]) ? P.staging[(size_t)s0 * S + i] : 0.0f;
-      nst1[k] = (s1 >= 0 && okp[k]) ? P.staging[(size_t)s1 * S + i] : 0.0f;
+      if constexpr (!VEC) {
+        nst0[k] = (s0 >= 0 && okp[k]) ? P.staging[(size_t)s0 * SG + i] : 0.0f;
+        nst1[k] = (s1 >= 0 && okp[k]) ? P.staging[(size_t)s1 * SG + i] : 0.0f;
+      }
       nds[k] = (dts && okp[k]) ? P.dts_in[db + i] : KB_NEG_INF;
+    }
+    if constexpr (VEC) {
+      // one unchecked vector load per row (the allocation's tail covers the
+      // positions past S, whose values are dropped where the rows are added;
+      // a side that does not exist reads row 0 and its flag is 0): a
+      // bounds-checked load would join into a register copy that waits here
+      // for every load just issued
+      static_assert(MAXS <= KB_STAGE_TAIL && CPT % 2 == 0, "staging tail, vector width");
+      auto ld_row = [&](const float* row, float (&v)[CPT]) {
+        if constexpr (CPT % 4 == 0) {
+#pragma unroll
+          for (int g = 0; g < CPT / 4; ++g) {
+            const float4 x = reinterpret_cast<const float4*>(row)[tid * (CPT / 4) + g];
+            v[4 * g] = x.x, v[4 * g + 1] = x.y, v[4 * g + 2] = x.z, v[4 * g + 3] = x.w;
+          }
+        } else {
+#pragma unroll
+          for (int g = 0; g < CPT / 2; ++g) {
+            const float2 x = reinterpret_cast<const float2*>(row)[tid * (CPT / 2) + g];
+            v[2 * g] = x.x, v[2 * g + 1] = x.y;
+          }
+        }
+      };
+      ld_row(P.staging + (size_t)max(s0, 0) * SG, nst0);
+      ld_row(P.staging + (size_t)max(s1, 0) * SG, nst1);
     }
   };
   int crec = 0, nrec = 0;  // records of the next two rows (AHEAD, below the class level)
@@ -320,18 +356,18 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   } else {
     if (__builtin_amdgcn_readlane(nfl, 0)) {
 #pragma unroll
-      for (int k = 0; k < CPT; ++k) rhs[k] += nst0[k];
+      for (int k = 0; k < CPT; ++k) rhs[k] += okp[k] ? nst0[k] : 0.0f;
     }
     if (__builtin_amdgcn_readlane(nfl, 1)) {
 #pragma unroll
-      for (int k = 0; k < CPT; ++k) rhs[k] += nst1[k];
+      for (int k = 0; k < CPT; ++k) rhs[k] += okp[k] ? nst1[k] : 0.0f;
     }
     if (f_s1 >= 0 && (f_s1 >> 30) != 0) {  // more than two child sides
       const int gb = P.child_ptr[row] + 2, ge = P.child_ptr[row + 1];
       for (int i = gb; i < ge; ++i) {
         const int side = P.child_in[i];
         if (!P.split_on[side >> 1]) continue;
-        const float* st = P.staging + (size_t)side * S;
+        const float* st = P.staging + (size_t)side * SG;
 #pragma unroll
         for (int k = 0; k < CPT; ++k)
           if (okp[k]) rhs[k] += st[own_pos_c<NT, CPT>(k)];
@@ -649,22 +685,22 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     local_scan_publish<NT, CPT>(sc, u, Pb, wt);
     __syncthreads();
     subtree_terms<NT, CPT>(sc, Pb, wt, endm1, wend, pm1, rest);
-    float x[8][CPT];
+    float x[2][4][CPT];  // buckets 0..3, 4..7
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const float aw0 = v[k] * q[0][k], aw1 = v[k] * q[1][k], aw2 = v[k] * q[2][k];
       const float aw3 = v[k] * q[3][k], aw4 = v[k] * q[4][k], aw5 = v[k] * q[5][k];
-      x[0][k] = aw0;
-      x[1][k] = aw3 + aw4 + aw5;
-      x[2][k] = aw0 + aw2;
-      x[3][k] = aw1;
-      x[4][k] = aw4;
-      x[5][k] = aw3;
-      x[6][k] = aw2;
-      x[7][k] = okp[k] ? pp[k] * (pm1[k] + rest[k]) : 0.0f;
+      x[0][0][k] = aw0;
+      x[0][1][k] = aw3 + aw4 + aw5;
+      x[0][2][k] = aw0 + aw2;
+      x[0][3][k] = aw1;
+      x[1][0][k] = aw4;
+      x[1][1][k] = aw3;
+      x[1][2][k] = aw2;
+      x[1][3][k] = okp[k] ? pp[k] * (pm1[k] + rest[k]) : 0.0f;
     }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) bucket_add(j, x[j]);
+    bucket_add4({0, 1, 2, 3}, x[0]);
+    bucket_add4({4, 5, 6, 7}, x[1]);
   }
 
   // ---- 7. split adjoints into the child rows (staging, preorder layout)
@@ -741,33 +777,39 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     __syncthreads();
     subtree_terms<NT, CPT>(scl, R2, wA, endm1, wend, pml, rsl);
     subtree_terms<NT, CPT>(scr, R3, wA + NW, endm1, wend, pmr, rsr);
-    float* stl = P.staging + (size_t)(2 * si) * S;
-    float* str = P.staging + (size_t)(2 * si + 1) * S;
-    float y[4][CPT];
+    float* stl = P.staging + (size_t)(2 * si) * SG;
+    float* str = P.staging + (size_t)(2 * si + 1) * SG;
+    float y[4][CPT], ysl[CPT], ysr[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const int i = own_pos_c<NT, CPT>(k);
-      y[0][k] = y[1][k] = y[2][k] = y[3][k] = 0.0f;
-      if (okp[k]) {
-        const float tl = ppl[k] * (pml[k] + rsl[k]);
-        const float tr = ppr[k] * (pmr[k] + rsr[k]);
-        const int pa = ppos[k];
-        const bool first = pfl[k] != 0;
-        const float sh3 = R0[pa], sh4 = R1[pa];  // padding slot holds 0
-        const float shl = first ? sh3 : sh4;
-        const float shr = first ? sh4 : sh3;
-        stl[i] = vd0[k] + vd1[k] + shl + tl;
-        str[i] = vd0[k] + vd2[k] + shr + tr;
-        y[0][k] = vd0[k];
-        y[1][k] = vd3[k] + vd4[k];
-        y[2][k] = vd1[k] + vd2[k];
-        y[3][k] = tl + tr;
-      }
+      // (padding positions: every operand below is 0 there, and so are the
+      // values; their parent slot ppos holds 0)
+      const float tl = ppl[k] * (pml[k] + rsl[k]);
+      const float tr = ppr[k] * (pmr[k] + rsr[k]);
+      const int pa = ppos[k];
+      const bool first = pfl[k] != 0;
+      const float sh3 = R0[pa], sh4 = R1[pa];  // padding slot holds 0
+      const float shl = first ? sh3 : sh4;
+      const float shr = first ? sh4 : sh3;
+      ysl[k] = okp[k] ? vd0[k] + vd1[k] + shl + tl : 0.0f;
+      ysr[k] = okp[k] ? vd0[k] + vd2[k] + shr + tr : 0.0f;
+      y[0][k] = vd0[k];
+      y[1][k] = vd3[k] + vd4[k];
+      y[2][k] = vd1[k] + vd2[k];
+      y[3][k] = okp[k] ? tl + tr : 0.0f;
     }
-    bucket_add(0, y[0]);
-    bucket_add(1, y[1]);
-    bucket_add(6, y[2]);
-    bucket_add(7, y[3]);
+    if constexpr (VEC) {
+      gst_own<CPT>(stl, S, ysl);
+      gst_own<CPT>(str, S, ysr);
+    } else {
+#pragma unroll
+      for (int k = 0; k < CPT; ++k)
+        if (okp[k]) {
+          stl[own_pos_c<NT, CPT>(k)] = ysl[k];
+          str[own_pos_c<NT, CPT>(k)] = ysr[k];
+        }
+    }
+    bucket_add4({0, 1, 6, 7}, y);
     if (tid == 0) P.split_on[si] = 1;
   }
 
@@ -841,7 +883,7 @@ __global__ __launch_bounds__(256) void bwd_gather0_kernel(BwdParams P) {
       for (int j = sb; j < se; ++j) {
         const int side = P.m_side[j];
         if (!P.split_on[side >> 1]) continue;  // uniform across the workgroup
-        const float* st = P.staging + (size_t)side * S;
+        const float* st = P.staging + (size_t)side * kb_stage_ld(S);
 #pragma unroll
         for (int e = 0; e < G0_E; ++e) {
           const int i = base + e * 256 + threadIdx.x;
@@ -922,7 +964,7 @@ __global__ __launch_bounds__(256) void bwd_chunk0_kernel(BwdParams P) {
     for (int j = P.m_side_ptr[mi]; j < P.m_side_ptr[mi + 1]; ++j) {
       const int side = P.m_side[j];
       const bool on = P.split_on[side >> 1] != 0;  // uniform across the workgroup
-      const float* st = P.staging + (size_t)side * S;
+      const float* st = P.staging + (size_t)side * kb_stage_ld(S);
 #pragma unroll
       for (int e = 0; e < G0_E; ++e) {
         const int i = e * 256 + tid;

@@ -226,8 +226,8 @@ void bwd_row_large_kernel(BwdParams P, int first, int n_rows) {
       const int s1 = f_s1 < 0 ? -1 : (f_s1 & ((1 << 30) - 1));
       const bool on0 = f_s0 >= 0 && P.split_on[f_s0 >> 1];
       const bool on1 = s1 >= 0 && P.split_on[s1 >> 1];
-      const float* st0 = P.staging + (size_t)(f_s0 >= 0 ? f_s0 : 0) * S;
-      const float* st1 = P.staging + (size_t)(s1 >= 0 ? s1 : 0) * S;
+      const float* st0 = P.staging + (size_t)(f_s0 >= 0 ? f_s0 : 0) * kb_stage_ld(S);
+      const float* st1 = P.staging + (size_t)(s1 >= 0 ? s1 : 0) * kb_stage_ld(S);
       float a0[CPT], a1[CPT];
 #pragma unroll
       for (int k = 0; k < CPT; ++k) {
@@ -245,7 +245,7 @@ void bwd_row_large_kernel(BwdParams P, int first, int n_rows) {
       for (int j = 0; j < n2; ++j) {
         const int side = P.child_in[P.child_ptr[row] + 2 + j];
         if (!P.split_on[side >> 1]) continue;
-        const float* st = P.staging + (size_t)side * S;
+        const float* st = P.staging + (size_t)side * kb_stage_ld(S);
 #pragma unroll
         for (int k = 0; k < CPT; ++k)
           if (pos(k) < S) rhs[k] += ldg(fresh(st, ep), pos(k));
@@ -640,8 +640,8 @@ void bwd_row_large_kernel(BwdParams P, int first, int n_rows) {
       const float p0l = wave_prev_lane(scl[CPT - 1]) + woffl;
       const float p0r = wave_prev_lane(scr[CPT - 1]) + woffr;
       ep = -4 * si - 3;
-      float* stl = P.staging + (size_t)(2 * si) * S;
-      float* str = P.staging + (size_t)(2 * si + 1) * S;
+      float* stl = P.staging + (size_t)(2 * si) * kb_stage_ld(S);
+      float* str = P.staging + (size_t)(2 * si + 1) * kb_stage_ld(S);
       int pkt[CPT];
       pk_now(pkt, ep);
 #pragma unroll

@@ -137,7 +137,7 @@ struct BwdParams {
   const int* split_ptr; const int* split_l; const int* split_r; const float* split_lsp;
   const int* child_ptr; const int* child_in;
   const int* bslot;           // [KB_BREC * C] record of every schedule slot (BrecField)
-  float* staging;             // [2 * n_splits, S]
+  float* staging;             // [2 * n_splits, kb_stage_ld(S)]
   unsigned char* split_on;    // [n_splits]
   unsigned char* mask;        // [C]
   float* contrib;             // [n_partials, 8, kb_slot_ld(S)] gradient buckets, one slot per workgroup
@@ -181,6 +181,12 @@ __host__ __device__ inline int kb_large_nt(int S) { return S <= 2048 ? 512 : 102
 __host__ __device__ inline int kb_large_ld(int S) { return S <= 2048 ? 2048 : (S <= 4096 ? 4096 : 8192); }
 // row stride (floats) of the workgroup bucket slots: kb_large_ld for the
 // low-register kernel, else S rounded up to a multiple of four (16-byte rows)
+// row stride (floats) of the backward's child staging rows: S rounded up to a
+// multiple of four, so rows start 16-byte aligned.  The allocation ends with
+// KB_STAGE_TAIL more floats, so a row kernel's vector read of its own positions
+// (up to 2048 from a row's start) stays inside it for every row.
+__host__ __device__ inline int kb_stage_ld(int S) { return (S + 3) & ~3; }
+constexpr int KB_STAGE_TAIL = 2048;
 __host__ __device__ inline int kb_slot_ld(int S, int large) {
   return kb_use_large(S, large) ? kb_large_ld(S) : ((S + 3) & ~3);
 }

@@ -5,6 +5,7 @@
 
 #include <algorithm>
 #include <array>
+#include <climits>
 #include <map>
 #include <cstdarg>
 #include <cstdio>
@@ -756,11 +757,16 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
     const char* w = getenv("KB_FWD_WIDE");
     F.wide = (w && (w[0] == '1' || w[0] == '2' || w[0] == '3')) ? w[0] - '0' : 0;
     // 512 x 4 keeps three rows per CU resident, 1024 x 2 two rows with a
-    // shorter per-row latency: the wider shape wins below ~6 rows per CU
+    // shorter per-row latency.  Measured per level on rows of 1025..2048
+    // states (config 3): the narrow shape wins on levels of less than one row
+    // per CU and on the leaf level (no split term; the last round of 512 x 4
+    // rows would run one row per CU), the 512 x 4 shape on the others (levels
+    // of 570..1428 rows: 4-6 us each).  Shorter rows keep the earlier rule,
+    // the narrow shape below six rows per CU.
     int dev = 0, n_cu = 0;
     KB_HIP(hipGetDevice(&dev));
     KB_HIP(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
-    F.narrow_below = 6 * n_cu;
+    F.narrow_below = S > 1024 ? n_cu : 6 * n_cu;
   }
   F.colw = p->c_colw;
   F.col = p->c_col;
@@ -797,7 +803,10 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
   p->fwd_pibar = io->pibar;
   for (int d = 0; d < p->n_levels; ++d) {
     if (p->prof) KB_HIP(hipEventRecord(p->ev_fwd[2 * d], st));
+    const int nb = F.narrow_below;
+    if (d == 0 && S > 1024) F.narrow_below = INT_MAX;  // the leaf level
     kb::launch_fwd_wave(F, p->f_level_ptr[d], p->f_level_ptr[d + 1] - p->f_level_ptr[d], st);
+    F.narrow_below = nb;
     if (p->prof) KB_HIP(hipEventRecord(p->ev_fwd[2 * d + 1], st));
   }
   KB_HIP(hipGetLastError());

@@ -55,7 +55,7 @@ struct FwdParams {
   PreDev pre;
   int S;
   int wide;                   // 1: 256 x 8, 2: 1024 x 2 on every level, 3: no narrow shape
-  int narrow_below;           // wide == 0: 1024 x 2 on levels with fewer rows than this
+  int narrow_below;           // wide == 0: 1024 x 2 on levels with fewer rows than this (and the leaf level)
   int n_sweeps;               // pi_iters - 1
   int use_col;
   // per-position constants: one [S] row in preorder, shared by every row

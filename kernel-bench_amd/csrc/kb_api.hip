@@ -827,9 +827,12 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   int dev = 0, n_cu = 0;
   KB_HIP(hipGetDevice(&dev));
   KB_HIP(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
-  // launch shape: 0 = 512 x 4 on levels with at least two rows per workgroup
-  // slot and 1024 x 2 (more, narrower threads: shorter per-row latency) on the
-  // smaller levels; KB_BWD_VARIANT=0 / 2 forces one shape everywhere
+  // launch shape: 1024 x 2 (more, narrower threads: four wavefronts per SIMD
+  // instead of two) on every level of rows of 1025..2048 states, where it
+  // measured faster on every level (config 3: 1.77 vs 1.96 ms); on shorter
+  // rows 512 x 4 on levels with at least two rows per workgroup slot and
+  // 1024 x 2 on the smaller ones; KB_BWD_VARIANT=0 / 2 forces one shape
+  // everywhere
   const char* vv = getenv("KB_BWD_VARIANT");
   const int variant = (vv && vv[0] == '2') ? 2 : (vv && vv[0] == '0') ? 0 : 1;
   // rows of 2049..8192 states: the low-register kernel (KB_BWD_LARGE=0: the
@@ -998,7 +1001,7 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
     const int n = d == 0 ? p->n_cls0 : p->level_ptr[d + 1] - p->level_ptr[d];
     B.class_mode = d == 0 ? 1 : 0;
     if (d == 0) kb::launch_bwd_level0_prep(B, p->level_ptr[1], p->n_cls0, st);
-    B.variant = p->b_variant == 1 ? (n < 2 * p->b_nb_max ? 2 : 0) : p->b_variant;
+    B.variant = p->b_variant == 1 ? ((S > 1024 || n < 2 * p->b_nb_max) ? 2 : 0) : p->b_variant;
     kb::launch_bwd_wave(B, p->level_ptr[d], n, std::min(n, p->b_nb_max), 0, st);
     if (p->prof) KB_HIP(hipEventRecord(p->ev_bwd[2 * d + 1], st));
   }

@@ -57,9 +57,9 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   const int tid = threadIdx.x;
   constexpr int ZERO = MAXS;
 
-  // The narrow 1024 x 2 shape runs the levels with about one row per
-  // workgroup: it fetches rows when needed instead of one row ahead (128
-  // VGPRs at 16 waves).
+  // The 1024 x 2 shape (rows of 1025..2048 states on every level, shorter
+  // rows on levels with about one row per workgroup) fetches rows when needed
+  // instead of one row ahead (128 VGPRs at 16 waves).
   constexpr bool AHEAD = NT < 1024;
   // the first split's child rows are prefetched into registers during the
   // Neumann loop, except where 1024 threads (128 VGPRs) own four or more

@@ -118,10 +118,42 @@ def _declare(lib):
     _native_ops.declare(lib)
 
 
+# Native handles (plans, trees) whose destruction waits for the end of a HIP
+# graph capture.  Destroying one frees device memory, and a free while a
+# capture is underway invalidates that capture; the garbage collector can drop
+# the last reference to a handle at any point, captures included.
+_held_back: list = []
+
+
+def _capture_underway() -> bool:
+    import torch
+
+    try:
+        return bool(torch.cuda.is_initialized() and torch.cuda.is_current_stream_capturing())
+    except Exception:  # pragma: no cover - interpreter shutdown order
+        return False
+
+
+def release(destroy: str, handle) -> None:
+    """Call the library's ``destroy`` entry point on ``handle`` now, or once no capture is underway."""
+    _held_back.append((destroy, handle))
+    if not _capture_underway():
+        release_held_back()
+
+
+def release_held_back() -> None:
+    """Destroy every handle held back by ``release`` (call outside graph captures)."""
+    while _held_back and _lib is not None:  # a handle exists only once the library is loaded
+        name, h = _held_back.pop()
+        getattr(_lib, name)(h)
+
+
 def lib():
     """Load (once) and return the HIP library; raise if it is unavailable."""
     global _lib, _load_error
     if _lib is not None:
+        if _held_back and not _capture_underway():
+            release_held_back()
         return _lib
     if not LIB_PATH.exists():
         raise NativeLibraryMissing(

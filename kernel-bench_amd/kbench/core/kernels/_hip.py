@@ -128,7 +128,7 @@ class _Tree:
     def __del__(self):  # pragma: no cover - interpreter shutdown order
         try:
             if self.handle:
-                N.lib().kb_tree_destroy(self.handle)
+                N.release("kb_tree_destroy", self.handle)  # held back while a graph capture is underway
         except Exception:
             pass
 

@@ -191,7 +191,7 @@ class FusedSolver:
 
     def close(self):
         if getattr(self, "_plan", None):
-            N.lib().kb_plan_destroy(self._plan)
+            N.release("kb_plan_destroy", self._plan)  # held back while a graph capture is underway
             self._plan = None
 
     def __del__(self):  # pragma: no cover - interpreter shutdown order

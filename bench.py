@@ -9,7 +9,10 @@ every row's sweeps, loss) plus backward (adjoint over every row, E adjoint,
 theta / column VJP), run through the native whole-pass driver with every
 input already in HBM.  Rows with identical inputs (row classes) are computed
 once in the forward; the line states how many rows that is and also times the
-solve with every row computed (``KB_DEDUP=0``).
+solve with every row computed (``KB_DEDUP=0``).  The backward stops each row's
+Neumann series at its first term whose entries are all at most 2^-24 of the
+row's largest right-hand-side entry (``FusedSolver.neumann_rtol``); ``neumann``
+gives the terms per row and times the same solve summing all 16 terms.
 
 Prints ONE JSON line.  ``value`` is ms per solve (fwd + bwd, HIP events),
 lower is better.
@@ -650,6 +653,22 @@ def main():
         dedup_off = {"ms": round(statistics.mean(t_all), 4), "fwd_ms": round(statistics.mean(f_all), 4),
                      "bwd_ms": round(statistics.mean(b_all), 4)}
         del flat
+    # ---- the Neumann series: terms per solved row at the solver's early stop, and the same solve
+    # with every term summed (the reference's series, neumann_rtol = 0)
+    _, saved_n = solver.run_forward(theta, cw)
+    terms = solver.run_backward(theta, cw, saved_n, return_info=True)[2]["neumann_terms"].cpu().numpy()
+    terms = terms[terms != 255]
+    neumann = {"neumann_terms": int(solver.so["neumann_terms"]), "rtol": solver.neumann_rtol,
+               "terms_mean": round(float(terms.mean()), 3), "terms_max": int(terms.max()),
+               "note": ("each row's series stops at its first term whose entries are all at most rtol times the "
+                        "row's largest right-hand-side entry (the term included); ms_full_series times the same "
+                        "solve summing every term")}
+    if not args.no_dedup_off:
+        full = FusedSolver(static, static.solver_options, neumann_rtol=0.0)
+        _timed_solves(full, theta, cw, 2)
+        t_all, f_all, b_all, _, _ = _timed_solves(full, theta, cw, max(3, args.steps // 2))
+        neumann.update(ms_full_series=round(statistics.mean(t_all), 4), bwd_ms_full_series=round(statistics.mean(b_all), 4))
+        del full
     per_call = None if args.no_per_call else per_call_timings(static, theta, cw, static_levels=static_levels)
     if per_call is not None:
         # the whole-pass solve against the pristine-structure proxy on the same GPU
@@ -676,7 +695,8 @@ def main():
         "config": {
             "workload": (f"config{args.config}: fwd+bwd solve, S={summ['S']} columns ({(summ['S'] + 1) // 2} "
                          f"leaves), C={summ['C']} rows, {summ['n_waves']} waves, {summ['n_splits']} splits, "
-                         f"per-species theta, pi_iters=16, neumann_terms=16; row classes: the forward computes "
+                         f"per-species theta, pi_iters=16, neumann_terms=16 (early stop at rtol {solver.neumann_rtol:.3g}, "
+                         f"{neumann['terms_mean']:.2f} terms per row on average); row classes: the forward computes "
                          f"{solver.n_forward_rows} of {summ['C']} rows (identical rows written from one "
                          f"computation), the backward solves {solver.n_backward_rows}"),
             "S_leaves": (summ["S"] + 1) // 2,
@@ -694,6 +714,7 @@ def main():
         "min_ms": round(min(tot), 4),
         "host_wall_ms_per_step": round(wall, 4),
         "dedup_off": dedup_off,
+        "neumann": neumann,
         "hbm_gbps_whole_solve": round(whole_bytes / (ms * 1e-3) / 1e9, 3),
         "e_step_iters": fstats["n_e_iter"],
         "bicgstab_iters": bstats["n_bicgstab"],

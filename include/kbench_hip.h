@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define KB_ABI_VERSION 3
+#define KB_ABI_VERSION 4
 
 #define KB_ERR_ARG (-1)    /* invalid argument / layout (reference raises ValueError) */
 #define KB_ERR_HIP (-2)    /* HIP runtime error (reference: RuntimeError) */
@@ -161,6 +161,14 @@ typedef struct kb_backward_io {
                                 pibar, or 0: with a token that is still current the
                                 split terms stored by that forward are reused instead
                                 of recomputed from pi / pibar */
+  double neumann_rtol;       /* 0: every row sums all neumann_terms terms (the
+                                reference's series).  > 0: a row's series stops at
+                                the first term n >= 1 whose every entry is at most
+                                neumann_rtol * max|adjoint of the row|; that term is
+                                included.  Not in the reference. */
+  uint8_t* neumann_terms_out; /* optional [C] out: J^T applications of every solved
+                                row (level-0 classes: at their first member);
+                                untouched for other rows */
 } kb_backward_io;
 
 int kb_backward(kb_plan* plan, const kb_backward_io* io, void* stream);

@@ -908,6 +908,8 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   if (!(io->bicgstab_tol > 0.0)) return set_error(KB_ERR_ARG, "tol must be positive");
   if (!(io->bicgstab_breakdown_tol > 0.0)) return set_error(KB_ERR_ARG, "breakdown_tol must be positive");
   if (io->pruning_threshold < 0.0) return set_error(KB_ERR_ARG, "adjoint_pruning_threshold must be non-negative");
+  if (!(io->neumann_rtol >= 0.0 && io->neumann_rtol < 1.0))
+    return set_error(KB_ERR_ARG, "neumann_rtol must be in [0, 1)");
   int rc = ensure_backward_work(p, io->use_col_weights);
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
@@ -941,6 +943,8 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   B.tr = p->tree();
   B.S = S;
   B.n_terms = io->neumann_terms;
+  B.rtol = (float)io->neumann_rtol;
+  B.terms_out = io->neumann_terms_out;
   B.thr = (float)io->pruning_threshold;
   B.use_pruning = io->use_pruning;
   B.use_col = io->use_col_weights;

@@ -32,6 +32,7 @@
 // and every per-row gradient bucket is stored and reduced over rows in a fixed
 // order, so results are bitwise reproducible.
 #include <algorithm>
+#include <type_traits>
 
 #include "kb_device.hpp"
 #include "kb_kernels.hpp"
@@ -39,13 +40,15 @@
 
 namespace kb {
 
-template <int NT, int CPT, bool WEIGHTED>
+// EARLY: the Neumann series may stop early (P.rtol > 0), a separate
+// instantiation so that the loop without it keeps its own code and registers
+template <int NT, int CPT, bool WEIGHTED, bool EARLY>
 __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int n_rows, int poff) {
   constexpr int MAXS = NT * CPT;
   constexpr int LD = MAXS + 64;  // [MAXS] is the padding slot, kept at 0
   constexpr int NW = NT / 64;
   __shared__ float L[4 * LD];
-  __shared__ float wA[2 * NW], wB[2 * NW];
+  __shared__ __align__(8) float wA[2 * NW], wB[2 * NW];
   __shared__ float wMk[NW];  // wavefront maxima of |adjoint| for the active mask
   float* R0 = L;
   float* R1 = L + LD;
@@ -377,7 +380,9 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   // rows below the roots: their adjoint is known here, so the wavefront maxima
   // for the active mask are published under the staging barrier below
   const bool mask_early = !P.class_mode && fam < 0;
-  if (mask_early) {
+  // (class rows publish them too when the Neumann series may stop early: its
+  // threshold is relative to the row's largest adjoint entry)
+  if (mask_early || (EARLY && P.class_mode)) {
     float am = 0.0f;
 #pragma unroll
     for (int k = 0; k < CPT; ++k) am = fmaxf(am, fabsf(rhs[k]));
@@ -398,6 +403,11 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     if (!okp[k]) piv[k] = pbv[k] = KB_NEG_INF;
+  }
+  float row_amax = 0.0f;  // max |adjoint| of the row
+  if (EARLY && P.class_mode) {
+#pragma unroll
+    for (int w = 0; w < NW; ++w) row_amax = fmaxf(row_amax, wMk[w]);
   }
   if (!P.class_mode) {
     if (fam >= 0) {
@@ -430,6 +440,7 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
     }
     any_active = P.use_pruning ? (amax >= P.thr) : (amax > P.thr);
     if (tid == 0) P.mask[row] = any_active ? 1 : 0;
+    row_amax = amax;
   }
   // row data of this row that is read after the next row's fetches
   const float rms = fsafe(cm ? P.rowmax[row] : lane_value(nrm, 0));
@@ -617,18 +628,40 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   // the previous lane, or the offset; P[end(i) - 1] and the parent's term are
   // read back.  Buffers alternate by parity, so the next term's writes never
   // race this term's reads.
+  //
+  // Stopping early (P.rtol > 0): the series ends at the first term n whose
+  // every entry is at most rtol * max|rhs| (the row's threshold tau); that
+  // term is already in v and J^T of it is not formed (a term n = 0 can pass
+  // only if rhs is zero).  Every adjoint entry has the sign of the root seeds
+  // (rhs <= 0, J^T and the split adjoints have nonnegative coefficients), so
+  // |v| >= |rhs| entrywise and the dropped remainder is below rtol of the
+  // row's largest adjoint entry times the tail's geometric factor.  Each
+  // wavefront publishes its vote with its scan total (wt[2w], wt[2w + 1]),
+  // under the term's barrier, and every thread reads all votes with the
+  // totals, so all take the same decision.  The loop without the early stop
+  // is a separate kernel instantiation, with the totals at wt[w].
   int wend[CPT];
 #pragma unroll
   for (int k = 0; k < CPT; ++k) wend[k] = endm1[k] < ZERO ? endm1[k] / (64 * CPT) : 0;
+  const float tau = P.rtol * row_amax;
   // term n uses the buffers of its parity; the loop runs the terms in pairs
-  // so that every LDS address is a register plus a constant
-  auto neumann_term = [&](float* Tb, float* Lb, float* wt) {
+  // so that every LDS address is a register plus a constant.  With the early
+  // stop (EARLY) a term returns true when the series stops at it.
+  auto neumann_term = [&](float* Tb, float* Lb, float* wt) -> bool {
     float sc[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) sc[k] = term[k] * pcoef[k] + (k > 0 ? sc[k - 1] : 0.0f);
     const float tsum = sc[CPT - 1];
     const float ws = wave_scan_incl(tsum);
-    if (lane == 63) wt[wv] = ws;
+    if constexpr (EARLY) {
+      bool small = true;
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) small = small && fabsf(term[k]) <= tau;
+      const float vote = __all(small) ? 1.0f : 0.0f;
+      if (lane == 63) reinterpret_cast<float2*>(wt)[wv] = make_float2(ws, vote);
+    } else {
+      if (lane == 63) wt[wv] = ws;
+    }
 #pragma unroll
     for (int k = 0; k < CPT; ++k) sc[k] += ws - tsum;  // wavefront-local inclusive scan
     lds_store_own<CPT>(Lb, sc);
@@ -640,7 +673,14 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       le[k] = Lb[endm1[k]];
       tpar[k] = Tb[ppos[k]];
     }
-    const float wtot = lane < NW ? wt[lane] : 0.0f;
+    float wtot;
+    if constexpr (EARLY) {
+      const float2 tv = lane < NW ? reinterpret_cast<const float2*>(wt)[lane] : make_float2(0.0f, 1.0f);
+      if (__all(tv.y != 0.0f)) return true;
+      wtot = tv.x;
+    } else {
+      wtot = lane < NW ? wt[lane] : 0.0f;
+    }
     const float wincl = wave_scan_first<NW>(wtot);
     const float wexcl = wincl - wtot;                 // lane x < NW: offset of wavefront x
     const float A = lane_value(wincl, NW - 1);
@@ -657,14 +697,29 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       term[k] = nt;
       v[k] += nt;
     }
+    return false;
   };
+  // calls: terms whose buffers were written (the stopping term included)
+  int calls = 0;
   {
-    int n = 0;
-    for (; n + 2 <= P.n_terms; n += 2) {
-      neumann_term(R0, R2, wA);
-      neumann_term(R1, R3, wB);
+    bool stopped = false;
+    for (; calls + 2 <= P.n_terms; calls += 2) {
+      if (neumann_term(R0, R2, wA)) {
+        calls += 1;
+        stopped = true;
+        break;
+      }
+      if (neumann_term(R1, R3, wB)) {
+        calls += 2;
+        stopped = true;
+        break;
+      }
     }
-    if (n < P.n_terms) neumann_term(R0, R2, wA);
+    if (!stopped && calls < P.n_terms) {
+      stopped = neumann_term(R0, R2, wA);
+      calls += 1;
+    }
+    if (P.terms_out && tid == 0) P.terms_out[row] = (unsigned char)min(stopped ? calls - 1 : calls, 255);
   }
 
   if (AHEAD && !cm) advance(rr);
@@ -676,9 +731,10 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
 
   // ---- 6. self-loop column gradient and parameter buckets
   {
-    const int n = P.n_terms;
-    float* Pb = (n & 1) ? R3 : R2;
-    float* wt = (n & 1) ? wB : wA;
+    // the buffers the last term did not write (its readers may still be
+    // reading its own)
+    float* Pb = (calls & 1) ? R3 : R2;
+    float* wt = (calls & 1) ? wB : wA;
     float u[CPT], sc[CPT], pm1[CPT], rest[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) u[k] = v[k] * pcoef[k];
@@ -831,13 +887,18 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   }
 }
 
-#define KB_BWD_CASE(NT_, CPT_)                                                                      \
-  if (S <= NT_ * CPT_) {                                                                            \
-    if (P.use_col)                                                                                  \
-      hipLaunchKernelGGL((bwd_row_kernel<NT_, CPT_, true>), dim3(nb), dim3(NT_), 0, st, P, first, W, poff);  \
-    else                                                                                            \
-      hipLaunchKernelGGL((bwd_row_kernel<NT_, CPT_, false>), dim3(nb), dim3(NT_), 0, st, P, first, W, poff); \
-    return;                                                                                         \
+#define KB_BWD_CASE(NT_, CPT_)                                                                        \
+  if (S <= NT_ * CPT_) {                                                                              \
+    const bool early = P.rtol > 0.0f;                                                                 \
+    if (P.use_col && early)                                                                           \
+      hipLaunchKernelGGL((bwd_row_kernel<NT_, CPT_, true, true>), dim3(nb), dim3(NT_), 0, st, P, first, W, poff);   \
+    else if (P.use_col)                                                                               \
+      hipLaunchKernelGGL((bwd_row_kernel<NT_, CPT_, true, false>), dim3(nb), dim3(NT_), 0, st, P, first, W, poff);  \
+    else if (early)                                                                                   \
+      hipLaunchKernelGGL((bwd_row_kernel<NT_, CPT_, false, true>), dim3(nb), dim3(NT_), 0, st, P, first, W, poff);  \
+    else                                                                                              \
+      hipLaunchKernelGGL((bwd_row_kernel<NT_, CPT_, false, false>), dim3(nb), dim3(NT_), 0, st, P, first, W, poff); \
+    return;                                                                                           \
   }
 
 // Level-0 rows, in two passes:
@@ -1095,9 +1156,9 @@ void launch_bwd_wave(const BwdParams& P, int first, int W, int nb, int poff, hip
   if (S <= NT_ * CPT_) {                                                                               \
     int n = 0;                                                                                         \
     if (use_col)                                                                                       \
-      (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, bwd_row_kernel<NT_, CPT_, true>, NT_, 0);  \
+      (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, bwd_row_kernel<NT_, CPT_, true, false>, NT_, 0);  \
     else                                                                                               \
-      (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, bwd_row_kernel<NT_, CPT_, false>, NT_, 0); \
+      (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, bwd_row_kernel<NT_, CPT_, false, false>, NT_, 0); \
     return n > 0 ? n : 1;                                                                              \
   }
 

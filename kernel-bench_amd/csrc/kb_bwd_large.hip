@@ -100,7 +100,8 @@ __device__ __forceinline__ void st4_add(float* p, float4 b, const float (&x)[4])
 // NT threads (1024, or 512 for rows of at most 2048 states) own CPT positions
 // each; at most 128 VGPRs, so 16 wavefronts per CU are resident (two
 // workgroups of 512).
-template <int NT, int CPT, bool WEIGHTED>
+// EARLY: the Neumann series may stop early (P.rtol > 0), as in bwd_row_kernel
+template <int NT, int CPT, bool WEIGHTED, bool EARLY>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4)))
 void bwd_row_large_kernel(BwdParams P, int first, int n_rows) {
   constexpr int MAXS = NT * CPT;
@@ -217,6 +218,7 @@ void bwd_row_large_kernel(BwdParams P, int first, int n_rows) {
         if (pos(k) < S) dts[k] = ldg(fresh(src, ep), pos(k));
     }
     bool any_active = false;
+    float row_amax = 0.0f;  // max |adjoint| of the row
     if (cm) {
       any_active = P.cls_active[rr] != 0;
       const float* src = P.rhsc + (size_t)rr * S;
@@ -252,7 +254,9 @@ void bwd_row_large_kernel(BwdParams P, int first, int n_rows) {
       }
     }
     const bool mask_early = !cm && fam < 0;
-    if (mask_early) {
+    // (class rows publish them too when the Neumann series may stop early: its
+    // threshold is relative to the row's largest adjoint entry)
+    if (mask_early || (EARLY && cm)) {
       float am = 0.0f;
 #pragma unroll
       for (int k = 0; k < CPT; ++k) am = fmaxf(am, fabsf(rhs[k]));
@@ -271,6 +275,10 @@ void bwd_row_large_kernel(BwdParams P, int first, int n_rows) {
 #pragma unroll
     for (int k = 0; k < CPT; ++k)
       if (pos(k) >= S) piv[k] = KB_NEG_INF;
+    if (EARLY && cm) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w) row_amax = fmaxf(row_amax, wMk[w]);
+    }
     if (!cm) {
       if (fam >= 0) {
         // logsumexp2 (logspace.py:11-16) and _safe_exp2_ratio (_implicit_grad.py:21-25)
@@ -302,6 +310,7 @@ void bwd_row_large_kernel(BwdParams P, int first, int n_rows) {
       }
       any_active = P.use_pruning ? (amax >= P.thr) : (amax > P.thr);
       if (tid == 0) P.mask[row] = any_active ? 1 : 0;
+      row_amax = amax;
     }
     if (!any_active) {
       for (int i = sb + tid; i < se; i += NT) P.split_on[i] = 0;
@@ -432,15 +441,18 @@ void bwd_row_large_kernel(BwdParams P, int first, int n_rows) {
     auto wend_of = [](int x) { return (x >> (16 + SEGSH)) & (NW - 1); };  // ZERO -> wavefront 0
 
     // ---- 5. Neumann series v = sum_{n<=N} (J^T)^n rhs with the row on chip:
-    // one barrier per term, buffers alternating by parity (as in
-    // bwd_row_kernel)
+    // one barrier per term, buffers alternating by parity, and with EARLY the
+    // same early stop as bwd_row_kernel (the series ends at the first term
+    // with every entry at most rtol * max|rhs|; the wavefronts' votes travel
+    // with their scan totals, in wt[NW + w])
     float v[CPT], term[CPT];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       v[k] = rhs[k];
       term[k] = rhs[k];
     }
-    auto neumann_term = [&](float* Tb, float* Lb, float* wt, int n_term) {
+    const float tau = P.rtol * row_amax;
+    auto neumann_term = [&](float* Tb, float* Lb, float* wt, int n_term) -> bool {
       // the LDS addresses come from the packed tables in every term: held
       // across the loop they would take 3 x CPT registers
       int pkt[CPT];
@@ -451,11 +463,22 @@ void bwd_row_large_kernel(BwdParams P, int first, int n_rows) {
       const float tsum = sc[CPT - 1];
       const float ws = wave_scan_incl(tsum);
       if (lane == 63) wt[wv] = ws;
+      if constexpr (EARLY) {
+        bool small = true;
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) small = small && fabsf(term[k]) <= tau;
+        const bool all_small = __all(small);
+        if (lane == 63) wt[NW + wv] = all_small ? 1.0f : 0.0f;
+      }
 #pragma unroll
       for (int k = 0; k < CPT; ++k) sc[k] += ws - tsum;
       lds_store_own<CPT>(Lb, sc);
       lds_store_own<CPT>(Tb, term);
       __syncthreads();
+      if constexpr (EARLY) {
+        const float f = lane < NW ? wt[NW + lane] : 1.0f;
+        if (__all(f != 0.0f)) return true;
+      }
       float le[CPT], tpar[CPT];
 #pragma unroll
       for (int k = 0; k < CPT; ++k) {
@@ -473,14 +496,29 @@ void bwd_row_large_kernel(BwdParams P, int first, int n_rows) {
         term[k] = nt;
         v[k] += nt;
       }
+      return false;
     };
+    // calls: terms whose buffers were written (the stopping term included)
+    int calls = 0;
     {
-      int n = 0;
-      for (; n + 2 <= P.n_terms; n += 2) {
-        neumann_term(R0, R2, wA, n);
-        neumann_term(R1, R3, wB, n + 1);
+      bool stopped = false;
+      for (; calls + 2 <= P.n_terms; calls += 2) {
+        if (neumann_term(R0, R2, wA, calls)) {
+          calls += 1;
+          stopped = true;
+          break;
+        }
+        if (neumann_term(R1, R3, wB, calls + 1)) {
+          calls += 2;
+          stopped = true;
+          break;
+        }
       }
-      if (n < P.n_terms) neumann_term(R0, R2, wA, n);
+      if (!stopped && calls < P.n_terms) {
+        stopped = neumann_term(R0, R2, wA, calls);
+        calls += 1;
+      }
+      if (P.terms_out && tid == 0) P.terms_out[row] = (unsigned char)min(stopped ? calls - 1 : calls, 255);
     }
 
     ep = rr * 16 + 6;
@@ -489,10 +527,11 @@ void bwd_row_large_kernel(BwdParams P, int first, int n_rows) {
     // recomputed coefficients' child gathers, the scan of u = v * pcoef to its
     // Lb buffer.
     {
-      const int n = P.n_terms;
-      float* Pt = (n & 1) ? R1 : R0;
-      float* Pb = (n & 1) ? R3 : R2;
-      float* wt = (n & 1) ? wB : wA;
+      // the buffers the last term did not write (its readers may still be
+      // reading its own)
+      float* Pt = (calls & 1) ? R1 : R0;
+      float* Pb = (calls & 1) ? R3 : R2;
+      float* wt = (calls & 1) ? wB : wA;
       {
         float x[CPT];
         vld<CPT>(srow(SL_PI), x);
@@ -677,13 +716,18 @@ void bwd_row_large_kernel(BwdParams P, int first, int n_rows) {
   }  // rows
 }
 
-#define KB_BWD_LARGE_CASE(NT_, CPT_)                                                                        \
-  if (S <= NT_ * CPT_) {                                                                                    \
-    if (P.use_col)                                                                                          \
-      hipLaunchKernelGGL((bwd_row_large_kernel<NT_, CPT_, true>), dim3(nb), dim3(NT_), 0, st, P, first, W); \
-    else                                                                                                    \
-      hipLaunchKernelGGL((bwd_row_large_kernel<NT_, CPT_, false>), dim3(nb), dim3(NT_), 0, st, P, first, W);\
-    return true;                                                                                            \
+#define KB_BWD_LARGE_CASE(NT_, CPT_)                                                                           \
+  if (S <= NT_ * CPT_) {                                                                                       \
+    const bool early = P.rtol > 0.0f;                                                                          \
+    if (P.use_col && early)                                                                                    \
+      hipLaunchKernelGGL((bwd_row_large_kernel<NT_, CPT_, true, true>), dim3(nb), dim3(NT_), 0, st, P, first, W);   \
+    else if (P.use_col)                                                                                        \
+      hipLaunchKernelGGL((bwd_row_large_kernel<NT_, CPT_, true, false>), dim3(nb), dim3(NT_), 0, st, P, first, W);  \
+    else if (early)                                                                                            \
+      hipLaunchKernelGGL((bwd_row_large_kernel<NT_, CPT_, false, true>), dim3(nb), dim3(NT_), 0, st, P, first, W);  \
+    else                                                                                                       \
+      hipLaunchKernelGGL((bwd_row_large_kernel<NT_, CPT_, false, false>), dim3(nb), dim3(NT_), 0, st, P, first, W); \
+    return true;                                                                                               \
   }
 
 bool launch_bwd_large(const BwdParams& P, int first, int W, int nb, hipStream_t st) {
@@ -702,11 +746,11 @@ int bwd_large_blocks_per_cu(int S, int use_col) {
   int n = 0;
   auto occ = [&](auto kernel, int nt) { (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, nt, 0); };
   if (kb_large_nt(S) == 512)
-    use_col ? occ(bwd_row_large_kernel<512, 4, true>, 512) : occ(bwd_row_large_kernel<512, 4, false>, 512);
+    use_col ? occ(bwd_row_large_kernel<512, 4, true, false>, 512) : occ(bwd_row_large_kernel<512, 4, false, false>, 512);
   else if (S <= 4096)
-    use_col ? occ(bwd_row_large_kernel<1024, 4, true>, 1024) : occ(bwd_row_large_kernel<1024, 4, false>, 1024);
+    use_col ? occ(bwd_row_large_kernel<1024, 4, true, false>, 1024) : occ(bwd_row_large_kernel<1024, 4, false, false>, 1024);
   else
-    use_col ? occ(bwd_row_large_kernel<1024, 8, true>, 1024) : occ(bwd_row_large_kernel<1024, 8, false>, 1024);
+    use_col ? occ(bwd_row_large_kernel<1024, 8, true, false>, 1024) : occ(bwd_row_large_kernel<1024, 8, false, false>, 1024);
   return n > 0 ? n : 1;
 }
 

@@ -125,6 +125,8 @@ struct BwdParams {
   PreDev pre;
   int S;
   int n_terms;                // neumann_terms
+  float rtol;                 // > 0: the series stops at the first term below rtol * max|rhs| (0: all terms)
+  unsigned char* terms_out;   // optional [C]: J^T applications of each solved row
   float thr;                  // adjoint_pruning_threshold
   int use_pruning;
   int use_col;

@@ -12,7 +12,7 @@ import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libkbench_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lib = None
 _load_error: str | None = None
@@ -71,6 +71,7 @@ class KbBackwardIO(ct.Structure):
         ("pi", vp), ("pibar", vp), ("pibar_row_max", vp),
         ("grad_theta", vp), ("grad_col", vp),
         ("active_mask", vp), ("acc_out", vp), ("forward_token", i64),
+        ("neumann_rtol", f64), ("neumann_terms_out", vp),
     ]
 
 

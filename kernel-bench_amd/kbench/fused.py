@@ -20,6 +20,7 @@ It computes what the reference's frozen glue computes
 from __future__ import annotations
 
 import ctypes as ct
+import os
 import weakref
 from types import SimpleNamespace
 
@@ -27,6 +28,15 @@ import numpy as np
 import torch
 
 from . import _native as N
+
+# Default early-stop tolerance of the backward's Neumann series: 2^-24,
+# float32's unit roundoff, relative to the row's largest right-hand-side entry.
+# Every adjoint entry has one sign and the terms decay geometrically (by about
+# 5-10x per term at config 3), so the dropped remainder is of that order
+# relative to the row's adjoints: gradients move by about 1e-7 relative, the
+# size of float32 rounding of the sums, while a row needs about half of its
+# 16 terms.
+DEFAULT_NEUMANN_RTOL = 2.0 ** -24
 
 FORWARD_SAVED_NAMES = (
     "E", "E_s1", "E_s2", "Ebar", "root_rows", "pi_wave", "pibar_wave",
@@ -153,8 +163,16 @@ def kb_layout(arrays: dict) -> "N.KbLayout":
 class FusedSolver:
     """Native whole-pass solver bound to one static layout and one device."""
 
-    def __init__(self, static, solver_options=None, device=None):
+    def __init__(self, static, solver_options=None, device=None, *, neumann_rtol=None):
         self.statewise = bool(_get(static, "statewise"))
+        # the Neumann series' early stop (``kb_backward_io.neumann_rtol``): a row's series
+        # ends at its first term whose entries are all at most this fraction of the row's
+        # largest adjoint entry; 0 sums every ``neumann_terms`` term, as the reference does
+        if neumann_rtol is None:
+            neumann_rtol = float(os.environ.get("KB_NEUMANN_RTOL", DEFAULT_NEUMANN_RTOL))
+        if not 0.0 <= float(neumann_rtol) < 1.0:
+            raise ValueError("neumann_rtol must be in [0, 1)")
+        self.neumann_rtol = float(neumann_rtol)
         self.itemwise = bool(_get(static, "itemwise"))
         if self.itemwise:
             raise NotImplementedError("the fused driver covers item_rows == 1 (itemwise=False)")
@@ -331,6 +349,7 @@ class FusedSolver:
         grad_col = torch.empty((S,), **f32)
         mask = torch.empty((C,), device=dev, dtype=torch.uint8)
         acc = torch.empty((8, S), device=dev, dtype=torch.float64) if return_info else None
+        terms = torch.full((C,), 255, device=dev, dtype=torch.uint8) if return_info else None
         c = lambda name: saved[name].detach().to(device=dev, dtype=torch.float32).contiguous()
         tens = {k: c(k) for k in ("E", "E_s1", "E_s2", "Ebar", "log_pS", "log_pD", "log_pL", "max_coupling",
                                   "col_log_probs", "pi_wave", "pibar_wave", "pibar_row_max")}
@@ -344,6 +363,7 @@ class FusedSolver:
             max_coupling=N.ptr(tens["max_coupling"]), col_log_probs=N.ptr(tens["col_log_probs"]),
             pi=N.ptr(tens["pi_wave"]), pibar=N.ptr(tens["pibar_wave"]), pibar_row_max=N.ptr(tens["pibar_row_max"]),
             grad_theta=N.ptr(grad_theta), grad_col=N.ptr(grad_col), active_mask=N.ptr(mask), acc_out=N.ptr(acc),
+            neumann_rtol=self.neumann_rtol, neumann_terms_out=N.ptr(terms),
         )
         token = 0
         last = self._last_forward
@@ -356,7 +376,8 @@ class FusedSolver:
             if check_solve:
                 self.backward_stats()
         if return_info:
-            return grad_theta, grad_col, {"active_mask": mask, "acc": acc}
+            # neumann_terms: J^T applications of every solved row (255: not solved here)
+            return grad_theta, grad_col, {"active_mask": mask, "acc": acc, "neumann_terms": terms}
         return grad_theta, grad_col
 
     def e_adjoint(self, saved, acc, *, q_extra=None, with_norm=False, use_col_weights=False, check_solve=True):

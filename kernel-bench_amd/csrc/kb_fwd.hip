@@ -20,19 +20,20 @@
 // k2 = 2^SL2 prepared once per solve.  NA(x)[s] = rowsum - pathsum(s) as in
 // the reference; the path sums come from an Euler-tour prefix scan.
 // Two layouts of the sweep loop:
-//  * fwd_row_kernel (rows of up to 4096 positions): ONE barrier per sweep.
-//    Thread t owns preorder positions t*CPT+k and postorder slots t*CPT+k.  The
-//    path sum is  ps(i) = Pre(i) - PostEx(tin(i) - i),  Pre the inclusive
-//    preorder prefix sum and PostEx the exclusive postorder prefix sum (the
-//    nodes left before entering i, tin(i) - i of them, are the first ones in
-//    postorder).  Each thread updates its preorder positions AND the nodes of
-//    its postorder slots (same arithmetic on the same published values, so both
-//    copies are identical), scans both in registers, and publishes y, the two
-//    wavefront-local scans and the wavefront totals under one barrier; the
-//    wavefront offsets are applied by the readers.  Three double-buffered LDS
-//    rows.
-//  * fwd_row_kernel_euler (larger rows): wavefront-segment ownership and an
-//    Euler-tour scan, three barriers per sweep, half the LDS.
+//  * fwd_row_kernel (rows of up to 8192 positions; 8 per thread with the
+//    owner-major tables): two barriers per sweep.  Thread t owns preorder
+//    positions t*CPT+k and postorder slots t*CPT+k.  The path sum is
+//    ps(i) = Pre(i) - PostEx(tin(i) - i),  Pre the inclusive preorder prefix
+//    sum and PostEx the exclusive postorder prefix sum (the nodes left before
+//    entering i, tin(i) - i of them, are the first ones in postorder).  Phase
+//    A scans the own positions in registers and publishes y and the
+//    wavefront totals; after the first barrier each thread reads the values
+//    of its postorder slots and scans them (phase B), published under the
+//    second barrier; phase C forms the path sums, the wavefront offsets being
+//    applied by the readers.
+//  * fwd_row_kernel_euler (rows past 4096 positions without the owner-major
+//    tables): wavefront-segment ownership and an Euler-tour scan, three
+//    barriers per sweep, half the LDS.
 #include "kb_device.hpp"
 #include "kb_kernels.hpp"
 #include "kb_rowops.hpp"

@@ -285,6 +285,21 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
       ld_row(P.staging + (size_t)max(s1, 0) * SG, nst1);
     }
   };
+  // The 1024 x 2 shape reads its rows' records from LDS: RCH of them at a
+  // time, one int per thread (KB_BREC fields of RCH rows), the first chunk
+  // with the set-up loads; a row then waits for one memory round trip (its
+  // data) instead of two (its record, then its data).
+  constexpr int RCH = 1024 / KB_BREC;
+  __shared__ int Rec[AHEAD ? 1 : RCH * KB_BREC];
+  auto load_chunk = [&](int rr2) {
+    if constexpr (!AHEAD) {
+      static_assert(NT == RCH * KB_BREC, "one record field per thread");
+      const int r2 = rr2 + (tid / KB_BREC) * (int)gridDim.x;
+      Rec[tid] = r2 < n_rows ? P.bslot[(size_t)KB_BREC * (first + r2) + (tid & (KB_BREC - 1))] : 0;
+    }
+  };
+  if (!AHEAD && !P.class_mode) load_chunk(blockIdx.x);
+  int ci = 0;  // (1024 x 2) this row's entry in the chunk
   int crec = 0, nrec = 0;  // records of the next two rows (AHEAD, below the class level)
   if (AHEAD && (int)blockIdx.x < n_rows) {
     if (P.class_mode) {
@@ -324,7 +339,17 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   for (int rr = blockIdx.x; rr < n_rows; rr += gridDim.x) {
   __syncthreads();  // LDS of the previous row is no longer read
   const int cm = P.class_mode;
-  const int rec = cm ? 0 : (AHEAD ? crec : load_rec(rr));
+  int rec = 0;
+  if constexpr (AHEAD) {
+    rec = cm ? 0 : crec;
+  } else if (!cm) {
+    if (ci == 0 && rr != (int)blockIdx.x) {  // uniform: the next chunk
+      load_chunk(rr);
+      __syncthreads();
+    }
+    rec = Rec[ci * KB_BREC + (tid & (KB_BREC - 1))];
+    ci = (ci + 1) & (RCH - 1);
+  }
   // every field read here, at a uniform point
   const int f_row = field(rec, BR_ROW), f_leaf = field(rec, BR_LEAF), f_sb = field(rec, BR_SB);
   const int f_se = field(rec, BR_SE), f_fam = field(rec, BR_FAM), f_s1 = field(rec, BR_S1);

@@ -839,7 +839,11 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   // general row kernel; =2: also rows of 1025..2048 states)
   const char* lv = getenv("KB_BWD_LARGE");
   const int large = (lv && lv[0] == '0') ? 0 : (lv && lv[0] == '2') ? 2 : 1;
-  const int nb_max = std::max(1, n_cu * kb::bwd_blocks_per_cu(S, use_col, variant, large));
+  int nb_max = std::max(1, n_cu * kb::bwd_blocks_per_cu(S, use_col, variant, large));
+  // KB_BWD_GRID=n caps the persistent grid at n workgroups (tests: every
+  // workgroup then walks many rows of a level)
+  const char* gv = getenv("KB_BWD_GRID");
+  if (gv && atoi(gv) > 0) nb_max = std::min(nb_max, atoi(gv));
   p->b_variant = variant;
   p->b_large = large;
   // owner-major constants of the low-register kernel (allocated once, when it first runs)

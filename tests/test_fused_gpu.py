@@ -335,3 +335,44 @@ def test_plan_rejects_leaf_rows_without_a_valid_state(bad):
     static = make_static(cap, "cuda")
     with pytest.raises(ValueError, match="leaf state"):
         FusedSolver(static, static.solver_options)
+
+
+@pytest.mark.parametrize("leaves,weighted", [(1024, True), (2048, False)])
+def test_backward_on_a_one_workgroup_grid_matches_oracle(leaves, weighted, monkeypatch):
+    """KB_BWD_GRID=1: one persistent workgroup walks every row of each level, so the 1024 x 2
+    kernel reloads its LDS chunk of 64 row records and the large-row kernel (S = 4095) keeps one
+    bucket slot for a whole level.  Gradients against the oracle and the default grid."""
+    import kbench_oracle as O
+    from kbench.fused import FusedSolver, problem_to_captured
+    from kbench.runtime import make_static
+
+    print(f"[fused-grid1] leaves={leaves} weighted={weighted}", flush=True)
+    p = _big_tree_problem(leaves, 16 if leaves == 1024 else 12, True)  # level 1: 130 / 123 rows
+    cap = problem_to_captured(p)
+    static = make_static(cap, "cuda")
+    theta = cap["inputs"]["theta"].cuda()
+    n = int(cap["inputs"]["col_weights"].numel())
+    cw32 = (np.random.default_rng(11).normal(0.0, 0.5, size=n) if weighted else np.zeros(n)).astype(np.float32)
+    cw = torch.from_numpy(cw32).cuda()
+    ref = FusedSolver(static, static.solver_options)
+    _, saved = ref.run_forward(theta, cw)
+    gt0, gc0 = ref.run_backward(theta, cw, saved)
+    monkeypatch.setenv("KB_BWD_GRID", "1")
+    one = FusedSolver(static, static.solver_options)
+    level_rows = one.level_shapes()[0][1:]
+    _, saved1 = one.run_forward(theta, cw)
+    gt1, gc1 = one.run_backward(theta, cw, saved1)
+    torch.cuda.synchronize()
+    prob = O.Problem.from_dict(p)
+    th = np.asarray(p["inputs"]["theta"], dtype=np.float32).astype(np.float64)
+    _, osv = O.forward(prob, th, cw32.astype(np.float64))
+    ogt, ogc, _ = O.backward(prob, th, cw32.astype(np.float64), osv)
+    rt = kbtest.norm_rel(gt1.cpu().numpy(), ogt)
+    rc = kbtest.norm_rel(gc1.cpu().numpy(), ogc)
+    dt = kbtest.norm_rel(gt1.cpu().numpy(), gt0.cpu().numpy())
+    dc = kbtest.norm_rel(gc1.cpu().numpy(), gc0.cpu().numpy())
+    print(f"  rows per split level (max) {int(level_rows.max())}; vs oracle theta={rt:.2e} col={rc:.2e}; "
+          f"vs default grid theta={dt:.2e} col={dc:.2e}")
+    assert int(level_rows.max()) > 64
+    assert rt <= 1e-4 and rc <= 1e-4
+    assert dt <= 1e-5 and dc <= 1e-5

@@ -15,7 +15,11 @@ row's largest right-hand-side entry (``FusedSolver.neumann_rtol``); ``neumann``
 gives the terms per row and times the same solve summing all 16 terms.
 
 Prints ONE JSON line.  ``value`` is ms per solve (fwd + bwd, HIP events),
-lower is better.
+lower is better, each solve one ``kb_solve`` call (``FusedSolver.solve``):
+the backward rows of the families that end at low dependency levels run on a
+second stream beside the forward's later, narrow levels.  ``two_calls``,
+``fwd_ms`` and ``bwd_ms`` time the same solves as ``run_forward`` then
+``run_backward``, the reference's split.
 
 * ``roofline``: the dominant row kernel's algorithmic HBM bytes per launch
   (S*4 bytes per row: the backward reads Pi*, Pibar* and the adjoint of every
@@ -489,8 +493,28 @@ def _traffic(kernel_symbol: str, config: str):
     return round(sum(float(v["traffic"]) * float(v["dispatches"]) for v in hits) / n, 1) if n else None
 
 
+def _timed_solve_calls(solver, theta, cw, steps: int):
+    """HIP-event times of ``steps`` one-call solves (``FusedSolver.solve``: the forward and its backward
+    in one ``kb_solve``, early families' backward rows beside the forward's later levels) and the host
+    wall time per solve; a failed E-adjoint solve raises."""
+    import torch
+
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    for a, b in ev:
+        a.record()
+        loss = solver.solve(theta, cw, check_solve=False)[0]
+        b.record()
+        solver.backward_stats()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t_wall) * 1e3 / steps
+    return [a.elapsed_time(b) for a, b in ev], wall, loss
+
+
 def _timed_solves(solver, theta, cw, steps: int):
-    """HIP-event times (total, fwd, bwd) of ``steps`` solves; a failed E-adjoint solve raises."""
+    """HIP-event times (total, fwd, bwd) of ``steps`` solves as two calls (``run_forward``, then
+    ``run_backward``); a failed E-adjoint solve raises."""
     import torch
 
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
@@ -554,16 +578,22 @@ def main():
         return
     solver = FusedSolver(static, static.solver_options)
     for i in range(args.warmup):
+        _timed_solve_calls(solver, theta, cw, 1)
         _timed_solves(solver, theta, cw, 1)
         log(args, f"[bench] warmup {i + 1}/{args.warmup}")
     fstats = solver.forward_stats()
 
-    # ---- timed region 1: whole solves (value)
-    tot, fwd, bwd, wall, loss = _timed_solves(solver, theta, cw, args.steps)
+    # ---- timed region 1: whole solves in one call each (value)
+    tot, wall, loss = _timed_solve_calls(solver, theta, cw, args.steps)
     ms = statistics.mean(tot)
     bstats = solver.backward_stats()
-    log(args, f"[bench] timed {args.steps} steps: {ms:.3f} ms/solve (fwd {statistics.mean(fwd):.3f}, "
-              f"bwd {statistics.mean(bwd):.3f}), wall {wall:.3f}")
+    # ---- the same solves as two calls (the reference's run_forward / run_backward split)
+    tot2, fwd, bwd, wall2, loss2 = _timed_solves(solver, theta, cw, args.steps)
+    if float(loss2) != float(loss):
+        raise RuntimeError(f"one-call and two-call solves disagree on the loss: {float(loss)} vs {float(loss2)}")
+    log(args, f"[bench] timed {args.steps} steps: {ms:.3f} ms/solve in one call (overlap cut {solver.overlap_cut}, "
+              f"{solver.overlap_rows} early rows); two calls {statistics.mean(tot2):.3f} (fwd "
+              f"{statistics.mean(fwd):.3f}, bwd {statistics.mean(bwd):.3f}), wall {wall:.3f}")
 
     # ---- timed region 2: per-launch HIP events around every row-kernel launch (roofline)
     solver.profile(True)
@@ -648,10 +678,12 @@ def main():
                 os.environ.pop("KB_DEDUP")
             else:
                 os.environ["KB_DEDUP"] = old
-        _timed_solves(flat, theta, cw, 2)
+        _timed_solve_calls(flat, theta, cw, 2)
+        _timed_solves(flat, theta, cw, 1)
+        t_one = _timed_solve_calls(flat, theta, cw, max(3, args.steps // 2))[0]
         t_all, f_all, b_all, _, _ = _timed_solves(flat, theta, cw, max(3, args.steps // 2))
-        dedup_off = {"ms": round(statistics.mean(t_all), 4), "fwd_ms": round(statistics.mean(f_all), 4),
-                     "bwd_ms": round(statistics.mean(b_all), 4)}
+        dedup_off = {"ms": round(statistics.mean(t_one), 4), "ms_two_calls": round(statistics.mean(t_all), 4),
+                     "fwd_ms": round(statistics.mean(f_all), 4), "bwd_ms": round(statistics.mean(b_all), 4)}
         del flat
     # ---- the Neumann series: terms per solved row at the solver's early stop, and the same solve
     # with every term summed (the reference's series, neumann_rtol = 0)
@@ -665,9 +697,13 @@ def main():
                         "solve summing every term")}
     if not args.no_dedup_off:
         full = FusedSolver(static, static.solver_options, neumann_rtol=0.0)
-        _timed_solves(full, theta, cw, 2)
+        _timed_solve_calls(full, theta, cw, 2)
+        _timed_solves(full, theta, cw, 1)
+        t_one = _timed_solve_calls(full, theta, cw, max(3, args.steps // 2))[0]
         t_all, f_all, b_all, _, _ = _timed_solves(full, theta, cw, max(3, args.steps // 2))
-        neumann.update(ms_full_series=round(statistics.mean(t_all), 4), bwd_ms_full_series=round(statistics.mean(b_all), 4))
+        neumann.update(ms_full_series=round(statistics.mean(t_one), 4),
+                       ms_two_calls_full_series=round(statistics.mean(t_all), 4),
+                       bwd_ms_full_series=round(statistics.mean(b_all), 4))
         del full
     per_call = None if args.no_per_call else per_call_timings(static, theta, cw, static_levels=static_levels)
     if per_call is not None:
@@ -698,7 +734,8 @@ def main():
                          f"per-species theta, pi_iters=16, neumann_terms=16 (early stop at rtol {solver.neumann_rtol:.3g}, "
                          f"{neumann['terms_mean']:.2f} terms per row on average); row classes: the forward computes "
                          f"{solver.n_forward_rows} of {summ['C']} rows (identical rows written from one "
-                         f"computation), the backward solves {solver.n_backward_rows}"),
+                         f"computation), the backward solves {solver.n_backward_rows}; one call per solve, "
+                         f"{solver.overlap_rows} backward rows beside the forward's levels above {solver.overlap_cut}"),
             "S_leaves": (summ["S"] + 1) // 2,
             "S_columns": summ["S"],
             "C": summ["C"],
@@ -708,6 +745,13 @@ def main():
             "forward_rows_computed": solver.n_forward_rows,
             "backward_rows_solved": solver.n_backward_rows,
         },
+        "overlap": {"cut": solver.overlap_cut, "early_rows": solver.overlap_rows,
+                    "note": ("value times one kb_solve call per solve: the backward rows of the families whose "
+                             "root lies at or below dependency level `cut` run on a second stream beside the "
+                             "forward's later levels (-1: no overlap, the two passes in order); two_calls times "
+                             "run_forward then run_backward, the reference's split, with fwd_ms / bwd_ms")},
+        "two_calls": {"ms": round(statistics.mean(tot2), 4), "median_ms": round(statistics.median(tot2), 4),
+                      "host_wall_ms_per_step": round(wall2, 4)},
         "fwd_ms": round(statistics.mean(fwd), 4),
         "bwd_ms": round(statistics.mean(bwd), 4),
         "median_ms": round(statistics.median(tot), 4),

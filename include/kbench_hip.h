@@ -69,9 +69,10 @@ typedef struct kb_plan kb_plan;
 /* Build the device-resident layout tables (allocates device memory). */
 int kb_plan_create(const kb_layout* layout, kb_plan** out);
 void kb_plan_destroy(kb_plan* plan);
-/* out[0..n), n <= 10: S, C, n_fam, n_waves, pointer-jump rounds, bottom-up
+/* out[0..n), n <= 13: S, C, n_fam, n_waves, pointer-jump rounds, bottom-up
  * levels, dependency levels, rows the forward computes (one per class of
- * identical rows), classes of level-0 rows, level-0 rows. */
+ * identical rows), classes of level-0 rows, level-0 rows, kb_solve's overlap
+ * cut (-1: none), the rows it solves early and the lowest level of those. */
 int kb_plan_info(const kb_plan* plan, int32_t* out, int n);
 
 /*
@@ -172,6 +173,29 @@ typedef struct kb_backward_io {
 } kb_backward_io;
 
 int kb_backward(kb_plan* plan, const kb_backward_io* io, void* stream);
+
+/*
+ * One forward and its backward in one call: what kb_forward followed by
+ * kb_backward computes (reference kbench/runtime.py:63-75 run_forward, then
+ * :77-115 run_backward on its outputs), with the two passes overlapped.  The
+ * rows of every family whose root lies at a dependency level <= the plan's
+ * overlap cut, at levels from the cut down to the window's lowest level, are
+ * solved on a second stream, once the forward has passed the cut, while the
+ * forward's later levels run; the other rows down to that level, then the
+ * levels below it whole, level 0 and the epilogue follow on the caller's
+ * stream, which has joined the second stream before kb_solve returns (in
+ * stream order).  Both are chosen when the plan is created: the cut is the
+ * highest level whose forward rows would not fit beside the early launches,
+ * the lowest level the lowest one at which the early launches still take no
+ * longer than the other stream's work beside them; -1 (two passes in order)
+ * when the early launches would hold fewer rows than CUs.  Environment
+ * KB_OVERLAP_CUT / KB_OVERLAP_LOW / KB_OVERLAP_GRID override the cut, the
+ * lowest level and the early launches' workgroups (default 5/8 of the CUs).
+ * bio must name the forward's outputs as its inputs (fio->pi etc.); its
+ * forward_token is ignored.  Same outputs as the two calls, up to the order of
+ * the gradient bucket sums (bitwise reproducible run to run).
+ */
+int kb_solve(kb_plan* plan, const kb_forward_io* fio, const kb_backward_io* bio, void* stream);
 
 /*
  * The E adjoint of the backward's epilogue for given cotangents, without the

@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <array>
 #include <climits>
+#include <functional>
 #include <map>
 #include <cstdarg>
 #include <cstdio>
@@ -140,6 +141,17 @@ struct kb_plan {
   int b_nb_max = 0, b_n_partials = 0, b_variant = 0, b_large = 1;
   size_t b_slot = 0;  // floats per workgroup slot of b_contrib
   std::vector<int> b_poff;
+  // kb_solve: rows of the families whose root lies at a level <= overlap_cut
+  // come first in their level's backward schedule (n_early of them); those of
+  // levels overlap_low .. overlap_cut are solved on a second stream while the
+  // forward's later levels run, the levels below overlap_low as whole levels
+  // afterwards
+  int overlap_cut = -1;
+  int overlap_low = 1;
+  int overlap_grid = 1;  // workgroups of the early launches
+  std::vector<int> n_early;
+  hipStream_t s2 = nullptr;
+  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
   // optional per-launch timing of the wave kernels (HIP events on the launch stream)
   int prof = 0;
   std::vector<hipEvent_t> ev_fwd, ev_bwd;
@@ -188,6 +200,9 @@ void kb_plan_destroy(kb_plan* p) {
   if (!p) return;
   for (hipEvent_t e : p->ev_fwd) (void)hipEventDestroy(e);
   for (hipEvent_t e : p->ev_bwd) (void)hipEventDestroy(e);
+  if (p->ev_fork) (void)hipEventDestroy(p->ev_fork);
+  if (p->ev_join) (void)hipEventDestroy(p->ev_join);
+  if (p->s2) (void)hipStreamDestroy(p->s2);
   for (void* ptr : p->owned)
     if (ptr) (void)hipFree(ptr);
   if (p->h_status) (void)hipHostFree(p->h_status);
@@ -539,6 +554,106 @@ int kb_plan_create(const kb_layout* L, kb_plan** out) {
   rc |= upload(&p->d_child_in, cin);
   rc |= upload(&p->d_unnorm, unnorm);
   rc |= upload(&p->d_root_index, root_index);
+  {
+    // kb_solve's overlap (KB_OVERLAP_CUT = c): every row of a family whose
+    // root lies at level <= c moves to the front of its level's backward
+    // schedule, in row order, the other rows after it, also in row order
+    // (kb_backward runs each level's rows in this order too, in one launch).
+    // An early row must have early parents only, and its children must be
+    // early as well: families that share a row are grouped (union-find) and a
+    // group is early when all of its roots are; rows no root reaches stay late.
+    std::vector<int> fam_of(C, -1), grp(L->n_fam);
+    for (int f = 0; f < L->n_fam; ++f) grp[f] = f;
+    std::function<int(int)> find = [&](int f) { return grp[f] == f ? f : (grp[f] = find(grp[f])); };
+    for (int f = 0; f < L->n_fam; ++f) {
+      std::vector<int> stack{roots[f]};
+      while (!stack.empty()) {
+        const int r = stack.back();
+        stack.pop_back();
+        if (fam_of[r] >= 0) {
+          const int a = find(fam_of[r]), b = find(f);
+          if (a != b) grp[a] = b;
+          continue;
+        }
+        fam_of[r] = f;
+        for (int i = sptr[r]; i < sptr[r + 1]; ++i) {
+          stack.push_back(sl[i]);
+          stack.push_back(sr[i]);
+        }
+      }
+    }
+    std::vector<int> grp_top(L->n_fam, 0);
+    for (int f = 0; f < L->n_fam; ++f) grp_top[find(f)] = std::max(grp_top[find(f)], dagd[roots[f]]);
+    std::vector<int> row_top(C, INT_MAX);
+    for (int r = 0; r < C; ++r)
+      if (fam_of[r] >= 0) row_top[r] = grp_top[find(fam_of[r])];
+    // The early launches get KB_OVERLAP_GRID workgroups (default 5/8 of the
+    // CUs, one backward workgroup per CU); the cut defaults to the highest level
+    // whose forward rows would not fit on the other CUs (two forward workgroups
+    // per CU, one for rows past 4096 states), so the forward's later levels run
+    // beside the early rows without waiting for CUs; with fewer early rows than
+    // CUs in the early launches there is nothing worth overlapping and the cut
+    // is -1.
+    int dev = 0, n_cu = 1;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      n_cu = 1;
+    const char* gv = getenv("KB_OVERLAP_GRID");
+    p->overlap_grid = std::max(1, gv && atoi(gv) > 0 ? atoi(gv) : n_cu * 5 / 8);
+    const char* cv = getenv("KB_OVERLAP_CUT");
+    int cut = -1;
+    if (cv) {
+      cut = atoi(cv);
+    } else if (p->n_levels >= 3) {
+      const int cap = std::max(1, n_cu - p->overlap_grid) * (S > 4096 ? 1 : 2);
+      cut = p->n_levels - 1;
+      while (cut >= 1 && p->f_level_ptr[cut + 1] - p->f_level_ptr[cut] <= cap) --cut;
+    }
+    if (cut >= p->n_levels - 1) cut = p->n_levels - 2;
+    p->n_early.assign(std::max(p->n_levels, 1), 0);
+    for (int d = 1; d < p->n_levels; ++d) {
+      const int b = p->level_ptr[d], e = p->level_ptr[d + 1];
+      std::stable_partition(sched.begin() + b, sched.begin() + e, [&](int r) { return row_top[r] <= cut; });
+      int ne = 0;
+      for (int k = b; k < e; ++k) ne += row_top[sched[k]] <= cut ? 1 : 0;
+      p->n_early[d] = ne;
+    }
+    // The early launches run the cut's levels down to overlap_low; below it
+    // the levels run whole, on every CU, after both streams have met.  The
+    // default low is the lowest level at which the early launches (their rows
+    // in rounds of one row per workgroup) still take no longer than what runs
+    // on the other CUs meanwhile: the forward's later levels (a round there
+    // counted as 0.8 of a backward round) and the late rows of the levels
+    // down to low.  With more early rows the early stream would hold 5/8 of
+    // the CUs for most of the backward.  A cut given by KB_OVERLAP_CUT keeps
+    // low = 1 unless KB_OVERLAP_LOW says otherwise.
+    const char* lv = getenv("KB_OVERLAP_LOW");
+    int low = 1;
+    if (lv) {
+      low = std::max(1, atoi(lv));
+    } else if (cut >= 1 && !cv) {
+      const int g = std::max(1, p->overlap_grid), rest = std::max(1, n_cu - g);
+      const int kf = S > 4096 ? 1 : 2;
+      double mf = 0.0;
+      for (int d = cut + 1; d < p->n_levels; ++d) {
+        const int nf = p->f_level_ptr[d + 1] - p->f_level_ptr[d];
+        mf += 0.8 * ((nf + kf * rest - 1) / (kf * rest));
+      }
+      auto rounds = [](long n, long w) { return (double)((n + w - 1) / w); };
+      for (low = 1; low <= cut; ++low) {
+        double e = 0.0, ml = 0.0;
+        for (int d = low; d <= cut; ++d) e += rounds(p->n_early[d], g);
+        for (int d = low; d < p->n_levels; ++d)
+          ml += rounds(p->level_ptr[d + 1] - p->level_ptr[d] - (d <= cut ? p->n_early[d] : 0), rest);
+        if (e <= mf + ml) break;
+      }
+      int ne = 0;
+      for (int d = low; d <= cut; ++d) ne += p->n_early[d];
+      if (ne < n_cu) low = cut + 1;
+    }
+    p->overlap_low = low;
+    if (low > cut) cut = -1;
+    p->overlap_cut = cut;
+  }
   rc |= upload(&p->d_sched_rows, sched);
   rc |= upload(&p->d_fsched, fsched);
   rc |= upload(&p->d_fsplit_l, fsl);
@@ -682,18 +797,25 @@ int kb_plan_info(const kb_plan* p, int32_t* out, int n) {
   if (!p || !out) return set_error(KB_ERR_ARG, "null argument");
   const int32_t n_fwd = p->f_level_ptr.empty() ? 0 : p->f_level_ptr.back();
   const int32_t rows0 = p->level_ptr.size() > 1 ? p->level_ptr[1] : 0;
-  int32_t v[10] = {p->S, p->C, p->n_fam, p->n_waves, p->n_jump, p->n_blevels, p->n_levels, n_fwd, p->n_cls0, rows0};
-  for (int i = 0; i < n && i < 10; ++i) out[i] = v[i];
+  int32_t n_early = 0;
+  for (int d = p->overlap_low; d <= p->overlap_cut; ++d) n_early += p->n_early[d];
+  int32_t v[13] = {p->S,      p->C,      p->n_fam,  p->n_waves,       p->n_jump,       p->n_blevels, p->n_levels,
+                   n_fwd,     p->n_cls0, rows0,     p->overlap_cut, n_early, p->overlap_low};
+  for (int i = 0; i < n && i < 13; ++i) out[i] = v[i];
   return 0;
 }
 
-int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
+}  // extern "C"
+
+// The forward in three parts (kb_forward runs them in order; kb_solve
+// interleaves the backward's early rows with the levels): checks, E-step and
+// the row kernels' parameters; one dependency level; the loss.
+static int forward_setup(kb_plan* p, const kb_forward_io* io, hipStream_t st, kb::FwdParams& F) {
   if (!p || !io) return set_error(KB_ERR_ARG, "null argument");
   if (io->pi_iters < 2 || io->pi_iters % 2 != 0)
     return set_error(KB_ERR_ARG, "pi_iters must be an even integer at least 2");
   if (io->e_max_iter < 1) return set_error(KB_ERR_ARG, "e_max_iter must be at least 1");
   if (!(io->e_tol > 0.0)) return set_error(KB_ERR_ARG, "e_tol must be positive");
-  hipStream_t st = (hipStream_t)stream;
   const int S = p->S;
 
   kb::EStepParams E{};
@@ -741,7 +863,7 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
   kb::launch_estep(E, st);
   KB_HIP(hipGetLastError());
 
-  kb::FwdParams F{};
+  F = kb::FwdParams{};
   F.tr = p->tree();
   F.S = S;
   F.n_sweeps = io->pi_iters - 1;
@@ -801,18 +923,32 @@ int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
   p->fwd_token += 1;
   p->fwd_pi = io->pi;
   p->fwd_pibar = io->pibar;
-  for (int d = 0; d < p->n_levels; ++d) {
-    if (p->prof) KB_HIP(hipEventRecord(p->ev_fwd[2 * d], st));
-    const int nb = F.narrow_below;
-    if (d == 0 && S > 1024) F.narrow_below = INT_MAX;  // the leaf level
-    kb::launch_fwd_wave(F, p->f_level_ptr[d], p->f_level_ptr[d + 1] - p->f_level_ptr[d], st);
-    F.narrow_below = nb;
-    if (p->prof) KB_HIP(hipEventRecord(p->ev_fwd[2 * d + 1], st));
-  }
+  return 0;
+}
+
+static int forward_level(kb_plan* p, kb::FwdParams& F, int d, hipStream_t st) {
+  if (p->prof) KB_HIP(hipEventRecord(p->ev_fwd[2 * d], st));
+  const int nb = F.narrow_below;
+  if (d == 0 && p->S > 1024) F.narrow_below = INT_MAX;  // the leaf level
+  kb::launch_fwd_wave(F, p->f_level_ptr[d], p->f_level_ptr[d + 1] - p->f_level_ptr[d], st);
+  F.narrow_below = nb;
+  if (p->prof) KB_HIP(hipEventRecord(p->ev_fwd[2 * d + 1], st));
+  return 0;
+}
+
+static int forward_finish(kb_plan* p, const kb_forward_io* io, hipStream_t st) {
   KB_HIP(hipGetLastError());
-  kb::launch_loss(io->pi, p->d_roots, io->E, S, p->n_fam, p->loss_terms, p->loss64, io->loss, st);
+  kb::launch_loss(io->pi, p->d_roots, io->E, p->S, p->n_fam, p->loss_terms, p->loss64, io->loss, st);
   KB_HIP(hipGetLastError());
   return 0;
+}
+
+extern "C" int kb_forward(kb_plan* p, const kb_forward_io* io, void* stream) {
+  hipStream_t st = (hipStream_t)stream;
+  kb::FwdParams F{};
+  int rc = forward_setup(p, io, st, F);
+  for (int d = 0; !rc && d < p->n_levels; ++d) rc = forward_level(p, F, d, st);
+  return rc ? rc : forward_finish(p, io, st);
 }
 
 // floats per workgroup slot of the backward row kernels
@@ -856,7 +992,9 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   if (p->b_contrib && p->b_nb_max == nb_max && p->b_slot == bwd_slot_floats(S, large)) return 0;
   p->b_slot = bwd_slot_floats(S, large);
   p->b_nb_max = nb_max;
-  p->b_n_partials = nb_max;  // one persistent bucket slot per workgroup of the per-level grids
+  // one persistent bucket slot per workgroup of the per-level grids; kb_solve's
+  // early launches use a second set, so slots for 2 nb_max are allocated
+  p->b_n_partials = nb_max;
   if (p->b_contrib) {
     (void)hipFree(p->b_contrib);
     (void)hipFree(p->b_partial);
@@ -865,8 +1003,8 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
     p->b_contrib = nullptr;
     p->b_partial = nullptr;
     int rc = 0;
-    rc |= alloc(&p->b_contrib, (size_t)std::max(1, p->b_n_partials) * p->b_slot);
-    rc |= alloc(&p->b_partial, (size_t)kb::reduce_chunks(std::max(1, p->b_n_partials)) * 8 * S);
+    rc |= alloc(&p->b_contrib, (size_t)2 * std::max(1, p->b_n_partials) * p->b_slot);
+    rc |= alloc(&p->b_partial, (size_t)kb::reduce_chunks(2 * std::max(1, p->b_n_partials)) * 8 * S);
     p->owned.push_back(p->b_contrib);
     p->owned.push_back(p->b_partial);
     return rc ? KB_ERR_HIP : 0;
@@ -881,8 +1019,8 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   rc |= alloc(&p->b_m_mask, (size_t)std::max(1, C > 0 ? p->level_ptr[1] : 1));
   rc |= alloc(&p->b_cls_active, (size_t)std::max(1, p->n_cls0));
   rc |= alloc(&p->b_ck_any, (size_t)std::max(1, p->n_chunks0));
-  rc |= alloc(&p->b_contrib, (size_t)std::max(1, p->b_n_partials) * p->b_slot);
-  rc |= alloc(&p->b_partial, (size_t)kb::reduce_chunks(std::max(1, p->b_n_partials)) * 8 * S);
+  rc |= alloc(&p->b_contrib, (size_t)2 * std::max(1, p->b_n_partials) * p->b_slot);
+  rc |= alloc(&p->b_partial, (size_t)kb::reduce_chunks(2 * std::max(1, p->b_n_partials)) * 8 * S);
   rc |= alloc(&p->b_acc, (size_t)8 * S);
   rc |= alloc(&p->b_work, (size_t)kb::epilogue_work_vectors() * S);
   rc |= alloc(&p->b_status, 2);
@@ -905,7 +1043,12 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   return rc ? KB_ERR_HIP : 0;
 }
 
-int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
+// The backward in three parts (kb_backward runs them in order): checks, work
+// buffers, constants, the row kernels' parameters and the zeroed bucket slots
+// (`sets` sets of b_nb_max slots: 1, or 2 for kb_solve's early rows); one
+// launch over rows [first, first + n) of level d on up to `grid` workgroups
+// whose slots start at `poff`; the slot reduction, E adjoint and VJP epilogue.
+static int backward_setup(kb_plan* p, const kb_backward_io* io, hipStream_t st, kb::BwdParams& B, int sets) {
   if (!p || !io) return set_error(KB_ERR_ARG, "null argument");
   if (io->neumann_terms < 0) return set_error(KB_ERR_ARG, "neumann_terms must be non-negative");
   if (io->bicgstab_max_iter < 1) return set_error(KB_ERR_ARG, "max_iter must be at least 1");
@@ -916,8 +1059,7 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
     return set_error(KB_ERR_ARG, "neumann_rtol must be in [0, 1)");
   int rc = ensure_backward_work(p, io->use_col_weights);
   if (rc) return rc;
-  hipStream_t st = (hipStream_t)stream;
-  const int S = p->S, C = p->C;
+  const int S = p->S;
 
   kb::BwdConstArgs K{};
   K.S = S;
@@ -943,7 +1085,7 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   K.om = kb::kb_use_large(S, p->b_large) ? p->b_om_const : nullptr;
   kb::launch_bwd_consts(K, st);
 
-  kb::BwdParams B{};
+  B = kb::BwdParams{};
   B.tr = p->tree();
   B.S = S;
   B.n_terms = io->neumann_terms;
@@ -1002,19 +1144,28 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   B.rep_of = p->d_rep_of;
   B.cls_ptr = p->d_cls_ptr;
   B.cls_rows = p->d_cls_rows;
-  kb::launch_fill_zero(p->b_contrib, (size_t)p->b_n_partials * p->b_slot, st);
-  for (int d = p->n_levels - 1; d >= 0; --d) {
-    if (p->prof) KB_HIP(hipEventRecord(p->ev_bwd[2 * d], st));
-    // level 0 (rows without splits) runs by class: one adjoint solve per class of identical rows
-    const int n = d == 0 ? p->n_cls0 : p->level_ptr[d + 1] - p->level_ptr[d];
-    B.class_mode = d == 0 ? 1 : 0;
-    if (d == 0) kb::launch_bwd_level0_prep(B, p->level_ptr[1], p->n_cls0, st);
-    B.variant = p->b_variant == 1 ? ((S > 1024 || n < 2 * p->b_nb_max) ? 2 : 0) : p->b_variant;
-    kb::launch_bwd_wave(B, p->level_ptr[d], n, std::min(n, p->b_nb_max), 0, st);
-    if (p->prof) KB_HIP(hipEventRecord(p->ev_bwd[2 * d + 1], st));
-  }
+  // (the slot count is known only once ensure_backward_work has run)
+  kb::launch_fill_zero(p->b_contrib, (size_t)sets * p->b_n_partials * p->b_slot, st);
   KB_HIP(hipGetLastError());
-  kb::launch_bwd_reduce(p->b_contrib, p->b_n_partials, S, p->b_slot, kb::kb_slot_ld(S, p->b_large), p->b_partial,
+  return 0;
+}
+
+static int backward_level(kb_plan* p, kb::BwdParams& B, int d, int first, int n, int grid, int poff, hipStream_t st) {
+  const int S = p->S;
+  if (p->prof) KB_HIP(hipEventRecord(p->ev_bwd[2 * d], st));
+  // level 0 (rows without splits) runs by class: one adjoint solve per class of identical rows
+  B.class_mode = d == 0 ? 1 : 0;
+  if (d == 0) kb::launch_bwd_level0_prep(B, p->level_ptr[1], p->n_cls0, st);
+  B.variant = p->b_variant == 1 ? ((S > 1024 || n < 2 * grid) ? 2 : 0) : p->b_variant;
+  kb::launch_bwd_wave(B, first, n, std::min(n, grid), poff, st);
+  if (p->prof) KB_HIP(hipEventRecord(p->ev_bwd[2 * d + 1], st));
+  return 0;
+}
+
+static int backward_finish(kb_plan* p, const kb_backward_io* io, int n_partials, hipStream_t st) {
+  const int S = p->S;
+  KB_HIP(hipGetLastError());
+  kb::launch_bwd_reduce(p->b_contrib, n_partials, S, p->b_slot, kb::kb_slot_ld(S, p->b_large), p->b_partial,
                         p->b_acc_pre, st);
   kb::launch_bwd_unpermute(p->b_acc_pre, p->d_pre, S, p->b_acc, st);
   KB_HIP(hipGetLastError());
@@ -1053,6 +1204,77 @@ int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   KB_HIP(hipGetLastError());
   return 0;
 }
+
+static int level_rows(const kb_plan* p, int d) { return d == 0 ? p->n_cls0 : p->level_ptr[d + 1] - p->level_ptr[d]; }
+
+extern "C" int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
+  hipStream_t st = (hipStream_t)stream;
+  kb::BwdParams B{};
+  int rc = backward_setup(p, io, st, B, 1);
+  for (int d = p ? p->n_levels - 1 : -1; !rc && d >= 0; --d)
+    rc = backward_level(p, B, d, p->level_ptr[d], level_rows(p, d), p->b_nb_max, 0, st);
+  return rc ? rc : backward_finish(p, io, p->b_n_partials, st);
+}
+
+extern "C" int kb_solve(kb_plan* p, const kb_forward_io* fio, const kb_backward_io* bio, void* stream) {
+  if (!p || !fio || !bio) return set_error(KB_ERR_ARG, "null argument");
+  if (bio->pi != fio->pi || bio->pibar != fio->pibar || bio->pibar_row_max != fio->pibar_row_max ||
+      bio->E != fio->E || bio->Ebar != fio->Ebar || bio->E_s1 != fio->E_s1 || bio->E_s2 != fio->E_s2 ||
+      bio->log_pS != fio->log_pS || bio->log_pD != fio->log_pD || bio->log_pL != fio->log_pL ||
+      bio->max_coupling != fio->max_coupling || bio->col_log_probs != fio->col_log_probs)
+    return set_error(KB_ERR_ARG, "kb_solve: the backward must read the forward's outputs");
+  hipStream_t st = (hipStream_t)stream;
+  kb::FwdParams F{};
+  int rc = forward_setup(p, fio, st, F);
+  if (rc) return rc;
+  const int cut = p->overlap_cut;
+  const int L = p->n_levels;
+  if (cut < 1 || L < 3) {  // nothing to overlap: the two passes one after the other
+    for (int d = 0; !rc && d < L; ++d) rc = forward_level(p, F, d, st);
+    if (!rc) rc = forward_finish(p, fio, st);
+    if (rc) return rc;
+    kb_backward_io b2 = *bio;
+    b2.forward_token = p->fwd_token;
+    return kb_backward(p, &b2, stream);
+  }
+  kb_backward_io b2 = *bio;
+  b2.forward_token = p->fwd_token;
+  kb::BwdParams B{};
+  // the early rows' workgroups use slots b_nb_max .. 2 b_nb_max - 1
+  rc = backward_setup(p, &b2, st, B, 2);
+  if (rc) return rc;
+  if (!p->s2) {
+    KB_HIP(hipStreamCreateWithFlags(&p->s2, hipStreamNonBlocking));
+    KB_HIP(hipEventCreateWithFlags(&p->ev_fork, hipEventDisableTiming));
+    KB_HIP(hipEventCreateWithFlags(&p->ev_join, hipEventDisableTiming));
+  }
+  // workgroups of the early launches: the rest of the CUs stay free for the
+  // forward's narrow levels that run beside them
+  const int eg = std::max(1, std::min(p->b_nb_max, p->overlap_grid));
+  const int low = p->overlap_low;
+  for (int d = 0; !rc && d <= cut; ++d) rc = forward_level(p, F, d, st);
+  if (rc) return rc;
+  KB_HIP(hipEventRecord(p->ev_fork, st));
+  KB_HIP(hipStreamWaitEvent(p->s2, p->ev_fork, 0));
+  kb::BwdParams B2 = B;
+  for (int d = cut; !rc && d >= low; --d)
+    if (p->n_early[d] > 0) rc = backward_level(p, B2, d, p->level_ptr[d], p->n_early[d], eg, p->b_nb_max, p->s2);
+  if (rc) return rc;
+  KB_HIP(hipEventRecord(p->ev_join, p->s2));
+  for (int d = cut + 1; !rc && d < L; ++d) rc = forward_level(p, F, d, st);
+  if (!rc) rc = forward_finish(p, fio, st);
+  // the late rows down to the window's lowest level, then the levels below it whole
+  for (int d = L - 1; !rc && d >= low; --d) {
+    const int ne = d <= cut ? p->n_early[d] : 0, n = level_rows(p, d) - ne;
+    if (n > 0) rc = backward_level(p, B, d, p->level_ptr[d] + ne, n, p->b_nb_max, 0, st);
+  }
+  if (rc) return rc;
+  KB_HIP(hipStreamWaitEvent(st, p->ev_join, 0));
+  for (int d = low - 1; !rc && d >= 0; --d) rc = backward_level(p, B, d, p->level_ptr[d], level_rows(p, d), p->b_nb_max, 0, st);
+  return rc ? rc : backward_finish(p, &b2, 2 * p->b_nb_max, st);
+}
+
+extern "C" {
 
 int kb_e_adjoint(kb_plan* p, const kb_e_adjoint_io* io, void* stream) {
   if (!p || !io) return set_error(KB_ERR_ARG, "null argument");

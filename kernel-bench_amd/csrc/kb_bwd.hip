@@ -136,7 +136,8 @@ __global__ __launch_bounds__(NT) void bwd_row_kernel(BwdParams P, int first, int
   // thread's positions are one vector access)
   const int SL = kb_slot_ld(S, 0);
   const int SG = kb_stage_ld(S);  // child staging rows likewise
-  float* const cr = P.contrib + (size_t)blockIdx.x * 8 * SL;
+  // (poff: the first slot of this launch's workgroups)
+  float* const cr = P.contrib + (size_t)(poff + (int)blockIdx.x) * 8 * SL;
   float old[8][CPT];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -1163,7 +1164,7 @@ void launch_fill_zero(float* p, size_t n, hipStream_t st) {
 
 void launch_bwd_wave(const BwdParams& P, int first, int W, int nb, int poff, hipStream_t st) {
   if (W <= 0 || nb <= 0) return;
-  if (launch_bwd_large(P, first, W, nb, st)) return;
+  if (launch_bwd_large(P, first, W, nb, poff, st)) return;
   const int S = P.S;
   if (P.variant == 2) {
     KB_BWD_CASE(1024, 2)

@@ -103,7 +103,7 @@ __device__ __forceinline__ void st4_add(float* p, float4 b, const float (&x)[4])
 // EARLY: the Neumann series may stop early (P.rtol > 0), as in bwd_row_kernel
 template <int NT, int CPT, bool WEIGHTED, bool EARLY>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4)))
-void bwd_row_large_kernel(BwdParams P, int first, int n_rows) {
+void bwd_row_large_kernel(BwdParams P, int first, int n_rows, int poff) {
   constexpr int MAXS = NT * CPT;
   constexpr int LD = MAXS + 64;  // [MAXS] is the padding slot, kept at 0
   constexpr int NW = NT / 64;
@@ -133,7 +133,7 @@ void bwd_row_large_kernel(BwdParams P, int first, int n_rows) {
   // this workgroup's slot (KB_LARGE_SLOT_ROWS rows of MAXS floats, preorder
   // positions): the eight bucket rows, then the current row's split term, Pi*
   // and Pibar*.  srow(j) is this thread's first own position of row j.
-  float* const slot = P.contrib + (size_t)blockIdx.x * KB_LARGE_SLOT_ROWS * MAXS;
+  float* const slot = P.contrib + (size_t)(poff + (int)blockIdx.x) * KB_LARGE_SLOT_ROWS * MAXS;
   int ep = 0;  // epoch of the current phase (see fresh)
   auto srow = [&](int j) {
     return reinterpret_cast<float*>(reinterpret_cast<char*>(fresh(slot + (size_t)j * MAXS, ep)) +
@@ -720,17 +720,17 @@ void bwd_row_large_kernel(BwdParams P, int first, int n_rows) {
   if (S <= NT_ * CPT_) {                                                                                       \
     const bool early = P.rtol > 0.0f;                                                                          \
     if (P.use_col && early)                                                                                    \
-      hipLaunchKernelGGL((bwd_row_large_kernel<NT_, CPT_, true, true>), dim3(nb), dim3(NT_), 0, st, P, first, W);   \
+      hipLaunchKernelGGL((bwd_row_large_kernel<NT_, CPT_, true, true>), dim3(nb), dim3(NT_), 0, st, P, first, W, poff);   \
     else if (P.use_col)                                                                                        \
-      hipLaunchKernelGGL((bwd_row_large_kernel<NT_, CPT_, true, false>), dim3(nb), dim3(NT_), 0, st, P, first, W);  \
+      hipLaunchKernelGGL((bwd_row_large_kernel<NT_, CPT_, true, false>), dim3(nb), dim3(NT_), 0, st, P, first, W, poff);  \
     else if (early)                                                                                            \
-      hipLaunchKernelGGL((bwd_row_large_kernel<NT_, CPT_, false, true>), dim3(nb), dim3(NT_), 0, st, P, first, W);  \
+      hipLaunchKernelGGL((bwd_row_large_kernel<NT_, CPT_, false, true>), dim3(nb), dim3(NT_), 0, st, P, first, W, poff);  \
     else                                                                                                       \
-      hipLaunchKernelGGL((bwd_row_large_kernel<NT_, CPT_, false, false>), dim3(nb), dim3(NT_), 0, st, P, first, W); \
+      hipLaunchKernelGGL((bwd_row_large_kernel<NT_, CPT_, false, false>), dim3(nb), dim3(NT_), 0, st, P, first, W, poff); \
     return true;                                                                                               \
   }
 
-bool launch_bwd_large(const BwdParams& P, int first, int W, int nb, hipStream_t st) {
+bool launch_bwd_large(const BwdParams& P, int first, int W, int nb, int poff, hipStream_t st) {
   const int S = P.S;
   if (!kb_use_large(S, P.large)) return false;
   // the shape kb_large_nt / kb_large_ld give the owner-major tables

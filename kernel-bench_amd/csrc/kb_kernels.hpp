@@ -231,7 +231,7 @@ void launch_bwd_wave(const BwdParams& P, int first, int n, int nb, int poff, hip
 int bwd_blocks_per_cu(int S, int use_col, int variant, int large);
 // Rows of 2049..8192 states on the low-register kernel (kb_bwd_large.hip);
 // false if P.large is off or S is outside that range.
-bool launch_bwd_large(const BwdParams& P, int first, int n, int nb, hipStream_t st);
+bool launch_bwd_large(const BwdParams& P, int first, int n, int nb, int poff, hipStream_t st);
 int bwd_large_blocks_per_cu(int S, int use_col);
 // Level-0 adjoint rows, masks and class sums.
 void launch_bwd_level0_prep(const BwdParams& P, int n_members, int n_cls, hipStream_t st);

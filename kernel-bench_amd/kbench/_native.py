@@ -103,6 +103,8 @@ def _declare(lib):
     if hasattr(lib, "kb_backward"):
         lib.kb_backward.argtypes = [vp, ct.POINTER(KbBackwardIO), vp]
         lib.kb_backward.restype = ct.c_int
+    lib.kb_solve.argtypes = [vp, ct.POINTER(KbForwardIO), ct.POINTER(KbBackwardIO), vp]
+    lib.kb_solve.restype = ct.c_int
     lib.kb_profile_enable.argtypes = [vp, ct.c_int]
     lib.kb_profile_enable.restype = ct.c_int
     lib.kb_profile_read.argtypes = [vp, ct.c_int, P_f32, ct.c_int]

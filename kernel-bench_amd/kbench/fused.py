@@ -195,13 +195,17 @@ class FusedSolver:
         self.root_row_ids = torch.as_tensor(roots, device=self.device)
         self.n_waves = len(ws)
         self.n_splits = L.n_splits
-        info = (ct.c_int32 * 10)()
-        N.check(lib.kb_plan_info(handle, info, 10))
+        info = (ct.c_int32 * 13)()
+        N.check(lib.kb_plan_info(handle, info, 13))
         self.n_levels = int(info[6])
         # row classes: the forward computes one row per class of identical rows;
         # the backward solves every split row and one row per class of level-0 rows
         self.n_forward_rows = int(info[7])
         self.n_backward_rows = C - int(info[9]) + int(info[8])
+        # solve(): the dependency level up to which whole families' backward rows run beside
+        # the forward's later levels (-1: none), how many rows that is, and the lowest level
+        # of those early launches (the levels below run whole afterwards)
+        self.overlap_cut, self.overlap_rows, self.overlap_low = int(info[10]), int(info[11]), int(info[12])
         self.last_n_e_iter = None
         self.last_n_bicgstab = None
         self._use_col_cache = None  # (_TensorKey of the caller's col_weights, answer)
@@ -237,6 +241,20 @@ class FusedSolver:
 
     def run_forward(self, theta, col_weights, *, use_col_weights=None):
         """theta -> (loss, saved), the reference ``run_forward`` contract."""
+        io, loss, saved, keep = self._forward_args(theta, col_weights, use_col_weights)
+        with torch.cuda.device(self.device):
+            N.check(N.lib().kb_forward(self._plan, ct.byref(io), N.stream_handle(self.device)))
+        self._forward_done(saved)
+        return loss, saved
+
+    def _forward_done(self, saved):
+        # the backward may reuse this forward's stored split terms while pi / pibar are
+        # these same, unmodified tensor objects
+        self._last_forward = (int(N.lib().kb_forward_token(self._plan)), _TensorKey(saved["pi_wave"]),
+                              _TensorKey(saved["pibar_wave"]))
+
+    def _forward_args(self, theta, col_weights, use_col_weights):
+        """(kb_forward_io, loss, saved, kept tensors) of one forward: its outputs allocated, not run."""
         so = self.so
         dev = self.device
         S, C = self.S, self.C
@@ -266,11 +284,6 @@ class FusedSolver:
             col_log_probs=N.ptr(col), pi=N.ptr(pi), pibar=N.ptr(pibar), pibar_row_max=N.ptr(rowmax),
             loss=N.ptr(loss),
         )
-        with torch.cuda.device(dev):
-            N.check(N.lib().kb_forward(self._plan, ct.byref(io), N.stream_handle(dev)))
-        # the backward may reuse this forward's stored split terms while pi / pibar are
-        # these same, unmodified tensor objects
-        self._last_forward = (int(N.lib().kb_forward_token(self._plan)), _TensorKey(pi), _TensorKey(pibar))
         if not self.statewise:
             pS, pD, pL = (t.reshape(()) for t in (pS, pD, pL))
         saved = dict(zip(FORWARD_SAVED_NAMES, (
@@ -278,7 +291,7 @@ class FusedSolver:
             pS, pD, pL, mt, col,
         )))
         saved["_use_col_weights"] = use_col
-        return loss, saved
+        return io, loss, saved, (theta, col_weights)
 
     def profile(self, enable: bool = True) -> None:
         """Record HIP events around every wave-kernel launch of later passes."""
@@ -329,6 +342,44 @@ class FusedSolver:
         from the device once per backward (``check_solve=False`` skips the read,
         and ``backward_stats`` reports the status later).
         """
+        io, grad_theta, grad_col, info = self._backward_args(theta, col_weights, saved, return_info)
+        io.forward_token = self._token_of(saved)
+        with torch.cuda.device(self.device):
+            N.check(N.lib().kb_backward(self._plan, ct.byref(io), N.stream_handle(self.device)))
+            if check_solve:
+                self.backward_stats()
+        if return_info:
+            # neumann_terms: J^T applications of every solved row (255: not solved here)
+            return grad_theta, grad_col, info
+        return grad_theta, grad_col
+
+    def _token_of(self, saved):
+        last = self._last_forward
+        if last is not None and last[1].matches(saved["pi_wave"]) and last[2].matches(saved["pibar_wave"]):
+            return last[0]
+        return 0
+
+    def solve(self, theta, col_weights, *, use_col_weights=None, return_info=False, check_solve=True):
+        """One forward and its backward -> (loss, saved, grad_theta, grad_col[, info]) (``kb_solve``).
+
+        The values of ``run_forward`` followed by ``run_backward`` on its outputs; with a plan
+        built under ``KB_OVERLAP_CUT`` the backward's rows of the families that end at or below
+        that dependency level run on a second stream beside the forward's later levels.
+        """
+        fio, loss, saved, keep = self._forward_args(theta, col_weights, use_col_weights)
+        bio, grad_theta, grad_col, info = self._backward_args(theta, col_weights, saved, return_info)
+        self._keep_solve = keep
+        with torch.cuda.device(self.device):
+            N.check(N.lib().kb_solve(self._plan, ct.byref(fio), ct.byref(bio), N.stream_handle(self.device)))
+            self._forward_done(saved)
+            if check_solve:
+                self.backward_stats()
+        if return_info:
+            return loss, saved, grad_theta, grad_col, info
+        return loss, saved, grad_theta, grad_col
+
+    def _backward_args(self, theta, col_weights, saved, return_info):
+        """(kb_backward_io without its forward token, grad_theta, grad_col, info) of one backward."""
         lib = N.lib()
         if not hasattr(lib, "kb_backward"):
             raise N.NativeLibraryMissing("libkbench_hip was built without kb_backward")
@@ -365,20 +416,9 @@ class FusedSolver:
             grad_theta=N.ptr(grad_theta), grad_col=N.ptr(grad_col), active_mask=N.ptr(mask), acc_out=N.ptr(acc),
             neumann_rtol=self.neumann_rtol, neumann_terms_out=N.ptr(terms),
         )
-        token = 0
-        last = self._last_forward
-        if last is not None and last[1].matches(saved["pi_wave"]) and last[2].matches(saved["pibar_wave"]):
-            token = last[0]
-        io.forward_token = token
         self._keep = (tens, theta_d, cw)
-        with torch.cuda.device(dev):
-            N.check(lib.kb_backward(self._plan, ct.byref(io), N.stream_handle(dev)))
-            if check_solve:
-                self.backward_stats()
-        if return_info:
-            # neumann_terms: J^T applications of every solved row (255: not solved here)
-            return grad_theta, grad_col, {"active_mask": mask, "acc": acc, "neumann_terms": terms}
-        return grad_theta, grad_col
+        info = {"active_mask": mask, "acc": acc, "neumann_terms": terms} if return_info else None
+        return io, grad_theta, grad_col, info
 
     def e_adjoint(self, saved, acc, *, q_extra=None, with_norm=False, use_col_weights=False, check_solve=True):
         """The E adjoint for the cotangents ``acc`` -> (w [S], g [5, S]), float64 (``kb_e_adjoint``).

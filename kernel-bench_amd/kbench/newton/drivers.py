@@ -66,8 +66,7 @@ class Objective:
         self.evals += 1
         th = self.theta(x)
         with torch.no_grad():
-            loss, saved = self.solver.run_forward(th, self.col_weights)
-            g, _ = self.solver.run_backward(th, self.col_weights, saved)
+            loss, _, g, _ = self.solver.solve(th, self.col_weights)
         return float(loss), g.reshape(-1).double()
 
     def hvp(self, x, kind: str):

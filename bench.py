@@ -595,7 +595,11 @@ def main():
               f"{solver.overlap_rows} early rows); two calls {statistics.mean(tot2):.3f} (fwd "
               f"{statistics.mean(fwd):.3f}, bwd {statistics.mean(bwd):.3f}), wall {wall:.3f}")
 
-    # ---- timed region 2: per-launch HIP events around every row-kernel launch (roofline)
+    # ---- timed region 2: per-launch HIP events around every row-kernel launch (roofline), on two-call
+    # solves (one launch per level and pass on one stream); the process's forwards number
+    # 2 W + 2 K + 1 .. 2 W + 3 K here (W warmup iterations of one one-call and one two-call solve,
+    # then K of each timed), the window of a kernel trace that matches these launches
+    prof_forwards = [2 * args.warmup + 2 * args.steps + 1, 2 * args.warmup + 3 * args.steps]
     solver.profile(True)
     fw_ms, bw_ms = [], []
     for _ in range(args.steps):
@@ -651,6 +655,7 @@ def main():
         "traffic": _traffic(sym, args.config),
         "launches": int(len(dur)),
         "launch_unit": "one launch per clade-DAG dependency level",
+        "events_over_forwards": prof_forwards,
         "avg_launch_ms": round(avg_ms, 5),
         "algorithmic_bytes_per_launch": round(avg_bytes, 1),
         "kernel_ms_per_solve": {k: round(float(v[0].sum()), 4) for k, v in kernels.items()},

@@ -1229,7 +1229,9 @@ extern "C" int kb_solve(kb_plan* p, const kb_forward_io* fio, const kb_backward_
   if (rc) return rc;
   const int cut = p->overlap_cut;
   const int L = p->n_levels;
-  if (cut < 1 || L < 3) {  // nothing to overlap: the two passes one after the other
+  // nothing to overlap, or per-launch timing on (its events time one launch per
+  // level on one stream): the two passes one after the other
+  if (cut < 1 || L < 3 || p->prof) {
     for (int d = 0; !rc && d < L; ++d) rc = forward_level(p, F, d, st);
     if (!rc) rc = forward_finish(p, fio, st);
     if (rc) return rc;

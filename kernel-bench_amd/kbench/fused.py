@@ -294,7 +294,11 @@ class FusedSolver:
         return io, loss, saved, (theta, col_weights)
 
     def profile(self, enable: bool = True) -> None:
-        """Record HIP events around every wave-kernel launch of later passes."""
+        """Record HIP events around every wave-kernel launch of later passes.
+
+        While it is on, ``solve`` runs the forward and the backward one after the other
+        (one launch per level and pass, on the caller's stream).
+        """
         N.check(N.lib().kb_profile_enable(self._plan, int(bool(enable))))
 
     def level_launch_ms(self, which: str):

@@ -5,16 +5,21 @@ Two sub-commands, both reading the CSV files rocprofv3 writes with
 
 ``stats DIR``
     Per-kernel table from ``DIR/*_kernel_stats.csv`` (calls, average and total
-    duration, share of GPU time), as Markdown.
+    duration, share of GPU time), as Markdown.  With ``--window K:FIRST:LAST``
+    the table is computed from ``DIR/*_kernel_trace.csv`` instead, over the
+    dispatches from the FIRST-th dispatch of the kernel whose name contains K
+    (counted from 1) up to, not including, its (LAST+1)-th: e.g. the solves
+    of one timed pass of a benchmark, counted by a kernel that runs once per
+    solve.
 
-``sq CSV [--json]``
+``sq CSV [--json] [--window K:FIRST:LAST]``
     Per-kernel SQ counters of one ``--pmc`` run divided by ``SQ_WAVES``; with
     ``--json`` also the fractions of wave cycles spent issuing VALU
     (``SQ_ACTIVE_INST_VALU / SQ_WAVE_CYCLES``) and waiting on LDS
     (``SQ_WAIT_INST_LDS / SQ_WAVE_CYCLES``), both counters in the same
     (quad-cycle) units.
 
-``traffic --fetch F --write W --cal-fetch CF --cal-write CW``
+``traffic --fetch F --write W --cal-fetch CF --cal-write CW [--window K:FIRST:LAST]``
     HBM bytes per dispatch of each solver kernel from two ``--pmc`` runs
     (``FETCH_SIZE``, then ``WRITE_SIZE``; both in KiB per dispatch), each scaled
     by what the same counter reads for a plain copy kernel of known size
@@ -60,8 +65,48 @@ def kernel_stats(path: str) -> list[dict]:
     return out
 
 
-def stats_markdown(path: str, top: int = 20) -> str:
-    rows = kernel_stats(path)
+def _window(rows, window: str | None):
+    """The rows of the dispatches inside ``window`` = "K:FIRST:LAST", in dispatch order: from the
+    FIRST-th dispatch of the kernel whose name contains K (from 1) up to, not including, its
+    (LAST+1)-th.  Without a window, every row."""
+    if not window:
+        return list(rows)
+    marker, a, b = window.rsplit(":", 2)
+    first, last = int(a), int(b)
+    seen, inside, out, prev = 0, False, [], None
+    for r in sorted(rows, key=lambda r: int(r["Dispatch_Id"])):
+        if marker in r["Kernel_Name"] and r["Dispatch_Id"] != prev:
+            seen += 1
+            inside = first <= seen <= last
+        prev = r["Dispatch_Id"]
+        if inside:
+            out.append(r)
+    if seen < last:
+        raise ValueError(f"{marker!r} dispatched {seen} times, fewer than {last}")
+    return out
+
+
+def window_stats(path: str, window: str) -> list[dict]:
+    """Per-kernel statistics of the dispatches inside ``window`` (see ``stats``)."""
+    files = glob.glob(os.path.join(path, "*kernel_trace.csv")) if os.path.isdir(path) else [path]
+    if not files:
+        raise FileNotFoundError(f"no *kernel_trace.csv under {path}")
+    with open(files[0], newline="") as fh:
+        rows = _window(csv.DictReader(fh), window)
+    dur = defaultdict(list)
+    for r in rows:
+        dur[r["Kernel_Name"]].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    total = sum(sum(v) for v in dur.values())
+    out = [{"kernel": k, "calls": len(v), "total_ms": sum(v) / 1e3, "avg_us": sum(v) / len(v), "min_us": min(v),
+            "max_us": max(v), "pct": 100.0 * sum(v) / total} for k, v in dur.items()]
+    return sorted(out, key=lambda r: -r["total_ms"])
+
+
+def stats_markdown(path: str, top: int = 20, window: str | None = None) -> str:
+    if window:
+        rows = window_stats(path, window)
+    else:
+        rows = kernel_stats(path)
     lines = ["| kernel | calls | avg us | min us | max us | total ms | % |", "|---|---:|---:|---:|---:|---:|---:|"]
     for r in rows[:top]:
         lines.append(f"| `{_short(r['kernel'])[:90]}` | {r['calls']} | {r['avg_us']:.1f} | {r['min_us']:.1f} | "
@@ -69,10 +114,10 @@ def stats_markdown(path: str, top: int = 20) -> str:
     return "\n".join(lines)
 
 
-def _counter_means(path: str, counter: str) -> dict[str, tuple[int, float]]:
+def _counter_means(path: str, counter: str, window: str | None = None) -> dict[str, tuple[int, float]]:
     acc = defaultdict(list)
     with open(path, newline="") as fh:
-        for r in csv.DictReader(fh):
+        for r in _window(csv.DictReader(fh), window):
             if r["Counter_Name"] == counter:
                 acc[r["Kernel_Name"]].append(float(r["Counter_Value"]))
     return {k: (len(v), sum(v) / len(v)) for k, v in acc.items()}
@@ -90,11 +135,12 @@ def _calibration(path: str, counter: str, expected_bytes: float) -> float:
     return expected_bytes / best
 
 
-def traffic(fetch: str, write: str, cal_fetch: str, cal_write: str, cal_bytes: float, prefix: str = "kb::") -> dict:
+def traffic(fetch: str, write: str, cal_fetch: str, cal_write: str, cal_bytes: float, prefix: str = "kb::",
+            window: str | None = None) -> dict:
     f_scale = _calibration(cal_fetch, "FETCH_SIZE", cal_bytes)
     w_scale = _calibration(cal_write, "WRITE_SIZE", cal_bytes)
-    fm = _counter_means(fetch, "FETCH_SIZE")
-    wm = _counter_means(write, "WRITE_SIZE")
+    fm = _counter_means(fetch, "FETCH_SIZE", window)
+    wm = _counter_means(write, "WRITE_SIZE", window)
     out = {"calibration": {"copy_bytes": cal_bytes, "fetch_bytes_per_unit": f_scale,
                            "write_bytes_per_unit": w_scale}, "kernels": {}}
     for name in sorted(set(fm) | set(wm)):
@@ -111,11 +157,11 @@ def traffic(fetch: str, write: str, cal_fetch: str, cal_write: str, cal_bytes: f
     return out
 
 
-def _sq_totals(path: str, prefix: str):
+def _sq_totals(path: str, prefix: str, window: str | None = None):
     tot = defaultdict(lambda: defaultdict(float))
     disp = defaultdict(set)
     with open(path, newline="") as fh:
-        for r in csv.DictReader(fh):
+        for r in _window(csv.DictReader(fh), window):
             if prefix and prefix not in r["Kernel_Name"]:
                 continue
             k = _short(r["Kernel_Name"])
@@ -124,9 +170,9 @@ def _sq_totals(path: str, prefix: str):
     return tot, disp
 
 
-def sq_json(path: str, prefix: str = "kb::") -> dict:
+def sq_json(path: str, prefix: str = "kb::", window: str | None = None) -> dict:
     """Per-kernel SQ counters per wave and the VALU-issue / LDS-wait fractions of wave cycles."""
-    tot, disp = _sq_totals(path, prefix)
+    tot, disp = _sq_totals(path, prefix, window)
     out = {}
     for k, v in tot.items():
         w = v.get("SQ_WAVES", 0.0)
@@ -142,9 +188,9 @@ def sq_json(path: str, prefix: str = "kb::") -> dict:
     return {"source": "rocprofv3 --pmc SQ counters", "kernels": out}
 
 
-def sq_markdown(path: str, prefix: str = "kb::") -> str:
+def sq_markdown(path: str, prefix: str = "kb::", window: str | None = None) -> str:
     """Per-kernel SQ counter totals of one ``--pmc`` run, normalised per wave."""
-    tot, disp = _sq_totals(path, prefix)
+    tot, disp = _sq_totals(path, prefix, window)
     names = sorted({c for v in tot.values() for c in v})
     per_wave = [c for c in names if c != "SQ_WAVES"]
     head = "| kernel | dispatches | waves | " + " | ".join(f"{c} / wave" for c in per_wave) + " |"
@@ -162,23 +208,27 @@ def main(argv=None):
     a = sub.add_parser("stats")
     a.add_argument("dir")
     a.add_argument("--top", type=int, default=20)
+    a.add_argument("--window", help="KERNEL:FIRST:LAST, from the kernel trace (see the module docstring)")
     b = sub.add_parser("traffic")
     b.add_argument("--fetch", required=True)
     b.add_argument("--write", required=True)
     b.add_argument("--cal-fetch", required=True)
     b.add_argument("--cal-write", required=True)
     b.add_argument("--cal-mib", type=float, default=512.0)
+    b.add_argument("--window", help="KERNEL:FIRST:LAST over the fetch and write runs")
     c = sub.add_parser("sq")
     c.add_argument("csv")
     c.add_argument("--json", action="store_true")
+    c.add_argument("--window", help="KERNEL:FIRST:LAST")
     args = ap.parse_args(argv)
     if args.cmd == "stats":
-        print(stats_markdown(args.dir, args.top))
+        print(stats_markdown(args.dir, args.top, args.window))
     elif args.cmd == "sq":
-        print(json.dumps(sq_json(args.csv), indent=1) if args.json else sq_markdown(args.csv))
+        print(json.dumps(sq_json(args.csv, window=args.window), indent=1) if args.json
+              else sq_markdown(args.csv, window=args.window))
     else:
-        print(json.dumps(traffic(args.fetch, args.write, args.cal_fetch, args.cal_write, args.cal_mib * (1 << 20)),
-                         indent=1))
+        print(json.dumps(traffic(args.fetch, args.write, args.cal_fetch, args.cal_write, args.cal_mib * (1 << 20),
+                                 window=args.window), indent=1))
 
 
 if __name__ == "__main__":

@@ -11,7 +11,8 @@ add into a second set of workgroup slots); and two solves bitwise equal.
 Checked with forced cuts and windows on configs 1 and 2 and on an S = 4095
 tree (the large-row kernel's slot offset), against the oracle as well, and
 with the default cut and window on config 3 (the bench's workload), where an
-overlap is chosen.
+overlap is chosen; and captured as one HIP graph, whose replays equal the
+eager solve bitwise.
 """
 
 import numpy as np
@@ -100,3 +101,30 @@ def test_default_cut_overlaps_config3_and_not_config1(monkeypatch):
     loss1, _, gt1, gc1 = over.solve(theta, cw)
     torch.cuda.synchronize()
     assert float(loss1) == float(loss0) and torch.equal(gt1, gt0) and torch.equal(gc1, gc0)
+
+
+def test_overlapped_solve_replays_from_a_hip_graph(monkeypatch):
+    """The one-call solve captured as one HIP graph: the second stream's launches join the capture
+    through the fork / join events; every replay, with eager solves between them, equals the eager
+    solve bitwise."""
+    print("[solve] HIP graph of the one-call solve, config 2 cut 4", flush=True)
+    plain, over, theta, cw = _solvers(kbtest.problem("2", None), monkeypatch, 4)
+    assert over.overlap_cut == 4 and over.overlap_rows > 0
+    loss0, _, gt0, gc0 = over.solve(theta, cw)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        loss_g, _, gt_g, gc_g = over.solve(theta, cw, check_solve=False)
+    for i in range(3):
+        loss_e, _, gt_e, gc_e = over.solve(theta, cw)  # eager work between the replays
+        plain.run_backward(theta, cw, plain.run_forward(theta, cw)[1])
+        torch.cuda.synchronize()
+        gt_g.zero_()
+        gc_g.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        print(f"  replay {i}: loss {float(loss_g):.6f}", flush=True)
+        assert float(loss_g) == float(loss0) == float(loss_e)
+        assert torch.equal(gt_g, gt0) and torch.equal(gc_g, gc0)
+        assert torch.equal(gt_e, gt0) and torch.equal(gc_e, gc0)
+    over.backward_stats()  # the E-adjoint solve of the last replay succeeded

@@ -128,3 +128,24 @@ def test_overlapped_solve_replays_from_a_hip_graph(monkeypatch):
         assert torch.equal(gt_g, gt0) and torch.equal(gc_g, gc0)
         assert torch.equal(gt_e, gt0) and torch.equal(gc_e, gc0)
     over.backward_stats()  # the E-adjoint solve of the last replay succeeded
+
+
+def test_solve_refuses_a_backward_that_does_not_read_the_forwards_outputs(monkeypatch):
+    """kb_solve checks on the host, before any launch, that the backward io names the forward's outputs."""
+    import ctypes as ct
+
+    from kbench import _native as N
+
+    print("[solve] mismatched backward io", flush=True)
+    _, over, theta, cw = _solvers(kbtest.problem("1", True), monkeypatch, 3)
+    fio, _, saved, keep = over._forward_args(theta, cw, None)
+    bio, _, _, _ = over._backward_args(theta, cw, saved, False)
+    other = torch.empty_like(saved["pi_wave"])
+    bio.pi = N.ptr(other)
+    with torch.cuda.device(over.device):
+        with pytest.raises(ValueError, match="forward.s outputs"):
+            N.check(N.lib().kb_solve(over._plan, ct.byref(fio), ct.byref(bio), N.stream_handle(over.device)))
+    del keep
+    loss, _, gt, gc = over.solve(theta, cw)  # the plan still works
+    torch.cuda.synchronize()
+    assert torch.isfinite(gt).all() and torch.isfinite(gc).all() and float(loss) == float(loss)

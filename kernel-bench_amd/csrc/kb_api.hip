@@ -1048,7 +1048,9 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
 // (`sets` sets of b_nb_max slots: 1, or 2 for kb_solve's early rows); one
 // launch over rows [first, first + n) of level d on up to `grid` workgroups
 // whose slots start at `poff`; the slot reduction, E adjoint and VJP epilogue.
-static int backward_setup(kb_plan* p, const kb_backward_io* io, hipStream_t st, kb::BwdParams& B, int sets) {
+// extra: workgroup slots beyond the first set that launches will add into
+// (kb_solve's early launches), zeroed here as well
+static int backward_setup(kb_plan* p, const kb_backward_io* io, hipStream_t st, kb::BwdParams& B, int extra) {
   if (!p || !io) return set_error(KB_ERR_ARG, "null argument");
   if (io->neumann_terms < 0) return set_error(KB_ERR_ARG, "neumann_terms must be non-negative");
   if (io->bicgstab_max_iter < 1) return set_error(KB_ERR_ARG, "max_iter must be at least 1");
@@ -1145,7 +1147,8 @@ static int backward_setup(kb_plan* p, const kb_backward_io* io, hipStream_t st, 
   B.cls_ptr = p->d_cls_ptr;
   B.cls_rows = p->d_cls_rows;
   // (the slot count is known only once ensure_backward_work has run)
-  kb::launch_fill_zero(p->b_contrib, (size_t)sets * p->b_n_partials * p->b_slot, st);
+  const size_t n_slots = (size_t)p->b_n_partials + std::min(std::max(extra, 0), p->b_n_partials);
+  kb::launch_fill_zero(p->b_contrib, n_slots * p->b_slot, st);
   KB_HIP(hipGetLastError());
   return 0;
 }
@@ -1210,7 +1213,7 @@ static int level_rows(const kb_plan* p, int d) { return d == 0 ? p->n_cls0 : p->
 extern "C" int kb_backward(kb_plan* p, const kb_backward_io* io, void* stream) {
   hipStream_t st = (hipStream_t)stream;
   kb::BwdParams B{};
-  int rc = backward_setup(p, io, st, B, 1);
+  int rc = backward_setup(p, io, st, B, 0);
   for (int d = p ? p->n_levels - 1 : -1; !rc && d >= 0; --d)
     rc = backward_level(p, B, d, p->level_ptr[d], level_rows(p, d), p->b_nb_max, 0, st);
   return rc ? rc : backward_finish(p, io, p->b_n_partials, st);
@@ -1242,8 +1245,8 @@ extern "C" int kb_solve(kb_plan* p, const kb_forward_io* fio, const kb_backward_
   kb_backward_io b2 = *bio;
   b2.forward_token = p->fwd_token;
   kb::BwdParams B{};
-  // the early rows' workgroups use slots b_nb_max .. 2 b_nb_max - 1
-  rc = backward_setup(p, &b2, st, B, 2);
+  // the early rows' workgroups use slots b_nb_max .. b_nb_max + overlap_grid - 1
+  rc = backward_setup(p, &b2, st, B, p->overlap_grid);
   if (rc) return rc;
   if (!p->s2) {
     KB_HIP(hipStreamCreateWithFlags(&p->s2, hipStreamNonBlocking));
@@ -1273,7 +1276,7 @@ extern "C" int kb_solve(kb_plan* p, const kb_forward_io* fio, const kb_backward_
   if (rc) return rc;
   KB_HIP(hipStreamWaitEvent(st, p->ev_join, 0));
   for (int d = low - 1; !rc && d >= 0; --d) rc = backward_level(p, B, d, p->level_ptr[d], level_rows(p, d), p->b_nb_max, 0, st);
-  return rc ? rc : backward_finish(p, &b2, 2 * p->b_nb_max, st);
+  return rc ? rc : backward_finish(p, &b2, p->b_nb_max + eg, st);
 }
 
 extern "C" {

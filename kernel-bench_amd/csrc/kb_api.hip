@@ -137,7 +137,7 @@ struct kb_plan {
   int* b_status = nullptr;
   int* h_status = nullptr;  // pinned host copy of b_status (kb_backward_stats)
   float* b_DL = nullptr; float* b_SL1 = nullptr; float* b_SL2 = nullptr; float* b_pS = nullptr; float* b_pD = nullptr;
-  float* b_Ebar = nullptr; float* b_E = nullptr; float* b_mt = nullptr; float* b_col = nullptr; double* b_acc_pre = nullptr;
+  float* b_Ebar = nullptr; float* b_E = nullptr; float* b_mt = nullptr; float* b_col = nullptr;
   int b_nb_max = 0, b_n_partials = 0, b_variant = 0, b_large = 1;
   size_t b_slot = 0;  // floats per workgroup slot of b_contrib
   std::vector<int> b_poff;
@@ -1033,8 +1033,7 @@ static int ensure_backward_work(kb_plan* p, int use_col) {
   rc |= alloc(&p->b_E, S);
   rc |= alloc(&p->b_mt, S);
   rc |= alloc(&p->b_col, S);
-  rc |= alloc(&p->b_acc_pre, (size_t)8 * S);
-  for (void* ptr : {(void*)p->b_Ebar, (void*)p->b_E, (void*)p->b_mt, (void*)p->b_col, (void*)p->b_acc_pre,
+  for (void* ptr : {(void*)p->b_Ebar, (void*)p->b_E, (void*)p->b_mt, (void*)p->b_col,
                     (void*)p->b_staging, (void*)p->b_split_on, (void*)p->b_mask, (void*)p->b_contrib,
                     (void*)p->b_rhs0, (void*)p->b_rhsc, (void*)p->b_cls_active, (void*)p->b_ck_any, (void*)p->b_m_mask,
                     (void*)p->b_partial, (void*)p->b_acc, (void*)p->b_work, (void*)p->b_status, (void*)p->b_DL,
@@ -1169,8 +1168,7 @@ static int backward_finish(kb_plan* p, const kb_backward_io* io, int n_partials,
   const int S = p->S;
   KB_HIP(hipGetLastError());
   kb::launch_bwd_reduce(p->b_contrib, n_partials, S, p->b_slot, kb::kb_slot_ld(S, p->b_large), p->b_partial,
-                        p->b_acc_pre, st);
-  kb::launch_bwd_unpermute(p->b_acc_pre, p->d_pre, S, p->b_acc, st);
+                        p->d_pre, p->b_acc, st);
   KB_HIP(hipGetLastError());
   if (io->acc_out)
     KB_HIP(hipMemcpyAsync(io->acc_out, p->b_acc, (size_t)8 * S * sizeof(double), hipMemcpyDeviceToDevice, st));

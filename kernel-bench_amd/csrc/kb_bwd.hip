@@ -1258,31 +1258,25 @@ __global__ void bwd_reduce_stage1(const float* contrib, int C, int S, size_t slo
   partial[(size_t)chunk * 8 * S + j] = acc;
 }
 
-__global__ void bwd_reduce_stage2(const double* partial, int n_chunks, int S, double* out) {
-  const int j = blockIdx.x * blockDim.x + threadIdx.x;
-  if (j >= 8 * S) return;
-  double acc = 0.0;
-  for (int c = 0; c < n_chunks; ++c) acc += partial[(size_t)c * 8 * S + j];
-  out[j] = acc;
-}
-
-__global__ void bwd_unpermute(const double* in, const int* pre, int S, double* out) {
+// Entry j = a * S + s of out (accumulator a, column s) sums the chunk
+// partials of its preorder position pre[s] in chunk order: the reduction and
+// the return from preorder to column order in one pass.
+__global__ void bwd_reduce_stage2(const double* partial, int n_chunks, int S, const int* pre, double* out) {
   const int j = blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= 8 * S) return;
   const int a = j / S, s = j - a * S;
-  out[j] = in[(size_t)a * S + pre[s]];
+  const size_t src = (size_t)a * S + pre[s];
+  double acc = 0.0;
+  for (int c = 0; c < n_chunks; ++c) acc += partial[(size_t)c * 8 * S + src];
+  out[j] = acc;
 }
 
-void launch_bwd_reduce(const float* contrib, int C, int S, size_t slot_stride, int ld, double* partial, double* out,
-                       hipStream_t st) {
+void launch_bwd_reduce(const float* contrib, int C, int S, size_t slot_stride, int ld, double* partial, const int* pre,
+                       double* out, hipStream_t st) {
   const int n_chunks = (C + RED_CHUNK - 1) / RED_CHUNK;
   dim3 g1((8 * S + 255) / 256, n_chunks);
   hipLaunchKernelGGL(bwd_reduce_stage1, g1, dim3(256), 0, st, contrib, C, S, slot_stride, ld, partial);
-  hipLaunchKernelGGL(bwd_reduce_stage2, dim3((8 * S + 255) / 256), dim3(256), 0, st, partial, n_chunks, S, out);
-}
-
-void launch_bwd_unpermute(const double* in, const int* pre, int S, double* out, hipStream_t st) {
-  hipLaunchKernelGGL(bwd_unpermute, dim3((8 * S + 255) / 256), dim3(256), 0, st, in, pre, S, out);
+  hipLaunchKernelGGL(bwd_reduce_stage2, dim3((8 * S + 255) / 256), dim3(256), 0, st, partial, n_chunks, S, pre, out);
 }
 
 int reduce_chunks(int C) { return (C + RED_CHUNK - 1) / RED_CHUNK; }

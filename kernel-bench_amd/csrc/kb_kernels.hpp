@@ -237,10 +237,10 @@ int bwd_large_blocks_per_cu(int S, int use_col);
 void launch_bwd_level0_prep(const BwdParams& P, int n_members, int n_cls, hipStream_t st);
 void launch_fill_zero(float* p, size_t n, hipStream_t st);
 // Sums the bucket rows of C workgroup slots (slot_stride floats apart, bucket
-// rows ld floats apart) in slot order.
-void launch_bwd_reduce(const float* contrib, int C, int S, size_t slot_stride, int ld, double* partial, double* out,
-                       hipStream_t st);
-void launch_bwd_unpermute(const double* in, const int* pre, int S, double* out, hipStream_t st);
+// rows ld floats apart, preorder positions) in slot order into out [8, S] in
+// column order (column s at preorder position pre[s]).
+void launch_bwd_reduce(const float* contrib, int C, int S, size_t slot_stride, int ld, double* partial, const int* pre,
+                       double* out, hipStream_t st);
 int reduce_chunks(int C);
 void launch_epilogue(const EpiParams& P, hipStream_t st);
 int epilogue_work_vectors();

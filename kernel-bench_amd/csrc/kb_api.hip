@@ -1084,6 +1084,10 @@ static int backward_setup(kb_plan* p, const kb_backward_io* io, hipStream_t st, 
   K.pS_state = p->b_pS;
   K.pD_state = p->b_pD;
   K.om = kb::kb_use_large(S, p->b_large) ? p->b_om_const : nullptr;
+  // the same launch zeroes the bucket slots the launches will add into
+  const size_t n_slots = (size_t)p->b_n_partials + std::min(std::max(extra, 0), p->b_n_partials);
+  K.zero = p->b_contrib;
+  K.n_zero = n_slots * p->b_slot;
   kb::launch_bwd_consts(K, st);
 
   B = kb::BwdParams{};
@@ -1145,9 +1149,6 @@ static int backward_setup(kb_plan* p, const kb_backward_io* io, hipStream_t st, 
   B.rep_of = p->d_rep_of;
   B.cls_ptr = p->d_cls_ptr;
   B.cls_rows = p->d_cls_rows;
-  // (the slot count is known only once ensure_backward_work has run)
-  const size_t n_slots = (size_t)p->b_n_partials + std::min(std::max(extra, 0), p->b_n_partials);
-  kb::launch_fill_zero(p->b_contrib, n_slots * p->b_slot, st);
   KB_HIP(hipGetLastError());
   return 0;
 }

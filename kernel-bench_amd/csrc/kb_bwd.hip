@@ -1152,16 +1152,6 @@ void launch_bwd_level0_prep(const BwdParams& P, int n_members, int n_cls, hipStr
   hipLaunchKernelGGL(bwd_classsum0_kernel, dim3(n_cls, nblk), dim3(256), 0, st, P);
 }
 
-__global__ __launch_bounds__(256) void fill_zero_kernel(float* p, size_t n) {
-  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = 0.0f;
-}
-
-void launch_fill_zero(float* p, size_t n, hipStream_t st) {
-  if (n == 0) return;
-  const int blocks = (int)std::min<size_t>(4096, (n + 255) / 256);
-  hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks), dim3(256), 0, st, p, n);
-}
-
 void launch_bwd_wave(const BwdParams& P, int first, int W, int nb, int poff, hipStream_t st) {
   if (W <= 0 || nb <= 0) return;
   if (launch_bwd_large(P, first, W, nb, poff, st)) return;
@@ -1206,7 +1196,8 @@ int bwd_blocks_per_cu(int S, int use_col, int variant, int large) {
 // ---- backward constants from the saved tensors, in the glue's float32 order
 // (_implicit_grad.py:136-143: DL = 1 + pD + E, SL1 = pS + E_s2, SL2 = pS + E_s1),
 // written at preorder positions for the row kernel.
-__global__ void bwd_consts_kernel(BwdConstArgs A) {
+__global__ __launch_bounds__(256) void bwd_consts_kernel(BwdConstArgs A) {
+  for (size_t z = (size_t)blockIdx.x * 256 + threadIdx.x; z < A.n_zero; z += (size_t)gridDim.x * 256) A.zero[z] = 0.0f;
   const int s = blockIdx.x * blockDim.x + threadIdx.x;
   if (s >= A.S) return;
   const int i = A.pre[s];
@@ -1238,12 +1229,13 @@ __global__ void bwd_consts_kernel(BwdConstArgs A) {
 }
 
 void launch_bwd_consts(const BwdConstArgs& A, hipStream_t st) {
-  hipLaunchKernelGGL(bwd_consts_kernel, dim3((A.S + 255) / 256), dim3(256), 0, st, A);
+  const size_t zb = std::min<size_t>(4096, (A.n_zero + 255) / 256);
+  hipLaunchKernelGGL(bwd_consts_kernel, dim3((unsigned)std::max<size_t>((A.S + 255) / 256, zb)), dim3(256), 0, st, A);
 }
 
 // ---- column sums of the per-row buckets over active rows, fixed order.
-// Stage 1: chunk c of rows -> partial[c][8*S]; stage 2: sum of chunks.
-// The result is in preorder-position order: out[j*S + pre(s)].
+// Stage 1: chunk c of rows -> partial[c][8*S] at preorder positions;
+// stage 2: sum of chunks, written in column order: out[j*S + s].
 constexpr int RED_CHUNK = 16;
 
 __global__ void bwd_reduce_stage1(const float* contrib, int C, int S, size_t slot_stride, int ld, double* partial) {

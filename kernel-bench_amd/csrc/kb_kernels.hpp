@@ -96,6 +96,7 @@ struct BwdConstArgs {
   float* DL; float* SL1; float* SL2; float* pS_state; float* pD_state;
   float* Ebar_pre; float* E_pre; float* mt_pre; float* col_pre;
   float* om;                  // also in the owner-major layout (KB_OM_CONSTS rows), or null
+  float* zero; size_t n_zero;  // n_zero floats set to zero by the same launch (the bucket slots)
 };
 
 // Owner-major layout of bwd_row_large_kernel's per-position tables: with
@@ -235,7 +236,6 @@ bool launch_bwd_large(const BwdParams& P, int first, int n, int nb, int poff, hi
 int bwd_large_blocks_per_cu(int S, int use_col);
 // Level-0 adjoint rows, masks and class sums.
 void launch_bwd_level0_prep(const BwdParams& P, int n_members, int n_cls, hipStream_t st);
-void launch_fill_zero(float* p, size_t n, hipStream_t st);
 // Sums the bucket rows of C workgroup slots (slot_stride floats apart, bucket
 // rows ld floats apart, preorder positions) in slot order into out [8, S] in
 // column order (column s at preorder position pre[s]).
